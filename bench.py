@@ -1,0 +1,226 @@
+"""Benchmark of the LCPP device hot path on one MI355X.
+
+Headline (`value`): onesweep SortKeys of 2^28 uniform uint32 keys (4 x 8-bit passes), Gkeys/s, inputs
+resident in HBM, one step = one SortKeys call.  The JSON line also carries the roofline of the
+dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
+one host thread), and the other benchmark configurations (reduce, scan, SortPairs) as achieved GB/s
+against the 8 TB/s HBM peak.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "luisacompute-parallelprimitive_amd"))
+
+HBM_PEAK_GBS = 8000.0
+SEED = 114521
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Runs `warmup` untimed steps, then times exactly `steps` steps on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def kernel_avg_ms(hip, fn, kernel: str, reps: int):
+    """Average device duration of `kernel` over `reps` calls (events recorded around each launch on the
+    launch stream by the library)."""
+    import torch
+    torch.cuda.synchronize()
+    hip.profile_reset()
+    hip.profile_enable(True)
+    try:
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        ms, launches = hip.profile_query(kernel)
+    finally:
+        hip.profile_enable(False)
+    return ms / max(launches, 1), launches
+
+
+def flush_mall(buf):
+    buf.add_(1)  # writes 1 GiB, evicting the 256 MB MALL
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extra", action="store_true", help="headline SortKeys only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+    import lcpp_hip as hip
+
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    steps, warmup = args.steps, args.warmup
+
+    # ---- headline: SortKeys 2^28 u32 ---------------------------------------------------------------
+    n = 1 << 28
+    keys = torch.empty(n, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_HI, keys, n, SEED)
+    out = torch.empty_like(keys)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.sort_keys_temp_bytes(n, 4)), dtype=torch.int32, device=dev)
+
+    def sort_step():
+        hip.sort_keys("u32", keys, out, n, temp=temp)
+
+    ms = time_steps(sort_step, steps, warmup)
+    gkeys = n / (ms * 1e-3) / 1e9
+    onesweep_ms, launches = kernel_avg_ms(hip, sort_step, "radix_onesweep", max(3, steps // 4))
+    hist_ms, _ = kernel_avg_ms(hip, sort_step, "radix_histogram", 3)
+    pass_bytes = 2 * n * 4  # read + write of the keys in one 8-bit pass
+    achieved = pass_bytes / (onesweep_ms * 1e-3) / 1e9
+    line = {
+        "metric": "onesweep SortKeys 2^28 u32 Gkeys/s; reduce/scan achieved HBM GB/s vs peak",
+        "value": round(gkeys, 3),
+        "unit": "Gkeys/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32",
+        "data": "synthetic (splitmix64, seed 114521), generated on the device",
+        "config": {"workload": "DeviceRadixSort::SortKeys, 2^28 uniform uint32 keys, 4 x 8-bit onesweep passes",
+                   "items": n, "device": props.name},
+        "roofline": {
+            "kernel": "radix_onesweep",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(onesweep_ms, 5),
+            "algorithmic_bytes_per_launch": pass_bytes,
+            "whole_sort_frac_4pass_model": round((32 * n) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "histogram_avg_ms": round(hist_ms, 5),
+        },
+    }
+    del temp
+
+    # ---- CPU baseline: the oracle's LSD radix sort, one thread, on a bounded sample -----------------
+    if not args.no_cpu:
+        import numpy as np
+        sys.path.insert(0, str(REPO))
+        import oracle
+        m = 1 << 24
+        sample = keys[:m].cpu().numpy().view(np.uint32).copy()
+        oracle.radix_sort(sample)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.radix_sort(sample)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > 8.0 or reps >= 20:
+                break
+        line["cpu_baseline"] = {
+            "value": round(m * reps / el / 1e9, 4),
+            "unit": "Gkeys/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"first 2^24 of the same keys, stable 8-bit LSD sort (oracle/oracle.c), {reps} reps",
+            "cpu": cpu_model(),
+            "host_threads_available": os.cpu_count(),
+        }
+
+    # ---- other configurations -----------------------------------------------------------------------
+    if not args.no_extra:
+        extra = {}
+        flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+
+        # Reduce 2^24 int32 (config 1): hot (MALL-resident) and cold (MALL flushed before each call).
+        m = 1 << 24
+        a = torch.empty(m, dtype=torch.int32, device=dev)
+        hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
+        s = torch.empty(1, dtype=torch.int32, device=dev)
+        rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+        hot = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
+        cold_k, _ = kernel_avg_ms(hip, lambda: (flush_mall(flush), hip.reduce_sum("i32", a, s, m, temp=rt)),
+                                  "reduce_sum_partials", 5)
+        extra["reduce_sum_i32_2p24"] = {"ms_hot": round(hot, 5), "GBps_hot": round(4 * m / hot / 1e6, 1),
+                                        "kernel_ms_cold": round(cold_k, 5),
+                                        "GBps_cold": round(4 * m / cold_k / 1e6, 1)}
+        # Reduce 2^28 int32 (north-star size).
+        m = 1 << 28
+        a = torch.empty(m, dtype=torch.int32, device=dev)
+        hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
+        rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+        t = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
+        extra["reduce_sum_i32_2p28"] = {"ms": round(t, 5), "GBps": round(4 * m / t / 1e6, 1),
+                                        "frac": round(4 * m / t / 1e6 / HBM_PEAK_GBS, 4)}
+        del a
+        # ExclusiveSum 2^28 uint32 in [0, 16) (config 2).
+        b = torch.empty(m, dtype=torch.int32, device=dev)
+        hip.generate(hip.GEN_U32_LT16, b, m, SEED)
+        c = torch.empty_like(b)
+        st = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+        t = time_steps(lambda: hip.scan_sum("u32", b, c, m, temp=st), steps, warmup)
+        sk, _ = kernel_avg_ms(hip, lambda: hip.scan_sum("u32", b, c, m, temp=st), "scan_sum", 5)
+        extra["exclusive_sum_u32_2p28"] = {"ms": round(t, 5), "GBps": round(8 * m / t / 1e6, 1),
+                                           "frac": round(8 * m / t / 1e6 / HBM_PEAK_GBS, 4),
+                                           "kernel_ms": round(sk, 5)}
+        del b, c, st
+        # SortPairs 2^27 u64 keys + u32 index values (config 4), uniform and AND-of-3 keys.
+        m = 1 << 27
+        for kind, gen in (("uniform", hip.GEN_U64), ("and3", hip.GEN_U64_AND3)):
+            k = torch.empty(m, dtype=torch.int64, device=dev)
+            hip.generate(gen, k, m, SEED)
+            v = torch.empty(m, dtype=torch.int32, device=dev)
+            hip.generate(hip.GEN_U32_IOTA, v, m, 0)
+            ko, vo = torch.empty_like(k), torch.empty_like(v)
+            pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32,
+                             device=dev)
+            t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), 1)
+            extra[f"sort_pairs_u64_u32_2p27_{kind}"] = {
+                "ms": round(t, 4), "Gpairs_per_s": round(m / t / 1e6, 3),
+                "GBps_8pass_model": round(2 * 8 * m * 12 / t / 1e6, 1),
+                "frac": round(2 * 8 * m * 12 / t / 1e6 / HBM_PEAK_GBS, 4)}
+            del k, v, ko, vo, pt
+        line["extra"] = extra
+
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

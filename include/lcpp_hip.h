@@ -1,0 +1,182 @@
+/*
+ * lcpp_hip.h — C-ABI of the MI355X (gfx950) implementation of the LuisaCompute-ParallelPrimitive
+ * (LCPP) device hot path: DeviceReduce::Sum, DeviceScan::ExclusiveSum/InclusiveSum, onesweep
+ * DeviceRadixSort::SortKeys/SortPairs and DeviceSpmv::CsrMV.
+ *
+ * Conventions
+ *   - Every pointer argument except `stream` is a device pointer (hipMalloc'd or a sub-range of one).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the null stream.  Work is enqueued
+ *     asynchronously, in order, on that stream; no entry point synchronises the host (the reference
+ *     records into a CommandList that runs on commit, README.md:182-184).
+ *   - `temp` / `temp_bytes` is caller-owned scratch of at least the size the matching
+ *     *_temp_bytes function returns.  Those functions return exactly the byte counts of the
+ *     reference's Get*TempStorageBytes, so a buffer sized for LCPP is always large enough.
+ *   - Return value: LCPP_HIP_OK (0) or a negative status; lcpp_hip_last_error() describes it
+ *     (thread-local).  The reference aborts through LUISA_ASSERT on the same preconditions.
+ *   - One stream per call; calls that share a temp buffer must be ordered on one stream.
+ *
+ * Element-type suffixes: i32 int32_t, u32 uint32_t, f32 float, i64 int64_t, u64 uint64_t,
+ * f64 double.  Value-size suffixes for SortPairs: v32 (any 4-byte value), v64 (any 8-byte value).
+ */
+#ifndef LCPP_HIP_H_
+#define LCPP_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LCPP_HIP_OK 0
+#define LCPP_HIP_ERR_INVALID_ARGUMENT (-1)
+#define LCPP_HIP_ERR_TEMP_TOO_SMALL (-2)
+#define LCPP_HIP_ERR_HIP (-3)
+#define LCPP_HIP_ERR_UNSUPPORTED (-4)
+
+/* ---------------------------------------------------------------------------------------------
+ * Library
+ * ------------------------------------------------------------------------------------------- */
+const char* lcpp_hip_version(void);
+const char* lcpp_hip_last_error(void);
+
+/* Per-kernel device-time accounting (hipEvents recorded around each launch on its stream).
+ * No reference counterpart: LCPP relies on external profilers (tests/lcpp_cub_bench.cpp:124-260). */
+int lcpp_hip_profile_enable(int enable);
+int lcpp_hip_profile_reset(void);
+int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches);
+int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes);
+
+/* ---------------------------------------------------------------------------------------------
+ * DeviceReduce::Sum
+ * replaces DeviceReduce<>::Sum (src/lcpp/device/device_reduce.h:280-288) and its temp query
+ * DeviceReduce<>::GetTempStorageBytes<T> (device_reduce.h:184-189, formula :517-536).
+ * n == 0 writes 0 to *out (device_reduce.h:238-243).  Integer sums wrap modulo 2^bits.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_reduce_temp_bytes_policy(uint64_t n, size_t elem_bytes, uint32_t block_size, uint32_t items_per_thread);
+size_t lcpp_hip_reduce_temp_bytes(uint64_t n, size_t elem_bytes); /* default policy 256 x 8 */
+int lcpp_hip_reduce_sum_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, void* stream);
+int lcpp_hip_reduce_sum_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
+int lcpp_hip_reduce_sum_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, void* stream);
+int lcpp_hip_reduce_sum_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, void* stream);
+int lcpp_hip_reduce_sum_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, void* stream);
+int lcpp_hip_reduce_sum_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * DeviceScan::ExclusiveSum / InclusiveSum (decoupled look-back, single pass)
+ * replaces DeviceScan<>::ExclusiveSum (src/lcpp/device/device_scan.h:370-385),
+ * DeviceScan<>::InclusiveSum (device_scan.h:409-422), InclusiveScanInit / ExclusiveScan with a
+ * sum operator and an initial value (device_scan.h:321-368), and
+ * DeviceScan<>::GetTempStorageBytes<T> (device_scan.h:295-308, layout :111-126).
+ * n == 0 is a no-op.  Integer sums wrap modulo 2^bits.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_scan_temp_bytes_policy(uint64_t n, size_t elem_bytes, uint32_t block_size, uint32_t items_per_thread,
+                                       int default_policy, int packed_tile_state);
+size_t lcpp_hip_scan_temp_bytes(uint64_t n, size_t elem_bytes); /* default policy 256 x 15 (+ 320 x 25 packed) */
+int lcpp_hip_scan_exclusive_sum_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_exclusive_sum_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_exclusive_sum_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, void* stream);
+/* Sum scan with an initial value: exclusive: out[i] = init + sum(in[0..i)); inclusive: init + sum(in[0..i]). */
+int lcpp_hip_scan_sum_init_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, int inclusive, int32_t init, void* stream);
+int lcpp_hip_scan_sum_init_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, int inclusive, uint32_t init, void* stream);
+int lcpp_hip_scan_sum_init_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, int inclusive, float init, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * DeviceRadixSort (onesweep, 8-bit digits, stable LSD)
+ * replaces DeviceRadixSort<>::SortKeys / SortKeysDescending / SortPairs / SortPairsDescending in
+ * their copy form (src/lcpp/device/device_radix_sort.h:369-466) and DoubleBuffer form
+ * (device_radix_sort.h:468-554), and GetSortKeysTempStorageBytes / GetSortPairsTempStorageBytes
+ * (device_radix_sort.h:337-362, layout :212-335).
+ * Copy form: keys_in/values_in are never written; results land in keys_out/values_out.
+ * DoubleBuffer form: buffers[*selector] holds the input; both buffers may be overwritten; *selector
+ * is flipped once per 8-bit pass before the function returns (host-side, like the reference).
+ * begin_bit == end_bit copies (copy form) or leaves *selector unchanged (DoubleBuffer form).
+ * Float keys order by IEEE total order with -0.0 == +0.0 (common/util_type.h:141-175,
+ * agent/radix_rank_sort_operations.h:31-42); signed keys in two's-complement order.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_radix_sort_temp_bytes_policy(uint32_t n, size_t key_bytes, size_t value_bytes, int keys_only,
+                                             uint32_t block_size, uint32_t items_per_thread, int cub_small_key_policy);
+size_t lcpp_hip_radix_sort_keys_temp_bytes(uint32_t n, size_t key_bytes);                      /* default policy */
+size_t lcpp_hip_radix_sort_pairs_temp_bytes(uint32_t n, size_t key_bytes, size_t value_bytes);  /* default policy */
+
+#define LCPP_HIP_DECLARE_SORT(K, KT)                                                                             \
+    int lcpp_hip_radix_sort_keys_##K(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out, uint32_t n,  \
+                                     uint32_t begin_bit, uint32_t end_bit, int descending, void* stream);         \
+    int lcpp_hip_radix_sort_keys_db_##K(void* temp, size_t temp_bytes, KT* keys0, KT* keys1, int* selector,       \
+                                        uint32_t n, uint32_t begin_bit, uint32_t end_bit, int descending,         \
+                                        void* stream);                                                            \
+    int lcpp_hip_radix_sort_pairs_##K##_v32(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out,       \
+                                            const void* values_in, void* values_out, uint32_t n,                  \
+                                            uint32_t begin_bit, uint32_t end_bit, int descending, void* stream);  \
+    int lcpp_hip_radix_sort_pairs_##K##_v64(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out,       \
+                                            const void* values_in, void* values_out, uint32_t n,                  \
+                                            uint32_t begin_bit, uint32_t end_bit, int descending, void* stream);  \
+    int lcpp_hip_radix_sort_pairs_db_##K##_v32(void* temp, size_t temp_bytes, KT* keys0, KT* keys1,               \
+                                               void* values0, void* values1, int* selector, uint32_t n,           \
+                                               uint32_t begin_bit, uint32_t end_bit, int descending,              \
+                                               void* stream);                                                     \
+    int lcpp_hip_radix_sort_pairs_db_##K##_v64(void* temp, size_t temp_bytes, KT* keys0, KT* keys1,               \
+                                               void* values0, void* values1, int* selector, uint32_t n,           \
+                                               uint32_t begin_bit, uint32_t end_bit, int descending,              \
+                                               void* stream);
+
+LCPP_HIP_DECLARE_SORT(u32, uint32_t)
+LCPP_HIP_DECLARE_SORT(i32, int32_t)
+LCPP_HIP_DECLARE_SORT(f32, float)
+LCPP_HIP_DECLARE_SORT(u64, uint64_t)
+LCPP_HIP_DECLARE_SORT(i64, int64_t)
+LCPP_HIP_DECLARE_SORT(f64, double)
+#undef LCPP_HIP_DECLARE_SORT
+
+/* Largest number of keys one onesweep launch ranks before the sort is split into portions.
+ * Setting a smaller limit (a multiple of the tile, >= one tile) exercises the multi-portion
+ * path on small inputs; 0 restores the default.  Process-wide; not thread-safe with running sorts.
+ * Replaces the fixed PORTION_SIZE of device_radix_sort.h:1056. */
+int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion);
+/* Tile (keys per workgroup) of the onesweep kernel for the given key/value sizes. */
+uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes);
+
+/* ---------------------------------------------------------------------------------------------
+ * DeviceSpmv::CsrMV  y = A * x  (CSR)
+ * replaces DeviceSpmv<>::CsrMV (src/lcpp/device/device_spmv.h:48-130) and
+ * GetTempStorageBytes == 0 (device_spmv.h:43-46).  rows == 0: no-op; nnz == 0: y[0..rows) = 0;
+ * a row whose offsets are decreasing or exceed nnz yields 0; columns >= cols are skipped.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_spmv_temp_bytes(uint64_t rows, uint64_t cols, uint64_t nnz);
+
+#define LCPP_HIP_DECLARE_SPMV(V, VT, I, IT)                                                                    \
+    int lcpp_hip_spmv_csr_##V##_##I(void* temp, size_t temp_bytes, const VT* values, const IT* row_offsets,    \
+                                    const IT* column_indices, const VT* x, VT* y, uint64_t rows, uint64_t cols, \
+                                    uint64_t nnz, void* stream);
+LCPP_HIP_DECLARE_SPMV(f32, float, i32, int32_t)
+LCPP_HIP_DECLARE_SPMV(f32, float, u32, uint32_t)
+LCPP_HIP_DECLARE_SPMV(f64, double, i32, int32_t)
+LCPP_HIP_DECLARE_SPMV(f64, double, u32, uint32_t)
+LCPP_HIP_DECLARE_SPMV(i32, int32_t, i32, int32_t)
+LCPP_HIP_DECLARE_SPMV(i32, int32_t, u32, uint32_t)
+LCPP_HIP_DECLARE_SPMV(u32, uint32_t, i32, int32_t)
+LCPP_HIP_DECLARE_SPMV(u32, uint32_t, u32, uint32_t)
+#undef LCPP_HIP_DECLARE_SPMV
+
+/* ---------------------------------------------------------------------------------------------
+ * Seeded synthetic workloads for tests and benchmarks (no reference counterpart; the reference
+ * generates on the host, e.g. tests/lcpp_cub_bench.cpp:516-521,666-672,814).
+ * Stream: splitmix64, r_i = mix(seed + (start + i + 1) * 0x9E3779B97F4A7C15).
+ * ------------------------------------------------------------------------------------------- */
+#define LCPP_HIP_GEN_U64 0            /* out[i] = r_i (uint64)                                   */
+#define LCPP_HIP_GEN_U32_HI 1         /* out[i] = r_i >> 32 (uint32)                             */
+#define LCPP_HIP_GEN_I32_PM1000 2     /* out[i] = (int32)(r_i % 2001) - 1000                     */
+#define LCPP_HIP_GEN_U32_LT16 3       /* out[i] = r_i & 15 (uint32)                              */
+#define LCPP_HIP_GEN_U64_AND3 4       /* out[i] = r_{3i} & r_{3i+1} & r_{3i+2} (uint64)          */
+#define LCPP_HIP_GEN_U32_IOTA 5       /* out[i] = start + i (uint32)                             */
+#define LCPP_HIP_GEN_F32_PM1 6        /* out[i] = uniform float in [-1, 1): ((r_i>>40) * 2^-23) - 1 */
+int lcpp_hip_generate(int kind, void* out, uint64_t n, uint64_t seed, uint64_t start, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LCPP_HIP_H_ */

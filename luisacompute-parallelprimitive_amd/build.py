@@ -1,0 +1,76 @@
+"""Builds the gfx950 HIP library ``liblcpp_hip.so`` in-tree.
+
+Every ``csrc/*.hip`` file is compiled by ``hipcc --offload-arch=gfx950`` into its own object (in
+parallel), host-only ``csrc/*.cpp`` files by ``g++``, and the objects are linked into one shared
+library next to this file.  The C-ABI is declared in ``include/lcpp_hip.h``.
+
+Usage: ``python luisacompute-parallelprimitive_amd/build.py [--jobs N]``
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+PKG = pathlib.Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "liblcpp_hip.so"
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    "-O3", "-std=c++20", f"--offload-arch={ARCH}", "-fPIC", "-Wall", "-Wno-unused-function",
+    # Keep the compiler from forming packed-FP32 VALU instructions.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{REPO / 'include'}",
+]
+HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", f"-I{REPO / 'include'}"]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; ROCm is required to build liblcpp_hip.so")
+    return path
+
+
+def _compile(src: pathlib.Path) -> pathlib.Path:
+    obj = BUILD / (src.name + ".o")
+    if src.suffix == ".hip":
+        cmd = [_hipcc(), "-x", "hip", *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = ["g++", *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, sources))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    args = ap.parse_args()
+    build(args.jobs, verbose=True)
+    sys.exit(0)

@@ -1,0 +1,611 @@
+// Onesweep DeviceRadixSort for gfx950 (stable LSD, 8-bit digits).
+//
+// Reference path: DeviceRadixSort<>::SortKeys/SortPairs (src/lcpp/device/device_radix_sort.h:369-554)
+// -> onesweep_radix_sort (:1018-1475): reset, all-pass histogram (device/details/radix_sort.h:51-79,
+// agent/agent_radix_sort_histogram.h:32-198), exclusive sum of the bins (radix_sort.h:81-123), then per
+// pass and portion a fused onesweep kernel (radix_sort.h:125-167, agent/agent_radix_sort_onesweep.h:
+// 45-540): atomic tile ticket, load + twiddle, block rank by match-any (block/block_radix_rank.h:
+// 207-486), PARTIAL publish, per-digit look-back, LDS scatter, global scatter.
+//
+// MI355X design
+//   * Keys are loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every
+//     load instruction is a fully coalesced 256/512-byte access and each wave ranks its keys in index
+//     order, which keeps the sort stable.
+//   * Rank: per wave, 8 ballots give each lane the 64-bit mask of lanes holding the same digit; the
+//     rank inside the round is the popcount of that mask below the lane (mbcnt), and the highest lane
+//     of each digit group advances the wave's LDS digit counter.  No LDS atomics are needed, so the
+//     rank never depends on the hardware's ordering of conflicting atomics.
+//   * Per-digit counts go to a look-back row of 256 32-bit words per tile: bits 31:30 hold the status
+//     (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics because
+//     the 8 XCDs do not share an L2.  Tiles are claimed through an atomic ticket.
+//   * Keys are reordered by digit in LDS and written out from LDS in order, so consecutive lanes
+//     write consecutive addresses inside each digit's run.  Pairs move values the same way.
+//   * Portions: one launch ranks at most 2^30 - tile keys so look-back counts fit in 30 bits.  The
+//     histogram keeps per-portion counts, and the bin scan turns them into per-portion global
+//     offsets (total of smaller digits + counts of the same digit in earlier portions).
+// Algorithmic traffic per pass: n * 2 * (sizeof(K) + sizeof(V)) bytes; the histogram reads n*sizeof(K).
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+#include <algorithm>
+
+namespace lcpp_hip {
+namespace radix {
+
+constexpr uint32_t kDigits = 256;
+constexpr uint32_t kFlagPartial = 1u << 30;
+constexpr uint32_t kFlagInclusive = 2u << 30;
+constexpr uint32_t kCountMask = (1u << 30) - 1;
+constexpr uint32_t kMaxPasses = 8;
+
+enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
+
+template <typename K> struct KeyTraits;
+template <> struct KeyTraits<uint32_t> { using U = uint32_t; static constexpr int kind = kUnsigned; };
+template <> struct KeyTraits<int32_t> { using U = uint32_t; static constexpr int kind = kSigned; };
+template <> struct KeyTraits<float> { using U = uint32_t; static constexpr int kind = kFloat; };
+template <> struct KeyTraits<uint64_t> { using U = uint64_t; static constexpr int kind = kUnsigned; };
+template <> struct KeyTraits<int64_t> { using U = uint64_t; static constexpr int kind = kSigned; };
+template <> struct KeyTraits<double> { using U = uint64_t; static constexpr int kind = kFloat; };
+
+template <int VB> struct ValueWord { using type = uint32_t; };
+template <> struct ValueWord<8> { using type = uint64_t; };
+
+// Bit-ordered transform (common/util_type.h:97-175 TwiddleIn/TwiddleOut; descending inverts,
+// agent/radix_rank_sort_operations.h:123-155).
+template <typename U, int KIND, bool DESC>
+__device__ __forceinline__ U twiddle_in(U k) {
+    constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+    if constexpr (KIND == kSigned) k ^= kHigh;
+    if constexpr (KIND == kFloat) k ^= (k & kHigh) ? U(~U(0)) : kHigh;
+    if constexpr (DESC) k = ~k;
+    return k;
+}
+
+template <typename U, int KIND, bool DESC>
+__device__ __forceinline__ U twiddle_out(U k) {
+    constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+    if constexpr (DESC) k = ~k;
+    if constexpr (KIND == kSigned) k ^= kHigh;
+    if constexpr (KIND == kFloat) k ^= (k & kHigh) ? kHigh : U(~U(0));
+    return k;
+}
+
+// Digit of a bit-ordered key.  For floats the ordered image of -0.0 is mapped to that of +0.0
+// before extraction (ShiftDigitExtractor / ProcessFloatMinusZero,
+// agent/radix_rank_sort_operations.h:31-62), so both zeros rank as equal keys.
+template <typename U, int KIND>
+__device__ __forceinline__ uint32_t digit_of(U ordered, uint32_t shift, uint32_t mask) {
+    if constexpr (KIND == kFloat) {
+        constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+        if (ordered == U(~kHigh)) ordered = kHigh;
+    }
+    return static_cast<uint32_t>(ordered >> shift) & mask;
+}
+
+// Lanes of the wave whose 8-bit digit equals this lane's.  Per digit bit: t = 0 or ~0 (the bit,
+// sign-extended), one ballot of t, and peers &= ~(ballot ^ t) on each 32-bit half, which gfx950
+// folds into a single three-input bit operation per half.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d) {
+    uint32_t lo = ~0u, hi = ~0u;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const uint32_t t = static_cast<uint32_t>(static_cast<int32_t>(d << (31 - b)) >> 31);
+        const uint64_t m = wave_ballot(t != 0);
+        lo &= ~(static_cast<uint32_t>(m) ^ t);
+        hi &= ~(static_cast<uint32_t>(m >> 32) ^ t);
+    }
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// --------------------------------------------------------------------------------------------
+// Histogram: digit counts of every pass for one portion.
+// --------------------------------------------------------------------------------------------
+constexpr int kHistBlock = 256;
+constexpr int kHistUnroll = 8;
+
+template <typename K, bool DESC>
+__global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restrict__ keys, uint32_t n,
+                                                                uint32_t* __restrict__ bins, uint32_t begin_bit,
+                                                                uint32_t end_bit, uint32_t passes) {
+    using U = typename KeyTraits<K>::U;
+    constexpr int KIND = KeyTraits<K>::kind;
+    __shared__ uint32_t s_hist[kMaxPasses * kDigits];
+    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) s_hist[i] = 0;
+    __syncthreads();
+
+    const U* ukeys = reinterpret_cast<const U*>(keys);
+    const uint64_t chunk = static_cast<uint64_t>(kHistBlock) * kHistUnroll;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * chunk;
+    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * chunk; base < n; base += stride) {
+        U k[kHistUnroll];
+        bool ok[kHistUnroll];
+#pragma unroll
+        for (int u = 0; u < kHistUnroll; ++u) {
+            const uint64_t i = base + static_cast<uint64_t>(u) * kHistBlock + threadIdx.x;
+            ok[u] = i < n;
+            k[u] = ok[u] ? __builtin_nontemporal_load(&ukeys[i]) : U(0);
+        }
+#pragma unroll
+        for (int u = 0; u < kHistUnroll; ++u) {
+            if (!ok[u]) continue;
+            const U ordered = twiddle_in<U, KIND, DESC>(k[u]);
+            for (uint32_t p = 0; p < passes; ++p) {
+                const uint32_t shift = begin_bit + 8 * p;
+                const uint32_t nb = min(8u, end_bit - shift);
+                const uint32_t d = digit_of<U, KIND>(ordered, shift, (1u << nb) - 1u);
+                atomicAdd(&s_hist[p * kDigits + d], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) {
+        const uint32_t c = s_hist[i];
+        if (c) atomic_add_agent(&bins[i], c);
+    }
+}
+
+// In place: counts[q][p][d] -> global output offset of digit d of pass p for portion q.
+__global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict__ bins, uint32_t passes,
+                                                            uint32_t portions) {
+    __shared__ uint32_t s_wave_totals[kDigits / kWave];
+    const uint32_t d = threadIdx.x;
+    const uint32_t wave = d / kWave;
+    for (uint32_t p = 0; p < passes; ++p) {
+        uint32_t total = 0;
+        for (uint32_t q = 0; q < portions; ++q) total += bins[(q * passes + p) * kDigits + d];
+        const uint32_t incl = wave_inclusive_scan(total, SumOp{});
+        if (lane_id() == kWave - 1) s_wave_totals[wave] = incl;
+        __syncthreads();
+        uint32_t run = incl - total;
+        for (uint32_t w = 0; w < wave; ++w) run += s_wave_totals[w];
+        for (uint32_t q = 0; q < portions; ++q) {
+            uint32_t* cell = &bins[(q * passes + p) * kDigits + d];
+            const uint32_t c = *cell;
+            *cell = run;
+            run += c;
+        }
+        __syncthreads();
+    }
+}
+
+// --------------------------------------------------------------------------------------------
+// Onesweep pass.
+// --------------------------------------------------------------------------------------------
+template <typename K, bool DESC, int VB, int BLOCK, int ITEMS>
+__global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ keys_in, K* __restrict__ keys_out,
+                                                         const void* __restrict__ values_in,
+                                                         void* __restrict__ values_out, uint32_t n,
+                                                         const uint32_t* __restrict__ digit_offsets,
+                                                         uint32_t* __restrict__ lookback,
+                                                         uint32_t* __restrict__ counter, uint32_t shift,
+                                                         uint32_t num_bits, uint32_t out_items) {
+    using U = typename KeyTraits<K>::U;
+    using VW = typename ValueWord<VB>::type;
+    constexpr int KIND = KeyTraits<K>::kind;
+    constexpr int W = BLOCK / kWave;
+    constexpr uint32_t TILE = static_cast<uint32_t>(BLOCK) * ITEMS;
+    constexpr size_t ELEM = (VB > static_cast<int>(sizeof(U))) ? VB : sizeof(U);
+    static_assert(BLOCK >= static_cast<int>(kDigits) && BLOCK % static_cast<int>(kDigits) == 0,
+                  "one thread per digit");
+
+    __shared__ __attribute__((aligned(16))) unsigned char s_tile[TILE * ELEM];
+    __shared__ uint32_t s_counts[W][kDigits];
+    __shared__ uint32_t s_global_minus_local[kDigits];
+    __shared__ uint32_t s_scan[kDigits / kWave];
+    __shared__ uint32_t s_ticket;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint32_t mask = (1u << num_bits) - 1u;
+
+    if (tid == 0) s_ticket = atomic_add_agent(counter, 1u);
+#pragma unroll
+    for (uint32_t i = lane; i < kDigits; i += kWave) s_counts[wave][i] = 0;
+    __syncthreads();
+    const uint32_t tile = s_ticket;
+    const uint32_t tile_base = tile * TILE;
+    const uint32_t valid = min(TILE, n - tile_base);
+
+    // Load (wave-striped) and twiddle; missing items become all-ones keys, which rank last.
+    const U* ukeys = reinterpret_cast<const U*>(keys_in) + tile_base;
+    const uint32_t wave_off = wave * kWave * ITEMS + lane;
+    U keys[ITEMS];
+    if (valid == TILE) {
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) keys[k] = twiddle_in<U, KIND, DESC>(__builtin_nontemporal_load(&ukeys[wave_off + k * kWave]));
+    } else {
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t i = wave_off + k * kWave;
+            keys[k] = i < valid ? twiddle_in<U, KIND, DESC>(ukeys[i]) : U(~U(0));
+        }
+    }
+    VW vals[VB ? ITEMS : 1];
+    if constexpr (VB != 0) {
+        const VW* uvals = reinterpret_cast<const VW*>(values_in) + tile_base;
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t i = wave_off + k * kWave;
+            vals[k] = i < valid ? __builtin_nontemporal_load(&uvals[i]) : VW(0);
+        }
+    }
+
+    // Rank inside the wave.
+    uint32_t rank[ITEMS];
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+        const uint64_t peers = match_digit(d);
+        const uint32_t below = popc_lanes_below(peers);
+        const uint32_t base = s_counts[wave][d];
+        rank[k] = base + below;
+        if ((peers >> lane) == 1ull) s_counts[wave][d] = base + below + 1;
+    }
+    __syncthreads();
+
+    // Per digit: wave offsets, tile count, PARTIAL publish, tile-local start.
+    uint32_t count = 0, local_start = 0;
+    if (tid < kDigits) {
+        const uint32_t d = tid;
+        uint32_t run = 0;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const uint32_t c = s_counts[w][d];
+            s_counts[w][d] = run;
+            run += c;
+        }
+        count = run;
+        const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
+        if (tile == 0)
+            atomic_store_agent(&lookback[d], kFlagInclusive | real);
+        else
+            atomic_store_agent(&lookback[tile * kDigits + d], kFlagPartial | real);
+        const uint32_t incl = wave_inclusive_scan(count, SumOp{});
+        if (lane == kWave - 1) s_scan[wave] = incl;
+        local_start = incl - count;
+    }
+    __syncthreads();
+    if (tid < kDigits) {
+        const uint32_t d = tid;
+        for (uint32_t w = 0; w < wave; ++w) local_start += s_scan[w];
+#pragma unroll
+        for (int w = 0; w < W; ++w) s_counts[w][d] += local_start;
+
+        // Look-back over earlier tiles of this digit.
+        uint32_t excl = 0;
+        if (tile > 0) {
+            const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
+            int64_t t = static_cast<int64_t>(tile) - 1;
+            while (true) {
+                const uint32_t v = atomic_load_agent(&lookback[static_cast<uint64_t>(t) * kDigits + d]);
+                if ((v & ~kCountMask) == 0) {
+                    __builtin_amdgcn_s_sleep(1);
+                    continue;
+                }
+                excl += v & kCountMask;
+                if ((v & kFlagInclusive) || t == 0) break;  // tile 0 always publishes INCLUSIVE
+                --t;
+            }
+            atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
+        }
+        s_global_minus_local[d] = digit_offsets[d] + excl - local_start;
+    }
+    __syncthreads();
+
+    // Reorder keys by digit in LDS.
+    U* s_keys = reinterpret_cast<U*>(s_tile);
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+        rank[k] += s_counts[wave][d];
+        s_keys[rank[k]] = keys[k];
+    }
+    __syncthreads();
+
+    U* ukeys_out = reinterpret_cast<U*>(keys_out);
+    uint32_t gpos[VB ? ITEMS : 1];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const uint32_t i = tid + j * BLOCK;
+        if (i < valid) {
+            const U key = s_keys[i];
+            const uint32_t d = digit_of<U, KIND>(key, shift, mask);
+            const uint32_t g = s_global_minus_local[d] + i;
+            if (g < out_items) ukeys_out[g] = twiddle_out<U, KIND, DESC>(key);  // always true for a correct sort
+            if constexpr (VB != 0) gpos[j] = g;
+        }
+    }
+
+    if constexpr (VB != 0) {
+        __syncthreads();
+        VW* s_vals = reinterpret_cast<VW*>(s_tile);
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) s_vals[rank[k]] = vals[k];
+        __syncthreads();
+        VW* uvals_out = reinterpret_cast<VW*>(values_out);
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const uint32_t i = tid + j * BLOCK;
+            if (i < valid && gpos[j] < out_items) uvals_out[gpos[j]] = s_vals[i];
+        }
+    }
+}
+
+// --------------------------------------------------------------------------------------------
+// Host orchestration.
+// --------------------------------------------------------------------------------------------
+struct Geometry {
+    int block;
+    int items;
+    uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
+};
+
+template <typename K, int VB>
+constexpr Geometry geometry() {
+    return Geometry{256, 16};
+}
+
+uint32_t g_portion_limit = 0;  // 0: default
+
+// Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
+// portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
+// never larger than the reference's and the layout always fits a reference-sized temp buffer.
+uint32_t portion_size(uint32_t tile, bool compact) {
+    const uint32_t def = compact ? ((1u << 28) - 1u) / tile * tile : ((1u << 30) - 1u) / tile * tile;
+    if (g_portion_limit == 0) return def;
+    uint32_t p = g_portion_limit / tile * tile;
+    if (p < tile) p = tile;
+    return std::min(p, def);
+}
+
+struct Layout {
+    uint32_t passes, portions, portion, tiles_max;
+    size_t bins_off, counters_off, lookback_off, keys_tmp_off, values_tmp_off, total;
+    size_t clear_bytes;  // bins + counters, zeroed per call
+};
+
+Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit, uint32_t end_bit,
+                   uint32_t tile, bool need_tmp, bool compact) {
+    Layout L{};
+    L.passes = (end_bit - begin_bit + 7) / 8;
+    L.portion = portion_size(tile, compact);
+    L.portions = static_cast<uint32_t>(ceil_div(n, L.portion));
+    L.tiles_max = static_cast<uint32_t>(ceil_div(std::min(n, L.portion), tile));
+    size_t off = 0;
+    L.bins_off = off;
+    off += static_cast<size_t>(L.portions) * L.passes * kDigits * 4;
+    L.counters_off = off;
+    off += static_cast<size_t>(L.portions) * L.passes * 4;
+    L.clear_bytes = off;
+    off = align_up(off, kViewAlign);
+    L.lookback_off = off;
+    off += static_cast<size_t>(L.tiles_max) * kDigits * 4;
+    L.keys_tmp_off = L.values_tmp_off = 0;
+    if (need_tmp && L.passes > 1) {
+        off = align_up(off, kViewAlign);
+        L.keys_tmp_off = off;
+        off += static_cast<size_t>(n) * key_bytes;
+        if (value_bytes) {
+            off = align_up(off, kViewAlign);
+            L.values_tmp_off = off;
+            off += static_cast<size_t>(n) * value_bytes;
+        }
+    }
+    L.total = off;
+    return L;
+}
+
+template <typename K, bool DESC, int VB>
+int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, const void* values_in, void* values_out,
+                K* keys_tmp, void* values_tmp, K* const* db_keys, void* const* db_values, int sel, uint32_t n,
+                uint32_t begin_bit, uint32_t end_bit, hipStream_t stream) {
+    constexpr Geometry G = geometry<K, VB>();
+    uint32_t* bins = reinterpret_cast<uint32_t*>(temp + L.bins_off);
+    uint32_t* counters = reinterpret_cast<uint32_t*>(temp + L.counters_off);
+    uint32_t* lookback = reinterpret_cast<uint32_t*>(temp + L.lookback_off);
+
+    int st = launch_fill_u32(bins, L.clear_bytes / 4, 0u, stream);
+    if (st != kOk) return st;
+
+    const K* hist_src = db_keys ? db_keys[sel] : keys_in;
+    const unsigned hist_grid = static_cast<unsigned>(device_cu_count()) * 4;
+    for (uint32_t q = 0; q < L.portions; ++q) {
+        const uint32_t len = std::min(L.portion, n - q * L.portion);
+        const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(hist_grid, ceil_div(len, kHistBlock * kHistUnroll)));
+        LaunchScope scope("radix_histogram", stream);
+        histogram_kernel<K, DESC><<<grid, kHistBlock, 0, stream>>>(hist_src + static_cast<size_t>(q) * L.portion, len,
+                                                                   bins + static_cast<size_t>(q) * L.passes * kDigits,
+                                                                   begin_bit, end_bit, L.passes);
+        st = check_hip(hipGetLastError(), "radix_histogram launch");
+        if (st != kOk) return st;
+    }
+    {
+        LaunchScope scope("radix_bins_scan", stream);
+        bins_scan_kernel<<<1, kDigits, 0, stream>>>(bins, L.passes, L.portions);
+        st = check_hip(hipGetLastError(), "radix_bins_scan launch");
+        if (st != kOk) return st;
+    }
+
+    using VW = typename ValueWord<VB>::type;
+    for (uint32_t p = 0; p < L.passes; ++p) {
+        const K* src;
+        K* dst;
+        const void* vsrc;
+        void* vdst;
+        if (db_keys) {
+            src = db_keys[sel];
+            dst = db_keys[sel ^ 1];
+            vsrc = VB ? db_values[sel] : nullptr;
+            vdst = VB ? db_values[sel ^ 1] : nullptr;
+            sel ^= 1;
+        } else {
+            // The last pass writes keys_out; earlier passes alternate so that pass 0 reads keys_in.
+            const bool to_out = ((L.passes - 1 - p) % 2) == 0;
+            dst = to_out ? keys_out : keys_tmp;
+            vdst = to_out ? values_out : values_tmp;
+            if (p == 0) {
+                src = keys_in;
+                vsrc = values_in;
+            } else {
+                src = to_out ? keys_tmp : keys_out;
+                vsrc = to_out ? values_tmp : values_out;
+            }
+        }
+        const uint32_t shift = begin_bit + 8 * p;
+        const uint32_t nb = std::min(8u, end_bit - shift);
+        for (uint32_t q = 0; q < L.portions; ++q) {
+            const uint32_t len = std::min(L.portion, n - q * L.portion);
+            const uint32_t tiles = static_cast<uint32_t>(ceil_div(len, G.tile()));
+            st = launch_fill_u32(lookback, static_cast<uint64_t>(tiles) * kDigits, 0u, stream);
+            if (st != kOk) return st;
+            const size_t qoff = static_cast<size_t>(q) * L.portion;
+            LaunchScope scope("radix_onesweep", stream);
+            onesweep_kernel<K, DESC, VB, G.block, G.items><<<tiles, G.block, 0, stream>>>(
+                src + qoff, dst, VB ? static_cast<const VW*>(vsrc) + qoff : nullptr, vdst, len,
+                bins + (static_cast<size_t>(q) * L.passes + p) * kDigits, lookback, counters + q * L.passes + p, shift,
+                nb, n);
+            st = check_hip(hipGetLastError(), "radix_onesweep launch");
+            if (st != kOk) return st;
+        }
+    }
+    return kOk;
+}
+
+template <typename K, int VB>
+int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, const void* values_in, void* values_out,
+               K* db0, K* db1, void* vdb0, void* vdb1, int* selector, uint32_t n, uint32_t begin_bit, uint32_t end_bit,
+               int descending, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const bool db = selector != nullptr;
+    const char* what = VB ? "DeviceRadixSort::SortPairs" : "DeviceRadixSort::SortKeys";
+    if (begin_bit > end_bit) return set_error(kInvalidArgument, "%s: begin_bit must not exceed end_bit", what);
+    if (end_bit > sizeof(K) * 8) return set_error(kInvalidArgument, "%s: end_bit exceeds the key width", what);
+    if (db && *selector != 0 && *selector != 1)
+        return set_error(kInvalidArgument, "%s: DoubleBuffer selector must be 0 or 1", what);
+    if (n == 0) return kOk;
+    if (db) {
+        if (!db0 || !db1 || (VB && (!vdb0 || !vdb1))) return set_error(kInvalidArgument, "%s: null buffer", what);
+    } else {
+        if (!keys_in || !keys_out || (VB && (!values_in || !values_out)))
+            return set_error(kInvalidArgument, "%s: null buffer", what);
+    }
+    if (begin_bit == end_bit) {
+        if (db) return kOk;
+        int st = check_hip(hipMemcpyAsync(keys_out, keys_in, static_cast<size_t>(n) * sizeof(K), hipMemcpyDeviceToDevice,
+                                          stream), "key copy");
+        if (st != kOk || !VB) return st;
+        return check_hip(hipMemcpyAsync(values_out, values_in, static_cast<size_t>(n) * VB, hipMemcpyDeviceToDevice,
+                                        stream), "value copy");
+    }
+    constexpr Geometry G = geometry<K, VB>();
+    Layout L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, false);
+    if (temp_bytes < L.total) L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, true);
+    if (!temp || temp_bytes < L.total)
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, L.total);
+    if (reinterpret_cast<uintptr_t>(temp) % 4 != 0) return set_error(kInvalidArgument, "%s: temp not 4-byte aligned", what);
+    char* t = static_cast<char*>(temp);
+    K* keys_tmp = L.keys_tmp_off ? reinterpret_cast<K*>(t + L.keys_tmp_off) : nullptr;
+    void* values_tmp = L.values_tmp_off ? static_cast<void*>(t + L.values_tmp_off) : nullptr;
+    K* db_keys[2] = {db0, db1};
+    void* db_values[2] = {vdb0, vdb1};
+    const int sel = db ? *selector : 0;
+    int st;
+    if (descending)
+        st = launch_sort<K, true, VB>(t, L, keys_in, keys_out, values_in, values_out, keys_tmp, values_tmp,
+                                      db ? db_keys : nullptr, db ? db_values : nullptr, sel, n, begin_bit, end_bit, stream);
+    else
+        st = launch_sort<K, false, VB>(t, L, keys_in, keys_out, values_in, values_out, keys_tmp, values_tmp,
+                                       db ? db_keys : nullptr, db ? db_values : nullptr, sel, n, begin_bit, end_bit, stream);
+    if (st == kOk && db) *selector = (*selector) ^ static_cast<int>(L.passes & 1u);
+    return st;
+}
+
+}  // namespace radix
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+using namespace lcpp_hip::radix;
+
+extern "C" {
+
+int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion) {
+    g_portion_limit = max_items_per_portion;
+    return kOk;
+}
+
+uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes) {
+    (void)key_bytes;
+    (void)value_bytes;
+    return geometry<uint32_t, 0>().tile();
+}
+
+// Smallest temp storage this implementation accepts for the call (the compact-portion layout); it is
+// never more than the reference's Get*TempStorageBytes for the same sizes.
+size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
+                                            uint32_t end_bit, int double_buffer) {
+    if (n == 0 || begin_bit >= end_bit) return 0;
+    return make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, geometry<uint32_t, 0>().tile(), !double_buffer,
+                       true)
+        .total;
+}
+
+// Portions the sort would use with `temp_bytes` of temp storage (0 if it does not fit).
+uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
+                                          uint32_t end_bit, int double_buffer, size_t temp_bytes) {
+    if (n == 0 || begin_bit >= end_bit) return 0;
+    const uint32_t tile = geometry<uint32_t, 0>().tile();
+    Layout L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, false);
+    if (temp_bytes < L.total) L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, true);
+    return temp_bytes < L.total ? 0 : L.portions;
+}
+
+#define LCPP_HIP_DEFINE_SORT(S, K)                                                                                  \
+    int lcpp_hip_radix_sort_keys_##S(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, uint32_t n,       \
+                                     uint32_t begin_bit, uint32_t end_bit, int descending, void* stream) {           \
+        return sort_entry<K, 0>(temp, temp_bytes, keys_in, keys_out, nullptr, nullptr, nullptr, nullptr, nullptr,   \
+                                nullptr, nullptr, n, begin_bit, end_bit, descending, stream);                       \
+    }                                                                                                               \
+    int lcpp_hip_radix_sort_keys_db_##S(void* temp, size_t temp_bytes, K* keys0, K* keys1, int* selector, uint32_t n, \
+                                        uint32_t begin_bit, uint32_t end_bit, int descending, void* stream) {        \
+        if (!selector) return set_error(kInvalidArgument, "DeviceRadixSort::SortKeys: null selector");              \
+        return sort_entry<K, 0>(temp, temp_bytes, nullptr, nullptr, nullptr, nullptr, keys0, keys1, nullptr,        \
+                                nullptr, selector, n, begin_bit, end_bit, descending, stream);                      \
+    }                                                                                                               \
+    int lcpp_hip_radix_sort_pairs_##S##_v32(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out,           \
+                                            const void* values_in, void* values_out, uint32_t n, uint32_t begin_bit, \
+                                            uint32_t end_bit, int descending, void* stream) {                       \
+        return sort_entry<K, 4>(temp, temp_bytes, keys_in, keys_out, values_in, values_out, nullptr, nullptr,       \
+                                nullptr, nullptr, nullptr, n, begin_bit, end_bit, descending, stream);              \
+    }                                                                                                               \
+    int lcpp_hip_radix_sort_pairs_##S##_v64(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out,           \
+                                            const void* values_in, void* values_out, uint32_t n, uint32_t begin_bit, \
+                                            uint32_t end_bit, int descending, void* stream) {                       \
+        return sort_entry<K, 8>(temp, temp_bytes, keys_in, keys_out, values_in, values_out, nullptr, nullptr,       \
+                                nullptr, nullptr, nullptr, n, begin_bit, end_bit, descending, stream);              \
+    }                                                                                                               \
+    int lcpp_hip_radix_sort_pairs_db_##S##_v32(void* temp, size_t temp_bytes, K* keys0, K* keys1, void* values0,     \
+                                               void* values1, int* selector, uint32_t n, uint32_t begin_bit,        \
+                                               uint32_t end_bit, int descending, void* stream) {                    \
+        if (!selector) return set_error(kInvalidArgument, "DeviceRadixSort::SortPairs: null selector");             \
+        return sort_entry<K, 4>(temp, temp_bytes, nullptr, nullptr, nullptr, nullptr, keys0, keys1, values0,        \
+                                values1, selector, n, begin_bit, end_bit, descending, stream);                      \
+    }                                                                                                               \
+    int lcpp_hip_radix_sort_pairs_db_##S##_v64(void* temp, size_t temp_bytes, K* keys0, K* keys1, void* values0,     \
+                                               void* values1, int* selector, uint32_t n, uint32_t begin_bit,        \
+                                               uint32_t end_bit, int descending, void* stream) {                    \
+        if (!selector) return set_error(kInvalidArgument, "DeviceRadixSort::SortPairs: null selector");             \
+        return sort_entry<K, 8>(temp, temp_bytes, nullptr, nullptr, nullptr, nullptr, keys0, keys1, values0,        \
+                                values1, selector, n, begin_bit, end_bit, descending, stream);                      \
+    }
+
+LCPP_HIP_DEFINE_SORT(u32, uint32_t)
+LCPP_HIP_DEFINE_SORT(i32, int32_t)
+LCPP_HIP_DEFINE_SORT(f32, float)
+LCPP_HIP_DEFINE_SORT(u64, uint64_t)
+LCPP_HIP_DEFINE_SORT(i64, int64_t)
+LCPP_HIP_DEFINE_SORT(f64, double)
+#undef LCPP_HIP_DEFINE_SORT
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+// Runtime plumbing of the C-ABI: error strings, HIP error mapping, the fill kernel, per-kernel
+// event timing and device queries.  The reference's equivalent is `lcpp_check`
+// (runtime/core.h:56-67), which asserts in debug builds; here every entry point returns a status
+// code and keeps a thread-local message.
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace lcpp_hip {
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+struct ProfileRecord {
+    std::string name;
+    hipEvent_t begin;
+    hipEvent_t end;
+};
+
+struct ProfileState {
+    std::mutex mu;
+    bool enabled = false;
+    std::vector<ProfileRecord> pending;
+    std::map<std::string, std::pair<double, uint64_t>> totals;  // name -> (ms, launches)
+    std::vector<hipEvent_t> pool;
+
+    hipEvent_t take_event() {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+};
+
+ProfileState& profile() {
+    static ProfileState s;
+    return s;
+}
+}  // namespace
+
+int set_error(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return kOk;
+    return set_error(kHipError, "%s: %s", what, hipGetErrorString(e));
+}
+
+__global__ void fill_u32_kernel(uint32_t* dst, uint64_t count, uint32_t value) {
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (; i < count; i += stride) dst[i] = value;
+}
+
+int launch_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, hipStream_t stream) {
+    if (count == 0) return kOk;
+    const uint64_t blocks = ceil_div(count, 256);
+    const unsigned grid = static_cast<unsigned>(blocks < 4096 ? blocks : 4096);
+    LaunchScope scope("fill_u32", stream);
+    fill_u32_kernel<<<grid, 256, 0, stream>>>(dst, count, value);
+    return check_hip(hipGetLastError(), "fill_u32 launch");
+}
+
+LaunchScope::LaunchScope(const char* n, hipStream_t s) : name(n), stream(s), begin_event(nullptr) {
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    if (!p.enabled) return;
+    hipEvent_t e = p.take_event();
+    if (e && hipEventRecord(e, s) == hipSuccess) begin_event = e;
+}
+
+LaunchScope::~LaunchScope() {
+    if (!begin_event) return;
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    hipEvent_t e = p.take_event();
+    if (e && hipEventRecord(e, stream) == hipSuccess) {
+        p.pending.push_back({name, static_cast<hipEvent_t>(begin_event), e});
+    }
+}
+
+int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+const char* lcpp_hip_last_error(void) { return g_last_error; }
+
+const char* lcpp_hip_version(void) { return "lcpp-hip 0.1.0 (gfx950)"; }
+
+int lcpp_hip_profile_enable(int enable) {
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    p.enabled = enable != 0;
+    return kOk;
+}
+
+int lcpp_hip_profile_reset(void) {
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    for (auto& r : p.pending) {
+        p.pool.push_back(r.begin);
+        p.pool.push_back(r.end);
+    }
+    p.pending.clear();
+    p.totals.clear();
+    return kOk;
+}
+
+// Waits for every recorded launch and folds its duration into the per-kernel totals.
+static int profile_collect_locked(ProfileState& p) {
+    for (auto& r : p.pending) {
+        if (hipEventSynchronize(r.end) != hipSuccess) return set_error(kHipError, "profile: event sync failed");
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, r.begin, r.end) != hipSuccess) return set_error(kHipError, "profile: elapsed failed");
+        auto& t = p.totals[r.name];
+        t.first += ms;
+        t.second += 1;
+        p.pool.push_back(r.begin);
+        p.pool.push_back(r.end);
+    }
+    p.pending.clear();
+    return kOk;
+}
+
+int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches) {
+    if (!kernel || !total_ms || !launches) return set_error(kInvalidArgument, "profile_query: null argument");
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    int st = profile_collect_locked(p);
+    if (st != kOk) return st;
+    auto it = p.totals.find(kernel);
+    *total_ms = it == p.totals.end() ? 0.0 : it->second.first;
+    *launches = it == p.totals.end() ? 0 : it->second.second;
+    return kOk;
+}
+
+int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes) {
+    ProfileState& p = profile();
+    std::lock_guard<std::mutex> lock(p.mu);
+    int st = profile_collect_locked(p);
+    if (st != kOk) return st;
+    std::string all;
+    for (auto& kv : p.totals) {
+        all += kv.first;
+        all += '\n';
+    }
+    if (!buffer || buffer_bytes < all.size() + 1) return set_error(kInvalidArgument, "profile_names: buffer too small");
+    std::memcpy(buffer, all.c_str(), all.size() + 1);
+    return kOk;
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// DeviceSpmv::CsrMV for gfx950: y = A * x with A in CSR.
+//
+// Reference: DeviceSpmv<>::CsrMV (src/lcpp/device/device_spmv.h:48-130): one 32-lane warp per row,
+// lane-strided products, warp tree reduction, lane 0 writes y; rows with decreasing offsets or
+// offsets past nnz produce 0; columns >= num_cols are skipped; nnz == 0 writes zeros (:133-155).
+//
+// MI355X design (no temp storage, like the reference): each wave owns 64 consecutive rows.
+//   * Every lane reads its row's bounds (one coalesced load of 65 offsets per wave).
+//   * Rows with at most kShortRow nonzeros are summed by their own lane, in order.
+//   * Longer rows are taken one at a time by the whole wave: 64 lanes stride the row with coalesced
+//     value/column loads, then a DPP wave reduction; the row's lane writes y.
+//   Power-law row lengths therefore cost each wave about (longest short row) + sum(long/64) steps,
+//   instead of one 64-lane pass per row.
+// Floating-point order: short rows are summed left to right; long rows as 64 lane-strided partial
+// sums combined by the DPP scan tree.  Integer values wrap modulo 2^32.
+// Algorithmic traffic: nnz * (sizeof(V) + sizeof(I)) + (rows + 1) * sizeof(I) + rows * sizeof(V)
+// + gathered x (at least cols * sizeof(V)).
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+namespace lcpp_hip {
+namespace {
+
+constexpr int kSpmvBlock = 256;
+constexpr uint32_t kShortRow = 8;
+
+template <typename V> struct AccumType { using type = V; };
+template <> struct AccumType<int32_t> { using type = uint32_t; };
+
+template <typename V, typename I>
+__global__ __launch_bounds__(kSpmvBlock) void spmv_csr_kernel(const V* __restrict__ values,
+                                                              const I* __restrict__ row_offsets,
+                                                              const I* __restrict__ column_indices,
+                                                              const V* __restrict__ x, V* __restrict__ y,
+                                                              uint32_t rows, uint32_t cols, uint32_t nnz) {
+    using A = typename AccumType<V>::type;
+    const uint32_t lane = lane_id();
+    const uint64_t wave_global = (static_cast<uint64_t>(blockIdx.x) * kSpmvBlock + threadIdx.x) / kWave;
+    const uint64_t row64 = wave_global * kWave + lane;
+    const bool in_range = row64 < rows;
+    const uint32_t row = static_cast<uint32_t>(row64);
+
+    uint32_t begin = 0, end = 0;
+    if (in_range) {
+        begin = static_cast<uint32_t>(row_offsets[row]);
+        end = static_cast<uint32_t>(row_offsets[row + 1]);
+    }
+    const bool valid = in_range && begin <= end && end <= nnz;
+    const uint32_t len = valid ? end - begin : 0;
+
+    A acc = A(0);
+    const bool is_short = len <= kShortRow;
+    if (is_short) {
+        for (uint32_t e = begin; e < begin + len; ++e) {
+            const uint32_t c = static_cast<uint32_t>(column_indices[e]);
+            if (c < cols) acc += static_cast<A>(values[e]) * static_cast<A>(x[c]);
+        }
+    }
+
+    uint64_t long_rows = wave_ballot(!is_short);
+    while (long_rows) {
+        const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(long_rows));
+        long_rows &= long_rows - 1;
+        const uint32_t rb = __builtin_amdgcn_readlane(begin, src);
+        const uint32_t re = __builtin_amdgcn_readlane(end, src);
+        A part = A(0);
+        for (uint32_t e = rb + lane; e < re; e += kWave) {
+            const uint32_t c = static_cast<uint32_t>(column_indices[e]);
+            if (c < cols) part += static_cast<A>(values[e]) * static_cast<A>(x[c]);
+        }
+        part = wave_reduce(part, SumOp{});
+        if (lane == src) acc = part;
+    }
+    if (in_range) y[row] = static_cast<V>(acc);
+}
+
+template <typename V, typename I>
+int spmv_csr(void* /*temp*/, size_t /*temp_bytes*/, const V* values, const I* row_offsets, const I* column_indices,
+             const V* x, V* y, uint64_t rows, uint64_t cols, uint64_t nnz, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (rows > 0xFFFFFFFFull / 32) return set_error(kInvalidArgument, "DeviceSpmv: too many rows");
+    if (cols > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceSpmv: too many columns");
+    if (nnz > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceSpmv: too many nonzero values");
+    if (rows == 0) return kOk;
+    if (!y) return set_error(kInvalidArgument, "DeviceSpmv: null output vector");
+    if (nnz == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(y), rows * sizeof(V) / 4, 0u, stream);
+    if (!values || !row_offsets || !column_indices || !x)
+        return set_error(kInvalidArgument, "DeviceSpmv: null matrix or vector");
+    if (cols == 0) return set_error(kInvalidArgument, "DeviceSpmv: a matrix with zero columns cannot hold nonzeros");
+    const uint64_t waves = ceil_div(rows, kWave);
+    const uint64_t blocks = ceil_div(waves * kWave, kSpmvBlock);
+    LaunchScope scope("spmv_csr", stream);
+    spmv_csr_kernel<V, I><<<static_cast<unsigned>(blocks), kSpmvBlock, 0, stream>>>(
+        values, row_offsets, column_indices, x, y, static_cast<uint32_t>(rows), static_cast<uint32_t>(cols),
+        static_cast<uint32_t>(nnz));
+    return check_hip(hipGetLastError(), "spmv_csr launch");
+}
+
+}  // namespace
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+#define LCPP_HIP_DEFINE_SPMV(VS, VT, IS, IT)                                                                      \
+    int lcpp_hip_spmv_csr_##VS##_##IS(void* temp, size_t temp_bytes, const VT* values, const IT* row_offsets,     \
+                                      const IT* column_indices, const VT* x, VT* y, uint64_t rows, uint64_t cols, \
+                                      uint64_t nnz, void* stream) {                                               \
+        return spmv_csr<VT, IT>(temp, temp_bytes, values, row_offsets, column_indices, x, y, rows, cols, nnz,     \
+                                stream);                                                                          \
+    }
+LCPP_HIP_DEFINE_SPMV(f32, float, i32, int32_t)
+LCPP_HIP_DEFINE_SPMV(f32, float, u32, uint32_t)
+LCPP_HIP_DEFINE_SPMV(f64, double, i32, int32_t)
+LCPP_HIP_DEFINE_SPMV(f64, double, u32, uint32_t)
+LCPP_HIP_DEFINE_SPMV(i32, int32_t, i32, int32_t)
+LCPP_HIP_DEFINE_SPMV(i32, int32_t, u32, uint32_t)
+LCPP_HIP_DEFINE_SPMV(u32, uint32_t, i32, int32_t)
+LCPP_HIP_DEFINE_SPMV(u32, uint32_t, u32, uint32_t)
+#undef LCPP_HIP_DEFINE_SPMV
+
+}  // extern "C"

@@ -1,0 +1,251 @@
+"""ctypes binding of ``liblcpp_hip.so`` (the C-ABI declared in ``include/lcpp_hip.h``).
+
+Device memory and streams come from PyTorch (``tensor.data_ptr()``, ``torch.cuda.current_stream()``);
+every call goes straight to the HIP library.  There is no CPU fallback: if the library cannot be
+loaded, :func:`lib` raises.
+
+The operation names follow the reference API (``DeviceReduce::Sum``, ``DeviceScan::ExclusiveSum``,
+``DeviceRadixSort::SortKeys/SortPairs``, ``DeviceSpmv::CsrMV``; src/lcpp/device/*.h) and the
+temp-storage queries return the reference's ``Get*TempStorageBytes`` values.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import pathlib
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "liblcpp_hip.so"
+
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_TEMP_TOO_SMALL = -2
+ERR_HIP = -3
+ERR_UNSUPPORTED = -4
+
+GEN_U64, GEN_U32_HI, GEN_I32_PM1000, GEN_U32_LT16, GEN_U64_AND3, GEN_U32_IOTA, GEN_F32_PM1 = range(7)
+
+SCALAR_SUFFIXES = ("i32", "u32", "f32", "i64", "u64", "f64")
+SCAN_SUFFIXES = ("i32", "u32", "f32")
+SORT_KEY_SUFFIXES = ("u32", "i32", "f32", "u64", "i64", "f64")
+SPMV_SUFFIXES = [(v, i) for v in ("f32", "f64", "i32", "u32") for i in ("i32", "u32")]
+
+_CTYPE = {
+    "i32": C.c_int32, "u32": C.c_uint32, "f32": C.c_float,
+    "i64": C.c_int64, "u64": C.c_uint64, "f64": C.c_double,
+}
+ELEM_BYTES = {"i32": 4, "u32": 4, "f32": 4, "i64": 8, "u64": 8, "f64": 8}
+
+
+class LcppHipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"lcpp_hip status {status}: {message}")
+        self.status = status
+
+
+_lib = None
+
+
+def _declare(lib: C.CDLL) -> None:
+    vp, sz, u64, u32, i32 = C.c_void_p, C.c_size_t, C.c_uint64, C.c_uint32, C.c_int
+
+    def sig(name, res, *args):
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = list(args)
+
+    sig("lcpp_hip_version", C.c_char_p)
+    sig("lcpp_hip_last_error", C.c_char_p)
+    sig("lcpp_hip_profile_enable", i32, i32)
+    sig("lcpp_hip_profile_reset", i32)
+    sig("lcpp_hip_profile_query", i32, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64))
+    sig("lcpp_hip_profile_names", i32, C.c_char_p, sz)
+    sig("lcpp_hip_reduce_temp_bytes_policy", sz, u64, sz, u32, u32)
+    sig("lcpp_hip_reduce_temp_bytes", sz, u64, sz)
+    sig("lcpp_hip_scan_temp_bytes_policy", sz, u64, sz, u32, u32, i32, i32)
+    sig("lcpp_hip_scan_temp_bytes", sz, u64, sz)
+    sig("lcpp_hip_radix_sort_temp_bytes_policy", sz, u32, sz, sz, i32, u32, u32, i32)
+    sig("lcpp_hip_radix_sort_keys_temp_bytes", sz, u32, sz)
+    sig("lcpp_hip_radix_sort_pairs_temp_bytes", sz, u32, sz, sz)
+    sig("lcpp_hip_spmv_temp_bytes", sz, u64, u64, u64)
+    sig("lcpp_hip_radix_set_portion_limit", i32, u32)
+    sig("lcpp_hip_radix_tile_items", u32, sz, sz)
+    sig("lcpp_hip_internal_scan_needed_bytes", sz, u64)
+    sig("lcpp_hip_internal_radix_needed_bytes", sz, u32, sz, sz, u32, u32, i32)
+    sig("lcpp_hip_internal_radix_portions", u32, u32, sz, sz, u32, u32, i32, sz)
+    sig("lcpp_hip_generate", i32, i32, vp, u64, u64, u64, vp)
+    for s in SCALAR_SUFFIXES:
+        sig(f"lcpp_hip_reduce_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
+    for s in SCAN_SUFFIXES:
+        sig(f"lcpp_hip_scan_exclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
+        sig(f"lcpp_hip_scan_inclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
+        sig(f"lcpp_hip_scan_sum_init_{s}", i32, vp, sz, vp, vp, u64, i32, _CTYPE[s], vp)
+    for k in SORT_KEY_SUFFIXES:
+        sig(f"lcpp_hip_radix_sort_keys_{k}", i32, vp, sz, vp, vp, u32, u32, u32, i32, vp)
+        sig(f"lcpp_hip_radix_sort_keys_db_{k}", i32, vp, sz, vp, vp, C.POINTER(C.c_int), u32, u32, u32, i32, vp)
+        for v in ("v32", "v64"):
+            sig(f"lcpp_hip_radix_sort_pairs_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, u32, u32, u32, i32, vp)
+            sig(f"lcpp_hip_radix_sort_pairs_db_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, C.POINTER(C.c_int), u32, u32,
+                u32, i32, vp)
+    for v, i in SPMV_SUFFIXES:
+        sig(f"lcpp_hip_spmv_csr_{v}_{i}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, u64, vp)
+
+
+def lib() -> C.CDLL:
+    """Loads liblcpp_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: run `python luisacompute-parallelprimitive_amd/build.py`")
+        handle = C.CDLL(str(LIB_PATH), mode=os.RTLD_GLOBAL if hasattr(os, "RTLD_GLOBAL") else 0)
+        _declare(handle)
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise LcppHipError(status, lib().lcpp_hip_last_error().decode(errors="replace"))
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+def ptr(t) -> int | None:
+    """Device address of a torch tensor (None for an absent buffer)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_handle(stream=None) -> int | None:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+# ---- temp-storage queries (reference Get*TempStorageBytes) --------------------------------------
+def reduce_temp_bytes(n: int, elem_bytes: int, block: int = 256, items: int = 8) -> int:
+    return lib().lcpp_hip_reduce_temp_bytes_policy(n, elem_bytes, block, items)
+
+
+def scan_temp_bytes(n: int, elem_bytes: int) -> int:
+    return lib().lcpp_hip_scan_temp_bytes(n, elem_bytes)
+
+
+def sort_keys_temp_bytes(n: int, key_bytes: int) -> int:
+    return lib().lcpp_hip_radix_sort_keys_temp_bytes(n, key_bytes)
+
+
+def sort_pairs_temp_bytes(n: int, key_bytes: int, value_bytes: int) -> int:
+    return lib().lcpp_hip_radix_sort_pairs_temp_bytes(n, key_bytes, value_bytes)
+
+
+def bytes_to_uint_count(nbytes: int) -> int:
+    return (nbytes + 3) // 4
+
+
+# ---- operations on torch tensors ----------------------------------------------------------------
+def _temp(nbytes: int, device):
+    import torch
+    return torch.empty(max(1, bytes_to_uint_count(nbytes)), dtype=torch.int32, device=device)
+
+
+def reduce_sum(suffix: str, d_in, d_out, n: int, temp=None, stream=None) -> None:
+    """DeviceReduce::Sum over d_in[0:n) into d_out[0]."""
+    if temp is None:
+        temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    call(f"lcpp_hip_reduce_sum_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out), n,
+         stream_handle(stream))
+
+
+def scan_sum(suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=None, temp=None, stream=None) -> None:
+    """DeviceScan::ExclusiveSum / InclusiveSum (optionally with an initial value)."""
+    if temp is None:
+        temp = _temp(scan_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    tb = temp.numel() * temp.element_size()
+    if init is None:
+        kind = "inclusive" if inclusive else "exclusive"
+        call(f"lcpp_hip_scan_{kind}_sum_{suffix}", ptr(temp), tb, ptr(d_in), ptr(d_out), n, stream_handle(stream))
+    else:
+        call(f"lcpp_hip_scan_sum_init_{suffix}", ptr(temp), tb, ptr(d_in), ptr(d_out), n, int(inclusive),
+             _CTYPE[suffix](init), stream_handle(stream))
+
+
+def sort_keys(key_suffix: str, keys_in, keys_out, n: int, begin_bit: int = 0, end_bit: int | None = None,
+              descending: bool = False, temp=None, stream=None) -> None:
+    """DeviceRadixSort::SortKeys / SortKeysDescending (copy form)."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    if temp is None:
+        temp = _temp(sort_keys_temp_bytes(n, kb), keys_in.device)
+    call(f"lcpp_hip_radix_sort_keys_{key_suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(keys_in),
+         ptr(keys_out), n, begin_bit, end_bit, int(descending), stream_handle(stream))
+
+
+def sort_pairs(key_suffix: str, value_bytes: int, keys_in, keys_out, values_in, values_out, n: int,
+               begin_bit: int = 0, end_bit: int | None = None, descending: bool = False, temp=None,
+               stream=None) -> None:
+    """DeviceRadixSort::SortPairs / SortPairsDescending (copy form)."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    if temp is None:
+        temp = _temp(sort_pairs_temp_bytes(n, kb, value_bytes), keys_in.device)
+    v = "v32" if value_bytes == 4 else "v64"
+    call(f"lcpp_hip_radix_sort_pairs_{key_suffix}_{v}", ptr(temp), temp.numel() * temp.element_size(), ptr(keys_in),
+         ptr(keys_out), ptr(values_in), ptr(values_out), n, begin_bit, end_bit, int(descending),
+         stream_handle(stream))
+
+
+def sort_keys_db(key_suffix: str, buf0, buf1, selector: int, n: int, begin_bit: int = 0, end_bit: int | None = None,
+                 descending: bool = False, temp=None, stream=None) -> int:
+    """DeviceRadixSort::SortKeys(DoubleBuffer); returns the updated selector."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    if temp is None:
+        temp = _temp(sort_keys_temp_bytes(n, kb), buf0.device)
+    sel = C.c_int(selector)
+    call(f"lcpp_hip_radix_sort_keys_db_{key_suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(buf0),
+         ptr(buf1), C.byref(sel), n, begin_bit, end_bit, int(descending), stream_handle(stream))
+    return sel.value
+
+
+def sort_pairs_db(key_suffix: str, value_bytes: int, k0, k1, v0, v1, selector: int, n: int, begin_bit: int = 0,
+                  end_bit: int | None = None, descending: bool = False, temp=None, stream=None) -> int:
+    """DeviceRadixSort::SortPairs(DoubleBuffer, DoubleBuffer); returns the updated selector."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    if temp is None:
+        temp = _temp(sort_pairs_temp_bytes(n, kb, value_bytes), k0.device)
+    sel = C.c_int(selector)
+    v = "v32" if value_bytes == 4 else "v64"
+    call(f"lcpp_hip_radix_sort_pairs_db_{key_suffix}_{v}", ptr(temp), temp.numel() * temp.element_size(), ptr(k0),
+         ptr(k1), ptr(v0), ptr(v1), C.byref(sel), n, begin_bit, end_bit, int(descending), stream_handle(stream))
+    return sel.value
+
+
+def spmv_csr(value_suffix: str, index_suffix: str, values, row_offsets, column_indices, x, y, rows: int, cols: int,
+             nnz: int, stream=None) -> None:
+    """DeviceSpmv::CsrMV: y = A x (temp storage: 0 bytes)."""
+    call(f"lcpp_hip_spmv_csr_{value_suffix}_{index_suffix}", None, 0, ptr(values), ptr(row_offsets),
+         ptr(column_indices), ptr(x), ptr(y), rows, cols, nnz, stream_handle(stream))
+
+
+def generate(kind: int, out, n: int, seed: int, start: int = 0, stream=None) -> None:
+    call("lcpp_hip_generate", kind, ptr(out), n, seed, start, stream_handle(stream))
+
+
+# ---- per-kernel device time ---------------------------------------------------------------------
+def profile_enable(on: bool = True) -> None:
+    check(lib().lcpp_hip_profile_enable(int(on)))
+
+
+def profile_reset() -> None:
+    check(lib().lcpp_hip_profile_reset())
+
+
+def profile_query(kernel: str) -> tuple[float, int]:
+    ms, cnt = C.c_double(), C.c_uint64()
+    check(lib().lcpp_hip_profile_query(kernel.encode(), C.byref(ms), C.byref(cnt)))
+    return ms.value, cnt.value

@@ -1,0 +1,230 @@
+/*
+ * CPU oracle for the LCPP device hot path — TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library, and only
+ * as the checker (or the timed CPU baseline).  The product (liblcpp_hip.so) never calls it.
+ *
+ * The reference (LuisaCompute-ParallelPrimitive) cannot be built here: every header includes
+ * LuisaCompute (src/lcpp/runtime/core.h:10-13), which is fetched from the network at configure time
+ * (CMakeLists.txt:7-30) and whose CPU backend is disabled (CMakeLists.txt:24).  This file therefore
+ * restates the reference's semantics from its sources and tests; each function cites what it follows.
+ * How each function is pinned (golden vectors, closed forms, independent algorithms) is listed in
+ * tests/test_oracle.py.
+ *
+ * Conventions: sizes are uint64_t; integer sums wrap modulo 2^bits (two's complement), as the
+ * reference's int32/uint32 arithmetic does on the device.
+ */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+
+/* ------------------------------------------------------------------------------------------------
+ * Seeded streams.  splitmix64 (Steele, Lea, Flood 2014; the generator of java.util.SplittableRandom):
+ * r_i = mix(seed + (i + 1) * 0x9E3779B97F4A7C15).  Known answer: seed 0 gives 0xE220A8397B1DCDAF,
+ * 0x6E789E6AA1B965F4, 0x06C45D188009454F (tests/test_oracle.py).
+ * ---------------------------------------------------------------------------------------------- */
+uint64_t oracle_splitmix64_at(uint64_t seed, uint64_t index) {
+    uint64_t z = seed + (index + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* Same kinds and mappings as lcpp_hip_generate (include/lcpp_hip.h). */
+int oracle_generate(int kind, void* out, uint64_t n, uint64_t seed, uint64_t start) {
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t g = start + i;
+        switch (kind) {
+            case 0: ((uint64_t*)out)[i] = oracle_splitmix64_at(seed, g); break;
+            case 1: ((uint32_t*)out)[i] = (uint32_t)(oracle_splitmix64_at(seed, g) >> 32); break;
+            case 2: ((int32_t*)out)[i] = (int32_t)(oracle_splitmix64_at(seed, g) % 2001ull) - 1000; break;
+            case 3: ((uint32_t*)out)[i] = (uint32_t)(oracle_splitmix64_at(seed, g) & 15ull); break;
+            case 4:
+                ((uint64_t*)out)[i] = oracle_splitmix64_at(seed, 3 * g) & oracle_splitmix64_at(seed, 3 * g + 1) &
+                                      oracle_splitmix64_at(seed, 3 * g + 2);
+                break;
+            case 5: ((uint32_t*)out)[i] = (uint32_t)g; break;
+            case 6:
+                ((float*)out)[i] = (float)(uint32_t)(oracle_splitmix64_at(seed, g) >> 40) * (1.0f / 8388608.0f) - 1.0f;
+                break;
+            default: return -1;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * DeviceReduce::Sum (src/lcpp/device/device_reduce.h:280-288; n == 0 -> init = 0, :238-243).
+ * Integer sum is associative modulo 2^bits, so any order gives the device result:
+ * (int32) sum_int64.  Also reports the exact int64 sum (for the "int64-safe" check).
+ * ---------------------------------------------------------------------------------------------- */
+int32_t oracle_reduce_sum_i32(const int32_t* in, uint64_t n, int64_t* exact) {
+    int64_t s = 0;
+    for (uint64_t i = 0; i < n; ++i) s += in[i];
+    if (exact) *exact = s;
+    return (int32_t)(uint32_t)(uint64_t)s;
+}
+uint32_t oracle_reduce_sum_u32(const uint32_t* in, uint64_t n) {
+    uint32_t s = 0;
+    for (uint64_t i = 0; i < n; ++i) s += in[i];
+    return s;
+}
+uint64_t oracle_reduce_sum_u64(const uint64_t* in, uint64_t n) {
+    uint64_t s = 0;
+    for (uint64_t i = 0; i < n; ++i) s += in[i];
+    return s;
+}
+/* Floating-point: sum in long double plus the sum of magnitudes (for a condition-aware tolerance). */
+double oracle_reduce_sum_f32(const float* in, uint64_t n, double* abs_sum) {
+    long double s = 0, a = 0;
+    for (uint64_t i = 0; i < n; ++i) { s += in[i]; a += fabsl((long double)in[i]); }
+    if (abs_sum) *abs_sum = (double)a;
+    return (double)s;
+}
+double oracle_reduce_sum_f64(const double* in, uint64_t n, double* abs_sum) {
+    long double s = 0, a = 0;
+    for (uint64_t i = 0; i < n; ++i) { s += in[i]; a += fabsl((long double)in[i]); }
+    if (abs_sum) *abs_sum = (double)a;
+    return (double)s;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * DeviceScan::ExclusiveSum / InclusiveSum / InclusiveScanInit with a sum operator
+ * (src/lcpp/device/device_scan.h:321-422; tests compare with std::exclusive_scan,
+ * tests/device_scan_test.cpp:117-118).  Exclusive: out[i] = init + sum(in[0..i)); inclusive:
+ * out[i] = init + sum(in[0..i]).  32-bit words wrap (signed and unsigned share the bits).
+ * ---------------------------------------------------------------------------------------------- */
+void oracle_scan_sum_u32(const uint32_t* in, uint32_t* out, uint64_t n, int inclusive, uint32_t init) {
+    uint32_t run = init;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t x = in[i];
+        if (inclusive) { run += x; out[i] = run; }
+        else { out[i] = run; run += x; }
+    }
+}
+/* Floating-point scan in double (reference value for a tolerance check), plus running |x| sums. */
+void oracle_scan_sum_f32(const float* in, double* out, double* abs_out, uint64_t n, int inclusive, float init) {
+    double run = init, arun = fabs((double)init);
+    for (uint64_t i = 0; i < n; ++i) {
+        const double x = in[i];
+        if (inclusive) { run += x; arun += fabs(x); out[i] = run; abs_out[i] = arun; }
+        else { out[i] = run; abs_out[i] = arun; run += x; arun += fabs(x); }
+    }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * DeviceRadixSort: stable LSD radix sort with 8-bit digits, restated from
+ * onesweep_radix_sort (src/lcpp/device/device_radix_sort.h:1380-1472: passes from begin_bit in steps
+ * of 8, num_bit = min(end_bit - current_bit, 8)), the key twiddles (common/util_type.h:97-175;
+ * descending inverts, agent/radix_rank_sort_operations.h:123-155) and ShiftDigitExtractor with the
+ * float -0.0 -> +0.0 digit rule (radix_rank_sort_operations.h:18-62).  Keys keep their original bits.
+ * key_kind: 0 unsigned, 1 signed, 2 floating point.  key_bytes / value_bytes: 4 or 8 (value_bytes 0:
+ * keys only).  Each pass is a counting sort on one digit (stable by construction).
+ * ---------------------------------------------------------------------------------------------- */
+static uint64_t load_bits(const void* p, uint64_t i, int bytes) {
+    return bytes == 4 ? ((const uint32_t*)p)[i] : ((const uint64_t*)p)[i];
+}
+static void store_bits(void* p, uint64_t i, int bytes, uint64_t v) {
+    if (bytes == 4) ((uint32_t*)p)[i] = (uint32_t)v;
+    else ((uint64_t*)p)[i] = v;
+}
+
+uint64_t oracle_twiddle_in(uint64_t key, int key_bytes, int key_kind, int descending) {
+    const uint64_t all = key_bytes == 4 ? 0xFFFFFFFFull : ~0ull;
+    const uint64_t high = 1ull << (key_bytes * 8 - 1);
+    key &= all;
+    if (key_kind == 1) key ^= high;
+    if (key_kind == 2) key ^= (key & high) ? all : high;
+    if (descending) key = ~key & all;
+    return key;
+}
+
+uint32_t oracle_radix_digit(uint64_t key, int key_bytes, int key_kind, int descending, uint32_t shift, uint32_t bits) {
+    uint64_t o = oracle_twiddle_in(key, key_bytes, key_kind, descending);
+    if (key_kind == 2) {
+        const uint64_t all = key_bytes == 4 ? 0xFFFFFFFFull : ~0ull;
+        const uint64_t high = 1ull << (key_bytes * 8 - 1);
+        if (o == (all & ~high)) o = high; /* ordered image of -0.0 -> that of +0.0 */
+    }
+    return (uint32_t)(o >> shift) & ((1u << bits) - 1u);
+}
+
+int oracle_radix_sort(const void* keys_in, void* keys_out, const void* values_in, void* values_out, uint64_t n,
+                      int key_bytes, int key_kind, int value_bytes, uint32_t begin_bit, uint32_t end_bit,
+                      int descending) {
+    if ((key_bytes != 4 && key_bytes != 8) || (value_bytes != 0 && value_bytes != 4 && value_bytes != 8)) return -1;
+    if (begin_bit > end_bit || end_bit > (uint32_t)key_bytes * 8) return -1;
+    if (n == 0) return 0;
+    void* ka = malloc(n * key_bytes);
+    void* kb = malloc(n * key_bytes);
+    void* va = value_bytes ? malloc(n * value_bytes) : NULL;
+    void* vb = value_bytes ? malloc(n * value_bytes) : NULL;
+    if (!ka || !kb || (value_bytes && (!va || !vb))) { free(ka); free(kb); free(va); free(vb); return -2; }
+    memcpy(ka, keys_in, n * key_bytes);
+    if (value_bytes) memcpy(va, values_in, n * value_bytes);
+    for (uint32_t cur = begin_bit; cur < end_bit; cur += 8) {
+        const uint32_t bits = end_bit - cur < 8 ? end_bit - cur : 8;
+        uint64_t count[257];
+        memset(count, 0, sizeof(count));
+        for (uint64_t i = 0; i < n; ++i)
+            count[oracle_radix_digit(load_bits(ka, i, key_bytes), key_bytes, key_kind, descending, cur, bits) + 1]++;
+        for (int d = 0; d < 256; ++d) count[d + 1] += count[d];
+        for (uint64_t i = 0; i < n; ++i) {
+            const uint64_t k = load_bits(ka, i, key_bytes);
+            const uint64_t pos = count[oracle_radix_digit(k, key_bytes, key_kind, descending, cur, bits)]++;
+            store_bits(kb, pos, key_bytes, k);
+            if (value_bytes) store_bits(vb, pos, value_bytes, load_bits(va, i, value_bytes));
+        }
+        void* t = ka; ka = kb; kb = t;
+        t = va; va = vb; vb = t;
+    }
+    memcpy(keys_out, ka, n * key_bytes);
+    if (value_bytes) memcpy(values_out, va, n * value_bytes);
+    free(ka); free(kb); free(va); free(vb);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * DeviceSpmv::CsrMV (src/lcpp/device/device_spmv.h:48-130): rows whose offsets decrease or pass nnz
+ * give 0; columns >= cols are skipped; nnz == 0 gives zeros.
+ *  - f64 reference (long double accumulation) plus sum |a*x| per row (condition-aware tolerance),
+ *    for float/double values;
+ *  - exact wrap-around sums for 32-bit integer values (signed and unsigned share the bits).
+ * index_bytes 4 (int32 or uint32; negative int32 reads as a large unsigned column, as the reference's
+ * cast<uint> does).
+ * ---------------------------------------------------------------------------------------------- */
+void oracle_spmv_csr_fp(const void* values, int value_bytes, const uint32_t* row_offsets, const uint32_t* cols_idx,
+                        const void* x, double* y, double* abs_y, uint64_t rows, uint64_t cols, uint64_t nnz) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        long double s = 0, a = 0;
+        const uint32_t b = row_offsets[r], e = row_offsets[r + 1];
+        if (nnz != 0 && b <= e && e <= nnz) {
+            for (uint32_t i = b; i < e; ++i) {
+                const uint32_t c = cols_idx[i];
+                if (c >= cols) continue;
+                const long double v = value_bytes == 4 ? ((const float*)values)[i] : ((const double*)values)[i];
+                const long double xv = value_bytes == 4 ? ((const float*)x)[c] : ((const double*)x)[c];
+                s += v * xv;
+                a += fabsl(v * xv);
+            }
+        }
+        y[r] = (double)s;
+        if (abs_y) abs_y[r] = (double)a;
+    }
+}
+
+void oracle_spmv_csr_u32(const uint32_t* values, const uint32_t* row_offsets, const uint32_t* cols_idx,
+                         const uint32_t* x, uint32_t* y, uint64_t rows, uint64_t cols, uint64_t nnz) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        uint32_t s = 0;
+        const uint32_t b = row_offsets[r], e = row_offsets[r + 1];
+        if (nnz != 0 && b <= e && e <= nnz) {
+            for (uint32_t i = b; i < e; ++i) {
+                const uint32_t c = cols_idx[i];
+                if (c < cols) s += values[i] * x[c];
+            }
+        }
+        y[r] = s;
+    }
+}

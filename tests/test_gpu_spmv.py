@@ -1,0 +1,80 @@
+"""DeviceSpmv::CsrMV on the GPU: reference known answers (tests/device_spmv_test.cpp:41-203) exactly,
+32-bit integer matrices bit-exact against the oracle, and fp32/fp64 within the condition-aware bound
+|y - y_exact| <= 1e-5 * max(|y_exact|, sum_j |a_ij x_j|) (fp32) / 1e-12 * (...) (fp64)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import fill_dev, log, to_dev, to_host
+from test_oracle import reference_int_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_spmv(hip, vs, isfx, va, ro, ci, x, rows, cols, nnz, y_init=0x12345678):
+    y = fill_dev(rows, va.dtype.itemsize if va.size else 4, y_init)
+    hip.spmv_csr(vs, isfx, to_dev(va) if va.size else None, to_dev(ro), to_dev(ci) if ci.size else None,
+                 to_dev(x) if x.size else None, y, rows, cols, nnz)
+    return y
+
+
+def test_int_csr_known_answer(hip, orc, dev):
+    va, ro, ci, x, rows, cols, nnz = reference_int_csr()
+    y = gpu_spmv(hip, "i32", "i32", va, ro, ci, x, rows, cols, nnz)
+    expected = [sum(int(va[i]) * int(x[ci[i]]) for i in range(ro[r], ro[r + 1])) for r in range(rows)]
+    assert to_host(y, np.int32, rows).tolist() == expected
+
+
+def test_float_unsigned_index_known_answer(hip, dev):
+    ro = np.array([0, 3, 3, 6, 8], np.uint32)
+    ci = np.array([0, 2, 4, 1, 2, 3, 0, 4], np.uint32)
+    va = np.array([1.5, -2.0, 0.25, 3.0, 1.25, -0.5, 2.0, 4.0], np.float32)
+    x = np.array([2.0, -1.0, 0.5, 3.0, -2.0], np.float32)
+    y = to_host(gpu_spmv(hip, "f32", "u32", va, ro, ci, x, 4, 5, 8), np.float32, 4)
+    expected = [1.5 * 2 - 2.0 * 0.5 + 0.25 * -2, 0.0, -3.0 + 0.625 - 1.5, 4.0 - 8.0]
+    assert np.all(np.abs(y - np.array(expected)) < 1e-5)
+
+
+def test_empty_and_zero_matrix(hip, dev):
+    hip.spmv_csr("f32", "i32", None, None, None, None, None, 0, 0, 0)
+    ro = np.zeros(6, np.int32)
+    y = torch.full((5,), 42.0, dtype=torch.float32, device=dev)
+    hip.spmv_csr("f32", "i32", None, to_dev(ro), None, None, y, 5, 7, 0)
+    assert to_host(y, np.float32).tolist() == [0.0] * 5
+
+
+def random_csr(orc, rows, cols, seed, max_len):
+    rng = np.random.default_rng(seed)
+    lengths = np.minimum(rng.zipf(1.5, size=rows), max_len).astype(np.int64)
+    ro = np.zeros(rows + 1, np.int64)
+    ro[1:] = np.cumsum(lengths)
+    nnz = int(ro[-1])
+    ci = np.concatenate([np.sort(rng.choice(cols, size=int(L), replace=False)) for L in lengths]).astype(np.int32)
+    return ro.astype(np.int32), ci, nnz
+
+
+@pytest.mark.parametrize("vs,dtype,rel", [("f32", np.float32, 1e-5), ("f64", np.float64, 1e-12)])
+def test_power_law_rows_within_tolerance(hip, orc, dev, vs, dtype, rel):
+    rows, cols = 20000, 5000
+    ro, ci, nnz = random_csr(orc, rows, cols, 3, 2000)
+    log(f"spmv {vs} nnz={nnz}")
+    va = orc.generate(6, nnz, 4).astype(dtype)
+    x = orc.generate(6, cols, 5).astype(dtype)
+    y = to_host(gpu_spmv(hip, vs, "i32", va, ro, ci, x, rows, cols, nnz), dtype, rows).astype(np.float64)
+    ye, ay = orc.spmv_csr_fp(va, ro, ci, x, rows, cols, nnz)
+    assert np.all(np.abs(y - ye) <= rel * np.maximum(np.abs(ye), ay))
+
+
+@pytest.mark.parametrize("isfx", ["i32", "u32"])
+def test_integer_values_bit_exact_with_invalid_entries(hip, orc, dev, isfx):
+    rows, cols = 5000, 3000
+    ro, ci, nnz = random_csr(orc, rows, cols, 8, 700)
+    ci = ci.copy()
+    ci[::97] = cols + 5          # out-of-range columns are skipped
+    ro = ro.copy()
+    ro[100] = ro[101] + 1        # row 99 and row 100 get invalid (decreasing) bounds
+    va = orc.generate(1, nnz, 9)
+    x = orc.generate(1, cols, 10)
+    y = gpu_spmv(hip, "u32", isfx, va, ro.view(np.uint32) if isfx == "u32" else ro,
+                 ci.view(np.uint32) if isfx == "u32" else ci, x, rows, cols, nnz)
+    assert np.array_equal(to_host(y, np.uint32, rows), orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz))

@@ -1,0 +1,261 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against (a) the known-answer cases of the reference's own tests
+(paths relative to the LCPP root), (b) closed forms, and (c) an independent algorithm (numpy / Python
+comparison sorts), chosen so that a dropped term, a wrong sign or index, or a wrong twiddle fails.
+"""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+
+# ---- splitmix64 ----------------------------------------------------------------------------------
+def test_splitmix64_known_answers(orc):
+    # Published SplittableRandom / splitmix64 outputs for seed 0.
+    assert orc.splitmix64_at(0, 0) == 0xE220A8397B1DCDAF
+    assert orc.splitmix64_at(0, 1) == 0x6E789E6AA1B965F4
+    assert orc.splitmix64_at(0, 2) == 0x06C45D188009454F
+
+
+def test_generator_mappings(orc):
+    seed = 114521
+    r = orc.generate(0, 1000, seed)
+    assert np.array_equal(orc.generate(1, 1000, seed), (r >> np.uint64(32)).astype(np.uint32))
+    pm = orc.generate(2, 1000, seed)
+    assert np.array_equal(pm, (r % np.uint64(2001)).astype(np.int64) - 1000)
+    assert pm.min() >= -1000 and pm.max() <= 1000
+    assert np.array_equal(orc.generate(3, 1000, seed), (r & np.uint64(15)).astype(np.uint32))
+    r3 = orc.generate(0, 3000, seed)
+    assert np.array_equal(orc.generate(4, 1000, seed), r3[0::3] & r3[1::3] & r3[2::3])
+    assert np.array_equal(orc.generate(5, 10, seed, start=7), np.arange(7, 17, dtype=np.uint32))
+    # counter-based: a window equals the slice of a longer stream
+    assert np.array_equal(orc.generate(0, 10, seed, start=500), r[500:510])
+
+
+# ---- reduce --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("k", range(0, 24, 3))
+def test_reduce_ones_known_answer(orc, k):
+    # tests/device_reduce_test.cpp:95-119: Sum of 2^k+1 ones is 2^k+1.
+    n = (1 << k) + 1
+    assert orc.reduce_sum_i32(np.ones(n, np.int32)) == (n, n)
+
+
+def test_reduce_shuffled_iota_and_empty(orc):
+    # tests/device_reduce_test.cpp:85-91: shuffled iota 0..4095.
+    a = np.random.default_rng(114521).permutation(4096).astype(np.int32)
+    assert orc.reduce_sum_i32(a)[0] == 4095 * 4096 // 2
+    assert orc.reduce_sum_i32(np.zeros(0, np.int32)) == (0, 0)
+
+
+def test_reduce_wraps_modulo_2_32(orc):
+    a = np.full(3, 2**31 - 1, np.int32)
+    wrapped, exact = orc.reduce_sum_i32(a)
+    assert exact == 3 * (2**31 - 1)
+    assert wrapped == ((exact + 2**31) % 2**32) - 2**31
+    assert orc.reduce_sum_u32(np.array([2**32 - 1, 2], np.uint32)) == 1
+    assert orc.reduce_sum_u64(np.array([2**64 - 1, 5], np.uint64)) == 4
+
+
+def test_reduce_closed_form_random(orc):
+    a = orc.generate(2, 1 << 20, 114521)
+    assert orc.reduce_sum_i32(a)[1] == int(a.astype(np.int64).sum())
+    f = orc.generate(6, 10000, 7)
+    s, absum = orc.reduce_sum_fp(f)
+    assert math.isclose(s, math.fsum(f.astype(np.float64)), rel_tol=0, abs_tol=1e-9)
+    assert math.isclose(absum, math.fsum(np.abs(f.astype(np.float64))), rel_tol=1e-12)
+
+
+# ---- scan ----------------------------------------------------------------------------------------
+@pytest.mark.parametrize("i", [0, 1, 5, 12, 17])
+def test_scan_ones_known_answer(orc, i):
+    # tests/device_scan_test.cpp:80-127: exclusive sum of 2^i ones is iota, inclusive is iota+1.
+    n = 1 << i
+    ones = np.ones(n, np.uint32)
+    assert np.array_equal(orc.scan_sum_u32(ones), np.arange(n, dtype=np.uint32))
+    assert np.array_equal(orc.scan_sum_u32(ones, inclusive=True), np.arange(1, n + 1, dtype=np.uint32))
+
+
+def test_scan_inclusive_init_known_answer(orc):
+    # tests/device_scan_test.cpp:288-321: InclusiveScanInit {1,2,3,4} + 10 -> {11,13,16,20}.
+    a = np.array([1, 2, 3, 4], np.int32)
+    assert orc.scan_sum_u32(a, inclusive=True, init=10).tolist() == [11, 13, 16, 20]
+
+
+def test_scan_matches_cumsum_with_wrap(orc):
+    # (i % 7) - 3 data of tests/device_scan_test.cpp:189-265 and tests/lcpp_cub_bench.cpp:666-672.
+    n = 100003
+    a = ((np.arange(n) % 7) - 3).astype(np.int32)
+    ref = np.concatenate([[0], np.cumsum(a.astype(np.int64))[:-1]])
+    assert np.array_equal(orc.scan_sum_u32(a).astype(np.int64), ref)
+    big = np.full(10, 2**31, np.uint32)
+    got = orc.scan_sum_u32(big, inclusive=True)
+    assert got.tolist() == [(2**31 * (i + 1)) % 2**32 for i in range(10)]
+
+
+# ---- radix sort ----------------------------------------------------------------------------------
+def _stable_order(keys, keyfunc):
+    return sorted(range(len(keys)), key=lambda i: keyfunc(keys[i]))
+
+
+def test_radix_partial_bits_known_answer(orc):
+    # tests/device_radix_sort_interface_test.cpp:68-159: 257 items, bits [1, 6), asc/desc, pairs.
+    n, b, e = 257, 1, 6
+    keys = np.array([((i * 53) % 64) | (((i * 17) % 11) << 8) for i in range(n)], np.uint32)
+    vals = np.arange(n, dtype=np.uint32)
+    sel = lambda k: (int(k) >> b) & ((1 << (e - b)) - 1)
+    asc = _stable_order(keys, sel)
+    desc = _stable_order(keys, lambda k: -sel(k))
+    assert np.array_equal(orc.radix_sort(keys, begin_bit=b, end_bit=e), keys[asc])
+    assert np.array_equal(orc.radix_sort(keys, begin_bit=b, end_bit=e, descending=True), keys[desc])
+    ko, vo = orc.radix_sort(keys, vals, begin_bit=b, end_bit=e)
+    assert np.array_equal(ko, keys[asc]) and np.array_equal(vo, vals[asc])
+    ko, vo = orc.radix_sort(keys, vals, begin_bit=b, end_bit=e, descending=True)
+    assert np.array_equal(ko, keys[desc]) and np.array_equal(vo, vals[desc])
+
+
+def test_radix_double_buffer_case_known_answer(orc):
+    # tests/device_radix_sort_interface_test.cpp:205-283: 65 items, bits [0, 5).
+    n = 65
+    keys = np.array([((i * 19) % 32) | ((i % 7) << 8) for i in range(n)], np.uint32)
+    asc = _stable_order(keys, lambda k: int(k) & 31)
+    assert np.array_equal(orc.radix_sort(keys, begin_bit=0, end_bit=5), keys[asc])
+
+
+def test_radix_u64_reversed_known_answer(orc):
+    # tests/device_radix_sort_one_sweep.cpp:175-205: 65,536 u64 keys (n-i-1)*2654435761.
+    n = 65536
+    keys = ((n - np.arange(n, dtype=np.uint64) - 1) * np.uint64(2654435761)).astype(np.uint64)
+    assert np.array_equal(orc.radix_sort(keys), np.sort(keys))
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.int32, np.uint64, np.int64])
+@pytest.mark.parametrize("descending", [False, True])
+def test_radix_integer_keys_vs_numpy_stable(orc, dtype, descending):
+    rng = np.random.default_rng(5)
+    n = 20000
+    info = np.iinfo(dtype)
+    keys = rng.integers(info.min, info.max, size=n, dtype=dtype, endpoint=True)
+    keys[::7] = keys[3]  # many duplicates for the stability check
+    vals = np.arange(n, dtype=np.uint32)
+    if descending:
+        order = sorted(range(n), key=lambda i: -int(keys[i]))
+    else:
+        order = np.argsort(keys, kind="stable")
+    ko, vo = orc.radix_sort(keys, vals, descending=descending)
+    assert np.array_equal(ko, keys[order])
+    assert np.array_equal(vo, vals[order])
+
+
+def test_radix_float_keys_total_order(orc):
+    # Float twiddle (common/util_type.h:141-175): -NaN < -inf < ... < -0.0 == +0.0 < ... < +inf < +NaN,
+    # with -0.0 and +0.0 ranked as equal keys (agent/radix_rank_sort_operations.h:31-42), so they
+    # keep their input order.
+    neg_nan = struct.unpack("<f", struct.pack("<I", 0xFFC00000))[0]
+    pos_nan = struct.unpack("<f", struct.pack("<I", 0x7FC00000))[0]
+    keys = np.array([1.5, -0.0, 0.0, -2.0, float("inf"), pos_nan, -0.0, float("-inf"), neg_nan, 0.0, -1e-30],
+                    np.float32)
+    bits = keys.view(np.uint32)
+    vals = np.arange(keys.size, dtype=np.uint32)
+    ko, vo = orc.radix_sort(keys, vals)
+    assert vo.tolist() == [8, 7, 3, 10, 1, 2, 6, 9, 0, 4, 5]
+    assert np.array_equal(ko.view(np.uint32), bits[vo])
+    ko, vo = orc.radix_sort(keys, vals, descending=True)
+    assert vo.tolist() == [5, 4, 0, 1, 2, 6, 9, 10, 3, 7, 8]
+
+
+def test_radix_float_keys_vs_python_sort(orc):
+    rng = np.random.default_rng(9)
+    keys = rng.standard_normal(5000).astype(np.float32)
+    keys[::5] = 0.0
+    keys[1::11] = -0.0
+    vals = np.arange(keys.size, dtype=np.uint32)
+    for desc in (False, True):
+        order = sorted(range(keys.size), key=lambda i: (-1 if desc else 1) * float(keys[i]))
+        ko, vo = orc.radix_sort(keys, vals, descending=desc)
+        assert vo.tolist() == order
+        kd = rng.standard_normal(3000)
+        od = sorted(range(kd.size), key=lambda i: (-1 if desc else 1) * float(kd[i]))
+        assert np.array_equal(orc.radix_sort(kd, descending=desc), kd[od])
+
+
+def test_radix_brute_force_tiny(orc):
+    rng = np.random.default_rng(11)
+    for n in range(0, 40):
+        keys = rng.integers(0, 4, size=n).astype(np.uint32)
+        vals = np.arange(n, dtype=np.uint32)
+        ko, vo = orc.radix_sort(keys, vals)
+        # brute force: rank of i = #{j: k_j < k_i} + #{j < i: k_j == k_i}
+        exp = np.empty(n, np.uint32)
+        for i in range(n):
+            r = int(np.sum(keys < keys[i]) + np.sum(keys[:i] == keys[i]))
+            exp[r] = i
+        assert np.array_equal(vo, exp)
+
+
+def test_radix_digit_known_values(orc):
+    # signed: 0x80000000 (INT_MIN) is the smallest ordered key; descending inverts.
+    assert orc.radix_digit(0x80000000, np.int32, False, 24, 8) == 0x00
+    assert orc.radix_digit(0x7FFFFFFF, np.int32, False, 24, 8) == 0xFF
+    assert orc.radix_digit(0x80000000, np.int32, True, 24, 8) == 0xFF
+    # float -0.0 digits equal +0.0 digits in both directions
+    for d in (False, True):
+        for s in (0, 8, 16, 24):
+            assert orc.radix_digit(0x80000000, np.float32, d, s, 8) == orc.radix_digit(0, np.float32, d, s, 8)
+
+
+# ---- spmv ----------------------------------------------------------------------------------------
+def reference_int_csr():
+    """tests/device_spmv_test.cpp:41-108 (8x13 int CSR with row lengths {0,1,5,33,2,64,0,7})."""
+    rows, cols = 8, 13
+    lengths = [0, 1, 5, 33, 2, 64, 0, 7]
+    ro = np.zeros(rows + 1, np.int32)
+    for r in range(rows):
+        ro[r + 1] = ro[r] + lengths[r]
+    nnz = int(ro[-1])
+    ci = np.zeros(nnz, np.int32)
+    va = np.zeros(nnz, np.int32)
+    for r in range(rows):
+        for it in range(lengths[r]):
+            idx = ro[r] + it
+            ci[idx] = (r * 5 + it * 7) % cols
+            va[idx] = ((r + it * 3) % 9) - 4
+    x = np.arange(cols, dtype=np.int32) - 6
+    return va, ro, ci, x, rows, cols, nnz
+
+
+def test_spmv_int_known_answer(orc):
+    va, ro, ci, x, rows, cols, nnz = reference_int_csr()
+    expected = [sum(int(va[i]) * int(x[ci[i]]) for i in range(ro[r], ro[r + 1])) for r in range(rows)]
+    got = orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz).view(np.int32)
+    assert got.tolist() == expected
+    # dense cross-check
+    dense = np.zeros((rows, cols), np.int64)
+    for r in range(rows):
+        for i in range(ro[r], ro[r + 1]):
+            dense[r, ci[i]] += va[i]
+    assert (dense @ x.astype(np.int64)).tolist() == expected
+
+
+def test_spmv_float_known_answer(orc):
+    # tests/device_spmv_test.cpp:110-155.
+    ro = np.array([0, 3, 3, 6, 8], np.uint32)
+    ci = np.array([0, 2, 4, 1, 2, 3, 0, 4], np.uint32)
+    va = np.array([1.5, -2.0, 0.25, 3.0, 1.25, -0.5, 2.0, 4.0], np.float32)
+    x = np.array([2.0, -1.0, 0.5, 3.0, -2.0], np.float32)
+    y, ay = orc.spmv_csr_fp(va, ro, ci, x, 4, 5, 8)
+    assert y.tolist() == [1.5 * 2 - 2.0 * 0.5 + 0.25 * -2, 0.0, -3.0 + 0.625 - 1.5, 4.0 - 8.0]
+    assert ay[0] == 3.0 + 1.0 + 0.5
+
+
+def test_spmv_invalid_rows_and_columns(orc):
+    # device_spmv.h:97-108: decreasing offsets or offsets past nnz -> 0; columns >= cols skipped.
+    ro = np.array([0, 2, 1, 4, 9], np.uint32)
+    ci = np.array([0, 5, 1, 2], np.uint32)
+    va = np.array([1, 2, 3, 4], np.uint32)
+    x = np.array([10, 20, 30], np.uint32)
+    y = orc.spmv_csr_u32(va, ro, ci, x, 4, 3, 4)
+    assert y.tolist() == [10, 0, 3 * 20 + 4 * 30, 0]
+    zero = orc.spmv_csr_u32(va, np.zeros(5, np.uint32), ci, x, 4, 3, 0)
+    assert zero.tolist() == [0, 0, 0, 0]
