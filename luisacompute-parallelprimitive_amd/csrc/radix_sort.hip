@@ -21,8 +21,11 @@
 //   * Keys are reordered by digit in LDS and written out from LDS in order, so consecutive lanes
 //     write consecutive addresses inside each digit's run.  Pairs move values the same way.
 //   * Portions: one launch ranks at most 2^30 - tile keys so look-back counts fit in 30 bits.  The
-//     histogram keeps per-portion counts, and the bin scan turns them into per-portion global
-//     offsets (total of smaller digits + counts of the same digit in earlier portions).
+//     upfront histogram gives each pass's global digit offsets for portion 0.  Within a pass, the
+//     last tile of portion q holds the inclusive count of every digit in that portion and writes
+//     portion q+1's offsets (offset + count); the next launch reads them.  (The reference intends the
+//     same carry, but selects the writing block by `(block+1) * RADIX_DIGITS >= n`,
+//     agent/agent_radix_sort_onesweep.h:362, so it never fires for large inputs.)
 // Algorithmic traffic per pass: n * 2 * (sizeof(K) + sizeof(V)) bytes; the histogram reads n*sizeof(K).
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
@@ -145,26 +148,20 @@ __global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restri
     }
 }
 
-// In place: counts[q][p][d] -> global output offset of digit d of pass p for portion q.
-__global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict__ bins, uint32_t passes,
-                                                            uint32_t portions) {
+// In place: counts[p][d] -> exclusive scan over d, the first output position of digit d in pass p
+// (device/details/radix_sort.h:81-123).
+__global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict__ bins, uint32_t passes) {
     __shared__ uint32_t s_wave_totals[kDigits / kWave];
     const uint32_t d = threadIdx.x;
     const uint32_t wave = d / kWave;
     for (uint32_t p = 0; p < passes; ++p) {
-        uint32_t total = 0;
-        for (uint32_t q = 0; q < portions; ++q) total += bins[(q * passes + p) * kDigits + d];
-        const uint32_t incl = wave_inclusive_scan(total, SumOp{});
+        const uint32_t count = bins[p * kDigits + d];
+        const uint32_t incl = wave_inclusive_scan(count, SumOp{});
         if (lane_id() == kWave - 1) s_wave_totals[wave] = incl;
         __syncthreads();
-        uint32_t run = incl - total;
+        uint32_t run = incl - count;
         for (uint32_t w = 0; w < wave; ++w) run += s_wave_totals[w];
-        for (uint32_t q = 0; q < portions; ++q) {
-            uint32_t* cell = &bins[(q * passes + p) * kDigits + d];
-            const uint32_t c = *cell;
-            *cell = run;
-            run += c;
-        }
+        bins[p * kDigits + d] = run;
         __syncthreads();
     }
 }
@@ -177,6 +174,7 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
                                                          const void* __restrict__ values_in,
                                                          void* __restrict__ values_out, uint32_t n,
                                                          const uint32_t* __restrict__ digit_offsets,
+                                                         uint32_t* __restrict__ next_offsets,
                                                          uint32_t* __restrict__ lookback,
                                                          uint32_t* __restrict__ counter, uint32_t shift,
                                                          uint32_t num_bits, uint32_t out_items) {
@@ -275,8 +273,8 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
 
         // Look-back over earlier tiles of this digit.
         uint32_t excl = 0;
+        const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
         if (tile > 0) {
-            const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
             int64_t t = static_cast<int64_t>(tile) - 1;
             while (true) {
                 const uint32_t v = atomic_load_agent(&lookback[static_cast<uint64_t>(t) * kDigits + d]);
@@ -290,7 +288,10 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
             }
             atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
         }
-        s_global_minus_local[d] = digit_offsets[d] + excl - local_start;
+        const uint32_t base = digit_offsets[d];
+        // Carry to the next portion of this pass: first position of digit d after this portion.
+        if (next_offsets != nullptr && tile == gridDim.x - 1) next_offsets[d] = base + excl + real;
+        s_global_minus_local[d] = base + excl - local_start;
     }
     __syncthreads();
 
@@ -415,15 +416,15 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         const uint32_t len = std::min(L.portion, n - q * L.portion);
         const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(hist_grid, ceil_div(len, kHistBlock * kHistUnroll)));
         LaunchScope scope("radix_histogram", stream);
+        // Every portion adds into the totals of portion 0's slots.
         histogram_kernel<K, DESC><<<grid, kHistBlock, 0, stream>>>(hist_src + static_cast<size_t>(q) * L.portion, len,
-                                                                   bins + static_cast<size_t>(q) * L.passes * kDigits,
-                                                                   begin_bit, end_bit, L.passes);
+                                                                   bins, begin_bit, end_bit, L.passes);
         st = check_hip(hipGetLastError(), "radix_histogram launch");
         if (st != kOk) return st;
     }
     {
         LaunchScope scope("radix_bins_scan", stream);
-        bins_scan_kernel<<<1, kDigits, 0, stream>>>(bins, L.passes, L.portions);
+        bins_scan_kernel<<<1, kDigits, 0, stream>>>(bins, L.passes);
         st = check_hip(hipGetLastError(), "radix_bins_scan launch");
         if (st != kOk) return st;
     }
@@ -464,8 +465,9 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             LaunchScope scope("radix_onesweep", stream);
             onesweep_kernel<K, DESC, VB, G.block, G.items><<<tiles, G.block, 0, stream>>>(
                 src + qoff, dst, VB ? static_cast<const VW*>(vsrc) + qoff : nullptr, vdst, len,
-                bins + (static_cast<size_t>(q) * L.passes + p) * kDigits, lookback, counters + q * L.passes + p, shift,
-                nb, n);
+                bins + (static_cast<size_t>(q) * L.passes + p) * kDigits,
+                q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr, lookback,
+                counters + q * L.passes + p, shift, nb, n);
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }

@@ -25,13 +25,13 @@ def gpu_sort(hip, keys, values=None, begin_bit=0, end_bit=None, descending=False
     kout = fill_dev(n, keys.dtype.itemsize, -1)
     if values is None:
         hip.sort_keys(sfx, kin, kout, n, begin_bit, end_bit, descending)
-        assert np.array_equal(to_host(kin, keys.dtype, n), keys), "input keys were modified"
+        check_bits(to_host(kin, keys.dtype, n), keys)  # the copy form never writes its input
         return to_host(kout, keys.dtype, n)
     vin = to_dev(values)
     vout = fill_dev(n, values.dtype.itemsize, -1)
     hip.sort_pairs(sfx, values.dtype.itemsize, kin, kout, vin, vout, n, begin_bit, end_bit, descending)
-    assert np.array_equal(to_host(kin, keys.dtype, n), keys), "input keys were modified"
-    assert np.array_equal(to_host(vin, values.dtype, n), values), "input values were modified"
+    check_bits(to_host(kin, keys.dtype, n), keys)
+    check_bits(to_host(vin, values.dtype, n), values)
     return to_host(kout, keys.dtype, n), to_host(vout, values.dtype, n)
 
 
