@@ -47,6 +47,14 @@ int lcpp_hip_profile_reset(void);
 int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches);
 int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes);
 
+/* Polls of a look-back predecessor that has not published yet before the waiting workgroup computes
+ * that predecessor's contribution from the input itself (scan and onesweep sort).  Any value is
+ * correct; 0 takes the fallback at once (used by tests), the default is 64.  Process-wide.
+ * No reference counterpart (the reference spins until the predecessor publishes,
+ * device/details/single_pass_scan_operator.h:96-113, agent/agent_radix_sort_onesweep.h:309-357). */
+int lcpp_hip_set_lookback_spin_limit(uint32_t polls);
+uint32_t lcpp_hip_get_lookback_spin_limit(void);
+
 /* ---------------------------------------------------------------------------------------------
  * DeviceReduce::Sum
  * replaces DeviceReduce<>::Sum (src/lcpp/device/device_reduce.h:280-288) and its temp query

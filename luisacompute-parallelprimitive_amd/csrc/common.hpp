@@ -173,4 +173,8 @@ int launch_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, hipStream_t s
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Polls of an INVALID look-back predecessor before the waiting workgroup computes that
+// predecessor's contribution itself (0: at once).  Shared by the scan and the onesweep sort.
+extern uint32_t g_lookback_spin_limit;
+
 }  // namespace lcpp_hip

@@ -40,6 +40,9 @@ constexpr uint32_t kFlagPartial = 1u << 30;
 constexpr uint32_t kFlagInclusive = 2u << 30;
 constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
+constexpr int kRankBallot = 0;
+constexpr int kRankLdsMatch = 1;
+constexpr int kLookbackWindow = 16;  // predecessor tiles inspected per look-back step
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
@@ -169,15 +172,35 @@ __global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict
 // --------------------------------------------------------------------------------------------
 // Onesweep pass.
 // --------------------------------------------------------------------------------------------
-template <typename K, bool DESC, int VB, int BLOCK, int ITEMS>
-__global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ keys_in, K* __restrict__ keys_out,
+
+// Look-back fallback: digit counts of the full tile `tile` of `keys`, accumulated in LDS `counts`
+// (256 words).  Called by every thread of the workgroup.
+template <typename K, bool DESC, int BLOCK, int ITEMS>
+__device__ void tile_digit_counts(const K* __restrict__ keys, uint32_t tile, uint32_t shift, uint32_t mask,
+                                  uint32_t* counts) {
+    using U = typename KeyTraits<K>::U;
+    constexpr int KIND = KeyTraits<K>::kind;
+    constexpr uint32_t TILE = static_cast<uint32_t>(BLOCK) * ITEMS;
+    for (uint32_t i = threadIdx.x; i < kDigits; i += BLOCK) counts[i] = 0;
+    __syncthreads();
+    const U* ukeys = reinterpret_cast<const U*>(keys) + static_cast<uint64_t>(tile) * TILE;
+    for (uint32_t i = threadIdx.x; i < TILE; i += BLOCK) {
+        const U ordered = twiddle_in<U, KIND, DESC>(ukeys[i]);
+        atomicAdd(&counts[digit_of<U, KIND>(ordered, shift, mask)], 1u);
+    }
+    __syncthreads();
+}
+template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int RANK>
+// Two workgroups per CU: at most 128 VGPRs (4 waves per SIMD).
+__global__ __launch_bounds__(BLOCK, 2 * BLOCK / kWave / 4) void onesweep_kernel(const K* __restrict__ keys_in,
+                                                                               K* __restrict__ keys_out,
                                                          const void* __restrict__ values_in,
                                                          void* __restrict__ values_out, uint32_t n,
                                                          const uint32_t* __restrict__ digit_offsets,
                                                          uint32_t* __restrict__ next_offsets,
-                                                         uint32_t* __restrict__ lookback,
-                                                         uint32_t* __restrict__ counter, uint32_t shift,
-                                                         uint32_t num_bits, uint32_t out_items) {
+                                                         uint32_t* __restrict__ lookback, uint32_t shift,
+                                                         uint32_t num_bits, uint32_t out_items,
+                                                         uint32_t spin_limit) {
     using U = typename KeyTraits<K>::U;
     using VW = typename ValueWord<VB>::type;
     constexpr int KIND = KeyTraits<K>::kind;
@@ -187,22 +210,29 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
     static_assert(BLOCK >= static_cast<int>(kDigits) && BLOCK % static_cast<int>(kDigits) == 0,
                   "one thread per digit");
 
+    // The per-wave lane-mask tables of the LDS ranker live in the tile buffer: they are dead before
+    // the keys are reordered there (a barrier separates the two uses).
+    static_assert(W * kDigits * sizeof(uint64_t) <= TILE * ELEM, "match tables must fit the tile buffer");
     __shared__ __attribute__((aligned(16))) unsigned char s_tile[TILE * ELEM];
     __shared__ uint32_t s_counts[W][kDigits];
     __shared__ uint32_t s_global_minus_local[kDigits];
     __shared__ uint32_t s_scan[kDigits / kWave];
-    __shared__ uint32_t s_ticket;
+    __shared__ uint32_t s_fallback[kDigits];
+    __shared__ uint32_t s_fallback_tile;
+    uint64_t (*s_match)[kDigits] = reinterpret_cast<uint64_t (*)[kDigits]>(s_tile);
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t mask = (1u << num_bits) - 1u;
 
-    if (tid == 0) s_ticket = atomic_add_agent(counter, 1u);
+    // Wave-private tables: no barrier needed before the wave uses them.
 #pragma unroll
-    for (uint32_t i = lane; i < kDigits; i += kWave) s_counts[wave][i] = 0;
-    __syncthreads();
-    const uint32_t tile = s_ticket;
+    for (uint32_t i = lane; i < kDigits; i += kWave) {
+        s_counts[wave][i] = 0;
+        if constexpr (RANK == kRankLdsMatch) s_match[wave][i] = 0;
+    }
+    const uint32_t tile = blockIdx.x;
     const uint32_t tile_base = tile * TILE;
     const uint32_t valid = min(TILE, n - tile_base);
 
@@ -230,16 +260,43 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
         }
     }
 
-    // Rank inside the wave.
+    // Rank inside the wave: rank = keys of the same digit in earlier rounds (the wave's LDS counter)
+    // + lanes of the same digit below this lane in this round.  The highest such lane advances the
+    // counter.  The peer mask comes from 8 ballots (RANK == kRankBallot) or from an LDS table of
+    // 64-bit lane masks, one per digit (RANK == kRankLdsMatch): every lane ORs its bit into its digit's
+    // entry, reads the entry back (all ORs of the instruction have landed: a wave's LDS operations
+    // complete in issue order), and the highest peer clears it.  OR is order-independent, so the mask
+    // does not depend on how the hardware serialises conflicting lanes.
     uint32_t rank[ITEMS];
+    if constexpr (RANK == kRankLdsMatch) {
+        const uint64_t lane_bit = 1ull << lane;
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
-        const uint64_t peers = match_digit(d);
-        const uint32_t below = popc_lanes_below(peers);
-        const uint32_t base = s_counts[wave][d];
-        rank[k] = base + below;
-        if ((peers >> lane) == 1ull) s_counts[wave][d] = base + below + 1;
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+            uint64_t* slot = &s_match[wave][d];
+            __hip_atomic_fetch_or(slot, lane_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t peers = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const uint32_t base = s_counts[wave][d];
+            const uint32_t below = popc_lanes_below(peers);
+            rank[k] = base + below;
+            __builtin_amdgcn_wave_barrier();
+            if ((peers >> lane) == 1ull) {
+                s_counts[wave][d] = base + below + 1;
+                __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+            const uint64_t peers = match_digit(d);
+            const uint32_t below = popc_lanes_below(peers);
+            const uint32_t base = s_counts[wave][d];
+            rank[k] = base + below;
+            if ((peers >> lane) == 1ull) s_counts[wave][d] = base + below + 1;
+        }
     }
     __syncthreads();
 
@@ -265,43 +322,134 @@ __global__ __launch_bounds__(BLOCK) void onesweep_kernel(const K* __restrict__ k
         local_start = incl - count;
     }
     __syncthreads();
+    const uint32_t d = tid;  // digit owned by this thread (threads >= 256 own none)
+    const uint32_t real = (tid < kDigits) ? ((d == mask) ? count - (TILE - valid) : count) : 0;
     if (tid < kDigits) {
-        const uint32_t d = tid;
         for (uint32_t w = 0; w < wave; ++w) local_start += s_scan[w];
 #pragma unroll
         for (int w = 0; w < W; ++w) s_counts[w][d] += local_start;
+    }
+    __syncthreads();
 
-        // Look-back over earlier tiles of this digit.
-        uint32_t excl = 0;
-        const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
-        if (tile > 0) {
-            int64_t t = static_cast<int64_t>(tile) - 1;
+    // Reorder keys by digit in LDS now: local positions do not depend on the look-back, and the key
+    // registers are free while the look-back runs.  (The match tables that shared this buffer are
+    // dead: the barrier after the rank loop separates the uses.)
+    U* s_keys = reinterpret_cast<U*>(s_tile);
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+        const uint32_t dk = digit_of<U, KIND>(keys[k], shift, mask);
+        rank[k] += s_counts[wave][dk];
+        s_keys[rank[k]] = keys[k];
+    }
+
+    // Look-back over a window of kLookbackWindow predecessor tiles per step: each digit's thread
+    // issues the window's loads together (one memory latency per step), then sums back to its nearest
+    // INCLUSIVE entry.  One entry per step would advance the INCLUSIVE frontier by one tile per
+    // memory round trip, which then paces the whole pass; a window advances it by up to
+    // kLookbackWindow tiles.  Steps are workgroup-synchronous.  A needed entry that stays unpublished
+    // for `spin_limit` polls is counted here from its tile's keys (a predecessor tile is always full:
+    // only the last tile is partial) and published as PARTIAL by compare-and-swap.
+    uint32_t excl = 0;
+    if (tile > 0) {
+        bool done = tid >= kDigits;
+        int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
+        uint32_t* const column = lookback + d;
+        while (true) {
+            uint32_t v[kLookbackWindow];
+#pragma unroll
+            for (int w = 0; w < kLookbackWindow; ++w) {
+                const int64_t j = top - w;
+                v[w] = (!done && j >= 0) ? atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]) : 0u;
+            }
+            uint32_t spins = 0;
             while (true) {
-                const uint32_t v = atomic_load_agent(&lookback[static_cast<uint64_t>(t) * kDigits + d]);
-                if ((v & ~kCountMask) == 0) {
-                    __builtin_amdgcn_s_sleep(1);
+                // First needed entry that is still unpublished (entries past the nearest INCLUSIVE one,
+                // or past tile 0, are not needed).
+                int first_invalid = -1;
+                bool scanning = !done;
+#pragma unroll
+                for (int w = 0; w < kLookbackWindow; ++w) {
+                    const bool live = scanning && top - w >= 0;
+                    if (live && (v[w] & ~kCountMask) == 0) first_invalid = w;
+                    scanning = live && (v[w] & ~kCountMask) != 0 && (v[w] & kFlagInclusive) == 0;
+                }
+                if (!__syncthreads_or(first_invalid >= 0)) break;
+                if (spins >= spin_limit) {
+                    // Fallback: count the newest tile that some digit is still waiting for.
+                    if (tid == 0) s_fallback_tile = 0;
+                    __syncthreads();
+                    if (first_invalid >= 0) atomicMax(&s_fallback_tile, static_cast<uint32_t>(top - first_invalid) + 1u);
+                    __syncthreads();
+                    const uint32_t jf = s_fallback_tile - 1u;
+                    tile_digit_counts<K, DESC, BLOCK, ITEMS>(keys_in, jf, shift, mask, s_fallback);
+                    const int wf = static_cast<int>(top - static_cast<int64_t>(jf));
+                    if (!done) {
+#pragma unroll
+                        for (int w = 0; w < kLookbackWindow; ++w) {
+                            if (w == wf && (v[w] & ~kCountMask) == 0) {
+                                uint32_t expected = 0;
+                                const uint32_t desired = kFlagPartial | s_fallback[d];
+                                v[w] = __hip_atomic_compare_exchange_strong(
+                                           &column[static_cast<uint64_t>(jf) * kDigits], &expected, desired,
+                                           __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                           ? desired
+                                           : expected;
+                            }
+                        }
+                    }
                     continue;
                 }
-                excl += v & kCountMask;
-                if ((v & kFlagInclusive) || t == 0) break;  // tile 0 always publishes INCLUSIVE
-                --t;
+                __builtin_amdgcn_s_sleep(1);
+                ++spins;
+                if (!done) {
+#pragma unroll
+                    for (int w = 0; w < kLookbackWindow; ++w) {
+                        const int64_t j = top - w;
+                        if (j >= 0 && (v[w] & ~kCountMask) == 0)
+                            v[w] = atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]);
+                    }
+                }
             }
-            atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
+            if (!done) {
+                int stop = kLookbackWindow;  // window slot of the entry that ends the walk, if any
+                uint32_t window_sum = 0;
+#pragma unroll
+                for (int w = 0; w < kLookbackWindow; ++w) {
+                    if (stop == kLookbackWindow) {
+                        window_sum += v[w] & kCountMask;
+                        // Tile 0's counts start at the portion base, so the walk always ends there.
+                        if ((v[w] & kFlagInclusive) || top - w == 0) stop = w;
+                    }
+                }
+                excl += window_sum;
+                if (stop < kLookbackWindow) {
+                    done = true;
+                    // Upgrade the PARTIAL entries this window crossed: each one's inclusive count is
+                    // the ending entry's count plus the partial counts from there up to it.  The value
+                    // is unique, so concurrent upgrades (and the owner's own INCLUSIVE) agree.  The
+                    // next tiles then find their predecessors INCLUSIVE instead of walking as far.
+                    uint32_t run = v[stop] & kCountMask;
+                    const bool stop_is_inclusive = (v[stop] & kFlagInclusive) != 0;
+#pragma unroll
+                    for (int w = kLookbackWindow - 1; w >= 0; --w) {
+                        if (w < stop) {
+                            run += v[w] & kCountMask;
+                            if (stop_is_inclusive && (v[w] & kFlagInclusive) == 0)
+                                atomic_store_agent(&column[static_cast<uint64_t>(top - w) * kDigits], kFlagInclusive | run);
+                        }
+                    }
+                }
+            }
+            if (!__syncthreads_or(!done)) break;
+            top -= kLookbackWindow;
         }
+        if (tid < kDigits) atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
+    }
+    if (tid < kDigits) {
         const uint32_t base = digit_offsets[d];
         // Carry to the next portion of this pass: first position of digit d after this portion.
         if (next_offsets != nullptr && tile == gridDim.x - 1) next_offsets[d] = base + excl + real;
         s_global_minus_local[d] = base + excl - local_start;
-    }
-    __syncthreads();
-
-    // Reorder keys by digit in LDS.
-    U* s_keys = reinterpret_cast<U*>(s_tile);
-#pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
-        rank[k] += s_counts[wave][d];
-        s_keys[rank[k]] = keys[k];
     }
     __syncthreads();
 
@@ -343,12 +491,20 @@ struct Geometry {
     uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
+// 16K-key tiles for 4-byte keys without values, 8K otherwise: the reordering buffer then takes at
+// most 64 KB of LDS, two workgroups fit a CU within 128 VGPRs, and a tile carries enough work that
+// the look-back (one cross-XCD round trip per window) stays short relative to the rest of the tile.
+constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
+    return (key_bytes <= 4 && value_bytes == 0) ? Geometry{512, 32} : Geometry{512, 16};
+}
+
 template <typename K, int VB>
 constexpr Geometry geometry() {
-    return Geometry{256, 16};
+    return geometry_for(sizeof(K), VB);
 }
 
 uint32_t g_portion_limit = 0;  // 0: default
+int g_rank_mode = kRankLdsMatch;
 
 // Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
 // portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
@@ -363,8 +519,8 @@ uint32_t portion_size(uint32_t tile, bool compact) {
 
 struct Layout {
     uint32_t passes, portions, portion, tiles_max;
-    size_t bins_off, counters_off, lookback_off, keys_tmp_off, values_tmp_off, total;
-    size_t clear_bytes;  // bins + counters, zeroed per call
+    size_t bins_off, lookback_off, keys_tmp_off, values_tmp_off, total;
+    size_t clear_bytes;  // bins, zeroed per call
 };
 
 Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit, uint32_t end_bit,
@@ -377,8 +533,6 @@ Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t be
     size_t off = 0;
     L.bins_off = off;
     off += static_cast<size_t>(L.portions) * L.passes * kDigits * 4;
-    L.counters_off = off;
-    off += static_cast<size_t>(L.portions) * L.passes * 4;
     L.clear_bytes = off;
     off = align_up(off, kViewAlign);
     L.lookback_off = off;
@@ -404,7 +558,6 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
                 uint32_t begin_bit, uint32_t end_bit, hipStream_t stream) {
     constexpr Geometry G = geometry<K, VB>();
     uint32_t* bins = reinterpret_cast<uint32_t*>(temp + L.bins_off);
-    uint32_t* counters = reinterpret_cast<uint32_t*>(temp + L.counters_off);
     uint32_t* lookback = reinterpret_cast<uint32_t*>(temp + L.lookback_off);
 
     int st = launch_fill_u32(bins, L.clear_bytes / 4, 0u, stream);
@@ -463,11 +616,15 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             if (st != kOk) return st;
             const size_t qoff = static_cast<size_t>(q) * L.portion;
             LaunchScope scope("radix_onesweep", stream);
-            onesweep_kernel<K, DESC, VB, G.block, G.items><<<tiles, G.block, 0, stream>>>(
-                src + qoff, dst, VB ? static_cast<const VW*>(vsrc) + qoff : nullptr, vdst, len,
-                bins + (static_cast<size_t>(q) * L.passes + p) * kDigits,
-                q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr, lookback,
-                counters + q * L.passes + p, shift, nb, n);
+            const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
+            uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
+            uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
+            if (g_rank_mode == kRankBallot)
+                onesweep_kernel<K, DESC, VB, G.block, G.items, kRankBallot><<<tiles, G.block, 0, stream>>>(
+                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
+            else
+                onesweep_kernel<K, DESC, VB, G.block, G.items, kRankLdsMatch><<<tiles, G.block, 0, stream>>>(
+                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
@@ -537,10 +694,18 @@ int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion) {
     return kOk;
 }
 
+// Selects the in-wave ranking of the onesweep kernel: 0 ballot match, 1 LDS lane-mask table
+// (default).  Both give the same stable ranks; the switch exists for tests and measurements.
+int lcpp_hip_internal_radix_rank_mode(int mode) {
+    if (mode != kRankBallot && mode != kRankLdsMatch) return set_error(kInvalidArgument, "rank mode must be 0 or 1");
+    g_rank_mode = mode;
+    return kOk;
+}
+
 uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes) {
     (void)key_bytes;
     (void)value_bytes;
-    return geometry<uint32_t, 0>().tile();
+    return geometry_for(key_bytes, value_bytes).tile();
 }
 
 // Smallest temp storage this implementation accepts for the call (the compact-portion layout); it is
@@ -548,7 +713,7 @@ uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes) {
 size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
                                             uint32_t end_bit, int double_buffer) {
     if (n == 0 || begin_bit >= end_bit) return 0;
-    return make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, geometry<uint32_t, 0>().tile(), !double_buffer,
+    return make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, geometry_for(key_bytes, value_bytes).tile(), !double_buffer,
                        true)
         .total;
 }
@@ -557,7 +722,7 @@ size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t
 uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
                                           uint32_t end_bit, int double_buffer, size_t temp_bytes) {
     if (n == 0 || begin_bit >= end_bit) return 0;
-    const uint32_t tile = geometry<uint32_t, 0>().tile();
+    const uint32_t tile = geometry_for(key_bytes, value_bytes).tile();
     Layout L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, false);
     if (temp_bytes < L.total) L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, true);
     return temp_bytes < L.total ? 0 : L.portions;

@@ -95,6 +95,8 @@ LaunchScope::~LaunchScope() {
     }
 }
 
+uint32_t g_lookback_spin_limit = 64;
+
 int device_cu_count() {
     static int cached[64] = {0};
     int dev = 0;
@@ -116,6 +118,13 @@ extern "C" {
 const char* lcpp_hip_last_error(void) { return g_last_error; }
 
 const char* lcpp_hip_version(void) { return "lcpp-hip 0.1.0 (gfx950)"; }
+
+int lcpp_hip_set_lookback_spin_limit(uint32_t polls) {
+    g_lookback_spin_limit = polls;
+    return kOk;
+}
+
+uint32_t lcpp_hip_get_lookback_spin_limit(void) { return g_lookback_spin_limit; }
 
 int lcpp_hip_profile_enable(int enable) {
     ProfileState& p = profile();

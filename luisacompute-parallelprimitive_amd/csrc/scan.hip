@@ -9,9 +9,13 @@
 //   * Tile = 256 threads x 4 rows x one 128-bit vector per thread per row (16 x 4-byte items per
 //     thread, 4096 items).  Row r of a tile is the contiguous range [r*1024, (r+1)*1024) and thread t
 //     holds items 4t..4t+3 of every row, so each row is one fully coalesced 4 KiB load and store.
-//   * Tiles are claimed through an atomic ticket, so a tile only ever waits on tiles that are
-//     already running (workgroups are spread round-robin over the 8 XCDs; launch order is not a
-//     safe order).
+//   * Tile = workgroup index.  There is no tile ticket: a same-address agent-scope atomic costs
+//     ~11 ns on MI355X and serialises, which would cap a 2^28 scan at ~0.75 ms.  Workgroups are
+//     dispatched in index order in practice, so predecessors are normally running; forward progress
+//     does not rely on it: a look-back that finds a predecessor still INVALID after a bounded spin
+//     computes that tile's aggregate from the input itself (same summation order as its owner, so
+//     float results do not depend on timing) and publishes it with a compare-and-swap
+//     INVALID -> PARTIAL ("decoupled fallback").
 //   * In-tile scan: per-thread 4-item scans, four interleaved wave64 DPP scans (one per row), and
 //     a 4x4 table of wave totals in LDS.
 //   * Look-back: wave 0 publishes PARTIAL, then inspects 64 predecessors per step (one per lane)
@@ -34,28 +38,86 @@ constexpr uint32_t kFlagInvalid = 0;
 constexpr uint32_t kFlagPartial = 1;
 constexpr uint32_t kFlagInclusive = 2;
 
-// Temp layout: [0, 256) ticket counter; [256, 256 + 8 * tiles) tile status words.
-size_t scan_needed_bytes(uint64_t n) {
-    const uint64_t tiles = ceil_div(n, kScanTile);
-    return kViewAlign + tiles * 8;
-}
+// Temp layout: one 8-byte status word per tile.
+size_t scan_needed_bytes(uint64_t n) { return ceil_div(n, kScanTile) * 8; }
+
 
 template <typename T>
 __device__ __forceinline__ uint64_t pack_status(uint32_t flag, T value) {
     return (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, value)) << 32) | flag;
 }
 
+// Item `idx` of the input, or 0 past the end.
+template <typename T>
+__device__ __forceinline__ T load_item(const T* in, uint64_t n, uint64_t idx) {
+    return idx < n ? in[idx] : T(0);
+}
+
+// Aggregate of (full) tile `tile`, computed by one wave in exactly the order its owner uses: per
+// thread ((x0+x1)+x2)+x3, a DPP wave scan per (row, wave), wave totals summed per row in wave order,
+// rows summed in row order.
+template <typename T>
+__device__ T tile_aggregate(const T* __restrict__ in, uint64_t n, uint32_t tile, int vector_io) {
+    using Vec = T __attribute__((ext_vector_type(4)));
+    const uint32_t lane = lane_id();
+    const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile;
+    T running = T(0);
+    for (int r = 0; r < kScanRows; ++r) {
+        T row_total = T(0);
+        for (int w = 0; w < kScanWaves; ++w) {
+            const uint64_t first = tile_base + (static_cast<uint64_t>(r) * kScanBlock + w * kWave + lane) * 4;
+            Vec v;
+            if (vector_io && tile_base + kScanTile <= n) {
+                v = *reinterpret_cast<const Vec*>(in + first);
+            } else {
+                v[0] = load_item(in, n, first);
+                v[1] = load_item(in, n, first + 1);
+                v[2] = load_item(in, n, first + 2);
+                v[3] = load_item(in, n, first + 3);
+            }
+            v[1] += v[0];
+            v[2] += v[1];
+            v[3] += v[2];
+            row_total += wave_read_lane(wave_inclusive_scan(v[3], SumOp{}), kWave - 1);
+        }
+        running += row_total;
+    }
+    return running;
+}
+
 // Exclusive prefix of tile `tile` (> 0) over all earlier tiles; called by all 64 lanes of one wave.
 template <typename T>
-__device__ T scan_lookback(const uint64_t* states, uint32_t tile) {
+__device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* __restrict__ in, uint64_t n, int vector_io,
+                           uint32_t spin_limit) {
     const uint32_t lane = lane_id();
     T prefix = T(0);
     int64_t end = tile;  // exclusive end of the window of predecessors
     while (true) {
         const int64_t idx = end - kWave + static_cast<int64_t>(lane);
         uint64_t st = idx >= 0 ? atomic_load_agent(&states[idx]) : pack_status(kFlagInclusive, T(0));
+        uint32_t spins = 0;
         while (wave_ballot(static_cast<uint32_t>(st) == kFlagInvalid) != 0) {
+            if (spins >= spin_limit) {
+                // Fallback: compute every still-INVALID predecessor's aggregate here.
+                uint64_t invalid = wave_ballot(static_cast<uint32_t>(st) == kFlagInvalid);
+                while (invalid != 0) {
+                    const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(invalid));
+                    invalid &= invalid - 1;
+                    const uint32_t j = static_cast<uint32_t>(end - kWave + src);
+                    const T agg = tile_aggregate(in, n, j, vector_io);
+                    if (lane == src) {
+                        uint64_t expected = 0;
+                        const uint64_t desired = pack_status(kFlagPartial, agg);
+                        st = __hip_atomic_compare_exchange_strong(&states[j], &expected, desired, __ATOMIC_RELAXED,
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 ? desired
+                                 : expected;
+                    }
+                }
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
+            ++spins;
             if (static_cast<uint32_t>(st) == kFlagInvalid) st = atomic_load_agent(&states[idx]);
         }
         const T value = __builtin_bit_cast(T, static_cast<uint32_t>(st >> 32));
@@ -72,20 +134,16 @@ __device__ T scan_lookback(const uint64_t* states, uint32_t tile) {
 
 template <typename T, bool INCLUSIVE>
 __global__ __launch_bounds__(kScanBlock) void scan_sum_kernel(const T* __restrict__ in, T* __restrict__ out,
-                                                              uint64_t n, uint32_t* __restrict__ counter,
-                                                              uint64_t* __restrict__ states, T init,
-                                                              int vector_io) {
+                                                              uint64_t n, uint64_t* __restrict__ states, T init,
+                                                              int vector_io, uint32_t spin_limit) {
     using Vec = T __attribute__((ext_vector_type(4)));
-    __shared__ uint32_t s_tile;
     __shared__ T s_wave_totals[kScanRows][kScanWaves];
     __shared__ T s_tile_prefix;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
-    if (tid == 0) s_tile = atomic_add_agent(counter, 1u);
-    __syncthreads();
-    const uint32_t tile = s_tile;
+    const uint32_t tile = blockIdx.x;
     const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile;
     const bool full = vector_io && tile_base + kScanTile <= n;
 
@@ -145,7 +203,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_sum_kernel(const T* __restric
     } else {
         if (wave == 0) {
             if (lane == 0) atomic_store_agent(&states[tile], pack_status(kFlagPartial, aggregate));
-            const T excl = scan_lookback<T>(states, tile);
+            const T excl = scan_lookback<T>(states, tile, in, n, vector_io, spin_limit);
             if (lane == 0) {
                 atomic_store_agent(&states[tile], pack_status(kFlagInclusive, excl + aggregate));
                 s_tile_prefix = excl;
@@ -208,19 +266,18 @@ int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, boo
         return set_error(kInvalidArgument, "DeviceScan: temp storage must be 8-byte aligned");
 
     const uint64_t tiles = ceil_div(n, kScanTile);
-    uint32_t* counter = static_cast<uint32_t*>(temp);
-    uint64_t* states = reinterpret_cast<uint64_t*>(static_cast<char*>(temp) + kViewAlign);
-    int st = launch_fill_u32(counter, needed / 4, 0u, stream);
+    uint64_t* states = static_cast<uint64_t*>(temp);
+    int st = launch_fill_u32(static_cast<uint32_t*>(temp), needed / 4, 0u, stream);
     if (st != kOk) return st;
 
     const int vector_io = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
     LaunchScope scope("scan_sum", stream);
     if (inclusive)
-        scan_sum_kernel<T, true><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, counter, states,
-                                                                                         init, vector_io);
+        scan_sum_kernel<T, true><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
+                                                                                         vector_io, g_lookback_spin_limit);
     else
-        scan_sum_kernel<T, false><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, counter, states,
-                                                                                          init, vector_io);
+        scan_sum_kernel<T, false><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
+                                                                                          vector_io, g_lookback_spin_limit);
     return check_hip(hipGetLastError(), "scan_sum launch");
 }
 

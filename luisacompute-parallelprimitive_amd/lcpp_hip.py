@@ -69,10 +69,13 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_radix_sort_pairs_temp_bytes", sz, u32, sz, sz)
     sig("lcpp_hip_spmv_temp_bytes", sz, u64, u64, u64)
     sig("lcpp_hip_radix_set_portion_limit", i32, u32)
+    sig("lcpp_hip_set_lookback_spin_limit", i32, u32)
+    sig("lcpp_hip_get_lookback_spin_limit", u32)
     sig("lcpp_hip_radix_tile_items", u32, sz, sz)
     sig("lcpp_hip_internal_scan_needed_bytes", sz, u64)
     sig("lcpp_hip_internal_radix_needed_bytes", sz, u32, sz, sz, u32, u32, i32)
     sig("lcpp_hip_internal_radix_portions", u32, u32, sz, sz, u32, u32, i32, sz)
+    sig("lcpp_hip_internal_radix_rank_mode", i32, i32)
     sig("lcpp_hip_generate", i32, i32, vp, u64, u64, u64, vp)
     for s in SCALAR_SUFFIXES:
         sig(f"lcpp_hip_reduce_sum_{s}", i32, vp, sz, vp, vp, u64, vp)

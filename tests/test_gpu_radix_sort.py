@@ -269,3 +269,60 @@ def test_benchmark_sort_pairs_2p27(hip, orc, dev, kind):
     ko, vo = torch.empty_like(k), torch.empty_like(v)
     hip.sort_pairs("u64", 4, k, ko, v, vo, n)
     complete_stable_check(to_host(k, np.uint64), to_host(ko, np.uint64), to_host(vo, np.uint32))
+
+
+@pytest.mark.parametrize("kdtype,vbytes,descending", [(np.uint32, 0, False), (np.uint32, 4, True),
+                                                      (np.uint64, 4, False), (np.float32, 0, True)])
+def test_forced_lookback_fallback(hip, orc, dev, kdtype, vbytes, descending):
+    """Spin limit 0: every unpublished predecessor's digit counts are computed by the waiting
+    workgroup from that tile's keys and published by compare-and-swap."""
+    lib = hip.lib()
+    n = (1 << 20) + 4321
+    log(f"sort forced fallback {kdtype.__name__} vbytes={vbytes} desc={descending}")
+    raw = orc.generate(0, n, 808)
+    keys = raw.copy() if kdtype == np.uint64 else (raw >> np.uint64(32)).astype(np.uint32).view(kdtype).copy()
+    vals = None if vbytes == 0 else np.arange(n, dtype=np.uint32)
+    old = lib.lcpp_hip_get_lookback_spin_limit()
+    try:
+        lib.lcpp_hip_set_lookback_spin_limit(0)
+        if vals is None:
+            check_bits(gpu_sort(hip, keys, descending=descending), orc.radix_sort(keys, descending=descending))
+        else:
+            ko, vo = gpu_sort(hip, keys, vals, descending=descending)
+            eko, evo = orc.radix_sort(keys, vals, descending=descending)
+            check_bits(ko, eko)
+            assert np.array_equal(vo, evo)
+    finally:
+        lib.lcpp_hip_set_lookback_spin_limit(old)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("case", ["u32_random", "u64_and3_pairs", "u32_low_entropy_desc", "f32_pairs"])
+def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
+    """Both in-wave rankers (ballot match, LDS lane-mask table) give the stable ranks; low-entropy keys
+    put many lanes of a wave on the same digit entry."""
+    lib = hip.lib()
+    n = 500009
+    raw = orc.generate(0, n, 4040)
+    vals = np.arange(n, dtype=np.uint32)
+    desc = case.endswith("desc")
+    if case == "u32_random":
+        keys, vals = (raw >> np.uint64(32)).astype(np.uint32), None
+    elif case == "u64_and3_pairs":
+        keys = orc.generate(4, n, 4041)
+    elif case == "u32_low_entropy_desc":
+        keys, vals = ((raw >> np.uint64(32)) & np.uint64(0x01010101)).astype(np.uint32), None
+    else:
+        keys = orc.generate(6, n, 4042)
+        keys[::3] = keys[7]
+    try:
+        assert lib.lcpp_hip_internal_radix_rank_mode(mode) == 0
+        if vals is None:
+            check_bits(gpu_sort(hip, keys, descending=desc), orc.radix_sort(keys, descending=desc))
+        else:
+            ko, vo = gpu_sort(hip, keys, vals, descending=desc)
+            eko, evo = orc.radix_sort(keys, vals, descending=desc)
+            check_bits(ko, eko)
+            assert np.array_equal(vo, evo)
+    finally:
+        lib.lcpp_hip_internal_radix_rank_mode(1)

@@ -104,3 +104,33 @@ def test_benchmark_input_2p28(hip, orc, dev):
     hip.scan_sum("u32", d, out, n)
     host_in = to_host(d, np.uint32)
     assert np.array_equal(to_host(out, np.uint32), orc.scan_sum_u32(host_in))
+
+
+@pytest.fixture
+def forced_fallback(hip):
+    """Every look-back predecessor that is not yet published is computed by the waiting workgroup."""
+    lib = hip.lib()
+    old = lib.lcpp_hip_get_lookback_spin_limit()
+    lib.lcpp_hip_set_lookback_spin_limit(0)
+    yield
+    lib.lcpp_hip_set_lookback_spin_limit(old)
+
+
+@pytest.mark.parametrize("n", [4097, 65536 * 3 + 5, (1 << 22) + 77])
+def test_forced_fallback_integer(hip, orc, dev, forced_fallback, n):
+    log(f"scan forced fallback n={n}")
+    a = orc.generate(1, n, n)
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan(hip, "u32", a, inclusive), orc.scan_sum_u32(a, inclusive))
+    assert np.array_equal(gpu_scan(hip, "u32", a, False, offset_in=1), orc.scan_sum_u32(a[1:]))
+
+
+def test_forced_fallback_float_within_tolerance(hip, orc, dev, forced_fallback):
+    # Float prefixes combine PARTIAL and INCLUSIVE aggregates in a timing-dependent grouping (as in any
+    # decoupled look-back), so the check is the order-independent bound of test_float_within_tolerance.
+    n = (1 << 22) + 123
+    a = orc.generate(6, n, 5)
+    got = gpu_scan(hip, "f32", a).astype(np.float64)
+    exact, absum = orc.scan_sum_f32(a)
+    bound = (np.arange(n) + 2) * np.finfo(np.float32).eps * absum
+    assert np.all(np.abs(got - exact) <= bound)

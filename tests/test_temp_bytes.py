@@ -85,6 +85,8 @@ def test_radix_single_portion_at_benchmark_sizes(hip):
     assert lib.lcpp_hip_internal_radix_portions(n, 4, 0, 0, 32, 0, hip.sort_keys_temp_bytes(n, 4)) == 1
     n = 1 << 27
     assert lib.lcpp_hip_internal_radix_portions(n, 8, 4, 0, 64, 0, hip.sort_pairs_temp_bytes(n, 8, 4)) == 1
-    # 3 * 2^28 keys do not fit one large portion in reference-sized temp: compact portions of 2^28 - tile.
-    n = 3 << 28
-    assert lib.lcpp_hip_internal_radix_portions(n, 4, 4, 0, 32, 0, hip.sort_pairs_temp_bytes(n, 4, 4)) == 4
+    # Above 2^30 keys the sort always splits into portions, and reference-sized temp always suffices.
+    for n, kb, vb in ((3 << 28, 4, 4), ((1 << 32) - 1, 4, 0), ((1 << 31) + 5, 8, 4)):
+        ref = hip.sort_keys_temp_bytes(n, kb) if vb == 0 else hip.sort_pairs_temp_bytes(n, kb, vb)
+        portions = lib.lcpp_hip_internal_radix_portions(n, kb, vb, 0, kb * 8, 0, ref)
+        assert portions >= (2 if n >= (1 << 30) else 1)
