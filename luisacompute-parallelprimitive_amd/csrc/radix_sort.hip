@@ -42,7 +42,7 @@ constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
-constexpr int kLookbackWindow = 16;  // predecessor tiles inspected per look-back step
+constexpr int kLookbackWindow = 8;  // predecessor tiles inspected per look-back step (measured best of 4..32)
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
@@ -191,8 +191,8 @@ __device__ void tile_digit_counts(const K* __restrict__ keys, uint32_t tile, uin
     __syncthreads();
 }
 template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int RANK>
-// Two workgroups per CU: at most 128 VGPRs (4 waves per SIMD).
-__global__ __launch_bounds__(BLOCK, 2 * BLOCK / kWave / 4) void onesweep_kernel(const K* __restrict__ keys_in,
+// At most 128 VGPRs (4 waves per SIMD): two 512-thread workgroups per CU.
+__global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict__ keys_in,
                                                                                K* __restrict__ keys_out,
                                                          const void* __restrict__ values_in,
                                                          void* __restrict__ values_out, uint32_t n,
@@ -312,11 +312,8 @@ __global__ __launch_bounds__(BLOCK, 2 * BLOCK / kWave / 4) void onesweep_kernel(
             run += c;
         }
         count = run;
-        const uint32_t real = (d == mask) ? count - (TILE - valid) : count;
-        if (tile == 0)
-            atomic_store_agent(&lookback[d], kFlagInclusive | real);
-        else
-            atomic_store_agent(&lookback[tile * kDigits + d], kFlagPartial | real);
+        const uint32_t real = (d == mask) ? count - (TILE - valid) : count;  // missing items excluded
+        atomic_store_agent(&lookback[tile * kDigits + d], (tile == 0 ? kFlagInclusive : kFlagPartial) | real);
         const uint32_t incl = wave_inclusive_scan(count, SumOp{});
         if (lane == kWave - 1) s_scan[wave] = incl;
         local_start = incl - count;
