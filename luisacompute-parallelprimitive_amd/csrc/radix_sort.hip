@@ -419,23 +419,9 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                     }
                 }
                 excl += window_sum;
-                if (stop < kLookbackWindow) {
-                    done = true;
-                    // Upgrade the PARTIAL entries this window crossed: each one's inclusive count is
-                    // the ending entry's count plus the partial counts from there up to it.  The value
-                    // is unique, so concurrent upgrades (and the owner's own INCLUSIVE) agree.  The
-                    // next tiles then find their predecessors INCLUSIVE instead of walking as far.
-                    uint32_t run = v[stop] & kCountMask;
-                    const bool stop_is_inclusive = (v[stop] & kFlagInclusive) != 0;
-#pragma unroll
-                    for (int w = kLookbackWindow - 1; w >= 0; --w) {
-                        if (w < stop) {
-                            run += v[w] & kCountMask;
-                            if (stop_is_inclusive && (v[w] & kFlagInclusive) == 0)
-                                atomic_store_agent(&column[static_cast<uint64_t>(top - w) * kDigits], kFlagInclusive | run);
-                        }
-                    }
-                }
+                // (Upgrading the crossed PARTIAL entries to INCLUSIVE was measured slower: the extra
+                // agent-scope stores cost more than the shorter walks they buy.)
+                if (stop < kLookbackWindow) done = true;
             }
             if (!__syncthreads_or(!done)) break;
             top -= kLookbackWindow;

@@ -6,9 +6,10 @@
 // (single_pass_scan_operator.h:119-172) and tile statuses INVALID / PARTIAL / INCLUSIVE (:26-32).
 //
 // MI355X design
-//   * Tile = 256 threads x 4 rows x one 128-bit vector per thread per row (16 x 4-byte items per
-//     thread, 4096 items).  Row r of a tile is the contiguous range [r*1024, (r+1)*1024) and thread t
-//     holds items 4t..4t+3 of every row, so each row is one fully coalesced 4 KiB load and store.
+//   * Tile = 256 threads x 24 rows x one 128-bit vector per thread per row (96 x 4-byte items per
+//     thread, 24,576 items, held in registers).  Row r of a tile is the contiguous range
+//     [r*1024, (r+1)*1024) and thread t holds items 4t..4t+3 of every row, so each row is one fully
+//     coalesced 4 KiB load and store.
 //   * Tile = workgroup index.  There is no tile ticket: a same-address agent-scope atomic costs
 //     ~11 ns on MI355X and serialises, which would cap a 2^28 scan at ~0.75 ms.  Workgroups are
 //     dispatched in index order in practice, so predecessors are normally running; forward progress
@@ -16,23 +17,26 @@
 //     computes that tile's aggregate from the input itself (same summation order as its owner, so
 //     float results do not depend on timing) and publishes it with a compare-and-swap
 //     INVALID -> PARTIAL ("decoupled fallback").
-//   * In-tile scan: per-thread 4-item scans, four interleaved wave64 DPP scans (one per row), and
-//     a 4x4 table of wave totals in LDS.
+//   * In-tile scan: per-thread 4-item scans, one wave64 DPP scan per row (independent, so they
+//     interleave), and a rows x waves table of wave totals in LDS.
 //   * Look-back: wave 0 publishes PARTIAL, then inspects 64 predecessors per step (one per lane)
 //     with agent-scope loads, sums back to the nearest INCLUSIVE predecessor with a DPP reduction,
 //     and publishes INCLUSIVE.  Status and value share one 64-bit word: flag in the low half,
 //     value bits in the high half, so one relaxed atomic load observes both consistently.
-// Algorithmic traffic: 2 * n * sizeof(T) bytes (read input, write output) + 8 bytes per 4096 items.
+// Algorithmic traffic: 2 * n * sizeof(T) bytes (read input, write output) + 8 bytes per tile.
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
 
 namespace lcpp_hip {
 namespace {
 
+// 24 rows: 96 items per thread and 24,576 per tile (measured best on MI355X among 4K..48K-item tiles
+// and 256..1024-thread workgroups).  Large tiles matter because a tile's look-back waits on its
+// predecessors' publications; fewer, larger tiles shorten that chain relative to the data moved.
 constexpr int kScanBlock = 256;
-constexpr int kScanRows = 4;
+constexpr int kScanRows = 24;
 constexpr int kScanWaves = kScanBlock / kWave;
-constexpr uint32_t kScanTile = kScanBlock * kScanRows * 4;  // 4096 items of 4 bytes
+constexpr uint32_t kScanTile = kScanBlock * kScanRows * 4;  // 24,576 items of 4 bytes
 
 constexpr uint32_t kFlagInvalid = 0;
 constexpr uint32_t kFlagPartial = 1;
