@@ -6,7 +6,11 @@ dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on 
 one host thread), and the other benchmark configurations (reduce, scan, SortPairs) as achieved GB/s
 against the 8 TB/s HBM peak.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+`roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
+FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
+runs the plain copy whose counter readings scale those counters to bytes.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
 """
 from __future__ import annotations
 
@@ -71,6 +75,34 @@ def flush_mall(buf):
     buf.add_(1)  # writes 1 GiB, evicting the 256 MB MALL
 
 
+TRAFFIC_PROFILE = REPO / "profiles" / "radix_onesweep_sortkeys_2p28_u32.md"
+
+
+def measured_traffic():
+    """HBM bytes per onesweep launch from the committed FETCH_SIZE/WRITE_SIZE summary (the line
+    `traffic_bytes_per_launch: N`), already scaled by the plain-copy calibration; None if absent."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip().strip("`"))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_calibration(mib: int) -> int:
+    """Runs a plain device-to-device copy of `mib` MiB three times: the reference kernel whose
+    FETCH_SIZE/WRITE_SIZE readings scale the onesweep counters to bytes."""
+    import torch
+    src = torch.ones(mib << 18, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": mib << 20, "launches": 3}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,11 +110,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline SortKeys only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
                           "n_gpus": args.gpus}))
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     import torch
     import lcpp_hip as hip
@@ -121,7 +157,7 @@ def main() -> int:
         "dtype": "u32",
         "data": "synthetic (splitmix64, seed 114521), generated on the device",
         "config": {"workload": "DeviceRadixSort::SortKeys, 2^28 uniform uint32 keys, 4 x 8-bit onesweep passes",
-                   "items": n, "device": props.name},
+                   "items": n, "device": props.name or getattr(props, "gcnArchName", "")},
         "roofline": {
             "kernel": "radix_onesweep",
             "bound": "hbm",
@@ -129,7 +165,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_ms": round(onesweep_ms, 5),
             "algorithmic_bytes_per_launch": pass_bytes,
             "whole_sort_frac_4pass_model": round((32 * n) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -151,7 +187,7 @@ def main() -> int:
             oracle.radix_sort(sample)
             reps += 1
             el = time.perf_counter() - t0
-            if el > 8.0 or reps >= 20:
+            if el > 12.0 or reps >= 40:
                 break
         line["cpu_baseline"] = {
             "value": round(m * reps / el / 1e9, 4),
