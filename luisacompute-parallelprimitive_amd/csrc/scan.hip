@@ -14,9 +14,11 @@
 //     ~11 ns on MI355X and serialises, which would cap a 2^28 scan at ~0.75 ms.  Workgroups are
 //     dispatched in index order in practice, so predecessors are normally running; forward progress
 //     does not rely on it: a look-back that finds a predecessor still INVALID after a bounded spin
-//     computes that tile's aggregate from the input itself (same summation order as its owner, so
-//     float results do not depend on timing) and publishes it with a compare-and-swap
-//     INVALID -> PARTIAL ("decoupled fallback").
+//     claims that tile (compare-and-swap INVALID -> CLAIMED), computes its aggregate from the input
+//     itself (same summation order as its owner, so float results do not depend on timing) and
+//     publishes it as PARTIAL ("decoupled fallback").  The owner publishes with a compare-and-swap
+//     too; when it finds its tile CLAIMED it waits for the claimer's PARTIAL before writing any
+//     output, so an in-place scan (in == out) never overwrites input that a claimer still reads.
 //   * In-tile scan: per-thread 4-item scans, one wave64 DPP scan per row (independent, so they
 //     interleave), and a rows x waves table of wave totals in LDS.
 //   * Look-back: wave 0 publishes PARTIAL, then inspects 64 predecessors per step (one per lane)
@@ -41,6 +43,7 @@ constexpr uint32_t kScanTile = kScanBlock * kScanRows * 4;  // 24,576 items of 4
 constexpr uint32_t kFlagInvalid = 0;
 constexpr uint32_t kFlagPartial = 1;
 constexpr uint32_t kFlagInclusive = 2;
+constexpr uint32_t kFlagClaimed = 3;  // a look-back is computing this tile's aggregate
 
 // Temp layout: one 8-byte status word per tile.
 size_t scan_needed_bytes(uint64_t n) { return ceil_div(n, kScanTile) * 8; }
@@ -49,6 +52,11 @@ size_t scan_needed_bytes(uint64_t n) { return ceil_div(n, kScanTile) * 8; }
 template <typename T>
 __device__ __forceinline__ uint64_t pack_status(uint32_t flag, T value) {
     return (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, value)) << 32) | flag;
+}
+
+// PARTIAL or INCLUSIVE: the word carries a usable value.
+__device__ __forceinline__ bool status_published(uint64_t st) {
+    return static_cast<uint32_t>(st) - kFlagPartial < 2u;
 }
 
 // Item `idx` of the input, or 0 past the end.
@@ -61,7 +69,7 @@ __device__ __forceinline__ T load_item(const T* in, uint64_t n, uint64_t idx) {
 // thread ((x0+x1)+x2)+x3, a DPP wave scan per (row, wave), wave totals summed per row in wave order,
 // rows summed in row order.
 template <typename T>
-__device__ T tile_aggregate(const T* __restrict__ in, uint64_t n, uint32_t tile, int vector_io) {
+__device__ T tile_aggregate(const T* in, uint64_t n, uint32_t tile, int vector_io) {
     using Vec = T __attribute__((ext_vector_type(4)));
     const uint32_t lane = lane_id();
     const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile;
@@ -91,7 +99,7 @@ __device__ T tile_aggregate(const T* __restrict__ in, uint64_t n, uint32_t tile,
 
 // Exclusive prefix of tile `tile` (> 0) over all earlier tiles; called by all 64 lanes of one wave.
 template <typename T>
-__device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* __restrict__ in, uint64_t n, int vector_io,
+__device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_t n, int vector_io,
                            uint32_t spin_limit) {
     const uint32_t lane = lane_id();
     T prefix = T(0);
@@ -100,29 +108,35 @@ __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* __restrict_
         const int64_t idx = end - kWave + static_cast<int64_t>(lane);
         uint64_t st = idx >= 0 ? atomic_load_agent(&states[idx]) : pack_status(kFlagInclusive, T(0));
         uint32_t spins = 0;
-        while (wave_ballot(static_cast<uint32_t>(st) == kFlagInvalid) != 0) {
+        while (wave_ballot(!status_published(st)) != 0) {
             if (spins >= spin_limit) {
-                // Fallback: compute every still-INVALID predecessor's aggregate here.
+                // Fallback: claim every still-INVALID predecessor and compute its aggregate here.
+                // Predecessors CLAIMED by another look-back are simply polled until published.
                 uint64_t invalid = wave_ballot(static_cast<uint32_t>(st) == kFlagInvalid);
                 while (invalid != 0) {
                     const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(invalid));
                     invalid &= invalid - 1;
                     const uint32_t j = static_cast<uint32_t>(end - kWave + src);
-                    const T agg = tile_aggregate(in, n, j, vector_io);
+                    bool won = false;
                     if (lane == src) {
-                        uint64_t expected = 0;
-                        const uint64_t desired = pack_status(kFlagPartial, agg);
-                        st = __hip_atomic_compare_exchange_strong(&states[j], &expected, desired, __ATOMIC_RELAXED,
-                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                 ? desired
-                                 : expected;
+                        uint64_t expected = 0;  // INVALID with value 0, as the clear leaves it
+                        won = __hip_atomic_compare_exchange_strong(&states[j], &expected, uint64_t(kFlagClaimed),
+                                                                   __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                   __HIP_MEMORY_SCOPE_AGENT);
+                        st = won ? uint64_t(kFlagClaimed) : expected;
+                    }
+                    if (wave_ballot(won) != 0) {
+                        const T agg = tile_aggregate(in, n, j, vector_io);
+                        if (lane == src) {
+                            st = pack_status(kFlagPartial, agg);
+                            atomic_store_agent(&states[j], st);
+                        }
                     }
                 }
-                break;
             }
             __builtin_amdgcn_s_sleep(1);
             ++spins;
-            if (static_cast<uint32_t>(st) == kFlagInvalid) st = atomic_load_agent(&states[idx]);
+            if (!status_published(st)) st = atomic_load_agent(&states[idx]);
         }
         const T value = __builtin_bit_cast(T, static_cast<uint32_t>(st >> 32));
         const uint64_t inclusive = wave_ballot(static_cast<uint32_t>(st) == kFlagInclusive);
@@ -137,7 +151,7 @@ __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* __restrict_
 }
 
 template <typename T, bool INCLUSIVE>
-__global__ __launch_bounds__(kScanBlock) void scan_sum_kernel(const T* __restrict__ in, T* __restrict__ out,
+__global__ __launch_bounds__(kScanBlock, 2) void scan_sum_kernel(const T* in, T* out,
                                                               uint64_t n, uint64_t* __restrict__ states, T init,
                                                               int vector_io, uint32_t spin_limit) {
     using Vec = T __attribute__((ext_vector_type(4)));
@@ -200,22 +214,31 @@ __global__ __launch_bounds__(kScanBlock) void scan_sum_kernel(const T* __restric
     }
     const T aggregate = running;
 
-    T tile_prefix;
-    if (tile == 0) {
-        if (tid == 0) atomic_store_agent(&states[0], pack_status(kFlagInclusive, aggregate));
-        tile_prefix = T(0);
-    } else {
-        if (wave == 0) {
-            if (lane == 0) atomic_store_agent(&states[tile], pack_status(kFlagPartial, aggregate));
-            const T excl = scan_lookback<T>(states, tile, in, n, vector_io, spin_limit);
-            if (lane == 0) {
-                atomic_store_agent(&states[tile], pack_status(kFlagInclusive, excl + aggregate));
-                s_tile_prefix = excl;
-            }
+    // Publish (tile 0: INCLUSIVE at once; others PARTIAL, then INCLUSIVE after the look-back).  The
+    // publication is a compare-and-swap from INVALID: if a look-back has CLAIMED this tile, the owner
+    // waits for the claimer's PARTIAL (the claimer has finished reading this tile's input) before the
+    // barrier that precedes every output store.
+    if (wave == 0) {
+        bool claimed_by_other = false;
+        if (lane == 0) {
+            uint64_t expected = 0;
+            claimed_by_other = !__hip_atomic_compare_exchange_strong(
+                &states[tile], &expected, pack_status(tile == 0 ? kFlagInclusive : kFlagPartial, aggregate),
+                __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __syncthreads();
-        tile_prefix = s_tile_prefix;
+        const T excl = tile == 0 ? T(0) : scan_lookback<T>(states, tile, in, n, vector_io, spin_limit);
+        if (lane == 0) {
+            if (claimed_by_other) {
+                while (static_cast<uint32_t>(atomic_load_agent(&states[tile])) != kFlagPartial)
+                    __builtin_amdgcn_s_sleep(1);
+            }
+            if (tile != 0 || claimed_by_other)
+                atomic_store_agent(&states[tile], pack_status(kFlagInclusive, excl + aggregate));
+            s_tile_prefix = excl;
+        }
     }
+    __syncthreads();
+    const T tile_prefix = s_tile_prefix;
 
     const T base_all = init + tile_prefix;
 #pragma unroll
@@ -224,10 +247,12 @@ __global__ __launch_bounds__(kScanBlock) void scan_sum_kernel(const T* __restric
         const T p = base_all + row_base[r] + thread_excl;
         Vec o;
         if constexpr (INCLUSIVE) {
+            // The last item's inclusive value comes from the wave scan, so v[r][3] need not stay live
+            // (keeps the kernel within 256 VGPRs, two workgroups per CU).
             o[0] = p + v[r][0];
             o[1] = p + v[r][1];
             o[2] = p + v[r][2];
-            o[3] = p + v[r][3];
+            o[3] = base_all + row_base[r] + wave_incl[r];
         } else {
             o[0] = p;
             o[1] = p + v[r][0];

@@ -1,0 +1,66 @@
+// DeviceReduce::Sum over the MI355X C-ABI (lcpp_hip_reduce_sum_*), with the reference's module
+// shape (src/lcpp/device/device_reduce.h:102-113 template, :154-173 create, :184-189 temp query,
+// :280-288 Sum) and its record-time checks (:238-264).  Sum records one command; the kernels run on
+// the stream the command list is committed to.
+#pragma once
+
+#include <limits>
+#include <type_traits>
+
+#include "lcpp/runtime/core.h"
+
+namespace luisa::parallel_primitive {
+
+template <size_t BLOCK_SIZE = 256, size_t WARP_NUMS = 32, size_t ITEMS_PER_THREAD = 8, bool CUDA_WARP_REDUX = false,
+          bool AUTO_CUDA_TUNED_POLICY = true>
+class DeviceReduce : public LuisaModule {
+  public:
+    void create(Device& device, Stream* debug_stream = nullptr, InteropContext* interop = nullptr) {
+        (void)debug_stream;
+        (void)interop;
+        create_module(device);
+    }
+
+    // Same bytes as the reference formula for this tile (device_reduce.h:517-536).
+    template <typename T>
+    static size_t GetTempStorageBytes(size_t num_item) {
+        return lcpp_hip_reduce_temp_bytes_policy(num_item, sizeof(T), static_cast<uint32_t>(BLOCK_SIZE),
+                                                 static_cast<uint32_t>(ITEMS_PER_THREAD));
+    }
+
+    template <NumericT T>
+    void Sum(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             size_t num_item) {
+        static_assert(sizeof(T) == 4 || sizeof(T) == 8, "DeviceReduce::Sum supports 4- and 8-byte numbers");
+        LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
+        LCPP_ASSERT(num_item <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
+        LCPP_ASSERT(d_out.size() >= 1u, "DeviceReduce output view is empty.");
+        if (num_item > 0) {
+            LCPP_ASSERT(d_in.size() >= num_item, "DeviceReduce input view is too small.");
+            LCPP_ASSERT(temp_storage.size() >= bytes_to_uint_count(GetTempStorageBytes<T>(num_item)),
+                        "DeviceReduce temporary storage is too small.");
+        }
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const T* in = d_in.data();
+        T* out = d_out.data();
+        cmdlist << [=](hipStream_t s) {
+            void* st = detail::stream_ptr(s);
+            int rc;
+            if constexpr (std::is_same_v<T, int32_t>) rc = lcpp_hip_reduce_sum_i32(temp, temp_bytes, in, out, num_item, st);
+            else if constexpr (std::is_same_v<T, uint32_t>) rc = lcpp_hip_reduce_sum_u32(temp, temp_bytes, in, out, num_item, st);
+            else if constexpr (std::is_same_v<T, float>) rc = lcpp_hip_reduce_sum_f32(temp, temp_bytes, in, out, num_item, st);
+            else if constexpr (std::is_integral_v<T> && std::is_signed_v<T> && sizeof(T) == 8)
+                rc = lcpp_hip_reduce_sum_i64(temp, temp_bytes, reinterpret_cast<const int64_t*>(in),
+                                             reinterpret_cast<int64_t*>(out), num_item, st);
+            else if constexpr (std::is_integral_v<T> && std::is_unsigned_v<T> && sizeof(T) == 8)
+                rc = lcpp_hip_reduce_sum_u64(temp, temp_bytes, reinterpret_cast<const uint64_t*>(in),
+                                             reinterpret_cast<uint64_t*>(out), num_item, st);
+            else if constexpr (std::is_same_v<T, double>) rc = lcpp_hip_reduce_sum_f64(temp, temp_bytes, in, out, num_item, st);
+            else static_assert(sizeof(T) == 0, "DeviceReduce::Sum: unsupported element type");
+            luisa::detail::abi_check(rc, "DeviceReduce::Sum");
+        };
+    }
+};
+
+}  // namespace luisa::parallel_primitive

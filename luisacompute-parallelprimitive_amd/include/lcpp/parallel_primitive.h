@@ -1,0 +1,9 @@
+// Umbrella header of the MI355X host facade: the device-level modules of the LCPP hot path
+// (the reference's src/lcpp/parallel_primitive.h includes every family; only these four are provided).
+#pragma once
+
+#include "lcpp/runtime/core.h"
+#include "lcpp/device/device_reduce.h"
+#include "lcpp/device/device_scan.h"
+#include "lcpp/device/device_radix_sort.h"
+#include "lcpp/device/device_spmv.h"

@@ -31,8 +31,7 @@ using slong = int64_t;
 template <typename T>
 using vector = std::vector<T>;
 using string = std::string;
-template <typename T>
-using span = std::span<T>;
+using std::span;  // luisa::span{v} deduces like the reference's luisa::span
 
 // Errors raised by the facade (the reference aborts through LUISA_ASSERT on the same conditions).
 class Error : public std::runtime_error {
@@ -86,8 +85,11 @@ class BufferView {
             if (b) detail::hip_check(hipMemcpyAsync(d, host, b, hipMemcpyHostToDevice, s), "copy_from");
         };
     }
-    template <typename U>
-    [[nodiscard]] Command copy_from(std::span<U> host) const { return copy_from(static_cast<const void*>(host.data())); }
+    template <typename U, size_t E>
+    [[nodiscard]] Command copy_from(std::span<U, E> host) const {
+        LCPP_ASSERT(host.size_bytes() >= size_bytes(), "BufferView::copy_from: host span is smaller than the view");
+        return copy_from(static_cast<const void*>(host.data()));
+    }
     [[nodiscard]] Command copy_from(BufferView<T> src) const {
         T* d = m_data;
         const T* sp = src.data();
@@ -103,8 +105,11 @@ class BufferView {
             if (b) detail::hip_check(hipMemcpyAsync(host, d, b, hipMemcpyDeviceToHost, s), "copy_to");
         };
     }
-    template <typename U>
-    [[nodiscard]] Command copy_to(std::span<U> host) const { return copy_to(static_cast<void*>(host.data())); }
+    template <typename U, size_t E>
+    [[nodiscard]] Command copy_to(std::span<U, E> host) const {
+        LCPP_ASSERT(host.size_bytes() >= size_bytes(), "BufferView::copy_to: host span is smaller than the view");
+        return copy_to(static_cast<void*>(host.data()));
+    }
 
   private:
     T* m_data = nullptr;
@@ -233,8 +238,8 @@ struct DoubleBuffer {
     int selector = 0;
     DoubleBuffer() = default;
     DoubleBuffer(BufferView<T> current, BufferView<T> alternate) : d_buffer{current, alternate}, selector(0) {}
-    [[nodiscard]] BufferView<T> current() const { return d_buffer[selector]; }
-    [[nodiscard]] BufferView<T> alternate() const { return d_buffer[selector ^ 1]; }
+    [[nodiscard]] BufferView<T> current() const { return d_buffer[selector & 1]; }
+    [[nodiscard]] BufferView<T> alternate() const { return d_buffer[(selector & 1) ^ 1]; }
 };
 
 // common/utils.h:247-250.

@@ -1,0 +1,529 @@
+// C++20 facade tests: the reference's module-level test cases, written against
+// luisa::parallel_primitive::{DeviceReduce, DeviceScan, DeviceRadixSort, DeviceSpmv} as a reference
+// user would call them (CommandList recording, commit on a Stream, host checks with std:: algorithms).
+//
+// Case sources: tests/device_reduce_test.cpp:95-173, tests/device_scan_test.cpp:80-321,
+// tests/device_radix_sort_interface_test.cpp:68-283, tests/device_radix_sort_one_sweep.cpp:79-333,
+// tests/device_spmv_test.cpp:41-203 and the bench generators of tests/lcpp_cub_bench.cpp:516-521,
+// 666-672, 814.
+//
+// Usage: facade_test [--list] [case-substring]
+#include <lcpp/parallel_primitive.h>
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <numeric>
+#include <string>
+#include <vector>
+
+using namespace luisa;
+using namespace luisa::compute;
+using namespace luisa::parallel_primitive;
+
+namespace {
+
+struct Case {
+    const char* name;
+    std::function<void()> body;
+};
+
+int g_failures = 0;
+std::string g_current;
+
+#define EXPECT(cond)                                                                               \
+    do {                                                                                           \
+        if (!(cond)) {                                                                             \
+            ++g_failures;                                                                          \
+            std::printf("  FAILED %s:%d in %s: %s\n", __FILE__, __LINE__, g_current.c_str(), #cond); \
+        }                                                                                          \
+    } while (0)
+
+template <typename F>
+bool throws_error(F&& f) {
+    try {
+        f();
+    } catch (const luisa::Error&) {
+        return true;
+    }
+    return false;
+}
+
+// splitmix64 stream, the generator the repository's tests and benchmarks use.
+uint64_t mix64(uint64_t seed, uint64_t i) {
+    uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+struct Env {
+    Context context;
+    Device device;
+    Stream stream;
+    DeviceReduce<> reduce;
+    DeviceScan<> scan;
+    DeviceRadixSort<> radix_sort;
+    DeviceSpmv<> spmv;
+    Env() : device(context.create_device("hip")), stream(device.create_stream()) {
+        reduce.create(device, &stream);
+        scan.create(device, &stream);
+        radix_sort.create(device, &stream);
+        spmv.create(device);
+    }
+};
+
+Env* g_env = nullptr;
+
+// ---- DeviceReduce ------------------------------------------------------------------------------
+
+void reduce_sum_of_ones() {
+    auto& e = *g_env;
+    for (uint k : {0u, 5u, 11u, 12u, 17u, 20u, 24u}) {
+        const uint n = (1u << k) + 1u;
+        std::vector<int> ones(n, 1);
+        auto in = e.device.create_buffer<int>(n);
+        auto out = e.device.create_buffer<int>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<int>(n)));
+        CommandList cmd;
+        e.reduce.Sum(cmd, temp.view(), in.view(), out.view(), n);
+        int result = -1;
+        e.stream << in.copy_from(luisa::span{ones}) << cmd.commit() << out.copy_to(&result) << synchronize();
+        EXPECT(result == static_cast<int>(n));
+    }
+}
+
+void reduce_empty_writes_init() {
+    auto& e = *g_env;
+    auto out = e.device.create_buffer<int>(1);
+    int sentinel = 77;
+    CommandList cmd;
+    e.reduce.Sum(cmd, BufferView<uint>{}, BufferView<int>{}, out.view(), 0u);
+    int result = -1;
+    e.stream << out.copy_from(&sentinel) << cmd.commit() << out.copy_to(&result) << synchronize();
+    EXPECT(result == 0);
+}
+
+void reduce_bench_pattern_int_and_float() {
+    auto& e = *g_env;
+    const uint n = (1u << 22) + 13u;
+    std::vector<int> a(n);
+    std::vector<float> f(n);
+    int64_t exact = 0;
+    double fexact = 0.0, fabs_sum = 0.0;
+    for (uint i = 0; i < n; ++i) {
+        a[i] = static_cast<int>(i % 13u) - 6;
+        exact += a[i];
+        f[i] = static_cast<float>(static_cast<int64_t>(mix64(5, i) >> 40) - (1 << 23)) / float(1 << 23);
+        fexact += f[i];
+        fabs_sum += std::fabs(f[i]);
+    }
+    auto in = e.device.create_buffer<int>(n);
+    auto fin = e.device.create_buffer<float>(n);
+    auto out = e.device.create_buffer<int>(1);
+    auto fout = e.device.create_buffer<float>(1);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<float>(n)));
+    CommandList cmd;
+    e.reduce.Sum(cmd, temp.view(), in.view(), out.view(), n);
+    e.reduce.Sum(cmd, temp.view(), fin.view(), fout.view(), n);
+    int result = 0;
+    float fresult = 0.0f;
+    e.stream << in.copy_from(luisa::span{a}) << fin.copy_from(luisa::span{f}) << cmd.commit()
+             << out.copy_to(&result) << fout.copy_to(&fresult) << synchronize();
+    EXPECT(result == static_cast<int>(static_cast<uint32_t>(exact)));
+    // Any summation order is within n * eps * sum|x| of the exact sum.
+    EXPECT(std::fabs(double(fresult) - fexact) <= double(n) * 1.2e-7 * fabs_sum);
+}
+
+// ---- DeviceScan --------------------------------------------------------------------------------
+
+void scan_sums_of_ones() {
+    auto& e = *g_env;
+    for (uint k : {0u, 1u, 7u, 12u, 15u, 20u}) {
+        const uint n = 1u << k;
+        std::vector<uint> ones(n, 1u), ex(n), inc(n);
+        auto in = e.device.create_buffer<uint>(n);
+        auto out_ex = e.device.create_buffer<uint>(n);
+        auto out_in = e.device.create_buffer<uint>(n);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<uint>(n)));
+        CommandList cmd;
+        e.scan.ExclusiveSum(cmd, temp.view(), in.view(), out_ex.view(), n);
+        e.scan.InclusiveSum(cmd, temp.view(), in.view(), out_in.view(), n);
+        e.stream << in.copy_from(luisa::span{ones}) << cmd.commit() << out_ex.copy_to(luisa::span{ex})
+                 << out_in.copy_to(luisa::span{inc}) << synchronize();
+        bool ok = true;
+        for (uint i = 0; i < n; ++i) ok = ok && ex[i] == i && inc[i] == i + 1;
+        EXPECT(ok);
+    }
+}
+
+void scan_inclusive_init_in_place() {
+    auto& e = *g_env;
+    std::array<int, 4> input{1, 2, 3, 4};
+    const std::array<int, 4> expected{11, 13, 16, 20};
+    auto data = e.device.create_buffer<int>(input.size());
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<int>(input.size())));
+    CommandList cmd;
+    e.scan.InclusiveScanInit(cmd, temp.view(), data.view(), data.view(), input.size(), SumOp{}, 10);
+    e.scan.InclusiveScanInit(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, 0u, SumOp{}, 10);
+    std::array<int, 4> result{};
+    e.stream << data.copy_from(luisa::span{input}) << cmd.commit() << data.copy_to(luisa::span{result})
+             << synchronize();
+    EXPECT(result == expected);
+}
+
+void scan_bench_pattern_vs_std() {
+    auto& e = *g_env;
+    const uint n = (1u << 22) + 5u;
+    std::vector<int> a(n), got(n), want(n), got_init(n), want_init(n);
+    for (uint i = 0; i < n; ++i) a[i] = static_cast<int>(i % 7u) - 3;
+    std::exclusive_scan(a.begin(), a.end(), want.begin(), 0);
+    std::exclusive_scan(a.begin(), a.end(), want_init.begin(), 1000);
+    auto in = e.device.create_buffer<int>(n);
+    auto out = e.device.create_buffer<int>(n);
+    auto out2 = e.device.create_buffer<int>(n);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<int>(n)));
+    CommandList cmd;
+    e.scan.ExclusiveSum(cmd, temp.view(), in.view(), out.view(), n);
+    e.scan.ExclusiveScan(cmd, temp.view(), in.view(), out2.view(), n, SumOp{}, 1000);
+    e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(luisa::span{got})
+             << out2.copy_to(luisa::span{got_init}) << synchronize();
+    EXPECT(got == want);
+    EXPECT(got_init == want_init);
+}
+
+// ---- DeviceRadixSort ---------------------------------------------------------------------------
+
+template <typename T, typename Sel>
+std::vector<uint> stable_order(const std::vector<T>& keys, Sel sel, bool descending) {
+    std::vector<uint> order(keys.size());
+    std::iota(order.begin(), order.end(), 0u);
+    std::stable_sort(order.begin(), order.end(), [&](uint l, uint r) {
+        return descending ? sel(keys[l]) > sel(keys[r]) : sel(keys[l]) < sel(keys[r]);
+    });
+    return order;
+}
+
+template <typename T>
+bool follows(const std::vector<T>& result, const std::vector<T>& source, const std::vector<uint>& order) {
+    for (size_t i = 0; i < order.size(); ++i)
+        if (std::memcmp(&result[i], &source[order[i]], sizeof(T)) != 0) return false;
+    return true;
+}
+
+void radix_stable_partial_bit_ranges() {
+    auto& e = *g_env;
+    constexpr uint n = 257u, b = 1u, en = 6u;
+    std::vector<uint> keys(n), values(n);
+    for (uint i = 0; i < n; ++i) {
+        keys[i] = ((i * 53u) % 64u) | (((i * 17u) % 11u) << 8u);
+        values[i] = i;
+    }
+    auto bits = [](uint k) { return (k >> b) & ((1u << (en - b)) - 1u); };
+    const auto asc = stable_order(keys, bits, false);
+    const auto desc = stable_order(keys, bits, true);
+    auto kin = e.device.create_buffer<uint>(n), vin = e.device.create_buffer<uint>(n);
+    auto ka = e.device.create_buffer<uint>(n), kd = e.device.create_buffer<uint>(n);
+    auto pka = e.device.create_buffer<uint>(n), pva = e.device.create_buffer<uint>(n);
+    auto pkd = e.device.create_buffer<uint>(n), pvd = e.device.create_buffer<uint>(n);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceRadixSort<>::GetSortPairsTempStorageBytes<uint, uint>(n)));
+    CommandList cmd;
+    e.radix_sort.SortKeys(cmd, temp.view(), kin.view(), ka.view(), n, b, en);
+    e.radix_sort.SortKeysDescending(cmd, temp.view(), kin.view(), kd.view(), n, b, en);
+    e.radix_sort.SortPairs(cmd, temp.view(), kin.view(), pka.view(), vin.view(), pva.view(), n, b, en);
+    e.radix_sort.SortPairsDescending(cmd, temp.view(), kin.view(), pkd.view(), vin.view(), pvd.view(), n, b, en);
+    e.stream << kin.copy_from(luisa::span{keys}) << vin.copy_from(luisa::span{values}) << cmd.commit();
+    std::vector<uint> r_ka(n), r_kd(n), r_pka(n), r_pva(n), r_pkd(n), r_pvd(n);
+    e.stream << ka.copy_to(luisa::span{r_ka}) << kd.copy_to(luisa::span{r_kd}) << pka.copy_to(luisa::span{r_pka})
+             << pva.copy_to(luisa::span{r_pva}) << pkd.copy_to(luisa::span{r_pkd})
+             << pvd.copy_to(luisa::span{r_pvd}) << synchronize();
+    EXPECT(follows(r_ka, keys, asc));
+    EXPECT(follows(r_kd, keys, desc));
+    EXPECT(follows(r_pka, keys, asc));
+    EXPECT(follows(r_pva, values, asc));
+    EXPECT(follows(r_pkd, keys, desc));
+    EXPECT(follows(r_pvd, values, desc));
+}
+
+void radix_zero_width_copies() {
+    auto& e = *g_env;
+    constexpr uint n = 17u;
+    std::vector<int> keys(n);
+    std::vector<uint> values(n);
+    for (uint i = 0; i < n; ++i) {
+        keys[i] = static_cast<int>(i * 7u) - 31;
+        values[i] = n - i;
+    }
+    auto kin = e.device.create_buffer<int>(n), kout = e.device.create_buffer<int>(n);
+    auto vin = e.device.create_buffer<uint>(n), vout = e.device.create_buffer<uint>(n);
+    CommandList cmd;
+    e.radix_sort.SortPairs(cmd, BufferView<uint>{}, kin.view(), kout.view(), vin.view(), vout.view(), n, 9u, 9u);
+    e.stream << kin.copy_from(luisa::span{keys}) << vin.copy_from(luisa::span{values}) << cmd.commit();
+    std::vector<int> rk(n);
+    std::vector<uint> rv(n);
+    e.stream << kout.copy_to(luisa::span{rk}) << vout.copy_to(luisa::span{rv}) << synchronize();
+    EXPECT(rk == keys);
+    EXPECT(rv == values);
+}
+
+void radix_empty_input() {
+    auto& e = *g_env;
+    CommandList cmd;
+    e.radix_sort.SortKeys(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, 0u);
+    e.stream << cmd.commit() << synchronize();
+    EXPECT(DeviceRadixSort<>::GetSortKeysTempStorageBytes<int>(0u) == 0u);
+}
+
+void radix_double_buffer_selectors() {
+    auto& e = *g_env;
+    constexpr uint n = 65u, b = 0u, en = 5u;
+    std::vector<uint> keys(n), values(n);
+    for (uint i = 0; i < n; ++i) {
+        keys[i] = ((i * 19u) % 32u) | ((i % 7u) << 8u);
+        values[i] = i;
+    }
+    auto bits = [](uint k) { return k & 31u; };
+    const auto asc = stable_order(keys, bits, false);
+    const auto desc = stable_order(keys, bits, true);
+    auto k0 = e.device.create_buffer<uint>(n), k1 = e.device.create_buffer<uint>(n);
+    auto pk0 = e.device.create_buffer<uint>(n), pk1 = e.device.create_buffer<uint>(n);
+    auto pv0 = e.device.create_buffer<uint>(n), pv1 = e.device.create_buffer<uint>(n);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceRadixSort<>::GetSortPairsTempStorageBytes<uint, uint>(n)));
+    DoubleBuffer<uint> kb(k0.view(), k1.view());
+    kb.selector = 1;
+    DoubleBuffer<uint> pk(pk0.view(), pk1.view());
+    DoubleBuffer<uint> pv(pv0.view(), pv1.view());
+    CommandList cmd;
+    e.radix_sort.SortKeys(cmd, temp.view(), kb, n, b, en);
+    e.radix_sort.SortPairsDescending(cmd, temp.view(), pk, pv, n, b, en);
+    EXPECT(kb.selector == 0);  // one pass flips the selector once, at record time
+    EXPECT(pk.selector == 1);
+    EXPECT(pv.selector == pk.selector);
+    e.stream << k1.copy_from(luisa::span{keys}) << pk0.copy_from(luisa::span{keys})
+             << pv0.copy_from(luisa::span{values}) << cmd.commit();
+    std::vector<uint> ra(n), rdk(n), rdv(n);
+    e.stream << kb.current().copy_to(luisa::span{ra}) << pk.current().copy_to(luisa::span{rdk})
+             << pv.current().copy_to(luisa::span{rdv}) << synchronize();
+    EXPECT(follows(ra, keys, asc));
+    EXPECT(follows(rdk, keys, desc));
+    EXPECT(follows(rdv, values, desc));
+}
+
+void radix_double_buffer_zero_width_keeps_current() {
+    auto& e = *g_env;
+    std::array<int, 3> input{7, 2, 5};
+    auto b0 = e.device.create_buffer<int>(3), b1 = e.device.create_buffer<int>(3);
+    DoubleBuffer<int> buffers(b0.view(), b1.view());
+    buffers.selector = 1;
+    CommandList cmd;
+    e.radix_sort.SortKeys(cmd, BufferView<uint>{}, buffers, 3u, 4u, 4u);
+    EXPECT(buffers.selector == 1);
+    e.stream << b1.copy_from(luisa::span{input}) << cmd.commit();
+    std::array<int, 3> result{};
+    e.stream << buffers.current().copy_to(luisa::span{result}) << synchronize();
+    EXPECT(result == input);
+}
+
+void radix_large_keys_and_pairs() {
+    auto& e = *g_env;
+    const uint n = (1u << 22) + 1234u;
+    std::vector<uint> keys(n);
+    for (uint i = 0; i < n; ++i) keys[i] = (i * 2654435761u) ^ (i >> 7);  // lcpp_cub_bench.cpp:814
+    std::vector<uint> want = keys;
+    std::sort(want.begin(), want.end());
+    std::vector<uint64_t> k64(n);
+    std::vector<uint> idx(n);
+    for (uint i = 0; i < n; ++i) {
+        k64[i] = mix64(9, i) & mix64(10, i) & mix64(11, i);  // low-entropy keys: long runs of equal digits
+        idx[i] = i;
+    }
+    const auto order = stable_order(k64, [](uint64_t k) { return k; }, false);
+    auto kin = e.device.create_buffer<uint>(n), kout = e.device.create_buffer<uint>(n);
+    auto pin = e.device.create_buffer<uint64_t>(n), pout = e.device.create_buffer<uint64_t>(n);
+    auto vin = e.device.create_buffer<uint>(n), vout = e.device.create_buffer<uint>(n);
+    const size_t tb = std::max(DeviceRadixSort<>::GetSortKeysTempStorageBytes<uint>(n),
+                               DeviceRadixSort<>::GetSortPairsTempStorageBytes<uint64_t, uint>(n));
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(tb));
+    CommandList cmd;
+    e.radix_sort.SortKeys(cmd, temp.view(), kin.view(), kout.view(), n);
+    e.radix_sort.SortPairs(cmd, temp.view(), pin.view(), pout.view(), vin.view(), vout.view(), n);
+    std::vector<uint> got(n), gv(n);
+    std::vector<uint64_t> gk(n);
+    e.stream << kin.copy_from(luisa::span{keys}) << pin.copy_from(luisa::span{k64}) << vin.copy_from(luisa::span{idx})
+             << cmd.commit() << kout.copy_to(luisa::span{got}) << pout.copy_to(luisa::span{gk})
+             << vout.copy_to(luisa::span{gv}) << synchronize();
+    EXPECT(got == want);
+    EXPECT(follows(gk, k64, order));
+    EXPECT(gv == order);
+}
+
+void radix_float_and_signed_keys() {
+    auto& e = *g_env;
+    const uint n = 100003u;
+    std::vector<float> f(n);
+    std::vector<int64_t> s(n);
+    for (uint i = 0; i < n; ++i) {
+        const uint64_t r = mix64(3, i);
+        f[i] = (i % 97u == 0u) ? ((i & 1u) ? -0.0f : 0.0f)
+                               : static_cast<float>(static_cast<int64_t>(r >> 40) - (1 << 23)) * 1e-3f;
+        s[i] = static_cast<int64_t>(mix64(4, i));
+    }
+    // -0.0 and +0.0 share a digit pattern (common/util_type.h:141-175), so they stay in input order.
+    auto fkey = [](float x) { return x == 0.0f ? 0.0f : x; };
+    const auto forder = stable_order(f, fkey, true);
+    const auto sorder = stable_order(s, [](int64_t x) { return x; }, false);
+    auto fin = e.device.create_buffer<float>(n), fout = e.device.create_buffer<float>(n);
+    auto sin = e.device.create_buffer<int64_t>(n), sout = e.device.create_buffer<int64_t>(n);
+    const size_t tb = DeviceRadixSort<>::GetSortKeysTempStorageBytes<int64_t>(n);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(tb));
+    CommandList cmd;
+    e.radix_sort.SortKeysDescending(cmd, temp.view(), fin.view(), fout.view(), n);
+    e.radix_sort.SortKeys(cmd, temp.view(), sin.view(), sout.view(), n);
+    std::vector<float> gf(n);
+    std::vector<int64_t> gs(n);
+    e.stream << fin.copy_from(luisa::span{f}) << sin.copy_from(luisa::span{s}) << cmd.commit()
+             << fout.copy_to(luisa::span{gf}) << sout.copy_to(luisa::span{gs}) << synchronize();
+    EXPECT(follows(gf, f, forder));
+    EXPECT(follows(gs, s, sorder));
+}
+
+// ---- DeviceSpmv --------------------------------------------------------------------------------
+
+void spmv_float_unsigned_indices() {
+    auto& e = *g_env;
+    constexpr uint rows = 4u, cols = 5u;
+    const std::vector<uint> ro{0u, 3u, 3u, 6u, 8u};
+    const std::vector<uint> ci{0u, 2u, 4u, 1u, 2u, 3u, 0u, 4u};
+    const std::vector<float> a{1.5f, -2.0f, 0.25f, 3.0f, 1.25f, -0.5f, 2.0f, 4.0f};
+    const std::vector<float> x{2.0f, -1.0f, 0.5f, 3.0f, -2.0f};
+    std::vector<float> want(rows, 0.0f);
+    for (uint r = 0; r < rows; ++r)
+        for (uint k = ro[r]; k < ro[r + 1]; ++k) want[r] += a[k] * x[ci[k]];
+    auto da = e.device.create_buffer<float>(a.size());
+    auto dro = e.device.create_buffer<uint>(ro.size());
+    auto dci = e.device.create_buffer<uint>(ci.size());
+    auto dx = e.device.create_buffer<float>(x.size());
+    auto dy = e.device.create_buffer<float>(rows);
+    CommandList cmd;
+    e.spmv.CsrMV(cmd, BufferView<uint>{}, da.view(), dro.view(), dci.view(), dx.view(), dy.view(), rows, cols,
+                 a.size());
+    e.stream << da.copy_from(luisa::span{a}) << dro.copy_from(luisa::span{ro}) << dci.copy_from(luisa::span{ci})
+             << dx.copy_from(luisa::span{x}) << cmd.commit();
+    std::vector<float> got(rows);
+    e.stream << dy.copy_to(luisa::span{got}) << synchronize();
+    for (uint r = 0; r < rows; ++r) EXPECT(std::fabs(got[r] - want[r]) < 1.0e-5f);
+}
+
+void spmv_int_values_and_empty_work() {
+    auto& e = *g_env;
+    constexpr uint rows = 3u, cols = 4u;
+    const std::vector<int> ro{0, 2, 2, 5};
+    const std::vector<int> ci{1, 3, 0, 2, 3};
+    const std::vector<int> a{2, -3, 4, 5, -1};
+    const std::vector<int> x{7, -2, 3, 6};
+    const std::vector<int> want{2 * -2 + -3 * 6, 0, 4 * 7 + 5 * 3 + -1 * 6};
+    auto da = e.device.create_buffer<int>(a.size());
+    auto dro = e.device.create_buffer<int>(ro.size());
+    auto dci = e.device.create_buffer<int>(ci.size());
+    auto dx = e.device.create_buffer<int>(x.size());
+    auto dy = e.device.create_buffer<int>(rows);
+    auto dz = e.device.create_buffer<int>(rows);
+    const std::vector<int> junk(rows, 99);
+    CommandList cmd;
+    e.spmv.CsrMV(cmd, BufferView<uint>{}, da.view(), dro.view(), dci.view(), dx.view(), dy.view(), rows, cols,
+                 a.size());
+    // nnz == 0 zero-fills y; rows == 0 records nothing (tests/device_spmv_test.cpp:157-203).
+    e.spmv.CsrMV(cmd, BufferView<uint>{}, BufferView<int>{}, dro.view(), BufferView<int>{}, BufferView<int>{},
+                 dz.view(), rows, 0u, 0u);
+    e.spmv.CsrMV(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, BufferView<int>{},
+                 BufferView<int>{}, BufferView<int>{}, 0u, 0u, 0u);
+    e.stream << da.copy_from(luisa::span{a}) << dro.copy_from(luisa::span{ro}) << dci.copy_from(luisa::span{ci})
+             << dx.copy_from(luisa::span{x}) << dz.copy_from(luisa::span{junk}) << cmd.commit();
+    std::vector<int> got(rows), zeros(rows, -1);
+    e.stream << dy.copy_to(luisa::span{got}) << dz.copy_to(luisa::span{zeros}) << synchronize();
+    EXPECT(got == want);
+    EXPECT(zeros == std::vector<int>(rows, 0));
+}
+
+// ---- record-time checks ------------------------------------------------------------------------
+
+void precondition_errors() {
+    auto& e = *g_env;
+    const uint n = 100000u;
+    auto a = e.device.create_buffer<uint>(n);
+    auto small = e.device.create_buffer<uint>(2);
+    CommandList cmd;
+    EXPECT(throws_error([&] { e.scan.ExclusiveSum(cmd, small.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error([&] { e.reduce.Sum(cmd, small.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 5u, 3u); }));
+    EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 0u, 33u); }));
+    EXPECT(throws_error([&] { e.scan.ExclusiveSum(cmd, small.view(), a.view(), a.view(), n + 1u); }));
+    DeviceScan<> not_created;
+    EXPECT(throws_error([&] { not_created.ExclusiveSum(cmd, small.view(), a.view(), a.view(), 1u); }));
+    DoubleBuffer<uint> bad(a.view(), a.view());
+    bad.selector = 2;
+    EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), bad, 4u); }));
+    EXPECT(cmd.empty());  // nothing was recorded by a rejected call
+}
+
+const std::vector<Case>& cases() {
+    static const std::vector<Case> all{
+        {"reduce_sum_of_ones", reduce_sum_of_ones},
+        {"reduce_empty_writes_init", reduce_empty_writes_init},
+        {"reduce_bench_pattern_int_and_float", reduce_bench_pattern_int_and_float},
+        {"scan_sums_of_ones", scan_sums_of_ones},
+        {"scan_inclusive_init_in_place", scan_inclusive_init_in_place},
+        {"scan_bench_pattern_vs_std", scan_bench_pattern_vs_std},
+        {"radix_stable_partial_bit_ranges", radix_stable_partial_bit_ranges},
+        {"radix_zero_width_copies", radix_zero_width_copies},
+        {"radix_empty_input", radix_empty_input},
+        {"radix_double_buffer_selectors", radix_double_buffer_selectors},
+        {"radix_double_buffer_zero_width_keeps_current", radix_double_buffer_zero_width_keeps_current},
+        {"radix_large_keys_and_pairs", radix_large_keys_and_pairs},
+        {"radix_float_and_signed_keys", radix_float_and_signed_keys},
+        {"spmv_float_unsigned_indices", spmv_float_unsigned_indices},
+        {"spmv_int_values_and_empty_work", spmv_int_values_and_empty_work},
+        {"precondition_errors", precondition_errors},
+    };
+    return all;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const char* filter = nullptr;
+    for (int i = 1; i < argc; ++i) {
+        if (std::strcmp(argv[i], "--list") == 0) {
+            for (const auto& c : cases()) std::printf("%s\n", c.name);
+            return 0;
+        }
+        filter = argv[i];
+    }
+    Env env;
+    g_env = &env;
+    int run = 0;
+    for (const auto& c : cases()) {
+        if (filter && !std::strstr(c.name, filter)) continue;
+        g_current = c.name;
+        std::printf("case %s\n", c.name);
+        std::fflush(stdout);
+        const int before = g_failures;
+        try {
+            c.body();
+        } catch (const std::exception& ex) {
+            ++g_failures;
+            std::printf("  FAILED %s: exception %s\n", c.name, ex.what());
+        }
+        std::printf("  %s\n", g_failures == before ? "ok" : "FAILED");
+        std::fflush(stdout);
+        ++run;
+    }
+    std::printf("%d cases, %d failures\n", run, g_failures);
+    return g_failures == 0 && run > 0 ? 0 : 1;
+}

@@ -45,3 +45,15 @@ def test_error_reporting_without_gpu(hip):
     assert lib.lcpp_hip_spmv_csr_f32_i32(None, 0, None, None, None, None, None, 1 << 30, 1, 1, None) == \
         hip.ERR_INVALID_ARGUMENT
     assert lib.lcpp_hip_version().startswith(b"lcpp-hip")
+
+
+def test_facade_tests_build_and_list_cases():
+    """The C++20 facade headers compile against the C-ABI and link (the binary lists its cases without
+    touching a GPU)."""
+    import pathlib
+    import subprocess
+    repo = pathlib.Path(__file__).resolve().parents[1]
+    subprocess.run(["make", "-s", "-C", str(repo / "tests" / "cpp")], check=True)
+    out = subprocess.run([str(repo / "tests" / "cpp" / "bin" / "facade_test"), "--list"], check=True,
+                         capture_output=True, text=True).stdout.split()
+    assert len(out) == 16 and "radix_double_buffer_selectors" in out and "scan_inclusive_init_in_place" in out

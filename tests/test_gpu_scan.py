@@ -134,3 +134,33 @@ def test_forced_fallback_float_within_tolerance(hip, orc, dev, forced_fallback):
     exact, absum = orc.scan_sum_f32(a)
     bound = (np.arange(n) + 2) * np.finfo(np.float32).eps * absum
     assert np.all(np.abs(got - exact) <= bound)
+
+
+def gpu_scan_in_place(hip, suffix, a, inclusive=False, init=None):
+    """Scans `a` with d_in == d_out, as the reference's InclusiveScanInit test does
+    (tests/device_scan_test.cpp:288-321)."""
+    d = to_dev(a)
+    hip.scan_sum(suffix, d, d, a.size, inclusive=inclusive, init=init)
+    return to_host(d, a.dtype)
+
+
+def test_in_place_known_answer(hip, dev):
+    a = np.array([1, 2, 3, 4], np.int32)
+    assert gpu_scan_in_place(hip, "i32", a, inclusive=True, init=10).tolist() == [11, 13, 16, 20]
+
+
+@pytest.mark.parametrize("n", [24576 * 3 + 11, (1 << 22) + 77])
+def test_in_place_matches_oracle(hip, orc, dev, n):
+    a = orc.generate(1, n, n + 1)
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan_in_place(hip, "u32", a, inclusive), orc.scan_sum_u32(a, inclusive))
+
+
+@pytest.mark.parametrize("n", [24576 * 5 + 3, (1 << 22) + 77])
+def test_in_place_forced_fallback(hip, orc, dev, forced_fallback, n):
+    """Every look-back claims and recomputes its unpublished predecessors while their owners may be
+    overwriting the same buffer: the claim protocol keeps the in-place result exact."""
+    log(f"scan in-place forced fallback n={n}")
+    a = orc.generate(1, n, n + 2)
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan_in_place(hip, "u32", a, inclusive), orc.scan_sum_u32(a, inclusive))
