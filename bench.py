@@ -252,6 +252,20 @@ def main() -> int:
                 "GBps_8pass_model": round(2 * 8 * m * 12 / t / 1e6, 1),
                 "frac": round(2 * 8 * m * 12 / t / 1e6 / HBM_PEAK_GBS, 4)}
             del k, v, ko, vo, pt
+        # CsrMV fp32 (config 5): 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
+        import workloads
+        rows = cols = 1 << 20
+        va, ro, ci, xv, nnz = workloads.zipf_csr(rows, cols, SEED)
+        d = [torch.from_numpy(t).to(dev) for t in (va, ro, ci, xv)]
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        spmv = lambda: hip.spmv_csr("f32", "i32", d[0], d[1], d[2], d[3], y, rows, cols, nnz)
+        t = time_steps(spmv, steps, warmup)
+        sk, _ = kernel_avg_ms(hip, spmv, "spmv_csr", 5)
+        spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * cols
+        extra["spmv_csr_f32_zipf1.5_2p20"] = {"nnz": nnz, "ms": round(t, 5), "kernel_ms": round(sk, 5),
+                                              "GBps": round(spmv_bytes / sk / 1e6, 1),
+                                              "frac": round(spmv_bytes / sk / 1e6 / HBM_PEAK_GBS, 4)}
+        del d, y
         line["extra"] = extra
 
     print(json.dumps(line))

@@ -78,3 +78,25 @@ def test_integer_values_bit_exact_with_invalid_entries(hip, orc, dev, isfx):
     y = gpu_spmv(hip, "u32", isfx, va, ro.view(np.uint32) if isfx == "u32" else ro,
                  ci.view(np.uint32) if isfx == "u32" else ci, x, rows, cols, nnz)
     assert np.array_equal(to_host(y, np.uint32, rows), orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz))
+
+
+def test_benchmark_matrix_zipf_2p20(hip, orc, dev):
+    """The SpMV benchmark matrix: 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096] (about 51.7 M nonzeros),
+    distinct sorted columns per row, fp32 values and x in [-1, 1).  y within the condition-aware
+    1e-5 bound of the oracle's long-double sums, and bit-identical between two runs."""
+    import workloads
+    log("spmv zipf 2^20 generate")
+    rows = cols = 1 << 20
+    va, ro, ci, x, nnz = workloads.zipf_csr(rows, cols, 114521)
+    d_va, d_ro, d_ci, d_x = to_dev(va), to_dev(ro), to_dev(ci), to_dev(x)
+    y1 = torch.empty(rows, dtype=torch.float32, device=dev)
+    y2 = torch.empty(rows, dtype=torch.float32, device=dev)
+    log(f"spmv zipf 2^20 nnz={nnz}")
+    hip.spmv_csr("f32", "i32", d_va, d_ro, d_ci, d_x, y1, rows, cols, nnz)
+    hip.spmv_csr("f32", "i32", d_va, d_ro, d_ci, d_x, y2, rows, cols, nnz)
+    got = to_host(y1, np.float32).astype(np.float64)
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    exact, absum = orc.spmv_csr_fp(va, ro, ci, x, rows, cols, nnz)
+    err = np.abs(got - exact)
+    bound = 1e-5 * np.maximum(np.abs(exact), absum)
+    assert np.all(err <= bound), f"worst ratio {np.max(err / bound)}"
