@@ -106,48 +106,79 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d) {
 
 // --------------------------------------------------------------------------------------------
 // Histogram: digit counts of every pass for one portion.
+//
+// LDS atomics are the cost here, and random digits make the lanes of one ds_add collide on banks.
+// Each of the 32 banks therefore gets its own copy of the counters: lane l counts into copy l & 31,
+// and word (pass, digit / 2, copy) sits at bank `copy`, so the 64 lanes of an instruction touch each
+// bank at most twice whatever the digits are (skewed digits included).  A word packs the 16-bit
+// counters of an even/odd digit pair; a workgroup counts at most kHistMaxItems keys, which bounds
+// every counter by kHistMaxItems / 32 < 2^16.  LDS: sizeof(key) passes x 16 KB.
 // --------------------------------------------------------------------------------------------
-constexpr int kHistBlock = 256;
-constexpr int kHistUnroll = 8;
+constexpr int kHistCopies = 32;
+constexpr int kHistVecItems = 4;             // 16-byte loads per thread per step
+constexpr uint32_t kHistMaxItems = 1u << 20;  // keys per workgroup
+
+template <typename K>
+constexpr int hist_block() { return sizeof(K) == 4 ? 512 : 1024; }
 
 template <typename K, bool DESC>
-__global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restrict__ keys, uint32_t n,
-                                                                uint32_t* __restrict__ bins, uint32_t begin_bit,
-                                                                uint32_t end_bit, uint32_t passes) {
+__global__ __launch_bounds__(hist_block<K>()) void histogram_kernel(const K* __restrict__ keys, uint32_t n,
+                                                                     uint32_t per_block, uint32_t* __restrict__ bins,
+                                                                     uint32_t begin_bit, uint32_t end_bit,
+                                                                     uint32_t passes) {
     using U = typename KeyTraits<K>::U;
     constexpr int KIND = KeyTraits<K>::kind;
-    __shared__ uint32_t s_hist[kMaxPasses * kDigits];
-    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) s_hist[i] = 0;
+    constexpr int BLOCK = hist_block<K>();
+    constexpr int PASSES_MAX = sizeof(U);
+    constexpr int PER_VEC = 16 / sizeof(U);  // keys per 16-byte load
+    constexpr uint32_t PASS_WORDS = kDigits / 2 * kHistCopies;
+    __shared__ uint32_t s_hist[PASSES_MAX * PASS_WORDS];
+    for (uint32_t i = threadIdx.x; i < passes * PASS_WORDS; i += BLOCK) s_hist[i] = 0;
     __syncthreads();
 
+    const uint32_t copy = threadIdx.x % kHistCopies;
+    const uint64_t first = static_cast<uint64_t>(blockIdx.x) * per_block;
+    const uint64_t last = min(static_cast<uint64_t>(n), first + per_block);
+    auto count = [&](U key) {
+        const U ordered = twiddle_in<U, KIND, DESC>(key);
+#pragma unroll
+        for (uint32_t p = 0; p < PASSES_MAX; ++p) {
+            if (p >= passes) break;
+            const uint32_t shift = begin_bit + 8 * p;
+            const uint32_t nb = min(8u, end_bit - shift);
+            const uint32_t d = digit_of<U, KIND>(ordered, shift, (1u << nb) - 1u);
+            atomicAdd(&s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies + copy], 1u << ((d & 1u) * 16u));
+        }
+    };
     const U* ukeys = reinterpret_cast<const U*>(keys);
-    const uint64_t chunk = static_cast<uint64_t>(kHistBlock) * kHistUnroll;
-    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * chunk;
-    for (uint64_t base = static_cast<uint64_t>(blockIdx.x) * chunk; base < n; base += stride) {
-        U k[kHistUnroll];
-        bool ok[kHistUnroll];
+    // Scalar head up to 16-byte alignment, vector body, scalar tail.
+    uint64_t head = first;
+    const uint64_t misalign = (reinterpret_cast<uintptr_t>(ukeys + first) % 16) / sizeof(U);
+    const uint64_t head_end = misalign ? min(last, first + (PER_VEC - misalign)) : first;
+    for (uint64_t i = head + threadIdx.x; i < head_end; i += BLOCK) count(ukeys[i]);
+    using Vec = U __attribute__((ext_vector_type(PER_VEC)));
+    const uint64_t body_items = (last - head_end) / (PER_VEC * kHistVecItems * BLOCK) * (PER_VEC * kHistVecItems * BLOCK);
+    const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + head_end);
+    for (uint64_t v = 0; v < body_items / PER_VEC; v += static_cast<uint64_t>(kHistVecItems) * BLOCK) {
+        Vec k[kHistVecItems];
 #pragma unroll
-        for (int u = 0; u < kHistUnroll; ++u) {
-            const uint64_t i = base + static_cast<uint64_t>(u) * kHistBlock + threadIdx.x;
-            ok[u] = i < n;
-            k[u] = ok[u] ? __builtin_nontemporal_load(&ukeys[i]) : U(0);
-        }
+        for (int u = 0; u < kHistVecItems; ++u) k[u] = __builtin_nontemporal_load(&vkeys[v + u * BLOCK + threadIdx.x]);
 #pragma unroll
-        for (int u = 0; u < kHistUnroll; ++u) {
-            if (!ok[u]) continue;
-            const U ordered = twiddle_in<U, KIND, DESC>(k[u]);
-            for (uint32_t p = 0; p < passes; ++p) {
-                const uint32_t shift = begin_bit + 8 * p;
-                const uint32_t nb = min(8u, end_bit - shift);
-                const uint32_t d = digit_of<U, KIND>(ordered, shift, (1u << nb) - 1u);
-                atomicAdd(&s_hist[p * kDigits + d], 1u);
-            }
-        }
+        for (int u = 0; u < kHistVecItems; ++u)
+#pragma unroll
+            for (int e = 0; e < PER_VEC; ++e) count(k[u][e]);
     }
+    for (uint64_t i = head_end + body_items + threadIdx.x; i < last; i += BLOCK) count(ukeys[i]);
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) {
-        const uint32_t c = s_hist[i];
-        if (c) atomic_add_agent(&bins[i], c);
+
+    // Sum the 32 copies of each (pass, digit); lanes start at different copies so the reads spread
+    // over the banks.
+    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += BLOCK) {
+        const uint32_t p = i / kDigits, d = i % kDigits;
+        const uint32_t* row = &s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies];
+        uint32_t total = 0;
+        for (uint32_t c = 0; c < kHistCopies; ++c) total += (row[(c + i) % kHistCopies] >> ((d & 1u) * 16u)) & 0xFFFFu;
+        if (total) atomic_add_agent(&bins[p * kDigits + d], total);
     }
 }
 
@@ -339,53 +370,63 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
         s_keys[rank[k]] = keys[k];
     }
 
-    // Look-back over a window of kLookbackWindow predecessor tiles per step: each digit's thread
-    // issues the window's loads together (one memory latency per step), then sums back to its nearest
-    // INCLUSIVE entry.  One entry per step would advance the INCLUSIVE frontier by one tile per
-    // memory round trip, which then paces the whole pass; a window advances it by up to
-    // kLookbackWindow tiles.  Steps are workgroup-synchronous.  A needed entry that stays unpublished
-    // for `spin_limit` polls is counted here from its tile's keys (a predecessor tile is always full:
-    // only the last tile is partial) and published as PARTIAL by compare-and-swap.
+    // Look-back.  Each step inspects LB_GROUPS * kLookbackWindow predecessor tiles: thread
+    // d + 256 g (group g) loads, for digit d, the kLookbackWindow entries just older than those of
+    // group g - 1, all loads of a step issued together (one memory latency per step).  Each group sums
+    // back to the nearest INCLUSIVE entry of its window; group 0 chains the group sums, newest window
+    // first, until some window holds an INCLUSIVE entry (or tile 0).  Fewer, wider steps matter
+    // because the walk usually crosses tens of PARTIAL tiles and every step costs one cross-XCD round
+    // trip.  Steps are workgroup-synchronous.  A group waits only for the unpublished entries of its own
+    // window up to its own nearest INCLUSIVE entry (possibly more than the walk needs, never less;
+    // older tiles publish without waiting on this one).  An entry that stays unpublished for
+    // `spin_limit` polls is counted here from its tile's keys (a predecessor tile is always full: only
+    // the last tile is partial) and published as PARTIAL by compare-and-swap.
+    // The group sums travel through s_counts, which is dead after the reorder above.
+    constexpr int LB_GROUPS = BLOCK / static_cast<int>(kDigits);
+    static_assert(LB_GROUPS <= W, "group sums and flags live in rows of s_counts");
     uint32_t excl = 0;
     if (tile > 0) {
-        bool done = tid >= kDigits;
+        const uint32_t grp = tid / kDigits;
+        const uint32_t ld = tid % kDigits;  // look-back digit of this thread
+        bool done = false;                  // same value in every group (group 0 decides)
         int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
-        uint32_t* const column = lookback + d;
+        uint32_t* const column = lookback + ld;
         while (true) {
+            const int64_t gtop = top - static_cast<int64_t>(grp) * kLookbackWindow;  // this group's newest
             uint32_t v[kLookbackWindow];
 #pragma unroll
             for (int w = 0; w < kLookbackWindow; ++w) {
-                const int64_t j = top - w;
+                const int64_t j = gtop - w;
                 v[w] = (!done && j >= 0) ? atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]) : 0u;
             }
             uint32_t spins = 0;
             while (true) {
-                // First needed entry that is still unpublished (entries past the nearest INCLUSIVE one,
-                // or past tile 0, are not needed).
+                // First entry of the window, up to its nearest INCLUSIVE one (and not past tile 0), that is
+                // still unpublished.
                 int first_invalid = -1;
                 bool scanning = !done;
 #pragma unroll
                 for (int w = 0; w < kLookbackWindow; ++w) {
-                    const bool live = scanning && top - w >= 0;
+                    const bool live = scanning && gtop - w >= 0;
                     if (live && (v[w] & ~kCountMask) == 0) first_invalid = w;
                     scanning = live && (v[w] & ~kCountMask) != 0 && (v[w] & kFlagInclusive) == 0;
                 }
                 if (!__syncthreads_or(first_invalid >= 0)) break;
                 if (spins >= spin_limit) {
-                    // Fallback: count the newest tile that some digit is still waiting for.
+                    // Fallback: count the newest tile that some thread is still waiting for.
                     if (tid == 0) s_fallback_tile = 0;
                     __syncthreads();
-                    if (first_invalid >= 0) atomicMax(&s_fallback_tile, static_cast<uint32_t>(top - first_invalid) + 1u);
+                    if (first_invalid >= 0) atomicMax(&s_fallback_tile, static_cast<uint32_t>(gtop - first_invalid) + 1u);
                     __syncthreads();
                     const uint32_t jf = s_fallback_tile - 1u;
                     tile_digit_counts<K, DESC, BLOCK, ITEMS>(keys_in, jf, shift, mask, s_fallback);
-                    const int wf = static_cast<int>(top - static_cast<int64_t>(jf));
+                    const int wf = static_cast<int>(gtop - static_cast<int64_t>(jf));
                     if (!done) {
 #pragma unroll
                         for (int w = 0; w < kLookbackWindow; ++w) {
                             if (w == wf && (v[w] & ~kCountMask) == 0) {
                                 uint32_t expected = 0;
-                                const uint32_t desired = kFlagPartial | s_fallback[d];
+                                const uint32_t desired = kFlagPartial | s_fallback[ld];
                                 v[w] = __hip_atomic_compare_exchange_strong(
                                            &column[static_cast<uint64_t>(jf) * kDigits], &expected, desired,
                                            __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -401,30 +442,51 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                 if (!done) {
 #pragma unroll
                     for (int w = 0; w < kLookbackWindow; ++w) {
-                        const int64_t j = top - w;
+                        const int64_t j = gtop - w;
                         if (j >= 0 && (v[w] & ~kCountMask) == 0)
                             v[w] = atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]);
                     }
                 }
             }
+            // Sum of the window down to (and including) its nearest INCLUSIVE entry or tile 0.
+            uint32_t window_sum = 0;
+            bool window_stops = false;
             if (!done) {
-                int stop = kLookbackWindow;  // window slot of the entry that ends the walk, if any
-                uint32_t window_sum = 0;
 #pragma unroll
                 for (int w = 0; w < kLookbackWindow; ++w) {
-                    if (stop == kLookbackWindow) {
+                    if (!window_stops && gtop - w >= 0) {
                         window_sum += v[w] & kCountMask;
                         // Tile 0's counts start at the portion base, so the walk always ends there.
-                        if ((v[w] & kFlagInclusive) || top - w == 0) stop = w;
+                        if ((v[w] & kFlagInclusive) || gtop - w == 0) window_stops = true;
                     }
                 }
-                excl += window_sum;
-                // (Upgrading the crossed PARTIAL entries to INCLUSIVE was measured slower: the extra
-                // agent-scope stores cost more than the shorter walks they buy.)
-                if (stop < kLookbackWindow) done = true;
             }
-            if (!__syncthreads_or(!done)) break;
-            top -= kLookbackWindow;
+            if constexpr (LB_GROUPS > 1) {
+                if (grp > 0) s_counts[grp - 1][ld] = window_sum | (window_stops ? 0x80000000u : 0u);
+                __syncthreads();
+                if (grp == 0 && !done) {
+#pragma unroll
+                    for (int g = 1; g < LB_GROUPS; ++g) {
+                        if (window_stops) break;
+                        const uint32_t x = s_counts[g - 1][ld];
+                        window_sum += x & 0x7FFFFFFFu;
+                        window_stops = (x >> 31) != 0;
+                    }
+                }
+            }
+            // (Upgrading the crossed PARTIAL entries to INCLUSIVE was measured slower: the extra
+            // agent-scope stores cost more than the shorter walks they buy.)
+            if (grp == 0 && !done) {
+                excl += window_sum;
+                done = window_stops;
+                if constexpr (LB_GROUPS > 1) s_counts[W - 1][ld] = done ? 1u : 0u;
+            }
+            const bool more = __syncthreads_or(grp == 0 && !done);
+            if constexpr (LB_GROUPS > 1) {
+                if (grp > 0) done = s_counts[W - 1][ld] != 0;
+            }
+            if (!more) break;
+            top -= static_cast<int64_t>(LB_GROUPS) * kLookbackWindow;
         }
         if (tid < kDigits) atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
     }
@@ -547,14 +609,20 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
     if (st != kOk) return st;
 
     const K* hist_src = db_keys ? db_keys[sel] : keys_in;
-    const unsigned hist_grid = static_cast<unsigned>(device_cu_count()) * 4;
+    // Two workgroups per CU for 4-byte keys (64 KB of counters each), one for 8-byte keys; contiguous
+    // slices of at most kHistMaxItems keys, rounded to whole 16-byte steps of the workgroup.
+    constexpr uint32_t hist_step = static_cast<uint32_t>(hist_block<K>()) * kHistVecItems * (16 / sizeof(K));
+    const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
     for (uint32_t q = 0; q < L.portions; ++q) {
         const uint32_t len = std::min(L.portion, n - q * L.portion);
-        const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(hist_grid, ceil_div(len, kHistBlock * kHistUnroll)));
+        uint64_t per = ceil_div(ceil_div(len, hist_target), hist_step) * hist_step;
+        per = std::min<uint64_t>(per, kHistMaxItems);
+        const unsigned grid = static_cast<unsigned>(ceil_div(len, per));
         LaunchScope scope("radix_histogram", stream);
         // Every portion adds into the totals of portion 0's slots.
-        histogram_kernel<K, DESC><<<grid, kHistBlock, 0, stream>>>(hist_src + static_cast<size_t>(q) * L.portion, len,
-                                                                   bins, begin_bit, end_bit, L.passes);
+        histogram_kernel<K, DESC><<<grid, hist_block<K>(), 0, stream>>>(
+            hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit,
+            L.passes);
         st = check_hip(hipGetLastError(), "radix_histogram launch");
         if (st != kOk) return st;
     }

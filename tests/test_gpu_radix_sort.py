@@ -271,13 +271,16 @@ def test_benchmark_sort_pairs_2p27(hip, orc, dev, kind):
     complete_stable_check(to_host(k, np.uint64), to_host(ko, np.uint64), to_host(vo, np.uint32))
 
 
-@pytest.mark.parametrize("kdtype,vbytes,descending", [(np.uint32, 0, False), (np.uint32, 4, True),
-                                                      (np.uint64, 4, False), (np.float32, 0, True)])
-def test_forced_lookback_fallback(hip, orc, dev, kdtype, vbytes, descending):
+@pytest.mark.parametrize("kdtype,vbytes,descending,n", [(np.uint32, 0, False, (1 << 20) + 4321),
+                                                        (np.uint32, 4, True, (1 << 20) + 4321),
+                                                        (np.uint64, 4, False, (1 << 20) + 4321),
+                                                        (np.float32, 0, True, (1 << 20) + 4321),
+                                                        (np.uint32, 0, False, (1 << 23) + 17)])
+def test_forced_lookback_fallback(hip, orc, dev, kdtype, vbytes, descending, n):
     """Spin limit 0: every unpublished predecessor's digit counts are computed by the waiting
-    workgroup from that tile's keys and published by compare-and-swap."""
+    workgroup from that tile's keys and published by compare-and-swap (the largest case walks back
+    over hundreds of tiles, several look-back steps per tile)."""
     lib = hip.lib()
-    n = (1 << 20) + 4321
     log(f"sort forced fallback {kdtype.__name__} vbytes={vbytes} desc={descending}")
     raw = orc.generate(0, n, 808)
     keys = raw.copy() if kdtype == np.uint64 else (raw >> np.uint64(32)).astype(np.uint32).view(kdtype).copy()
@@ -326,3 +329,31 @@ def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
             assert np.array_equal(vo, evo)
     finally:
         lib.lcpp_hip_internal_radix_rank_mode(1)
+
+
+def test_constant_keys_large(hip, dev):
+    """2^25 identical keys: every histogram count lands in one digit of every pass (the packed 16-bit
+    per-bank counters of one workgroup must not overflow), and the sort is the identity."""
+    n = 1 << 25
+    log("sort constant keys 2^25")
+    d = torch.full((n,), 0x12345678, dtype=torch.int32, device=dev)
+    out = torch.empty_like(d)
+    hip.sort_keys("u32", d, out, n)
+    assert torch.equal(out, d)
+
+
+def test_two_valued_u64_pairs_large(hip, dev):
+    """2^24 u64 keys taking two values (1/3 vs 2/3 of the items) with index values: keys grouped,
+    values increasing inside each group (stability), counts exact."""
+    n = 1 << 24
+    log("sort pairs two-valued u64 2^24")
+    idx = torch.arange(n, dtype=torch.int64, device=dev)
+    k = torch.where(idx % 3 == 0, torch.tensor(7 << 40, device=dev), torch.tensor(5 << 40, device=dev))
+    v = idx.to(torch.int32)
+    ko, vo = torch.empty_like(k), torch.empty_like(v)
+    hip.sort_pairs("u64", 4, k, ko, v, vo, n)
+    n7 = (n + 2) // 3
+    expect_v = torch.cat([idx[idx % 3 != 0], idx[idx % 3 == 0]]).to(torch.int32)
+    assert torch.equal(vo, expect_v)
+    assert torch.equal(ko[: n - n7], torch.full((n - n7,), 5 << 40, dtype=torch.int64, device=dev))
+    assert torch.equal(ko[n - n7:], torch.full((n7,), 7 << 40, dtype=torch.int64, device=dev))
