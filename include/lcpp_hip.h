@@ -28,6 +28,11 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden visibility; only the declarations below are exported. */
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
 #define LCPP_HIP_OK 0
 #define LCPP_HIP_ERR_INVALID_ARGUMENT (-1)
 #define LCPP_HIP_ERR_TEMP_TOO_SMALL (-2)
@@ -182,6 +187,22 @@ LCPP_HIP_DECLARE_SPMV(u32, uint32_t, u32, uint32_t)
 #define LCPP_HIP_GEN_U32_IOTA 5       /* out[i] = start + i (uint32)                             */
 #define LCPP_HIP_GEN_F32_PM1 6        /* out[i] = uniform float in [-1, 1): ((r_i>>40) * 2^-23) - 1 */
 int lcpp_hip_generate(int kind, void* out, uint64_t n, uint64_t seed, uint64_t start, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Introspection and test hooks (no reference counterpart): the bytes of temp storage the kernels
+ * actually carve, the onesweep portion count for a given temp size, and the in-wave ranking variant
+ * of the onesweep kernel (0 ballot match, 1 LDS lane-mask table, the default; same ranks).
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n);
+size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
+                                            uint32_t end_bit, int double_buffer);
+uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
+                                          uint32_t end_bit, int double_buffer, size_t temp_bytes);
+int lcpp_hip_internal_radix_rank_mode(int mode);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
 
 #ifdef __cplusplus
 }

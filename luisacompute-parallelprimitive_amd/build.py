@@ -24,12 +24,12 @@ LIB = PKG / "liblcpp_hip.so"
 ARCH = "gfx950"
 
 HIP_FLAGS = [
-    "-O3", "-std=c++20", f"--offload-arch={ARCH}", "-fPIC", "-Wall", "-Wno-unused-function",
+    "-O3", "-std=c++20", f"--offload-arch={ARCH}", "-fPIC", "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
     # Keep the compiler from forming packed-FP32 VALU instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{REPO / 'include'}",
 ]
-HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-Wall", f"-I{REPO / 'include'}"]
+HOST_FLAGS = ["-O2", "-std=c++20", "-fPIC", "-fvisibility=hidden", "-Wall", f"-I{REPO / 'include'}"]
 
 
 def _hipcc() -> str:
@@ -58,7 +58,12 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # Only the C-ABI (lcpp_hip_*) is exported: kernel stubs and C++ internals stay local, so two builds
+    # loaded into one process never resolve each other's internals.
+    exports = BUILD / "exports.map"
+    exports.write_text("{\n  global: lcpp_hip_*;\n  local: *;\n};\n")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={exports}", "-o", str(tmp),
+           *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

@@ -112,68 +112,81 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d) {
 // and word (pass, digit / 2, copy) sits at bank `copy`, so the 64 lanes of an instruction touch each
 // bank at most twice whatever the digits are (skewed digits included).  A word packs the 16-bit
 // counters of an even/odd digit pair; a workgroup counts at most kHistMaxItems keys, which bounds
-// every counter by kHistMaxItems / 32 < 2^16.  LDS: sizeof(key) passes x 16 KB.
+// every counter by kHistMaxItems / 32 (+ a few head/tail keys) < 2^16.  LDS: sizeof(key) passes x
+// 16 KB, so two 1024-thread workgroups per CU for 4-byte keys and one for 8-byte keys.
 // --------------------------------------------------------------------------------------------
 constexpr int kHistCopies = 32;
-constexpr int kHistVecItems = 4;             // 16-byte loads per thread per step
+constexpr int kHistBlock = 1024;
+constexpr int kHistVecItems = 8;             // 16-byte loads per thread per step
 constexpr uint32_t kHistMaxItems = 1u << 20;  // keys per workgroup
 
-template <typename K>
-constexpr int hist_block() { return sizeof(K) == 4 ? 512 : 1024; }
-
-template <typename K, bool DESC>
-__global__ __launch_bounds__(hist_block<K>()) void histogram_kernel(const K* __restrict__ keys, uint32_t n,
-                                                                     uint32_t per_block, uint32_t* __restrict__ bins,
-                                                                     uint32_t begin_bit, uint32_t end_bit,
-                                                                     uint32_t passes) {
+// FULL: every 8-bit digit of the key (begin_bit 0, end_bit = key bits), so digit positions are
+// compile-time constants and each pass costs two bit-field extracts, one address and one increment.
+template <typename K, bool DESC, bool FULL>
+__global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restrict__ keys, uint32_t n,
+                                                                uint32_t per_block, uint32_t* __restrict__ bins,
+                                                                uint32_t begin_bit, uint32_t end_bit, uint32_t passes) {
     using U = typename KeyTraits<K>::U;
     constexpr int KIND = KeyTraits<K>::kind;
-    constexpr int BLOCK = hist_block<K>();
     constexpr int PASSES_MAX = sizeof(U);
     constexpr int PER_VEC = 16 / sizeof(U);  // keys per 16-byte load
     constexpr uint32_t PASS_WORDS = kDigits / 2 * kHistCopies;
     __shared__ uint32_t s_hist[PASSES_MAX * PASS_WORDS];
-    for (uint32_t i = threadIdx.x; i < passes * PASS_WORDS; i += BLOCK) s_hist[i] = 0;
+    if constexpr (FULL) passes = PASSES_MAX;
+    for (uint32_t i = threadIdx.x; i < passes * PASS_WORDS; i += kHistBlock) s_hist[i] = 0;
     __syncthreads();
 
     const uint32_t copy = threadIdx.x % kHistCopies;
     const uint64_t first = static_cast<uint64_t>(blockIdx.x) * per_block;
     const uint64_t last = min(static_cast<uint64_t>(n), first + per_block);
     auto count = [&](U key) {
-        const U ordered = twiddle_in<U, KIND, DESC>(key);
+        U ordered = twiddle_in<U, KIND, DESC>(key);
+        if constexpr (KIND == kFloat) {
+            // -0.0 counts as +0.0 (digit_of applies the same mapping).
+            constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+            if (ordered == U(~kHigh)) ordered = kHigh;
+        }
 #pragma unroll
         for (uint32_t p = 0; p < PASSES_MAX; ++p) {
-            if (p >= passes) break;
-            const uint32_t shift = begin_bit + 8 * p;
-            const uint32_t nb = min(8u, end_bit - shift);
-            const uint32_t d = digit_of<U, KIND>(ordered, shift, (1u << nb) - 1u);
-            atomicAdd(&s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies + copy], 1u << ((d & 1u) * 16u));
+            uint32_t pair, odd;  // digit / 2 and digit % 2
+            if constexpr (FULL) {
+                pair = static_cast<uint32_t>(ordered >> (8 * p + 1)) & 0x7Fu;
+                odd = static_cast<uint32_t>(ordered >> (8 * p)) & 1u;
+            } else {
+                if (p >= passes) break;
+                const uint32_t shift = begin_bit + 8 * p;
+                const uint32_t nb = min(8u, end_bit - shift);
+                const uint32_t d = static_cast<uint32_t>(ordered >> shift) & ((1u << nb) - 1u);
+                pair = d >> 1;
+                odd = d & 1u;
+            }
+            atomicAdd(&s_hist[p * PASS_WORDS + pair * kHistCopies + copy], 1u + odd * 0xFFFFu);
         }
     };
     const U* ukeys = reinterpret_cast<const U*>(keys);
     // Scalar head up to 16-byte alignment, vector body, scalar tail.
-    uint64_t head = first;
     const uint64_t misalign = (reinterpret_cast<uintptr_t>(ukeys + first) % 16) / sizeof(U);
     const uint64_t head_end = misalign ? min(last, first + (PER_VEC - misalign)) : first;
-    for (uint64_t i = head + threadIdx.x; i < head_end; i += BLOCK) count(ukeys[i]);
+    for (uint64_t i = first + threadIdx.x; i < head_end; i += kHistBlock) count(ukeys[i]);
     using Vec = U __attribute__((ext_vector_type(PER_VEC)));
-    const uint64_t body_items = (last - head_end) / (PER_VEC * kHistVecItems * BLOCK) * (PER_VEC * kHistVecItems * BLOCK);
+    constexpr uint64_t STEP = static_cast<uint64_t>(PER_VEC) * kHistVecItems * kHistBlock;
+    const uint64_t body_items = (last - head_end) / STEP * STEP;
     const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + head_end);
-    for (uint64_t v = 0; v < body_items / PER_VEC; v += static_cast<uint64_t>(kHistVecItems) * BLOCK) {
+    for (uint64_t v = 0; v < body_items / PER_VEC; v += static_cast<uint64_t>(kHistVecItems) * kHistBlock) {
         Vec k[kHistVecItems];
 #pragma unroll
-        for (int u = 0; u < kHistVecItems; ++u) k[u] = __builtin_nontemporal_load(&vkeys[v + u * BLOCK + threadIdx.x]);
+        for (int u = 0; u < kHistVecItems; ++u) k[u] = __builtin_nontemporal_load(&vkeys[v + u * kHistBlock + threadIdx.x]);
 #pragma unroll
         for (int u = 0; u < kHistVecItems; ++u)
 #pragma unroll
             for (int e = 0; e < PER_VEC; ++e) count(k[u][e]);
     }
-    for (uint64_t i = head_end + body_items + threadIdx.x; i < last; i += BLOCK) count(ukeys[i]);
+    for (uint64_t i = head_end + body_items + threadIdx.x; i < last; i += kHistBlock) count(ukeys[i]);
     __syncthreads();
 
     // Sum the 32 copies of each (pass, digit); lanes start at different copies so the reads spread
     // over the banks.
-    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += BLOCK) {
+    for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) {
         const uint32_t p = i / kDigits, d = i % kDigits;
         const uint32_t* row = &s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies];
         uint32_t total = 0;
@@ -611,8 +624,9 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
     const K* hist_src = db_keys ? db_keys[sel] : keys_in;
     // Two workgroups per CU for 4-byte keys (64 KB of counters each), one for 8-byte keys; contiguous
     // slices of at most kHistMaxItems keys, rounded to whole 16-byte steps of the workgroup.
-    constexpr uint32_t hist_step = static_cast<uint32_t>(hist_block<K>()) * kHistVecItems * (16 / sizeof(K));
+    constexpr uint32_t hist_step = static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
     const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
+    const bool full = begin_bit == 0 && end_bit == sizeof(K) * 8;
     for (uint32_t q = 0; q < L.portions; ++q) {
         const uint32_t len = std::min(L.portion, n - q * L.portion);
         uint64_t per = ceil_div(ceil_div(len, hist_target), hist_step) * hist_step;
@@ -620,9 +634,14 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         const unsigned grid = static_cast<unsigned>(ceil_div(len, per));
         LaunchScope scope("radix_histogram", stream);
         // Every portion adds into the totals of portion 0's slots.
-        histogram_kernel<K, DESC><<<grid, hist_block<K>(), 0, stream>>>(
-            hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit,
-            L.passes);
+        if (full)
+            histogram_kernel<K, DESC, true><<<grid, kHistBlock, 0, stream>>>(
+                hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit,
+                end_bit, L.passes);
+        else
+            histogram_kernel<K, DESC, false><<<grid, kHistBlock, 0, stream>>>(
+                hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit,
+                end_bit, L.passes);
         st = check_hip(hipGetLastError(), "radix_histogram launch");
         if (st != kOk) return st;
     }
