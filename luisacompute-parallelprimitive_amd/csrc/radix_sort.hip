@@ -217,6 +217,24 @@ __global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict
 // Onesweep pass.
 // --------------------------------------------------------------------------------------------
 
+// Tile of a workgroup.  The dispatcher sends workgroup b to XCD b % 8 (measured), and tile t's digit
+// runs end in the same cache lines where tile t + 1's begin.  So XCD x's j-th workgroup takes tile
+// ((j / G) * 8 + x) * G + j % G: each XCD handles G consecutive tiles at a time, their shared boundary
+// lines merge in that XCD's L2, and the write traffic of a pass drops (the scatter pattern alone runs
+// 0.69 -> 0.52 ms at 2^28 with G = 16).  A full super-block of 8 G tiles is permuted; the remainder
+// keeps its order, so the map is a bijection on [0, tiles).  Look-back stays deadlock-free: a tile
+// waits only on tiles of lower index, which are dispatched no more than G - 1 steps later on the
+// lower-numbered XCDs (and the look-back fallback computes any predecessor that stays unpublished).
+constexpr uint32_t kXcds = 8;
+constexpr uint32_t kXcdGroup = 16;
+
+__device__ __forceinline__ uint32_t tile_of_block(uint32_t b, uint32_t tiles) {
+    constexpr uint32_t kSuper = kXcds * kXcdGroup;
+    if (b >= tiles / kSuper * kSuper) return b;
+    const uint32_t x = b % kXcds, j = b / kXcds;
+    return ((j / kXcdGroup) * kXcds + x) * kXcdGroup + j % kXcdGroup;
+}
+
 // Look-back fallback: digit counts of the full tile `tile` of `keys`, accumulated in LDS `counts`
 // (256 words).  Called by every thread of the workgroup.
 template <typename K, bool DESC, int BLOCK, int ITEMS>
@@ -276,7 +294,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
         s_counts[wave][i] = 0;
         if constexpr (RANK == kRankLdsMatch) s_match[wave][i] = 0;
     }
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = tile_of_block(blockIdx.x, gridDim.x);
     const uint32_t tile_base = tile * TILE;
     const uint32_t valid = min(TILE, n - tile_base);
 
