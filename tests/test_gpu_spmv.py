@@ -100,3 +100,30 @@ def test_benchmark_matrix_zipf_2p20(hip, orc, dev):
     err = np.abs(got - exact)
     bound = 1e-5 * np.maximum(np.abs(exact), absum)
     assert np.all(err <= bound), f"worst ratio {np.max(err / bound)}"
+
+
+def test_integer_stream_segments_bit_exact(hip, orc, dev):
+    """Integer sums are exact in any order, so this pins the nonzero-stream walk: runs of empty rows
+    (also at the start and end of a wave's 64 rows), rows of length 1, and rows long enough to span
+    several 512-nonzero chunks and lane boundaries."""
+    rng = np.random.default_rng(77)
+    rows, cols = 6000, 9000
+    kind = rng.integers(0, 10, rows)
+    lengths = np.where(kind < 3, 0, np.where(kind < 6, 1, rng.integers(2, 40, rows)))
+    lengths[rng.integers(0, rows, 25)] = rng.integers(500, 4000, 25)  # multi-chunk rows
+    lengths[0:70] = 0              # a fully empty wave and the start of the next one
+    lengths[127] = 0
+    lengths[128:140] = 1
+    lengths[191] = 2000            # a long row as the last row of a wave
+    lengths[-5:] = 0               # trailing empty rows
+    ro = np.zeros(rows + 1, np.int64)
+    ro[1:] = np.cumsum(lengths)
+    nnz = int(ro[-1])
+    ci = np.concatenate([np.sort(rng.choice(cols, size=int(L), replace=False)) if L else np.zeros(0, np.int64)
+                         for L in lengths]).astype(np.uint32)
+    ro = ro.astype(np.uint32)
+    va = orc.generate(1, nnz, 31)
+    x = orc.generate(1, cols, 32)
+    log(f"spmv integer stream nnz={nnz}")
+    y = gpu_spmv(hip, "u32", "u32", va, ro, ci, x, rows, cols, nnz)
+    assert np.array_equal(to_host(y, np.uint32, rows), orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz))
