@@ -11,6 +11,7 @@ FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `-
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
+                       [--only reduce|scan|sortpairs|spmv]
 """
 from __future__ import annotations
 
@@ -103,6 +104,95 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def extra_reduce(hip, dev, steps, warmup, extra):
+    import torch
+    flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
+    # Reduce 2^24 int32 (config 1): hot (MALL-resident) and cold (MALL flushed before each call).
+    m = 1 << 24
+    a = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
+    s = torch.empty(1, dtype=torch.int32, device=dev)
+    rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+    hot = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
+    cold_k, _ = kernel_avg_ms(hip, lambda: (flush_mall(flush), hip.reduce_sum("i32", a, s, m, temp=rt)),
+                              "reduce_sum_partials", 5)
+    extra["reduce_sum_i32_2p24"] = {"ms_hot": round(hot, 5), "GBps_hot": round(4 * m / hot / 1e6, 1),
+                                    "kernel_ms_cold": round(cold_k, 5),
+                                    "GBps_cold": round(4 * m / cold_k / 1e6, 1)}
+    del flush
+    # Reduce 2^28 int32 (north-star size).
+    m = 1 << 28
+    a = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
+    rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+    t = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
+    extra["reduce_sum_i32_2p28"] = {"ms": round(t, 5), "GBps": round(4 * m / t / 1e6, 1),
+                                    "frac": round(4 * m / t / 1e6 / HBM_PEAK_GBS, 4)}
+
+
+def extra_scan(hip, dev, steps, warmup, extra):
+    import torch
+    # ExclusiveSum 2^28 uint32 in [0, 16) (config 2).
+    m = 1 << 28
+    b = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_LT16, b, m, SEED)
+    c = torch.empty_like(b)
+    st = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+    t = time_steps(lambda: hip.scan_sum("u32", b, c, m, temp=st), steps, warmup)
+    sk, _ = kernel_avg_ms(hip, lambda: hip.scan_sum("u32", b, c, m, temp=st), "scan_sum", 5)
+    extra["exclusive_sum_u32_2p28"] = {"ms": round(t, 5), "GBps": round(8 * m / t / 1e6, 1),
+                                       "frac": round(8 * m / t / 1e6 / HBM_PEAK_GBS, 4),
+                                       "kernel_ms": round(sk, 5)}
+
+
+def extra_sort_pairs(hip, dev, steps, warmup, extra):
+    import torch
+    # SortPairs 2^27 u64 keys + u32 index values (config 4), uniform and AND-of-3 keys.
+    m = 1 << 27
+    for kind, gen in (("uniform", hip.GEN_U64), ("and3", hip.GEN_U64_AND3)):
+        k = torch.empty(m, dtype=torch.int64, device=dev)
+        hip.generate(gen, k, m, SEED)
+        v = torch.empty(m, dtype=torch.int32, device=dev)
+        hip.generate(hip.GEN_U32_IOTA, v, m, 0)
+        ko, vo = torch.empty_like(k), torch.empty_like(v)
+        pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32, device=dev)
+        t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), 1)
+        extra[f"sort_pairs_u64_u32_2p27_{kind}"] = {
+            "ms": round(t, 4), "Gpairs_per_s": round(m / t / 1e6, 3),
+            "GBps_8pass_model": round(2 * 8 * m * 12 / t / 1e6, 1),
+            "frac": round(2 * 8 * m * 12 / t / 1e6 / HBM_PEAK_GBS, 4)}
+        del k, v, ko, vo, pt
+
+
+def extra_spmv(hip, dev, steps, warmup, extra):
+    import torch
+    import workloads
+    # CsrMV fp32 (config 5): 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
+    rows = cols = 1 << 20
+    va, ro, ci, xv, nnz = workloads.zipf_csr(rows, cols, SEED)
+    d = [torch.from_numpy(t).to(dev) for t in (va, ro, ci, xv)]
+    y = torch.empty(rows, dtype=torch.float32, device=dev)
+    spmv = lambda: hip.spmv_csr("f32", "i32", d[0], d[1], d[2], d[3], y, rows, cols, nnz)
+    t = time_steps(spmv, steps, warmup)
+    sk, _ = kernel_avg_ms(hip, spmv, "spmv_csr", 5)
+    spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * cols
+    extra["spmv_csr_f32_zipf1.5_2p20"] = {"nnz": nnz, "ms": round(t, 5), "kernel_ms": round(sk, 5),
+                                          "GBps": round(spmv_bytes / sk / 1e6, 1),
+                                          "frac": round(spmv_bytes / sk / 1e6 / HBM_PEAK_GBS, 4)}
+
+
+EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv}
+
+
+def run_extras(hip, dev, steps, warmup, names):
+    import torch
+    extra = {}
+    for name in names:
+        EXTRAS[name](hip, dev, steps, warmup, extra)
+        torch.cuda.empty_cache()
+    return extra
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,6 +200,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline SortKeys only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=sorted(EXTRAS), default=None,
+                    help="run only this secondary configuration (for profiling); prints its extra entry")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
@@ -126,6 +218,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
     steps, warmup = args.steps, args.warmup
+    if args.only:
+        print(json.dumps({"only": args.only, "extra": run_extras(hip, dev, steps, warmup, [args.only])}))
+        return 0
 
     # ---- headline: SortKeys 2^28 u32 ---------------------------------------------------------------
     n = 1 << 28
@@ -201,72 +296,7 @@ def main() -> int:
 
     # ---- other configurations -----------------------------------------------------------------------
     if not args.no_extra:
-        extra = {}
-        flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
-
-        # Reduce 2^24 int32 (config 1): hot (MALL-resident) and cold (MALL flushed before each call).
-        m = 1 << 24
-        a = torch.empty(m, dtype=torch.int32, device=dev)
-        hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
-        s = torch.empty(1, dtype=torch.int32, device=dev)
-        rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
-        hot = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
-        cold_k, _ = kernel_avg_ms(hip, lambda: (flush_mall(flush), hip.reduce_sum("i32", a, s, m, temp=rt)),
-                                  "reduce_sum_partials", 5)
-        extra["reduce_sum_i32_2p24"] = {"ms_hot": round(hot, 5), "GBps_hot": round(4 * m / hot / 1e6, 1),
-                                        "kernel_ms_cold": round(cold_k, 5),
-                                        "GBps_cold": round(4 * m / cold_k / 1e6, 1)}
-        # Reduce 2^28 int32 (north-star size).
-        m = 1 << 28
-        a = torch.empty(m, dtype=torch.int32, device=dev)
-        hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
-        rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
-        t = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
-        extra["reduce_sum_i32_2p28"] = {"ms": round(t, 5), "GBps": round(4 * m / t / 1e6, 1),
-                                        "frac": round(4 * m / t / 1e6 / HBM_PEAK_GBS, 4)}
-        del a
-        # ExclusiveSum 2^28 uint32 in [0, 16) (config 2).
-        b = torch.empty(m, dtype=torch.int32, device=dev)
-        hip.generate(hip.GEN_U32_LT16, b, m, SEED)
-        c = torch.empty_like(b)
-        st = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
-        t = time_steps(lambda: hip.scan_sum("u32", b, c, m, temp=st), steps, warmup)
-        sk, _ = kernel_avg_ms(hip, lambda: hip.scan_sum("u32", b, c, m, temp=st), "scan_sum", 5)
-        extra["exclusive_sum_u32_2p28"] = {"ms": round(t, 5), "GBps": round(8 * m / t / 1e6, 1),
-                                           "frac": round(8 * m / t / 1e6 / HBM_PEAK_GBS, 4),
-                                           "kernel_ms": round(sk, 5)}
-        del b, c, st
-        # SortPairs 2^27 u64 keys + u32 index values (config 4), uniform and AND-of-3 keys.
-        m = 1 << 27
-        for kind, gen in (("uniform", hip.GEN_U64), ("and3", hip.GEN_U64_AND3)):
-            k = torch.empty(m, dtype=torch.int64, device=dev)
-            hip.generate(gen, k, m, SEED)
-            v = torch.empty(m, dtype=torch.int32, device=dev)
-            hip.generate(hip.GEN_U32_IOTA, v, m, 0)
-            ko, vo = torch.empty_like(k), torch.empty_like(v)
-            pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32,
-                             device=dev)
-            t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), 1)
-            extra[f"sort_pairs_u64_u32_2p27_{kind}"] = {
-                "ms": round(t, 4), "Gpairs_per_s": round(m / t / 1e6, 3),
-                "GBps_8pass_model": round(2 * 8 * m * 12 / t / 1e6, 1),
-                "frac": round(2 * 8 * m * 12 / t / 1e6 / HBM_PEAK_GBS, 4)}
-            del k, v, ko, vo, pt
-        # CsrMV fp32 (config 5): 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
-        import workloads
-        rows = cols = 1 << 20
-        va, ro, ci, xv, nnz = workloads.zipf_csr(rows, cols, SEED)
-        d = [torch.from_numpy(t).to(dev) for t in (va, ro, ci, xv)]
-        y = torch.empty(rows, dtype=torch.float32, device=dev)
-        spmv = lambda: hip.spmv_csr("f32", "i32", d[0], d[1], d[2], d[3], y, rows, cols, nnz)
-        t = time_steps(spmv, steps, warmup)
-        sk, _ = kernel_avg_ms(hip, spmv, "spmv_csr", 5)
-        spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * cols
-        extra["spmv_csr_f32_zipf1.5_2p20"] = {"nnz": nnz, "ms": round(t, 5), "kernel_ms": round(sk, 5),
-                                              "GBps": round(spmv_bytes / sk / 1e6, 1),
-                                              "frac": round(spmv_bytes / sk / 1e6 / HBM_PEAK_GBS, 4)}
-        del d, y
-        line["extra"] = extra
+        line["extra"] = run_extras(hip, dev, steps, warmup, list(EXTRAS))
 
     print(json.dumps(line))
     return 0
