@@ -8,18 +8,28 @@
 // 207-486), PARTIAL publish, per-digit look-back, LDS scatter, global scatter.
 //
 // MI355X design
-//   * Keys are loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every
-//     load instruction is a fully coalesced 256/512-byte access and each wave ranks its keys in index
-//     order, which keeps the sort stable.
-//   * Rank: per wave, 8 ballots give each lane the 64-bit mask of lanes holding the same digit; the
-//     rank inside the round is the popcount of that mask below the lane (mbcnt), and the highest lane
-//     of each digit group advances the wave's LDS digit counter.  No LDS atomics are needed, so the
-//     rank never depends on the hardware's ordering of conflicting atomics.
-//   * Per-digit counts go to a look-back row of 256 32-bit words per tile: bits 31:30 hold the status
-//     (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics because
-//     the 8 XCDs do not share an L2.  Tiles are claimed through an atomic ticket.
-//   * Keys are reordered by digit in LDS and written out from LDS in order, so consecutive lanes
-//     write consecutive addresses inside each digit's run.  Pairs move values the same way.
+//   * Histogram: one read of the keys counts every pass's digits in LDS copies private to each bank
+//     (see histogram_kernel); the bins are scanned once per sort.
+//   * Onesweep tiles: 512 threads x 32 keys (4-byte keys without values) or x 16 keys.  Keys are
+//     loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every load
+//     instruction is one coalesced access and each wave ranks its keys in index order (stability).
+//   * Rank: per wave and round, the 64-bit mask of lanes holding the same digit comes from an LDS
+//     table of lane masks (every lane ORs its bit into its digit's entry and reads it back) or, as an
+//     alternative, from 8 ballots; the rank is the wave's running count of the digit plus the
+//     popcount of the mask below the lane, and the highest lane of each digit group advances the
+//     count.  OR is order-independent, so ranks never depend on how conflicting lanes are serialised.
+//   * Tile order: workgroup b is tile tile_of_block(b): 16 consecutive tiles per XCD at a time, so
+//     the boundary cache lines of neighbouring tiles' digit runs merge in one L2.  There is no tile
+//     ticket (a same-address agent-scope atomic serialises at ~11 ns on MI355X).
+//   * Look-back: per-digit counts go to a row of 256 32-bit words per tile: bits 31:30 hold the
+//     status (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics
+//     because the 8 XCDs do not share an L2.  Both 256-thread halves of the workgroup walk back, 8
+//     predecessor tiles each per step; an entry unpublished after a bounded spin is counted by the
+//     waiting workgroup from that tile's keys and published by compare-and-swap, so progress never
+//     depends on dispatch order.
+//   * Keys are reordered by digit in LDS (before the look-back) and written out from LDS in order, so
+//     consecutive lanes write consecutive addresses inside each digit's run.  Pairs move values the
+//     same way after the keys.
 //   * Portions: one launch ranks at most 2^30 - tile keys so look-back counts fit in 30 bits.  The
 //     upfront histogram gives each pass's global digit offsets for portion 0.  Within a pass, the
 //     last tile of portion q holds the inclusive count of every digit in that portion and writes
@@ -42,7 +52,7 @@ constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
-constexpr int kLookbackWindow = 8;  // predecessor tiles inspected per look-back step (measured best of 4..32)
+constexpr int kLookbackWindow = 8;  // predecessor tiles per thread group and look-back step (measured best of 4..16)
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
