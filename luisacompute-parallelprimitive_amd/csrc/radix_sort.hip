@@ -10,7 +10,8 @@
 // MI355X design
 //   * Histogram: one read of the keys counts every pass's digits in LDS copies private to each bank
 //     (see histogram_kernel); the bins are scanned once per sort.
-//   * Onesweep tiles: 512 threads x 32 keys (4-byte keys without values) or x 16 keys.  Keys are
+//   * Onesweep tiles: 1024 threads x 16 keys (4-byte keys without values), 1024 x 8 (8-byte keys)
+//     or 512 x 16 (4-byte keys with values); two workgroups per CU (see geometry_for).  Keys are
 //     loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every load
 //     instruction is one coalesced access and each wave ranks its keys in index order (stability).
 //   * Rank: per wave and round, the 64-bit mask of lanes holding the same digit comes from an LDS
@@ -23,10 +24,10 @@
 //     ticket (a same-address agent-scope atomic serialises at ~11 ns on MI355X).
 //   * Look-back: per-digit counts go to a row of 256 32-bit words per tile: bits 31:30 hold the
 //     status (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics
-//     because the 8 XCDs do not share an L2.  Both 256-thread halves of the workgroup walk back, 8
-//     predecessor tiles each per step; an entry unpublished after a bounded spin is counted by the
-//     waiting workgroup from that tile's keys and published by compare-and-swap, so progress never
-//     depends on dispatch order.
+//     because the 8 XCDs do not share an L2.  Every 256-thread group of the workgroup walks back
+//     over its own window of 4 or 8 predecessor tiles per step; an entry unpublished after a
+//     bounded spin is counted by the waiting workgroup from that tile's keys and published by
+//     compare-and-swap, so progress never depends on dispatch order.
 //   * Keys are reordered by digit in LDS (before the look-back) and written out from LDS in order, so
 //     consecutive lanes write consecutive addresses inside each digit's run.  Pairs move values the
 //     same way after the keys.
@@ -52,7 +53,6 @@ constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
-constexpr int kLookbackWindow = 8;  // predecessor tiles per thread group and look-back step (measured best of 4..16)
 
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
@@ -262,9 +262,10 @@ __device__ void tile_digit_counts(const K* __restrict__ keys, uint32_t tile, uin
     }
     __syncthreads();
 }
-template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int RANK>
-// At most 128 VGPRs (4 waves per SIMD): two 512-thread workgroups per CU.
-__global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict__ keys_in,
+template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW, int RANK>
+// Register budget for two workgroups per CU: BLOCK / 128 waves per SIMD (128 VGPRs at 512 threads,
+// 64 at 1024).
+__global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* __restrict__ keys_in,
                                                                                K* __restrict__ keys_out,
                                                          const void* __restrict__ values_in,
                                                          void* __restrict__ values_out, uint32_t n,
@@ -282,16 +283,22 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
     static_assert(BLOCK >= static_cast<int>(kDigits) && BLOCK % static_cast<int>(kDigits) == 0,
                   "one thread per digit");
 
-    // The per-wave lane-mask tables of the LDS ranker live in the tile buffer: they are dead before
-    // the keys are reordered there (a barrier separates the two uses).
-    static_assert(W * kDigits * sizeof(uint64_t) <= TILE * ELEM, "match tables must fit the tile buffer");
+    // The tile buffer first holds, per wave, the lane-mask table of the LDS ranker (256 x 8 B) and the
+    // digit-count row (256 x 4 B; running counts during the rank, then the wave's offsets inside the
+    // tile).  Once every thread has read its offsets back (a barrier), the buffer holds the keys
+    // reordered by digit, and after the key scatter the values.
+    constexpr int LB_GROUPS = BLOCK / static_cast<int>(kDigits);
+    static_assert(W * kDigits * (sizeof(uint64_t) + sizeof(uint32_t)) <= TILE * ELEM,
+                  "rank tables and count rows must fit the tile buffer");
     __shared__ __attribute__((aligned(16))) unsigned char s_tile[TILE * ELEM];
-    __shared__ uint32_t s_counts[W][kDigits];
+    __shared__ uint32_t s_lb[LB_GROUPS][kDigits];  // look-back: group sums (rows 0..G-2), done flag (row G-1)
     __shared__ uint32_t s_global_minus_local[kDigits];
     __shared__ uint32_t s_scan[kDigits / kWave];
     __shared__ uint32_t s_fallback[kDigits];
     __shared__ uint32_t s_fallback_tile;
     uint64_t (*s_match)[kDigits] = reinterpret_cast<uint64_t (*)[kDigits]>(s_tile);
+    uint32_t (*s_counts)[kDigits] =
+        reinterpret_cast<uint32_t (*)[kDigits]>(s_tile + W * kDigits * sizeof(uint64_t));
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
@@ -401,18 +408,17 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
     __syncthreads();
 
     // Reorder keys by digit in LDS now: local positions do not depend on the look-back, and the key
-    // registers are free while the look-back runs.  (The match tables that shared this buffer are
-    // dead: the barrier after the rank loop separates the uses.)
+    // registers are free while the look-back runs.  The offsets are read first: their rows share
+    // the buffer the keys go to.
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) rank[k] += s_counts[wave][digit_of<U, KIND>(keys[k], shift, mask)];
+    __syncthreads();
     U* s_keys = reinterpret_cast<U*>(s_tile);
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) {
-        const uint32_t dk = digit_of<U, KIND>(keys[k], shift, mask);
-        rank[k] += s_counts[wave][dk];
-        s_keys[rank[k]] = keys[k];
-    }
+    for (int k = 0; k < ITEMS; ++k) s_keys[rank[k]] = keys[k];
 
-    // Look-back.  Each step inspects LB_GROUPS * kLookbackWindow predecessor tiles: thread
-    // d + 256 g (group g) loads, for digit d, the kLookbackWindow entries just older than those of
+    // Look-back.  Each step inspects LB_GROUPS * WINDOW predecessor tiles: thread
+    // d + 256 g (group g) loads, for digit d, the WINDOW entries just older than those of
     // group g - 1, all loads of a step issued together (one memory latency per step).  Each group sums
     // back to the nearest INCLUSIVE entry of its window; group 0 chains the group sums, newest window
     // first, until some window holds an INCLUSIVE entry (or tile 0).  Fewer, wider steps matter
@@ -422,9 +428,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
     // older tiles publish without waiting on this one).  An entry that stays unpublished for
     // `spin_limit` polls is counted here from its tile's keys (a predecessor tile is always full: only
     // the last tile is partial) and published as PARTIAL by compare-and-swap.
-    // The group sums travel through s_counts, which is dead after the reorder above.
-    constexpr int LB_GROUPS = BLOCK / static_cast<int>(kDigits);
-    static_assert(LB_GROUPS <= W, "group sums and flags live in rows of s_counts");
+    // The group sums and the done flag travel through s_lb.
     uint32_t excl = 0;
     if (tile > 0) {
         const uint32_t grp = tid / kDigits;
@@ -433,10 +437,10 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
         int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
         uint32_t* const column = lookback + ld;
         while (true) {
-            const int64_t gtop = top - static_cast<int64_t>(grp) * kLookbackWindow;  // this group's newest
-            uint32_t v[kLookbackWindow];
+            const int64_t gtop = top - static_cast<int64_t>(grp) * WINDOW;  // this group's newest
+            uint32_t v[WINDOW];
 #pragma unroll
-            for (int w = 0; w < kLookbackWindow; ++w) {
+            for (int w = 0; w < WINDOW; ++w) {
                 const int64_t j = gtop - w;
                 v[w] = (!done && j >= 0) ? atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]) : 0u;
             }
@@ -447,7 +451,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                 int first_invalid = -1;
                 bool scanning = !done;
 #pragma unroll
-                for (int w = 0; w < kLookbackWindow; ++w) {
+                for (int w = 0; w < WINDOW; ++w) {
                     const bool live = scanning && gtop - w >= 0;
                     if (live && (v[w] & ~kCountMask) == 0) first_invalid = w;
                     scanning = live && (v[w] & ~kCountMask) != 0 && (v[w] & kFlagInclusive) == 0;
@@ -464,7 +468,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                     const int wf = static_cast<int>(gtop - static_cast<int64_t>(jf));
                     if (!done) {
 #pragma unroll
-                        for (int w = 0; w < kLookbackWindow; ++w) {
+                        for (int w = 0; w < WINDOW; ++w) {
                             if (w == wf && (v[w] & ~kCountMask) == 0) {
                                 uint32_t expected = 0;
                                 const uint32_t desired = kFlagPartial | s_fallback[ld];
@@ -482,7 +486,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                 ++spins;
                 if (!done) {
 #pragma unroll
-                    for (int w = 0; w < kLookbackWindow; ++w) {
+                    for (int w = 0; w < WINDOW; ++w) {
                         const int64_t j = gtop - w;
                         if (j >= 0 && (v[w] & ~kCountMask) == 0)
                             v[w] = atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]);
@@ -494,7 +498,7 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
             bool window_stops = false;
             if (!done) {
 #pragma unroll
-                for (int w = 0; w < kLookbackWindow; ++w) {
+                for (int w = 0; w < WINDOW; ++w) {
                     if (!window_stops && gtop - w >= 0) {
                         window_sum += v[w] & kCountMask;
                         // Tile 0's counts start at the portion base, so the walk always ends there.
@@ -503,13 +507,13 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
                 }
             }
             if constexpr (LB_GROUPS > 1) {
-                if (grp > 0) s_counts[grp - 1][ld] = window_sum | (window_stops ? 0x80000000u : 0u);
+                if (grp > 0) s_lb[grp - 1][ld] = window_sum | (window_stops ? 0x80000000u : 0u);
                 __syncthreads();
                 if (grp == 0 && !done) {
 #pragma unroll
                     for (int g = 1; g < LB_GROUPS; ++g) {
                         if (window_stops) break;
-                        const uint32_t x = s_counts[g - 1][ld];
+                        const uint32_t x = s_lb[g - 1][ld];
                         window_sum += x & 0x7FFFFFFFu;
                         window_stops = (x >> 31) != 0;
                     }
@@ -520,14 +524,14 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
             if (grp == 0 && !done) {
                 excl += window_sum;
                 done = window_stops;
-                if constexpr (LB_GROUPS > 1) s_counts[W - 1][ld] = done ? 1u : 0u;
+                if constexpr (LB_GROUPS > 1) s_lb[LB_GROUPS - 1][ld] = done ? 1u : 0u;
             }
             const bool more = __syncthreads_or(grp == 0 && !done);
             if constexpr (LB_GROUPS > 1) {
-                if (grp > 0) done = s_counts[W - 1][ld] != 0;
+                if (grp > 0) done = s_lb[LB_GROUPS - 1][ld] != 0;
             }
             if (!more) break;
-            top -= static_cast<int64_t>(LB_GROUPS) * kLookbackWindow;
+            top -= static_cast<int64_t>(LB_GROUPS) * WINDOW;
         }
         if (tid < kDigits) atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
     }
@@ -574,14 +578,23 @@ __global__ __launch_bounds__(BLOCK, 4) void onesweep_kernel(const K* __restrict_
 struct Geometry {
     int block;
     int items;
+    int window;  // predecessor tiles per 256-thread group and look-back step
     uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
-// 16K-key tiles for 4-byte keys without values, 8K otherwise: the reordering buffer then takes at
-// most 64 KB of LDS, two workgroups fit a CU within 128 VGPRs, and a tile carries enough work that
-// the look-back (one cross-XCD round trip per window) stays short relative to the rest of the tile.
+// The reordering buffer takes at most 64 KB of LDS, so two workgroups share a CU.  16K-key tiles
+// for 4-byte keys without values, 8K otherwise: a tile carries enough work that the look-back (one
+// cross-XCD round trip per step) stays short relative to the rest of the tile.  1024-thread
+// workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice the items per thread: every
+// wave's rank is a chain of dependent LDS round trips, and shorter chains on more waves hide them
+// better (SortKeys 2^28 u32 3.04 -> 2.81 ms, SortPairs 2^27 u64 + u32 6.08 -> 5.97 ms on MI355X).
+// 4-byte keys with values keep 512 threads: their keys, values, ranks and output positions do not
+// fit 64 VGPRs.  The window is the widest that compiles without register spills (4 tiles with
+// values at 1024 threads, 8 otherwise; a spilling window runs several times slower).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    return (key_bytes <= 4 && value_bytes == 0) ? Geometry{512, 32} : Geometry{512, 16};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 16, 8};
+    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 4 : 8};
+    return Geometry{512, 16, 8};
 }
 
 template <typename K, int VB>
@@ -718,10 +731,10 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
             if (g_rank_mode == kRankBallot)
-                onesweep_kernel<K, DESC, VB, G.block, G.items, kRankBallot><<<tiles, G.block, 0, stream>>>(
+                onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankBallot><<<tiles, G.block, 0, stream>>>(
                     src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
             else
-                onesweep_kernel<K, DESC, VB, G.block, G.items, kRankLdsMatch><<<tiles, G.block, 0, stream>>>(
+                onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankLdsMatch><<<tiles, G.block, 0, stream>>>(
                     src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
