@@ -292,10 +292,12 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
                   "rank tables and count rows must fit the tile buffer");
     __shared__ __attribute__((aligned(16))) unsigned char s_tile[TILE * ELEM];
     __shared__ uint32_t s_lb[LB_GROUPS][kDigits];  // look-back: group sums (rows 0..G-2), done flag (row G-1)
+    // Digit counts of a predecessor tile during the look-back fallback, then (after the look-back's
+    // last barrier) each digit's global-minus-local output offset.
     __shared__ uint32_t s_global_minus_local[kDigits];
     __shared__ uint32_t s_scan[kDigits / kWave];
-    __shared__ uint32_t s_fallback[kDigits];
     __shared__ uint32_t s_fallback_tile;
+    uint32_t* const s_fallback = s_global_minus_local;
     uint64_t (*s_match)[kDigits] = reinterpret_cast<uint64_t (*)[kDigits]>(s_tile);
     uint32_t (*s_counts)[kDigits] =
         reinterpret_cast<uint32_t (*)[kDigits]>(s_tile + W * kDigits * sizeof(uint64_t));

@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kSpmvBlock = 256;
 constexpr uint32_t kShortRow = 8;
+constexpr int kLongUnroll = 4;  // wave-strided elements of a long row loaded together per lane
 
 template <typename V> struct AccumType { using type = V; };
 template <> struct AccumType<int32_t> { using type = uint32_t; };
@@ -48,12 +49,27 @@ __global__ __launch_bounds__(kSpmvBlock) void spmv_csr_kernel(const V* __restric
     const bool valid = in_range && begin <= end && end <= nnz;
     const uint32_t len = valid ? end - begin : 0;
 
+    // Every load of a row (or of an unrolled group of a long row's elements) is issued before any
+    // of them is used, so a lane waits for two memory round trips per group rather than two per
+    // nonzero; products are still added in element order.
     A acc = A(0);
     const bool is_short = len <= kShortRow;
     if (is_short) {
-        for (uint32_t e = begin; e < begin + len; ++e) {
-            const uint32_t c = static_cast<uint32_t>(column_indices[e]);
-            if (c < cols) acc += static_cast<A>(values[e]) * static_cast<A>(x[c]);
+        uint32_t c[kShortRow];
+        A v[kShortRow];
+#pragma unroll
+        for (uint32_t k = 0; k < kShortRow; ++k) {
+            if (k < len) {
+                c[k] = static_cast<uint32_t>(column_indices[begin + k]);
+                v[k] = static_cast<A>(values[begin + k]);
+            }
+        }
+        A xv[kShortRow];
+#pragma unroll
+        for (uint32_t k = 0; k < kShortRow; ++k) xv[k] = (k < len && c[k] < cols) ? static_cast<A>(x[c[k]]) : A(0);
+#pragma unroll
+        for (uint32_t k = 0; k < kShortRow; ++k) {
+            if (k < len && c[k] < cols) acc += v[k] * xv[k];
         }
     }
 
@@ -64,7 +80,24 @@ __global__ __launch_bounds__(kSpmvBlock) void spmv_csr_kernel(const V* __restric
         const uint32_t rb = __builtin_amdgcn_readlane(begin, src);
         const uint32_t re = __builtin_amdgcn_readlane(end, src);
         A part = A(0);
-        for (uint32_t e = rb + lane; e < re; e += kWave) {
+        uint32_t e = rb + lane;
+        for (; e + (kLongUnroll - 1) * kWave < re; e += kLongUnroll * kWave) {
+            uint32_t c[kLongUnroll];
+            A v[kLongUnroll];
+#pragma unroll
+            for (int j = 0; j < kLongUnroll; ++j) {
+                c[j] = static_cast<uint32_t>(column_indices[e + j * kWave]);
+                v[j] = static_cast<A>(values[e + j * kWave]);
+            }
+            A xv[kLongUnroll];
+#pragma unroll
+            for (int j = 0; j < kLongUnroll; ++j) xv[j] = c[j] < cols ? static_cast<A>(x[c[j]]) : A(0);
+#pragma unroll
+            for (int j = 0; j < kLongUnroll; ++j) {
+                if (c[j] < cols) part += v[j] * xv[j];
+            }
+        }
+        for (; e < re; e += kWave) {
             const uint32_t c = static_cast<uint32_t>(column_indices[e]);
             if (c < cols) part += static_cast<A>(values[e]) * static_cast<A>(x[c]);
         }
@@ -80,7 +113,9 @@ int spmv_csr(void* /*temp*/, size_t /*temp_bytes*/, const V* values, const I* ro
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (rows > 0xFFFFFFFFull / 32) return set_error(kInvalidArgument, "DeviceSpmv: too many rows");
     if (cols > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceSpmv: too many columns");
-    if (nnz > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceSpmv: too many nonzero values");
+    // 32-bit element indices advance by up to kLongUnroll * kWave past a row's end without wrapping.
+    if (nnz > 0xFFFFFFFFull - kLongUnroll * kWave)
+        return set_error(kInvalidArgument, "DeviceSpmv: too many nonzero values");
     if (rows == 0) return kOk;
     if (!y) return set_error(kInvalidArgument, "DeviceSpmv: null output vector");
     if (nnz == 0) return launch_fill_u32(reinterpret_cast<uint32_t*>(y), rows * sizeof(V) / 4, 0u, stream);
