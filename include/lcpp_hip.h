@@ -157,7 +157,7 @@ uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes);
  * replaces DeviceSpmv<>::CsrMV (src/lcpp/device/device_spmv.h:48-130) and
  * GetTempStorageBytes == 0 (device_spmv.h:43-46).  rows == 0: no-op; nnz == 0: y[0..rows) = 0;
  * a row whose offsets are decreasing or exceed nnz yields 0; columns >= cols are skipped.
- * Limits (status -1 beyond them): rows < 2^27, cols < 2^32, nnz <= 2^32 - 257.
+ * Limits (status -1 beyond them): rows < 2^27, cols < 2^32, nnz <= 2^32 - 513.
  * ------------------------------------------------------------------------------------------- */
 size_t lcpp_hip_spmv_temp_bytes(uint64_t rows, uint64_t cols, uint64_t nnz);
 

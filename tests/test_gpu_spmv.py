@@ -127,3 +127,36 @@ def test_integer_stream_segments_bit_exact(hip, orc, dev):
     log(f"spmv integer stream nnz={nnz}")
     y = gpu_spmv(hip, "u32", "u32", va, ro, ci, x, rows, cols, nnz)
     assert np.array_equal(to_host(y, np.uint32, rows), orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz))
+
+
+@pytest.mark.parametrize("offset_values,offset_columns", [(False, False), (True, True), (True, False), (False, True)])
+def test_grouped_long_rows_bit_exact(hip, orc, dev, offset_values, offset_columns):
+    """Rows longer than 64 nonzeros stream their columns and values in 16-byte groups when both arrays
+    are 16-byte aligned.  Integer sums are exact in any order, so this pins that path: rows whose
+    groups start before and end after the row, a last row whose final group crosses nnz (nnz not a
+    multiple of the group), and streams passed as views offset by one element (4 bytes), which must
+    take the element-wise path."""
+    rng = np.random.default_rng(91)
+    rows, cols = 3000, 7000
+    lengths = np.where(rng.integers(0, 4, rows) == 0, rng.integers(65, 700, rows), rng.integers(0, 70, rows))
+    lengths[-1] = 517              # the last row is long and nnz % 8 != 0 below
+    ro = np.zeros(rows + 1, np.int64)
+    ro[1:] = np.cumsum(lengths)
+    nnz = int(ro[-1])
+    if nnz % 8 == 0:
+        lengths[-1] += 3
+        ro[-1] += 3
+        nnz += 3
+    assert nnz % 8 != 0
+    ci = np.concatenate([np.sort(rng.choice(cols, size=int(L), replace=False)) if L else np.zeros(0, np.int64)
+                         for L in lengths]).astype(np.uint32)
+    ci[::131] = cols + 9           # out-of-range columns are skipped
+    ro = ro.astype(np.uint32)
+    va = orc.generate(1, nnz, 41)
+    x = orc.generate(1, cols, 42)
+    log(f"spmv grouped rows nnz={nnz} offsets={offset_values},{offset_columns}")
+    d_va = to_dev(np.concatenate([np.array([7], np.uint32), va]))[1:] if offset_values else to_dev(va)
+    d_ci = to_dev(np.concatenate([np.array([3], np.uint32), ci]))[1:] if offset_columns else to_dev(ci)
+    y = fill_dev(rows, 4, 0x12345678)
+    hip.spmv_csr("u32", "u32", d_va, to_dev(ro), d_ci, to_dev(x), y, rows, cols, nnz)
+    assert np.array_equal(to_host(y, np.uint32, rows), orc.spmv_csr_u32(va, ro, ci, x, rows, cols, nnz))
