@@ -176,6 +176,49 @@ LCPP_HIP_DECLARE_SPMV(u32, uint32_t, u32, uint32_t)
 #undef LCPP_HIP_DECLARE_SPMV
 
 /* ---------------------------------------------------------------------------------------------
+ * Scan-by-key and reduce-by-key with the sum operator (decoupled look-back, single pass)
+ * replaces DeviceScan<>::ExclusiveSumByKey / InclusiveSumByKey and ExclusiveScanByKey /
+ * InclusiveScanByKey with a sum operator and an initial value (src/lcpp/device/device_scan.h:
+ * 424-597), DeviceScan<>::GetScanByKeyTempStorageBytes<K, V> (:310-315, layout :129-142),
+ * DeviceReduce<>::ReduceByKey with a sum operator (src/lcpp/device/device_reduce.h:437-487) and
+ * DeviceReduce<>::GetReduceByKeyTempStorageBytes<K, V> (:207-223).
+ * A run is a maximal range of consecutive items whose keys are equal; keys compare by bits under
+ * `key_mask` (equal when ((a ^ b) & key_mask) == 0): all-ones is the reference's default
+ * equality_op (lhs == rhs) for integer keys, other masks express bit-class equalities such as the
+ * parity test of tests/device_scan_test.cpp:419-447.
+ * Scan: exclusive (inclusive == 0): out[i] = init + (sum of the run's items before i), out[head] =
+ * init (ExclusiveSumByKey passes init = 0); inclusive without init (use_init == 0): out[i] = sum of
+ * the run's items up to i; with init: init + that sum (the reference's "prepend an initial value to
+ * every segment" overloads, device_scan.h:488-519).  values_out may equal values_in.
+ * Reduce: unique_out[r] = first key of run r, aggregates_out[r] = sum of run r, *num_runs_out = runs;
+ * n == 0 writes 0 runs (device_reduce.h:449-458).  Integer sums wrap; n <= 2^32 - 1.
+ * Key suffixes: i32, u32, i64, u64; value suffixes i32, u32, f32, i64, u64, f64.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);
+size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);
+
+#define LCPP_HIP_DECLARE_BY_KEY(KS, KT, VS, VT)                                                                      \
+    int lcpp_hip_scan_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in,     \
+                                             VT* values_out, uint64_t n, int inclusive, int use_init, VT init,       \
+                                             uint64_t key_mask, void* stream);                                       \
+    int lcpp_hip_reduce_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in, const VT* values_in, \
+                                               KT* unique_out, VT* aggregates_out, uint32_t* num_runs_out, uint64_t n, \
+                                               uint64_t key_mask, void* stream);
+#define LCPP_HIP_DECLARE_BY_KEY_VALUES(KS, KT)          \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, i32, int32_t)       \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, u32, uint32_t)      \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, f32, float)         \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, i64, int64_t)       \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, u64, uint64_t)      \
+    LCPP_HIP_DECLARE_BY_KEY(KS, KT, f64, double)
+LCPP_HIP_DECLARE_BY_KEY_VALUES(i32, int32_t)
+LCPP_HIP_DECLARE_BY_KEY_VALUES(u32, uint32_t)
+LCPP_HIP_DECLARE_BY_KEY_VALUES(i64, int64_t)
+LCPP_HIP_DECLARE_BY_KEY_VALUES(u64, uint64_t)
+#undef LCPP_HIP_DECLARE_BY_KEY_VALUES
+#undef LCPP_HIP_DECLARE_BY_KEY
+
+/* ---------------------------------------------------------------------------------------------
  * Seeded synthetic workloads for tests and benchmarks (no reference counterpart; the reference
  * generates on the host, e.g. tests/lcpp_cub_bench.cpp:516-521,666-672,814).
  * Stream: splitmix64, r_i = mix(seed + (start + i + 1) * 0x9E3779B97F4A7C15).
@@ -200,6 +243,7 @@ size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t
 uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
                                           uint32_t end_bit, int double_buffer, size_t temp_bytes);
 int lcpp_hip_internal_radix_rank_mode(int mode);
+size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

@@ -1,0 +1,514 @@
+// DeviceScan::ExclusiveScanByKey / InclusiveScanByKey (sum operator) and DeviceReduce::ReduceByKey
+// (sum operator) for gfx950: single-pass decoupled look-back over run-segmented sums.
+//
+// Reference path: DeviceScan<>::ExclusiveSumByKey / InclusiveSumByKey / Exclusive- and
+// InclusiveScanByKey (src/lcpp/device/device_scan.h:424-597) -> dispatch_scan_by_key (:993-1012) ->
+// ScanByKeyModule (device/details/scan_by_key.h); DeviceReduce<>::ReduceByKey (device_reduce.h:
+// 437-487) -> reduce_by_key_array (:1024-1153) -> ReduceByKeyModule (device/details/reduce_by_key.h).
+// Both pair a run-head flag with each value (KeyValuePair<int, V>, common/util_type.h:17-21) and scan
+// with the segmented operator over decoupled look-back tile states
+// (device/details/single_pass_scan_operator.h).
+//
+// Semantics: item i starts a run when i == 0 or its key differs from key i-1; keys compare by bits
+// under a caller mask ((a ^ b) & mask == 0 means equal; all-ones is plain equality, 1 is the
+// reference test's parity equality).  Scan: exclusive out[i] = init + (sum of the run's items before
+// i), out[head] = init; inclusive out[i] = (sum of the run's items up to i), plus init when one is
+// given.  Reduce: unique_out[r] = first key of run r, aggregates_out[r] = sum of run r,
+// num_runs_out[0] = runs (0 for n == 0).  Integer sums wrap.
+//
+// MI355X design
+//   * Tile = 256 threads x 16 consecutive items per thread (4096 items), read and written as
+//     16-byte vectors when the arrays are 16-byte aligned.  The previous item of a thread's first
+//     item is read from global memory (it sits in the neighbour's cache line).
+//   * State of a span of items: (heads, sum since the last head).  States combine as
+//     (c1, s1) + (c2, s2) = (c1 + c2, c2 ? s2 : s1 + s2), which is associative.  Each thread folds its
+//     items serially; a DPP wave scan (the shared row_shr / row_bcast pattern) and one pass over the
+//     4 wave totals in LDS give each thread its carry-in and the tile its aggregate.
+//   * Tile states are 64-bit words with the status in the low half and 32 payload bits in the high
+//     half: word 0 holds the head count, words 1.. the sum.  A reader accepts a state only when every
+//     word shows the same published status, so each word is one relaxed agent-scope atomic (the 8
+//     XCDs do not share an L2) and no fence is needed.  Only the workgroup that wins word 0 by
+//     compare-and-swap writes a PARTIAL state.
+//   * Look-back: wave 0 reads 64 predecessors per step (one per lane).  Ballots find the newest
+//     INCLUSIVE state (or tile 0) and, for the scan, the newest state with a head: the scan stops
+//     there because older sums cannot reach this tile; ReduceByKey continues to an INCLUSIVE state
+//     since run indices need the full head count.  Counts and sums reduce with DPP.
+//   * Forward progress never depends on dispatch order: a predecessor still unpublished after
+//     `spin_limit` polls is claimed (word 0: INVALID -> CLAIMED), its state is computed by the whole
+//     waiting workgroup with the owner's own code (the same float summation order), and published
+//     PARTIAL.  An owner that finds its tile claimed waits for that PARTIAL before it stores anything,
+//     so an in-place scan (values_out == values_in) never overwrites input a helper still reads.
+// Algorithmic traffic: scan n*(sizeof(K) + 2*sizeof(V)); reduce n*(sizeof(K) + sizeof(V)) plus
+// runs*(sizeof(K) + sizeof(V)) written.
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+namespace lcpp_hip {
+namespace {
+
+constexpr int kBkBlock = 256;
+constexpr int kBkItems = 16;
+constexpr int kBkWaves = kBkBlock / kWave;
+constexpr uint32_t kBkTile = static_cast<uint32_t>(kBkBlock) * kBkItems;  // 4096 items
+
+constexpr uint32_t kStInvalid = 0;
+constexpr uint32_t kStPartial = 1;
+constexpr uint32_t kStInclusive = 2;
+constexpr uint32_t kStClaimed = 3;
+
+constexpr int kModeScan = 0;
+constexpr int kModeReduce = 1;
+
+// Look-back decisions broadcast from wave 0.
+constexpr uint32_t kActDone = 0;
+constexpr uint32_t kActAdvance = 1;
+constexpr uint32_t kActWait = 2;
+constexpr uint32_t kActHelp = 3;
+
+template <typename V>
+struct Seg {
+    uint32_t count;  // run heads in the span
+    V sum;           // sum of the items after the span's last head (all items if it has none)
+};
+
+template <typename V>
+__device__ __forceinline__ Seg<V> seg_combine(Seg<V> older, Seg<V> newer) {
+    Seg<V> r;
+    r.count = older.count + newer.count;
+    r.sum = newer.count != 0 ? newer.sum : static_cast<V>(older.sum + newer.sum);
+    return r;
+}
+
+template <typename V>
+constexpr int kValueWords = static_cast<int>(sizeof(V) / 4);
+template <typename V>
+constexpr int kStateWords = 1 + kValueWords<V>;
+
+size_t state_bytes(uint64_t n, size_t value_bytes) {
+    return ceil_div(n, kBkTile) * (1 + value_bytes / 4) * sizeof(uint64_t);
+}
+
+__device__ __forceinline__ uint64_t state_word(uint32_t status, uint32_t payload) {
+    return (static_cast<uint64_t>(payload) << 32) | status;
+}
+
+template <typename V>
+__device__ __forceinline__ uint32_t value_part(V v, int w) {
+    if constexpr (sizeof(V) == 4) {
+        return __builtin_bit_cast(uint32_t, v);
+    } else {
+        return static_cast<uint32_t>(__builtin_bit_cast(uint64_t, v) >> (32 * w));
+    }
+}
+
+// Stores the sum words of a state.  Only the holder of the tile's word 0 calls it.
+template <typename V>
+__device__ __forceinline__ void store_sum_words(uint64_t* slot, uint32_t status, V sum) {
+#pragma unroll
+    for (int w = 0; w < kValueWords<V>; ++w) atomic_store_agent(&slot[1 + w], state_word(status, value_part(sum, w)));
+}
+
+// Reads a tile state; returns its status if every word carries the same published status
+// (PARTIAL or INCLUSIVE), kStInvalid otherwise.
+template <typename V>
+__device__ __forceinline__ uint32_t read_state(const uint64_t* slot, Seg<V>& s) {
+    uint64_t w[kStateWords<V>];
+#pragma unroll
+    for (int i = 0; i < kStateWords<V>; ++i) w[i] = atomic_load_agent(&slot[i]);
+    const uint32_t st = static_cast<uint32_t>(w[0]);
+    bool ok = st == kStPartial || st == kStInclusive;
+#pragma unroll
+    for (int i = 1; i < kStateWords<V>; ++i) ok = ok && static_cast<uint32_t>(w[i]) == st;
+    s.count = static_cast<uint32_t>(w[0] >> 32);
+    if constexpr (sizeof(V) == 4) {
+        s.sum = __builtin_bit_cast(V, static_cast<uint32_t>(w[1] >> 32));
+    } else {
+        s.sum = __builtin_bit_cast(V, (w[2] & 0xFFFFFFFF00000000ull) | (w[1] >> 32));
+    }
+    return ok ? st : kStInvalid;
+}
+
+template <typename T>
+struct alignas(16) Run16 {
+    T v[kBkItems];
+};
+
+// The 16 items [first, first + 16) of `p` (0 past n): one 64/128-byte vector load when aligned.
+template <typename T>
+__device__ __forceinline__ void load_items(const T* p, uint64_t first, uint64_t n, bool vec, T (&out)[kBkItems]) {
+    if (vec && first + kBkItems <= n) {
+        const Run16<T> r = *reinterpret_cast<const Run16<T>*>(p + first);
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) out[k] = r.v[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) out[k] = first + k < n ? p[first + k] : T(0);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_items(T* p, uint64_t first, uint64_t n, bool vec, const T (&in)[kBkItems]) {
+    if (vec && first + kBkItems <= n) {
+        Run16<T> r;
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) r.v[k] = in[k];
+        *reinterpret_cast<Run16<T>*>(p + first) = r;
+    } else {
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) {
+            if (first + k < n) p[first + k] = in[k];
+        }
+    }
+}
+
+template <typename K, typename V>
+struct ThreadItems {
+    K key[kBkItems];
+    V val[kBkItems];
+    uint32_t heads;  // bit k: item k starts a run
+};
+
+template <typename K, typename V>
+__device__ __forceinline__ void load_thread(const K* keys, const V* values, uint64_t n, uint64_t first, K mask,
+                                            bool vec_k, bool vec_v, ThreadItems<K, V>& t) {
+    load_items(keys, first, n, vec_k, t.key);
+    load_items(values, first, n, vec_v, t.val);
+    K prev = (first > 0 && first - 1 < n) ? keys[first - 1] : K(0);
+    uint32_t heads = 0;
+#pragma unroll
+    for (int k = 0; k < kBkItems; ++k) {
+        const uint64_t i = first + k;
+        const bool head = i < n && (i == 0 || ((t.key[k] ^ prev) & mask) != 0);
+        heads |= (head ? 1u : 0u) << k;
+        prev = t.key[k];
+    }
+    t.heads = heads;
+}
+
+template <typename K, typename V>
+__device__ __forceinline__ Seg<V> fold_thread(const ThreadItems<K, V>& t, uint64_t first, uint64_t n) {
+    Seg<V> s{0u, V(0)};
+#pragma unroll
+    for (int k = 0; k < kBkItems; ++k) {
+        if (first + k < n) {
+            if ((t.heads >> k) & 1u) {
+                s.count += 1;
+                s.sum = t.val[k];
+            } else {
+                s.sum = static_cast<V>(s.sum + t.val[k]);
+            }
+        }
+    }
+    return s;
+}
+
+// One step of the wave scan: combine with the state DPP brings from an older lane (identity where
+// the pattern has no source).
+template <int CTRL, int ROW_MASK = 0xf, typename V>
+__device__ __forceinline__ Seg<V> seg_dpp_step(Seg<V> x) {
+    Seg<V> o;
+    o.count = dpp_move_u32<CTRL, ROW_MASK>(0u, x.count);
+    o.sum = dpp_move<CTRL, ROW_MASK>(V(0), x.sum);
+    return seg_combine(o, x);
+}
+
+// Exclusive prefix of each thread's state within the tile, and the tile aggregate.  Called by every
+// thread; leaves `s_wave` free for reuse (barriers on both sides of its use).
+template <typename V>
+__device__ __forceinline__ void block_seg_scan(Seg<V> x, Seg<V>* s_wave, Seg<V>& exclusive, Seg<V>& aggregate) {
+    Seg<V> inc = x;
+    inc = seg_dpp_step<dpp::kRowShr1>(inc);
+    inc = seg_dpp_step<dpp::kRowShr2>(inc);
+    inc = seg_dpp_step<dpp::kRowShr4>(inc);
+    inc = seg_dpp_step<dpp::kRowShr8>(inc);
+    inc = seg_dpp_step<dpp::kRowBcast15, 0xa>(inc);
+    inc = seg_dpp_step<dpp::kRowBcast31, 0xc>(inc);
+    Seg<V> ex;
+    ex.count = dpp_move_u32<dpp::kWaveShr1>(0u, inc.count);
+    ex.sum = dpp_move<dpp::kWaveShr1>(V(0), inc.sum);
+    const uint32_t wave = threadIdx.x / kWave;
+    __syncthreads();  // earlier readers of s_wave are done
+    if (lane_id() == kWave - 1) s_wave[wave] = inc;
+    __syncthreads();
+    Seg<V> prefix{0u, V(0)};
+    Seg<V> total{0u, V(0)};
+#pragma unroll
+    for (int w = 0; w < kBkWaves; ++w) {
+        if (static_cast<uint32_t>(w) == wave) prefix = total;
+        total = seg_combine(total, s_wave[w]);
+    }
+    exclusive = seg_combine(prefix, ex);
+    aggregate = total;
+}
+
+// Aggregate of tile `tile`, computed by the whole workgroup exactly as the tile's owner computes it.
+template <typename K, typename V>
+__device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
+                                 bool vec_v, Seg<V>* s_wave) {
+    const uint64_t first = static_cast<uint64_t>(tile) * kBkTile + static_cast<uint64_t>(threadIdx.x) * kBkItems;
+    ThreadItems<K, V> t;
+    load_thread(keys, values, n, first, mask, vec_k, vec_v, t);
+    Seg<V> ex, agg;
+    block_seg_scan(fold_thread(t, first, n), s_wave, ex, agg);
+    return agg;
+}
+
+template <typename K, typename V, int MODE>
+__global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ keys, const V* values_in,
+                                                          V* values_out, K* __restrict__ unique_out,
+                                                          V* __restrict__ aggregates_out,
+                                                          uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
+                                                          uint64_t* __restrict__ states, int inclusive, int use_init,
+                                                          V init, bool vec_k, bool vec_v, bool vec_o,
+                                                          uint32_t spin_limit) {
+    constexpr int W = kStateWords<V>;
+    __shared__ Seg<V> s_wave[kBkWaves];
+    __shared__ uint32_t s_ctl[2][2];  // look-back decision and helped tile, two alternating rows
+    __shared__ uint32_t s_flag;
+    __shared__ Seg<V> s_prefix;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint32_t tile = blockIdx.x;
+    const uint64_t first = static_cast<uint64_t>(tile) * kBkTile + static_cast<uint64_t>(tid) * kBkItems;
+
+    ThreadItems<K, V> t;
+    load_thread(keys, values_in, n, first, mask, vec_k, vec_v, t);
+    Seg<V> in_tile, agg;
+    block_seg_scan(fold_thread(t, first, n), s_wave, in_tile, agg);
+
+    // Publish: win word 0 (INVALID -> PARTIAL, or INCLUSIVE for tile 0), then the sum words.  A
+    // tile already claimed by a helper gets its PARTIAL from that helper.
+    uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
+    if (tid == 0) {
+        uint64_t expected = 0;
+        const uint32_t st = tile == 0 ? kStInclusive : kStPartial;
+        const bool won = __hip_atomic_compare_exchange_strong(&my_slot[0], &expected, state_word(st, agg.count),
+                                                              __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+        if (won) store_sum_words(my_slot, st, agg.sum);
+        s_flag = won ? 0u : 1u;
+    }
+
+    Seg<V> prefix{0u, V(0)};
+    if (tile > 0) {
+        int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
+        Seg<V> acc{0u, V(0)};                           // states consumed so far (wave 0)
+        uint32_t spins = 0;
+        uint32_t row = 0;
+        while (true) {
+            if (wave == 0) {
+                const int64_t j = top - static_cast<int64_t>(lane);
+                Seg<V> s{0u, V(0)};
+                const uint32_t st = j >= 0 ? read_state<V>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
+                const bool exists = j >= 0;
+                const bool published = st != kStInvalid;
+                // A complete prefix: an INCLUSIVE state, or tile 0 (nothing precedes it).
+                const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
+                uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
+                const uint64_t head_mask = wave_ballot(published && s.count != 0);
+                if constexpr (MODE == kModeScan) {
+                    if (head_mask) cut = min(cut, static_cast<uint32_t>(__builtin_ctzll(head_mask)));
+                }
+                const uint64_t upto = cut >= kWave - 1 ? ~0ull : ((2ull << cut) - 1);
+                const uint64_t missing = upto & wave_ballot(exists) & ~wave_ballot(published);
+                uint32_t action;
+                uint32_t help_tile = 0;
+                if (missing) {
+                    if (spins >= spin_limit) {
+                        action = kActHelp;
+                        help_tile = static_cast<uint32_t>(top - __builtin_ctzll(missing));
+                    } else {
+                        action = kActWait;
+                    }
+                } else {
+                    const bool take = exists && lane <= cut;
+                    // Sum of the lanes from the newest up to the newest head (or the cut).
+                    const uint64_t heads_in = head_mask & upto;
+                    const uint32_t sum_cut = heads_in ? min(cut, static_cast<uint32_t>(__builtin_ctzll(heads_in))) : cut;
+                    Seg<V> window;
+                    window.count = wave_reduce(take ? s.count : 0u, SumOp{});
+                    window.sum = wave_reduce((exists && lane <= sum_cut) ? s.sum : V(0), SumOp{});
+                    acc = seg_combine(window, acc);
+                    const bool complete = stop_mask != 0 && cut == static_cast<uint32_t>(__builtin_ctzll(stop_mask));
+                    const bool found_head = MODE == kModeScan && heads_in != 0;
+                    action = (complete || found_head || top < kWave) ? kActDone : kActAdvance;
+                }
+                if (lane == 0) {
+                    s_ctl[row][0] = action;
+                    s_ctl[row][1] = help_tile;
+                    if (action == kActDone) s_prefix = acc;
+                }
+            }
+            __syncthreads();
+            const uint32_t action = s_ctl[row][0];
+            const uint32_t help_tile = s_ctl[row][1];
+            row ^= 1u;
+            if (action == kActDone) break;
+            if (action == kActAdvance) {
+                top -= kWave;
+                spins = 0;
+                continue;
+            }
+            if (action == kActWait) {
+                __builtin_amdgcn_s_sleep(1);
+                ++spins;
+                continue;
+            }
+            // kActHelp: claim the unpublished predecessor, compute its state, publish it PARTIAL.
+            uint64_t* const slot = states + static_cast<uint64_t>(help_tile) * W;
+            if (tid == 0) {
+                uint64_t expected = 0;
+                s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&slot[0], &expected, state_word(kStClaimed, 0),
+                                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT)
+                                    ? 1u
+                                    : 0u;
+            }
+            __syncthreads();
+            const bool claimed = s_ctl[row][0] != 0;
+            row ^= 1u;
+            if (claimed) {
+                const Seg<V> h = tile_aggregate<K, V>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_wave);
+                if (tid == 0) {
+                    store_sum_words(slot, kStPartial, h.sum);
+                    atomic_store_agent(&slot[0], state_word(kStPartial, h.count));
+                }
+            }
+            spins = 0;
+        }
+        prefix = s_prefix;
+    }
+
+    // A claimed tile: wait until the helper's PARTIAL is complete, so none of its stores can land
+    // after ours and no input it reads is overwritten.  Then publish this tile's INCLUSIVE state.
+    if (tid == 0) {
+        if (s_flag != 0) {
+            Seg<V> dummy;
+            while (read_state<V>(my_slot, dummy) == kStInvalid) __builtin_amdgcn_s_sleep(1);
+        }
+        if (tile > 0 || s_flag != 0) {
+            const Seg<V> incl = seg_combine(prefix, agg);
+            store_sum_words(my_slot, kStInclusive, incl.sum);
+            atomic_store_agent(&my_slot[0], state_word(kStInclusive, incl.count));
+        }
+    }
+    __syncthreads();
+
+    Seg<V> run = seg_combine(prefix, in_tile);
+    if constexpr (MODE == kModeScan) {
+        V out[kBkItems];
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) {
+            const bool head = (t.heads >> k) & 1u;
+            if (!inclusive) out[k] = head ? init : static_cast<V>(init + run.sum);
+            if (head) {
+                run.count += 1;
+                run.sum = t.val[k];
+            } else {
+                run.sum = static_cast<V>(run.sum + t.val[k]);
+            }
+            if (inclusive) out[k] = use_init ? static_cast<V>(init + run.sum) : run.sum;
+        }
+        store_items(values_out, first, n, vec_o, out);
+    } else {
+#pragma unroll
+        for (int k = 0; k < kBkItems; ++k) {
+            if (first + k < n) {
+                if ((t.heads >> k) & 1u) {
+                    if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
+                    unique_out[run.count] = t.key[k];
+                    run.count += 1;
+                    run.sum = t.val[k];
+                } else {
+                    run.sum = static_cast<V>(run.sum + t.val[k]);
+                }
+            }
+        }
+        if (first < n && n - first <= kBkItems) {  // this thread holds the last item
+            aggregates_out[run.count - 1] = run.sum;
+            num_runs_out[0] = run.count;
+        }
+    }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+template <typename K, typename V, int MODE>
+int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* values_out, K* unique_out,
+           V* aggregates_out, uint32_t* num_runs_out, uint64_t n, uint64_t key_mask, int inclusive, int use_init,
+           V init, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const char* what = MODE == kModeScan ? "DeviceScan::ScanByKey" : "DeviceReduce::ReduceByKey";
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items", what);
+    if constexpr (MODE == kModeReduce) {
+        if (!num_runs_out) return set_error(kInvalidArgument, "%s: null run-count output", what);
+        if (n == 0) return launch_fill_u32(num_runs_out, 1, 0u, stream);
+        if (!unique_out || !aggregates_out) return set_error(kInvalidArgument, "%s: null output", what);
+    } else {
+        if (n == 0) return kOk;
+        if (!values_out) return set_error(kInvalidArgument, "%s: null output", what);
+    }
+    if (!keys || !values_in) return set_error(kInvalidArgument, "%s: null input", what);
+    const size_t need = state_bytes(n, sizeof(V));
+    if (!temp || temp_bytes < need)
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, need);
+    if (reinterpret_cast<uintptr_t>(temp) % 8 != 0) return set_error(kInvalidArgument, "%s: temp not 8-byte aligned", what);
+    uint64_t* states = static_cast<uint64_t*>(temp);
+    int st = launch_fill_u32(reinterpret_cast<uint32_t*>(states), need / 4, 0u, stream);
+    if (st != kOk) return st;
+    const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kBkTile));
+    LaunchScope scope(MODE == kModeScan ? "scan_by_key" : "reduce_by_key", stream);
+    by_key_kernel<K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
+        keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
+        inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
+        g_lookback_spin_limit);
+    return check_hip(hipGetLastError(), MODE == kModeScan ? "scan_by_key launch" : "reduce_by_key launch");
+}
+
+}  // namespace
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+// Smallest temp storage these kernels use (one state of 1 + sizeof(V)/4 64-bit words per 4096-item
+// tile); never more than the reference's GetScanByKeyTempStorageBytes / GetReduceByKeyTempStorageBytes.
+size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) { return state_bytes(n, value_bytes); }
+
+#define LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, VS, VT, VU)                                                                 \
+    int lcpp_hip_scan_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in,      \
+                                             VT* values_out, uint64_t n, int inclusive, int use_init, VT init,        \
+                                             uint64_t key_mask, void* stream) {                                      \
+        return by_key<KU, VU, kModeScan>(temp, temp_bytes, reinterpret_cast<const KU*>(keys),                         \
+                                         reinterpret_cast<const VU*>(values_in), reinterpret_cast<VU*>(values_out),   \
+                                         nullptr, nullptr, nullptr, n, key_mask, inclusive, use_init,                 \
+                                         __builtin_bit_cast(VU, init), stream);                                      \
+    }                                                                                                                 \
+    int lcpp_hip_reduce_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in, const VT* values_in, \
+                                               KT* unique_out, VT* aggregates_out, uint32_t* num_runs_out, uint64_t n, \
+                                               uint64_t key_mask, void* stream) {                                    \
+        return by_key<KU, VU, kModeReduce>(temp, temp_bytes, reinterpret_cast<const KU*>(keys_in),                    \
+                                           reinterpret_cast<const VU*>(values_in), nullptr,                           \
+                                           reinterpret_cast<KU*>(unique_out), reinterpret_cast<VU*>(aggregates_out),  \
+                                           num_runs_out, n, key_mask, 0, 0, VU(0), stream);                          \
+    }
+
+#define LCPP_HIP_DEFINE_BY_KEY_VALUES(KS, KT, KU)                  \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, i32, int32_t, uint32_t)     \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, u32, uint32_t, uint32_t)    \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, f32, float, float)          \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, i64, int64_t, uint64_t)     \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, u64, uint64_t, uint64_t)    \
+    LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, f64, double, double)
+
+LCPP_HIP_DEFINE_BY_KEY_VALUES(i32, int32_t, uint32_t)
+LCPP_HIP_DEFINE_BY_KEY_VALUES(u32, uint32_t, uint32_t)
+LCPP_HIP_DEFINE_BY_KEY_VALUES(i64, int64_t, uint64_t)
+LCPP_HIP_DEFINE_BY_KEY_VALUES(u64, uint64_t, uint64_t)
+#undef LCPP_HIP_DEFINE_BY_KEY_VALUES
+#undef LCPP_HIP_DEFINE_BY_KEY
+
+}  // extern "C"

@@ -145,4 +145,39 @@ size_t lcpp_hip_radix_sort_pairs_temp_bytes(uint32_t n, size_t key_bytes, size_t
 // DeviceSpmv::GetTempStorageBytes (device/device_spmv.h:43-46).
 size_t lcpp_hip_spmv_temp_bytes(uint64_t, uint64_t, uint64_t) { return 0; }
 
+// sizeof(KeyValuePair<int, V>) (common/util_type.h:17-21): an int and a V with natural alignment.
+static size_t flag_value_pair_bytes(size_t value_bytes) { return value_bytes <= 4 ? 8 : 2 * value_bytes; }
+
+// DeviceScan<>::GetScanByKeyTempStorageBytes<K, V> (device/device_scan.h:310-315) =
+// scan_by_key_temp_storage_bytes (:129-142) with num_tiles_for (:102-109) at 256 x 15 items.
+size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    if (key_bytes == 0 || value_bytes == 0) return 0;
+    const size_t tiles = std::max<size_t>(1, ceil_div(n, 256 * 15));
+    const size_t tile_count = kWarpSize + tiles;
+    const size_t pair = flag_value_pair_bytes(value_bytes);
+    size_t bytes = tile_count * 4;
+    bytes = align_up(bytes);
+    bytes += bytes_to_uint_count(tile_count * pair) * 4;
+    bytes = align_up(bytes);
+    bytes += bytes_to_uint_count(tile_count * pair) * 4;
+    bytes = align_up(bytes);
+    bytes += bytes_to_uint_count(tiles * key_bytes) * 4;
+    return bytes;
+}
+
+// DeviceReduce<>::GetReduceByKeyTempStorageBytes<K, V> (device/device_reduce.h:207-223) with the
+// fixed 256 x 4 reduce-by-key tile (REDUCE_BY_KEY_ITEMS_PER_THREAD, :100).
+size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    if (key_bytes == 0 || value_bytes == 0) return 0;
+    const size_t tiles = std::max<size_t>(1, ceil_div(n, 4 * 256));
+    const size_t tile_count = kWarpSize + tiles;
+    const size_t pair = flag_value_pair_bytes(value_bytes);
+    size_t bytes = tile_count * 4;
+    bytes = align_up(bytes);
+    bytes += tile_count * pair;
+    bytes = align_up(bytes);
+    bytes += tile_count * pair;
+    return bytes;
+}
+
 }  // extern "C"

@@ -5,7 +5,8 @@ every call goes straight to the HIP library.  There is no CPU fallback: if the l
 loaded, :func:`lib` raises.
 
 The operation names follow the reference API (``DeviceReduce::Sum``, ``DeviceScan::ExclusiveSum``,
-``DeviceRadixSort::SortKeys/SortPairs``, ``DeviceSpmv::CsrMV``; src/lcpp/device/*.h) and the
+``DeviceRadixSort::SortKeys/SortPairs``, ``DeviceSpmv::CsrMV``, ``DeviceScan::*SumByKey``,
+``DeviceReduce::ReduceByKey``; src/lcpp/device/*.h) and the
 temp-storage queries return the reference's ``Get*TempStorageBytes`` values.
 """
 from __future__ import annotations
@@ -29,6 +30,8 @@ SCALAR_SUFFIXES = ("i32", "u32", "f32", "i64", "u64", "f64")
 SCAN_SUFFIXES = ("i32", "u32", "f32")
 SORT_KEY_SUFFIXES = ("u32", "i32", "f32", "u64", "i64", "f64")
 SPMV_SUFFIXES = [(v, i) for v in ("f32", "f64", "i32", "u32") for i in ("i32", "u32")]
+BY_KEY_KEY_SUFFIXES = ("i32", "u32", "i64", "u64")
+BY_KEY_VALUE_SUFFIXES = SCALAR_SUFFIXES
 
 _CTYPE = {
     "i32": C.c_int32, "u32": C.c_uint32, "f32": C.c_float,
@@ -92,6 +95,13 @@ def _declare(lib: C.CDLL) -> None:
                 u32, i32, vp)
     for v, i in SPMV_SUFFIXES:
         sig(f"lcpp_hip_spmv_csr_{v}_{i}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, u64, vp)
+    sig("lcpp_hip_scan_by_key_temp_bytes", sz, u64, sz, sz)
+    sig("lcpp_hip_reduce_by_key_temp_bytes", sz, u64, sz, sz)
+    sig("lcpp_hip_internal_by_key_needed_bytes", sz, u64, sz)
+    for k in BY_KEY_KEY_SUFFIXES:
+        for v in BY_KEY_VALUE_SUFFIXES:
+            sig(f"lcpp_hip_scan_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, u64, i32, i32, _CTYPE[v], u64, vp)
+            sig(f"lcpp_hip_reduce_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
 
 
 def lib() -> C.CDLL:
@@ -143,6 +153,14 @@ def sort_keys_temp_bytes(n: int, key_bytes: int) -> int:
 
 def sort_pairs_temp_bytes(n: int, key_bytes: int, value_bytes: int) -> int:
     return lib().lcpp_hip_radix_sort_pairs_temp_bytes(n, key_bytes, value_bytes)
+
+
+def scan_by_key_temp_bytes(n: int, key_bytes: int, value_bytes: int) -> int:
+    return lib().lcpp_hip_scan_by_key_temp_bytes(n, key_bytes, value_bytes)
+
+
+def reduce_by_key_temp_bytes(n: int, key_bytes: int, value_bytes: int) -> int:
+    return lib().lcpp_hip_reduce_by_key_temp_bytes(n, key_bytes, value_bytes)
 
 
 def bytes_to_uint_count(nbytes: int) -> int:
@@ -252,3 +270,27 @@ def profile_query(kernel: str) -> tuple[float, int]:
     ms, cnt = C.c_double(), C.c_uint64()
     check(lib().lcpp_hip_profile_query(kernel.encode(), C.byref(ms), C.byref(cnt)))
     return ms.value, cnt.value
+
+
+def scan_by_key(key_suffix: str, value_suffix: str, keys, values_in, values_out, n: int, inclusive: bool = False,
+                init=None, key_mask: int = -1, temp=None, stream=None) -> None:
+    """DeviceScan::ExclusiveSumByKey / InclusiveSumByKey (sum operator); `init` as in
+    ExclusiveScanByKey / InclusiveScanByKey with an initial value; keys equal when
+    ((a ^ b) & key_mask) == 0."""
+    if temp is None:
+        temp = _temp(scan_by_key_temp_bytes(n, ELEM_BYTES[key_suffix], ELEM_BYTES[value_suffix]), values_in.device)
+    use_init = init is not None
+    call(f"lcpp_hip_scan_by_key_sum_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
+         ptr(keys), ptr(values_in), ptr(values_out), n, int(inclusive), int(use_init),
+         _CTYPE[value_suffix](init if use_init else 0), key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))
+
+
+def reduce_by_key(key_suffix: str, value_suffix: str, keys, values, unique_out, aggregates_out, num_runs_out,
+                  n: int, key_mask: int = -1, temp=None, stream=None) -> None:
+    """DeviceReduce::ReduceByKey (sum operator): first key and sum of each run, and the run count."""
+    if temp is None:
+        temp = _temp(reduce_by_key_temp_bytes(n, ELEM_BYTES[key_suffix], ELEM_BYTES[value_suffix]),
+                     num_runs_out.device)
+    call(f"lcpp_hip_reduce_by_key_sum_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
+         ptr(keys), ptr(values), ptr(unique_out), ptr(aggregates_out), ptr(num_runs_out), n,
+         key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))

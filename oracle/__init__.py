@@ -51,6 +51,14 @@ def lib() -> C.CDLL:
         h.oracle_spmv_csr_fp.argtypes = [vp, i32, vp, vp, vp, vp, vp, u64, u64, u64]
         h.oracle_spmv_csr_u32.restype = None
         h.oracle_spmv_csr_u32.argtypes = [vp, vp, vp, vp, vp, u64, u64, u64]
+        h.oracle_scan_by_key_int.restype = None
+        h.oracle_scan_by_key_int.argtypes = [vp, i32, vp, i32, vp, u64, i32, i32, u64, u64]
+        h.oracle_scan_by_key_fp.restype = None
+        h.oracle_scan_by_key_fp.argtypes = [vp, i32, vp, i32, vp, vp, u64, i32, i32, C.c_double, u64]
+        h.oracle_reduce_by_key_int.restype = u64
+        h.oracle_reduce_by_key_int.argtypes = [vp, i32, vp, i32, vp, vp, u64, u64]
+        h.oracle_reduce_by_key_fp.restype = u64
+        h.oracle_reduce_by_key_fp.argtypes = [vp, i32, vp, i32, vp, vp, vp, u64, u64]
         _lib = h
     return _lib
 
@@ -164,3 +172,50 @@ def spmv_csr_u32(values, row_offsets, cols_idx, x, rows: int, cols: int, nnz: in
     y = np.empty(rows, dtype=np.uint32)
     lib().oracle_spmv_csr_u32(_p(v), _p(ro), _p(ci), _p(xx), _p(y), rows, cols, nnz)
     return y
+
+
+def _mask(key_mask: int) -> int:
+    return key_mask & 0xFFFFFFFFFFFFFFFF
+
+
+def scan_by_key_int(keys: np.ndarray, values: np.ndarray, inclusive: bool = False, use_init: bool = False,
+                    init: int = 0, key_mask: int = -1) -> np.ndarray:
+    """Sum scan by key over 4/8-byte integer values, exact modulo 2^bits (oracle.c)."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    out = np.empty_like(values)
+    lib().oracle_scan_by_key_int(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(out), values.size,
+                                 int(inclusive), int(use_init), int(init) & ((1 << (8 * values.itemsize)) - 1),
+                                 _mask(key_mask))
+    return out
+
+
+def scan_by_key_fp(keys: np.ndarray, values: np.ndarray, inclusive: bool = False, use_init: bool = False,
+                   init: float = 0.0, key_mask: int = -1) -> tuple[np.ndarray, np.ndarray]:
+    """Sum scan by key over float/double values in long double: (result, sum of |terms|)."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    out = np.empty(values.size, np.float64)
+    ab = np.empty(values.size, np.float64)
+    lib().oracle_scan_by_key_fp(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(out), _p(ab), values.size,
+                                int(inclusive), int(use_init), float(init), _mask(key_mask))
+    return out, ab
+
+
+def reduce_by_key_int(keys: np.ndarray, values: np.ndarray, key_mask: int = -1) -> tuple[np.ndarray, np.ndarray]:
+    """(first key of each run, sum of each run) for integer values, exact modulo 2^bits."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    uniq = np.empty(max(keys.size, 1), keys.dtype)
+    agg = np.empty(max(values.size, 1), values.dtype)
+    runs = lib().oracle_reduce_by_key_int(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(uniq), _p(agg),
+                                          values.size, _mask(key_mask))
+    return uniq[:runs], agg[:runs]
+
+
+def reduce_by_key_fp(keys: np.ndarray, values: np.ndarray, key_mask: int = -1):
+    """(first key of each run, long-double sum of each run, sum of |items| of each run)."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    uniq = np.empty(max(keys.size, 1), keys.dtype)
+    agg = np.empty(max(values.size, 1), np.float64)
+    ab = np.empty(max(values.size, 1), np.float64)
+    runs = lib().oracle_reduce_by_key_fp(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(uniq), _p(agg),
+                                         _p(ab), values.size, _mask(key_mask))
+    return uniq[:runs], agg[:runs], ab[:runs]

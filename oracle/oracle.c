@@ -228,3 +228,106 @@ void oracle_spmv_csr_u32(const uint32_t* values, const uint32_t* row_offsets, co
         y[r] = s;
     }
 }
+
+/* ------------------------------------------------------------------------------------------------
+ * Scan-by-key and reduce-by-key with the sum operator.  Follows DeviceScan<>::ExclusiveScanByKey /
+ * InclusiveScanByKey (src/lcpp/device/device_scan.h:424-519; ExclusiveSumByKey passes init 0,
+ * :520-558) and DeviceReduce<>::ReduceByKey (src/lcpp/device/device_reduce.h:437-487): a run starts at
+ * item 0 and wherever an item's key differs from the previous item's, compared bitwise under
+ * key_mask (all-ones = the default lhs == rhs for integer keys).
+ *   exclusive: out[i] = init + (sum of the run's items before i); a head gets init;
+ *   inclusive: out[i] = sum of the run's items up to i, plus init when use_init;
+ *   reduce: unique[r] = first key of run r, aggregates[r] = sum of run r; returns the run count.
+ * Integer values (value_bytes 4 or 8) sum exactly modulo 2^bits; float values (4 = float,
+ * 8 = double) sum in long double, with the matching sums of |items| for condition-aware tolerances.
+ * ---------------------------------------------------------------------------------------------- */
+static int by_key_head(const void* keys, int key_bytes, uint64_t i, uint64_t key_mask) {
+    if (i == 0) return 1;
+    return ((load_bits(keys, i, key_bytes) ^ load_bits(keys, i - 1, key_bytes)) & key_mask) != 0;
+}
+
+static long double fp_at(const void* values, int value_bytes, uint64_t i) {
+    return value_bytes == 4 ? (long double)((const float*)values)[i] : (long double)((const double*)values)[i];
+}
+
+void oracle_scan_by_key_int(const void* keys, int key_bytes, const void* values, int value_bytes, void* out,
+                            uint64_t n, int inclusive, int use_init, uint64_t init, uint64_t key_mask) {
+    const uint64_t vmask = value_bytes == 4 ? 0xFFFFFFFFull : ~0ull;
+    uint64_t run = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t v = load_bits(values, i, value_bytes);
+        const int head = by_key_head(keys, key_bytes, i, key_mask);
+        uint64_t o = 0;
+        if (!inclusive) o = head ? init : init + run;
+        run = head ? v : run + v;
+        if (inclusive) o = use_init ? init + run : run;
+        store_bits(out, i, value_bytes, o & vmask);
+    }
+}
+
+void oracle_scan_by_key_fp(const void* keys, int key_bytes, const void* values, int value_bytes, double* out,
+                           double* abs_out, uint64_t n, int inclusive, int use_init, double init, uint64_t key_mask) {
+    long double run = 0, arun = 0;
+    const long double ai = fabsl((long double)init);
+    for (uint64_t i = 0; i < n; ++i) {
+        const long double v = fp_at(values, value_bytes, i);
+        const int head = by_key_head(keys, key_bytes, i, key_mask);
+        if (!inclusive) {
+            out[i] = head ? init : (double)((long double)init + run);
+            abs_out[i] = head ? (double)ai : (double)(ai + arun);
+        }
+        run = head ? v : run + v;
+        arun = head ? fabsl(v) : arun + fabsl(v);
+        if (inclusive) {
+            out[i] = use_init ? (double)((long double)init + run) : (double)run;
+            abs_out[i] = use_init ? (double)(ai + arun) : (double)arun;
+        }
+    }
+}
+
+uint64_t oracle_reduce_by_key_int(const void* keys, int key_bytes, const void* values, int value_bytes,
+                                  void* unique_out, void* aggregates_out, uint64_t n, uint64_t key_mask) {
+    const uint64_t vmask = value_bytes == 4 ? 0xFFFFFFFFull : ~0ull;
+    uint64_t runs = 0, s = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t v = load_bits(values, i, value_bytes);
+        if (by_key_head(keys, key_bytes, i, key_mask)) {
+            if (runs > 0) store_bits(aggregates_out, runs - 1, value_bytes, s & vmask);
+            store_bits(unique_out, runs, key_bytes, load_bits(keys, i, key_bytes));
+            ++runs;
+            s = v;
+        } else {
+            s += v;
+        }
+    }
+    if (runs > 0) store_bits(aggregates_out, runs - 1, value_bytes, s & vmask);
+    return runs;
+}
+
+uint64_t oracle_reduce_by_key_fp(const void* keys, int key_bytes, const void* values, int value_bytes,
+                                 void* unique_out, double* aggregates_out, double* abs_out, uint64_t n,
+                                 uint64_t key_mask) {
+    uint64_t runs = 0;
+    long double s = 0, a = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const long double v = fp_at(values, value_bytes, i);
+        if (by_key_head(keys, key_bytes, i, key_mask)) {
+            if (runs > 0) {
+                aggregates_out[runs - 1] = (double)s;
+                abs_out[runs - 1] = (double)a;
+            }
+            store_bits(unique_out, runs, key_bytes, load_bits(keys, i, key_bytes));
+            ++runs;
+            s = v;
+            a = fabsl(v);
+        } else {
+            s += v;
+            a += fabsl(v);
+        }
+    }
+    if (runs > 0) {
+        aggregates_out[runs - 1] = (double)s;
+        abs_out[runs - 1] = (double)a;
+    }
+    return runs;
+}

@@ -259,3 +259,130 @@ def test_spmv_invalid_rows_and_columns(orc):
     assert y.tolist() == [10, 0, 3 * 20 + 4 * 30, 0]
     zero = orc.spmv_csr_u32(va, np.zeros(5, np.uint32), ci, x, 4, 3, 0)
     assert zero.tolist() == [0, 0, 0, 0]
+
+
+# ---- scan-by-key / reduce-by-key ---------------------------------------------------------------
+
+def numpy_by_key(keys, values, key_mask=-1):
+    """Independent formulation: head flags, then running totals per run from one cumulative sum
+    (modulo 2^64 in uint64).  Returns (heads, inclusive-within-run, per-run sums, run starts)."""
+    k = keys.astype(np.uint64) if keys.dtype.kind == "u" else keys.view(f"u{keys.itemsize}").astype(np.uint64)
+    m = np.uint64(key_mask & 0xFFFFFFFFFFFFFFFF)
+    heads = np.ones(k.size, bool)
+    heads[1:] = ((k[1:] ^ k[:-1]) & m) != 0
+    v = values.view(f"u{values.itemsize}").astype(np.uint64)
+    with np.errstate(over="ignore"):
+        cs = np.cumsum(v, dtype=np.uint64)
+        starts = np.flatnonzero(heads)
+        seg = np.cumsum(heads) - 1
+        base = cs[starts] - v[starts]
+        incl = cs - base[seg]
+        sums = np.add.reduceat(v, starts, dtype=np.uint64) if v.size else np.zeros(0, np.uint64)
+    return heads, incl, sums, starts
+
+
+@pytest.mark.parametrize("log_n", [5, 8, 12, 16])
+def test_exclusive_sum_by_key_ones_known_answer(orc, log_n):
+    """device_scan_test.cpp:325-385: ones with keys i / 100 give i % 100 (per-segment exclusive sum)."""
+    n = 1 << log_n
+    keys = (np.arange(n) // 100).astype(np.int32)
+    out = orc.scan_by_key_int(keys, np.ones(n, np.int32))
+    assert np.array_equal(out, (np.arange(n) % 100).astype(np.int32))
+
+
+def test_inclusive_sum_by_key_three_tiles_known_answer(orc):
+    """device_scan_test.cpp:387-417: int keys 1 | 2 | 3 split at tile + 1 and 2 tile + 1 (tile = 256 x 15),
+    int64 ones; the inclusive sums restart at every key change."""
+    tile = 256 * 15
+    n = 2 * tile + 2
+    idx = np.arange(n)
+    keys = np.where(idx < tile + 1, 1, np.where(idx < 2 * tile + 1, 2, 3)).astype(np.int32)
+    out = orc.scan_by_key_int(keys, np.ones(n, np.int64), inclusive=True)
+    expected = np.concatenate([np.arange(1, tile + 2), np.arange(1, tile + 1), np.arange(1, 2)]).astype(np.int64)
+    assert np.array_equal(out, expected)
+
+
+def test_inclusive_sum_by_key_parity_equality_known_answer(orc):
+    """device_scan_test.cpp:419-447: equality (lhs & 1) == (rhs & 1) over keys {1,3,5,2,4} gives {1,2,3,1,2}."""
+    out = orc.scan_by_key_int(np.array([1, 3, 5, 2, 4], np.int32), np.ones(5, np.int32), inclusive=True, key_mask=1)
+    assert out.tolist() == [1, 2, 3, 1, 2]
+
+
+def test_reduce_by_key_blocks_of_100_known_answer(orc):
+    """device_reduce_test.cpp:420-478: 4096 items, keys i / 100, values a permutation of 0..4095: 41 runs,
+    unique keys 0..40 and block sums (the reference shuffles with std::shuffle, whose permutation is
+    implementation-defined; any permutation exercises the same closed form)."""
+    n = 4096
+    keys = (np.arange(n) // 100).astype(np.int32)
+    vals = np.random.default_rng(114521).permutation(n).astype(np.int32)
+    uniq, agg = orc.reduce_by_key_int(keys, vals)
+    assert uniq.tolist() == list(range(41))
+    expected = [int(vals[i * 100:(i + 1) * 100].sum()) for i in range(41)]
+    assert agg.astype(np.int64).tolist() == expected
+
+
+def test_reduce_by_key_empty_input(orc):
+    """device_reduce_test.cpp:480-512: n == 0 gives 0 runs."""
+    uniq, agg = orc.reduce_by_key_int(np.zeros(0, np.int32), np.zeros(0, np.int32))
+    assert uniq.size == 0 and agg.size == 0
+
+
+@pytest.mark.parametrize("kdt,vdt,mask", [(np.uint32, np.uint32, -1), (np.int32, np.int64, -1),
+                                          (np.uint64, np.uint32, 0xFF00), (np.int64, np.uint64, -1)])
+@pytest.mark.parametrize("mode", ["exclusive", "inclusive", "inclusive_init"])
+def test_scan_by_key_vs_numpy(orc, kdt, vdt, mask, mode):
+    rng = np.random.default_rng(5)
+    n = 20000
+    runs = np.repeat(rng.integers(0, 1 << 20, 6000), rng.integers(1, 12, 6000))[:n]
+    assert runs.size == n
+    keys = runs.astype(kdt)
+    vals = rng.integers(0, np.iinfo(vdt).max, n, dtype=vdt, endpoint=True)
+    init = 0x9E3779B9 if mode != "inclusive" else 0
+    heads, incl, _, _ = numpy_by_key(keys, vals, mask)
+    vmask = np.uint64((1 << (8 * vals.itemsize)) - 1)
+    v = vals.view(f"u{vals.itemsize}").astype(np.uint64)
+    with np.errstate(over="ignore"):
+        if mode == "exclusive":
+            want = np.where(heads, np.uint64(init), np.uint64(init) + incl - v)
+        elif mode == "inclusive":
+            want = incl
+        else:
+            want = np.uint64(init) + incl
+    want = (want & vmask).astype(f"u{vals.itemsize}").view(vdt)
+    got = orc.scan_by_key_int(keys, vals, inclusive=mode != "exclusive", use_init=mode == "inclusive_init",
+                              init=init, key_mask=mask)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kdt,vdt,mask", [(np.int32, np.int32, -1), (np.uint64, np.uint64, -1), (np.uint32, np.int64, 3)])
+def test_reduce_by_key_vs_numpy(orc, kdt, vdt, mask):
+    rng = np.random.default_rng(9)
+    n = 30000
+    keys = np.repeat(rng.integers(0, 50, 12000), rng.integers(1, 9, 12000))[:n].astype(kdt)
+    assert keys.size == n
+    vals = rng.integers(np.iinfo(vdt).min, np.iinfo(vdt).max, n, dtype=vdt, endpoint=True)
+    heads, _, sums, starts = numpy_by_key(keys, vals, mask)
+    vmask = np.uint64((1 << (8 * vals.itemsize)) - 1)
+    uniq, agg = orc.reduce_by_key_int(keys, vals, key_mask=mask)
+    assert np.array_equal(uniq, keys[starts])
+    assert np.array_equal(agg, (sums & vmask).astype(f"u{vals.itemsize}").view(vdt))
+
+
+def test_by_key_float_paths_match_exact_sums(orc):
+    """Float values: every output equals the exactly rounded (math.fsum) sum of its run prefix."""
+    rng = np.random.default_rng(13)
+    keys = np.repeat(np.arange(40), rng.integers(1, 30, 40)).astype(np.int32)
+    vals = rng.uniform(-1e3, 1e3, keys.size).astype(np.float32)
+    heads, _, _, starts = numpy_by_key(keys, vals)
+    incl, _ = orc.scan_by_key_fp(keys, vals, inclusive=True)
+    excl, _ = orc.scan_by_key_fp(keys, vals, inclusive=False, init=2.5)
+    uniq, agg, _ = orc.reduce_by_key_fp(keys, vals)
+    seg_start = np.maximum.accumulate(np.where(heads, np.arange(keys.size), 0))
+    for i in range(keys.size):
+        part = [float(x) for x in vals[seg_start[i]:i + 1]]
+        assert incl[i] == pytest.approx(math.fsum(part), rel=1e-15, abs=1e-12)
+        assert excl[i] == pytest.approx(2.5 + math.fsum(part[:-1]), rel=1e-15, abs=1e-12)
+    ends = np.r_[starts[1:], keys.size]
+    assert np.array_equal(uniq, keys[starts])
+    for r, (b, e) in enumerate(zip(starts, ends)):
+        assert agg[r] == pytest.approx(math.fsum(float(x) for x in vals[b:e]), rel=1e-15, abs=1e-12)

@@ -90,3 +90,31 @@ def test_radix_single_portion_at_benchmark_sizes(hip):
         ref = hip.sort_keys_temp_bytes(n, kb) if vb == 0 else hip.sort_pairs_temp_bytes(n, kb, vb)
         portions = lib.lcpp_hip_internal_radix_portions(n, kb, vb, 0, kb * 8, 0, ref)
         assert portions >= (2 if n >= (1 << 30) else 1)
+
+
+def test_by_key_temp_bytes_known_values(hip):
+    """GetScanByKeyTempStorageBytes (device_scan.h:129-142, 310-315) and GetReduceByKeyTempStorageBytes
+    (device_reduce.h:207-223) worked by hand.
+    scan, n = 10000, int32 keys and values: tiles = ceil(10000 / 3840) = 3, tile_count = 35:
+      35*4 = 140 -> 256; + 35*8 = 280 -> 536 -> 768; + 280 -> 1048 -> 1280; + 3*4 = 12 -> 1292.
+    scan, n = 10000, int32 keys, int64 values: pairs of 16 B: 256 + 560 = 816 -> 1024 + 560 = 1584 -> 1792 + 12 = 1804.
+    reduce, n = 10000, int32 / int32: tiles = ceil(10000 / 1024) = 10, tile_count = 42:
+      168 -> 256; + 336 = 592 -> 768; + 336 = 1104.
+    n = 0 still reserves one tile (max(1, ...))."""
+    lib = hip.lib()
+    assert lib.lcpp_hip_scan_by_key_temp_bytes(10000, 4, 4) == 1292
+    assert lib.lcpp_hip_scan_by_key_temp_bytes(10000, 4, 8) == 1804
+    assert lib.lcpp_hip_reduce_by_key_temp_bytes(10000, 4, 4) == 1104
+    assert lib.lcpp_hip_scan_by_key_temp_bytes(0, 4, 4) == lib.lcpp_hip_scan_by_key_temp_bytes(1, 4, 4)
+    assert lib.lcpp_hip_reduce_by_key_temp_bytes(0, 4, 4) == lib.lcpp_hip_reduce_by_key_temp_bytes(1024, 4, 4)
+
+
+@pytest.mark.parametrize("kb,vb", [(4, 4), (4, 8), (8, 4), (8, 8)])
+def test_by_key_kernels_fit_reference_temp(hip, kb, vb):
+    """The by-key kernels carve at most what the reference formulas return, for every size."""
+    lib = hip.lib()
+    sizes = list(range(0, 50000, 61)) + [1 << 20, (1 << 24) + 1, 1 << 28, (1 << 32) - 1]
+    for n in sizes:
+        need = lib.lcpp_hip_internal_by_key_needed_bytes(n, vb)
+        assert need <= lib.lcpp_hip_scan_by_key_temp_bytes(n, kb, vb)
+        assert need <= lib.lcpp_hip_reduce_by_key_temp_bytes(n, kb, vb)
