@@ -3,15 +3,15 @@
 Headline (`value`): onesweep SortKeys of 2^28 uniform uint32 keys (4 x 8-bit passes), Gkeys/s, inputs
 resident in HBM, one step = one SortKeys call.  The JSON line also carries the roofline of the
 dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
-one host thread), and the other benchmark configurations (reduce, scan, SortPairs) as achieved GB/s
-against the 8 TB/s HBM peak.
+one host thread), and the other benchmark configurations (reduce, scan, SortPairs, CsrMV) plus
+ExclusiveSumByKey / ReduceByKey as achieved GB/s against the 8 TB/s HBM peak.
 
 `roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
 FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only reduce|scan|sortpairs|spmv]
+                       [--only bykey|reduce|scan|sortpairs|spmv]
 """
 from __future__ import annotations
 
@@ -181,7 +181,36 @@ def extra_spmv(hip, dev, steps, warmup, extra):
                                           "frac": round(spmv_bytes / sk / 1e6 / HBM_PEAK_GBS, 4)}
 
 
-EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv}
+def extra_by_key(hip, dev, steps, warmup, extra):
+    import torch
+    # ExclusiveSumByKey and ReduceByKey over 2^28 uint32 values in [0, 16) with int32 keys in runs of
+    # geometric length (mean 64: an item starts a run when 6 random bits are zero).
+    m = 1 << 28
+    r = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_HI, r, m, SEED + 7)
+    keys = torch.cumsum(((r & 63) == 0).to(torch.int32), 0, dtype=torch.int32)
+    del r
+    vals = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_LT16, vals, m, SEED)
+    out = torch.empty_like(vals)
+    st = torch.empty(hip.bytes_to_uint_count(hip.scan_by_key_temp_bytes(m, 4, 4)), dtype=torch.int32, device=dev)
+    t = time_steps(lambda: hip.scan_by_key("i32", "u32", keys, vals, out, m, inclusive=False, temp=st), steps, warmup)
+    sk, _ = kernel_avg_ms(hip, lambda: hip.scan_by_key("i32", "u32", keys, vals, out, m, temp=st), "scan_by_key", 5)
+    extra["exclusive_sum_by_key_i32_u32_2p28"] = {"ms": round(t, 5), "GBps": round(12 * m / t / 1e6, 1),
+                                                  "frac": round(12 * m / t / 1e6 / HBM_PEAK_GBS, 4),
+                                                  "kernel_ms": round(sk, 5)}
+    runs_out = torch.zeros(1, dtype=torch.int32, device=dev)
+    rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_by_key_temp_bytes(m, 4, 4)), dtype=torch.int32, device=dev)
+    uniq, agg = out, torch.empty_like(vals)
+    t = time_steps(lambda: hip.reduce_by_key("i32", "u32", keys, vals, uniq, agg, runs_out, m, temp=rt), steps, warmup)
+    runs = int(runs_out.item())
+    moved = 8 * m + 8 * runs
+    extra["reduce_by_key_i32_u32_2p28"] = {"ms": round(t, 5), "runs": runs, "GBps": round(moved / t / 1e6, 1),
+                                           "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+
+
+EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
+          "bykey": extra_by_key}
 
 
 def run_extras(hip, dev, steps, warmup, names):

@@ -25,19 +25,26 @@
 //     items serially; a DPP wave scan (the shared row_shr / row_bcast pattern) and one pass over the
 //     4 wave totals in LDS give each thread its carry-in and the tile its aggregate.
 //   * Tile states are 64-bit words with the status in the low half and 32 payload bits in the high
-//     half: word 0 holds the head count, words 1.. the sum.  A reader accepts a state only when every
+//     half.  Reduce-by-key: word 0 holds the head count, words 1.. the sum.  Scan-by-key needs only
+//     a has-head flag, kept beside the status, so its state is just the sum words (one word for
+//     4-byte values: half the look-back loads).  A reader accepts a state only when every
 //     word shows the same published status, so each word is one relaxed agent-scope atomic (the 8
-//     XCDs do not share an L2) and no fence is needed.  Only the workgroup that wins word 0 by
-//     compare-and-swap writes a PARTIAL state.
+//     XCDs do not share an L2) and no fence is needed.  The owner publishes PARTIAL (tile 0:
+//     INCLUSIVE) with plain stores from lane 0 of its last wave: a wave's vector memory operations
+//     complete in issue order, so stores issued by wave 0 would delay its own look-back loads.
 //   * Look-back: wave 0 reads 64 predecessors per step (one per lane).  Ballots find the newest
 //     INCLUSIVE state (or tile 0) and, for the scan, the newest state with a head: the scan stops
 //     there because older sums cannot reach this tile; ReduceByKey continues to an INCLUSIVE state
 //     since run indices need the full head count.  Counts and sums reduce with DPP.
-//   * Forward progress never depends on dispatch order: a predecessor still unpublished after
-//     `spin_limit` polls is claimed (word 0: INVALID -> CLAIMED), its state is computed by the whole
-//     waiting workgroup with the owner's own code (the same float summation order), and published
-//     PARTIAL.  An owner that finds its tile claimed waits for that PARTIAL before it stores anything,
-//     so an in-place scan (values_out == values_in) never overwrites input a helper still reads.
+//   * Forward progress never depends on dispatch order.  Each tile has a claim word (in an array
+//     after the state slots).  A predecessor still unpublished after `spin_limit` polls is claimed
+//     by compare-and-swap
+//     (OPEN -> HELPER), its state computed by the whole waiting workgroup with the owner's own code
+//     (the same float summation order) and published PARTIAL, then the claim is marked DONE with
+//     release ordering.  The owner closes its claim word (OPEN -> OWNED) right after publishing and
+//     looks at the result only after its look-back; if a helper got there first it waits for DONE
+//     before publishing INCLUSIVE or storing outputs, so no PARTIAL store can land after its
+//     INCLUSIVE ones and an in-place scan never overwrites input a helper still reads.
 // Algorithmic traffic: scan n*(sizeof(K) + 2*sizeof(V)); reduce n*(sizeof(K) + sizeof(V)) plus
 // runs*(sizeof(K) + sizeof(V)) written.
 #include "common.hpp"
@@ -54,7 +61,13 @@ constexpr uint32_t kBkTile = static_cast<uint32_t>(kBkBlock) * kBkItems;  // 409
 constexpr uint32_t kStInvalid = 0;
 constexpr uint32_t kStPartial = 1;
 constexpr uint32_t kStInclusive = 2;
-constexpr uint32_t kStClaimed = 3;
+
+// Claim word of a tile (a separate array after all state slots, so the slots the look-back reads
+// stay densely packed).
+constexpr uint64_t kClaimOpen = 0;    // nobody has closed or claimed the tile yet
+constexpr uint64_t kClaimOwned = 1;   // the owner closed it: no helper will ever read its input
+constexpr uint64_t kClaimHelper = 2;  // a helper is computing the tile's state from its input
+constexpr uint64_t kClaimDone = 3;    // the helper's PARTIAL stores have all been performed
 
 constexpr int kModeScan = 0;
 constexpr int kModeReduce = 1;
@@ -81,12 +94,19 @@ __device__ __forceinline__ Seg<V> seg_combine(Seg<V> older, Seg<V> newer) {
 
 template <typename V>
 constexpr int kValueWords = static_cast<int>(sizeof(V) / 4);
-template <typename V>
-constexpr int kStateWords = 1 + kValueWords<V>;
+// Words of a tile state.  Reduce-by-key keeps the head count in a word of its own (word 0) ahead
+// of the sum words; scan-by-key only needs to know whether a span holds a head, which rides in bit 2
+// of the status half of the first sum word, so a 4-byte sum makes a one-word state.
+template <typename V, bool COUNTED>
+constexpr int kStateWords = (COUNTED ? 1 : 0) + kValueWords<V>;
 
-size_t state_bytes(uint64_t n, size_t value_bytes) {
-    return ceil_div(n, kBkTile) * (1 + value_bytes / 4) * sizeof(uint64_t);
+// Temp layout: tiles x state words, then one claim word per tile.
+size_t state_bytes(uint64_t n, size_t value_bytes, bool counted) {
+    return ceil_div(n, kBkTile) * ((counted ? 2 : 1) + value_bytes / 4) * sizeof(uint64_t);
 }
+
+constexpr uint32_t kStatusMask = 3;
+constexpr uint32_t kHeadFlag = 4;
 
 __device__ __forceinline__ uint64_t state_word(uint32_t status, uint32_t payload) {
     return (static_cast<uint64_t>(payload) << 32) | status;
@@ -101,29 +121,43 @@ __device__ __forceinline__ uint32_t value_part(V v, int w) {
     }
 }
 
-// Stores the sum words of a state.  Only the holder of the tile's word 0 calls it.
-template <typename V>
-__device__ __forceinline__ void store_sum_words(uint64_t* slot, uint32_t status, V sum) {
+// Publishes state `s` with `status` (by the owner, or by the helper that claimed the tile).
+template <typename V, bool COUNTED>
+__device__ __forceinline__ void publish_state(uint64_t* slot, uint32_t status, Seg<V> s) {
+    if constexpr (COUNTED) {
 #pragma unroll
-    for (int w = 0; w < kValueWords<V>; ++w) atomic_store_agent(&slot[1 + w], state_word(status, value_part(sum, w)));
+        for (int w = 0; w < kValueWords<V>; ++w) atomic_store_agent(&slot[1 + w], state_word(status, value_part(s.sum, w)));
+        atomic_store_agent(&slot[0], state_word(status, s.count));
+    } else {
+#pragma unroll
+        for (int w = 1; w < kValueWords<V>; ++w) atomic_store_agent(&slot[w], state_word(status, value_part(s.sum, w)));
+        atomic_store_agent(&slot[0], state_word(status | (s.count != 0 ? kHeadFlag : 0u), value_part(s.sum, 0)));
+    }
 }
 
 // Reads a tile state; returns its status if every word carries the same published status
-// (PARTIAL or INCLUSIVE), kStInvalid otherwise.
-template <typename V>
+// (PARTIAL or INCLUSIVE), kStInvalid otherwise.  Without COUNTED, s.count is 1 when the span holds
+// a head, else 0.
+template <typename V, bool COUNTED>
 __device__ __forceinline__ uint32_t read_state(const uint64_t* slot, Seg<V>& s) {
-    uint64_t w[kStateWords<V>];
+    constexpr int N = kStateWords<V, COUNTED>;
+    constexpr int B = COUNTED ? 1 : 0;  // first sum word
+    uint64_t w[N];
 #pragma unroll
-    for (int i = 0; i < kStateWords<V>; ++i) w[i] = atomic_load_agent(&slot[i]);
-    const uint32_t st = static_cast<uint32_t>(w[0]);
+    for (int i = 0; i < N; ++i) w[i] = atomic_load_agent(&slot[i]);
+    const uint32_t st = static_cast<uint32_t>(w[0]) & kStatusMask;
     bool ok = st == kStPartial || st == kStInclusive;
 #pragma unroll
-    for (int i = 1; i < kStateWords<V>; ++i) ok = ok && static_cast<uint32_t>(w[i]) == st;
-    s.count = static_cast<uint32_t>(w[0] >> 32);
-    if constexpr (sizeof(V) == 4) {
-        s.sum = __builtin_bit_cast(V, static_cast<uint32_t>(w[1] >> 32));
+    for (int i = 1; i < N; ++i) ok = ok && (static_cast<uint32_t>(w[i]) & kStatusMask) == st;
+    if constexpr (COUNTED) {
+        s.count = static_cast<uint32_t>(w[0] >> 32);
     } else {
-        s.sum = __builtin_bit_cast(V, (w[2] & 0xFFFFFFFF00000000ull) | (w[1] >> 32));
+        s.count = (static_cast<uint32_t>(w[0]) & kHeadFlag) != 0 ? 1u : 0u;
+    }
+    if constexpr (sizeof(V) == 4) {
+        s.sum = __builtin_bit_cast(V, static_cast<uint32_t>(w[B] >> 32));
+    } else {
+        s.sum = __builtin_bit_cast(V, (w[B + 1] & 0xFFFFFFFF00000000ull) | (w[B] >> 32));
     }
     return ok ? st : kStInvalid;
 }
@@ -253,6 +287,26 @@ __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uin
     return agg;
 }
 
+// Scan outputs of a thread's items from the state carried into its first item.
+template <typename K, typename V>
+__device__ __forceinline__ void scan_outputs(const ThreadItems<K, V>& t, Seg<V> run, int inclusive, int use_init, V init,
+                                             V* values_out, uint64_t first, uint64_t n, bool vec_o) {
+    V out[kBkItems];
+#pragma unroll
+    for (int k = 0; k < kBkItems; ++k) {
+        const bool head = (t.heads >> k) & 1u;
+        if (!inclusive) out[k] = head ? init : static_cast<V>(init + run.sum);
+        if (head) {
+            run.count += 1;
+            run.sum = t.val[k];
+        } else {
+            run.sum = static_cast<V>(run.sum + t.val[k]);
+        }
+        if (inclusive) out[k] = use_init ? static_cast<V>(init + run.sum) : run.sum;
+    }
+    store_items(values_out, first, n, vec_o, out);
+}
+
 template <typename K, typename V, int MODE>
 __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ keys, const V* values_in,
                                                           V* values_out, K* __restrict__ unique_out,
@@ -260,11 +314,16 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
                                                           uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
                                                           uint64_t* __restrict__ states, int inclusive, int use_init,
                                                           V init, bool vec_k, bool vec_v, bool vec_o,
-                                                          uint32_t spin_limit) {
-    constexpr int W = kStateWords<V>;
+                                                          bool in_place, uint32_t spin_limit) {
+    constexpr bool COUNTED = MODE == kModeReduce;
+    constexpr int W = kStateWords<V, COUNTED>;
+    uint64_t* const claims = states + static_cast<uint64_t>(gridDim.x) * W;
+    // The thread that publishes this tile's states and closes its claim word: lane 0 of the last
+    // wave.  A wave's vector memory operations complete in issue order, so publishing from wave 0
+    // would make its look-back loads wait for the publishing stores and the compare-and-swap.
+    constexpr uint32_t kPublisher = kBkBlock - kWave;
     __shared__ Seg<V> s_wave[kBkWaves];
     __shared__ uint32_t s_ctl[2][2];  // look-back decision and helped tile, two alternating rows
-    __shared__ uint32_t s_flag;
     __shared__ Seg<V> s_prefix;
 
     const uint32_t tid = threadIdx.x;
@@ -278,17 +337,28 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
     Seg<V> in_tile, agg;
     block_seg_scan(fold_thread(t, first, n), s_wave, in_tile, agg);
 
-    // Publish: win word 0 (INVALID -> PARTIAL, or INCLUSIVE for tile 0), then the sum words.  A
-    // tile already claimed by a helper gets its PARTIAL from that helper.
+    // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
+    // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
+    // first stores the same PARTIAL values.
     uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
-    if (tid == 0) {
-        uint64_t expected = 0;
+    bool owned = true;
+    if (tid == kPublisher) {
         const uint32_t st = tile == 0 ? kStInclusive : kStPartial;
-        const bool won = __hip_atomic_compare_exchange_strong(&my_slot[0], &expected, state_word(st, agg.count),
-                                                              __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-        if (won) store_sum_words(my_slot, st, agg.sum);
-        s_flag = won ? 0u : 1u;
+        publish_state<V, COUNTED>(my_slot, st, agg);
+        uint64_t expected = kClaimOpen;
+        owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // Scan outputs that do not depend on the tile's prefix (a run starts in this tile before or at the
+    // thread's first item) are stored now, after the publish and by waves other than wave 0, so they
+    // overlap the look-back without delaying the publish or wave 0's look-back loads (a wave's
+    // vector memory operations complete in issue order).  Not for in-place scans: their input may
+    // still be read by a helper until the claim is settled.
+    bool early = false;
+    if constexpr (MODE == kModeScan) {
+        early = !in_place && wave != 0 && (in_tile.count != 0 || (t.heads & 1u) != 0);
+        if (early) scan_outputs(t, in_tile, inclusive, use_init, init, values_out, first, n, vec_o);
     }
 
     Seg<V> prefix{0u, V(0)};
@@ -301,7 +371,7 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
             if (wave == 0) {
                 const int64_t j = top - static_cast<int64_t>(lane);
                 Seg<V> s{0u, V(0)};
-                const uint32_t st = j >= 0 ? read_state<V>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
+                const uint32_t st = j >= 0 ? read_state<V, COUNTED>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
                 const bool exists = j >= 0;
                 const bool published = st != kStInvalid;
                 // A complete prefix: an INCLUSIVE state, or tile 0 (nothing precedes it).
@@ -356,11 +426,12 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
                 ++spins;
                 continue;
             }
-            // kActHelp: claim the unpublished predecessor, compute its state, publish it PARTIAL.
+            // kActHelp: claim the unpublished predecessor, compute its state, publish it PARTIAL, and
+            // mark the claim DONE with release ordering (after every PARTIAL store is performed).
             uint64_t* const slot = states + static_cast<uint64_t>(help_tile) * W;
             if (tid == 0) {
-                uint64_t expected = 0;
-                s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&slot[0], &expected, state_word(kStClaimed, 0),
+                uint64_t expected = kClaimOpen;
+                s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&claims[help_tile], &expected, kClaimHelper,
                                                                      __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                                      __HIP_MEMORY_SCOPE_AGENT)
                                     ? 1u
@@ -372,8 +443,8 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
             if (claimed) {
                 const Seg<V> h = tile_aggregate<K, V>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_wave);
                 if (tid == 0) {
-                    store_sum_words(slot, kStPartial, h.sum);
-                    atomic_store_agent(&slot[0], state_word(kStPartial, h.count));
+                    publish_state<V, COUNTED>(slot, kStPartial, h);
+                    __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
             spins = 0;
@@ -381,37 +452,24 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
         prefix = s_prefix;
     }
 
-    // A claimed tile: wait until the helper's PARTIAL is complete, so none of its stores can land
-    // after ours and no input it reads is overwritten.  Then publish this tile's INCLUSIVE state.
-    if (tid == 0) {
-        if (s_flag != 0) {
-            Seg<V> dummy;
-            while (read_state<V>(my_slot, dummy) == kStInvalid) __builtin_amdgcn_s_sleep(1);
+    // A tile a helper claimed first: wait until the helper is DONE, so none of its PARTIAL stores can
+    // land after the INCLUSIVE ones and no input it reads is overwritten (in-place scans).  Then
+    // publish this tile's INCLUSIVE state (tile 0's initial state already was, unless helped).
+    if (tid == kPublisher) {
+        if (!owned) {
+            while (__hip_atomic_load(&claims[tile], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != kClaimDone)
+                __builtin_amdgcn_s_sleep(1);
         }
-        if (tile > 0 || s_flag != 0) {
+        if (tile > 0 || !owned) {
             const Seg<V> incl = seg_combine(prefix, agg);
-            store_sum_words(my_slot, kStInclusive, incl.sum);
-            atomic_store_agent(&my_slot[0], state_word(kStInclusive, incl.count));
+            publish_state<V, COUNTED>(my_slot, kStInclusive, incl);
         }
     }
-    __syncthreads();
+    __syncthreads();  // outputs only after the claim is settled
 
     Seg<V> run = seg_combine(prefix, in_tile);
     if constexpr (MODE == kModeScan) {
-        V out[kBkItems];
-#pragma unroll
-        for (int k = 0; k < kBkItems; ++k) {
-            const bool head = (t.heads >> k) & 1u;
-            if (!inclusive) out[k] = head ? init : static_cast<V>(init + run.sum);
-            if (head) {
-                run.count += 1;
-                run.sum = t.val[k];
-            } else {
-                run.sum = static_cast<V>(run.sum + t.val[k]);
-            }
-            if (inclusive) out[k] = use_init ? static_cast<V>(init + run.sum) : run.sum;
-        }
-        store_items(values_out, first, n, vec_o, out);
+        if (!early) scan_outputs(t, run, inclusive, use_init, init, values_out, first, n, vec_o);
     } else {
 #pragma unroll
         for (int k = 0; k < kBkItems; ++k) {
@@ -451,7 +509,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
         if (!values_out) return set_error(kInvalidArgument, "%s: null output", what);
     }
     if (!keys || !values_in) return set_error(kInvalidArgument, "%s: null input", what);
-    const size_t need = state_bytes(n, sizeof(V));
+    const size_t need = state_bytes(n, sizeof(V), MODE == kModeReduce);
     if (!temp || temp_bytes < need)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, need);
     if (reinterpret_cast<uintptr_t>(temp) % 8 != 0) return set_error(kInvalidArgument, "%s: temp not 8-byte aligned", what);
@@ -463,7 +521,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     by_key_kernel<K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
-        g_lookback_spin_limit);
+        values_out != nullptr && values_out == values_in, g_lookback_spin_limit);
     return check_hip(hipGetLastError(), MODE == kModeScan ? "scan_by_key launch" : "reduce_by_key launch");
 }
 
@@ -474,9 +532,10 @@ using namespace lcpp_hip;
 
 extern "C" {
 
-// Smallest temp storage these kernels use (one state of 1 + sizeof(V)/4 64-bit words per 4096-item
-// tile); never more than the reference's GetScanByKeyTempStorageBytes / GetReduceByKeyTempStorageBytes.
-size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) { return state_bytes(n, value_bytes); }
+// Temp storage the reduce-by-key kernel carves (the larger of the two layouts: per 4096-item tile a
+// count word, sizeof(V)/4 sum words and a claim word); never more than the reference's
+// GetScanByKeyTempStorageBytes / GetReduceByKeyTempStorageBytes.
+size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) { return state_bytes(n, value_bytes, true); }
 
 #define LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, VS, VT, VU)                                                                 \
     int lcpp_hip_scan_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in,      \
