@@ -196,6 +196,14 @@ LCPP_HIP_DECLARE_SPMV(u32, uint32_t, u32, uint32_t)
  * ------------------------------------------------------------------------------------------- */
 size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);
 size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);
+/* The same queries for other DeviceScan<BLOCK, 32, ITEMS> / DeviceReduce<BLOCK> policies
+ * (device_scan.h:129-142,310-315; device_reduce.h:207-223).  Where a policy's tiles are so large
+ * that the reference layout is smaller than the by-key kernel's tile states, the result is raised
+ * to the kernel's need; for the default policies it is the reference's figure exactly. */
+size_t lcpp_hip_scan_by_key_temp_bytes_policy(uint64_t n, size_t key_bytes, size_t value_bytes, uint32_t block_size,
+                                              uint32_t items_per_thread);
+size_t lcpp_hip_reduce_by_key_temp_bytes_policy(uint64_t n, size_t key_bytes, size_t value_bytes,
+                                                uint32_t block_size);
 
 #define LCPP_HIP_DECLARE_BY_KEY(KS, KT, VS, VT)                                                                      \
     int lcpp_hip_scan_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in,     \

@@ -9,13 +9,13 @@
 //   * Rows with at most kShortRow nonzeros are summed by their own lane, in order.
 //   * Longer rows are taken one at a time by the whole wave: 64 lanes stride the row with coalesced
 //     value/column loads, then a DPP wave reduction; the row's lane writes y.  Rows longer than
-//     kVecRow read both streams in 16-byte groups of 4 elements when the arrays are 16-byte aligned,
-//     cutting the vector memory instructions per nonzero (the texture addresser, not HBM, limits
-//     this kernel).
+//     kVecRow read both streams in groups of kGroup consecutive elements per lane (16-byte-aligned
+//     vector loads) when the arrays are 16-byte aligned, cutting the vector memory instructions per
+//     nonzero (the texture addresser, not HBM, limits this kernel).
 //   Power-law row lengths therefore cost each wave about (longest short row) + sum(long/64) steps,
 //   instead of one 64-lane pass per row.
 // Floating-point order: short rows are summed left to right; other rows as 64 per-lane partial sums
-// (lane-strided elements, or for the grouped path the lane's groups of 4 consecutive elements)
+// (lane-strided elements, or for the grouped path the lane's groups of kGroup consecutive elements)
 // combined by the DPP scan tree.  Integer values wrap modulo 2^32.
 // Algorithmic traffic: nnz * (sizeof(V) + sizeof(I)) + (rows + 1) * sizeof(I) + rows * sizeof(V)
 // + gathered x (at least cols * sizeof(V)).

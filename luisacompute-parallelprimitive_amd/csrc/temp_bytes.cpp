@@ -148,11 +148,14 @@ size_t lcpp_hip_spmv_temp_bytes(uint64_t, uint64_t, uint64_t) { return 0; }
 // sizeof(KeyValuePair<int, V>) (common/util_type.h:17-21): an int and a V with natural alignment.
 static size_t flag_value_pair_bytes(size_t value_bytes) { return value_bytes <= 4 ? 8 : 2 * value_bytes; }
 
-// DeviceScan<>::GetScanByKeyTempStorageBytes<K, V> (device/device_scan.h:310-315) =
-// scan_by_key_temp_storage_bytes (:129-142) with num_tiles_for (:102-109) at 256 x 15 items.
-size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
-    if (key_bytes == 0 || value_bytes == 0) return 0;
-    const size_t tiles = std::max<size_t>(1, ceil_div(n, 256 * 15));
+// DeviceScan<BLOCK, 32, ITEMS>::GetScanByKeyTempStorageBytes<K, V> (device/device_scan.h:310-315) =
+// scan_by_key_temp_storage_bytes (:129-142) with num_tiles_for (:102-109), raised to what the
+// by-key kernel carves when a policy's tiles are so large that the reference layout is smaller.
+size_t lcpp_hip_scan_by_key_temp_bytes_policy(uint64_t n, size_t key_bytes, size_t value_bytes, uint32_t block_size,
+                                              uint32_t items_per_thread) {
+    const size_t tile = static_cast<size_t>(block_size) * items_per_thread;
+    if (tile == 0 || key_bytes == 0 || value_bytes == 0) return 0;
+    const size_t tiles = std::max<size_t>(1, ceil_div(n, tile));
     const size_t tile_count = kWarpSize + tiles;
     const size_t pair = flag_value_pair_bytes(value_bytes);
     size_t bytes = tile_count * 4;
@@ -162,14 +165,21 @@ size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t valu
     bytes += bytes_to_uint_count(tile_count * pair) * 4;
     bytes = align_up(bytes);
     bytes += bytes_to_uint_count(tiles * key_bytes) * 4;
-    return bytes;
+    return std::max(bytes, lcpp_hip_internal_by_key_needed_bytes(n, value_bytes));
 }
 
-// DeviceReduce<>::GetReduceByKeyTempStorageBytes<K, V> (device/device_reduce.h:207-223) with the
-// fixed 256 x 4 reduce-by-key tile (REDUCE_BY_KEY_ITEMS_PER_THREAD, :100).
-size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
-    if (key_bytes == 0 || value_bytes == 0) return 0;
-    const size_t tiles = std::max<size_t>(1, ceil_div(n, 4 * 256));
+// DeviceScan<> (256 x 15 items, device/device_scan.h:40-49).
+size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    return lcpp_hip_scan_by_key_temp_bytes_policy(n, key_bytes, value_bytes, 256, 15);
+}
+
+// DeviceReduce<BLOCK>::GetReduceByKeyTempStorageBytes<K, V> (device/device_reduce.h:207-223) with
+// the fixed REDUCE_BY_KEY_ITEMS_PER_THREAD = 4 (:100), raised like the scan-by-key query above.
+size_t lcpp_hip_reduce_by_key_temp_bytes_policy(uint64_t n, size_t key_bytes, size_t value_bytes,
+                                                uint32_t block_size) {
+    const size_t tile = static_cast<size_t>(block_size) * 4;
+    if (tile == 0 || key_bytes == 0 || value_bytes == 0) return 0;
+    const size_t tiles = std::max<size_t>(1, ceil_div(n, tile));
     const size_t tile_count = kWarpSize + tiles;
     const size_t pair = flag_value_pair_bytes(value_bytes);
     size_t bytes = tile_count * 4;
@@ -177,7 +187,12 @@ size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t va
     bytes += tile_count * pair;
     bytes = align_up(bytes);
     bytes += tile_count * pair;
-    return bytes;
+    return std::max(bytes, lcpp_hip_internal_by_key_needed_bytes(n, value_bytes));
+}
+
+// DeviceReduce<> (BLOCK_SIZE = 256).
+size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    return lcpp_hip_reduce_by_key_temp_bytes_policy(n, key_bytes, value_bytes, 256);
 }
 
 }  // extern "C"

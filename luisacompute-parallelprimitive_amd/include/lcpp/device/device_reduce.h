@@ -1,12 +1,14 @@
 // DeviceReduce::Sum over the MI355X C-ABI (lcpp_hip_reduce_sum_*), with the reference's module
 // shape (src/lcpp/device/device_reduce.h:102-113 template, :154-173 create, :184-189 temp query,
 // :280-288 Sum) and its record-time checks (:238-264).  Sum records one command; the kernels run on
-// the stream the command list is committed to.
+// the stream the command list is committed to.  ReduceByKey with a sum operator (:437-487, temp
+// query :207-223) runs lcpp_hip_reduce_by_key_sum_*, which writes 0 runs for empty input (:449-458).
 #pragma once
 
 #include <limits>
 #include <type_traits>
 
+#include "lcpp/device/by_key_abi.h"
 #include "lcpp/runtime/core.h"
 
 namespace luisa::parallel_primitive {
@@ -26,6 +28,49 @@ class DeviceReduce : public LuisaModule {
     static size_t GetTempStorageBytes(size_t num_item) {
         return lcpp_hip_reduce_temp_bytes_policy(num_item, sizeof(T), static_cast<uint32_t>(BLOCK_SIZE),
                                                  static_cast<uint32_t>(ITEMS_PER_THREAD));
+    }
+
+    // Temp bytes of ReduceByKey: tiles of REDUCE_BY_KEY_ITEMS_PER_THREAD (4) x BLOCK_SIZE items.
+    template <typename KeyType, typename ValueType>
+    static size_t GetReduceByKeyTempStorageBytes(size_t num_elements) {
+        return lcpp_hip_reduce_by_key_temp_bytes_policy(num_elements, sizeof(KeyType), sizeof(ValueType),
+                                                        static_cast<uint32_t>(BLOCK_SIZE));
+    }
+
+    // Runs of equal keys (under `equality_op`) reduce to (first key, sum); g_num_runs_out[0] = runs.
+    // d_unique_out and g_aggregates_out must hold one element per run.
+    template <NumericT KeyType, NumericT ValueType>
+    void ReduceByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                     BufferView<ValueType> d_values_in, BufferView<KeyType> d_unique_out,
+                     BufferView<ValueType> g_aggregates_out, BufferView<uint> g_num_runs_out, SumOp,
+                     size_t num_elements, KeyMaskEquality equality_op = {}) {
+        static_assert(detail::by_key_key_ok<KeyType>, "ReduceByKey takes 4- or 8-byte integer keys");
+        static_assert(detail::by_key_value_ok<ValueType>, "ReduceByKey sums 4- or 8-byte integers, float or double");
+        LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
+        LCPP_ASSERT(num_elements <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
+        LCPP_ASSERT(g_num_runs_out.size() >= 1u, "DeviceReduce run-count output view is empty.");
+        if (num_elements > 0) {
+            LCPP_ASSERT(d_keys_in.size() >= num_elements, "DeviceReduce key view is too small.");
+            LCPP_ASSERT(d_values_in.size() >= num_elements, "DeviceReduce value view is too small.");
+            LCPP_ASSERT(temp_storage.size() >=
+                            bytes_to_uint_count(GetReduceByKeyTempStorageBytes<KeyType, ValueType>(num_elements)),
+                        "DeviceReduce temporary storage is too small.");
+        }
+        using KA = detail::by_key_abi_t<KeyType>;
+        using VA = detail::by_key_abi_t<ValueType>;
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const KA* keys = reinterpret_cast<const KA*>(d_keys_in.data());
+        const VA* values = reinterpret_cast<const VA*>(d_values_in.data());
+        KA* unique = reinterpret_cast<KA*>(d_unique_out.data());
+        VA* aggregates = reinterpret_cast<VA*>(g_aggregates_out.data());
+        uint32_t* runs = g_num_runs_out.data();
+        const uint64_t mask = equality_op.mask;
+        cmdlist << [=](hipStream_t s) {
+            const int rc = detail::reduce_by_key_sum(temp, temp_bytes, keys, values, unique, aggregates, runs,
+                                                     num_elements, mask, detail::stream_ptr(s));
+            luisa::detail::abi_check(rc, "DeviceReduce::ReduceByKey");
+        };
     }
 
     template <NumericT T>

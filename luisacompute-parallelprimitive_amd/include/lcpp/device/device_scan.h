@@ -2,12 +2,15 @@
 // (src/lcpp/device/device_scan.h:40-49 template, :269-284 create, :295-308 temp query) and entry
 // points ExclusiveSum (:370-385), InclusiveSum (:409-422), ExclusiveScan / InclusiveScan /
 // InclusiveScanInit with a sum operator (:321-368), checked like validate_scan_views (:213-226).
-// The single-pass kernel is a decoupled look-back over the caller's temp storage.
+// The single-pass kernel is a decoupled look-back over the caller's temp storage.  The by-key
+// entry points (:424-597, temp query :310-315) run the segmented scan of lcpp_hip_scan_by_key_sum_*,
+// checked like validate_scan_by_key_views (:228-246).
 #pragma once
 
 #include <limits>
 #include <type_traits>
 
+#include "lcpp/device/by_key_abi.h"
 #include "lcpp/runtime/core.h"
 
 namespace luisa::parallel_primitive {
@@ -75,7 +78,89 @@ class DeviceScan : public LuisaModule {
         record(cmdlist, temp_storage, d_in, d_out, num_items, true, initial_value);
     }
 
+    // ---- by key ---------------------------------------------------------------------------------
+    template <typename KeyType, typename ValueType>
+    static size_t GetScanByKeyTempStorageBytes(size_t num_items) {
+        return lcpp_hip_scan_by_key_temp_bytes_policy(num_items, sizeof(KeyType), sizeof(ValueType),
+                                                      static_cast<uint32_t>(BLOCK_SIZE),
+                                                      static_cast<uint32_t>(ITEMS_PER_THREAD));
+    }
+
+    template <NumericT KeyType, NumericT ValueType>
+    void ExclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            size_t num_items, ValueType initial_value, KeyMaskEquality equality_op = {}) {
+        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
+                      initial_value, equality_op, "DeviceScan::ExclusiveScanByKey");
+    }
+
+    template <NumericT KeyType, NumericT ValueType>
+    void InclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            size_t num_items, KeyMaskEquality equality_op = {}) {
+        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
+                      ValueType(0), equality_op, "DeviceScan::InclusiveScanByKey");
+    }
+
+    // Inclusive scan with `initial_value` prepended to every segment (device_scan.h:488-519).
+    template <NumericT KeyType, NumericT ValueType>
+    void InclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            size_t num_items, ValueType initial_value, KeyMaskEquality equality_op = {}) {
+        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, true,
+                      initial_value, equality_op, "DeviceScan::InclusiveScanByKey");
+    }
+
+    template <NumericT KeyType, NumericT ValueType>
+    void ExclusiveSumByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                           BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
+                           KeyMaskEquality equality_op = {}) {
+        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
+                      ValueType(0), equality_op, "DeviceScan::ExclusiveSumByKey");
+    }
+
+    template <NumericT KeyType, NumericT ValueType>
+    void InclusiveSumByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                           BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
+                           KeyMaskEquality equality_op = {}) {
+        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
+                      ValueType(0), equality_op, "DeviceScan::InclusiveSumByKey");
+    }
+
   private:
+    template <NumericT KeyType, NumericT ValueType>
+    void record_by_key(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+                       BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
+                       bool inclusive, bool use_init, ValueType init, KeyMaskEquality equality_op, const char* what) {
+        static_assert(detail::by_key_key_ok<KeyType>, "scan by key takes 4- or 8-byte integer keys");
+        static_assert(detail::by_key_value_ok<ValueType>, "scan by key sums 4- or 8-byte integers, float or double");
+        LCPP_ASSERT(m_created, "DeviceScan::create must be called before dispatch.");
+        LCPP_ASSERT(num_items <= std::numeric_limits<uint>::max(), "Too many items for DeviceScan.");
+        if (num_items == 0u) return;
+        LCPP_ASSERT(d_keys_in.size() >= num_items, "DeviceScan key view is too small.");
+        LCPP_ASSERT(d_values_in.size() >= num_items, "DeviceScan value view is too small.");
+        LCPP_ASSERT(d_values_out.size() >= num_items, "DeviceScan output view is too small.");
+        LCPP_ASSERT(temp_storage.size() >=
+                        bytes_to_uint_count(GetScanByKeyTempStorageBytes<KeyType, ValueType>(num_items)),
+                    "DeviceScan temporary storage is too small.");
+        using KA = detail::by_key_abi_t<KeyType>;
+        using VA = detail::by_key_abi_t<ValueType>;
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const KA* keys = reinterpret_cast<const KA*>(d_keys_in.data());
+        const VA* in = reinterpret_cast<const VA*>(d_values_in.data());
+        VA* out = reinterpret_cast<VA*>(d_values_out.data());
+        const VA init_abi = static_cast<VA>(init);
+        const int inc = inclusive ? 1 : 0;
+        const int with_init = use_init ? 1 : 0;
+        const uint64_t mask = equality_op.mask;
+        cmdlist << [=](hipStream_t s) {
+            const int rc = detail::scan_by_key_sum(temp, temp_bytes, keys, in, out, num_items, inc, with_init,
+                                                   init_abi, mask, detail::stream_ptr(s));
+            luisa::detail::abi_check(rc, what);
+        };
+    }
+
     template <NumericT T>
     void record(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
                 size_t num_items, bool inclusive, T init) {

@@ -97,6 +97,8 @@ def _declare(lib: C.CDLL) -> None:
         sig(f"lcpp_hip_spmv_csr_{v}_{i}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, u64, vp)
     sig("lcpp_hip_scan_by_key_temp_bytes", sz, u64, sz, sz)
     sig("lcpp_hip_reduce_by_key_temp_bytes", sz, u64, sz, sz)
+    sig("lcpp_hip_scan_by_key_temp_bytes_policy", sz, u64, sz, sz, u32, u32)
+    sig("lcpp_hip_reduce_by_key_temp_bytes_policy", sz, u64, sz, sz, u32)
     sig("lcpp_hip_internal_by_key_needed_bytes", sz, u64, sz)
     for k in BY_KEY_KEY_SUFFIXES:
         for v in BY_KEY_VALUE_SUFFIXES:

@@ -2,7 +2,7 @@
 // luisa::parallel_primitive::{DeviceReduce, DeviceScan, DeviceRadixSort, DeviceSpmv} as a reference
 // user would call them (CommandList recording, commit on a Stream, host checks with std:: algorithms).
 //
-// Case sources: tests/device_reduce_test.cpp:95-173, tests/device_scan_test.cpp:80-321,
+// Case sources: tests/device_reduce_test.cpp:95-173,425-514, tests/device_scan_test.cpp:80-447,
 // tests/device_radix_sort_interface_test.cpp:68-283, tests/device_radix_sort_one_sweep.cpp:79-333,
 // tests/device_spmv_test.cpp:41-203 and the bench generators of tests/lcpp_cub_bench.cpp:516-521,
 // 666-672, 814.
@@ -450,6 +450,153 @@ void spmv_int_values_and_empty_work() {
     EXPECT(zeros == std::vector<int>(rows, 0));
 }
 
+// ---- by key -------------------------------------------------------------------------------------
+
+// tests/device_scan_test.cpp:323-377: keys i / 100, ones, for sizes 2^5 .. 2^20 (plus a ragged size).
+void scan_exclusive_sum_by_key_segments_of_100() {
+    auto& e = *g_env;
+    for (uint n : {32u, 100u, 4096u, 65536u, (1u << 20), (1u << 20) + 37u}) {
+        std::vector<int> keys(n), ones(n, 1), want(n);
+        for (uint i = 0; i < n; ++i) {
+            keys[i] = static_cast<int>(i / 100u);
+            want[i] = static_cast<int>(i % 100u);
+        }
+        auto kb = e.device.create_buffer<int>(n), vb = e.device.create_buffer<int>(n), ob = e.device.create_buffer<int>(n);
+        auto temp = e.device.create_buffer<uint>(
+            bytes_to_uint_count(DeviceScan<>::GetScanByKeyTempStorageBytes<int, int>(n)));
+        CommandList cmd;
+        e.scan.ExclusiveSumByKey(cmd, temp.view(), kb.view(), vb.view(), ob.view(), n);
+        std::vector<int> got(n, -1);
+        e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{ones}) << cmd.commit()
+                 << ob.copy_to(luisa::span{got}) << synchronize();
+        EXPECT(got == want);
+    }
+}
+
+// tests/device_scan_test.cpp:380-416: int keys, 64-bit values, runs crossing two 256 x 15 tiles.
+void scan_inclusive_sum_by_key_three_tiles_int64() {
+    auto& e = *g_env;
+    constexpr size_t tile = 256u * 15u;
+    constexpr size_t n = tile * 2u + 2u;
+    std::vector<int> keys(n);
+    std::vector<int64_t> ones(n, 1), want(n);
+    int64_t run = 0;
+    for (size_t i = 0; i < n; ++i) {
+        keys[i] = i < tile + 1u ? 1 : i < tile * 2u + 1u ? 2 : 3;
+        if (i == 0 || keys[i] != keys[i - 1]) run = 0;
+        want[i] = ++run;
+    }
+    auto kb = e.device.create_buffer<int>(n);
+    auto vb = e.device.create_buffer<int64_t>(n), ob = e.device.create_buffer<int64_t>(n);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceScan<>::GetScanByKeyTempStorageBytes<int, int64_t>(n)));
+    CommandList cmd;
+    e.scan.InclusiveSumByKey(cmd, temp.view(), kb.view(), vb.view(), ob.view(), n);
+    std::vector<int64_t> got(n, -1);
+    e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{ones}) << cmd.commit()
+             << ob.copy_to(luisa::span{got}) << synchronize();
+    EXPECT(got == want);
+}
+
+// tests/device_scan_test.cpp:419-447: keys equal when their parities match.
+void scan_by_key_custom_equality() {
+    auto& e = *g_env;
+    const std::vector<int> keys{1, 3, 5, 2, 4};
+    const std::vector<int> ones(keys.size(), 1);
+    auto kb = e.device.create_buffer<int>(keys.size()), vb = e.device.create_buffer<int>(keys.size());
+    auto ob = e.device.create_buffer<int>(keys.size());
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceScan<>::GetScanByKeyTempStorageBytes<int, int>(keys.size())));
+    CommandList cmd;
+    e.scan.InclusiveSumByKey(cmd, temp.view(), kb.view(), vb.view(), ob.view(), keys.size(), KeyMaskEquality{1u});
+    std::vector<int> got(keys.size(), -1);
+    e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{ones}) << cmd.commit()
+             << ob.copy_to(luisa::span{got}) << synchronize();
+    EXPECT((got == std::vector<int>{1, 2, 3, 1, 2}));
+}
+
+// ExclusiveScanByKey / InclusiveScanByKey with an initial value (device_scan.h:424-519), float
+// values holding small integers (exact sums) and 64-bit unsigned keys; the inclusive scan runs in place.
+void scan_by_key_initial_values_float_in_place() {
+    auto& e = *g_env;
+    const size_t n = 50000u;
+    std::vector<uint64_t> keys(n);
+    std::vector<float> vals(n), want_ex(n), want_in(n);
+    uint64_t key = 0;
+    float run = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        if (mix64(9, i) % 37u == 0u) ++key;
+        keys[i] = key * 0x100000001ull;
+        vals[i] = static_cast<float>(static_cast<int>(mix64(10, i) % 9u) - 4);
+        if (i == 0 || keys[i] != keys[i - 1]) run = 0.0f;
+        want_ex[i] = 2.5f + run;
+        run += vals[i];
+        want_in[i] = -1.0f + run;
+    }
+    auto kb = e.device.create_buffer<uint64_t>(n);
+    auto vb = e.device.create_buffer<float>(n), ob = e.device.create_buffer<float>(n);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceScan<>::GetScanByKeyTempStorageBytes<uint64_t, float>(n)));
+    CommandList cmd;
+    e.scan.ExclusiveScanByKey(cmd, temp.view(), kb.view(), vb.view(), ob.view(), SumOp{}, n, 2.5f);
+    std::vector<float> got_ex(n), got_in(n);
+    e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{vals}) << cmd.commit()
+             << ob.copy_to(luisa::span{got_ex}) << synchronize();
+    CommandList cmd2;
+    e.scan.InclusiveScanByKey(cmd2, temp.view(), kb.view(), vb.view(), vb.view(), SumOp{}, n, -1.0f);
+    e.stream << cmd2.commit() << vb.copy_to(luisa::span{got_in}) << synchronize();
+    EXPECT(got_ex == want_ex);
+    EXPECT(got_in == want_in);
+}
+
+// tests/device_reduce_test.cpp:425-480: keys i / 100 over 4096 items of value i.
+void reduce_by_key_segments_of_100() {
+    auto& e = *g_env;
+    for (uint n : {4096u, 1000003u}) {
+        const uint segments = (n + 99u) / 100u;
+        std::vector<int> keys(n), vals(n);
+        for (uint i = 0; i < n; ++i) {
+            keys[i] = static_cast<int>(i / 100u);
+            vals[i] = static_cast<int>(i % 1000u);
+        }
+        auto kb = e.device.create_buffer<int>(n), vb = e.device.create_buffer<int>(n);
+        auto ub = e.device.create_buffer<int>(segments), ab = e.device.create_buffer<int>(segments);
+        auto rb = e.device.create_buffer<uint>(1);
+        auto temp = e.device.create_buffer<uint>(
+            bytes_to_uint_count(DeviceReduce<>::GetReduceByKeyTempStorageBytes<int, int>(n)));
+        CommandList cmd;
+        e.reduce.ReduceByKey(cmd, temp.view(), kb.view(), vb.view(), ub.view(), ab.view(), rb.view(), SumOp{}, n);
+        std::vector<int> uniq(segments, -1), agg(segments, -1);
+        uint runs = 0;
+        e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{vals}) << cmd.commit()
+                 << ub.copy_to(luisa::span{uniq}) << ab.copy_to(luisa::span{agg}) << rb.copy_to(&runs)
+                 << synchronize();
+        EXPECT(runs == segments);
+        bool ok = true;
+        for (uint r = 0; r < segments; ++r) {
+            int sum = 0;
+            for (uint i = r * 100u; i < std::min(n, r * 100u + 100u); ++i) sum += vals[i];
+            ok = ok && uniq[r] == static_cast<int>(r) && agg[r] == sum;
+        }
+        EXPECT(ok);
+    }
+}
+
+// tests/device_reduce_test.cpp:483-513: empty input writes zero runs.
+void reduce_by_key_empty_input() {
+    auto& e = *g_env;
+    auto kb = e.device.create_buffer<int>(1), vb = e.device.create_buffer<int>(1);
+    auto ub = e.device.create_buffer<int>(1), ab = e.device.create_buffer<int>(1);
+    auto rb = e.device.create_buffer<uint>(1);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceReduce<>::GetReduceByKeyTempStorageBytes<int, int>(0u)));
+    uint runs = 17u;
+    CommandList cmd;
+    e.reduce.ReduceByKey(cmd, temp.view(), kb.view(), vb.view(), ub.view(), ab.view(), rb.view(), SumOp{}, 0u);
+    e.stream << rb.copy_from(&runs) << cmd.commit() << rb.copy_to(&runs) << synchronize();
+    EXPECT(runs == 0u);
+}
+
 // ---- record-time checks ------------------------------------------------------------------------
 
 void precondition_errors() {
@@ -460,6 +607,12 @@ void precondition_errors() {
     CommandList cmd;
     EXPECT(throws_error([&] { e.scan.ExclusiveSum(cmd, small.view(), a.view(), a.view(), n); }));
     EXPECT(throws_error([&] { e.reduce.Sum(cmd, small.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error([&] { e.scan.ExclusiveSumByKey(cmd, small.view(), a.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error(
+        [&] { e.reduce.ReduceByKey(cmd, small.view(), a.view(), a.view(), a.view(), a.view(), small.view(), SumOp{}, n); }));
+    EXPECT(throws_error([&] {
+        e.reduce.ReduceByKey(cmd, small.view(), a.view(), a.view(), a.view(), a.view(), BufferView<uint>{}, SumOp{}, 0u);
+    }));
     EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), n); }));
     EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 5u, 3u); }));
     EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 0u, 33u); }));
@@ -487,6 +640,12 @@ const std::vector<Case>& cases() {
         {"radix_double_buffer_zero_width_keeps_current", radix_double_buffer_zero_width_keeps_current},
         {"radix_large_keys_and_pairs", radix_large_keys_and_pairs},
         {"radix_float_and_signed_keys", radix_float_and_signed_keys},
+        {"scan_exclusive_sum_by_key_segments_of_100", scan_exclusive_sum_by_key_segments_of_100},
+        {"scan_inclusive_sum_by_key_three_tiles_int64", scan_inclusive_sum_by_key_three_tiles_int64},
+        {"scan_by_key_custom_equality", scan_by_key_custom_equality},
+        {"scan_by_key_initial_values_float_in_place", scan_by_key_initial_values_float_in_place},
+        {"reduce_by_key_segments_of_100", reduce_by_key_segments_of_100},
+        {"reduce_by_key_empty_input", reduce_by_key_empty_input},
         {"spmv_float_unsigned_indices", spmv_float_unsigned_indices},
         {"spmv_int_values_and_empty_work", spmv_int_values_and_empty_work},
         {"precondition_errors", precondition_errors},

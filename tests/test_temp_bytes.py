@@ -118,3 +118,26 @@ def test_by_key_kernels_fit_reference_temp(hip, kb, vb):
         need = lib.lcpp_hip_internal_by_key_needed_bytes(n, vb)
         assert need <= lib.lcpp_hip_scan_by_key_temp_bytes(n, kb, vb)
         assert need <= lib.lcpp_hip_reduce_by_key_temp_bytes(n, kb, vb)
+
+
+def test_by_key_temp_bytes_policies(hip):
+    """Policy queries: the default tiles reproduce the default queries; a smaller tile gives the
+    reference formula (DeviceScan<128, 32, 8>, n = 10000: tiles = ceil(10000 / 1024) = 10,
+    tile_count = 42: 168 -> 256; + 336 = 592 -> 768; + 336 = 1104 -> 1280; + 40 = 1320;
+    DeviceReduce<128>: tiles = ceil(10000 / 512) = 20, tile_count = 52: 208 -> 256; + 416 = 672 -> 768;
+    + 416 = 1184); tiles so large that the reference layout is smaller than the kernel's tile states
+    are raised to the kernel's need."""
+    lib = hip.lib()
+    for n in (0, 1, 3840, 10000, 1 << 20, (1 << 32) - 1):
+        for kb, vb in ((4, 4), (8, 8), (4, 8)):
+            assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(n, kb, vb, 256, 15) == \
+                lib.lcpp_hip_scan_by_key_temp_bytes(n, kb, vb)
+            assert lib.lcpp_hip_reduce_by_key_temp_bytes_policy(n, kb, vb, 256) == \
+                lib.lcpp_hip_reduce_by_key_temp_bytes(n, kb, vb)
+    assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(10000, 4, 4, 128, 8) == 1320
+    assert lib.lcpp_hip_reduce_by_key_temp_bytes_policy(10000, 4, 4, 128) == 1184
+    for n in (1 << 20, (1 << 28) + 5):
+        need = lib.lcpp_hip_internal_by_key_needed_bytes(n, 8)
+        assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(n, 4, 8, 1024, 64) == need
+        assert lib.lcpp_hip_reduce_by_key_temp_bytes_policy(n, 4, 8, 8192) == need
+    assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(100, 4, 4, 0, 15) == 0
