@@ -227,6 +227,108 @@ LCPP_HIP_DECLARE_BY_KEY_VALUES(u64, uint64_t)
 #undef LCPP_HIP_DECLARE_BY_KEY
 
 /* ---------------------------------------------------------------------------------------------
+ * Stream compaction: DeviceSelect, DevicePartition, DeviceRunLengthEncode.
+ * Replaces DeviceSelect<>::Flagged / If / FlaggedIf / Unique / UniqueByKey (device_select.h:65-344,
+ * temp query :56-63), DevicePartition<>::Flagged / If / three-way If (device_partition.h:73-209, temp
+ * queries :55-71) and DeviceRunLengthEncode<>::Encode / NonTrivialRuns (device_run_length_encode.h:
+ * 56-153).  Semantics as the reference: selected items keep their order and *num_selected_out
+ * receives their count; partition writes the rejected items after them in reverse order
+ * (out[n - 1 - j] for the j-th reject, device_partition.h:530-579); the three-way partition writes the
+ * first and second categories in order and the unselected items reversed within their own output,
+ * with num_selected_out[0..1] = the two category sizes (:581-663); Unique / UniqueByKey keep the
+ * first item (key and value) of every run of equal items; Encode writes each run's value and length,
+ * NonTrivialRuns the offset and length of every run longer than one item (CUB's conventions).
+ * n == 0 writes zero counts.  Selects whose output overlaps their input or flags are the in-place
+ * forms (device_select.h:106-117,160-175,201-212,226-265).
+ *
+ * The reference's predicates and equalities are device lambdas.  Here a predicate is two clauses
+ * that must both hold (op[c] with operands a[c], b[c], given as the bits of values of the item or
+ * flag type in the low bytes); flags select when != 0; adjacent keys are equal when
+ * ((x ^ y) & key_mask) == 0 for integers, and by value (x == y) for floats, as lhs == rhs is.
+ * Item suffixes T: i32 u32 f32 i64 u64 f64; flag suffixes F: b8 (bool / uint8) i32 u32 i64 u64.
+ * ------------------------------------------------------------------------------------------- */
+#define LCPP_HIP_PRED_TRUE 0     /* always                                   */
+#define LCPP_HIP_PRED_LT 1       /* x <  a                                   */
+#define LCPP_HIP_PRED_LE 2       /* x <= a                                   */
+#define LCPP_HIP_PRED_GT 3       /* x >  a                                   */
+#define LCPP_HIP_PRED_GE 4       /* x >= a                                   */
+#define LCPP_HIP_PRED_EQ 5       /* x == a                                   */
+#define LCPP_HIP_PRED_NE 6       /* x != a                                   */
+#define LCPP_HIP_PRED_RANGE 7    /* a <= x && x < b                          */
+#define LCPP_HIP_PRED_MASK_EQ 8  /* (bits(x) & bits(a)) == bits(b)           */
+#define LCPP_HIP_PRED_MASK_NE 9  /* (bits(x) & bits(a)) != bits(b)           */
+#define LCPP_HIP_PRED_MOD_EQ 10  /* x % a == b (integers, C remainder; a != 0) */
+#define LCPP_HIP_PRED_MOD_NE 11  /* x % a != b                               */
+typedef struct lcpp_hip_predicate {
+    int32_t op[2];
+    uint64_t a[2];
+    uint64_t b[2];
+} lcpp_hip_predicate;
+
+/* DeviceSelect<BLOCK, 32, ITEMS>::GetTempStorageBytes (and DevicePartition's, the same formula):
+ * 0 for n == 0, else 8 n + DeviceScan<BLOCK, 32, ITEMS>::GetTempStorageBytes<uint>(n); three-way
+ * 12 n + that; DeviceRunLengthEncode: align256(4 (6 n + 1)) + that.  The *_policy forms take the
+ * module's BLOCK_SIZE and ITEMS_PER_THREAD (defaults 256 and 4, runtime/core.h:17-23) and are raised
+ * to the kernels' need where a policy's scan layout would be smaller. */
+size_t lcpp_hip_select_temp_bytes(uint64_t n);
+size_t lcpp_hip_select_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread);
+size_t lcpp_hip_partition_three_way_temp_bytes(uint64_t n);
+size_t lcpp_hip_partition_three_way_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread);
+size_t lcpp_hip_run_length_encode_temp_bytes(uint64_t n);
+size_t lcpp_hip_run_length_encode_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread);
+
+#define LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, FS, FT)                                                               \
+    int lcpp_hip_select_flagged_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags, TT* out, \
+                                            uint32_t* num_selected_out, uint64_t n, void* stream);                \
+    int lcpp_hip_select_flagged_if_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags,      \
+                                               TT* out, uint32_t* num_selected_out, uint64_t n,                   \
+                                               const lcpp_hip_predicate* pred, void* stream);                     \
+    int lcpp_hip_partition_flagged_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags,      \
+                                               TT* out, uint32_t* num_selected_out, uint64_t n, void* stream);
+#define LCPP_HIP_DECLARE_SELECT_ITEMS(TS, TT)                                                                        \
+    int lcpp_hip_select_if_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out, uint32_t* num_selected_out,  \
+                                uint64_t n, const lcpp_hip_predicate* pred, void* stream);                         \
+    int lcpp_hip_partition_if_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                           \
+                                   uint32_t* num_selected_out, uint64_t n, const lcpp_hip_predicate* pred,          \
+                                   void* stream);                                                                   \
+    int lcpp_hip_partition_three_way_##TS(void* temp, size_t temp_bytes, const TT* in, TT* first_out,              \
+                                          TT* second_out, TT* unselected_out, uint32_t* num_selected_out,           \
+                                          uint64_t n, const lcpp_hip_predicate* select_first,                      \
+                                          const lcpp_hip_predicate* select_second, void* stream);                  \
+    int lcpp_hip_select_unique_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                          \
+                                    uint32_t* num_selected_out, uint64_t n, uint64_t key_mask, void* stream);      \
+    int lcpp_hip_run_length_encode_##TS(void* temp, size_t temp_bytes, const TT* in, TT* unique_out,               \
+                                        uint32_t* counts_out, uint32_t* num_runs_out, uint64_t n, void* stream);   \
+    int lcpp_hip_run_length_non_trivial_##TS(void* temp, size_t temp_bytes, const TT* in, uint32_t* offsets_out,   \
+                                             uint32_t* lengths_out, uint32_t* num_runs_out, uint64_t n,             \
+                                             void* stream);                                                         \
+    LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, b8, uint8_t)                                                               \
+    LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, i32, int32_t)                                                              \
+    LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, u32, uint32_t)                                                             \
+    LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, i64, int64_t)                                                              \
+    LCPP_HIP_DECLARE_SELECT_FLAGS(TS, TT, u64, uint64_t)                                                             \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, i32, int32_t)                                                             \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, u32, uint32_t)                                                            \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, f32, float)                                                               \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, i64, int64_t)                                                             \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, u64, uint64_t)                                                            \
+    LCPP_HIP_DECLARE_UNIQUE_BY_KEY(TS, TT, f64, double)
+#define LCPP_HIP_DECLARE_UNIQUE_BY_KEY(KS, KT, VS, VT)                                                               \
+    int lcpp_hip_select_unique_by_key_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in,                \
+                                                  const VT* values_in, KT* keys_out, VT* values_out,                \
+                                                  uint32_t* num_selected_out, uint64_t n, uint64_t key_mask,        \
+                                                  void* stream);
+LCPP_HIP_DECLARE_SELECT_ITEMS(i32, int32_t)
+LCPP_HIP_DECLARE_SELECT_ITEMS(u32, uint32_t)
+LCPP_HIP_DECLARE_SELECT_ITEMS(f32, float)
+LCPP_HIP_DECLARE_SELECT_ITEMS(i64, int64_t)
+LCPP_HIP_DECLARE_SELECT_ITEMS(u64, uint64_t)
+LCPP_HIP_DECLARE_SELECT_ITEMS(f64, double)
+#undef LCPP_HIP_DECLARE_UNIQUE_BY_KEY
+#undef LCPP_HIP_DECLARE_SELECT_ITEMS
+#undef LCPP_HIP_DECLARE_SELECT_FLAGS
+
+/* ---------------------------------------------------------------------------------------------
  * Seeded synthetic workloads for tests and benchmarks (no reference counterpart; the reference
  * generates on the host, e.g. tests/lcpp_cub_bench.cpp:516-521,666-672,814).
  * Stream: splitmix64, r_i = mix(seed + (start + i + 1) * 0x9E3779B97F4A7C15).
@@ -252,6 +354,7 @@ uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t v
                                           uint32_t end_bit, int double_buffer, size_t temp_bytes);
 int lcpp_hip_internal_radix_rank_mode(int mode);
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);
+size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int words, int staged);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

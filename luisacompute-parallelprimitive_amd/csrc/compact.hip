@@ -1,0 +1,934 @@
+// DeviceSelect (Flagged, If, FlaggedIf, Unique, UniqueByKey; copy and in-place forms),
+// DevicePartition (Flagged, If, three-way If) and DeviceRunLengthEncode (Encode, NonTrivialRuns) for
+// gfx950: single-pass stream compaction over a decoupled look-back of per-tile selection counts.
+//
+// Reference paths (src/lcpp/device/): DeviceSelect<> (device_select.h:65-344: flags or predicate ->
+// DeviceScan<>::ExclusiveSum of the selection flags -> scatter, count written by the last item),
+// DevicePartition<> (device_partition.h:73-209: selected items in order at the front, rejected items
+// in reverse order from the back, :530-579; three-way: first and second categories in order, the
+// unselected items reversed within their own output, :581-663), DeviceRunLengthEncode<>
+// (device_run_length_encode.h:71-153: unique values with run lengths; offsets and lengths of the runs
+// longer than one item).  The reference runs each as flag, scan and scatter kernels over n-sized
+// temp arrays; its predicates and equalities are device lambdas compiled at run time.
+//
+// Selection vocabulary here: a predicate is two clauses that must both hold, each comparing the
+// item with operands (<, <=, >, >=, ==, !=, a half-open range, a C remainder test, a bit-mask test);
+// flags select when != 0; adjacent keys are equal under a bit mask (integers) or by value (floats,
+// where -0.0 == +0.0 and NaN differs from everything, like the reference's lhs == rhs).
+//
+// MI355X design
+//   * One workgroup of 256 threads per tile; each thread holds 128 bytes of consecutive items (32
+//     four-byte or 16 eight-byte items; 16-byte vector loads when aligned), so a tile is 8,192 or
+//     4,096 items and every thread's selection fits in a 32-bit mask.
+//   * Per-thread counts (W = 1 or 2 words) are scanned across the tile with DPP and LDS; the tile
+//     publishes its aggregate, wave 0 walks back 64 predecessor tiles per step to the newest
+//     INCLUSIVE state, and the tile publishes INCLUSIVE.  Tile states are 64-bit words (status in the
+//     low half, count in the high half) read with agent-scope relaxed atomics; a multi-word state is
+//     accepted only when all its words show the same status.  A predecessor still unpublished after
+//     `spin_limit` polls is claimed (a claim word per tile) and counted by the waiting workgroup with
+//     the owner's own code; the owner waits for such a helper to finish before publishing INCLUSIVE.
+//   * Selected items are staged in LDS at their rank within the tile, then written with coalesced
+//     stores to out[prefix + q]; rejected items (partition) follow them in LDS and are written
+//     backwards from the end.  Run-length outputs (one store per run) are written directly.
+//   * Run lengths come from a second state word combined by max: the position of the last run head
+//     before each item, so a run crossing any number of tiles needs no second pass.
+//   * In-place selects (output overlapping the input or the flags) compact into temp storage and
+//     copy the selected prefix back; the three-way partition stages its unselected items in temp
+//     storage and reverses them into their output in a second small kernel.
+// Algorithmic traffic: select / partition n*(sizeof(T) [+ sizeof(F)]) read + selected (or n) items
+// written; run-length encode n*sizeof(T) read + runs*(sizeof(T) + 4) written.
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+#include <cstring>
+
+namespace lcpp_hip {
+namespace {
+
+constexpr int kCpBlock = 256;
+constexpr int kCpWaves = kCpBlock / kWave;
+
+constexpr uint32_t kStInvalid = 0;
+constexpr uint32_t kStPartial = 1;
+constexpr uint32_t kStInclusive = 2;
+constexpr uint32_t kStatusMask = 3;
+
+constexpr uint64_t kClaimOpen = 0;    // nobody has closed or claimed the tile yet
+constexpr uint64_t kClaimOwned = 1;   // the owner closed it
+constexpr uint64_t kClaimHelper = 2;  // a helper is counting the tile
+constexpr uint64_t kClaimDone = 3;    // the helper's PARTIAL stores have all been performed
+
+constexpr uint32_t kActDone = 0;
+constexpr uint32_t kActAdvance = 1;
+constexpr uint32_t kActWait = 2;
+constexpr uint32_t kActHelp = 3;
+
+enum : int {
+    kSelect = 0,       // items (or flags) tested by a predicate; optional partition of the rejects
+    kThreeWay = 1,     // first / second / unselected categories
+    kUnique = 2,       // first item of every run of equal items
+    kUniqueByKey = 3,  // first (key, value) of every run of equal keys
+    kEncode = 4,       // unique values and run lengths
+    kNonTrivial = 5,   // offsets and lengths of runs longer than one item
+};
+
+template <int MODE>
+constexpr int kWords = (MODE == kThreeWay || MODE == kEncode || MODE == kNonTrivial) ? 2 : 1;
+// Word 1 of the run-length modes is the position of the last run head, combined by max.
+template <int MODE>
+constexpr bool kWord1Max = MODE == kEncode || MODE == kNonTrivial;
+
+template <typename U, typename V>
+constexpr int kCpItems = static_cast<int>(128 / (sizeof(U) > sizeof(V) ? sizeof(U) : sizeof(V)));
+
+template <typename P>
+struct Clause {
+    int32_t op;
+    P a;
+    P b;
+};
+
+template <typename P>
+struct Predicate {
+    Clause<P> c[2];
+};
+
+template <typename T>
+using Bits = std::conditional_t<sizeof(T) == 8, uint64_t, std::conditional_t<sizeof(T) == 4, uint32_t, uint8_t>>;
+
+// Bit k set when clause `c` holds for x[k].  The switch is uniform (a kernel argument), so each
+// thread runs one branch over all of its items.
+template <typename P, int N>
+__device__ __forceinline__ uint32_t clause_bits(const Clause<P>& c, const P (&x)[N]) {
+    uint32_t bits = 0;
+#define LCPP_CLAUSE(OP, EXPR)                                               \
+    case OP: {                                                              \
+        _Pragma("unroll") for (int k = 0; k < N; ++k) {                     \
+            const P v = x[k];                                               \
+            bits |= ((EXPR) ? 1u : 0u) << k;                                \
+        }                                                                   \
+        return bits;                                                        \
+    }
+    switch (c.op) {
+        LCPP_CLAUSE(LCPP_HIP_PRED_LT, v < c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_LE, v <= c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_GT, v > c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_GE, v >= c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_EQ, v == c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_NE, v != c.a)
+        LCPP_CLAUSE(LCPP_HIP_PRED_RANGE, c.a <= v && v < c.b)
+        LCPP_CLAUSE(LCPP_HIP_PRED_MASK_EQ, (__builtin_bit_cast(Bits<P>, v) & __builtin_bit_cast(Bits<P>, c.a)) ==
+                                               __builtin_bit_cast(Bits<P>, c.b))
+        LCPP_CLAUSE(LCPP_HIP_PRED_MASK_NE, (__builtin_bit_cast(Bits<P>, v) & __builtin_bit_cast(Bits<P>, c.a)) !=
+                                               __builtin_bit_cast(Bits<P>, c.b))
+        default:
+            break;
+    }
+    if constexpr (std::is_integral_v<P>) {
+        switch (c.op) {
+            LCPP_CLAUSE(LCPP_HIP_PRED_MOD_EQ, v % c.a == c.b)
+            LCPP_CLAUSE(LCPP_HIP_PRED_MOD_NE, v % c.a != c.b)
+            default:
+                break;
+        }
+    }
+#undef LCPP_CLAUSE
+    return c.op == LCPP_HIP_PRED_TRUE ? ~0u : 0u;
+}
+
+template <typename K>
+__device__ __forceinline__ bool keys_equal(K a, K b, uint64_t mask) {
+    if constexpr (std::is_floating_point_v<K>) {
+        return a == b;
+    } else {
+        return ((a ^ b) & static_cast<K>(mask)) == 0;
+    }
+}
+
+template <typename T, int N>
+struct alignas(16) Vec {
+    T v[N];
+};
+
+// Items [first, first + N) of p (0 past n): vector loads when `vec` (p 16-byte aligned).
+template <typename T, int N>
+__device__ __forceinline__ void load_run(const T* p, uint64_t first, uint64_t n, bool vec, T (&out)[N]) {
+    if (vec && first + N <= n) {
+        const Vec<T, N> r = *reinterpret_cast<const Vec<T, N>*>(p + first);
+#pragma unroll
+        for (int k = 0; k < N; ++k) out[k] = r.v[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < N; ++k) out[k] = first + k < n ? p[first + k] : T(0);
+    }
+}
+
+template <typename U, typename P, typename V>
+struct CompactArgs {
+    const U* in;          // items (keys for unique-by-key)
+    const P* flags;       // selection flags (flagged forms)
+    const V* values_in;   // unique-by-key values
+    U* out;               // selected / first category / unique items or keys
+    U* out2;              // three-way: second category
+    U* out3;              // three-way: unselected items in order (temp staging)
+    V* values_out;        // unique-by-key values
+    uint32_t* aux0;       // run-length encode: counts; non-trivial runs: offsets
+    uint32_t* aux1;       // non-trivial runs: lengths
+    uint32_t* num_out;    // selected count(s)
+    uint64_t* states;     // tiles x W state words, then one claim word per tile
+    uint64_t n;
+    uint64_t key_mask;
+    Predicate<P> pred;    // select / flagged-if / three-way first
+    Predicate<P> pred2;   // three-way second
+    uint32_t spin_limit;
+    bool partition;       // select: write the rejected items backwards after the selected ones
+    bool vec_in;
+    bool vec_flags;
+    bool vec_values;
+};
+
+template <typename U, typename V, int ITEMS>
+struct ThreadItems {
+    U x[ITEMS];
+    V v[ITEMS];
+    uint32_t sel;    // selected / first category / run heads / non-trivial run starts
+    uint32_t sel2;   // three-way second category / run ends / non-trivial run ends
+    uint32_t heads;  // run heads (run-length modes)
+};
+
+template <int ITEMS>
+__device__ __forceinline__ uint32_t valid_mask(uint64_t first, uint64_t n) {
+    if (first >= n) return 0u;
+    const uint64_t left = n - first;
+    if (left >= static_cast<uint64_t>(ITEMS)) return ITEMS == 32 ? ~0u : ((1u << ITEMS) - 1u);
+    return (1u << left) - 1u;
+}
+
+// Loads a thread's items and computes its selection masks.
+template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS>
+__device__ __forceinline__ void load_thread(const CompactArgs<U, P, V>& a, uint64_t first, ThreadItems<U, V, ITEMS>& t) {
+    const uint32_t valid = valid_mask<ITEMS>(first, a.n);
+    load_run<U, ITEMS>(a.in, first, a.n, a.vec_in, t.x);
+    t.sel2 = 0;
+    t.heads = 0;
+    if constexpr (MODE == kSelect || MODE == kThreeWay) {
+        uint32_t s1, s2 = 0;
+        if constexpr (FLAGS) {
+            P f[ITEMS];
+            load_run<P, ITEMS>(a.flags, first, a.n, a.vec_flags, f);
+            s1 = clause_bits(a.pred.c[0], f) & clause_bits(a.pred.c[1], f);
+        } else {
+            s1 = clause_bits(a.pred.c[0], t.x) & clause_bits(a.pred.c[1], t.x);
+            if constexpr (MODE == kThreeWay) s2 = clause_bits(a.pred2.c[0], t.x) & clause_bits(a.pred2.c[1], t.x);
+        }
+        t.sel = s1 & valid;
+        t.sel2 = s2 & ~s1 & valid;
+    } else {
+        if constexpr (MODE == kUniqueByKey) load_run<V, ITEMS>(a.values_in, first, a.n, a.vec_values, t.v);
+        U prev = first > 0 && first - 1 < a.n ? a.in[first - 1] : t.x[0];
+        uint32_t heads = 0;
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const bool head = (first + k == 0) || !keys_equal(t.x[k], prev, a.key_mask);
+            heads |= (head ? 1u : 0u) << k;
+            prev = t.x[k];
+        }
+        heads &= valid;
+        t.heads = heads;
+        if constexpr (MODE == kUnique || MODE == kUniqueByKey) {
+            t.sel = heads;
+        } else {
+            // Heads of the following items: bit k is the head flag of item first + k + 1.
+            const uint64_t next_i = first + ITEMS;
+            const bool next_head = next_i < a.n && !keys_equal(a.in[next_i], t.x[ITEMS - 1], a.key_mask);
+            const uint32_t next_heads = (heads >> 1) | ((next_head ? 1u : 0u) << (ITEMS - 1));
+            // Bit of the input's last item, if this thread holds it.
+            const uint32_t last = (first < a.n && a.n - first <= static_cast<uint64_t>(ITEMS))
+                                      ? (1u << (a.n - first - 1))
+                                      : 0u;
+            const uint32_t ends = valid & (next_heads | last);
+            if constexpr (MODE == kEncode) {
+                t.sel = heads;
+                t.sel2 = ends;
+            } else {
+                t.sel = heads & ~ends;   // a head whose run continues: a run longer than one item
+                t.sel2 = ends & ~heads;  // the end of such a run
+            }
+        }
+    }
+}
+
+struct MaxU32Op {
+    __device__ __forceinline__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+    template <typename T>
+    __device__ __forceinline__ static constexpr T identity() { return T(0); }
+};
+
+template <int MODE>
+__device__ __forceinline__ uint32_t combine_word(int w, uint32_t older, uint32_t newer) {
+    if (kWord1Max<MODE> && w == 1) return older > newer ? older : newer;
+    return older + newer;
+}
+
+// The thread's count words: selected items (and second category), or run heads / non-trivial starts
+// and the position of the thread's last run head (0 when it has none).
+template <int MODE, typename U, typename V, int ITEMS>
+__device__ __forceinline__ void thread_words(const ThreadItems<U, V, ITEMS>& t, uint64_t first, uint32_t (&w)[kWords<MODE>]) {
+    w[0] = static_cast<uint32_t>(__builtin_popcount(t.sel));
+    if constexpr (MODE == kThreeWay) {
+        w[1] = static_cast<uint32_t>(__builtin_popcount(t.sel2));
+    } else if constexpr (kWord1Max<MODE>) {
+        w[1] = t.heads ? static_cast<uint32_t>(first + 31 - __builtin_clz(t.heads)) : 0u;
+    }
+}
+
+// Exclusive prefix of each thread's words within the tile, and the tile aggregate.  Called by every
+// thread; barriers on both sides of the use of s_wave.
+template <int MODE>
+__device__ __forceinline__ void block_scan_words(const uint32_t (&x)[kWords<MODE>],
+                                                 uint32_t (*s_wave)[kCpWaves], uint32_t (&ex)[kWords<MODE>],
+                                                 uint32_t (&agg)[kWords<MODE>]) {
+    constexpr int W = kWords<MODE>;
+    const uint32_t wave = threadIdx.x / kWave;
+    uint32_t inc[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        if (kWord1Max<MODE> && w == 1) {
+            inc[w] = wave_inclusive_scan(x[w], MaxU32Op{});
+            ex[w] = wave_shift_exclusive<uint32_t, MaxU32Op>(inc[w]);
+        } else {
+            inc[w] = wave_inclusive_scan(x[w], SumOp{});
+            ex[w] = wave_shift_exclusive<uint32_t, SumOp>(inc[w]);
+        }
+    }
+    __syncthreads();
+    if (lane_id() == kWave - 1) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) s_wave[w][wave] = inc[w];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        uint32_t prefix = 0, total = 0;
+#pragma unroll
+        for (int j = 0; j < kCpWaves; ++j) {
+            if (static_cast<uint32_t>(j) == wave) prefix = total;
+            total = combine_word<MODE>(w, total, s_wave[w][j]);
+        }
+        ex[w] = combine_word<MODE>(w, prefix, ex[w]);
+        agg[w] = total;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void publish_words(uint64_t* slot, uint32_t status, const uint32_t (&v)[W]) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) atomic_store_agent(&slot[w], (static_cast<uint64_t>(v[w]) << 32) | status);
+}
+
+// Status of a tile state if all its words carry the same published status, else kStInvalid.
+template <int W>
+__device__ __forceinline__ uint32_t read_words(const uint64_t* slot, uint32_t (&v)[W]) {
+    uint64_t s[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) s[w] = atomic_load_agent(&slot[w]);
+    const uint32_t st = static_cast<uint32_t>(s[0]) & kStatusMask;
+    bool ok = st == kStPartial || st == kStInclusive;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        ok = ok && (static_cast<uint32_t>(s[w]) & kStatusMask) == st;
+        v[w] = static_cast<uint32_t>(s[w] >> 32);
+    }
+    return ok ? st : kStInvalid;
+}
+
+// Aggregate words of tile `tile`, computed by the whole workgroup exactly as its owner computes them.
+template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS>
+__device__ void tile_aggregate(const CompactArgs<U, P, V>& a, uint32_t tile, uint32_t (*s_wave)[kCpWaves],
+                               uint32_t (&agg)[kWords<MODE>]) {
+    constexpr uint64_t kTile = static_cast<uint64_t>(kCpBlock) * ITEMS;
+    const uint64_t first = static_cast<uint64_t>(tile) * kTile + static_cast<uint64_t>(threadIdx.x) * ITEMS;
+    ThreadItems<U, V, ITEMS> t;
+    load_thread<U, P, V, MODE, FLAGS, ITEMS>(a, first, t);
+    uint32_t w[kWords<MODE>], ex[kWords<MODE>];
+    thread_words<MODE>(t, first, w);
+    block_scan_words<MODE>(w, s_wave, ex, agg);
+}
+
+template <typename U, typename P, typename V, int MODE, bool FLAGS>
+__global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, P, V> a) {
+    constexpr int ITEMS = kCpItems<U, V>;
+    constexpr int W = kWords<MODE>;
+    constexpr uint64_t kTile = static_cast<uint64_t>(kCpBlock) * ITEMS;
+    constexpr size_t kStageBytes = kTile * (sizeof(U) > sizeof(V) ? sizeof(U) : sizeof(V));
+    constexpr uint32_t kPublisher = kCpBlock - kWave;
+    __shared__ __align__(16) unsigned char s_stage[kStageBytes];
+    __shared__ uint32_t s_wave[W][kCpWaves];
+    __shared__ uint32_t s_ctl[2][2];
+    __shared__ uint32_t s_prefix[W];
+
+    uint64_t* const states = a.states;
+    uint64_t* const claims = states + static_cast<uint64_t>(gridDim.x) * W;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint32_t tile = blockIdx.x;
+    const uint64_t tile_first = static_cast<uint64_t>(tile) * kTile;
+    const uint64_t first = tile_first + static_cast<uint64_t>(tid) * ITEMS;
+
+    ThreadItems<U, V, ITEMS> t;
+    load_thread<U, P, V, MODE, FLAGS, ITEMS>(a, first, t);
+    uint32_t words[W], ex[W], agg[W];
+    thread_words<MODE>(t, first, words);
+    block_scan_words<MODE>(words, s_wave, ex, agg);
+
+    uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
+    bool owned = true;
+    if (tid == kPublisher) {
+        publish_words<W>(my_slot, tile == 0 ? kStInclusive : kStPartial, agg);
+        uint64_t expected = kClaimOpen;
+        owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    uint32_t prefix[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) prefix[w] = 0;
+    if (tile > 0) {
+        int64_t top = static_cast<int64_t>(tile) - 1;
+        uint32_t acc[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc[w] = 0;
+        uint32_t spins = 0;
+        uint32_t row = 0;
+        while (true) {
+            if (wave == 0) {
+                const int64_t j = top - static_cast<int64_t>(lane);
+                uint32_t v[W];
+                const uint32_t st = j >= 0 ? read_words<W>(states + static_cast<uint64_t>(j) * W, v) : kStInvalid;
+                const bool exists = j >= 0;
+                const bool published = st != kStInvalid;
+                const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
+                const uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
+                const uint64_t upto = cut >= kWave - 1 ? ~0ull : ((2ull << cut) - 1);
+                const uint64_t missing = upto & wave_ballot(exists) & ~wave_ballot(published);
+                uint32_t action;
+                uint32_t help_tile = 0;
+                if (missing) {
+                    if (spins >= a.spin_limit) {
+                        action = kActHelp;
+                        help_tile = static_cast<uint32_t>(top - __builtin_ctzll(missing));
+                    } else {
+                        action = kActWait;
+                    }
+                } else {
+                    const bool take = exists && lane <= cut;
+#pragma unroll
+                    for (int w = 0; w < W; ++w) {
+                        const uint32_t mine = take ? v[w] : 0u;
+                        const uint32_t window = (kWord1Max<MODE> && w == 1) ? wave_reduce(mine, MaxU32Op{})
+                                                                           : wave_reduce(mine, SumOp{});
+                        acc[w] = combine_word<MODE>(w, window, acc[w]);
+                    }
+                    const bool complete = stop_mask != 0;
+                    action = (complete || top < kWave) ? kActDone : kActAdvance;
+                }
+                if (lane == 0) {
+                    s_ctl[row][0] = action;
+                    s_ctl[row][1] = help_tile;
+                    if (action == kActDone) {
+#pragma unroll
+                        for (int w = 0; w < W; ++w) s_prefix[w] = acc[w];
+                    }
+                }
+            }
+            __syncthreads();
+            const uint32_t action = s_ctl[row][0];
+            const uint32_t help_tile = s_ctl[row][1];
+            row ^= 1u;
+            if (action == kActDone) break;
+            if (action == kActAdvance) {
+                top -= kWave;
+                spins = 0;
+                continue;
+            }
+            if (action == kActWait) {
+                __builtin_amdgcn_s_sleep(1);
+                ++spins;
+                continue;
+            }
+            // kActHelp: claim the unpublished predecessor, count it, publish it PARTIAL and mark the
+            // claim DONE with release ordering.
+            if (tid == 0) {
+                uint64_t expected = kClaimOpen;
+                s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&claims[help_tile], &expected, kClaimHelper,
+                                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT)
+                                    ? 1u
+                                    : 0u;
+            }
+            __syncthreads();
+            const bool claimed = s_ctl[row][0] != 0;
+            row ^= 1u;
+            if (claimed) {
+                uint32_t h[W];
+                tile_aggregate<U, P, V, MODE, FLAGS, ITEMS>(a, help_tile, s_wave, h);
+                if (tid == 0) {
+                    publish_words<W>(states + static_cast<uint64_t>(help_tile) * W, kStPartial, h);
+                    __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            spins = 0;
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) prefix[w] = s_prefix[w];
+    }
+
+    if (tid == kPublisher) {
+        if (!owned) {
+            while (__hip_atomic_load(&claims[tile], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != kClaimDone)
+                __builtin_amdgcn_s_sleep(1);
+        }
+        if (tile > 0 || !owned) {
+            uint32_t incl[W];
+#pragma unroll
+            for (int w = 0; w < W; ++w) incl[w] = combine_word<MODE>(w, prefix[w], agg[w]);
+            publish_words<W>(my_slot, kStInclusive, incl);
+        }
+    }
+    if (tile + 1 == gridDim.x && tid == 0) {
+        a.num_out[0] = prefix[0] + agg[0];
+        if constexpr (MODE == kThreeWay) a.num_out[1] = prefix[1] + agg[1];
+    }
+
+    // ---- outputs ------------------------------------------------------------------------------
+    const uint64_t tile_valid = a.n - tile_first < kTile ? a.n - tile_first : kTile;
+    const uint32_t local0 = tid * ITEMS;  // tile-local index of the thread's first item
+    U* const stage = reinterpret_cast<U*>(s_stage);
+
+    if constexpr (MODE == kEncode || MODE == kNonTrivial) {
+        uint32_t count = prefix[0] + ex[0];  // heads (encode) or non-trivial starts before the thread
+        uint32_t last = prefix[1] > ex[1] ? prefix[1] : ex[1];  // last head position before it
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t i = static_cast<uint32_t>(first + k);
+            if ((t.heads >> k) & 1u) last = i;
+            if constexpr (MODE == kEncode) {
+                if ((t.sel >> k) & 1u) ++count;
+                if ((t.sel2 >> k) & 1u) a.aux0[count - 1] = i + 1 - last;
+            } else {
+                if ((t.sel >> k) & 1u) a.aux0[count++] = i;
+                if ((t.sel2 >> k) & 1u) a.aux1[count - 1] = i + 1 - last;
+            }
+        }
+        if constexpr (MODE == kNonTrivial) return;
+    }
+
+    // Stage: selected items at their tile rank; partition rejects, or the three-way categories,
+    // after them.
+    {
+        uint32_t r1 = ex[0];
+        uint32_t r2 = 0;
+        if constexpr (MODE == kThreeWay) r2 = ex[1];
+        const bool rejects = (MODE == kSelect && a.partition) || MODE == kThreeWay;
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const uint32_t bit = 1u << k;
+            if (t.sel & bit) {
+                stage[r1++] = t.x[k];
+            } else if (MODE == kThreeWay && (t.sel2 & bit)) {
+                stage[agg[0] + r2++] = t.x[k];
+            } else if (rejects && first + k < a.n) {
+                const uint32_t local = local0 + k;
+                uint32_t taken = r1;
+                if constexpr (MODE == kThreeWay) taken += r2;
+                uint32_t base = agg[0];
+                if constexpr (MODE == kThreeWay) base += agg[1];
+                stage[base + (local - taken)] = t.x[k];
+            }
+        }
+    }
+    __syncthreads();
+    U* const out = a.out;
+    for (uint32_t q = tid; q < agg[0]; q += kCpBlock) out[prefix[0] + q] = stage[q];
+    if constexpr (MODE == kThreeWay) {
+        for (uint32_t q = tid; q < agg[1]; q += kCpBlock) a.out2[prefix[1] + q] = stage[agg[0] + q];
+        const uint32_t rejected = static_cast<uint32_t>(tile_valid) - agg[0] - agg[1];
+        const uint64_t before = tile_first - prefix[0] - prefix[1];
+        for (uint32_t q = tid; q < rejected; q += kCpBlock) a.out3[before + q] = stage[agg[0] + agg[1] + q];
+    } else if constexpr (MODE == kSelect) {
+        if (a.partition) {
+            const uint32_t rejected = static_cast<uint32_t>(tile_valid) - agg[0];
+            const uint64_t before = tile_first - prefix[0];
+            for (uint32_t q = tid; q < rejected; q += kCpBlock) out[a.n - 1 - (before + q)] = stage[agg[0] + q];
+        }
+    } else if constexpr (MODE == kUniqueByKey) {
+        __syncthreads();
+        V* const vstage = reinterpret_cast<V*>(s_stage);
+        uint32_t r1 = ex[0];
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            if ((t.sel >> k) & 1u) vstage[r1++] = t.v[k];
+        }
+        __syncthreads();
+        for (uint32_t q = tid; q < agg[0]; q += kCpBlock) a.values_out[prefix[0] + q] = vstage[q];
+    }
+}
+
+// dst[q] = src[q] for q < *count (the in-place select's copy back).
+template <typename U>
+__global__ __launch_bounds__(256) void copy_prefix_kernel(U* __restrict__ dst, const U* __restrict__ src,
+                                                          const uint32_t* __restrict__ count) {
+    const uint64_t c = *count;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t q = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < c; q += stride) dst[q] = src[q];
+}
+
+// dst[u - 1 - j] = src[j] for j < u = n - counts[0] - counts[1] (three-way unselected, reversed).
+template <typename U>
+__global__ __launch_bounds__(256) void reverse_rejects_kernel(U* __restrict__ dst, const U* __restrict__ src,
+                                                              const uint32_t* __restrict__ counts, uint64_t n) {
+    const uint64_t u = n - counts[0] - counts[1];
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < u; j += stride)
+        dst[u - 1 - j] = src[j];
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
+    if (!a || !b || a_bytes == 0 || b_bytes == 0) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + b_bytes && y < x + a_bytes;
+}
+
+unsigned grid_for(uint64_t n) {
+    const uint64_t blocks = ceil_div(n, 256 * 8);
+    return static_cast<unsigned>(blocks < 1 ? 1 : (blocks > 8192 ? 8192 : blocks));
+}
+
+// Temp layout: [states: tiles x W words | claims: tiles words] (256-byte aligned), then the staging
+// array of n items when the call needs one.
+struct TempPlan {
+    uint64_t tiles;
+    size_t state_bytes;
+    size_t stage_offset;
+    size_t total;
+};
+
+TempPlan plan_temp(uint64_t n, uint64_t tile, int words, size_t stage_item_bytes) {
+    TempPlan p;
+    p.tiles = ceil_div(n, tile);
+    p.state_bytes = p.tiles * (static_cast<size_t>(words) + 1) * sizeof(uint64_t);
+    p.stage_offset = align_up(p.state_bytes, kViewAlign);
+    p.total = stage_item_bytes ? p.stage_offset + n * stage_item_bytes : p.state_bytes;
+    return p;
+}
+
+template <typename P>
+int convert_predicate(const lcpp_hip_predicate* in, Predicate<P>& out, const char* what) {
+    if (!in) return set_error(kInvalidArgument, "%s: null predicate", what);
+    for (int c = 0; c < 2; ++c) {
+        const int op = in->op[c];
+        if (op < LCPP_HIP_PRED_TRUE || op > LCPP_HIP_PRED_MOD_NE)
+            return set_error(kInvalidArgument, "%s: unknown predicate clause %d", what, op);
+        out.c[c].op = op;
+        std::memcpy(&out.c[c].a, &in->a[c], sizeof(P));
+        std::memcpy(&out.c[c].b, &in->b[c], sizeof(P));
+        if (op == LCPP_HIP_PRED_MOD_EQ || op == LCPP_HIP_PRED_MOD_NE) {
+            if constexpr (!std::is_integral_v<P>) {
+                return set_error(kInvalidArgument, "%s: remainder clauses need integer operands", what);
+            } else {
+                if (out.c[c].a == P(0)) return set_error(kInvalidArgument, "%s: remainder by zero", what);
+            }
+        }
+    }
+    return kOk;
+}
+
+template <typename P>
+Predicate<P> nonzero_predicate() {
+    Predicate<P> p{};
+    p.c[0].op = LCPP_HIP_PRED_NE;
+    p.c[0].a = P(0);
+    p.c[1].op = LCPP_HIP_PRED_TRUE;
+    return p;
+}
+
+struct Outputs {
+    void* out = nullptr;
+    void* out2 = nullptr;
+    void* out3 = nullptr;  // caller's three-way unselected output
+    void* values_out = nullptr;
+    uint32_t* aux0 = nullptr;
+    uint32_t* aux1 = nullptr;
+    uint32_t* num_out = nullptr;
+};
+
+// Shared host path: checks, temp carving, state reset, launch, and the second kernel of the in-place
+// select and of the three-way partition.
+template <typename U, typename P, typename V, int MODE, bool FLAGS>
+int run_compact(const char* what, void* temp, size_t temp_bytes, const U* in, const P* flags, const V* values_in,
+                const Outputs& o, uint64_t n, uint64_t key_mask, const Predicate<P>& pred,
+                const Predicate<P>& pred2, bool partition, hipStream_t stream) {
+    constexpr int ITEMS = kCpItems<U, V>;
+    constexpr uint64_t kTile = static_cast<uint64_t>(kCpBlock) * ITEMS;
+    constexpr int W = kWords<MODE>;
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items", what);
+    if (!o.num_out) return set_error(kInvalidArgument, "%s: null count output", what);
+    if (n == 0) return launch_fill_u32(o.num_out, MODE == kThreeWay ? 2 : 1, 0u, stream);
+    if (!in || (FLAGS && !flags) || (MODE == kUniqueByKey && !values_in))
+        return set_error(kInvalidArgument, "%s: null input", what);
+    if (!o.out && MODE != kNonTrivial) return set_error(kInvalidArgument, "%s: null output", what);
+    if ((MODE == kThreeWay && (!o.out2 || !o.out3)) || (MODE == kUniqueByKey && !o.values_out) ||
+        ((MODE == kEncode || MODE == kNonTrivial) && !o.aux0) || (MODE == kNonTrivial && !o.aux1))
+        return set_error(kInvalidArgument, "%s: null output", what);
+    // Selects whose output overlaps their input or flags run into temp storage and copy back.
+    const bool in_place = MODE != kNonTrivial && MODE != kThreeWay &&
+                          (overlaps(o.out, n * sizeof(U), in, n * sizeof(U)) ||
+                           (FLAGS && overlaps(o.out, n * sizeof(U), flags, n * sizeof(P))));
+    if (in_place && (partition || MODE == kUniqueByKey))
+        return set_error(kInvalidArgument, "%s: output overlaps the input", what);
+    const TempPlan plan = plan_temp(n, kTile, W, (in_place || MODE == kThreeWay) ? sizeof(U) : 0);
+    if (!temp || temp_bytes < plan.total)
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, plan.total);
+    if (reinterpret_cast<uintptr_t>(temp) % 8 != 0) return set_error(kInvalidArgument, "%s: temp not 8-byte aligned", what);
+    if (plan.tiles > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many tiles", what);
+    U* const stage = reinterpret_cast<U*>(static_cast<unsigned char*>(temp) + plan.stage_offset);
+
+    CompactArgs<U, P, V> a{};
+    a.in = in;
+    a.flags = flags;
+    a.values_in = values_in;
+    a.out = in_place ? stage : static_cast<U*>(o.out);
+    a.out2 = static_cast<U*>(o.out2);
+    a.out3 = MODE == kThreeWay ? stage : nullptr;
+    a.values_out = static_cast<V*>(o.values_out);
+    a.aux0 = o.aux0;
+    a.aux1 = o.aux1;
+    a.num_out = o.num_out;
+    a.states = static_cast<uint64_t*>(temp);
+    a.n = n;
+    a.key_mask = key_mask;
+    a.pred = pred;
+    a.pred2 = pred2;
+    a.spin_limit = g_lookback_spin_limit;
+    a.partition = partition;
+    a.vec_in = aligned16(in);
+    a.vec_flags = FLAGS && aligned16(flags);
+    a.vec_values = MODE == kUniqueByKey && aligned16(values_in);
+
+    int st = launch_fill_u32(reinterpret_cast<uint32_t*>(temp), plan.state_bytes / 4, 0u, stream);
+    if (st != kOk) return st;
+    {
+        LaunchScope scope("compact", stream);
+        compact_kernel<U, P, V, MODE, FLAGS><<<static_cast<unsigned>(plan.tiles), kCpBlock, 0, stream>>>(a);
+        st = check_hip(hipGetLastError(), "compact launch");
+        if (st != kOk) return st;
+    }
+    if (in_place) {
+        LaunchScope scope("compact_copy_back", stream);
+        copy_prefix_kernel<U><<<grid_for(n), 256, 0, stream>>>(static_cast<U*>(o.out), stage, o.num_out);
+        return check_hip(hipGetLastError(), "compact copy-back launch");
+    }
+    if constexpr (MODE == kThreeWay) {
+        LaunchScope scope("compact_reverse_rejects", stream);
+        reverse_rejects_kernel<U><<<grid_for(n), 256, 0, stream>>>(static_cast<U*>(o.out3), stage, o.num_out, n);
+        return check_hip(hipGetLastError(), "compact reverse launch");
+    }
+    return kOk;
+}
+
+template <typename T>
+using Storage = std::conditional_t<sizeof(T) == 8, uint64_t, uint32_t>;
+
+// Key type for adjacency tests: floats compare by value, integers by bits under the mask.
+template <typename T>
+using KeyOf = std::conditional_t<std::is_floating_point_v<T>, T, Storage<T>>;
+
+}  // namespace
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+// Temp storage the compaction kernels carve: per tile of 8192 (4-byte items) or 4096 (8-byte items)
+// one or two state words and a claim word, plus n items of staging for in-place selects and the
+// three-way partition; never more than the reference's Get*TempStorageBytes.
+size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int words, int staged) {
+    if (n == 0) return 0;
+    const uint64_t tile = static_cast<uint64_t>(kCpBlock) * (128 / item_bytes);
+    return plan_temp(n, tile, words, staged ? item_bytes : 0).total;
+}
+
+#define LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, FS, FT)                                                                 \
+    int lcpp_hip_select_flagged_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags, TT* out,   \
+                                            uint32_t* num_selected_out, uint64_t n, void* stream) {                 \
+        using U = Storage<TT>;                                                                                       \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        const auto p = nonzero_predicate<FT>();                                                                      \
+        return run_compact<U, FT, U, kSelect, true>("DeviceSelect::Flagged", temp, temp_bytes,                       \
+                                                    reinterpret_cast<const U*>(in), flags, nullptr, o, n, 0, p, p,   \
+                                                    false, static_cast<hipStream_t>(stream));                        \
+    }                                                                                                                \
+    int lcpp_hip_select_flagged_if_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags,        \
+                                               TT* out, uint32_t* num_selected_out, uint64_t n,                     \
+                                               const lcpp_hip_predicate* pred, void* stream) {                      \
+        using U = Storage<TT>;                                                                                       \
+        Predicate<FT> p;                                                                                             \
+        const int st = convert_predicate(pred, p, "DeviceSelect::FlaggedIf");                                        \
+        if (st != kOk) return st;                                                                                    \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        return run_compact<U, FT, U, kSelect, true>("DeviceSelect::FlaggedIf", temp, temp_bytes,                     \
+                                                    reinterpret_cast<const U*>(in), flags, nullptr, o, n, 0, p, p,   \
+                                                    false, static_cast<hipStream_t>(stream));                        \
+    }                                                                                                                \
+    int lcpp_hip_partition_flagged_##TS##_##FS(void* temp, size_t temp_bytes, const TT* in, const FT* flags,        \
+                                               TT* out, uint32_t* num_selected_out, uint64_t n, void* stream) {     \
+        using U = Storage<TT>;                                                                                       \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        const auto p = nonzero_predicate<FT>();                                                                      \
+        return run_compact<U, FT, U, kSelect, true>("DevicePartition::Flagged", temp, temp_bytes,                    \
+                                                    reinterpret_cast<const U*>(in), flags, nullptr, o, n, 0, p, p,   \
+                                                    true, static_cast<hipStream_t>(stream));                         \
+    }
+
+#define LCPP_HIP_DEFINE_SELECT_FLAG_TYPES(TS, TT)           \
+    LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, b8, uint8_t)       \
+    LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, i32, int32_t)      \
+    LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, u32, uint32_t)     \
+    LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, i64, int64_t)      \
+    LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, u64, uint64_t)
+
+#define LCPP_HIP_DEFINE_SELECT_ITEMS(TS, TT)                                                                         \
+    int lcpp_hip_select_if_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out, uint32_t* num_selected_out,   \
+                                uint64_t n, const lcpp_hip_predicate* pred, void* stream) {                          \
+        Predicate<TT> p;                                                                                             \
+        const int st = convert_predicate(pred, p, "DeviceSelect::If");                                               \
+        if (st != kOk) return st;                                                                                    \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        return run_compact<TT, TT, TT, kSelect, false>("DeviceSelect::If", temp, temp_bytes, in, nullptr, nullptr,  \
+                                                       o, n, 0, p, p, false, static_cast<hipStream_t>(stream));      \
+    }                                                                                                                \
+    int lcpp_hip_partition_if_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                            \
+                                   uint32_t* num_selected_out, uint64_t n, const lcpp_hip_predicate* pred,           \
+                                   void* stream) {                                                                   \
+        Predicate<TT> p;                                                                                             \
+        const int st = convert_predicate(pred, p, "DevicePartition::If");                                            \
+        if (st != kOk) return st;                                                                                    \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        return run_compact<TT, TT, TT, kSelect, false>("DevicePartition::If", temp, temp_bytes, in, nullptr,        \
+                                                       nullptr, o, n, 0, p, p, true, static_cast<hipStream_t>(stream)); \
+    }                                                                                                                \
+    int lcpp_hip_partition_three_way_##TS(void* temp, size_t temp_bytes, const TT* in, TT* first_out,               \
+                                          TT* second_out, TT* unselected_out, uint32_t* num_selected_out,            \
+                                          uint64_t n, const lcpp_hip_predicate* select_first,                       \
+                                          const lcpp_hip_predicate* select_second, void* stream) {                  \
+        Predicate<TT> p1, p2;                                                                                        \
+        int st = convert_predicate(select_first, p1, "DevicePartition::If (three-way)");                            \
+        if (st != kOk) return st;                                                                                    \
+        st = convert_predicate(select_second, p2, "DevicePartition::If (three-way)");                               \
+        if (st != kOk) return st;                                                                                    \
+        Outputs o;                                                                                                   \
+        o.out = first_out;                                                                                           \
+        o.out2 = second_out;                                                                                         \
+        o.out3 = unselected_out;                                                                                     \
+        o.num_out = num_selected_out;                                                                                \
+        return run_compact<TT, TT, TT, kThreeWay, false>("DevicePartition::If (three-way)", temp, temp_bytes, in,  \
+                                                         nullptr, nullptr, o, n, 0, p1, p2, false,                  \
+                                                         static_cast<hipStream_t>(stream));                          \
+    }                                                                                                                \
+    int lcpp_hip_select_unique_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                           \
+                                    uint32_t* num_selected_out, uint64_t n, uint64_t key_mask, void* stream) {      \
+        using K = KeyOf<TT>;                                                                                         \
+        Outputs o;                                                                                                   \
+        o.out = out;                                                                                                 \
+        o.num_out = num_selected_out;                                                                                \
+        const Predicate<K> none{};                                                                                   \
+        return run_compact<K, K, K, kUnique, false>("DeviceSelect::Unique", temp, temp_bytes,                        \
+                                                    reinterpret_cast<const K*>(in), nullptr, nullptr, o, n, key_mask, \
+                                                    none, none, false, static_cast<hipStream_t>(stream));            \
+    }                                                                                                                \
+    int lcpp_hip_run_length_encode_##TS(void* temp, size_t temp_bytes, const TT* in, TT* unique_out,                \
+                                        uint32_t* counts_out, uint32_t* num_runs_out, uint64_t n, void* stream) {   \
+        using K = KeyOf<TT>;                                                                                         \
+        Outputs o;                                                                                                   \
+        o.out = unique_out;                                                                                          \
+        o.aux0 = counts_out;                                                                                         \
+        o.num_out = num_runs_out;                                                                                    \
+        const Predicate<K> none{};                                                                                   \
+        return run_compact<K, K, K, kEncode, false>("DeviceRunLengthEncode::Encode", temp, temp_bytes,               \
+                                                    reinterpret_cast<const K*>(in), nullptr, nullptr, o, n, ~0ull,  \
+                                                    none, none, false, static_cast<hipStream_t>(stream));            \
+    }                                                                                                                \
+    int lcpp_hip_run_length_non_trivial_##TS(void* temp, size_t temp_bytes, const TT* in, uint32_t* offsets_out,    \
+                                             uint32_t* lengths_out, uint32_t* num_runs_out, uint64_t n,              \
+                                             void* stream) {                                                         \
+        using K = KeyOf<TT>;                                                                                         \
+        Outputs o;                                                                                                   \
+        o.aux0 = offsets_out;                                                                                        \
+        o.aux1 = lengths_out;                                                                                        \
+        o.num_out = num_runs_out;                                                                                    \
+        const Predicate<K> none{};                                                                                   \
+        return run_compact<K, K, K, kNonTrivial, false>("DeviceRunLengthEncode::NonTrivialRuns", temp, temp_bytes,  \
+                                                        reinterpret_cast<const K*>(in), nullptr, nullptr, o, n,     \
+                                                        ~0ull, none, none, false, static_cast<hipStream_t>(stream)); \
+    }                                                                                                                \
+    LCPP_HIP_DEFINE_SELECT_FLAG_TYPES(TS, TT)
+
+LCPP_HIP_DEFINE_SELECT_ITEMS(i32, int32_t)
+LCPP_HIP_DEFINE_SELECT_ITEMS(u32, uint32_t)
+LCPP_HIP_DEFINE_SELECT_ITEMS(f32, float)
+LCPP_HIP_DEFINE_SELECT_ITEMS(i64, int64_t)
+LCPP_HIP_DEFINE_SELECT_ITEMS(u64, uint64_t)
+LCPP_HIP_DEFINE_SELECT_ITEMS(f64, double)
+
+#define LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, VS, VT)                                                                \
+    int lcpp_hip_select_unique_by_key_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in,                 \
+                                                  const VT* values_in, KT* keys_out, VT* values_out,                 \
+                                                  uint32_t* num_selected_out, uint64_t n, uint64_t key_mask,         \
+                                                  void* stream) {                                                    \
+        using K = KeyOf<KT>;                                                                                         \
+        using V = Storage<VT>;                                                                                       \
+        Outputs o;                                                                                                   \
+        o.out = keys_out;                                                                                            \
+        o.values_out = values_out;                                                                                   \
+        o.num_out = num_selected_out;                                                                                \
+        const Predicate<K> none{};                                                                                   \
+        return run_compact<K, K, V, kUniqueByKey, false>("DeviceSelect::UniqueByKey", temp, temp_bytes,              \
+                                                         reinterpret_cast<const K*>(keys_in), nullptr,               \
+                                                         reinterpret_cast<const V*>(values_in), o, n, key_mask,      \
+                                                         none, none, false, static_cast<hipStream_t>(stream));       \
+    }
+#define LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(KS, KT)          \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, i32, int32_t)       \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, u32, uint32_t)      \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, f32, float)         \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, i64, int64_t)       \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, u64, uint64_t)      \
+    LCPP_HIP_DEFINE_UNIQUE_BY_KEY(KS, KT, f64, double)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(i32, int32_t)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(u32, uint32_t)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(f32, float)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(i64, int64_t)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(u64, uint64_t)
+LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES(f64, double)
+
+#undef LCPP_HIP_DEFINE_UNIQUE_BY_KEY_VALUES
+#undef LCPP_HIP_DEFINE_UNIQUE_BY_KEY
+#undef LCPP_HIP_DEFINE_SELECT_ITEMS
+#undef LCPP_HIP_DEFINE_SELECT_FLAG_TYPES
+#undef LCPP_HIP_DEFINE_SELECT_FLAGS
+
+}  // extern "C"

@@ -195,4 +195,46 @@ size_t lcpp_hip_reduce_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t va
     return lcpp_hip_reduce_by_key_temp_bytes_policy(n, key_bytes, value_bytes, 256);
 }
 
+// DeviceScan<BLOCK, 32, ITEMS>::GetTempStorageBytes<uint>, the scan the compaction modules size for
+// (device_select.h:22,56-63): the default-policy reservation applies only to the 256 x 15 tile.
+static size_t compaction_scan_bytes(uint64_t n, uint32_t block_size, uint32_t items_per_thread) {
+    const int default_policy = block_size == 256 && items_per_thread == 15 ? 1 : 0;
+    return lcpp_hip_scan_temp_bytes_policy(n, 4, block_size, items_per_thread, default_policy, 0);
+}
+
+// DeviceSelect<BLOCK, 32, ITEMS>::GetTempStorageBytes (device_select.h:56-63) and
+// DevicePartition<>::GetTempStorageBytes (device_partition.h:55-62): 2 n uints + the scan's bytes;
+// raised to the compaction kernels' need (in-place staging of 8-byte items) where a policy's scan
+// layout is smaller.
+size_t lcpp_hip_select_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread) {
+    if (n == 0 || block_size == 0 || items_per_thread == 0) return 0;
+    const size_t bytes = 2 * n * 4 + compaction_scan_bytes(n, block_size, items_per_thread);
+    return std::max(bytes, lcpp_hip_internal_compact_needed_bytes(n, 8, 1, 1));
+}
+
+size_t lcpp_hip_select_temp_bytes(uint64_t n) { return lcpp_hip_select_temp_bytes_policy(n, 256, 4); }
+
+// DevicePartition<BLOCK, 32, ITEMS>::GetThreeWayTempStorageBytes (device_partition.h:64-71).
+size_t lcpp_hip_partition_three_way_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread) {
+    if (n == 0 || block_size == 0 || items_per_thread == 0) return 0;
+    const size_t bytes = 3 * n * 4 + compaction_scan_bytes(n, block_size, items_per_thread);
+    return std::max(bytes, lcpp_hip_internal_compact_needed_bytes(n, 8, 2, 1));
+}
+
+size_t lcpp_hip_partition_three_way_temp_bytes(uint64_t n) {
+    return lcpp_hip_partition_three_way_temp_bytes_policy(n, 256, 4);
+}
+
+// DeviceRunLengthEncode<BLOCK, 32, ITEMS>::GetTempStorageBytes (device_run_length_encode.h:56-69):
+// six n-sized uint arrays and a run counter, 256-byte aligned, then the scan's bytes.
+size_t lcpp_hip_run_length_encode_temp_bytes_policy(uint64_t n, uint32_t block_size, uint32_t items_per_thread) {
+    if (n == 0 || block_size == 0 || items_per_thread == 0) return 0;
+    const size_t bytes = align_up((6 * n + 1) * 4) + compaction_scan_bytes(n, block_size, items_per_thread);
+    return std::max(bytes, lcpp_hip_internal_compact_needed_bytes(n, 8, 2, 1));
+}
+
+size_t lcpp_hip_run_length_encode_temp_bytes(uint64_t n) {
+    return lcpp_hip_run_length_encode_temp_bytes_policy(n, 256, 4);
+}
+
 }  // extern "C"

@@ -6,7 +6,8 @@ loaded, :func:`lib` raises.
 
 The operation names follow the reference API (``DeviceReduce::Sum``, ``DeviceScan::ExclusiveSum``,
 ``DeviceRadixSort::SortKeys/SortPairs``, ``DeviceSpmv::CsrMV``, ``DeviceScan::*SumByKey``,
-``DeviceReduce::ReduceByKey``; src/lcpp/device/*.h) and the
+``DeviceReduce::ReduceByKey``, ``DeviceSelect``, ``DevicePartition``, ``DeviceRunLengthEncode``;
+src/lcpp/device/*.h) and the
 temp-storage queries return the reference's ``Get*TempStorageBytes`` values.
 """
 from __future__ import annotations
@@ -32,12 +33,24 @@ SORT_KEY_SUFFIXES = ("u32", "i32", "f32", "u64", "i64", "f64")
 SPMV_SUFFIXES = [(v, i) for v in ("f32", "f64", "i32", "u32") for i in ("i32", "u32")]
 BY_KEY_KEY_SUFFIXES = ("i32", "u32", "i64", "u64")
 BY_KEY_VALUE_SUFFIXES = SCALAR_SUFFIXES
+FLAG_SUFFIXES = ("b8", "i32", "u32", "i64", "u64")
+
+# Predicate clause ops (include/lcpp_hip.h LCPP_HIP_PRED_*).
+(PRED_TRUE, PRED_LT, PRED_LE, PRED_GT, PRED_GE, PRED_EQ, PRED_NE, PRED_RANGE, PRED_MASK_EQ, PRED_MASK_NE,
+ PRED_MOD_EQ, PRED_MOD_NE) = range(12)
+
+
+class Predicate(C.Structure):
+    """lcpp_hip_predicate: two clauses that must both hold; operands are bits of the item type."""
+    _fields_ = [("op", C.c_int32 * 2), ("a", C.c_uint64 * 2), ("b", C.c_uint64 * 2)]
 
 _CTYPE = {
     "i32": C.c_int32, "u32": C.c_uint32, "f32": C.c_float,
     "i64": C.c_int64, "u64": C.c_uint64, "f64": C.c_double,
 }
 ELEM_BYTES = {"i32": 4, "u32": 4, "f32": 4, "i64": 8, "u64": 8, "f64": 8}
+_NP_DTYPE = {"i32": "int32", "u32": "uint32", "f32": "float32", "i64": "int64", "u64": "uint64", "f64": "float64",
+             "b8": "uint8"}
 
 
 class LcppHipError(RuntimeError):
@@ -104,6 +117,24 @@ def _declare(lib: C.CDLL) -> None:
         for v in BY_KEY_VALUE_SUFFIXES:
             sig(f"lcpp_hip_scan_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, u64, i32, i32, _CTYPE[v], u64, vp)
             sig(f"lcpp_hip_reduce_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
+    pp = C.POINTER(Predicate)
+    for name in ("select", "partition_three_way", "run_length_encode"):
+        sig(f"lcpp_hip_{name}_temp_bytes", sz, u64)
+        sig(f"lcpp_hip_{name}_temp_bytes_policy", sz, u64, u32, u32)
+    sig("lcpp_hip_internal_compact_needed_bytes", sz, u64, sz, i32, i32)
+    for t in SCALAR_SUFFIXES:
+        sig(f"lcpp_hip_select_if_{t}", i32, vp, sz, vp, vp, vp, u64, pp, vp)
+        sig(f"lcpp_hip_partition_if_{t}", i32, vp, sz, vp, vp, vp, u64, pp, vp)
+        sig(f"lcpp_hip_partition_three_way_{t}", i32, vp, sz, vp, vp, vp, vp, vp, u64, pp, pp, vp)
+        sig(f"lcpp_hip_select_unique_{t}", i32, vp, sz, vp, vp, vp, u64, u64, vp)
+        sig(f"lcpp_hip_run_length_encode_{t}", i32, vp, sz, vp, vp, vp, vp, u64, vp)
+        sig(f"lcpp_hip_run_length_non_trivial_{t}", i32, vp, sz, vp, vp, vp, vp, u64, vp)
+        for f in FLAG_SUFFIXES:
+            sig(f"lcpp_hip_select_flagged_{t}_{f}", i32, vp, sz, vp, vp, vp, vp, u64, vp)
+            sig(f"lcpp_hip_select_flagged_if_{t}_{f}", i32, vp, sz, vp, vp, vp, vp, u64, pp, vp)
+            sig(f"lcpp_hip_partition_flagged_{t}_{f}", i32, vp, sz, vp, vp, vp, vp, u64, vp)
+        for v in SCALAR_SUFFIXES:
+            sig(f"lcpp_hip_select_unique_by_key_{t}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
 
 
 def lib() -> C.CDLL:
@@ -296,3 +327,120 @@ def reduce_by_key(key_suffix: str, value_suffix: str, keys, values, unique_out, 
     call(f"lcpp_hip_reduce_by_key_sum_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
          ptr(keys), ptr(values), ptr(unique_out), ptr(aggregates_out), ptr(num_runs_out), n,
          key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))
+
+
+# ---- stream compaction (DeviceSelect, DevicePartition, DeviceRunLengthEncode) -------------------
+def operand_bits(value, suffix: str) -> int:
+    """Bits of `value` as an item of type `suffix`, in the low bytes (how the C-ABI takes operands)."""
+    import numpy as np
+    arr = np.array([value], dtype=_NP_DTYPE[suffix])
+    return int(arr.view({1: np.uint8, 4: np.uint32, 8: np.uint64}[arr.itemsize])[0])
+
+
+def predicate(suffix: str, *clauses) -> Predicate:
+    """Predicate from up to two (op, a[, b]) clauses with operands given as values of type `suffix`."""
+    p = Predicate()
+    for c in range(2):
+        op, a, b = (tuple(clauses[c]) + (0, 0))[:3] if c < len(clauses) else (PRED_TRUE, 0, 0)
+        p.op[c] = op
+        p.a[c] = operand_bits(a, suffix)
+        p.b[c] = operand_bits(b, suffix)
+    return p
+
+
+def select_temp_bytes(n: int, block: int = 256, items: int = 4) -> int:
+    return lib().lcpp_hip_select_temp_bytes_policy(n, block, items)
+
+
+def partition_three_way_temp_bytes(n: int, block: int = 256, items: int = 4) -> int:
+    return lib().lcpp_hip_partition_three_way_temp_bytes_policy(n, block, items)
+
+
+def run_length_encode_temp_bytes(n: int, block: int = 256, items: int = 4) -> int:
+    return lib().lcpp_hip_run_length_encode_temp_bytes_policy(n, block, items)
+
+
+def _temp_for(nbytes: int, like, temp):
+    if temp is not None:
+        return temp
+    return _temp(nbytes, like.device)
+
+
+def _tb(temp) -> int:
+    return temp.numel() * temp.element_size()
+
+
+def select_flagged(suffix: str, flag_suffix: str, d_in, flags, d_out, num_out, n: int, temp=None, stream=None):
+    """DeviceSelect::Flagged: items whose flag != 0, in order (in place when d_out overlaps d_in)."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_select_flagged_{suffix}_{flag_suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(flags), ptr(d_out),
+         ptr(num_out), n, stream_handle(stream))
+
+
+def select_flagged_if(suffix: str, flag_suffix: str, d_in, flags, d_out, num_out, n: int, pred: Predicate,
+                      temp=None, stream=None):
+    """DeviceSelect::FlaggedIf: items whose flag satisfies `pred` (a predicate over the flag type)."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_select_flagged_if_{suffix}_{flag_suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(flags),
+         ptr(d_out), ptr(num_out), n, C.byref(pred), stream_handle(stream))
+
+
+def select_if(suffix: str, d_in, d_out, num_out, n: int, pred: Predicate, temp=None, stream=None):
+    """DeviceSelect::If."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_select_if_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(d_out), ptr(num_out), n,
+         C.byref(pred), stream_handle(stream))
+
+
+def select_unique(suffix: str, d_in, d_out, num_out, n: int, key_mask: int = -1, temp=None, stream=None):
+    """DeviceSelect::Unique: the first item of every run of equal items."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_select_unique_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(d_out), ptr(num_out), n,
+         key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))
+
+
+def select_unique_by_key(key_suffix: str, value_suffix: str, keys_in, values_in, keys_out, values_out, num_out,
+                         n: int, key_mask: int = -1, temp=None, stream=None):
+    """DeviceSelect::UniqueByKey: the first (key, value) of every run of equal keys."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_select_unique_by_key_{key_suffix}_{value_suffix}", ptr(temp), _tb(temp), ptr(keys_in),
+         ptr(values_in), ptr(keys_out), ptr(values_out), ptr(num_out), n, key_mask & 0xFFFFFFFFFFFFFFFF,
+         stream_handle(stream))
+
+
+def partition_flagged(suffix: str, flag_suffix: str, d_in, flags, d_out, num_out, n: int, temp=None, stream=None):
+    """DevicePartition::Flagged: flagged items in order, then the others in reverse order."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_partition_flagged_{suffix}_{flag_suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(flags),
+         ptr(d_out), ptr(num_out), n, stream_handle(stream))
+
+
+def partition_if(suffix: str, d_in, d_out, num_out, n: int, pred: Predicate, temp=None, stream=None):
+    """DevicePartition::If."""
+    temp = _temp_for(select_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_partition_if_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(d_out), ptr(num_out), n,
+         C.byref(pred), stream_handle(stream))
+
+
+def partition_three_way(suffix: str, d_in, first_out, second_out, unselected_out, num_out, n: int,
+                        select_first: Predicate, select_second: Predicate, temp=None, stream=None):
+    """DevicePartition::If with two predicates (num_out[0..1] = the two category sizes)."""
+    temp = _temp_for(partition_three_way_temp_bytes(n), num_out, temp)
+    call(f"lcpp_hip_partition_three_way_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(first_out),
+         ptr(second_out), ptr(unselected_out), ptr(num_out), n, C.byref(select_first), C.byref(select_second),
+         stream_handle(stream))
+
+
+def run_length_encode(suffix: str, d_in, unique_out, counts_out, num_runs_out, n: int, temp=None, stream=None):
+    """DeviceRunLengthEncode::Encode."""
+    temp = _temp_for(run_length_encode_temp_bytes(n), num_runs_out, temp)
+    call(f"lcpp_hip_run_length_encode_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(unique_out), ptr(counts_out),
+         ptr(num_runs_out), n, stream_handle(stream))
+
+
+def run_length_non_trivial(suffix: str, d_in, offsets_out, lengths_out, num_runs_out, n: int, temp=None,
+                           stream=None):
+    """DeviceRunLengthEncode::NonTrivialRuns."""
+    temp = _temp_for(run_length_encode_temp_bytes(n), num_runs_out, temp)
+    call(f"lcpp_hip_run_length_non_trivial_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(offsets_out),
+         ptr(lengths_out), ptr(num_runs_out), n, stream_handle(stream))

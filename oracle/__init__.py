@@ -59,6 +59,18 @@ def lib() -> C.CDLL:
         h.oracle_reduce_by_key_int.argtypes = [vp, i32, vp, i32, vp, vp, u64, u64]
         h.oracle_reduce_by_key_fp.restype = u64
         h.oracle_reduce_by_key_fp.argtypes = [vp, i32, vp, i32, vp, vp, vp, u64, u64]
+        h.oracle_run_heads.restype = None
+        h.oracle_run_heads.argtypes = [i32, vp, u64, u64, vp]
+        h.oracle_predicate.restype = None
+        h.oracle_predicate.argtypes = [i32, vp, u64, vp, vp, vp, vp]
+        h.oracle_select.restype = u64
+        h.oracle_select.argtypes = [i32, vp, vp, u64, vp, i32]
+        h.oracle_partition_three_way.restype = None
+        h.oracle_partition_three_way.argtypes = [i32, vp, vp, vp, u64, vp, vp, vp, vp]
+        h.oracle_run_length_encode.restype = u64
+        h.oracle_run_length_encode.argtypes = [i32, vp, u64, vp, vp]
+        h.oracle_non_trivial_runs.restype = u64
+        h.oracle_non_trivial_runs.argtypes = [i32, vp, u64, vp, vp]
         _lib = h
     return _lib
 
@@ -219,3 +231,73 @@ def reduce_by_key_fp(keys: np.ndarray, values: np.ndarray, key_mask: int = -1):
     runs = lib().oracle_reduce_by_key_fp(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(uniq), _p(agg),
                                          _p(ab), values.size, _mask(key_mask))
     return uniq[:runs], agg[:runs], ab[:runs]
+
+
+# ---- stream compaction (oracle.c: select, partition, run-length encode) -------------------------
+_TYPE_CODES = {np.dtype(np.int32): 0, np.dtype(np.uint32): 1, np.dtype(np.float32): 2, np.dtype(np.int64): 3,
+               np.dtype(np.uint64): 4, np.dtype(np.float64): 5, np.dtype(np.uint8): 6, np.dtype(np.bool_): 6}
+
+
+def _code(a: np.ndarray) -> int:
+    return _TYPE_CODES[a.dtype]
+
+
+def _bits_of(value, dtype) -> int:
+    """The operand's bits in the item type, as the C-ABI takes them (low bytes of a uint64)."""
+    arr = np.array([value], dtype=dtype)
+    return int(arr.view({1: np.uint8, 4: np.uint32, 8: np.uint64}[arr.itemsize])[0])
+
+
+def predicate(x: np.ndarray, clauses) -> np.ndarray:
+    """uint8 mask: both clauses hold.  `clauses` = [(op, a, b), (op, a, b)] with values of x's type."""
+    x = np.ascontiguousarray(x)
+    cl = [tuple(c) + (0,) * (3 - len(c)) for c in clauses] + [(0, 0, 0)] * (2 - len(clauses))
+    ops = np.array([c[0] for c in cl], np.int32)
+    a = np.array([_bits_of(c[1], x.dtype) for c in cl], np.uint64)
+    b = np.array([_bits_of(c[2], x.dtype) for c in cl], np.uint64)
+    sel = np.empty(x.size, np.uint8)
+    lib().oracle_predicate(_code(x), _p(x), x.size, _p(ops), _p(a), _p(b), _p(sel))
+    return sel
+
+
+def run_heads(x: np.ndarray, key_mask: int = -1) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    heads = np.empty(x.size, np.uint8)
+    lib().oracle_run_heads(_code(x), _p(x), x.size, _mask(key_mask), _p(heads))
+    return heads
+
+
+def select(x: np.ndarray, sel: np.ndarray, partition: bool = False) -> tuple[np.ndarray, int]:
+    """(output of n items, kept count): kept items in order; partition puts rejects reversed at the end."""
+    x = np.ascontiguousarray(x)
+    sel = np.ascontiguousarray(sel, dtype=np.uint8)
+    out = np.zeros_like(x)
+    kept = lib().oracle_select(x.itemsize, _p(x), _p(sel), x.size, _p(out), int(partition))
+    return out, int(kept)
+
+
+def partition_three_way(x: np.ndarray, first: np.ndarray, second: np.ndarray):
+    """(first_out, second_out, unselected_out, (c1, c2)); outputs are n-sized, written prefixes."""
+    x = np.ascontiguousarray(x)
+    f = np.ascontiguousarray(first, dtype=np.uint8)
+    s = np.ascontiguousarray(second, dtype=np.uint8)
+    o1, o2, o3 = np.zeros_like(x), np.zeros_like(x), np.zeros_like(x)
+    counts = np.zeros(2, np.uint64)
+    lib().oracle_partition_three_way(x.itemsize, _p(x), _p(f), _p(s), x.size, _p(o1), _p(o2), _p(o3), _p(counts))
+    return o1, o2, o3, (int(counts[0]), int(counts[1]))
+
+
+def run_length_encode(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x)
+    uniq = np.zeros(max(x.size, 1), x.dtype)
+    counts = np.zeros(max(x.size, 1), np.uint32)
+    runs = lib().oracle_run_length_encode(_code(x), _p(x), x.size, _p(uniq), _p(counts))
+    return uniq[:runs], counts[:runs]
+
+
+def non_trivial_runs(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x)
+    offs = np.zeros(max(x.size, 1), np.uint32)
+    lens = np.zeros(max(x.size, 1), np.uint32)
+    runs = lib().oracle_non_trivial_runs(_code(x), _p(x), x.size, _p(offs), _p(lens))
+    return offs[:runs], lens[:runs]

@@ -331,3 +331,169 @@ uint64_t oracle_reduce_by_key_fp(const void* keys, int key_bytes, const void* va
     }
     return runs;
 }
+
+/* ------------------------------------------------------------------------------------------------
+ * Stream compaction.  Follows DeviceSelect<> (src/lcpp/device/device_select.h:65-344: an item is
+ * kept when its flag != 0 or the predicate holds, kept items keep their order, the count is written
+ * once), DevicePartition<> (src/lcpp/device/device_partition.h:530-579: kept items in order at the
+ * front, the j-th rejected item at out[n - 1 - j]; three-way :581-663: first category, then second
+ * (not first), in order; the j-th unselected item at unselected[u - 1 - j] for u unselected items)
+ * and DeviceRunLengthEncode<> (src/lcpp/device/device_run_length_encode.h:71-153: the value and
+ * length of every run; offset and length of every run longer than one item).  A run starts at item
+ * 0 and wherever an item differs from the previous one: integers compare bitwise under key_mask,
+ * floats by value (lhs == rhs: -0.0 equals +0.0, NaN equals nothing).
+ * Predicates: two clauses that must both hold; see oracle_predicate below.
+ * Item types: 0 int32, 1 uint32, 2 float, 3 int64, 4 uint64, 5 double, 6 uint8.
+ * ---------------------------------------------------------------------------------------------- */
+static int type_bytes(int type) { return type == 6 ? 1 : (type <= 2 ? 4 : 8); }
+
+static int item_equal(int type, const void* p, uint64_t i, uint64_t j, uint64_t key_mask) {
+    if (type == 2) return ((const float*)p)[i] == ((const float*)p)[j];
+    if (type == 5) return ((const double*)p)[i] == ((const double*)p)[j];
+    const int b = type_bytes(type);
+    return ((load_bits(p, i, b) ^ load_bits(p, j, b)) & key_mask) == 0;
+}
+
+void oracle_run_heads(int type, const void* in, uint64_t n, uint64_t key_mask, uint8_t* heads) {
+    for (uint64_t i = 0; i < n; ++i) heads[i] = (uint8_t)(i == 0 || !item_equal(type, in, i, i - 1, key_mask));
+}
+
+/* Clause ops (same numbering as the C-ABI): 0 true, 1 <, 2 <=, 3 >, 4 >=, 5 ==, 6 !=,
+ * 7 a <= x < b, 8 (x & a) == b, 9 (x & a) != b, 10 x % a == b, 11 x % a != b (C remainder). */
+static int clause_holds(int type, const void* p, uint64_t i, int op, uint64_t a_bits, uint64_t b_bits) {
+    if (op == 0) return 1;
+    const int bytes = type_bytes(type);
+    const uint64_t mask = bytes == 8 ? ~0ull : ((1ull << (8 * bytes)) - 1);
+    if (op == 8 || op == 9) {
+        const int eq = (load_bits(p, i, bytes) & a_bits & mask) == (b_bits & mask);
+        return op == 8 ? eq : !eq;
+    }
+    if (type == 2 || type == 5) {
+        double x, a, b;
+        if (type == 2) {
+            float fa, fb;
+            const uint32_t ua = (uint32_t)a_bits, ub = (uint32_t)b_bits;
+            memcpy(&fa, &ua, 4);
+            memcpy(&fb, &ub, 4);
+            x = ((const float*)p)[i];
+            a = fa;
+            b = fb;
+        } else {
+            memcpy(&a, &a_bits, 8);
+            memcpy(&b, &b_bits, 8);
+            x = ((const double*)p)[i];
+        }
+        switch (op) {
+            case 1: return x < a;
+            case 2: return x <= a;
+            case 3: return x > a;
+            case 4: return x >= a;
+            case 5: return x == a;
+            case 6: return x != a;
+            case 7: return a <= x && x < b;
+            default: return 0;
+        }
+    }
+    const int is_signed = type == 0 || type == 3;
+    if (is_signed) {
+        const int64_t x = bytes == 4 ? (int64_t)(int32_t)load_bits(p, i, 4) : (int64_t)load_bits(p, i, 8);
+        const int64_t a = bytes == 4 ? (int64_t)(int32_t)(uint32_t)a_bits : (int64_t)a_bits;
+        const int64_t b = bytes == 4 ? (int64_t)(int32_t)(uint32_t)b_bits : (int64_t)b_bits;
+        switch (op) {
+            case 1: return x < a;
+            case 2: return x <= a;
+            case 3: return x > a;
+            case 4: return x >= a;
+            case 5: return x == a;
+            case 6: return x != a;
+            case 7: return a <= x && x < b;
+            case 10: return a != 0 && x % a == b;
+            case 11: return a != 0 && x % a != b;
+            default: return 0;
+        }
+    }
+    const uint64_t x = load_bits(p, i, bytes);
+    const uint64_t a = a_bits & mask, b = b_bits & mask;
+    switch (op) {
+        case 1: return x < a;
+        case 2: return x <= a;
+        case 3: return x > a;
+        case 4: return x >= a;
+        case 5: return x == a;
+        case 6: return x != a;
+        case 7: return a <= x && x < b;
+        case 10: return a != 0 && x % a == b;
+        case 11: return a != 0 && x % a != b;
+        default: return 0;
+    }
+}
+
+/* sel[i] = clause 0 and clause 1 hold for item i. */
+void oracle_predicate(int type, const void* in, uint64_t n, const int32_t* ops, const uint64_t* a, const uint64_t* b,
+                      uint8_t* sel) {
+    for (uint64_t i = 0; i < n; ++i)
+        sel[i] = (uint8_t)(clause_holds(type, in, i, ops[0], a[0], b[0]) && clause_holds(type, in, i, ops[1], a[1], b[1]));
+}
+
+/* Kept items in order; with `partition`, the j-th rejected item at out[n - 1 - j].  Returns the
+ * number kept. */
+uint64_t oracle_select(int item_bytes, const void* in, const uint8_t* sel, uint64_t n, void* out, int partition) {
+    uint64_t kept = 0, rejected = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t v = load_bits(in, i, item_bytes);
+        if (sel[i]) store_bits(out, kept++, item_bytes, v);
+        else if (partition) store_bits(out, n - 1 - rejected++, item_bytes, v);
+    }
+    return kept;
+}
+
+void oracle_partition_three_way(int item_bytes, const void* in, const uint8_t* first, const uint8_t* second,
+                                uint64_t n, void* first_out, void* second_out, void* unselected_out,
+                                uint64_t* counts) {
+    uint64_t c1 = 0, c2 = 0, u = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        if (first[i]) ++c1;
+        else if (second[i]) ++c2;
+        else ++u;
+    }
+    uint64_t k1 = 0, k2 = 0, ku = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t v = load_bits(in, i, item_bytes);
+        if (first[i]) store_bits(first_out, k1++, item_bytes, v);
+        else if (second[i]) store_bits(second_out, k2++, item_bytes, v);
+        else store_bits(unselected_out, u - 1 - ku++, item_bytes, v);
+    }
+    counts[0] = c1;
+    counts[1] = c2;
+}
+
+/* unique[r] = value of run r, counts[r] = its length; returns the number of runs. */
+uint64_t oracle_run_length_encode(int type, const void* in, uint64_t n, void* unique_out, uint32_t* counts) {
+    const int bytes = type_bytes(type);
+    uint64_t runs = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        if (i == 0 || !item_equal(type, in, i, i - 1, ~0ull)) {
+            store_bits(unique_out, runs, bytes, load_bits(in, i, bytes));
+            counts[runs++] = 1;
+        } else {
+            counts[runs - 1] += 1;
+        }
+    }
+    return runs;
+}
+
+/* offsets[r], lengths[r] of the r-th run longer than one item; returns how many there are. */
+uint64_t oracle_non_trivial_runs(int type, const void* in, uint64_t n, uint32_t* offsets, uint32_t* lengths) {
+    uint64_t found = 0, start = 0;
+    for (uint64_t i = 1; i <= n; ++i) {
+        if (i == n || !item_equal(type, in, i, i - 1, ~0ull)) {
+            if (i - start > 1) {
+                offsets[found] = (uint32_t)start;
+                lengths[found] = (uint32_t)(i - start);
+                ++found;
+            }
+            start = i;
+        }
+    }
+    return n == 0 ? 0 : found;
+}

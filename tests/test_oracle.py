@@ -386,3 +386,176 @@ def test_by_key_float_paths_match_exact_sums(orc):
     assert np.array_equal(uniq, keys[starts])
     for r, (b, e) in enumerate(zip(starts, ends)):
         assert agg[r] == pytest.approx(math.fsum(float(x) for x in vals[b:e]), rel=1e-15, abs=1e-12)
+
+
+# ---- stream compaction --------------------------------------------------------------------------
+# Known answers from the reference's tests, then an independent pure-Python formulation on small
+# random inputs (list comprehensions and explicit C remainders, sharing nothing with oracle.c).
+
+def test_run_length_encode_cub_example_known_answer(orc):
+    """tests/device_run_length_encode_test.cpp:172-245 (CUB's documented example)."""
+    x = np.array([0, 2, 2, 9, 5, 5, 5, 8], np.int32)
+    u, c = orc.run_length_encode(x)
+    assert u.tolist() == [0, 2, 9, 5, 8] and c.tolist() == [1, 2, 1, 3, 1]
+    o, ln = orc.non_trivial_runs(x)
+    assert o.tolist() == [1, 4] and ln.tolist() == [2, 3]
+
+
+def test_run_length_encode_wide_values_known_answer(orc):
+    """tests/device_run_length_encode_test.cpp:41-72: 64-bit values 2^40, 2^40, 2^41, 2^42 x3, 2^43."""
+    x = np.array([1 << 40, 1 << 40, 1 << 41, 1 << 42, 1 << 42, 1 << 42, 1 << 43], np.uint64)
+    u, c = orc.run_length_encode(x)
+    assert u.tolist() == [1 << 40, 1 << 41, 1 << 42, 1 << 43] and c.tolist() == [2, 1, 3, 1]
+
+
+def test_run_length_encode_host_reference_runs(orc):
+    """tests/device_run_length_encode_test.cpp:282-340: 180 runs of length run % 7 + 1."""
+    x = np.concatenate([np.full(r % 7 + 1, r, np.int32) for r in range(180)])
+    u, c = orc.run_length_encode(x)
+    assert u.tolist() == list(range(180)) and c.tolist() == [r % 7 + 1 for r in range(180)]
+    o, ln = orc.non_trivial_runs(x)
+    starts = np.cumsum([0] + [r % 7 + 1 for r in range(179)])
+    want = [(int(starts[r]), r % 7 + 1) for r in range(180) if r % 7 + 1 > 1]
+    assert list(zip(o.tolist(), ln.tolist())) == want
+
+
+def test_partition_three_way_known_answer(orc):
+    """tests/device_partition_test.cpp:292-349: 0..11, first = x % 3 == 0, second = x < 8."""
+    x = np.arange(12, dtype=np.int32)
+    f = orc.predicate(x, [(10, 3, 0)])
+    s = orc.predicate(x, [(1, 8, 0)])
+    o1, o2, o3, (c1, c2) = orc.partition_three_way(x, f, s)
+    assert (c1, c2) == (4, 5)
+    assert o1[:4].tolist() == [0, 3, 6, 9] and o2[:5].tolist() == [1, 2, 4, 5, 7] and o3[:3].tolist() == [11, 10, 8]
+
+
+def test_partition_flagged_and_if_ordering_known_answer(orc):
+    """tests/device_partition_test.cpp:103-177: flags i % 3 == 0 and x < 7 over 0..11."""
+    x = np.arange(12, dtype=np.int32)
+    out, k = orc.select(x, (np.arange(12) % 3 == 0).astype(np.uint8), partition=True)
+    assert k == 4 and out.tolist() == [0, 3, 6, 9, 11, 10, 8, 7, 5, 4, 2, 1]
+    out, k = orc.select(x, orc.predicate(x, [(1, 7, 0)]), partition=True)
+    assert k == 7 and out.tolist() == [0, 1, 2, 3, 4, 5, 6, 11, 10, 9, 8, 7]
+
+
+def test_select_unique_and_unique_by_key_known_answer(orc):
+    """tests/device_select_test.cpp:301-357: keys {1,1,2,2,2,4,7,7,9}."""
+    keys = np.array([1, 1, 2, 2, 2, 4, 7, 7, 9], np.int32)
+    vals = np.array([10, 11, 20, 21, 22, 40, 70, 71, 90], np.int32)
+    heads = orc.run_heads(keys)
+    uk, k = orc.select(keys, heads)
+    uv, kv = orc.select(vals, heads)
+    assert k == kv == 5 and uk[:5].tolist() == [1, 2, 4, 7, 9] and uv[:5].tolist() == [10, 20, 40, 70, 90]
+
+
+def test_select_flagged_if_positive_odd_known_answer(orc):
+    """tests/device_select_test.cpp:359-425: flags -3..5, flag > 0 and flag % 2 != 0 -> 104, 106, 108."""
+    data = np.arange(100, 109, dtype=np.int32)
+    flags = np.arange(-3, 6, dtype=np.int32)
+    sel = orc.predicate(flags, [(3, 0, 0), (11, 2, 0)])
+    out, k = orc.select(data, sel)
+    assert k == 3 and out[:3].tolist() == [104, 106, 108]
+
+
+def test_select_in_place_cases_known_answer(orc):
+    """tests/device_select_test.cpp:427-500: aliased flags, x > 0, same-parity Unique, default Unique."""
+    aliased = np.array([0, 2, 0, 3, 4, 0, 5, 0], np.int32)
+    out, k = orc.select(aliased, (aliased != 0).astype(np.uint8))
+    assert out[:k].tolist() == [2, 3, 4, 5]
+    pred = np.array([-3, 4, -1, 6, 0, 2, 7, -8], np.int32)
+    out, k = orc.select(pred, orc.predicate(pred, [(3, 0, 0)]))
+    assert out[:k].tolist() == [4, 6, 2, 7]
+    uni = np.array([1, 3, 2, 4, 5, 7, 8, 10], np.int32)
+    out, k = orc.select(uni, orc.run_heads(uni, key_mask=1))
+    assert out[:k].tolist() == [1, 2, 5, 8]
+    dflt = np.array([1, 1, 2, 2, 2, 4, 4, 9], np.int32)
+    out, k = orc.select(dflt, orc.run_heads(dflt))
+    assert out[:k].tolist() == [1, 2, 4, 9]
+
+
+def _c_rem(x: int, a: int) -> int:
+    q = abs(x) // abs(a)
+    return x - (q if (x < 0) == (a < 0) else -q) * a
+
+
+def _py_clause(x, op, a, b, bits):
+    if op == 0:
+        return True
+    if op in (8, 9):
+        m = (1 << bits) - 1
+        xv = int(np.array([x]).view({8: np.uint8, 32: np.uint32, 64: np.uint64}[bits])[0]) if bits else x
+        eq = (xv & a & m) == (b & m)
+        return eq if op == 8 else not eq
+    return {1: x < a, 2: x <= a, 3: x > a, 4: x >= a, 5: x == a, 6: x != a, 7: a <= x < b,
+            10: a != 0 and _c_rem(x, a) == b, 11: a != 0 and _c_rem(x, a) != b}[op]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32, np.int64, np.uint64])
+def test_predicate_vs_python(orc, dtype):
+    rng = np.random.default_rng(71)
+    info = np.iinfo(dtype)
+    x = rng.integers(max(info.min, -50), min(info.max, 50), size=300, endpoint=True).astype(dtype)
+    bits = 8 * np.dtype(dtype).itemsize
+    for op, a, b in [(1, 7, 0), (2, -3, 0), (3, 0, 0), (4, 9, 0), (5, 4, 0), (6, 0, 0), (7, -5, 12), (10, 3, 0),
+                     (10, 4, 1), (11, 2, 0), (8, 1, 0), (9, 6, 2)]:
+        if info.min == 0 and (a < 0 or b < 0):
+            continue
+        got = orc.predicate(x, [(op, a, b)])
+        want = [_py_clause(int(v), op, a, b, bits) if op not in (8, 9) else
+                ((int(v) & ((1 << bits) - 1)) & a) == b if op == 8 else ((int(v) & ((1 << bits) - 1)) & a) != b
+                for v in x]
+        assert got.astype(bool).tolist() == want, (op, a, b)
+
+
+def test_predicate_float_and_two_clauses(orc):
+    x = np.array([-2.5, -0.0, 0.0, 1.0, 6.99, 7.0, np.nan, np.inf], np.float32)
+    assert orc.predicate(x, [(1, 7.0, 0)]).tolist() == [1, 1, 1, 1, 1, 0, 0, 0]
+    assert orc.predicate(x, [(5, 0.0, 0)]).tolist() == [0, 1, 1, 0, 0, 0, 0, 0]
+    assert orc.predicate(x, [(7, 0.0, 7.0)]).tolist() == [0, 1, 1, 1, 1, 0, 0, 0]
+    assert orc.predicate(x, [(3, -1.0, 0), (2, 1.0, 0)]).tolist() == [0, 1, 1, 1, 0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint64, np.float32, np.float64])
+def test_compaction_vs_python(orc, dtype):
+    rng = np.random.default_rng(5)
+    for n in (0, 1, 2, 7, 64, 257):
+        raw = rng.integers(0, 4, size=n)
+        x = np.repeat(raw, rng.integers(1, 4, size=n))[:n].astype(dtype)
+        if dtype == np.float32 and n > 3:
+            x[1] = -0.0  # equal to +0.0 by value
+            x[2] = 0.0
+        sel = (rng.integers(0, 3, size=n) == 0).astype(np.uint8)
+        xs = x.tolist()
+        out, k = orc.select(x, sel)
+        assert out[:k].tolist() == [v for v, s in zip(xs, sel) if s]
+        out, k = orc.select(x, sel, partition=True)
+        assert out.tolist() == [v for v, s in zip(xs, sel) if s] + [v for v, s in zip(xs, sel) if not s][::-1]
+        sel2 = (rng.integers(0, 2, size=n) == 0).astype(np.uint8)
+        o1, o2, o3, (c1, c2) = orc.partition_three_way(x, sel, sel2)
+        first = [v for v, s in zip(xs, sel) if s]
+        second = [v for v, s, t in zip(xs, sel, sel2) if not s and t]
+        rest = [v for v, s, t in zip(xs, sel, sel2) if not s and not t]
+        assert (c1, c2) == (len(first), len(second))
+        assert o1[:c1].tolist() == first and o2[:c2].tolist() == second and o3[:len(rest)].tolist() == rest[::-1]
+        runs = []
+        for v in xs:
+            if runs and runs[-1][0] == v:
+                runs[-1][1] += 1
+            else:
+                runs.append([v, 1])
+        u, c = orc.run_length_encode(x)
+        assert u.tolist() == [r[0] for r in runs] and c.tolist() == [r[1] for r in runs]
+        starts = np.cumsum([0] + [r[1] for r in runs])[:-1] if runs else []
+        o, ln = orc.non_trivial_runs(x)
+        assert list(zip(o.tolist(), ln.tolist())) == [(int(s), r[1]) for s, r in zip(starts, runs) if r[1] > 1]
+        heads = orc.run_heads(x)
+        assert heads.tolist() == [int(i == 0 or xs[i] != xs[i - 1]) for i in range(n)]
+
+
+def test_select_stability_with_index_payload(orc):
+    """Kept items keep their order: selecting indices returns an increasing sequence."""
+    rng = np.random.default_rng(9)
+    idx = np.arange(5000, dtype=np.uint32)
+    sel = (rng.random(5000) < 0.3).astype(np.uint8)
+    out, k = orc.select(idx, sel)
+    assert np.all(np.diff(out[:k].astype(np.int64)) > 0) and k == int(sel.sum())

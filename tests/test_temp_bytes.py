@@ -141,3 +141,39 @@ def test_by_key_temp_bytes_policies(hip):
         assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(n, 4, 8, 1024, 64) == need
         assert lib.lcpp_hip_reduce_by_key_temp_bytes_policy(n, 4, 8, 8192) == need
     assert lib.lcpp_hip_scan_by_key_temp_bytes_policy(100, 4, 4, 0, 15) == 0
+
+
+def test_compaction_temp_bytes_known_values(hip):
+    """DeviceSelect / DevicePartition / DeviceRunLengthEncode temp queries worked by hand
+    (device_select.h:56-63, device_partition.h:55-71, device_run_length_encode.h:56-69) at n = 1000 with
+    the default DeviceScan<256, 32, 4> scan: tiles = ceil(1000 / 1024) = 1, tile_count = 33:
+      scan = 132 -> 256; + 132 = 388 -> 512; + 132 = 644 bytes;
+      select = 8 * 1000 + 644 = 8644; three-way = 12 * 1000 + 644 = 12644;
+      run-length encode = align256(4 * 6001 = 24004) = 24064 + 644 = 24708.  n = 0 needs nothing."""
+    lib = hip.lib()
+    assert lib.lcpp_hip_select_temp_bytes(1000) == 8644
+    assert lib.lcpp_hip_partition_three_way_temp_bytes(1000) == 12644
+    assert lib.lcpp_hip_run_length_encode_temp_bytes(1000) == 24708
+    for f in ("select", "partition_three_way", "run_length_encode"):
+        assert getattr(lib, f"lcpp_hip_{f}_temp_bytes")(0) == 0
+    # DeviceSelect<256, 32, 15> uses the default scan policy, which reserves the packed 320 x 25 layout too.
+    assert lib.lcpp_hip_select_temp_bytes_policy(1000, 256, 15) == 8000 + lib.lcpp_hip_scan_temp_bytes(1000, 4)
+
+
+def test_compaction_kernels_fit_reference_temp(hip):
+    """The compaction kernels carve at most what the reference formulas return, for every size: one
+    state word (select, unique) or two (three-way, run-length) per tile, plus n items of staging
+    (in-place selects, the three-way partition, in-place encode)."""
+    lib = hip.lib()
+    sizes = list(range(1, 60000, 97)) + [1 << 20, (1 << 24) + 3, 1 << 28, (1 << 32) - 1]
+    for n in sizes:
+        sel = lib.lcpp_hip_select_temp_bytes(n)
+        three = lib.lcpp_hip_partition_three_way_temp_bytes(n)
+        rle = lib.lcpp_hip_run_length_encode_temp_bytes(n)
+        for item in (4, 8):
+            assert lib.lcpp_hip_internal_compact_needed_bytes(n, item, 1, 1) <= sel
+            assert lib.lcpp_hip_internal_compact_needed_bytes(n, item, 2, 1) <= three
+            assert lib.lcpp_hip_internal_compact_needed_bytes(n, item, 2, 1) <= rle
+    # Large-tile policies are raised to the kernels' need.
+    n = 1 << 24
+    assert lib.lcpp_hip_select_temp_bytes_policy(n, 1024, 64) >= lib.lcpp_hip_internal_compact_needed_bytes(n, 8, 1, 1)
