@@ -4,14 +4,15 @@ Headline (`value`): onesweep SortKeys of 2^28 uniform uint32 keys (4 x 8-bit pas
 resident in HBM, one step = one SortKeys call.  The JSON line also carries the roofline of the
 dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
 one host thread), and the other benchmark configurations (reduce, scan, SortPairs, CsrMV) plus
-ExclusiveSumByKey / ReduceByKey as achieved GB/s against the 8 TB/s HBM peak.
+ExclusiveSumByKey / ReduceByKey and the stream-compaction family (select, partition, unique, run-length
+encode) as achieved GB/s against the 8 TB/s HBM peak.
 
 `roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
 FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only bykey|reduce|scan|sortpairs|spmv]
+                       [--only bykey|compact|reduce|scan|sortpairs|spmv]
 """
 from __future__ import annotations
 
@@ -209,8 +210,46 @@ def extra_by_key(hip, dev, steps, warmup, extra):
                                            "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+def extra_compact(hip, dev, steps, warmup, extra):
+    import torch
+    # DeviceSelect::If and DevicePartition::If over 2^28 uniform uint32 items with x < 2^31 (half
+    # selected); DeviceSelect::Unique and DeviceRunLengthEncode::Encode over 2^28 uint32 items in runs of
+    # geometric length (mean 64).
+    m = 1 << 28
+    x = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_HI, x, m, SEED + 11)
+    out = torch.empty_like(x)
+    num = torch.zeros(2, dtype=torch.int32, device=dev)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.run_length_encode_temp_bytes(m)), dtype=torch.int32, device=dev)
+    half = hip.predicate("u32", (hip.PRED_LT, 1 << 31))
+    for name, fn, written in (("select_if_u32_half_2p28", hip.select_if, None),
+                              ("partition_if_u32_half_2p28", hip.partition_if, m)):
+        call = lambda fn=fn: fn("u32", x, out, num, m, half, temp=temp)
+        t = time_steps(call, steps, warmup)
+        kept = int(num[0].item())
+        moved = 4 * m + 4 * (kept if written is None else written)
+        kms, _ = kernel_avg_ms(hip, call, "compact", 5)
+        extra[name] = {"ms": round(t, 5), "kernel_ms": round(kms, 5), "selected": kept,
+                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+    r = x
+    hip.generate(hip.GEN_U32_HI, r, m, SEED + 7)
+    runs_in = torch.cumsum(((r & 63) == 0).to(torch.int32), 0, dtype=torch.int32)
+    del x, r
+    counts = torch.empty_like(out)
+    for name, call, per_run in (
+            ("unique_u32_runs64_2p28", lambda: hip.select_unique("u32", runs_in, out, num, m, temp=temp), 4),
+            ("run_length_encode_u32_runs64_2p28",
+             lambda: hip.run_length_encode("u32", runs_in, out, counts, num, m, temp=temp), 8)):
+        t = time_steps(call, steps, warmup)
+        runs = int(num[0].item())
+        moved = 4 * m + per_run * runs
+        kms, _ = kernel_avg_ms(hip, call, "compact", 5)
+        extra[name] = {"ms": round(t, 5), "kernel_ms": round(kms, 5), "runs": runs,
+                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
-          "bykey": extra_by_key}
+          "bykey": extra_by_key, "compact": extra_compact}
 
 
 def run_extras(hip, dev, steps, warmup, names):

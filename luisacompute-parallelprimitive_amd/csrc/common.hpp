@@ -31,7 +31,7 @@ struct SumOp {
 // ------------------------------------------------------------------------------------------------
 // DPP lane moves. `__builtin_amdgcn_update_dpp(old, src, ctrl, row_mask, bank_mask, bound_ctrl)`:
 // lanes whose source lane is invalid, or whose row is masked off, receive `old`.
-// Control codes (GFX9 DPP): row_shr:n = 0x110+n, wave_shr:1 = 0x138, row_bcast:15 = 0x142,
+// Control codes (GFX9 DPP): row_shr:n = 0x110+n, wave_shl:1 = 0x130, wave_shr:1 = 0x138, row_bcast:15 = 0x142,
 // row_bcast:31 = 0x143.
 // ------------------------------------------------------------------------------------------------
 namespace dpp {
@@ -39,6 +39,7 @@ constexpr int kRowShr1 = 0x111;
 constexpr int kRowShr2 = 0x112;
 constexpr int kRowShr4 = 0x114;
 constexpr int kRowShr8 = 0x118;
+constexpr int kWaveShl1 = 0x130;
 constexpr int kWaveShr1 = 0x138;
 constexpr int kRowBcast15 = 0x142;
 constexpr int kRowBcast31 = 0x143;

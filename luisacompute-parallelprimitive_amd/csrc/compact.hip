@@ -17,21 +17,25 @@
 // where -0.0 == +0.0 and NaN differs from everything, like the reference's lhs == rhs).
 //
 // MI355X design
-//   * One workgroup of 256 threads per tile; each thread holds 128 bytes of consecutive items (32
-//     four-byte or 16 eight-byte items; 16-byte vector loads when aligned), so a tile is 8,192 or
-//     4,096 items and every thread's selection fits in a 32-bit mask.
-//   * Per-thread counts (W = 1 or 2 words) are scanned across the tile with DPP and LDS; the tile
+//   * One workgroup of 256 threads (4 waves) per tile.  A wave owns 64 x ITEMS consecutive items
+//     (ITEMS = 128 / item bytes: 32 four-byte or 16 eight-byte items per lane), lane l holding items
+//     seg + 64 j + l, so every load instruction of a wave reads consecutive addresses and a tile is
+//     8,192 or 4,096 items.
+//   * Selection masks are per-lane bit sets (bit j = item j of the lane).  Ranks come from wave ballots:
+//     row j's selected items take consecutive tile ranks (k + selected lanes below), so they are
+//     staged in LDS at consecutive addresses (no bank conflicts) and the workgroup copies each
+//     category out with full-width coalesced stores.  Run heads compare each item with the item
+//     before it, moved across lanes with DPP wave shifts.
+//   * Wave counts (W = 1 or 2 words) are combined across the tile's 4 waves in LDS; the tile
 //     publishes its aggregate, wave 0 walks back 64 predecessor tiles per step to the newest
 //     INCLUSIVE state, and the tile publishes INCLUSIVE.  Tile states are 64-bit words (status in the
 //     low half, count in the high half) read with agent-scope relaxed atomics; a multi-word state is
 //     accepted only when all its words show the same status.  A predecessor still unpublished after
 //     `spin_limit` polls is claimed (a claim word per tile) and counted by the waiting workgroup with
 //     the owner's own code; the owner waits for such a helper to finish before publishing INCLUSIVE.
-//   * Selected items are staged in LDS at their rank within the tile, then written with coalesced
-//     stores to out[prefix + q]; rejected items (partition) follow them in LDS and are written
-//     backwards from the end.  Run-length outputs (one store per run) are written directly.
-//   * Run lengths come from a second state word combined by max: the position of the last run head
-//     before each item, so a run crossing any number of tiles needs no second pass.
+//   * Partition rejects are written backwards from the end the same way.  Run lengths come from a
+//     second state word combined by max: the position of the last run head before each item, so a
+//     run crossing any number of tiles needs no second pass.
 //   * In-place selects (output overlapping the input or the flags) compact into temp storage and
 //     copy the selected prefix back; the three-way partition stages its unselected items in temp
 //     storage and reverses them into their output in a second small kernel.
@@ -98,14 +102,14 @@ using Bits = std::conditional_t<sizeof(T) == 8, uint64_t, std::conditional_t<siz
 
 // Bit k set when clause `c` holds for x[k].  The switch is uniform (a kernel argument), so each
 // thread runs one branch over all of its items.
-template <typename P, int N>
-__device__ __forceinline__ uint32_t clause_bits(const Clause<P>& c, const P (&x)[N]) {
-    uint32_t bits = 0;
+template <typename P, int N, typename M>
+__device__ __forceinline__ M clause_bits(const Clause<P>& c, const P (&x)[N]) {
+    M bits = 0;
 #define LCPP_CLAUSE(OP, EXPR)                                               \
     case OP: {                                                              \
         _Pragma("unroll") for (int k = 0; k < N; ++k) {                     \
             const P v = x[k];                                               \
-            bits |= ((EXPR) ? 1u : 0u) << k;                                \
+            bits |= static_cast<M>((EXPR) ? 1 : 0) << k;                     \
         }                                                                   \
         return bits;                                                        \
     }
@@ -133,7 +137,7 @@ __device__ __forceinline__ uint32_t clause_bits(const Clause<P>& c, const P (&x)
         }
     }
 #undef LCPP_CLAUSE
-    return c.op == LCPP_HIP_PRED_TRUE ? ~0u : 0u;
+    return c.op == LCPP_HIP_PRED_TRUE ? static_cast<M>(~static_cast<M>(0)) : static_cast<M>(0);
 }
 
 template <typename K>
@@ -145,23 +149,9 @@ __device__ __forceinline__ bool keys_equal(K a, K b, uint64_t mask) {
     }
 }
 
-template <typename T, int N>
-struct alignas(16) Vec {
-    T v[N];
-};
-
-// Items [first, first + N) of p (0 past n): vector loads when `vec` (p 16-byte aligned).
-template <typename T, int N>
-__device__ __forceinline__ void load_run(const T* p, uint64_t first, uint64_t n, bool vec, T (&out)[N]) {
-    if (vec && first + N <= n) {
-        const Vec<T, N> r = *reinterpret_cast<const Vec<T, N>*>(p + first);
-#pragma unroll
-        for (int k = 0; k < N; ++k) out[k] = r.v[k];
-    } else {
-#pragma unroll
-        for (int k = 0; k < N; ++k) out[k] = first + k < n ? p[first + k] : T(0);
-    }
-}
+// Per-lane item masks: bit j stands for item j of the lane.
+template <int ITEMS>
+using LaneMask = std::conditional_t<(ITEMS > 32), uint64_t, uint32_t>;
 
 template <typename U, typename P, typename V>
 struct CompactArgs {
@@ -182,71 +172,83 @@ struct CompactArgs {
     Predicate<P> pred2;   // three-way second
     uint32_t spin_limit;
     bool partition;       // select: write the rejected items backwards after the selected ones
-    bool vec_in;
-    bool vec_flags;
-    bool vec_values;
 };
 
+// A wave owns 64 * ITEMS consecutive items starting at `seg`; item j of lane l is seg + 64 j + l, so
+// every load and every output store of the wave covers consecutive addresses.
 template <typename U, typename V, int ITEMS>
-struct ThreadItems {
+struct LaneItems {
     U x[ITEMS];
     V v[ITEMS];
-    uint32_t sel;    // selected / first category / run heads / non-trivial run starts
-    uint32_t sel2;   // three-way second category / run ends / non-trivial run ends
-    uint32_t heads;  // run heads (run-length modes)
+    LaneMask<ITEMS> valid;
+    LaneMask<ITEMS> sel;    // selected / first category / run heads (encode) / non-trivial run starts
+    LaneMask<ITEMS> sel2;   // three-way second category / run ends (encode) / non-trivial run ends
+    LaneMask<ITEMS> heads;  // run heads (run-length modes)
 };
 
-template <int ITEMS>
-__device__ __forceinline__ uint32_t valid_mask(uint64_t first, uint64_t n) {
-    if (first >= n) return 0u;
-    const uint64_t left = n - first;
-    if (left >= static_cast<uint64_t>(ITEMS)) return ITEMS == 32 ? ~0u : ((1u << ITEMS) - 1u);
-    return (1u << left) - 1u;
-}
-
-// Loads a thread's items and computes its selection masks.
 template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS>
-__device__ __forceinline__ void load_thread(const CompactArgs<U, P, V>& a, uint64_t first, ThreadItems<U, V, ITEMS>& t) {
-    const uint32_t valid = valid_mask<ITEMS>(first, a.n);
-    load_run<U, ITEMS>(a.in, first, a.n, a.vec_in, t.x);
+__device__ __forceinline__ void load_lane(const CompactArgs<U, P, V>& a, uint64_t seg, LaneItems<U, V, ITEMS>& t) {
+    using M = LaneMask<ITEMS>;
+    const uint32_t lane = lane_id();
+    M valid = 0;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        const uint64_t i = seg + static_cast<uint64_t>(kWave) * j + lane;
+        const bool ok = i < a.n;
+        valid |= static_cast<M>(ok ? 1 : 0) << j;
+        t.x[j] = ok ? a.in[i] : U(0);
+        if constexpr (MODE == kUniqueByKey) t.v[j] = ok ? a.values_in[i] : V(0);
+    }
+    t.valid = valid;
     t.sel2 = 0;
     t.heads = 0;
     if constexpr (MODE == kSelect || MODE == kThreeWay) {
-        uint32_t s1, s2 = 0;
+        M s1, s2 = 0;
         if constexpr (FLAGS) {
             P f[ITEMS];
-            load_run<P, ITEMS>(a.flags, first, a.n, a.vec_flags, f);
-            s1 = clause_bits(a.pred.c[0], f) & clause_bits(a.pred.c[1], f);
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                const uint64_t i = seg + static_cast<uint64_t>(kWave) * j + lane;
+                f[j] = i < a.n ? a.flags[i] : P(0);
+            }
+            s1 = clause_bits<P, ITEMS, M>(a.pred.c[0], f) & clause_bits<P, ITEMS, M>(a.pred.c[1], f);
         } else {
-            s1 = clause_bits(a.pred.c[0], t.x) & clause_bits(a.pred.c[1], t.x);
-            if constexpr (MODE == kThreeWay) s2 = clause_bits(a.pred2.c[0], t.x) & clause_bits(a.pred2.c[1], t.x);
+            s1 = clause_bits<P, ITEMS, M>(a.pred.c[0], t.x) & clause_bits<P, ITEMS, M>(a.pred.c[1], t.x);
+            if constexpr (MODE == kThreeWay)
+                s2 = clause_bits<P, ITEMS, M>(a.pred2.c[0], t.x) & clause_bits<P, ITEMS, M>(a.pred2.c[1], t.x);
         }
         t.sel = s1 & valid;
         t.sel2 = s2 & ~s1 & valid;
     } else {
-        if constexpr (MODE == kUniqueByKey) load_run<V, ITEMS>(a.values_in, first, a.n, a.vec_values, t.v);
-        U prev = first > 0 && first - 1 < a.n ? a.in[first - 1] : t.x[0];
-        uint32_t heads = 0;
+        // Item i starts a run when i == 0 or it differs from item i - 1: lane l - 1's item j, lane 63's
+        // item j - 1, or the item before the segment.
+        U carry = seg > 0 && seg - 1 < a.n ? a.in[seg - 1] : U(0);
+        M heads = 0;
 #pragma unroll
-        for (int k = 0; k < ITEMS; ++k) {
-            const bool head = (first + k == 0) || !keys_equal(t.x[k], prev, a.key_mask);
-            heads |= (head ? 1u : 0u) << k;
-            prev = t.x[k];
+        for (int j = 0; j < ITEMS; ++j) {
+            const U prev = dpp_move<dpp::kWaveShr1>(carry, t.x[j]);
+            const uint64_t i = seg + static_cast<uint64_t>(kWave) * j + lane;
+            const bool head = i == 0 || !keys_equal(t.x[j], prev, a.key_mask);
+            heads |= static_cast<M>(head ? 1 : 0) << j;
+            carry = wave_read_lane(t.x[j], kWave - 1);
         }
         heads &= valid;
         t.heads = heads;
         if constexpr (MODE == kUnique || MODE == kUniqueByKey) {
             t.sel = heads;
         } else {
-            // Heads of the following items: bit k is the head flag of item first + k + 1.
-            const uint64_t next_i = first + ITEMS;
-            const bool next_head = next_i < a.n && !keys_equal(a.in[next_i], t.x[ITEMS - 1], a.key_mask);
-            const uint32_t next_heads = (heads >> 1) | ((next_head ? 1u : 0u) << (ITEMS - 1));
-            // Bit of the input's last item, if this thread holds it.
-            const uint32_t last = (first < a.n && a.n - first <= static_cast<uint64_t>(ITEMS))
-                                      ? (1u << (a.n - first - 1))
-                                      : 0u;
-            const uint32_t ends = valid & (next_heads | last);
+            // Item i ends a run when it is the last item or item i + 1 is a head: lane l + 1's item j,
+            // lane 0's item j + 1, or the item after the segment.
+            const uint64_t after = seg + static_cast<uint64_t>(kWave) * ITEMS;
+            const bool after_head = after < a.n && !keys_equal(a.in[after], wave_read_lane(t.x[ITEMS - 1], kWave - 1),
+                                                               a.key_mask);
+            const M top = (wave_read_lane(heads, 0) >> 1) | (static_cast<M>(after_head ? 1 : 0) << (ITEMS - 1));
+            const M next_heads = dpp_move<dpp::kWaveShl1>(top, heads);
+            M last = 0;
+            if (a.n > seg && a.n - 1 - seg < static_cast<uint64_t>(kWave) * ITEMS &&
+                (a.n - 1 - seg) % kWave == lane)
+                last = static_cast<M>(1) << ((a.n - 1 - seg) / kWave);
+            const M ends = valid & (next_heads | last);
             if constexpr (MODE == kEncode) {
                 t.sel = heads;
                 t.sel2 = ends;
@@ -270,41 +272,44 @@ __device__ __forceinline__ uint32_t combine_word(int w, uint32_t older, uint32_t
     return older + newer;
 }
 
-// The thread's count words: selected items (and second category), or run heads / non-trivial starts
-// and the position of the thread's last run head (0 when it has none).
-template <int MODE, typename U, typename V, int ITEMS>
-__device__ __forceinline__ void thread_words(const ThreadItems<U, V, ITEMS>& t, uint64_t first, uint32_t (&w)[kWords<MODE>]) {
-    w[0] = static_cast<uint32_t>(__builtin_popcount(t.sel));
-    if constexpr (MODE == kThreeWay) {
-        w[1] = static_cast<uint32_t>(__builtin_popcount(t.sel2));
-    } else if constexpr (kWord1Max<MODE>) {
-        w[1] = t.heads ? static_cast<uint32_t>(first + 31 - __builtin_clz(t.heads)) : 0u;
+template <typename M>
+__device__ __forceinline__ uint32_t popcount(M m) {
+    if constexpr (sizeof(M) == 8) {
+        return static_cast<uint32_t>(__builtin_popcountll(m));
+    } else {
+        return static_cast<uint32_t>(__builtin_popcount(m));
     }
 }
 
-// Exclusive prefix of each thread's words within the tile, and the tile aggregate.  Called by every
-// thread; barriers on both sides of the use of s_wave.
+// The wave's count words: selected items (and the second category), or run heads / non-trivial
+// starts and the position of the wave's last run head (0 when it has none).  Uniform results.
+template <int MODE, typename U, typename V, int ITEMS>
+__device__ __forceinline__ void wave_words(const LaneItems<U, V, ITEMS>& t, uint64_t seg, uint32_t (&w)[kWords<MODE>]) {
+    w[0] = wave_reduce(popcount(t.sel), SumOp{});
+    if constexpr (MODE == kThreeWay) {
+        w[1] = wave_reduce(popcount(t.sel2), SumOp{});
+    } else if constexpr (kWord1Max<MODE>) {
+        uint32_t last = 0;
+        if (t.heads) {
+            const int j = static_cast<int>(sizeof(t.heads) == 8 ? 63 - __builtin_clzll(static_cast<uint64_t>(t.heads))
+                                                                : 31 - __builtin_clz(static_cast<uint32_t>(t.heads)));
+            last = static_cast<uint32_t>(seg + static_cast<uint64_t>(kWave) * j + lane_id());
+        }
+        w[1] = wave_reduce(last, MaxU32Op{});
+    }
+}
+
+// Combines the waves' words: each wave's prefix within the tile and the tile aggregate.  Called by
+// every thread; barriers on both sides of the use of s_wave.
 template <int MODE>
-__device__ __forceinline__ void block_scan_words(const uint32_t (&x)[kWords<MODE>],
-                                                 uint32_t (*s_wave)[kCpWaves], uint32_t (&ex)[kWords<MODE>],
-                                                 uint32_t (&agg)[kWords<MODE>]) {
+__device__ __forceinline__ void block_words(const uint32_t (&x)[kWords<MODE>], uint32_t (*s_wave)[kCpWaves],
+                                            uint32_t (&wave_prefix)[kWords<MODE>], uint32_t (&agg)[kWords<MODE>]) {
     constexpr int W = kWords<MODE>;
     const uint32_t wave = threadIdx.x / kWave;
-    uint32_t inc[W];
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-        if (kWord1Max<MODE> && w == 1) {
-            inc[w] = wave_inclusive_scan(x[w], MaxU32Op{});
-            ex[w] = wave_shift_exclusive<uint32_t, MaxU32Op>(inc[w]);
-        } else {
-            inc[w] = wave_inclusive_scan(x[w], SumOp{});
-            ex[w] = wave_shift_exclusive<uint32_t, SumOp>(inc[w]);
-        }
-    }
     __syncthreads();
-    if (lane_id() == kWave - 1) {
+    if (lane_id() == 0) {
 #pragma unroll
-        for (int w = 0; w < W; ++w) s_wave[w][wave] = inc[w];
+        for (int w = 0; w < W; ++w) s_wave[w][wave] = x[w];
     }
     __syncthreads();
 #pragma unroll
@@ -315,7 +320,7 @@ __device__ __forceinline__ void block_scan_words(const uint32_t (&x)[kWords<MODE
             if (static_cast<uint32_t>(j) == wave) prefix = total;
             total = combine_word<MODE>(w, total, s_wave[w][j]);
         }
-        ex[w] = combine_word<MODE>(w, prefix, ex[w]);
+        wave_prefix[w] = prefix;
         agg[w] = total;
     }
 }
@@ -347,12 +352,12 @@ template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS>
 __device__ void tile_aggregate(const CompactArgs<U, P, V>& a, uint32_t tile, uint32_t (*s_wave)[kCpWaves],
                                uint32_t (&agg)[kWords<MODE>]) {
     constexpr uint64_t kTile = static_cast<uint64_t>(kCpBlock) * ITEMS;
-    const uint64_t first = static_cast<uint64_t>(tile) * kTile + static_cast<uint64_t>(threadIdx.x) * ITEMS;
-    ThreadItems<U, V, ITEMS> t;
-    load_thread<U, P, V, MODE, FLAGS, ITEMS>(a, first, t);
-    uint32_t w[kWords<MODE>], ex[kWords<MODE>];
-    thread_words<MODE>(t, first, w);
-    block_scan_words<MODE>(w, s_wave, ex, agg);
+    const uint64_t seg = static_cast<uint64_t>(tile) * kTile + static_cast<uint64_t>(threadIdx.x / kWave) * kWave * ITEMS;
+    LaneItems<U, V, ITEMS> t;
+    load_lane<U, P, V, MODE, FLAGS, ITEMS>(a, seg, t);
+    uint32_t w[kWords<MODE>], wp[kWords<MODE>];
+    wave_words<MODE>(t, seg, w);
+    block_words<MODE>(w, s_wave, wp, agg);
 }
 
 template <typename U, typename P, typename V, int MODE, bool FLAGS>
@@ -360,8 +365,8 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
     constexpr int ITEMS = kCpItems<U, V>;
     constexpr int W = kWords<MODE>;
     constexpr uint64_t kTile = static_cast<uint64_t>(kCpBlock) * ITEMS;
-    constexpr size_t kStageBytes = kTile * (sizeof(U) > sizeof(V) ? sizeof(U) : sizeof(V));
     constexpr uint32_t kPublisher = kCpBlock - kWave;
+    constexpr size_t kStageBytes = kTile * (sizeof(U) > sizeof(V) ? sizeof(U) : sizeof(V));
     __shared__ __align__(16) unsigned char s_stage[kStageBytes];
     __shared__ uint32_t s_wave[W][kCpWaves];
     __shared__ uint32_t s_ctl[2][2];
@@ -373,14 +378,13 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t tile = blockIdx.x;
-    const uint64_t tile_first = static_cast<uint64_t>(tile) * kTile;
-    const uint64_t first = tile_first + static_cast<uint64_t>(tid) * ITEMS;
+    const uint64_t seg = static_cast<uint64_t>(tile) * kTile + static_cast<uint64_t>(wave) * kWave * ITEMS;
 
-    ThreadItems<U, V, ITEMS> t;
-    load_thread<U, P, V, MODE, FLAGS, ITEMS>(a, first, t);
-    uint32_t words[W], ex[W], agg[W];
-    thread_words<MODE>(t, first, words);
-    block_scan_words<MODE>(words, s_wave, ex, agg);
+    LaneItems<U, V, ITEMS> t;
+    load_lane<U, P, V, MODE, FLAGS, ITEMS>(a, seg, t);
+    uint32_t words[W], wp[W], agg[W];
+    wave_words<MODE>(t, seg, words);
+    block_words<MODE>(words, s_wave, wp, agg);
 
     uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
     bool owned = true;
@@ -389,6 +393,51 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
         uint64_t expected = kClaimOpen;
         owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- staging --------------------------------------------------------------------------------
+    // Tile ranks are known before the look-back: row j of a wave puts its selected items at
+    // consecutive ranks (ballot ranks), staged in LDS without bank conflicts, while predecessors
+    // publish.  After the look-back the workgroup copies each category out with full-width stores.
+    U* const stage = reinterpret_cast<U*>(s_stage);
+    if constexpr (MODE == kEncode) {
+        uint32_t l1 = wp[0];
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const bool is_sel = (t.sel >> j) & 1;
+            const uint64_t sb = wave_ballot(is_sel);
+            if (is_sel) stage[l1 + popc_lanes_below(sb)] = t.x[j];
+            l1 += static_cast<uint32_t>(__builtin_popcountll(sb));
+        }
+    } else if constexpr (MODE != kNonTrivial) {
+        const bool rejects = (MODE == kSelect && a.partition) || MODE == kThreeWay;
+        uint32_t l1 = wp[0];
+        uint32_t l2 = 0;
+        if constexpr (MODE == kThreeWay) l2 = agg[0] + wp[1];
+        uint32_t base = agg[0];
+        if constexpr (MODE == kThreeWay) base += agg[1];
+        // Rejects before the wave's items within the tile (every earlier item of the tile is valid).
+        uint32_t lr = base + wave * kWave * ITEMS - wp[0];
+        if constexpr (MODE == kThreeWay) lr -= wp[1];
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const bool s1 = (t.sel >> j) & 1;
+            const uint64_t b1 = wave_ballot(s1);
+            if (s1) stage[l1 + popc_lanes_below(b1)] = t.x[j];
+            l1 += static_cast<uint32_t>(__builtin_popcountll(b1));
+            if constexpr (MODE == kThreeWay) {
+                const bool s2 = (t.sel2 >> j) & 1;
+                const uint64_t b2 = wave_ballot(s2);
+                if (s2) stage[l2 + popc_lanes_below(b2)] = t.x[j];
+                l2 += static_cast<uint32_t>(__builtin_popcountll(b2));
+            }
+            if (rejects) {
+                const bool r = ((t.valid & ~t.sel & ~t.sel2) >> j) & 1;
+                const uint64_t rb = wave_ballot(r);
+                if (r) stage[lr + popc_lanes_below(rb)] = t.x[j];
+                lr += static_cast<uint32_t>(__builtin_popcountll(rb));
+            }
+        }
     }
 
     uint32_t prefix[W];
@@ -430,8 +479,7 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
                                                                            : wave_reduce(mine, SumOp{});
                         acc[w] = combine_word<MODE>(w, window, acc[w]);
                     }
-                    const bool complete = stop_mask != 0;
-                    action = (complete || top < kWave) ? kActDone : kActAdvance;
+                    action = (stop_mask != 0 || top < kWave) ? kActDone : kActAdvance;
                 }
                 if (lane == 0) {
                     s_ctl[row][0] = action;
@@ -501,74 +549,63 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
         if constexpr (MODE == kThreeWay) a.num_out[1] = prefix[1] + agg[1];
     }
 
-    // ---- outputs ------------------------------------------------------------------------------
-    const uint64_t tile_valid = a.n - tile_first < kTile ? a.n - tile_first : kTile;
-    const uint32_t local0 = tid * ITEMS;  // tile-local index of the thread's first item
-    U* const stage = reinterpret_cast<U*>(s_stage);
-
+    // ---- outputs -------------------------------------------------------------------------------
+    // Run lengths and non-trivial run offsets (one store per run) are written directly.
     if constexpr (MODE == kEncode || MODE == kNonTrivial) {
-        uint32_t count = prefix[0] + ex[0];  // heads (encode) or non-trivial starts before the thread
-        uint32_t last = prefix[1] > ex[1] ? prefix[1] : ex[1];  // last head position before it
+        const uint64_t lanes_le = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1);
+        uint32_t k1 = prefix[0] + wp[0];  // heads / starts before the wave's items
+        uint32_t last = prefix[1] > wp[1] ? prefix[1] : wp[1];  // last head position before them
 #pragma unroll
-        for (int k = 0; k < ITEMS; ++k) {
-            const uint32_t i = static_cast<uint32_t>(first + k);
-            if ((t.heads >> k) & 1u) last = i;
-            if constexpr (MODE == kEncode) {
-                if ((t.sel >> k) & 1u) ++count;
-                if ((t.sel2 >> k) & 1u) a.aux0[count - 1] = i + 1 - last;
-            } else {
-                if ((t.sel >> k) & 1u) a.aux0[count++] = i;
-                if ((t.sel2 >> k) & 1u) a.aux1[count - 1] = i + 1 - last;
+        for (int j = 0; j < ITEMS; ++j) {
+            const bool is_sel = (t.sel >> j) & 1;
+            const bool is_end = (t.sel2 >> j) & 1;
+            const uint64_t hb = wave_ballot((t.heads >> j) & 1);
+            const uint64_t sb = wave_ballot(is_sel);
+            const uint32_t row_first = static_cast<uint32_t>(seg + static_cast<uint64_t>(kWave) * j);
+            const uint32_t i = row_first + lane;
+            if constexpr (MODE == kNonTrivial) {
+                if (is_sel) a.aux0[k1 + popc_lanes_below(sb)] = i;
             }
+            if (is_end) {
+                const uint64_t le = hb & lanes_le;
+                const uint32_t start = le ? row_first + static_cast<uint32_t>(63 - __builtin_clzll(le)) : last;
+                const uint32_t run = k1 + static_cast<uint32_t>(__builtin_popcountll(sb & lanes_le)) - 1;
+                if constexpr (MODE == kEncode) {
+                    a.aux0[run] = i + 1 - start;
+                } else {
+                    a.aux1[run] = i + 1 - start;
+                }
+            }
+            k1 += static_cast<uint32_t>(__builtin_popcountll(sb));
+            if (hb) last = row_first + static_cast<uint32_t>(63 - __builtin_clzll(hb));
         }
         if constexpr (MODE == kNonTrivial) return;
     }
-
-    // Stage: selected items at their tile rank; partition rejects, or the three-way categories,
-    // after them.
-    {
-        uint32_t r1 = ex[0];
-        uint32_t r2 = 0;
-        if constexpr (MODE == kThreeWay) r2 = ex[1];
-        const bool rejects = (MODE == kSelect && a.partition) || MODE == kThreeWay;
-#pragma unroll
-        for (int k = 0; k < ITEMS; ++k) {
-            const uint32_t bit = 1u << k;
-            if (t.sel & bit) {
-                stage[r1++] = t.x[k];
-            } else if (MODE == kThreeWay && (t.sel2 & bit)) {
-                stage[agg[0] + r2++] = t.x[k];
-            } else if (rejects && first + k < a.n) {
-                const uint32_t local = local0 + k;
-                uint32_t taken = r1;
-                if constexpr (MODE == kThreeWay) taken += r2;
-                uint32_t base = agg[0];
-                if constexpr (MODE == kThreeWay) base += agg[1];
-                stage[base + (local - taken)] = t.x[k];
-            }
-        }
-    }
-    __syncthreads();
-    U* const out = a.out;
-    for (uint32_t q = tid; q < agg[0]; q += kCpBlock) out[prefix[0] + q] = stage[q];
+    __syncthreads();  // staged items visible to every thread (tile 0 has no look-back barrier)
+    const uint64_t tile_first = static_cast<uint64_t>(tile) * kTile;
+    const uint32_t tile_valid = static_cast<uint32_t>(a.n - tile_first < kTile ? a.n - tile_first : kTile);
+    for (uint32_t q = tid; q < agg[0]; q += kCpBlock) a.out[prefix[0] + q] = stage[q];
     if constexpr (MODE == kThreeWay) {
         for (uint32_t q = tid; q < agg[1]; q += kCpBlock) a.out2[prefix[1] + q] = stage[agg[0] + q];
-        const uint32_t rejected = static_cast<uint32_t>(tile_valid) - agg[0] - agg[1];
+        const uint32_t rejected = tile_valid - agg[0] - agg[1];
         const uint64_t before = tile_first - prefix[0] - prefix[1];
         for (uint32_t q = tid; q < rejected; q += kCpBlock) a.out3[before + q] = stage[agg[0] + agg[1] + q];
     } else if constexpr (MODE == kSelect) {
         if (a.partition) {
-            const uint32_t rejected = static_cast<uint32_t>(tile_valid) - agg[0];
+            const uint32_t rejected = tile_valid - agg[0];
             const uint64_t before = tile_first - prefix[0];
-            for (uint32_t q = tid; q < rejected; q += kCpBlock) out[a.n - 1 - (before + q)] = stage[agg[0] + q];
+            for (uint32_t q = tid; q < rejected; q += kCpBlock) a.out[a.n - 1 - (before + q)] = stage[agg[0] + q];
         }
     } else if constexpr (MODE == kUniqueByKey) {
         __syncthreads();
         V* const vstage = reinterpret_cast<V*>(s_stage);
-        uint32_t r1 = ex[0];
+        uint32_t r1 = wp[0];
 #pragma unroll
-        for (int k = 0; k < ITEMS; ++k) {
-            if ((t.sel >> k) & 1u) vstage[r1++] = t.v[k];
+        for (int j = 0; j < ITEMS; ++j) {
+            const bool s1 = (t.sel >> j) & 1;
+            const uint64_t b1 = wave_ballot(s1);
+            if (s1) vstage[r1 + popc_lanes_below(b1)] = t.v[j];
+            r1 += static_cast<uint32_t>(__builtin_popcountll(b1));
         }
         __syncthreads();
         for (uint32_t q = tid; q < agg[0]; q += kCpBlock) a.values_out[prefix[0] + q] = vstage[q];
@@ -593,8 +630,6 @@ __global__ __launch_bounds__(256) void reverse_rejects_kernel(U* __restrict__ ds
     for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < u; j += stride)
         dst[u - 1 - j] = src[j];
 }
-
-bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
     if (!a || !b || a_bytes == 0 || b_bytes == 0) return false;
@@ -714,9 +749,6 @@ int run_compact(const char* what, void* temp, size_t temp_bytes, const U* in, co
     a.pred2 = pred2;
     a.spin_limit = g_lookback_spin_limit;
     a.partition = partition;
-    a.vec_in = aligned16(in);
-    a.vec_flags = FLAGS && aligned16(flags);
-    a.vec_values = MODE == kUniqueByKey && aligned16(values_in);
 
     int st = launch_fill_u32(reinterpret_cast<uint32_t*>(temp), plan.state_bytes / 4, 0u, stream);
     if (st != kOk) return st;
