@@ -3,6 +3,8 @@
 // user would call them (CommandList recording, commit on a Stream, host checks with std:: algorithms).
 //
 // Case sources: tests/device_reduce_test.cpp:95-173,425-514, tests/device_scan_test.cpp:80-447,
+// tests/device_select_test.cpp:248-500, tests/device_partition_test.cpp:103-377,
+// tests/device_run_length_encode_test.cpp:172-340,
 // tests/device_radix_sort_interface_test.cpp:68-283, tests/device_radix_sort_one_sweep.cpp:79-333,
 // tests/device_spmv_test.cpp:41-203 and the bench generators of tests/lcpp_cub_bench.cpp:516-521,
 // 666-672, 814.
@@ -68,7 +70,13 @@ struct Env {
     DeviceScan<> scan;
     DeviceRadixSort<> radix_sort;
     DeviceSpmv<> spmv;
+    DeviceSelect<> select;
+    DevicePartition<> partition;
+    DeviceRunLengthEncode<> rle;
     Env() : device(context.create_device("hip")), stream(device.create_stream()) {
+        select.create(device);
+        partition.create(device);
+        rle.create(device);
         reduce.create(device, &stream);
         scan.create(device, &stream);
         radix_sort.create(device, &stream);
@@ -597,6 +605,196 @@ void reduce_by_key_empty_input() {
     EXPECT(runs == 0u);
 }
 
+// ---- stream compaction ----------------------------------------------------------------------------
+
+template <typename T>
+std::vector<T> download(Env& e, Buffer<T>& b, size_t n) {
+    std::vector<T> h(n);
+    if (n) e.stream << b.view(0, n).copy_to(luisa::span{h}) << synchronize();
+    return h;
+}
+
+uint read_count(Env& e, Buffer<uint>& b, size_t i = 0) {
+    uint v = 0;
+    e.stream << b.view(i, 1).copy_to(&v) << synchronize();
+    return v;
+}
+
+// tests/device_select_test.cpp:248-299.
+void select_flagged_and_if_are_stable() {
+    auto& e = *g_env;
+    constexpr uint n = 17u;
+    std::vector<int> in(n);
+    std::vector<uint> flags(n);
+    for (uint i = 0; i < n; ++i) {
+        in[i] = static_cast<int>(100u + i);
+        flags[i] = i % 3u == 1u ? 7u : 0u;
+    }
+    auto ib = e.device.create_buffer<int>(n), fo = e.device.create_buffer<int>(n), io = e.device.create_buffer<int>(n);
+    auto fb = e.device.create_buffer<uint>(n);
+    auto fc = e.device.create_buffer<uint>(1), ic = e.device.create_buffer<uint>(1);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceSelect<>::GetTempStorageBytes(n)));
+    CommandList cmd;
+    e.select.Flagged(cmd, temp.view(), ib.view(), fb.view(), fo.view(), fc.view(), n);
+    e.select.If(cmd, temp.view(), ib.view(), io.view(), ic.view(), n, ItemPredicate<int>::remainder_equal(2, 0));
+    e.stream << ib.copy_from(luisa::span{in}) << fb.copy_from(luisa::span{flags}) << cmd.commit() << synchronize();
+    std::vector<int> want_f, want_i;
+    for (uint i = 0; i < n; ++i) {
+        if (flags[i]) want_f.push_back(in[i]);
+        if (in[i] % 2 == 0) want_i.push_back(in[i]);
+    }
+    const uint kf = read_count(e, fc), ki = read_count(e, ic);
+    EXPECT(kf == want_f.size() && ki == want_i.size());
+    EXPECT(download(e, fo, kf) == want_f);
+    EXPECT(download(e, io, ki) == want_i);
+}
+
+// tests/device_select_test.cpp:301-357 and :359-425.
+void select_unique_by_key_and_flagged_if() {
+    auto& e = *g_env;
+    const std::vector<int> keys{1, 1, 2, 2, 2, 4, 7, 7, 9}, vals{10, 11, 20, 21, 22, 40, 70, 71, 90};
+    const uint n = static_cast<uint>(keys.size());
+    auto kb = e.device.create_buffer<int>(n), vb = e.device.create_buffer<int>(n), uo = e.device.create_buffer<int>(n);
+    auto ko = e.device.create_buffer<int>(n), vo = e.device.create_buffer<int>(n);
+    auto c1 = e.device.create_buffer<uint>(1), c2 = e.device.create_buffer<uint>(1);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceSelect<>::GetTempStorageBytes(n)));
+    CommandList cmd;
+    e.select.Unique(cmd, temp.view(), kb.view(), uo.view(), c1.view(), n);
+    e.select.UniqueByKey(cmd, temp.view(), kb.view(), vb.view(), ko.view(), vo.view(), c2.view(), n);
+    e.stream << kb.copy_from(luisa::span{keys}) << vb.copy_from(luisa::span{vals}) << cmd.commit() << synchronize();
+    EXPECT(read_count(e, c1) == 5u && read_count(e, c2) == 5u);
+    EXPECT((download(e, uo, 5) == std::vector<int>{1, 2, 4, 7, 9}));
+    EXPECT((download(e, ko, 5) == std::vector<int>{1, 2, 4, 7, 9}));
+    EXPECT((download(e, vo, 5) == std::vector<int>{10, 20, 40, 70, 90}));
+
+    const std::vector<int> data{100, 101, 102, 103, 104, 105, 106, 107, 108}, flags{-3, -2, -1, 0, 1, 2, 3, 4, 5};
+    auto db = e.device.create_buffer<int>(9), ip = e.device.create_buffer<int>(9), fl = e.device.create_buffer<int>(9);
+    auto co = e.device.create_buffer<int>(9);
+    auto cc = e.device.create_buffer<uint>(1), pc = e.device.create_buffer<uint>(1);
+    const auto positive_odd = ItemPredicate<int>::greater(0) && ItemPredicate<int>::remainder_not_equal(2, 0);
+    CommandList cmd2;
+    e.select.FlaggedIf(cmd2, temp.view(), db.view(), fl.view(), co.view(), cc.view(), 9u, positive_odd);
+    e.select.FlaggedIf(cmd2, temp.view(), ip.view(), fl.view(), pc.view(), 9u, positive_odd);
+    e.stream << db.copy_from(luisa::span{data}) << ip.copy_from(luisa::span{data}) << fl.copy_from(luisa::span{flags})
+             << cmd2.commit() << synchronize();
+    EXPECT(read_count(e, cc) == 3u && read_count(e, pc) == 3u);
+    EXPECT((download(e, co, 3) == std::vector<int>{104, 106, 108}));
+    EXPECT((download(e, ip, 3) == std::vector<int>{104, 106, 108}));
+    EXPECT(download(e, db, 9) == data);
+}
+
+// tests/device_select_test.cpp:427-500: in-place forms, flags aliased with the data, empty input.
+void select_in_place_forms() {
+    auto& e = *g_env;
+    const std::vector<int> aliased{0, 2, 0, 3, 4, 0, 5, 0}, pred{-3, 4, -1, 6, 0, 2, 7, -8};
+    const std::vector<int> uniq{1, 3, 2, 4, 5, 7, 8, 10}, dflt{1, 1, 2, 2, 2, 4, 4, 9};
+    auto ab = e.device.create_buffer<int>(8), pb = e.device.create_buffer<int>(8);
+    auto ub = e.device.create_buffer<int>(8), db = e.device.create_buffer<int>(8);
+    auto counts = e.device.create_buffer<uint>(5);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceSelect<>::GetTempStorageBytes(8)));
+    const uint ones[5] = {9, 9, 9, 9, 9};
+    CommandList cmd;
+    e.select.Flagged(cmd, temp.view(), ab.view(), ab.view(), counts.view(0, 1), 8u);
+    e.select.If(cmd, temp.view(), pb.view(), counts.view(1, 1), 8u, ItemPredicate<int>::greater(0));
+    e.select.Unique(cmd, temp.view(), ub.view(), counts.view(2, 1), 8u, KeyMaskEquality{1u});
+    e.select.Unique(cmd, temp.view(), db.view(), counts.view(3, 1), 8u);
+    e.select.If(cmd, BufferView<uint>{}, BufferView<int>{}, counts.view(4, 1), 0u, ItemPredicate<int>::greater(0));
+    e.stream << ab.copy_from(luisa::span{aliased}) << pb.copy_from(luisa::span{pred}) << ub.copy_from(luisa::span{uniq})
+             << db.copy_from(luisa::span{dflt}) << counts.copy_from(static_cast<const void*>(ones)) << cmd.commit()
+             << synchronize();
+    EXPECT((download(e, ab, read_count(e, counts, 0)) == std::vector<int>{2, 3, 4, 5}));
+    EXPECT((download(e, pb, read_count(e, counts, 1)) == std::vector<int>{4, 6, 2, 7}));
+    EXPECT((download(e, ub, read_count(e, counts, 2)) == std::vector<int>{1, 2, 5, 8}));
+    EXPECT((download(e, db, read_count(e, counts, 3)) == std::vector<int>{1, 2, 4, 9}));
+    EXPECT(read_count(e, counts, 4) == 0u);
+}
+
+// tests/device_partition_test.cpp:103-177 and :292-377.
+void partition_ordering_and_three_way() {
+    auto& e = *g_env;
+    constexpr uint n = 12u;
+    std::vector<int> in(n);
+    std::vector<uint> flags(n);
+    for (uint i = 0; i < n; ++i) {
+        in[i] = static_cast<int>(i);
+        flags[i] = i % 3u == 0u ? 1u : 0u;
+    }
+    auto ib = e.device.create_buffer<int>(n), fo = e.device.create_buffer<int>(n), po = e.device.create_buffer<int>(n);
+    auto fb = e.device.create_buffer<uint>(n);
+    auto o1 = e.device.create_buffer<int>(n), o2 = e.device.create_buffer<int>(n), o3 = e.device.create_buffer<int>(n);
+    auto counts = e.device.create_buffer<uint>(6);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DevicePartition<>::GetThreeWayTempStorageBytes(n)));
+    const uint nines[6] = {9, 9, 9, 9, 9, 9};
+    CommandList cmd;
+    e.partition.Flagged(cmd, temp.view(), ib.view(), fb.view(), fo.view(), counts.view(0, 1), n);
+    e.partition.If(cmd, temp.view(), ib.view(), po.view(), counts.view(1, 1), n, ItemPredicate<int>::less(7));
+    e.partition.If(cmd, temp.view(), ib.view(), o1.view(), o2.view(), o3.view(), counts.view(2, 2), n,
+                   ItemPredicate<int>::remainder_equal(3, 0), ItemPredicate<int>::less(8));
+    e.partition.If(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, BufferView<int>{}, BufferView<int>{},
+                   counts.view(4, 2), 0u, ItemPredicate<int>::less(0), ItemPredicate<int>::greater(0));
+    e.stream << ib.copy_from(luisa::span{in}) << fb.copy_from(luisa::span{flags})
+             << counts.copy_from(static_cast<const void*>(nines)) << cmd.commit() << synchronize();
+    EXPECT(read_count(e, counts, 0) == 4u && read_count(e, counts, 1) == 7u);
+    EXPECT((download(e, fo, n) == std::vector<int>{0, 3, 6, 9, 11, 10, 8, 7, 5, 4, 2, 1}));
+    EXPECT((download(e, po, n) == std::vector<int>{0, 1, 2, 3, 4, 5, 6, 11, 10, 9, 8, 7}));
+    EXPECT(read_count(e, counts, 2) == 4u && read_count(e, counts, 3) == 5u);
+    EXPECT((download(e, o1, 4) == std::vector<int>{0, 3, 6, 9}));
+    EXPECT((download(e, o2, 5) == std::vector<int>{1, 2, 4, 5, 7}));
+    EXPECT((download(e, o3, 3) == std::vector<int>{11, 10, 8}));
+    EXPECT(read_count(e, counts, 4) == 0u && read_count(e, counts, 5) == 0u);
+}
+
+// tests/device_run_length_encode_test.cpp:172-340: CUB's example, 180 runs of length run % 7 + 1,
+// and zero counts for empty input.
+void run_length_encode_examples() {
+    auto& e = *g_env;
+    std::vector<int> in{0, 2, 2, 9, 5, 5, 5, 8};
+    std::vector<int> want_u{0, 2, 9, 5, 8};
+    std::vector<uint> want_c{1, 2, 1, 3, 1}, want_o{1, 4}, want_l{2, 3};
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) {
+            in.clear();
+            want_u.clear();
+            want_c.clear();
+            want_o.clear();
+            want_l.clear();
+            for (uint run = 0; run < 180u; ++run) {
+                const uint len = run % 7u + 1u;
+                want_u.push_back(static_cast<int>(run));
+                want_c.push_back(len);
+                if (len > 1u) {
+                    want_o.push_back(static_cast<uint>(in.size()));
+                    want_l.push_back(len);
+                }
+                for (uint k = 0; k < len; ++k) in.push_back(static_cast<int>(run));
+            }
+        }
+        const uint n = static_cast<uint>(in.size());
+        auto ib = e.device.create_buffer<int>(n), uo = e.device.create_buffer<int>(n);
+        auto co = e.device.create_buffer<uint>(n), oo = e.device.create_buffer<uint>(n), lo = e.device.create_buffer<uint>(n);
+        auto counts = e.device.create_buffer<uint>(2);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceRunLengthEncode<>::GetTempStorageBytes(n)));
+        CommandList cmd;
+        e.rle.Encode(cmd, temp.view(), ib.view(), uo.view(), co.view(), counts.view(0, 1), n);
+        e.rle.NonTrivialRuns(cmd, temp.view(), ib.view(), oo.view(), lo.view(), counts.view(1, 1), n);
+        e.stream << ib.copy_from(luisa::span{in}) << cmd.commit() << synchronize();
+        const uint runs = read_count(e, counts, 0), nt = read_count(e, counts, 1);
+        EXPECT(runs == want_u.size() && nt == want_o.size());
+        EXPECT(download(e, uo, runs) == want_u);
+        EXPECT(download(e, co, runs) == want_c);
+        EXPECT(download(e, oo, nt) == want_o);
+        EXPECT(download(e, lo, nt) == want_l);
+    }
+    auto counts = e.device.create_buffer<uint>(2);
+    const uint nines[2] = {99, 99};
+    CommandList cmd;
+    e.rle.Encode(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, BufferView<uint>{}, counts.view(0, 1), 0u);
+    e.rle.NonTrivialRuns(cmd, BufferView<uint>{}, BufferView<int>{}, BufferView<uint>{}, BufferView<uint>{},
+                         counts.view(1, 1), 0u);
+    e.stream << counts.copy_from(static_cast<const void*>(nines)) << cmd.commit() << synchronize();
+    EXPECT(read_count(e, counts, 0) == 0u && read_count(e, counts, 1) == 0u);
+}
+
 // ---- record-time checks ------------------------------------------------------------------------
 
 void precondition_errors() {
@@ -608,6 +806,13 @@ void precondition_errors() {
     EXPECT(throws_error([&] { e.scan.ExclusiveSum(cmd, small.view(), a.view(), a.view(), n); }));
     EXPECT(throws_error([&] { e.reduce.Sum(cmd, small.view(), a.view(), a.view(), n); }));
     EXPECT(throws_error([&] { e.scan.ExclusiveSumByKey(cmd, small.view(), a.view(), a.view(), a.view(), n); }));
+    EXPECT(throws_error([&] { e.select.Flagged(cmd, small.view(), a.view(), a.view(), a.view(), small.view(), n); }));
+    EXPECT(throws_error([&] {
+        e.partition.If(cmd, small.view(), a.view(), a.view(), small.view(), n, ItemPredicate<uint>::less(3u));
+    }));
+    EXPECT(throws_error([&] { e.rle.Encode(cmd, small.view(), a.view(), a.view(), a.view(), small.view(), n); }));
+    DeviceSelect<> no_select;
+    EXPECT(throws_error([&] { no_select.Unique(cmd, small.view(), a.view(), small.view(), 1u); }));
     EXPECT(throws_error(
         [&] { e.reduce.ReduceByKey(cmd, small.view(), a.view(), a.view(), a.view(), a.view(), small.view(), SumOp{}, n); }));
     EXPECT(throws_error([&] {
@@ -646,6 +851,11 @@ const std::vector<Case>& cases() {
         {"scan_by_key_initial_values_float_in_place", scan_by_key_initial_values_float_in_place},
         {"reduce_by_key_segments_of_100", reduce_by_key_segments_of_100},
         {"reduce_by_key_empty_input", reduce_by_key_empty_input},
+        {"select_flagged_and_if_are_stable", select_flagged_and_if_are_stable},
+        {"select_unique_by_key_and_flagged_if", select_unique_by_key_and_flagged_if},
+        {"select_in_place_forms", select_in_place_forms},
+        {"partition_ordering_and_three_way", partition_ordering_and_three_way},
+        {"run_length_encode_examples", run_length_encode_examples},
         {"spmv_float_unsigned_indices", spmv_float_unsigned_indices},
         {"spmv_int_values_and_empty_work", spmv_int_values_and_empty_work},
         {"precondition_errors", precondition_errors},
