@@ -329,6 +329,60 @@ LCPP_HIP_DECLARE_SELECT_ITEMS(f64, double)
 #undef LCPP_HIP_DECLARE_SELECT_FLAGS
 
 /* ---------------------------------------------------------------------------------------------
+ * Segmented reductions and scans: DeviceSegmentReduce, DeviceSegmentedScan.
+ * Replaces DeviceSegmentReduce<>::Sum / Min / Max (begin/end offsets or fixed segment_size) and
+ * ArgMin / ArgMax (device_segment_reduce.h:87-420) and DeviceSegmentedScan<>::ExclusiveSegmentedSum /
+ * InclusiveSegmentedSum / InclusiveSegmentedScanInit with the sum operator
+ * (device_segmented_scan.h:52-224).  Segment s covers input[begin[s], end[s]); a segment with
+ * begin >= end is empty and reduces to the initial value (0 for Sum, the type's max for Min, lowest for
+ * Max; ArgMin / ArgMax write that value with index 1, details/segment_reduce.h:138-146).  Arg indices
+ * are relative to the segment's begin, ties go to the lower index.  Scans write
+ * output[out_begin[s] + k] (out_begin_offsets may be NULL: the input offsets), exclusive scans start
+ * from init; in-place (output == input, same offsets) is allowed.  Integer sums wrap; float Min / Max
+ * ignore NaN operands.  Temp storage: none (the Arg query returns the reference's figure).
+ * Suffixes: Sum / Min / Max / scans i32 u32 f32 i64 u64 f64; ArgMin / ArgMax i32 u32 f32.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_segment_reduce_temp_bytes(uint64_t n);
+size_t lcpp_hip_segment_reduce_arg_temp_bytes(uint64_t n, uint64_t num_segments);
+size_t lcpp_hip_segmented_scan_temp_bytes(uint64_t n, uint64_t num_segments);
+#define LCPP_HIP_DECLARE_SEGMENT_REDUCE(OPS, TS, TT)                                                                 \
+    int lcpp_hip_segment_reduce_##OPS##_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                 \
+                                             uint64_t num_segments, const uint32_t* begin_offsets,                 \
+                                             const uint32_t* end_offsets, void* stream);                           \
+    int lcpp_hip_segment_reduce_fixed_##OPS##_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,           \
+                                                   uint64_t num_segments, uint32_t segment_size, void* stream);
+#define LCPP_HIP_DECLARE_SEGMENT_ARG(OPS, TS, TT)                                                                    \
+    int lcpp_hip_segment_##OPS##_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out, uint32_t* index_out,   \
+                                      uint64_t num_segments, const uint32_t* begin_offsets,                        \
+                                      const uint32_t* end_offsets, void* stream);                                  \
+    int lcpp_hip_segment_fixed_##OPS##_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                  \
+                                            uint32_t* index_out, uint64_t num_segments, uint32_t segment_size,     \
+                                            void* stream);
+#define LCPP_HIP_DECLARE_SEGMENTED(TS, TT)                                                                           \
+    LCPP_HIP_DECLARE_SEGMENT_REDUCE(sum, TS, TT)                                                                     \
+    LCPP_HIP_DECLARE_SEGMENT_REDUCE(min, TS, TT)                                                                     \
+    LCPP_HIP_DECLARE_SEGMENT_REDUCE(max, TS, TT)                                                                     \
+    int lcpp_hip_segmented_scan_sum_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                     \
+                                         const uint32_t* begin_offsets, const uint32_t* end_offsets,               \
+                                         const uint32_t* out_begin_offsets, uint64_t num_segments, int inclusive,  \
+                                         int use_init, TT init, void* stream);
+LCPP_HIP_DECLARE_SEGMENTED(i32, int32_t)
+LCPP_HIP_DECLARE_SEGMENTED(u32, uint32_t)
+LCPP_HIP_DECLARE_SEGMENTED(f32, float)
+LCPP_HIP_DECLARE_SEGMENTED(i64, int64_t)
+LCPP_HIP_DECLARE_SEGMENTED(u64, uint64_t)
+LCPP_HIP_DECLARE_SEGMENTED(f64, double)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmin, i32, int32_t)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmin, u32, uint32_t)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmin, f32, float)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmax, i32, int32_t)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmax, u32, uint32_t)
+LCPP_HIP_DECLARE_SEGMENT_ARG(argmax, f32, float)
+#undef LCPP_HIP_DECLARE_SEGMENTED
+#undef LCPP_HIP_DECLARE_SEGMENT_ARG
+#undef LCPP_HIP_DECLARE_SEGMENT_REDUCE
+
+/* ---------------------------------------------------------------------------------------------
  * Seeded synthetic workloads for tests and benchmarks (no reference counterpart; the reference
  * generates on the host, e.g. tests/lcpp_cub_bench.cpp:516-521,666-672,814).
  * Stream: splitmix64, r_i = mix(seed + (start + i + 1) * 0x9E3779B97F4A7C15).

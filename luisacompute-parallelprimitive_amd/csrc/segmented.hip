@@ -1,0 +1,340 @@
+// DeviceSegmentReduce (Sum, Min, Max, ArgMin, ArgMax over begin/end offsets or fixed-size segments)
+// and DeviceSegmentedScan (exclusive / inclusive sums, optional initial value, separate output
+// offsets) for gfx950.
+//
+// Reference paths (src/lcpp/device/): DeviceSegmentReduce<> (device_segment_reduce.h:110-420): one
+// block per segment; an empty segment (begin == end) writes the initial value (0, the type's max for
+// Min, lowest for Max); otherwise reduce_op(initial, aggregate) (details/segment_reduce.h:120-165).
+// ArgMin / ArgMax reduce (global index, value) pairs with the lower index winning ties
+// (common/thread_operators.h:19-47) and report the index relative to the segment's begin; an empty
+// segment reports index 1 and the initial value (details/segment_reduce.h:141-146, 302-345).
+// DeviceSegmentedScan<> (device_segmented_scan.h:52-224): segment s scans input[begin[s], end[s]) into
+// output[out_begin[s] + k]; exclusive scans start from the initial value (0 for the Sum forms).
+//
+// MI355X design: one 256-thread workgroup per segment.  Reductions stream the segment with eight
+// loads in flight per thread (consecutive lanes read consecutive items), fold in registers, then a
+// wave shuffle reduction and a 4-wave combine in LDS.  Scans walk the segment in chunks of 1024
+// items: each thread folds 4 consecutive items, a DPP wave scan and the LDS wave totals give every
+// thread its chunk prefix, and a running carry crosses chunks.  Segments with begin >= end are
+// empty.  Integer sums wrap; float sums are ordered (per-thread folds, then a fixed tree).
+// Algorithmic traffic: reduce sizeof(T) per item + 8 bytes of offsets and sizeof(T) (+4) per segment;
+// scan 2 * sizeof(T) per item.
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+#include <limits>
+
+namespace lcpp_hip {
+namespace {
+
+constexpr int kSgBlock = 256;
+constexpr int kSgWaves = kSgBlock / kWave;
+constexpr int kSgUnroll = 8;
+constexpr int kScanItems = 4;  // consecutive items per thread and scan chunk
+
+enum : int { kOpSum = 0, kOpMin = 1, kOpMax = 2, kOpArgMin = 3, kOpArgMax = 4 };
+
+template <typename T>
+struct Arith {
+    using type = T;
+};
+template <>
+struct Arith<int32_t> {
+    using type = uint32_t;  // wrapping sums
+};
+template <>
+struct Arith<int64_t> {
+    using type = uint64_t;
+};
+
+template <typename T>
+__device__ __forceinline__ T add_wrap(T a, T b) {
+    using A = typename Arith<T>::type;
+    return static_cast<T>(static_cast<A>(a) + static_cast<A>(b));
+}
+
+template <typename T>
+struct Arg {
+    T value;
+    uint32_t index;
+};
+
+template <typename T, int OP>
+struct Reducer {
+    using Acc = std::conditional_t<(OP == kOpArgMin || OP == kOpArgMax), Arg<T>, T>;
+    __device__ __forceinline__ static Acc identity() {
+        if constexpr (OP == kOpSum) return T(0);
+        else if constexpr (OP == kOpMin) return std::numeric_limits<T>::max();
+        else if constexpr (OP == kOpMax) return std::numeric_limits<T>::lowest();
+        else if constexpr (OP == kOpArgMin) return Arg<T>{std::numeric_limits<T>::max(), 0xFFFFFFFFu};
+        else return Arg<T>{std::numeric_limits<T>::lowest(), 0xFFFFFFFFu};
+    }
+    __device__ __forceinline__ static Acc lift(T v, uint32_t i) {
+        if constexpr (OP == kOpArgMin || OP == kOpArgMax) return Arg<T>{v, i};
+        else return v;
+    }
+    __device__ __forceinline__ static Acc combine(Acc a, Acc b) {
+        if constexpr (OP == kOpSum) {
+            return add_wrap(a, b);
+        } else if constexpr (OP == kOpMin) {
+            if constexpr (std::is_floating_point_v<T>) return fmin(a, b);
+            else return b < a ? b : a;
+        } else if constexpr (OP == kOpMax) {
+            if constexpr (std::is_floating_point_v<T>) return fmax(a, b);
+            else return b > a ? b : a;
+        } else if constexpr (OP == kOpArgMin) {
+            return (b.value < a.value || (b.value == a.value && b.index < a.index)) ? b : a;
+        } else {
+            return (b.value > a.value || (b.value == a.value && b.index < a.index)) ? b : a;
+        }
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ T shfl_xor_any(T v, int mask) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __shfl_xor(__builtin_bit_cast(int, v), mask));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u)), mask));
+        const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u >> 32)), mask));
+        return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+}
+
+template <typename T, int OP>
+__device__ __forceinline__ typename Reducer<T, OP>::Acc wave_combine(typename Reducer<T, OP>::Acc x) {
+    using R = Reducer<T, OP>;
+#pragma unroll
+    for (int off = kWave / 2; off >= 1; off >>= 1) {
+        if constexpr (OP == kOpArgMin || OP == kOpArgMax) {
+            Arg<T> o;
+            o.value = shfl_xor_any(x.value, off);
+            o.index = static_cast<uint32_t>(__shfl_xor(static_cast<int>(x.index), off));
+            x = R::combine(x, o);
+        } else {
+            x = R::combine(x, shfl_xor_any(x, off));
+        }
+    }
+    return x;
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(kSgBlock) void segment_reduce_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                                  uint32_t* __restrict__ index_out,
+                                                                  const uint32_t* __restrict__ begins,
+                                                                  const uint32_t* __restrict__ ends,
+                                                                  uint64_t fixed_size) {
+    using R = Reducer<T, OP>;
+    using Acc = typename R::Acc;
+    constexpr bool ARG = OP == kOpArgMin || OP == kOpArgMax;
+    __shared__ Acc s_wave[kSgWaves];
+    const uint32_t seg = blockIdx.x;
+    uint64_t b, e;
+    if (begins) {
+        b = begins[seg];
+        e = ends[seg];
+    } else {
+        b = static_cast<uint64_t>(seg) * fixed_size;
+        e = b + fixed_size;
+    }
+    if (b >= e) {
+        if (threadIdx.x == 0) {
+            if constexpr (ARG) {
+                out[seg] = R::identity().value;
+                index_out[seg] = 1;
+            } else {
+                out[seg] = R::identity();
+            }
+        }
+        return;
+    }
+    Acc acc = R::identity();
+    uint64_t i = b + threadIdx.x;
+    for (; i + static_cast<uint64_t>(kSgUnroll - 1) * kSgBlock < e; i += static_cast<uint64_t>(kSgUnroll) * kSgBlock) {
+        T v[kSgUnroll];
+#pragma unroll
+        for (int k = 0; k < kSgUnroll; ++k) v[k] = in[i + static_cast<uint64_t>(k) * kSgBlock];
+#pragma unroll
+        for (int k = 0; k < kSgUnroll; ++k)
+            acc = R::combine(acc, R::lift(v[k], static_cast<uint32_t>(i + static_cast<uint64_t>(k) * kSgBlock)));
+    }
+    for (; i < e; i += kSgBlock) acc = R::combine(acc, R::lift(in[i], static_cast<uint32_t>(i)));
+    acc = wave_combine<T, OP>(acc);
+    const uint32_t wave = threadIdx.x / kWave;
+    if (lane_id() == 0) s_wave[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Acc total = s_wave[0];
+#pragma unroll
+        for (int w = 1; w < kSgWaves; ++w) total = R::combine(total, s_wave[w]);
+        if constexpr (ARG) {
+            out[seg] = total.value;
+            index_out[seg] = total.index - static_cast<uint32_t>(b);
+        } else {
+            out[seg] = total;
+        }
+    }
+}
+
+// Inclusive scan of one 32-/64-bit value per lane with wrapping or float addition.
+template <typename T>
+__device__ __forceinline__ T wave_scan_sum(T x) {
+    x = add_wrap(x, dpp_move<dpp::kRowShr1>(T(0), x));
+    x = add_wrap(x, dpp_move<dpp::kRowShr2>(T(0), x));
+    x = add_wrap(x, dpp_move<dpp::kRowShr4>(T(0), x));
+    x = add_wrap(x, dpp_move<dpp::kRowShr8>(T(0), x));
+    x = add_wrap(x, dpp_move<dpp::kRowBcast15, 0xa>(T(0), x));
+    x = add_wrap(x, dpp_move<dpp::kRowBcast31, 0xc>(T(0), x));
+    return x;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                                  const uint32_t* __restrict__ begins,
+                                                                  const uint32_t* __restrict__ ends,
+                                                                  const uint32_t* __restrict__ out_begins,
+                                                                  int inclusive, int use_init, T init) {
+    constexpr uint64_t kChunk = static_cast<uint64_t>(kSgBlock) * kScanItems;
+    __shared__ T s_wave[kSgWaves];
+    const uint32_t seg = blockIdx.x;
+    const uint64_t b = begins[seg];
+    const uint64_t e = ends[seg];
+    if (b >= e) return;
+    const uint64_t ob = out_begins[seg];
+    const uint32_t wave = threadIdx.x / kWave;
+    T carry = use_init ? init : T(0);
+    for (uint64_t c = b; c < e; c += kChunk) {
+        const uint64_t first = c + static_cast<uint64_t>(threadIdx.x) * kScanItems;
+        T v[kScanItems];
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) v[k] = first + k < e ? in[first + k] : T(0);
+        T own = v[0];
+#pragma unroll
+        for (int k = 1; k < kScanItems; ++k) own = add_wrap(own, v[k]);
+        const T inc = wave_scan_sum(own);
+        __syncthreads();  // earlier readers of s_wave are done
+        if (lane_id() == kWave - 1) s_wave[wave] = inc;
+        __syncthreads();
+        T before = T(0), total = T(0);
+#pragma unroll
+        for (int w = 0; w < kSgWaves; ++w) {
+            if (static_cast<uint32_t>(w) == wave) before = total;
+            total = add_wrap(total, s_wave[w]);
+        }
+        // Prefix of this thread's first item: carry + earlier waves + earlier lanes of this wave.
+        const T lanes_before = dpp_move<dpp::kWaveShr1>(T(0), inc);
+        T run = add_wrap(carry, add_wrap(before, lanes_before));
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            if (first + k < e) {
+                const T next = add_wrap(run, v[k]);
+                out[ob + (first + k - b)] = inclusive ? next : run;
+                run = next;
+            }
+        }
+        carry = add_wrap(carry, total);
+    }
+}
+
+unsigned checked_grid(uint64_t segments) { return static_cast<unsigned>(segments); }
+
+template <typename T, int OP>
+int segment_reduce(const T* in, T* out, uint32_t* index_out, uint64_t num_segments, const uint32_t* begins,
+                   const uint32_t* ends, uint64_t fixed_size, void* stream_ptr, const char* what) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (num_segments == 0) return kOk;
+    if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
+    if (!out || ((OP == kOpArgMin || OP == kOpArgMax) && !index_out))
+        return set_error(kInvalidArgument, "%s: null output", what);
+    if (!begins && fixed_size == 0) {
+        // Every fixed-size-0 segment is empty: the kernel writes the initial values without reading.
+    } else if (!in) {
+        return set_error(kInvalidArgument, "%s: null input", what);
+    }
+    if (!begins && num_segments * fixed_size > 0xFFFFFFFFull + 1)
+        return set_error(kInvalidArgument, "%s: segments exceed 2^32 items", what);
+    if (begins == nullptr && ends != nullptr) return set_error(kInvalidArgument, "%s: bad offsets", what);
+    LaunchScope scope("segment_reduce", stream);
+    segment_reduce_kernel<T, OP><<<checked_grid(num_segments), kSgBlock, 0, stream>>>(in, out, index_out, begins,
+                                                                                      ends, fixed_size);
+    return check_hip(hipGetLastError(), "segment_reduce launch");
+}
+
+template <typename T>
+int segmented_scan(const T* in, T* out, const uint32_t* begins, const uint32_t* ends, const uint32_t* out_begins,
+                   uint64_t num_segments, int inclusive, int use_init, T init, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const char* what = "DeviceSegmentedScan";
+    if (num_segments == 0) return kOk;
+    if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
+    if (!in || !out || !begins || !ends) return set_error(kInvalidArgument, "%s: null input or output", what);
+    LaunchScope scope("segmented_scan", stream);
+    segmented_scan_kernel<T><<<checked_grid(num_segments), kSgBlock, 0, stream>>>(
+        in, out, begins, ends, out_begins ? out_begins : begins, inclusive, use_init, init);
+    return check_hip(hipGetLastError(), "segmented_scan launch");
+}
+
+}  // namespace
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+#define LCPP_HIP_DEFINE_SEGMENT_REDUCE(OPS, OP, TS, TT)                                                               \
+    int lcpp_hip_segment_reduce_##OPS##_##TS(void*, size_t, const TT* in, TT* out, uint64_t num_segments,             \
+                                             const uint32_t* begin_offsets, const uint32_t* end_offsets,             \
+                                             void* stream) {                                                         \
+        if (num_segments && (!begin_offsets || !end_offsets))                                                        \
+            return set_error(kInvalidArgument, "DeviceSegmentReduce: null offsets");                                 \
+        return segment_reduce<TT, OP>(in, out, nullptr, num_segments, begin_offsets, end_offsets, 0, stream,          \
+                                      "DeviceSegmentReduce");                                                         \
+    }                                                                                                                 \
+    int lcpp_hip_segment_reduce_fixed_##OPS##_##TS(void*, size_t, const TT* in, TT* out, uint64_t num_segments,       \
+                                                   uint32_t segment_size, void* stream) {                            \
+        return segment_reduce<TT, OP>(in, out, nullptr, num_segments, nullptr, nullptr, segment_size, stream,         \
+                                      "DeviceSegmentReduce");                                                         \
+    }
+#define LCPP_HIP_DEFINE_SEGMENT_ARG(OPS, OP, TS, TT)                                                                  \
+    int lcpp_hip_segment_##OPS##_##TS(void*, size_t, const TT* in, TT* out, uint32_t* index_out,                     \
+                                      uint64_t num_segments, const uint32_t* begin_offsets,                          \
+                                      const uint32_t* end_offsets, void* stream) {                                   \
+        if (num_segments && (!begin_offsets || !end_offsets))                                                        \
+            return set_error(kInvalidArgument, "DeviceSegmentReduce: null offsets");                                 \
+        return segment_reduce<TT, OP>(in, out, index_out, num_segments, begin_offsets, end_offsets, 0, stream,        \
+                                      "DeviceSegmentReduce::Arg");                                                    \
+    }                                                                                                                 \
+    int lcpp_hip_segment_fixed_##OPS##_##TS(void*, size_t, const TT* in, TT* out, uint32_t* index_out,               \
+                                            uint64_t num_segments, uint32_t segment_size, void* stream) {            \
+        return segment_reduce<TT, OP>(in, out, index_out, num_segments, nullptr, nullptr, segment_size, stream,       \
+                                      "DeviceSegmentReduce::Arg");                                                    \
+    }
+#define LCPP_HIP_DEFINE_SEGMENTED(TS, TT)                                                                             \
+    LCPP_HIP_DEFINE_SEGMENT_REDUCE(sum, kOpSum, TS, TT)                                                               \
+    LCPP_HIP_DEFINE_SEGMENT_REDUCE(min, kOpMin, TS, TT)                                                               \
+    LCPP_HIP_DEFINE_SEGMENT_REDUCE(max, kOpMax, TS, TT)                                                               \
+    int lcpp_hip_segmented_scan_sum_##TS(void*, size_t, const TT* in, TT* out, const uint32_t* begin_offsets,         \
+                                         const uint32_t* end_offsets, const uint32_t* out_begin_offsets,             \
+                                         uint64_t num_segments, int inclusive, int use_init, TT init,                 \
+                                         void* stream) {                                                             \
+        return segmented_scan<TT>(in, out, begin_offsets, end_offsets, out_begin_offsets, num_segments, inclusive,    \
+                                  use_init, init, stream);                                                            \
+    }
+LCPP_HIP_DEFINE_SEGMENTED(i32, int32_t)
+LCPP_HIP_DEFINE_SEGMENTED(u32, uint32_t)
+LCPP_HIP_DEFINE_SEGMENTED(f32, float)
+LCPP_HIP_DEFINE_SEGMENTED(i64, int64_t)
+LCPP_HIP_DEFINE_SEGMENTED(u64, uint64_t)
+LCPP_HIP_DEFINE_SEGMENTED(f64, double)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmin, kOpArgMin, i32, int32_t)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmin, kOpArgMin, u32, uint32_t)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmin, kOpArgMin, f32, float)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmax, kOpArgMax, i32, int32_t)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmax, kOpArgMax, u32, uint32_t)
+LCPP_HIP_DEFINE_SEGMENT_ARG(argmax, kOpArgMax, f32, float)
+#undef LCPP_HIP_DEFINE_SEGMENTED
+#undef LCPP_HIP_DEFINE_SEGMENT_ARG
+#undef LCPP_HIP_DEFINE_SEGMENT_REDUCE
+
+}  // extern "C"

@@ -237,4 +237,16 @@ size_t lcpp_hip_run_length_encode_temp_bytes(uint64_t n) {
     return lcpp_hip_run_length_encode_temp_bytes_policy(n, 256, 4);
 }
 
+// DeviceSegmentReduce<>::GetTempStorageBytes (device_segment_reduce.h:87-91) and
+// DeviceSegmentedScan<>::GetTempStorageBytes (device_segmented_scan.h:52-56): no temp storage.
+size_t lcpp_hip_segment_reduce_temp_bytes(uint64_t) { return 0; }
+size_t lcpp_hip_segmented_scan_temp_bytes(uint64_t, uint64_t) { return 0; }
+
+// DeviceSegmentReduce<>::GetArgTempStorageBytes<T> (device_segment_reduce.h:95-104): n and
+// num_segments (index, value) pairs of 8 bytes, the second array 256-byte aligned.  The ArgMin / ArgMax
+// kernels here carve none of it.
+size_t lcpp_hip_segment_reduce_arg_temp_bytes(uint64_t n, uint64_t num_segments) {
+    return align_up(n * 8) + num_segments * 8;
+}
+
 }  // extern "C"

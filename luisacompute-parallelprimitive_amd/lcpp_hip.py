@@ -117,6 +117,18 @@ def _declare(lib: C.CDLL) -> None:
         for v in BY_KEY_VALUE_SUFFIXES:
             sig(f"lcpp_hip_scan_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, u64, i32, i32, _CTYPE[v], u64, vp)
             sig(f"lcpp_hip_reduce_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
+    sig("lcpp_hip_segment_reduce_temp_bytes", sz, u64)
+    sig("lcpp_hip_segment_reduce_arg_temp_bytes", sz, u64, u64)
+    sig("lcpp_hip_segmented_scan_temp_bytes", sz, u64, u64)
+    for t in SCALAR_SUFFIXES:
+        for op in ("sum", "min", "max"):
+            sig(f"lcpp_hip_segment_reduce_{op}_{t}", i32, vp, sz, vp, vp, u64, vp, vp, vp)
+            sig(f"lcpp_hip_segment_reduce_fixed_{op}_{t}", i32, vp, sz, vp, vp, u64, u32, vp)
+        sig(f"lcpp_hip_segmented_scan_sum_{t}", i32, vp, sz, vp, vp, vp, vp, vp, u64, i32, i32, _CTYPE[t], vp)
+    for t in SCAN_SUFFIXES:
+        for op in ("argmin", "argmax"):
+            sig(f"lcpp_hip_segment_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, vp, vp, vp)
+            sig(f"lcpp_hip_segment_fixed_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, u32, vp)
     pp = C.POINTER(Predicate)
     for name in ("select", "partition_three_way", "run_length_encode"):
         sig(f"lcpp_hip_{name}_temp_bytes", sz, u64)
@@ -444,3 +456,30 @@ def run_length_non_trivial(suffix: str, d_in, offsets_out, lengths_out, num_runs
     temp = _temp_for(run_length_encode_temp_bytes(n), num_runs_out, temp)
     call(f"lcpp_hip_run_length_non_trivial_{suffix}", ptr(temp), _tb(temp), ptr(d_in), ptr(offsets_out),
          ptr(lengths_out), ptr(num_runs_out), n, stream_handle(stream))
+
+
+# ---- segmented reductions and scans (DeviceSegmentReduce, DeviceSegmentedScan) ------------------
+def segment_reduce(op: str, suffix: str, d_in, d_out, num_segments: int, begins=None, ends=None,
+                   segment_size: int | None = None, index_out=None, stream=None) -> None:
+    """DeviceSegmentReduce::{Sum,Min,Max,ArgMin,ArgMax}: offsets (begins, ends) or a fixed segment_size."""
+    arg = op in ("argmin", "argmax")
+    if segment_size is not None:
+        name = f"lcpp_hip_segment_fixed_{op}_{suffix}" if arg else f"lcpp_hip_segment_reduce_fixed_{op}_{suffix}"
+        extra = (ptr(index_out),) if arg else ()
+        call(name, None, 0, ptr(d_in), ptr(d_out), *extra, num_segments, segment_size, stream_handle(stream))
+    else:
+        name = f"lcpp_hip_segment_{op}_{suffix}" if arg else f"lcpp_hip_segment_reduce_{op}_{suffix}"
+        extra = (ptr(index_out),) if arg else ()
+        call(name, None, 0, ptr(d_in), ptr(d_out), *extra, num_segments, ptr(begins), ptr(ends),
+             stream_handle(stream))
+
+
+def segmented_scan(suffix: str, d_in, d_out, begins, ends, num_segments: int, inclusive: bool = False, init=None,
+                   out_begins=None, stream=None) -> None:
+    """DeviceSegmentedScan::{Exclusive,Inclusive}SegmentedSum, InclusiveSegmentedScanInit (sum)."""
+    use_init = init is not None
+    if not inclusive and not use_init:
+        init, use_init = 0, True
+    call(f"lcpp_hip_segmented_scan_sum_{suffix}", None, 0, ptr(d_in), ptr(d_out), ptr(begins), ptr(ends),
+         ptr(out_begins), num_segments, int(inclusive), int(use_init), _CTYPE[suffix](init if use_init else 0),
+         stream_handle(stream))

@@ -71,6 +71,10 @@ def lib() -> C.CDLL:
         h.oracle_run_length_encode.argtypes = [i32, vp, u64, vp, vp]
         h.oracle_non_trivial_runs.restype = u64
         h.oracle_non_trivial_runs.argtypes = [i32, vp, u64, vp, vp]
+        h.oracle_segment_reduce.restype = None
+        h.oracle_segment_reduce.argtypes = [i32, i32, vp, vp, vp, u64, vp, vp, vp]
+        h.oracle_segmented_scan.restype = None
+        h.oracle_segmented_scan.argtypes = [i32, vp, vp, vp, vp, u64, i32, i32, u64, C.c_double, vp, vp]
         _lib = h
     return _lib
 
@@ -301,3 +305,37 @@ def non_trivial_runs(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     lens = np.zeros(max(x.size, 1), np.uint32)
     runs = lib().oracle_non_trivial_runs(_code(x), _p(x), x.size, _p(offs), _p(lens))
     return offs[:runs], lens[:runs]
+
+
+# ---- segmented reductions and scans (oracle.c) --------------------------------------------------
+SEG_OPS = {"sum": 0, "min": 1, "max": 2, "argmin": 3, "argmax": 4}
+
+
+def segment_reduce(op: str, x: np.ndarray, begins, ends):
+    """(out, index or None, sum of |items| or None) per segment."""
+    x = np.ascontiguousarray(x)
+    b = np.ascontiguousarray(begins, dtype=np.uint32)
+    e = np.ascontiguousarray(ends, dtype=np.uint32)
+    m = b.size
+    out = np.zeros(max(m, 1), x.dtype)
+    idx = np.zeros(max(m, 1), np.uint32) if op in ("argmin", "argmax") else None
+    ab = np.zeros(max(m, 1), np.float64) if op == "sum" and x.dtype.kind == "f" else None
+    lib().oracle_segment_reduce(_code(x), SEG_OPS[op], _p(x), _p(b), _p(e), m, _p(out), _p(idx), _p(ab))
+    return out[:m], (idx[:m] if idx is not None else None), (ab[:m] if ab is not None else None)
+
+
+def segmented_scan(x: np.ndarray, begins, ends, out_begins=None, inclusive=False, init=None, out_size=None):
+    """(out, sum of |terms| or None); positions no segment writes hold 0."""
+    x = np.ascontiguousarray(x)
+    b = np.ascontiguousarray(begins, dtype=np.uint32)
+    e = np.ascontiguousarray(ends, dtype=np.uint32)
+    ob = b if out_begins is None else np.ascontiguousarray(out_begins, dtype=np.uint32)
+    use_init = init is not None
+    n_out = out_size if out_size is not None else x.size
+    out = np.zeros(max(n_out, 1), x.dtype)
+    ab = np.zeros(max(n_out, 1), np.float64) if x.dtype.kind == "f" else None
+    init_v = init if use_init else 0
+    init_bits = _bits_of(init_v, x.dtype) if x.dtype.kind != "f" else 0
+    lib().oracle_segmented_scan(_code(x), _p(x), _p(b), _p(e), _p(ob), b.size, int(inclusive), int(use_init),
+                                init_bits, float(init_v), _p(out), _p(ab))
+    return out[:n_out], (ab[:n_out] if ab is not None else None)

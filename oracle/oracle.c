@@ -497,3 +497,122 @@ uint64_t oracle_non_trivial_runs(int type, const void* in, uint64_t n, uint32_t*
     }
     return n == 0 ? 0 : found;
 }
+
+/* ------------------------------------------------------------------------------------------------
+ * Segmented reductions and scans.  Follows DeviceSegmentReduce<> (src/lcpp/device/
+ * device_segment_reduce.h:110-420, details/segment_reduce.h:120-165,302-345) and DeviceSegmentedScan<>
+ * (src/lcpp/device/device_segmented_scan.h:52-224).  Segment s covers [begin[s], end[s]); begin >= end
+ * is empty.  op: 0 sum, 1 min, 2 max, 3 argmin, 4 argmax.  Empty segments: sum 0, min = the type's
+ * max, max = lowest, arg: that value and index 1.  Arg indices are relative to begin, ties go to the
+ * lower index.  Integer sums wrap; float min / max ignore NaN (fmin / fmax); float sums are long
+ * double with the sum of |items| in abs_out (may be NULL).
+ * ---------------------------------------------------------------------------------------------- */
+static long double fp_type_at(int type, const void* p, uint64_t i) {
+    return type == 2 ? (long double)((const float*)p)[i] : (long double)((const double*)p)[i];
+}
+
+static int int_less(int type, uint64_t a, uint64_t b) {
+    if (type == 0) return (int32_t)(uint32_t)a < (int32_t)(uint32_t)b;
+    if (type == 3) return (int64_t)a < (int64_t)b;
+    return a < b;
+}
+
+void oracle_segment_reduce(int type, int op, const void* in, const uint32_t* begins, const uint32_t* ends,
+                           uint64_t num_segments, void* out, uint32_t* index_out, double* abs_out) {
+    const int bytes = type_bytes(type);
+    const int is_fp = type == 2 || type == 5;
+    const uint64_t mask = bytes == 8 ? ~0ull : 0xFFFFFFFFull;
+    for (uint64_t s = 0; s < num_segments; ++s) {
+        const uint64_t b = begins[s], e = ends[s];
+        if (op == 0) {
+            if (is_fp) {
+                long double acc = 0, ab = 0;
+                for (uint64_t i = b; i < e; ++i) {
+                    acc += fp_type_at(type, in, i);
+                    ab += fabsl(fp_type_at(type, in, i));
+                }
+                if (type == 2) ((float*)out)[s] = (float)acc;
+                else ((double*)out)[s] = (double)acc;
+                if (abs_out) abs_out[s] = (double)ab;
+            } else {
+                uint64_t acc = 0;
+                for (uint64_t i = b; i < e; ++i) acc += load_bits(in, i, bytes);
+                store_bits(out, s, bytes, acc & mask);
+            }
+            continue;
+        }
+        const int want_min = op == 1 || op == 3;
+        int have = 0;
+        uint64_t best_bits = 0, best_i = 0;
+        double best_fp = 0;
+        for (uint64_t i = b; i < e; ++i) {
+            if (is_fp) {
+                const double v = (double)fp_type_at(type, in, i);
+                if (v != v) continue; /* NaN never wins */
+                if (!have || (want_min ? v < best_fp : v > best_fp)) {
+                    best_fp = v;
+                    best_i = i;
+                    have = 1;
+                }
+            } else {
+                const uint64_t v = load_bits(in, i, bytes);
+                if (!have || (want_min ? int_less(type, v, best_bits) : int_less(type, best_bits, v))) {
+                    best_bits = v;
+                    best_i = i;
+                    have = 1;
+                }
+            }
+        }
+        if (!have) {
+            /* initial value: the type's max for min forms, lowest for max forms */
+            if (type == 2) ((float*)out)[s] = want_min ? 3.40282347e+38f : -3.40282347e+38f;
+            else if (type == 5) ((double*)out)[s] = want_min ? 1.7976931348623157e308 : -1.7976931348623157e308;
+            else if (type == 0) store_bits(out, s, 4, want_min ? 0x7FFFFFFFull : 0x80000000ull);
+            else if (type == 3) store_bits(out, s, 8, want_min ? 0x7FFFFFFFFFFFFFFFull : 0x8000000000000000ull);
+            else store_bits(out, s, bytes, want_min ? mask : 0);
+            if (index_out) index_out[s] = 1;
+        } else {
+            if (type == 2) ((float*)out)[s] = (float)best_fp;
+            else if (type == 5) ((double*)out)[s] = best_fp;
+            else store_bits(out, s, bytes, best_bits);
+            if (index_out) index_out[s] = (uint32_t)(best_i - b);
+        }
+    }
+}
+
+/* out[out_begin[s] + k] = init + sum of the segment's items before k (exclusive) or up to k
+ * (inclusive; plus init when use_init). */
+void oracle_segmented_scan(int type, const void* in, const uint32_t* begins, const uint32_t* ends,
+                           const uint32_t* out_begins, uint64_t num_segments, int inclusive, int use_init,
+                           uint64_t init_bits, double init_fp, void* out, double* abs_out) {
+    const int bytes = type_bytes(type);
+    const int is_fp = type == 2 || type == 5;
+    const uint64_t mask = bytes == 8 ? ~0ull : 0xFFFFFFFFull;
+    for (uint64_t s = 0; s < num_segments; ++s) {
+        const uint64_t b = begins[s], e = ends[s], ob = out_begins[s];
+        uint64_t acc = (use_init || !inclusive) ? init_bits : 0;
+        long double facc = (use_init || !inclusive) ? init_fp : 0, ab = fabsl((long double)init_fp);
+        for (uint64_t i = b; i < e; ++i) {
+            const uint64_t o = ob + (i - b);
+            if (is_fp) {
+                const long double v = fp_type_at(type, in, i);
+                if (inclusive) {
+                    facc += v;
+                    ab += fabsl(v);
+                }
+                if (type == 2) ((float*)out)[o] = (float)facc;
+                else ((double*)out)[o] = (double)facc;
+                if (abs_out) abs_out[o] = (double)ab;
+                if (!inclusive) {
+                    facc += v;
+                    ab += fabsl(v);
+                }
+            } else {
+                const uint64_t v = load_bits(in, i, bytes);
+                if (inclusive) acc += v;
+                store_bits(out, o, bytes, acc & mask);
+                if (!inclusive) acc += v;
+            }
+        }
+    }
+}

@@ -559,3 +559,79 @@ def test_select_stability_with_index_payload(orc):
     sel = (rng.random(5000) < 0.3).astype(np.uint8)
     out, k = orc.select(idx, sel)
     assert np.all(np.diff(out[:k].astype(np.int64)) > 0) and k == int(sel.sum())
+
+
+# ---- segmented reductions and scans -----------------------------------------------------------------
+def test_segment_reduce_known_answers(orc):
+    """tests/device_segment_reduce.cpp:438-548: empty segments take the initial value; ArgMax of
+    negative ties and empty segments; ArgMin's first relative index."""
+    assert orc.segment_reduce("sum", np.array([4, 6, 8, 10], np.int32), [0, 2, 2], [2, 2, 4])[0].tolist() == [10, 0, 18]
+    v, i, _ = orc.segment_reduce("argmax", np.array([-9, -2, -2, -8, -5], np.float32), [0, 1, 4], [0, 4, 4])
+    lo = float(np.finfo(np.float32).min)
+    assert v.tolist() == [lo, -2.0, lo] and i.tolist() == [1, 0, 1]
+    v, i, _ = orc.segment_reduce("argmin", np.array([7, 1, 1, 9, 4, 2], np.int32), [0, 3], [3, 6])
+    assert v.tolist() == [1, 2] and i.tolist() == [1, 2]
+
+
+def test_segmented_scan_known_answers(orc):
+    """tests/device_segmented_scan_test.cpp:11-103 (expected_values), same and packed output offsets."""
+    x = np.array([100, 1, 2, 3, 5, 6, 7, 200, 9, 10, 11, 12, 300, 400], np.int32)
+    b, e, packed = [1, 4, 4, 8], [4, 4, 7, 12], [0, 4, 6, 10]
+
+    def expected(out_begins, mode):
+        want = [None] * 14
+        for s in range(4):
+            if b[s] == e[s]:
+                continue
+            agg = 0 if mode == "ex" else (10 if mode == "init" else None)
+            for k, idx in enumerate(range(b[s], e[s])):
+                if mode == "ex":
+                    want[out_begins[s] + k] = agg
+                    agg += int(x[idx])
+                else:
+                    agg = int(x[idx]) if agg is None else agg + int(x[idx])
+                    want[out_begins[s] + k] = agg
+        return want
+
+    for ob in (b, packed):
+        for mode, kw in (("ex", {}), ("in", {"inclusive": True}), ("init", {"inclusive": True, "init": 10})):
+            got, _ = orc.segmented_scan(x, b, e, out_begins=ob, **kw)
+            want = expected(ob, mode)
+            assert [int(g) for g, w in zip(got, want) if w is not None] == [w for w in want if w is not None]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32, np.int64, np.float32])
+def test_segment_ops_vs_numpy(orc, dtype):
+    """Independent numpy formulation on random ragged, empty and reversed segments."""
+    rng = np.random.default_rng(17)
+    n = 3000
+    x = (rng.integers(-1000, 1000, n) if dtype != np.uint32 else rng.integers(0, 2000, n)).astype(dtype)
+    b = rng.integers(0, n, 200).astype(np.uint32)
+    e = np.minimum(b + rng.integers(0, 60, 200), n).astype(np.uint32)
+    e[::17] = b[::17]          # empty
+    e[5::23] = b[5::23] // 2   # reversed: empty
+    for op in ("sum", "min", "max") + (("argmin", "argmax") if np.dtype(dtype).itemsize == 4 else ()):
+        out, idx, _ = orc.segment_reduce(op, x, b, e)
+        for s in range(200):
+            seg = x[b[s]:e[s]] if e[s] > b[s] else x[:0]
+            if op == "sum":
+                want = seg.astype(np.float64).sum() if dtype == np.float32 else int(seg.astype(np.int64).sum())
+                if dtype != np.float32:
+                    want = np.array([want]).astype(np.int64).astype(dtype)[0] if seg.size else 0
+                assert np.isclose(float(out[s]), float(want)), (op, s)
+            elif seg.size == 0:
+                info = np.finfo(dtype) if dtype == np.float32 else np.iinfo(dtype)
+                assert out[s] == (info.max if op in ("min", "argmin") else info.min)
+                if idx is not None:
+                    assert idx[s] == 1
+            else:
+                f = np.argmin if op in ("min", "argmin") else np.argmax
+                k = int(f(seg))
+                assert out[s] == seg[k]
+                if idx is not None:
+                    assert idx[s] == k
+    got, _ = orc.segmented_scan(x, b, e, inclusive=True)
+    for s in range(0, 200, 7):
+        if e[s] > b[s] and all(not (b[t] < e[s] and b[s] < e[t]) or t == s for t in range(200)):
+            want = np.cumsum(x[b[s]:e[s]].astype(np.float64 if dtype == np.float32 else np.int64))
+            assert np.allclose(got[b[s]:e[s]].astype(np.float64), want.astype(dtype).astype(np.float64))
