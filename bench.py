@@ -5,14 +5,14 @@ resident in HBM, one step = one SortKeys call.  The JSON line also carries the r
 dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
 one host thread), and the other benchmark configurations (reduce, scan, SortPairs, CsrMV) plus
 ExclusiveSumByKey / ReduceByKey and the stream-compaction family (select, partition, unique, run-length
-encode) as achieved GB/s against the 8 TB/s HBM peak.
+encode) and the segmented reduce / scan as achieved GB/s against the 8 TB/s HBM peak.
 
 `roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
 FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only bykey|compact|reduce|scan|sortpairs|spmv]
+                       [--only bykey|compact|reduce|scan|segmented|sortpairs|spmv]
 """
 from __future__ import annotations
 
@@ -248,8 +248,36 @@ def extra_compact(hip, dev, steps, warmup, extra):
                        "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+def extra_segmented(hip, dev, steps, warmup, extra):
+    import torch
+    # DeviceSegmentReduce::Sum and DeviceSegmentedScan::InclusiveSegmentedSum over 2^28 int32 items in
+    # 2^16 segments of 4096 (begin/end offsets).
+    m, segs = 1 << 28, 1 << 16
+    x = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_I32_PM1000, x, m, SEED)
+    begins = torch.arange(segs, dtype=torch.int64, device=dev).mul_(m // segs).to(torch.int32)
+    ends = begins + (m // segs)
+    out = torch.empty(segs, dtype=torch.int32, device=dev)
+    call = lambda: hip.segment_reduce("sum", "i32", x, out, segs, begins=begins, ends=ends)
+    t = time_steps(call, steps, warmup)
+    kms, _ = kernel_avg_ms(hip, call, "segment_reduce", 5)
+    moved = 4 * m + 12 * segs
+    extra["segment_reduce_sum_i32_2p28_4096"] = {"ms": round(t, 5), "kernel_ms": round(kms, 5),
+                                                 "GBps": round(moved / t / 1e6, 1),
+                                                 "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+    y = torch.empty_like(x)
+    call = lambda: hip.segmented_scan("i32", x, y, begins, ends, segs, inclusive=True)
+    t = time_steps(call, steps, warmup)
+    kms, _ = kernel_avg_ms(hip, call, "segmented_scan", 5)
+    moved = 8 * m + 8 * segs
+    extra["segmented_inclusive_sum_i32_2p28_4096"] = {"ms": round(t, 5), "kernel_ms": round(kms, 5),
+                                                      "GBps": round(moved / t / 1e6, 1),
+                                                      "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
-          "bykey": extra_by_key, "compact": extra_compact}
+          "bykey": extra_by_key, "compact": extra_compact,
+          "segmented": extra_segmented}
 
 
 def run_extras(hip, dev, steps, warmup, names):

@@ -13,9 +13,10 @@
 //
 // MI355X design: one 256-thread workgroup per segment.  Reductions stream the segment with eight
 // loads in flight per thread (consecutive lanes read consecutive items), fold in registers, then a
-// wave shuffle reduction and a 4-wave combine in LDS.  Scans walk the segment in chunks of 1024
-// items: each thread folds 4 consecutive items, a DPP wave scan and the LDS wave totals give every
-// thread its chunk prefix, and a running carry crosses chunks.  Segments with begin >= end are
+// wave shuffle reduction and a 4-wave combine in LDS.  Scans walk the segment in chunks of 2048
+// items: each thread folds 8 consecutive items (16-byte accesses when the segment start is aligned),
+// a DPP wave scan and the LDS wave totals give every thread its chunk prefix, and a running carry
+// crosses chunks.  Segments with begin >= end are
 // empty.  Integer sums wrap; float sums are ordered (per-thread folds, then a fixed tree).
 // Algorithmic traffic: reduce sizeof(T) per item + 8 bytes of offsets and sizeof(T) (+4) per segment;
 // scan 2 * sizeof(T) per item.
@@ -30,7 +31,7 @@ namespace {
 constexpr int kSgBlock = 256;
 constexpr int kSgWaves = kSgBlock / kWave;
 constexpr int kSgUnroll = 8;
-constexpr int kScanItems = 4;  // consecutive items per thread and scan chunk
+constexpr int kScanItems = 8;  // consecutive items per thread and scan chunk
 
 enum : int { kOpSum = 0, kOpMin = 1, kOpMax = 2, kOpArgMin = 3, kOpArgMax = 4 };
 
@@ -177,6 +178,11 @@ __global__ __launch_bounds__(kSgBlock) void segment_reduce_kernel(const T* __res
     }
 }
 
+template <typename T>
+struct alignas(16) ScanRun {
+    T v[kScanItems];
+};
+
 // Inclusive scan of one 32-/64-bit value per lane with wrapping or float addition.
 template <typename T>
 __device__ __forceinline__ T wave_scan_sum(T x) {
@@ -203,12 +209,22 @@ __global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __res
     if (b >= e) return;
     const uint64_t ob = out_begins[seg];
     const uint32_t wave = threadIdx.x / kWave;
+    // Every thread's run of items starts at a multiple of kScanItems from the segment's begin, so
+    // 16-byte vector accesses apply when the segment starts on a 16-byte boundary.
+    const bool vec_in = (reinterpret_cast<uintptr_t>(in + b) & 15) == 0;
+    const bool vec_out = (reinterpret_cast<uintptr_t>(out + ob) & 15) == 0;
     T carry = use_init ? init : T(0);
     for (uint64_t c = b; c < e; c += kChunk) {
         const uint64_t first = c + static_cast<uint64_t>(threadIdx.x) * kScanItems;
         T v[kScanItems];
+        if (vec_in && first + kScanItems <= e) {
+            const ScanRun<T> r = *reinterpret_cast<const ScanRun<T>*>(in + first);
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) v[k] = first + k < e ? in[first + k] : T(0);
+            for (int k = 0; k < kScanItems; ++k) v[k] = r.v[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < kScanItems; ++k) v[k] = first + k < e ? in[first + k] : T(0);
+        }
         T own = v[0];
 #pragma unroll
         for (int k = 1; k < kScanItems; ++k) own = add_wrap(own, v[k]);
@@ -225,12 +241,23 @@ __global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __res
         // Prefix of this thread's first item: carry + earlier waves + earlier lanes of this wave.
         const T lanes_before = dpp_move<dpp::kWaveShr1>(T(0), inc);
         T run = add_wrap(carry, add_wrap(before, lanes_before));
+        T o[kScanItems];
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
-            if (first + k < e) {
-                const T next = add_wrap(run, v[k]);
-                out[ob + (first + k - b)] = inclusive ? next : run;
-                run = next;
+            const T next = add_wrap(run, v[k]);
+            o[k] = inclusive ? next : run;
+            run = next;
+        }
+        T* const dst = out + ob + (first - b);
+        if (vec_out && first + kScanItems <= e) {
+            ScanRun<T> r;
+#pragma unroll
+            for (int k = 0; k < kScanItems; ++k) r.v[k] = o[k];
+            *reinterpret_cast<ScanRun<T>*>(dst) = r;
+        } else {
+#pragma unroll
+            for (int k = 0; k < kScanItems; ++k) {
+                if (first + k < e) dst[k] = o[k];
             }
         }
         carry = add_wrap(carry, total);
