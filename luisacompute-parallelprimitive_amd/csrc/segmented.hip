@@ -16,8 +16,8 @@
 // wave shuffle reduction and a 4-wave combine in LDS.  Scans walk the segment in chunks of 2048
 // items: each thread folds 8 consecutive items (16-byte accesses when the segment start is aligned),
 // a DPP wave scan and the LDS wave totals give every thread its chunk prefix, and a running carry
-// crosses chunks.  Segments with begin >= end are
-// empty.  Integer sums wrap; float sums are ordered (per-thread folds, then a fixed tree).
+// crosses chunks.  Segments with begin >= end are empty.  Integer sums wrap; float sums are ordered
+// (per-thread folds, then a fixed tree).
 // Algorithmic traffic: reduce sizeof(T) per item + 8 bytes of offsets and sizeof(T) (+4) per segment;
 // scan 2 * sizeof(T) per item.
 #include "common.hpp"

@@ -10,3 +10,5 @@
 #include "lcpp/device/device_select.h"
 #include "lcpp/device/device_partition.h"
 #include "lcpp/device/device_run_length_encode.h"
+#include "lcpp/device/device_segment_reduce.h"
+#include "lcpp/device/device_segmented_scan.h"

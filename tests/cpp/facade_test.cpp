@@ -4,7 +4,8 @@
 //
 // Case sources: tests/device_reduce_test.cpp:95-173,425-514, tests/device_scan_test.cpp:80-447,
 // tests/device_select_test.cpp:248-500, tests/device_partition_test.cpp:103-377,
-// tests/device_run_length_encode_test.cpp:172-340,
+// tests/device_run_length_encode_test.cpp:172-340, tests/device_segment_reduce.cpp:438-548,
+// tests/device_segmented_scan_test.cpp:11-257,
 // tests/device_radix_sort_interface_test.cpp:68-283, tests/device_radix_sort_one_sweep.cpp:79-333,
 // tests/device_spmv_test.cpp:41-203 and the bench generators of tests/lcpp_cub_bench.cpp:516-521,
 // 666-672, 814.
@@ -18,6 +19,7 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <limits>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -73,7 +75,11 @@ struct Env {
     DeviceSelect<> select;
     DevicePartition<> partition;
     DeviceRunLengthEncode<> rle;
+    DeviceSegmentReduce<> segment_reduce;
+    DeviceSegmentedScan<> segmented_scan;
     Env() : device(context.create_device("hip")), stream(device.create_stream()) {
+        segment_reduce.create(device);
+        segmented_scan.create(device);
         select.create(device);
         partition.create(device);
         rle.create(device);
@@ -795,6 +801,76 @@ void run_length_encode_examples() {
     EXPECT(read_count(e, counts, 0) == 0u && read_count(e, counts, 1) == 0u);
 }
 
+// ---- segmented ------------------------------------------------------------------------------------
+
+// tests/device_segment_reduce.cpp:438-548.
+void segment_reduce_known_answers() {
+    auto& e = *g_env;
+    const std::vector<int> a{4, 6, 8, 10};
+    const std::vector<uint> ab{0u, 2u, 2u}, ae{2u, 2u, 4u};
+    const std::vector<float> f{-9.0f, -2.0f, -2.0f, -8.0f, -5.0f};
+    const std::vector<uint> fb{0u, 1u, 4u}, fe{0u, 4u, 4u};
+    const std::vector<int> g{7, 1, 1, 9, 4, 2};
+    const std::vector<uint> gb{0u, 3u}, ge{3u, 6u};
+    auto ai = e.device.create_buffer<int>(4), ao = e.device.create_buffer<int>(3);
+    auto abb = e.device.create_buffer<uint>(3), aeb = e.device.create_buffer<uint>(3);
+    auto fi = e.device.create_buffer<float>(5), fo = e.device.create_buffer<float>(3);
+    auto fbb = e.device.create_buffer<uint>(3), feb = e.device.create_buffer<uint>(3), fx = e.device.create_buffer<uint>(3);
+    auto gi = e.device.create_buffer<int>(6), go = e.device.create_buffer<int>(2);
+    auto gbb = e.device.create_buffer<uint>(2), geb = e.device.create_buffer<uint>(2), gx = e.device.create_buffer<uint>(2);
+    auto fsum = e.device.create_buffer<int>(2);
+    CommandList cmd;
+    e.segment_reduce.Sum(cmd, BufferView<uint>{}, ai.view(), ao.view(), 3u, abb.view(), aeb.view());
+    e.segment_reduce.ArgMax(cmd, BufferView<uint>{}, fi.view(), fo.view(), fx.view(), 3u, fbb.view(), feb.view());
+    e.segment_reduce.ArgMin(cmd, BufferView<uint>{}, gi.view(), go.view(), gx.view(), 2u, gbb.view(), geb.view());
+    e.segment_reduce.Max(cmd, BufferView<uint>{}, gi.view(), fsum.view(), 2u, 3u);  // fixed size 3
+    e.stream << ai.copy_from(luisa::span{a}) << abb.copy_from(luisa::span{ab}) << aeb.copy_from(luisa::span{ae})
+             << fi.copy_from(luisa::span{f}) << fbb.copy_from(luisa::span{fb}) << feb.copy_from(luisa::span{fe})
+             << gi.copy_from(luisa::span{g}) << gbb.copy_from(luisa::span{gb}) << geb.copy_from(luisa::span{ge})
+             << cmd.commit() << synchronize();
+    EXPECT((download(e, ao, 3) == std::vector<int>{10, 0, 18}));
+    const float lo = std::numeric_limits<float>::lowest();
+    EXPECT((download(e, fo, 3) == std::vector<float>{lo, -2.0f, lo}));
+    EXPECT((download(e, fx, 3) == std::vector<uint>{1u, 0u, 1u}));
+    EXPECT((download(e, go, 2) == std::vector<int>{1, 2}));
+    EXPECT((download(e, gx, 2) == std::vector<uint>{1u, 2u}));
+    EXPECT((download(e, fsum, 2) == std::vector<int>{7, 9}));
+}
+
+// tests/device_segmented_scan_test.cpp:104-257 (sum forms): same and packed output offsets, and the
+// exact in-place inclusive sum.
+void segmented_scan_known_answers() {
+    auto& e = *g_env;
+    const std::vector<int> x{100, 1, 2, 3, 5, 6, 7, 200, 9, 10, 11, 12, 300, 400};
+    const std::vector<uint> b{1u, 4u, 4u, 8u}, en{4u, 4u, 7u, 12u}, packed{0u, 4u, 6u, 10u};
+    constexpr int S = -777;
+    auto xi = e.device.create_buffer<int>(14);
+    auto bb = e.device.create_buffer<uint>(4), eb = e.device.create_buffer<uint>(4), pb = e.device.create_buffer<uint>(4);
+    auto ex = e.device.create_buffer<int>(14), in = e.device.create_buffer<int>(14), ini = e.device.create_buffer<int>(14);
+    auto pex = e.device.create_buffer<int>(14), inplace = e.device.create_buffer<int>(14);
+    const std::vector<int> sentinel(14, S);
+    CommandList cmd;
+    e.segmented_scan.ExclusiveSegmentedSum(cmd, BufferView<uint>{}, xi.view(), ex.view(), bb.view(), eb.view(), 4u);
+    e.segmented_scan.InclusiveSegmentedSum(cmd, BufferView<uint>{}, xi.view(), in.view(), bb.view(), eb.view(), 4u);
+    e.segmented_scan.InclusiveSegmentedScanInit(cmd, BufferView<uint>{}, xi.view(), ini.view(), bb.view(), eb.view(), 4u,
+                                                SumOp{}, 10);
+    e.segmented_scan.ExclusiveSegmentedSum(cmd, BufferView<uint>{}, xi.view(), pex.view(), bb.view(), eb.view(), pb.view(),
+                                           4u);
+    e.segmented_scan.InclusiveSegmentedSum(cmd, BufferView<uint>{}, inplace.view(), inplace.view(), bb.view(), eb.view(),
+                                           4u);
+    e.segmented_scan.InclusiveSegmentedSum(cmd, BufferView<uint>{}, inplace.view(), inplace.view(), BufferView<uint>{},
+                                           BufferView<uint>{}, 0u);
+    e.stream << xi.copy_from(luisa::span{x}) << bb.copy_from(luisa::span{b}) << eb.copy_from(luisa::span{en})
+             << pb.copy_from(luisa::span{packed}) << ex.copy_from(luisa::span{sentinel})
+             << in.copy_from(luisa::span{sentinel}) << ini.copy_from(luisa::span{sentinel})
+             << pex.copy_from(luisa::span{sentinel}) << inplace.copy_from(luisa::span{x}) << cmd.commit() << synchronize();
+    EXPECT((download(e, ex, 14) == std::vector<int>{S, 0, 1, 3, 0, 5, 11, S, 0, 9, 19, 30, S, S}));
+    EXPECT((download(e, in, 14) == std::vector<int>{S, 1, 3, 6, 5, 11, 18, S, 9, 19, 30, 42, S, S}));
+    EXPECT((download(e, ini, 14) == std::vector<int>{S, 11, 13, 16, 15, 21, 28, S, 19, 29, 40, 52, S, S}));
+    EXPECT((download(e, pex, 14) == std::vector<int>{0, 1, 3, S, S, S, 0, 5, 11, S, 0, 9, 19, 30}));
+    EXPECT((download(e, inplace, 14) == std::vector<int>{100, 1, 3, 6, 5, 11, 18, 200, 9, 19, 30, 42, 300, 400}));
+}
+
 // ---- record-time checks ------------------------------------------------------------------------
 
 void precondition_errors() {
@@ -856,6 +932,8 @@ const std::vector<Case>& cases() {
         {"select_in_place_forms", select_in_place_forms},
         {"partition_ordering_and_three_way", partition_ordering_and_three_way},
         {"run_length_encode_examples", run_length_encode_examples},
+        {"segment_reduce_known_answers", segment_reduce_known_answers},
+        {"segmented_scan_known_answers", segmented_scan_known_answers},
         {"spmv_float_unsigned_indices", spmv_float_unsigned_indices},
         {"spmv_int_values_and_empty_work", spmv_int_values_and_empty_work},
         {"precondition_errors", precondition_errors},
