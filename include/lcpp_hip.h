@@ -383,6 +383,54 @@ LCPP_HIP_DECLARE_SEGMENT_ARG(argmax, f32, float)
 #undef LCPP_HIP_DECLARE_SEGMENT_REDUCE
 
 /* ---------------------------------------------------------------------------------------------
+ * Segmented sorts: DeviceSegmentedRadixSort and DeviceSegmentedSort.
+ * Replaces DeviceSegmentedRadixSort<>::SortKeys / SortPairs (+Descending; copy and DoubleBuffer
+ * forms; begin_bit / end_bit, device_segmented_radix_sort.h:28-205) and DeviceSegmentedSort<>::SortKeys
+ * / StableSortKeys / SortPairs / StableSortPairs (+Descending, device_segmented_sort.h:49-505) with the
+ * default comparators.  Each segment [begin[s], end[s]) is sorted stably (begins ascending, segments
+ * disjoint, end <= n; items outside every segment are not written).  value_order == 0: radix order of
+ * the twiddled key bits [begin_bit, end_bit) (DeviceSegmentedRadixSort); value_order == 1: lhs < rhs on
+ * the key values (DeviceSegmentedSort; differs only for floats: -0.0 equals +0.0).  descending flips
+ * the order.  DoubleBuffer forms (*_db_*) sort from the buffer *selector picks into the one the
+ * reference's selector points to after its ceil(log2 n) flips, flipping *selector the same way; a radix
+ * sort of zero bits leaves them untouched.  Key suffixes u32 i32 f32 u64 i64 f64; values v32 / v64.
+ * Temp (copy forms): 0 for n <= 1, else n keys (+ n values at their alignment), each rounded to 4 bytes.
+ * ------------------------------------------------------------------------------------------- */
+size_t lcpp_hip_segmented_sort_keys_temp_bytes(uint64_t n, size_t key_bytes);
+size_t lcpp_hip_segmented_sort_pairs_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);
+#define LCPP_HIP_DECLARE_SEGSORT_PAIRS(KS, KT, VS, VT)                                                               \
+    int lcpp_hip_segmented_sort_pairs_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out,  \
+                                                  const VT* values_in, VT* values_out, uint64_t n,                \
+                                                  uint64_t num_segments, const uint32_t* begin_offsets,            \
+                                                  const uint32_t* end_offsets, uint32_t begin_bit,                 \
+                                                  uint32_t end_bit, int descending, int value_order, void* stream); \
+    int lcpp_hip_segmented_sort_pairs_db_##KS##_##VS(KT* keys0, KT* keys1, int* key_selector, VT* values0,         \
+                                                     VT* values1, int* value_selector, uint64_t n,                \
+                                                     uint64_t num_segments, const uint32_t* begin_offsets,         \
+                                                     const uint32_t* end_offsets, uint32_t begin_bit,              \
+                                                     uint32_t end_bit, int descending, int value_order,            \
+                                                     void* stream);
+#define LCPP_HIP_DECLARE_SEGSORT(KS, KT)                                                                             \
+    int lcpp_hip_segmented_sort_keys_##KS(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out,          \
+                                          uint64_t n, uint64_t num_segments, const uint32_t* begin_offsets,        \
+                                          const uint32_t* end_offsets, uint32_t begin_bit, uint32_t end_bit,       \
+                                          int descending, int value_order, void* stream);                          \
+    int lcpp_hip_segmented_sort_keys_db_##KS(KT* keys0, KT* keys1, int* key_selector, uint64_t n,                  \
+                                             uint64_t num_segments, const uint32_t* begin_offsets,                 \
+                                             const uint32_t* end_offsets, uint32_t begin_bit, uint32_t end_bit,    \
+                                             int descending, int value_order, void* stream);                       \
+    LCPP_HIP_DECLARE_SEGSORT_PAIRS(KS, KT, v32, uint32_t)                                                            \
+    LCPP_HIP_DECLARE_SEGSORT_PAIRS(KS, KT, v64, uint64_t)
+LCPP_HIP_DECLARE_SEGSORT(u32, uint32_t)
+LCPP_HIP_DECLARE_SEGSORT(i32, int32_t)
+LCPP_HIP_DECLARE_SEGSORT(f32, float)
+LCPP_HIP_DECLARE_SEGSORT(u64, uint64_t)
+LCPP_HIP_DECLARE_SEGSORT(i64, int64_t)
+LCPP_HIP_DECLARE_SEGSORT(f64, double)
+#undef LCPP_HIP_DECLARE_SEGSORT
+#undef LCPP_HIP_DECLARE_SEGSORT_PAIRS
+
+/* ---------------------------------------------------------------------------------------------
  * Seeded synthetic workloads for tests and benchmarks (no reference counterpart; the reference
  * generates on the host, e.g. tests/lcpp_cub_bench.cpp:516-521,666-672,814).
  * Stream: splitmix64, r_i = mix(seed + (start + i + 1) * 0x9E3779B97F4A7C15).

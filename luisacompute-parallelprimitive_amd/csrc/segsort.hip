@@ -1,0 +1,438 @@
+// DeviceSegmentedRadixSort and DeviceSegmentedSort (keys and key-value pairs, ascending and
+// descending, bit ranges, DoubleBuffer) for gfx950: a stable merge sort per segment.
+//
+// Reference paths (src/lcpp/device/): DeviceSegmentedSort<> (device_segmented_sort.h:43-505): a
+// stable merge sort by a comparator (lhs < rhs, or lhs > rhs for the descending forms) in passes of
+// doubling width over all items; the segment of item i is found by binary search over the begin
+// offsets (ascending, disjoint segments), only items inside a segment are written
+// (dispatch_key_merge, :300-420); DoubleBuffer forms flip the selector once per pass, ceil(log2 n)
+// times.  DeviceSegmentedRadixSort<> (device_segmented_radix_sort.h:26-246) is that sort with the
+// comparator "twiddled key bits [begin_bit, end_bit) compare less (greater)"; begin_bit == end_bit
+// leaves a DoubleBuffer untouched.
+//
+// MI355X design:
+//   * Block phase: one 256-thread workgroup per segment sorts the segment's 2,048-item chunks
+//     (8 items per thread): a stable odd-even transposition sort of each thread's 8 items in registers,
+//     then 8 merge-path passes in LDS (widths 8 .. 1,024), each thread producing 8 outputs after one
+//     binary search; chunks are written to the output.
+//   * Global phase, only for segments longer than 2,048 items: merge-path passes of width 2,048, 4,096,
+//     ... between the output and a scratch buffer, one thread per item; a segment takes part while the
+//     width is below its length, so every segment ends in the output or, after an odd number of its
+//     own passes, in the scratch buffer, from where a final kernel copies it back.
+//   * Orders: radix order compares (twiddled bits >> begin_bit) & mask (descending: the complement);
+//     value order (floats of DeviceSegmentedSort) compares the values, so -0.0 equals +0.0.
+// Algorithmic traffic: 2 * (sizeof(K) + sizeof(V)) per item in segments up to 2,048 items, plus the
+// same per global pass for longer segments.
+#include "common.hpp"
+#include "../../include/lcpp_hip.h"
+
+#include <utility>
+
+namespace lcpp_hip {
+namespace {
+
+constexpr int kSsBlock = 256;
+constexpr int kSsItems = 8;
+constexpr uint32_t kSsChunk = kSsBlock * kSsItems;  // 2048
+
+enum : int { kKindUnsigned = 0, kKindSigned = 1, kKindFloat = 2 };
+
+struct SortOrder {
+    uint64_t mask;       // bit_count ones (all ones for the full width)
+    uint32_t begin_bit;
+    uint32_t descending;
+    uint32_t value_order;  // compare float values instead of twiddled bits
+};
+
+template <typename K, int KIND>
+__device__ __forceinline__ K twiddle(K bits) {
+    constexpr K sign = static_cast<K>(K(1) << (sizeof(K) * 8 - 1));
+    if constexpr (KIND == kKindSigned) {
+        return bits ^ sign;
+    } else if constexpr (KIND == kKindFloat) {
+        return (bits & sign) ? static_cast<K>(~bits) : static_cast<K>(bits | sign);
+    } else {
+        return bits;
+    }
+}
+
+// a strictly before b in the sort order.
+template <typename K, int KIND>
+__device__ __forceinline__ bool before(K a, K b, const SortOrder& o) {
+    if constexpr (KIND == kKindFloat) {
+        if (o.value_order) {
+            using F = std::conditional_t<sizeof(K) == 8, double, float>;
+            const F fa = __builtin_bit_cast(F, a), fb = __builtin_bit_cast(F, b);
+            return o.descending ? fb < fa : fa < fb;
+        }
+    }
+    const K ka = static_cast<K>((twiddle<K, KIND>(a) >> o.begin_bit) & static_cast<K>(o.mask));
+    const K kb = static_cast<K>((twiddle<K, KIND>(b) >> o.begin_bit) & static_cast<K>(o.mask));
+    return o.descending ? kb < ka : ka < kb;
+}
+
+// Number of items taken from `left` among the first `diag` outputs of the stable merge of left[0, lw)
+// and right[0, rw) (ties take left first).
+template <typename K, int KIND, typename GetLeft, typename GetRight>
+__device__ __forceinline__ uint32_t merge_path(uint32_t diag, uint32_t lw, uint32_t rw, GetLeft left, GetRight right,
+                                               const SortOrder& o) {
+    uint32_t lo = diag > rw ? diag - rw : 0u;
+    uint32_t hi = diag < lw ? diag : lw;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (before<K, KIND>(right(diag - 1 - mid), left(mid), o)) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, const V* values_in,
+                                                                 V* values_out, const uint32_t* __restrict__ begins,
+                                                                 const uint32_t* __restrict__ ends, uint64_t n,
+                                                                 SortOrder o) {
+    __shared__ K s_keys[2][kSsChunk];
+    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsChunk : 1];
+    const uint32_t seg = blockIdx.x;
+    const uint64_t b = begins[seg];
+    const uint64_t e = ends[seg];
+    if (b >= e || e > n) return;
+    const uint32_t tid = threadIdx.x;
+    for (uint64_t c = b; c < e; c += kSsChunk) {
+        const uint32_t len = static_cast<uint32_t>(e - c < kSsChunk ? e - c : kSsChunk);
+        // Thread-local stable sort of items [8 tid, 8 tid + 8) of the chunk (padding never moves
+        // before real items: it is only compared with other padding).
+        K k[kSsItems];
+        V v[kSsItems];
+        const uint32_t base = tid * kSsItems;
+#pragma unroll
+        for (int j = 0; j < kSsItems; ++j) {
+            const bool ok = base + j < len;
+            k[j] = ok ? keys_in[c + base + j] : K(0);
+            if constexpr (PAIRS) v[j] = ok ? values_in[c + base + j] : V(0);
+        }
+        const uint32_t mine = base < len ? (len - base < kSsItems ? len - base : kSsItems) : 0u;
+#pragma unroll
+        for (int round = 0; round < kSsItems; ++round) {
+#pragma unroll
+            for (int j = round & 1; j + 1 < kSsItems; j += 2) {
+                if (static_cast<uint32_t>(j + 1) < mine && before<K, KIND>(k[j + 1], k[j], o)) {
+                    const K tk = k[j];
+                    k[j] = k[j + 1];
+                    k[j + 1] = tk;
+                    if constexpr (PAIRS) {
+                        const V tv = v[j];
+                        v[j] = v[j + 1];
+                        v[j + 1] = tv;
+                    }
+                }
+            }
+        }
+        __syncthreads();  // the previous chunk's readers of s_keys are done
+#pragma unroll
+        for (int j = 0; j < kSsItems; ++j) {
+            s_keys[0][base + j] = k[j];
+            if constexpr (PAIRS) s_vals[0][base + j] = v[j];
+        }
+        __syncthreads();
+        int cur = 0;
+        for (uint32_t w = kSsItems; w < len; w *= 2) {
+            // Output positions [base, base + 8) of the merged pair of runs that holds them.
+            if (base < len) {
+                const uint32_t l0 = base / (2 * w) * (2 * w);
+                const uint32_t lw = len - l0 < w ? len - l0 : w;
+                const uint32_t r0 = l0 + lw;
+                const uint32_t rw = r0 < len ? (len - r0 < w ? len - r0 : w) : 0u;
+                const uint32_t diag = base - l0;
+                const K* sk = s_keys[cur];
+                auto left = [&](uint32_t i) { return sk[l0 + i]; };
+                auto right = [&](uint32_t i) { return sk[r0 + i]; };
+                uint32_t li = merge_path<K, KIND>(diag, lw, rw, left, right, o);
+                uint32_t ri = diag - li;
+                const uint32_t count = len - base < kSsItems ? len - base : kSsItems;
+                for (uint32_t j = 0; j < count; ++j) {
+                    const bool take_left = li < lw && (ri >= rw || !before<K, KIND>(sk[r0 + ri], sk[l0 + li], o));
+                    const uint32_t src = take_left ? l0 + li : r0 + ri;
+                    s_keys[cur ^ 1][base + j] = sk[src];
+                    if constexpr (PAIRS) s_vals[cur ^ 1][base + j] = s_vals[cur][src];
+                    if (take_left) ++li;
+                    else ++ri;
+                }
+            }
+            cur ^= 1;
+            __syncthreads();
+        }
+        for (uint32_t q = tid; q < len; q += kSsBlock) {
+            keys_out[c + q] = s_keys[cur][q];
+            if constexpr (PAIRS) values_out[c + q] = s_vals[cur][q];
+        }
+    }
+}
+
+// Segment of item i (begins ascending): the last segment whose begin <= i, or -1.
+__device__ __forceinline__ int64_t find_segment(const uint32_t* begins, uint32_t num_segments, uint64_t i) {
+    uint32_t lo = 0, hi = num_segments;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (begins[mid] <= i) lo = mid + 1;
+        else hi = mid;
+    }
+    return static_cast<int64_t>(lo) - 1;
+}
+
+// Number of global passes a segment of `len` items takes (widths 2048, 4096, ... below len).
+__device__ __forceinline__ uint32_t global_passes(uint64_t len) {
+    uint32_t p = 0;
+    for (uint64_t w = kSsChunk; w < len; w *= 2) ++p;
+    return p;
+}
+
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(256) void segsort_merge_kernel(const K* __restrict__ src_k, K* __restrict__ dst_k,
+                                                            const V* __restrict__ src_v, V* __restrict__ dst_v,
+                                                            const uint32_t* __restrict__ begins,
+                                                            const uint32_t* __restrict__ ends, uint32_t num_segments,
+                                                            uint64_t n, uint64_t w, SortOrder o) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t s = find_segment(begins, num_segments, i);
+    if (s < 0) return;
+    const uint64_t b = begins[s], e = ends[s];
+    if (!(b <= i && i < e && e <= n) || e - b <= w) return;
+    const uint64_t local = i - b;
+    const uint64_t l0 = b + local / (2 * w) * (2 * w);
+    const uint64_t lw = e - l0 < w ? e - l0 : w;
+    const uint64_t r0 = l0 + lw;
+    const uint64_t rw = r0 < e ? (e - r0 < w ? e - r0 : w) : 0;
+    const uint32_t diag = static_cast<uint32_t>(i - l0);
+    auto left = [&](uint32_t j) { return src_k[l0 + j]; };
+    auto right = [&](uint32_t j) { return src_k[r0 + j]; };
+    const uint32_t li = merge_path<K, KIND>(diag, static_cast<uint32_t>(lw), static_cast<uint32_t>(rw), left, right, o);
+    const uint32_t ri = diag - li;
+    const bool take_left = li < lw && (ri >= rw || !before<K, KIND>(src_k[r0 + ri], src_k[l0 + li], o));
+    const uint64_t from = take_left ? l0 + li : r0 + ri;
+    dst_k[i] = src_k[from];
+    if constexpr (PAIRS) dst_v[i] = src_v[from];
+}
+
+// Items of segments that took an odd number of global passes move from the scratch buffers back.
+template <typename K, typename V, bool PAIRS>
+__global__ __launch_bounds__(256) void segsort_copy_back_kernel(const K* __restrict__ src_k, K* __restrict__ dst_k,
+                                                                const V* __restrict__ src_v, V* __restrict__ dst_v,
+                                                                const uint32_t* __restrict__ begins,
+                                                                const uint32_t* __restrict__ ends,
+                                                                uint32_t num_segments, uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t s = find_segment(begins, num_segments, i);
+    if (s < 0) return;
+    const uint64_t b = begins[s], e = ends[s];
+    if (!(b <= i && i < e && e <= n) || (global_passes(e - b) & 1u) == 0) return;
+    dst_k[i] = src_k[i];
+    if constexpr (PAIRS) dst_v[i] = src_v[i];
+}
+
+// Merge passes of a DoubleBuffer sort in the reference: ceil(log2 n) for n >= 2.
+uint32_t reference_pass_count(uint64_t n) {
+    uint32_t p = 0;
+    for (uint64_t w = 1; w < n; w *= 2) ++p;
+    return p;
+}
+
+template <typename K, typename V, bool PAIRS, int KIND>
+int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_out, V* values_scratch, uint64_t n,
+            uint64_t num_segments, const uint32_t* begins, const uint32_t* ends, uint32_t begin_bit, uint32_t end_bit,
+            int descending, int value_order, hipStream_t stream) {
+    const uint32_t width = sizeof(K) * 8;
+    SortOrder o;
+    o.begin_bit = begin_bit;
+    o.descending = descending ? 1u : 0u;
+    o.value_order = (KIND == kKindFloat && value_order) ? 1u : 0u;
+    const uint32_t bits = end_bit - begin_bit;
+    o.mask = bits >= 64 ? ~0ull : ((1ull << bits) - 1);
+    if (bits == 0 && !o.value_order) {
+        o.mask = 0;  // every key compares equal: a stable copy
+        o.begin_bit = 0;
+    }
+    (void)width;
+    int st;
+    {
+        LaunchScope scope("segsort_block", stream);
+        segsort_block_kernel<K, V, PAIRS, KIND><<<static_cast<unsigned>(num_segments), kSsBlock, 0, stream>>>(
+            keys_in, keys_out, values_in, values_out, begins, ends, n, o);
+        st = check_hip(hipGetLastError(), "segsort block launch");
+        if (st != kOk) return st;
+    }
+    if (n <= kSsChunk) return kOk;
+    const unsigned grid = static_cast<unsigned>(ceil_div(n, 256));
+    K* src_k = keys_out;
+    K* dst_k = keys_scratch;
+    V* src_v = values_out;
+    V* dst_v = values_scratch;
+    for (uint64_t w = kSsChunk; w < n; w *= 2) {
+        LaunchScope scope("segsort_merge", stream);
+        segsort_merge_kernel<K, V, PAIRS, KIND><<<grid, 256, 0, stream>>>(
+            src_k, dst_k, src_v, dst_v, begins, ends, static_cast<uint32_t>(num_segments), n, w, o);
+        st = check_hip(hipGetLastError(), "segsort merge launch");
+        if (st != kOk) return st;
+        std::swap(src_k, dst_k);
+        std::swap(src_v, dst_v);
+    }
+    LaunchScope scope("segsort_copy_back", stream);
+    segsort_copy_back_kernel<K, V, PAIRS><<<grid, 256, 0, stream>>>(keys_scratch, keys_out, values_scratch,
+                                                                    values_out, begins, ends,
+                                                                    static_cast<uint32_t>(num_segments), n);
+    return check_hip(hipGetLastError(), "segsort copy-back launch");
+}
+
+size_t round4(size_t bytes) { return (bytes + 3) / 4 * 4; }
+
+// Temp layout of the copy forms (the reference's GetSort*TempStorageBytes): n scratch keys, then (pairs)
+// n scratch values at the value type's alignment.
+size_t segsort_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    if (n <= 1) return 0;
+    const size_t kb = round4(n * key_bytes);
+    if (!value_bytes) return kb;
+    return align_up(kb, value_bytes) + round4(n * value_bytes);
+}
+
+template <typename K, typename V, bool PAIRS, int KIND>
+int segsort_entry(const char* what, void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, const V* values_in,
+                  V* values_out, uint64_t n, uint64_t num_segments, const uint32_t* begins, const uint32_t* ends,
+                  uint32_t begin_bit, uint32_t end_bit, int descending, int value_order, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items", what);
+    if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
+    if (begin_bit > end_bit || end_bit > sizeof(K) * 8)
+        return set_error(kInvalidArgument, "%s: bad bit range [%u, %u)", what, begin_bit, end_bit);
+    if (n == 0 || num_segments == 0) return kOk;
+    if (!keys_in || !keys_out || !begins || !ends || (PAIRS && (!values_in || !values_out)))
+        return set_error(kInvalidArgument, "%s: null input or output", what);
+    const size_t need = segsort_temp_bytes(n, sizeof(K), PAIRS ? sizeof(V) : 0);
+    if (n > kSsChunk && (!temp || temp_bytes < need))
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, need);
+    K* ks = static_cast<K*>(temp);
+    V* vs = PAIRS ? reinterpret_cast<V*>(static_cast<unsigned char*>(temp) + align_up(round4(n * sizeof(K)), sizeof(V)))
+                  : nullptr;
+    return segsort<K, V, PAIRS, KIND>(const_cast<K*>(keys_in), keys_out, ks, const_cast<V*>(values_in), values_out,
+                                      vs, n, num_segments, begins, ends, begin_bit, end_bit, descending, value_order,
+                                      stream);
+}
+
+// DoubleBuffer forms: the result lands where the reference's selector points after its
+// ceil(log2 n) flips; the other buffer is the scratch.
+template <typename K, typename V, bool PAIRS, int KIND>
+int segsort_db(const char* what, K* keys0, K* keys1, int* key_selector, V* values0, V* values1, int* value_selector,
+               uint64_t n, uint64_t num_segments, const uint32_t* begins, const uint32_t* ends, uint32_t begin_bit,
+               uint32_t end_bit, int descending, int value_order, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (!key_selector || (PAIRS && !value_selector)) return set_error(kInvalidArgument, "%s: null selector", what);
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items", what);
+    if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
+    if (begin_bit > end_bit || end_bit > sizeof(K) * 8)
+        return set_error(kInvalidArgument, "%s: bad bit range [%u, %u)", what, begin_bit, end_bit);
+    if (n <= 1 || num_segments == 0) return kOk;
+    if (!value_order && begin_bit == end_bit) return kOk;  // radix sort of no bits: buffers untouched
+    if (!keys0 || !keys1 || !begins || !ends || (PAIRS && (!values0 || !values1)))
+        return set_error(kInvalidArgument, "%s: null buffer", what);
+    const uint32_t passes = reference_pass_count(n);
+    const int ks = *key_selector & 1;
+    K* kcur = ks ? keys1 : keys0;
+    K* kalt = ks ? keys0 : keys1;
+    V* vcur = nullptr;
+    V* valt = nullptr;
+    if constexpr (PAIRS) {
+        const int vsel = *value_selector & 1;
+        vcur = vsel ? values1 : values0;
+        valt = vsel ? values0 : values1;
+    }
+    const bool odd = passes & 1u;
+    K* kout = odd ? kalt : kcur;
+    K* kscr = odd ? kcur : kalt;
+    V* vout = odd ? valt : vcur;
+    V* vscr = odd ? vcur : valt;
+    // When the result goes to the alternate buffer the input stays in current, which the global phase
+    // then uses as scratch (the block phase has read it by then).
+    const int st = segsort<K, V, PAIRS, KIND>(kcur, kout, kscr, vcur, vout, vscr, n, num_segments, begins, ends,
+                                              begin_bit, end_bit, descending, value_order, stream);
+    if (st != kOk) return st;
+    if (odd) {
+        *key_selector ^= 1;
+        if constexpr (PAIRS) *value_selector ^= 1;
+    }
+    return kOk;
+}
+
+template <typename T>
+using Storage = std::conditional_t<sizeof(T) == 8, uint64_t, uint32_t>;
+template <typename T>
+constexpr int kKindOf = std::is_floating_point_v<T> ? kKindFloat : (std::is_signed_v<T> ? kKindSigned : kKindUnsigned);
+
+}  // namespace
+}  // namespace lcpp_hip
+
+using namespace lcpp_hip;
+
+extern "C" {
+
+size_t lcpp_hip_segmented_sort_keys_temp_bytes(uint64_t n, size_t key_bytes) {
+    return segsort_temp_bytes(n, key_bytes, 0);
+}
+size_t lcpp_hip_segmented_sort_pairs_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes) {
+    return segsort_temp_bytes(n, key_bytes, value_bytes);
+}
+
+#define LCPP_HIP_DEFINE_SEGSORT_PAIRS(KS, KT, VS, VT)                                                                 \
+    int lcpp_hip_segmented_sort_pairs_##KS##_##VS(                                                                    \
+        void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out, const VT* values_in, VT* values_out,         \
+        uint64_t n, uint64_t num_segments, const uint32_t* begin_offsets, const uint32_t* end_offsets,              \
+        uint32_t begin_bit, uint32_t end_bit, int descending, int value_order, void* stream) {                      \
+        using K = Storage<KT>;                                                                                        \
+        return segsort_entry<K, VT, true, kKindOf<KT>>(                                                               \
+            "DeviceSegmentedSort::SortPairs", temp, temp_bytes, reinterpret_cast<const K*>(keys_in),                  \
+            reinterpret_cast<K*>(keys_out), values_in, values_out, n, num_segments, begin_offsets, end_offsets,     \
+            begin_bit, end_bit, descending, value_order, stream);                                                     \
+    }                                                                                                                 \
+    int lcpp_hip_segmented_sort_pairs_db_##KS##_##VS(                                                                 \
+        KT* keys0, KT* keys1, int* key_selector, VT* values0, VT* values1, int* value_selector, uint64_t n,         \
+        uint64_t num_segments, const uint32_t* begin_offsets, const uint32_t* end_offsets, uint32_t begin_bit,      \
+        uint32_t end_bit, int descending, int value_order, void* stream) {                                          \
+        using K = Storage<KT>;                                                                                        \
+        return segsort_db<K, VT, true, kKindOf<KT>>(                                                                  \
+            "DeviceSegmentedSort::SortPairs", reinterpret_cast<K*>(keys0), reinterpret_cast<K*>(keys1),             \
+            key_selector, values0, values1, value_selector, n, num_segments, begin_offsets, end_offsets, begin_bit,  \
+            end_bit, descending, value_order, stream);                                                                \
+    }
+#define LCPP_HIP_DEFINE_SEGSORT(KS, KT)                                                                               \
+    int lcpp_hip_segmented_sort_keys_##KS(void* temp, size_t temp_bytes, const KT* keys_in, KT* keys_out,           \
+                                          uint64_t n, uint64_t num_segments, const uint32_t* begin_offsets,         \
+                                          const uint32_t* end_offsets, uint32_t begin_bit, uint32_t end_bit,        \
+                                          int descending, int value_order, void* stream) {                          \
+        using K = Storage<KT>;                                                                                        \
+        return segsort_entry<K, uint32_t, false, kKindOf<KT>>(                                                        \
+            "DeviceSegmentedSort::SortKeys", temp, temp_bytes, reinterpret_cast<const K*>(keys_in),                   \
+            reinterpret_cast<K*>(keys_out), nullptr, nullptr, n, num_segments, begin_offsets, end_offsets,           \
+            begin_bit, end_bit, descending, value_order, stream);                                                     \
+    }                                                                                                                 \
+    int lcpp_hip_segmented_sort_keys_db_##KS(KT* keys0, KT* keys1, int* key_selector, uint64_t n,                   \
+                                             uint64_t num_segments, const uint32_t* begin_offsets,                  \
+                                             const uint32_t* end_offsets, uint32_t begin_bit, uint32_t end_bit,     \
+                                             int descending, int value_order, void* stream) {                       \
+        using K = Storage<KT>;                                                                                        \
+        return segsort_db<K, uint32_t, false, kKindOf<KT>>(                                                           \
+            "DeviceSegmentedSort::SortKeys", reinterpret_cast<K*>(keys0), reinterpret_cast<K*>(keys1),              \
+            key_selector, nullptr, nullptr, nullptr, n, num_segments, begin_offsets, end_offsets, begin_bit,        \
+            end_bit, descending, value_order, stream);                                                                \
+    }                                                                                                                 \
+    LCPP_HIP_DEFINE_SEGSORT_PAIRS(KS, KT, v32, uint32_t)                                                              \
+    LCPP_HIP_DEFINE_SEGSORT_PAIRS(KS, KT, v64, uint64_t)
+LCPP_HIP_DEFINE_SEGSORT(u32, uint32_t)
+LCPP_HIP_DEFINE_SEGSORT(i32, int32_t)
+LCPP_HIP_DEFINE_SEGSORT(f32, float)
+LCPP_HIP_DEFINE_SEGSORT(u64, uint64_t)
+LCPP_HIP_DEFINE_SEGSORT(i64, int64_t)
+LCPP_HIP_DEFINE_SEGSORT(f64, double)
+#undef LCPP_HIP_DEFINE_SEGSORT
+#undef LCPP_HIP_DEFINE_SEGSORT_PAIRS
+
+}  // extern "C"

@@ -129,6 +129,17 @@ def _declare(lib: C.CDLL) -> None:
         for op in ("argmin", "argmax"):
             sig(f"lcpp_hip_segment_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, vp, vp, vp)
             sig(f"lcpp_hip_segment_fixed_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, u32, vp)
+    sig("lcpp_hip_segmented_sort_keys_temp_bytes", sz, u64, sz)
+    sig("lcpp_hip_segmented_sort_pairs_temp_bytes", sz, u64, sz, sz)
+    ip = C.POINTER(C.c_int)
+    for k in SORT_KEY_SUFFIXES:
+        sig(f"lcpp_hip_segmented_sort_keys_{k}", i32, vp, sz, vp, vp, u64, u64, vp, vp, u32, u32, i32, i32, vp)
+        sig(f"lcpp_hip_segmented_sort_keys_db_{k}", i32, vp, vp, ip, u64, u64, vp, vp, u32, u32, i32, i32, vp)
+        for v in ("v32", "v64"):
+            sig(f"lcpp_hip_segmented_sort_pairs_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, u64, u64, vp, vp, u32, u32,
+                i32, i32, vp)
+            sig(f"lcpp_hip_segmented_sort_pairs_db_{k}_{v}", i32, vp, vp, ip, vp, vp, ip, u64, u64, vp, vp, u32, u32,
+                i32, i32, vp)
     pp = C.POINTER(Predicate)
     for name in ("select", "partition_three_way", "run_length_encode"):
         sig(f"lcpp_hip_{name}_temp_bytes", sz, u64)
@@ -483,3 +494,44 @@ def segmented_scan(suffix: str, d_in, d_out, begins, ends, num_segments: int, in
     call(f"lcpp_hip_segmented_scan_sum_{suffix}", None, 0, ptr(d_in), ptr(d_out), ptr(begins), ptr(ends),
          ptr(out_begins), num_segments, int(inclusive), int(use_init), _CTYPE[suffix](init if use_init else 0),
          stream_handle(stream))
+
+
+# ---- segmented sorts (DeviceSegmentedRadixSort, DeviceSegmentedSort) -----------------------------
+def segmented_sort(key_suffix: str, keys_in, keys_out, n: int, num_segments: int, begins, ends, values_in=None,
+                   values_out=None, begin_bit: int = 0, end_bit: int | None = None, descending: bool = False,
+                   value_order: bool = False, temp=None, stream=None) -> None:
+    """Stable per-segment sort (radix order of bits [begin_bit, end_bit), or value order)."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    if values_in is None:
+        nbytes = lib().lcpp_hip_segmented_sort_keys_temp_bytes(n, kb)
+        temp = _temp_for(nbytes, keys_out, temp)
+        call(f"lcpp_hip_segmented_sort_keys_{key_suffix}", ptr(temp), _tb(temp), ptr(keys_in), ptr(keys_out), n,
+             num_segments, ptr(begins), ptr(ends), begin_bit, end_bit, int(descending), int(value_order),
+             stream_handle(stream))
+    else:
+        vb = values_in.element_size()
+        nbytes = lib().lcpp_hip_segmented_sort_pairs_temp_bytes(n, kb, vb)
+        temp = _temp_for(nbytes, keys_out, temp)
+        call(f"lcpp_hip_segmented_sort_pairs_{key_suffix}_v{8 * vb}", ptr(temp), _tb(temp), ptr(keys_in),
+             ptr(keys_out), ptr(values_in), ptr(values_out), n, num_segments, ptr(begins), ptr(ends), begin_bit,
+             end_bit, int(descending), int(value_order), stream_handle(stream))
+
+
+def segmented_sort_db(key_suffix: str, keys0, keys1, selector: int, n: int, num_segments: int, begins, ends,
+                      values0=None, values1=None, value_selector: int = 0, begin_bit: int = 0,
+                      end_bit: int | None = None, descending: bool = False, value_order: bool = False,
+                      stream=None):
+    """DoubleBuffer form; returns the new (key selector, value selector)."""
+    kb = ELEM_BYTES[key_suffix]
+    end_bit = kb * 8 if end_bit is None else end_bit
+    ks = C.c_int(selector)
+    vs = C.c_int(value_selector)
+    if values0 is None:
+        call(f"lcpp_hip_segmented_sort_keys_db_{key_suffix}", ptr(keys0), ptr(keys1), C.byref(ks), n, num_segments,
+             ptr(begins), ptr(ends), begin_bit, end_bit, int(descending), int(value_order), stream_handle(stream))
+    else:
+        call(f"lcpp_hip_segmented_sort_pairs_db_{key_suffix}_v{8 * values0.element_size()}", ptr(keys0), ptr(keys1),
+             C.byref(ks), ptr(values0), ptr(values1), C.byref(vs), n, num_segments, ptr(begins), ptr(ends),
+             begin_bit, end_bit, int(descending), int(value_order), stream_handle(stream))
+    return ks.value, vs.value

@@ -75,6 +75,8 @@ def lib() -> C.CDLL:
         h.oracle_segment_reduce.argtypes = [i32, i32, vp, vp, vp, u64, vp, vp, vp]
         h.oracle_segmented_scan.restype = None
         h.oracle_segmented_scan.argtypes = [i32, vp, vp, vp, vp, u64, i32, i32, u64, C.c_double, vp, vp]
+        h.oracle_segmented_sort.restype = i32
+        h.oracle_segmented_sort.argtypes = [i32, vp, vp, i32, vp, vp, u64, u64, vp, vp, u32, u32, i32, i32]
         _lib = h
     return _lib
 
@@ -339,3 +341,23 @@ def segmented_scan(x: np.ndarray, begins, ends, out_begins=None, inclusive=False
     lib().oracle_segmented_scan(_code(x), _p(x), _p(b), _p(e), _p(ob), b.size, int(inclusive), int(use_init),
                                 init_bits, float(init_v), _p(out), _p(ab))
     return out[:n_out], (ab[:n_out] if ab is not None else None)
+
+
+def segmented_sort(keys: np.ndarray, begins, ends, values: np.ndarray | None = None, begin_bit: int = 0,
+                   end_bit: int | None = None, descending: bool = False, value_order: bool = False,
+                   keys_out: np.ndarray | None = None, values_out: np.ndarray | None = None):
+    """Stable per-segment sort (oracle.c).  Items outside every segment keep keys_out / values_out
+    (copies of the inputs unless given)."""
+    keys = np.ascontiguousarray(keys)
+    b = np.ascontiguousarray(begins, dtype=np.uint32)
+    e = np.ascontiguousarray(ends, dtype=np.uint32)
+    ko = keys.copy() if keys_out is None else np.ascontiguousarray(keys_out).copy()
+    vin = None if values is None else np.ascontiguousarray(values)
+    vo = None if vin is None else (vin.copy() if values_out is None else np.ascontiguousarray(values_out).copy())
+    end_bit = keys.itemsize * 8 if end_bit is None else end_bit
+    rc = lib().oracle_segmented_sort(_code(keys), _p(keys), _p(ko), 0 if vin is None else vin.itemsize, _p(vin),
+                                     _p(vo), keys.size, b.size, _p(b), _p(e), begin_bit, end_bit, int(descending),
+                                     int(value_order))
+    if rc != 0:
+        raise MemoryError("oracle_segmented_sort")
+    return ko, vo

@@ -616,3 +616,84 @@ void oracle_segmented_scan(int type, const void* in, const uint32_t* begins, con
         }
     }
 }
+
+/* ------------------------------------------------------------------------------------------------
+ * Segmented sorts.  Follows DeviceSegmentedSort<> (src/lcpp/device/device_segmented_sort.h:43-505):
+ * every segment [begin[s], end[s]) (begin < end <= n) is sorted stably by the comparator; items outside
+ * every segment are not written.  DeviceSegmentedRadixSort<> (device_segmented_radix_sort.h:215-246)
+ * compares ((TwiddleIn(bits) >> begin_bit) & mask) for bits [begin_bit, end_bit); value_order compares
+ * the values (lhs < rhs; for floats -0.0 equals +0.0).  descending reverses the comparison.
+ * ---------------------------------------------------------------------------------------------- */
+static uint64_t sort_order_key(int type, uint64_t bits, uint32_t begin_bit, uint32_t end_bit) {
+    const int width = type_bytes(type) * 8;
+    const uint64_t sign = 1ull << (width - 1);
+    const uint64_t full = width == 64 ? ~0ull : ((1ull << width) - 1);
+    uint64_t t = bits & full;
+    if (type == 0 || type == 3) t ^= sign;
+    else if (type == 2 || type == 5) t = (t & sign) ? (~t & full) : (t | sign);
+    const uint32_t nb = end_bit - begin_bit;
+    if (nb == 0) return 0;
+    const uint64_t mask = nb >= 64 ? ~0ull : ((1ull << nb) - 1);
+    return (t >> begin_bit) & mask;
+}
+
+typedef struct {
+    int type, descending, value_order;
+    uint32_t begin_bit, end_bit;
+    const void* keys;
+} sort_ctx;
+
+/* a strictly before b */
+static int sort_before(const sort_ctx* c, uint64_t a, uint64_t b) {
+    if (c->value_order && (c->type == 2 || c->type == 5)) {
+        const double x = (double)fp_type_at(c->type, c->keys, a), y = (double)fp_type_at(c->type, c->keys, b);
+        return c->descending ? y < x : x < y;
+    }
+    const int bytes = type_bytes(c->type);
+    const uint64_t x = sort_order_key(c->type, load_bits(c->keys, a, bytes), c->begin_bit, c->end_bit);
+    const uint64_t y = sort_order_key(c->type, load_bits(c->keys, b, bytes), c->begin_bit, c->end_bit);
+    return c->descending ? y < x : x < y;
+}
+
+/* Stable bottom-up merge sort of idx[0, len) by sort_before. */
+static void stable_sort_indices(const sort_ctx* c, uint64_t* idx, uint64_t* tmp, uint64_t len) {
+    for (uint64_t w = 1; w < len; w *= 2) {
+        for (uint64_t lo = 0; lo < len; lo += 2 * w) {
+            const uint64_t mid = lo + w < len ? lo + w : len, hi = lo + 2 * w < len ? lo + 2 * w : len;
+            uint64_t i = lo, j = mid, k = lo;
+            while (i < mid && j < hi) tmp[k++] = sort_before(c, idx[j], idx[i]) ? idx[j++] : idx[i++];
+            while (i < mid) tmp[k++] = idx[i++];
+            while (j < hi) tmp[k++] = idx[j++];
+        }
+        memcpy(idx, tmp, len * sizeof(uint64_t));
+    }
+}
+
+int oracle_segmented_sort(int type, const void* keys_in, void* keys_out, int value_bytes, const void* values_in,
+                          void* values_out, uint64_t n, uint64_t num_segments, const uint32_t* begins,
+                          const uint32_t* ends, uint32_t begin_bit, uint32_t end_bit, int descending,
+                          int value_order) {
+    const int kb = type_bytes(type);
+    sort_ctx c = {type, descending, value_order, begin_bit, end_bit, keys_in};
+    for (uint64_t s = 0; s < num_segments; ++s) {
+        const uint64_t b = begins[s], e = ends[s];
+        if (b >= e || e > n) continue;
+        const uint64_t len = e - b;
+        uint64_t* idx = (uint64_t*)malloc(len * sizeof(uint64_t));
+        uint64_t* tmp = (uint64_t*)malloc(len * sizeof(uint64_t));
+        if (!idx || !tmp) {
+            free(idx);
+            free(tmp);
+            return -1;
+        }
+        for (uint64_t i = 0; i < len; ++i) idx[i] = b + i;
+        stable_sort_indices(&c, idx, tmp, len);
+        for (uint64_t i = 0; i < len; ++i) {
+            store_bits(keys_out, b + i, kb, load_bits(keys_in, idx[i], kb));
+            if (value_bytes) store_bits(values_out, b + i, value_bytes, load_bits(values_in, idx[i], value_bytes));
+        }
+        free(idx);
+        free(tmp);
+    }
+    return 0;
+}

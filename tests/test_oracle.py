@@ -635,3 +635,62 @@ def test_segment_ops_vs_numpy(orc, dtype):
         if e[s] > b[s] and all(not (b[t] < e[s] and b[s] < e[t]) or t == s for t in range(200)):
             want = np.cumsum(x[b[s]:e[s]].astype(np.float64 if dtype == np.float32 else np.int64))
             assert np.allclose(got[b[s]:e[s]].astype(np.float64), want.astype(dtype).astype(np.float64))
+
+
+# ---- segmented sorts ----------------------------------------------------------------------------------
+SEG_KEYS = [91, 3, -2, 3, 92, 8, 1, 8, 4, 93, 5, -1, 5, 2, -1, 7, 2, 5, 0]
+SEG_B, SEG_E = [1, 5, 5, 10], [4, 5, 9, 19]
+
+
+def _py_segmented(keys, begins, ends, key_fn, reverse=False):
+    out = list(range(len(keys)))
+    for b, e in zip(begins, ends):
+        if b < e:
+            # Python's sort is stable; descending keeps ties in order with reverse=True on a stable sort.
+            out[b:e] = sorted(range(b, e), key=lambda i: key_fn(keys[i]), reverse=reverse)
+    return out
+
+
+def test_segmented_sort_known_answer(orc):
+    """tests/device_segmented_sort_test.cpp:19-264: int keys {91, 3, -2, ...}, segments [1,4) [5,5) [5,9)
+    [10,19), values = index; items outside every segment untouched."""
+    keys = np.array(SEG_KEYS, np.int32)
+    vals = np.arange(19, dtype=np.uint32)
+    for desc in (False, True):
+        for value_order in (False, True):
+            ko, vo = orc.segmented_sort(keys, SEG_B, SEG_E, values=vals, descending=desc, value_order=value_order,
+                                        keys_out=np.full(19, -777, np.int32), values_out=np.full(19, 2**32 - 1, np.uint32))
+            order = _py_segmented(SEG_KEYS, SEG_B, SEG_E, lambda k: k, reverse=desc)
+            inside = [any(b <= i < e for b, e in zip(SEG_B, SEG_E)) for i in range(19)]
+            assert [int(k) for k, f in zip(ko, inside) if f] == [SEG_KEYS[order[i]] for i in range(19) if inside[i]]
+            assert [int(v) for v, f in zip(vo, inside) if f] == [order[i] for i in range(19) if inside[i]]
+            assert all(int(k) == -777 for k, f in zip(ko, inside) if not f)
+
+
+@pytest.mark.parametrize("dtype", [np.uint32, np.int32, np.int64, np.float32])
+def test_segmented_radix_bits_vs_python(orc, dtype):
+    """Radix order over bit ranges: stable by ((twiddled bits >> begin) & mask)."""
+    rng = np.random.default_rng(4)
+    n = 3000
+    keys = (rng.integers(-500, 500, n) if dtype != np.uint32 else rng.integers(0, 1000, n)).astype(dtype)
+    if dtype == np.float32:
+        keys = (keys / 7.0).astype(np.float32)
+    b = np.sort(rng.choice(n, 40, replace=False)).astype(np.uint32)
+    e = np.append(b[1:], n).astype(np.uint32)
+    e[::5] = b[::5]
+    bits = np.dtype(dtype).itemsize * 8
+    ubits = keys.view({4: np.uint32, 8: np.uint64}[keys.itemsize]).astype(object)
+    sign = 1 << (bits - 1)
+
+    def tw(u):
+        if dtype in (np.int32, np.int64):
+            return u ^ sign
+        if dtype == np.float32:
+            return (~u & ((1 << bits) - 1)) if u & sign else u | sign
+        return u
+    for lo, hi in ((0, bits), (2, 6), (3, bits - 1)):
+        mask = (1 << (hi - lo)) - 1
+        for desc in (False, True):
+            ko, _ = orc.segmented_sort(keys, b, e, begin_bit=lo, end_bit=hi, descending=desc)
+            order = _py_segmented(list(ubits), b, e, lambda u: (tw(int(u)) >> lo) & mask, reverse=desc)
+            np.testing.assert_array_equal(ko.view(np.uint8), keys[order].view(np.uint8))
