@@ -5,14 +5,15 @@ resident in HBM, one step = one SortKeys call.  The JSON line also carries the r
 dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
 one host thread), and the other benchmark configurations (reduce, scan, SortPairs, CsrMV) plus
 ExclusiveSumByKey / ReduceByKey and the stream-compaction family (select, partition, unique, run-length
-encode) and the segmented reduce / scan as achieved GB/s against the 8 TB/s HBM peak.
+encode), the segmented reduce / scan and the segmented sorts as achieved GB/s against the 8 TB/s HBM
+peak.
 
 `roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
 FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only bykey|compact|reduce|scan|segmented|sortpairs|spmv]
+                       [--only bykey|compact|reduce|scan|segmented|segsort|sortpairs|spmv]
 """
 from __future__ import annotations
 
@@ -275,9 +276,43 @@ def extra_segmented(hip, dev, steps, warmup, extra):
                                                       "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+def extra_segsort(hip, dev, steps, warmup, extra):
+    import torch
+    # DeviceSegmentedRadixSort::SortPairs over 2^26 uint32 keys + uint32 values in 2^14 segments of 4096
+    # (the LDS block phase, then one global merge pass), and SortKeys over 2^26 uint32 keys in 2^16
+    # segments of 1024 (block phase only).  Algorithmic bytes: every key (and value) read once and
+    # written once.
+    m = 1 << 26
+    keys = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_HI, keys, m, SEED + 13)
+    vals = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_IOTA, vals, m, 0)
+    ko, vo = torch.empty_like(keys), torch.empty_like(vals)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.segmented_sort_pairs_temp_bytes(m, 4, 4)), dtype=torch.int32,
+                       device=dev)
+    for name, seg_len, pairs in (("segmented_radix_sort_pairs_u32_2p26_4096", 4096, True),
+                                 ("segmented_radix_sort_keys_u32_2p26_1024", 1024, False)):
+        segs = m // seg_len
+        begins = torch.arange(segs, dtype=torch.int64, device=dev).mul_(seg_len).to(torch.int32)
+        ends = begins + seg_len
+        if pairs:
+            call = lambda: hip.segmented_sort("u32", keys, ko, m, segs, begins, ends, values_in=vals, values_out=vo,
+                                              temp=temp)
+        else:
+            call = lambda: hip.segmented_sort("u32", keys, ko, m, segs, begins, ends, temp=temp)
+        t = time_steps(call, steps, warmup)
+        block_ms, _ = kernel_avg_ms(hip, call, "segsort_block", 3)
+        merge_ms, merges = kernel_avg_ms(hip, call, "segsort_merge", 3)
+        moved = (16 if pairs else 8) * m
+        extra[name] = {"ms": round(t, 5), "Gkeys_per_s": round(m / t / 1e6, 2),
+                       "block_kernel_ms": round(block_ms, 5), "merge_kernel_ms": round(merge_ms, 5),
+                       "merge_launches_per_call": merges // 3,
+                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
           "bykey": extra_by_key, "compact": extra_compact,
-          "segmented": extra_segmented}
+          "segmented": extra_segmented, "segsort": extra_segsort}
 
 
 def run_extras(hip, dev, steps, warmup, names):

@@ -12,3 +12,5 @@
 #include "lcpp/device/device_run_length_encode.h"
 #include "lcpp/device/device_segment_reduce.h"
 #include "lcpp/device/device_segmented_scan.h"
+#include "lcpp/device/device_segmented_sort.h"
+#include "lcpp/device/device_segmented_radix_sort.h"

@@ -497,6 +497,14 @@ def segmented_scan(suffix: str, d_in, d_out, begins, ends, num_segments: int, in
 
 
 # ---- segmented sorts (DeviceSegmentedRadixSort, DeviceSegmentedSort) -----------------------------
+def segmented_sort_keys_temp_bytes(n: int, key_bytes: int) -> int:
+    return lib().lcpp_hip_segmented_sort_keys_temp_bytes(n, key_bytes)
+
+
+def segmented_sort_pairs_temp_bytes(n: int, key_bytes: int, value_bytes: int) -> int:
+    return lib().lcpp_hip_segmented_sort_pairs_temp_bytes(n, key_bytes, value_bytes)
+
+
 def segmented_sort(key_suffix: str, keys_in, keys_out, n: int, num_segments: int, begins, ends, values_in=None,
                    values_out=None, begin_bit: int = 0, end_bit: int | None = None, descending: bool = False,
                    value_order: bool = False, temp=None, stream=None) -> None:

@@ -5,7 +5,7 @@
 // Case sources: tests/device_reduce_test.cpp:95-173,425-514, tests/device_scan_test.cpp:80-447,
 // tests/device_select_test.cpp:248-500, tests/device_partition_test.cpp:103-377,
 // tests/device_run_length_encode_test.cpp:172-340, tests/device_segment_reduce.cpp:438-548,
-// tests/device_segmented_scan_test.cpp:11-257,
+// tests/device_segmented_scan_test.cpp:11-257, tests/device_segmented_sort_test.cpp:19-790,
 // tests/device_radix_sort_interface_test.cpp:68-283, tests/device_radix_sort_one_sweep.cpp:79-333,
 // tests/device_spmv_test.cpp:41-203 and the bench generators of tests/lcpp_cub_bench.cpp:516-521,
 // 666-672, 814.
@@ -77,9 +77,13 @@ struct Env {
     DeviceRunLengthEncode<> rle;
     DeviceSegmentReduce<> segment_reduce;
     DeviceSegmentedScan<> segmented_scan;
+    DeviceSegmentedSort<> segmented_sort;
+    DeviceSegmentedRadixSort<> segmented_radix_sort;
     Env() : device(context.create_device("hip")), stream(device.create_stream()) {
         segment_reduce.create(device);
         segmented_scan.create(device);
+        segmented_sort.create(device);
+        segmented_radix_sort.create(device);
         select.create(device);
         partition.create(device);
         rle.create(device);
@@ -871,6 +875,281 @@ void segmented_scan_known_answers() {
     EXPECT((download(e, inplace, 14) == std::vector<int>{100, 1, 3, 6, 5, 11, 18, 200, 9, 19, 30, 42, 300, 400}));
 }
 
+// ---- segmented sorts ----------------------------------------------------------------------------
+
+// Stable per-segment order of `keys` under `less`; items outside every segment map to UINT_MAX.
+template <typename K, typename Less>
+std::vector<uint> segment_order(const std::vector<K>& keys, const std::vector<uint>& b, const std::vector<uint>& en,
+                                Less less) {
+    std::vector<uint> order(keys.size(), std::numeric_limits<uint>::max());
+    for (size_t s = 0; s < b.size(); ++s) {
+        if (en[s] <= b[s]) continue;
+        std::vector<uint> idx(en[s] - b[s]);
+        std::iota(idx.begin(), idx.end(), b[s]);
+        std::stable_sort(idx.begin(), idx.end(), [&](uint x, uint y) { return less(keys[x], keys[y]); });
+        std::copy(idx.begin(), idx.end(), order.begin() + b[s]);
+    }
+    return order;
+}
+
+template <typename T>
+bool matches_order(const std::vector<T>& got, const std::vector<T>& src, const std::vector<uint>& order, T sentinel) {
+    for (size_t i = 0; i < got.size(); ++i) {
+        const T want = order[i] == std::numeric_limits<uint>::max() ? sentinel : src[order[i]];
+        if (std::memcmp(&got[i], &want, sizeof(T)) != 0) return false;
+    }
+    return true;
+}
+
+const std::vector<int> kSegKeys{91, 3, -2, 3, 92, 8, 1, 8, 4, 93, 5, -1, 5, 2, -1, 7, 2, 5, 0};
+const std::vector<uint> kSegBegin{1u, 5u, 5u, 10u}, kSegEnd{4u, 5u, 9u, 19u};
+
+// tests/device_segmented_sort_test.cpp:84-264: every copy-form entry point of DeviceSegmentedSort on
+// the 19-item, 4-segment case (one empty segment, items outside every segment keep the sentinel).
+void segmented_sort_all_entry_points() {
+    auto& e = *g_env;
+    constexpr uint n = 19u, m = 4u;
+    constexpr int KS = -777;
+    constexpr uint VS = std::numeric_limits<uint>::max();
+    std::vector<uint> vals(n);
+    std::iota(vals.begin(), vals.end(), 0u);
+    const auto asc = segment_order(kSegKeys, kSegBegin, kSegEnd, std::less<>{});
+    const auto desc = segment_order(kSegKeys, kSegBegin, kSegEnd, std::greater<>{});
+    auto ki = e.device.create_buffer<int>(n);
+    auto vi = e.device.create_buffer<uint>(n);
+    auto bb = e.device.create_buffer<uint>(m), eb = e.device.create_buffer<uint>(m);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceSegmentedSort<>::GetSortPairsTempStorageBytes<int, uint>(n)));
+    std::vector<Buffer<int>> ko;
+    std::vector<Buffer<uint>> vo;
+    for (int i = 0; i < 8; ++i) ko.push_back(e.device.create_buffer<int>(n));
+    for (int i = 0; i < 4; ++i) vo.push_back(e.device.create_buffer<uint>(n));
+    CommandList cmd;
+    auto t = temp.view();
+    e.segmented_sort.SortKeys(cmd, t, ki.view(), ko[0].view(), n, m, bb.view(), eb.view());
+    e.segmented_sort.SortKeysDescending(cmd, t, ki.view(), ko[1].view(), n, m, bb.view(), eb.view());
+    e.segmented_sort.StableSortKeys(cmd, t, ki.view(), ko[2].view(), n, m, bb.view(), eb.view());
+    e.segmented_sort.StableSortKeysDescending(cmd, t, ki.view(), ko[3].view(), n, m, bb.view(), eb.view());
+    e.segmented_sort.SortPairs(cmd, t, ki.view(), ko[4].view(), vi.view(), vo[0].view(), n, m, bb.view(), eb.view());
+    e.segmented_sort.SortPairsDescending(cmd, t, ki.view(), ko[5].view(), vi.view(), vo[1].view(), n, m, bb.view(),
+                                         eb.view());
+    e.segmented_sort.StableSortPairs(cmd, t, ki.view(), ko[6].view(), vi.view(), vo[2].view(), n, m, bb.view(),
+                                     eb.view());
+    e.segmented_sort.StableSortPairsDescending(cmd, t, ki.view(), ko[7].view(), vi.view(), vo[3].view(), n, m,
+                                               bb.view(), eb.view());
+    const std::vector<int> kfill(n, KS);
+    const std::vector<uint> vfill(n, VS);
+    e.stream << ki.copy_from(luisa::span{kSegKeys}) << vi.copy_from(luisa::span{vals})
+             << bb.copy_from(luisa::span{kSegBegin}) << eb.copy_from(luisa::span{kSegEnd});
+    for (auto& b : ko) e.stream << b.copy_from(luisa::span{kfill});
+    for (auto& b : vo) e.stream << b.copy_from(luisa::span{vfill});
+    e.stream << cmd.commit() << synchronize();
+    for (int i = 0; i < 8; ++i) EXPECT(matches_order(download(e, ko[i], n), kSegKeys, (i & 1) ? desc : asc, KS));
+    for (int i = 0; i < 4; ++i) EXPECT(matches_order(download(e, vo[i], n), vals, (i & 1) ? desc : asc, VS));
+    // Stability: the two 3s of segment 0 and the 8s of segment 2 keep their input order.
+    EXPECT((download(e, vo[0], n)[2] == 1u && download(e, vo[0], n)[3] == 3u));
+}
+
+// tests/device_segmented_sort_test.cpp:266-435: DoubleBuffer forms; 19 items take ceil(log2 19) = 5
+// merge passes, so the selector flips once (1 -> 0 for keys, 0 -> 1 for pairs) when the call is recorded.
+void segmented_sort_double_buffers() {
+    auto& e = *g_env;
+    constexpr uint n = 19u, m = 4u;
+    constexpr int KS = -777;
+    constexpr uint VS = std::numeric_limits<uint>::max();
+    std::vector<int> keys = kSegKeys;
+    std::vector<uint> vals(n);
+    std::iota(vals.begin(), vals.end(), 0u);
+    for (uint i : {0u, 4u, 9u}) keys[i] = KS, vals[i] = VS;
+    auto bb = e.device.create_buffer<uint>(m), eb = e.device.create_buffer<uint>(m);
+    e.stream << bb.copy_from(luisa::span{kSegBegin}) << eb.copy_from(luisa::span{kSegEnd});
+    const std::vector<int> kfill(n, KS);
+    const std::vector<uint> vfill(n, VS);
+    for (int desc = 0; desc < 2; ++desc) {
+        const auto order = desc ? segment_order(keys, kSegBegin, kSegEnd, std::greater<>{})
+                                : segment_order(keys, kSegBegin, kSegEnd, std::less<>{});
+        auto k0 = e.device.create_buffer<int>(n), k1 = e.device.create_buffer<int>(n);
+        DoubleBuffer<int> kb(k0.view(), k1.view());
+        kb.selector = 1;
+        CommandList cmd;
+        if (desc) e.segmented_sort.StableSortKeysDescending(cmd, BufferView<uint>{}, kb, n, m, bb.view(), eb.view());
+        else e.segmented_sort.SortKeys(cmd, BufferView<uint>{}, kb, n, m, bb.view(), eb.view());
+        EXPECT(kb.selector == 0);
+        e.stream << k0.copy_from(luisa::span{kfill}) << k1.copy_from(luisa::span{keys}) << cmd.commit()
+                 << synchronize();
+        EXPECT(matches_order(download(e, k0, n), keys, order, KS));
+
+        auto pk0 = e.device.create_buffer<int>(n), pk1 = e.device.create_buffer<int>(n);
+        auto pv0 = e.device.create_buffer<uint>(n), pv1 = e.device.create_buffer<uint>(n);
+        DoubleBuffer<int> pk(pk0.view(), pk1.view());
+        DoubleBuffer<uint> pv(pv0.view(), pv1.view());
+        CommandList cmd2;
+        if (desc) e.segmented_sort.SortPairsDescending(cmd2, BufferView<uint>{}, pk, pv, n, m, bb.view(), eb.view());
+        else e.segmented_sort.StableSortPairs(cmd2, BufferView<uint>{}, pk, pv, n, m, bb.view(), eb.view());
+        EXPECT(pk.selector == 1 && pv.selector == 1);
+        e.stream << pk0.copy_from(luisa::span{keys}) << pk1.copy_from(luisa::span{kfill})
+                 << pv0.copy_from(luisa::span{vals}) << pv1.copy_from(luisa::span{vfill}) << cmd2.commit()
+                 << synchronize();
+        EXPECT(matches_order(download(e, pk1, n), keys, order, KS));
+        EXPECT(matches_order(download(e, pv1, n), vals, order, VS));
+    }
+}
+
+// tests/device_segmented_sort_test.cpp:438-640: DeviceSegmentedRadixSort over bits [2, 6), copy and
+// DoubleBuffer forms, keys and pairs, ascending and descending.
+void segmented_radix_sort_partial_bits() {
+    auto& e = *g_env;
+    constexpr uint n = 19u, m = 4u, lo = 2u, hi = 6u;
+    constexpr uint VS = std::numeric_limits<uint>::max();
+    const std::vector<uint> keys{999u, 44u, 12u, 76u, 998u, 63u, 31u, 95u, 27u, 997u,
+                                 84u, 20u, 52u, 16u, 80u, 48u, 24u, 56u, 4u};
+    std::vector<uint> vals(n);
+    std::iota(vals.begin(), vals.end(), 0u);
+    auto field = [](uint k) { return (k >> lo) & ((1u << (hi - lo)) - 1u); };
+    const auto asc = segment_order(keys, kSegBegin, kSegEnd, [&](uint x, uint y) { return field(x) < field(y); });
+    const auto desc = segment_order(keys, kSegBegin, kSegEnd, [&](uint x, uint y) { return field(x) > field(y); });
+    auto ki = e.device.create_buffer<uint>(n), vi = e.device.create_buffer<uint>(n);
+    auto bb = e.device.create_buffer<uint>(m), eb = e.device.create_buffer<uint>(m);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceSegmentedRadixSort<>::GetSortPairsTempStorageBytes<uint, uint>(n)));
+    std::vector<Buffer<uint>> out;
+    for (int i = 0; i < 6; ++i) out.push_back(e.device.create_buffer<uint>(n));
+    CommandList cmd;
+    auto t = temp.view();
+    e.segmented_radix_sort.SortKeys(cmd, t, ki.view(), out[0].view(), n, m, bb.view(), eb.view(), lo, hi);
+    e.segmented_radix_sort.SortKeysDescending(cmd, t, ki.view(), out[1].view(), n, m, bb.view(), eb.view(), lo, hi);
+    e.segmented_radix_sort.SortPairs(cmd, t, ki.view(), out[2].view(), vi.view(), out[3].view(), n, m, bb.view(),
+                                     eb.view(), lo, hi);
+    e.segmented_radix_sort.SortPairsDescending(cmd, t, ki.view(), out[4].view(), vi.view(), out[5].view(), n, m,
+                                               bb.view(), eb.view(), lo, hi);
+    const std::vector<uint> fill(n, VS);
+    e.stream << ki.copy_from(luisa::span{keys}) << vi.copy_from(luisa::span{vals})
+             << bb.copy_from(luisa::span{kSegBegin}) << eb.copy_from(luisa::span{kSegEnd});
+    for (auto& b : out) e.stream << b.copy_from(luisa::span{fill});
+    e.stream << cmd.commit() << synchronize();
+    EXPECT(matches_order(download(e, out[0], n), keys, asc, VS));
+    EXPECT(matches_order(download(e, out[1], n), keys, desc, VS));
+    EXPECT(matches_order(download(e, out[2], n), keys, asc, VS));
+    EXPECT(matches_order(download(e, out[3], n), vals, asc, VS));
+    EXPECT(matches_order(download(e, out[4], n), keys, desc, VS));
+    EXPECT(matches_order(download(e, out[5], n), vals, desc, VS));
+
+    // DoubleBuffer forms start from selector 0 and 1 (the reference's :556-640).
+    std::vector<uint> dkeys = keys, dvals = vals;
+    for (uint i : {0u, 4u, 9u}) dkeys[i] = VS, dvals[i] = VS;
+    const auto dasc = segment_order(dkeys, kSegBegin, kSegEnd, [&](uint x, uint y) { return field(x) < field(y); });
+    for (int sel = 0; sel < 2; ++sel) {
+        auto a0 = e.device.create_buffer<uint>(n), a1 = e.device.create_buffer<uint>(n);
+        auto b0 = e.device.create_buffer<uint>(n), b1 = e.device.create_buffer<uint>(n);
+        DoubleBuffer<uint> kb(a0.view(), a1.view()), vb(b0.view(), b1.view());
+        kb.selector = vb.selector = sel;
+        CommandList c2;
+        e.segmented_radix_sort.SortPairs(c2, BufferView<uint>{}, kb, vb, n, m, bb.view(), eb.view(), lo, hi);
+        EXPECT(kb.selector == (sel ^ 1) && vb.selector == kb.selector);
+        e.stream << (sel ? a1 : a0).copy_from(luisa::span{dkeys}) << (sel ? a0 : a1).copy_from(luisa::span{fill})
+                 << (sel ? b1 : b0).copy_from(luisa::span{dvals}) << (sel ? b0 : b1).copy_from(luisa::span{fill})
+                 << c2.commit() << synchronize();
+        EXPECT(matches_order(download(e, sel ? a0 : a1, n), dkeys, dasc, VS));
+        EXPECT(matches_order(download(e, sel ? b0 : b1, n), dvals, dasc, VS));
+    }
+}
+
+// tests/device_segmented_sort_test.cpp:700-790: empty work, temp sizes of one item, signed keys over
+// the full width, and zero-width sorts (copy form copies, DoubleBuffer form keeps its selector).
+void segmented_sort_empty_signed_zero_width() {
+    auto& e = *g_env;
+    CommandList empty;
+    e.segmented_sort.SortKeys(empty, BufferView<uint>{}, BufferView<int>{}, BufferView<int>{}, 0u, 0u,
+                              BufferView<uint>{}, BufferView<uint>{});
+    e.segmented_radix_sort.SortKeys(empty, BufferView<uint>{}, BufferView<uint>{}, BufferView<uint>{}, 0u, 0u,
+                                    BufferView<uint>{}, BufferView<uint>{});
+    EXPECT(empty.empty());
+    EXPECT(DeviceSegmentedSort<>::GetSortKeysTempStorageBytes<int>(1u) == 0u);
+    EXPECT(DeviceSegmentedRadixSort<>::GetSortKeysTempStorageBytes<uint>(1u) == 0u);
+    // Temp layout of the reference (device_segmented_sort.h:49-75): keys, then values at their alignment.
+    EXPECT((DeviceSegmentedSort<>::GetSortKeysTempStorageBytes<int>(1000u) == 4000u));
+    EXPECT((DeviceSegmentedSort<>::GetSortPairsTempStorageBytes<int, double>(1001u) == 4008u + 8008u));
+
+    constexpr uint n = 8u;
+    const std::vector<int> keys{41, -7, 3, -7, 0, 22, -1, 3};
+    std::vector<uint> vals(n);
+    std::iota(vals.begin(), vals.end(), 0u);
+    std::vector<int> sorted = keys;
+    std::stable_sort(sorted.begin(), sorted.end());
+    auto ki = e.device.create_buffer<int>(n), sk = e.device.create_buffer<int>(n), zk = e.device.create_buffer<int>(n);
+    auto vi = e.device.create_buffer<uint>(n), zv = e.device.create_buffer<uint>(n);
+    auto d0 = e.device.create_buffer<int>(n), d1 = e.device.create_buffer<int>(n);
+    auto bb = e.device.create_buffer<uint>(1), eb = e.device.create_buffer<uint>(1);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceSegmentedRadixSort<>::GetSortPairsTempStorageBytes<int, uint>(n)));
+    DoubleBuffer<int> db(d0.view(), d1.view());
+    db.selector = 1;
+    CommandList cmd;
+    e.segmented_radix_sort.SortKeys(cmd, temp.view(), ki.view(), sk.view(), n, 1u, bb.view(), eb.view());
+    e.segmented_radix_sort.SortPairs(cmd, temp.view(), ki.view(), zk.view(), vi.view(), zv.view(), n, 1u, bb.view(),
+                                     eb.view(), 13u, 13u);
+    e.segmented_radix_sort.SortKeys(cmd, temp.view(), db, n, 1u, bb.view(), eb.view(), 13u, 13u);
+    EXPECT(db.selector == 1);
+    const uint b0 = 0u, e0 = n;
+    const std::vector<int> fill(n, -777);
+    e.stream << ki.copy_from(luisa::span{keys}) << vi.copy_from(luisa::span{vals}) << d0.copy_from(luisa::span{fill})
+             << d1.copy_from(luisa::span{keys}) << bb.copy_from(luisa::span{&b0, 1u})
+             << eb.copy_from(luisa::span{&e0, 1u}) << cmd.commit() << synchronize();
+    EXPECT(download(e, sk, n) == sorted);
+    EXPECT(download(e, zk, n) == keys);
+    EXPECT(download(e, zv, n) == vals);
+    EXPECT(download(e, d1, n) == keys);
+}
+
+// Larger inputs: 300,000 float keys (many ties, both zero signs) in 500 random segments, one of them
+// 70,000 items long (global merge passes); value order (DeviceSegmentedSort, -0.0 == +0.0) and radix
+// order (DeviceSegmentedRadixSort, -0.0 before +0.0) against std::stable_sort per segment.
+void segmented_sort_large_float_keys() {
+    auto& e = *g_env;
+    constexpr uint n = 300000u, m = 500u;
+    std::vector<float> keys(n);
+    for (uint i = 0; i < n; ++i) {
+        keys[i] = static_cast<float>(static_cast<int>(mix64(77, i) % 601u) - 300) / 8.0f;
+        if (keys[i] == 0.0f && (mix64(79, i) & 1u)) keys[i] = -0.0f;
+    }
+    std::vector<uint> cuts;
+    for (uint s = 1; s < m; ++s) cuts.push_back(static_cast<uint>(mix64(78, s) % n));
+    cuts.push_back(70000u);
+    std::sort(cuts.begin(), cuts.end());
+    cuts.erase(std::unique(cuts.begin(), cuts.end()), cuts.end());
+    // Segments: [0, 70000), then the random cuts above 70000 (contiguous up to n).
+    std::vector<uint> b2{0u}, e2{70000u};
+    for (uint c : cuts)
+        if (c > 70000u) e2.push_back(c), b2.push_back(c);
+    b2.insert(b2.begin() + 1, 70000u);
+    e2.push_back(n);
+    const uint segs = static_cast<uint>(b2.size());
+    std::vector<uint> vals(n);
+    std::iota(vals.begin(), vals.end(), 0u);
+    auto bits = [](float f) {
+        uint u;
+        std::memcpy(&u, &f, 4);
+        return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    };
+    const auto vorder = segment_order(keys, b2, e2, std::less<>{});
+    const auto rorder = segment_order(keys, b2, e2, [&](float x, float y) { return bits(x) > bits(y); });
+    auto ki = e.device.create_buffer<float>(n), k1 = e.device.create_buffer<float>(n);
+    auto k2 = e.device.create_buffer<float>(n);
+    auto vi = e.device.create_buffer<uint>(n), v1 = e.device.create_buffer<uint>(n);
+    auto bb = e.device.create_buffer<uint>(segs), eb = e.device.create_buffer<uint>(segs);
+    auto temp = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceSegmentedSort<>::GetSortPairsTempStorageBytes<float, uint>(n)));
+    CommandList cmd;
+    e.segmented_sort.SortPairs(cmd, temp.view(), ki.view(), k1.view(), vi.view(), v1.view(), n, segs, bb.view(),
+                               eb.view());
+    e.segmented_radix_sort.SortKeysDescending(cmd, temp.view(), ki.view(), k2.view(), n, segs, bb.view(), eb.view());
+    e.stream << ki.copy_from(luisa::span{keys}) << vi.copy_from(luisa::span{vals}) << bb.copy_from(luisa::span{b2})
+             << eb.copy_from(luisa::span{e2}) << cmd.commit() << synchronize();
+    EXPECT(matches_order(download(e, k1, n), keys, vorder, 0.0f));
+    EXPECT(matches_order(download(e, v1, n), vals, vorder, 0u));
+    EXPECT(matches_order(download(e, k2, n), keys, rorder, 0.0f));
+}
+
 // ---- record-time checks ------------------------------------------------------------------------
 
 void precondition_errors() {
@@ -903,6 +1182,19 @@ void precondition_errors() {
     DoubleBuffer<uint> bad(a.view(), a.view());
     bad.selector = 2;
     EXPECT(throws_error([&] { e.radix_sort.SortKeys(cmd, small.view(), bad, 4u); }));
+    EXPECT(throws_error([&] {
+        e.segmented_radix_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 1u, small.view(), small.view(), 5u, 4u);
+    }));
+    EXPECT(throws_error([&] {
+        e.segmented_sort.SortKeys(cmd, small.view(), a.view(), a.view(), n, 1u, small.view(), small.view());
+    }));
+    EXPECT(throws_error([&] {
+        e.segmented_sort.SortKeys(cmd, small.view(), a.view(), a.view(), 4u, 3u, small.view(), small.view());
+    }));
+    DeviceSegmentedSort<> no_segsort;
+    EXPECT(throws_error([&] {
+        no_segsort.SortKeys(cmd, small.view(), a.view(), a.view(), 1u, 1u, small.view(), small.view());
+    }));
     EXPECT(cmd.empty());  // nothing was recorded by a rejected call
 }
 
@@ -934,6 +1226,11 @@ const std::vector<Case>& cases() {
         {"run_length_encode_examples", run_length_encode_examples},
         {"segment_reduce_known_answers", segment_reduce_known_answers},
         {"segmented_scan_known_answers", segmented_scan_known_answers},
+        {"segmented_sort_all_entry_points", segmented_sort_all_entry_points},
+        {"segmented_sort_double_buffers", segmented_sort_double_buffers},
+        {"segmented_radix_sort_partial_bits", segmented_radix_sort_partial_bits},
+        {"segmented_sort_empty_signed_zero_width", segmented_sort_empty_signed_zero_width},
+        {"segmented_sort_large_float_keys", segmented_sort_large_float_keys},
         {"spmv_float_unsigned_indices", spmv_float_unsigned_indices},
         {"spmv_int_values_and_empty_work", spmv_int_values_and_empty_work},
         {"precondition_errors", precondition_errors},

@@ -18,4 +18,4 @@ def test_facade_cases():
     print(r.stdout)
     print(r.stderr)
     assert r.returncode == 0, r.stdout[-4000:] + r.stderr[-2000:]
-    assert "29 cases, 0 failures" in r.stdout
+    assert "34 cases, 0 failures" in r.stdout
