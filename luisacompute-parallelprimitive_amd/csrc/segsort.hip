@@ -19,8 +19,8 @@
 //     ... between the output and a scratch buffer, one thread per item; a segment takes part while the
 //     width is below its length.  The block phase writes a segment with an odd number of global passes
 //     to the scratch buffer, so that every segment's last pass lands in the output.  The block phase
-//     also records the longest segment in a per-stream device word; passes at or above that length
-//     exit after reading it.
+//     also records the longest segment in a per-stream device word (a slot of a static device array);
+//     passes at or above that length exit after reading it.
 //   * Orders: radix order compares (twiddled bits >> begin_bit) & mask (descending: the complement);
 //     value order (floats of DeviceSegmentedSort) compares the values, so -0.0 equals +0.0.
 // Algorithmic traffic: 2 * (sizeof(K) + sizeof(V)) per item in segments up to 2,048 items, plus the
@@ -342,28 +342,37 @@ uint32_t reference_pass_count(uint64_t n) {
     return p;
 }
 
-// One device word per (device, stream) that receives the longest segment of the call in flight on that
-// stream (calls on one stream run in order, so they never share it while running).  It is allocated on
-// the first call from a stream that is not being captured; a captured first call gets nullptr, and its
-// global passes then run without the early exit.
+// One device word per (device, stream) receives the longest segment of the call in flight on that
+// stream (calls on one stream run in order, so they never share it while running).  The words are slots
+// of a static device array (each GPU holds its own copy, found by hipGetSymbolAddress), handed out to
+// streams on their first call; no entry point allocates.  Past kLongestSlots distinct streams a call gets
+// nullptr and its global passes run without the early exit (same results).
+constexpr uint32_t kLongestSlots = 4096;
+__device__ uint32_t g_longest_slots[kLongestSlots];
+
 uint32_t* longest_word(hipStream_t stream) {
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, uint32_t*> words;
+    static std::map<int, std::pair<uint32_t*, uint32_t>> slots;  // device -> (array address, next slot)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lock(mu);
     const auto key = std::make_pair(dev, stream);
     const auto it = words.find(key);
     if (it != words.end()) return it->second;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    uint32_t* p = nullptr;
-    if (hipMalloc(reinterpret_cast<void**>(&p), 256) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
+    auto& slot = slots[dev];
+    if (!slot.first) {
+        void* base = nullptr;
+        if (hipGetSymbolAddress(&base, HIP_SYMBOL(g_longest_slots)) != hipSuccess || !base) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        slot.first = static_cast<uint32_t*>(base);
     }
-    words.emplace(key, p);
-    return p;
+    if (slot.second >= kLongestSlots) return nullptr;
+    uint32_t* word = slot.first + slot.second++;
+    words.emplace(key, word);
+    return word;
 }
 
 template <typename K, typename V, bool PAIRS, int KIND>

@@ -694,3 +694,24 @@ def test_segmented_radix_bits_vs_python(orc, dtype):
             ko, _ = orc.segmented_sort(keys, b, e, begin_bit=lo, end_bit=hi, descending=desc)
             order = _py_segmented(list(ubits), b, e, lambda u: (tw(int(u)) >> lo) & mask, reverse=desc)
             np.testing.assert_array_equal(ko.view(np.uint8), keys[order].view(np.uint8))
+
+
+def test_segmented_sort_value_order_floats(orc):
+    """DeviceSegmentedSort's default comparator (lhs < rhs, device_segmented_sort.h:77-105) on floats:
+    -0.0 and +0.0 are equal, so they keep their input order; against Python's stable sorted()."""
+    rng = np.random.default_rng(12)
+    n = 2000
+    keys = (rng.integers(-40, 40, n) / 4.0).astype(np.float64)
+    keys[rng.random(n) < 0.05] = -0.0
+    b = np.array([0, 700, 701, 1500], np.uint32)
+    e = np.array([700, 701, 1500, n], np.uint32)
+    for dtype in (np.float32, np.float64):
+        k = keys.astype(dtype)
+        for desc in (False, True):
+            ko, _ = orc.segmented_sort(k, b, e, value_order=True, descending=desc)
+            order = _py_segmented([float(x) for x in k], b, e, lambda x: x, reverse=desc)
+            np.testing.assert_array_equal(ko.view(np.uint8), k[order].view(np.uint8))
+    # Radix order of the same keys puts -0.0 before +0.0 (ascending).
+    k = np.array([0.0, -0.0, 0.0, -0.0], np.float32)
+    ko, _ = orc.segmented_sort(k, [0], [4])
+    assert np.signbit(ko).tolist() == [True, True, False, False]
