@@ -114,6 +114,24 @@ def test_long_segments_global_passes(hip, orc, dev, length):
         check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
 
 
+@pytest.mark.parametrize("ks", ["u64", "i64", "f64"])
+def test_eight_byte_keys_and_values(hip, orc, dev, ks):
+    """8-byte keys with 8-byte values (the largest LDS footprint: 72 KiB per workgroup), short segments and
+    segments that take global passes, ascending and descending; value order for f64."""
+    rng = np.random.default_rng(64 + len(ks))
+    n = 60_000
+    keys = keys_for(rng, n, ks)
+    vals = rng.integers(0, 1 << 63, n, dtype=np.uint64)
+    b = np.array([0, 5, 2000, 2049, 9000, 31_000], np.uint32)
+    e = np.array([5, 2000, 2049, 9000, 31_000, n - 7], np.uint32)
+    for desc in (False, True):
+        gk, gv = g_sort(hip, keys, b, e, values=vals, descending=desc)
+        check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
+    if ks == "f64":
+        gk, gv = g_sort(hip, keys, b, e, values=vals, value_order=True)
+        check(orc, keys, b, e, gk, gv, values=vals, value_order=True)
+
+
 def test_double_buffer_forms(hip, orc, dev):
     """DoubleBuffer sorts: the result lands where the selector points after ceil(log2 n) flips; a radix
     sort of zero bits leaves buffers and selector alone."""
