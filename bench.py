@@ -279,8 +279,8 @@ def extra_segmented(hip, dev, steps, warmup, extra):
 def extra_segsort(hip, dev, steps, warmup, extra):
     import torch
     # DeviceSegmentedRadixSort::SortPairs over 2^26 uint32 keys + uint32 values in 2^14 segments of 4096
-    # (the LDS block phase, then one global merge pass), and SortKeys over 2^26 uint32 keys in 2^16
-    # segments of 1024 (block phase only).  Algorithmic bytes: every key (and value) read once and
+    # (the chunk kernel sorts their 2048-item chunks, then one global merge pass), and SortKeys over 2^26
+    # uint32 keys in 2^16 segments of 1024 (the per-segment block kernel only).  Algorithmic bytes: every key (and value) read once and
     # written once.
     m = 1 << 26
     keys = torch.empty(m, dtype=torch.int32, device=dev)
@@ -302,10 +302,12 @@ def extra_segsort(hip, dev, steps, warmup, extra):
             call = lambda: hip.segmented_sort("u32", keys, ko, m, segs, begins, ends, temp=temp)
         t = time_steps(call, steps, warmup)
         block_ms, _ = kernel_avg_ms(hip, call, "segsort_block", 3)
+        chunk_ms, _ = kernel_avg_ms(hip, call, "segsort_chunk", 3)
         merge_ms, merges = kernel_avg_ms(hip, call, "segsort_merge", 3)
         moved = (16 if pairs else 8) * m
         extra[name] = {"ms": round(t, 5), "Gkeys_per_s": round(m / t / 1e6, 2),
-                       "block_kernel_ms": round(block_ms, 5), "merge_kernel_ms": round(merge_ms, 5),
+                       "block_kernel_ms": round(block_ms, 5), "chunk_kernel_ms": round(chunk_ms, 5),
+                       "merge_kernel_ms": round(merge_ms, 5),
                        "merge_launches_per_call": merges // 3,
                        "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
 

@@ -11,13 +11,17 @@
 // leaves a DoubleBuffer untouched.
 //
 // MI355X design:
-//   * Block phase: one 256-thread workgroup per segment sorts the segment's 2,048-item chunks
-//     (8 items per thread): a stable odd-even transposition sort of each thread's 8 items in registers,
+//   * Block phase: 2,048-item chunks are sorted by one 256-thread workgroup each (8 items per thread):
+//     one workgroup per segment for segments of at most 2,048 items, and for longer segments a
+//     grid-stride kernel over 2,048-item tiles of the item range that sorts the segment-aligned chunks
+//     starting in each tile (so a few long segments still fill the GPU).  Per chunk: a stable
+//     odd-even transposition sort of each thread's 8 items in registers,
 //     then 8 merge-path passes in LDS (widths 8 .. 1,024), each thread producing 8 outputs after one
 //     binary search; chunks are written to the output.
 //   * Global phase, only for segments longer than 2,048 items: merge-path passes of width 2,048, 4,096,
-//     ... between the output and a scratch buffer, one thread per item; a segment takes part while the
-//     width is below its length.  The block phase writes a segment with an odd number of global passes
+//     ... between the output and a scratch buffer, over 2,048-item output tiles (merge-path splits by
+//     wave-level searches, inputs staged in LDS); a segment takes part while the width is below its
+//     length.  The block phase writes a segment with an odd number of global passes
 //     to the scratch buffer, so that every segment's last pass lands in the output.  The block phase
 //     also records the longest segment in a per-stream device word (a slot of a static device array);
 //     passes at or above that length exit after reading it.
@@ -106,10 +110,89 @@ __device__ __forceinline__ uint32_t global_passes(uint64_t len) {
     return p;
 }
 
+// Sorts the chunk [c, c + len) (len <= 2,048) of keys_in / values_in into kdst / vdst with the whole
+// workgroup (it may be in place: every item is read before any is written).  Collective: every thread of
+// the workgroup calls it with the same arguments.
 template <typename K, typename V, bool PAIRS, int KIND>
-__global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, K* keys_scratch,
-                                                                 const V* values_in, V* values_out, V* values_scratch,
-                                                                 const uint32_t* __restrict__ begins,
+__device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* values_in, V* vdst, uint64_t c,
+                                           uint32_t len, const SortOrder& o, K (*s_keys)[kSsPadded<PAIRS>],
+                                           V (*s_vals)[PAIRS ? kSsPadded<PAIRS> : 1]) {
+    const uint32_t tid = threadIdx.x;
+    // Thread-local stable sort of items [8 tid, 8 tid + 8) of the chunk (padding never moves
+    // before real items: it is only compared with other padding).
+    K k[kSsItems];
+    V v[kSsItems];
+    const uint32_t base = tid * kSsItems;
+#pragma unroll
+    for (int j = 0; j < kSsItems; ++j) {
+        const bool ok = base + j < len;
+        k[j] = ok ? keys_in[c + base + j] : K(0);
+        if constexpr (PAIRS) v[j] = ok ? values_in[c + base + j] : V(0);
+    }
+    const uint32_t mine = base < len ? (len - base < kSsItems ? len - base : kSsItems) : 0u;
+#pragma unroll
+    for (int round = 0; round < kSsItems; ++round) {
+#pragma unroll
+        for (int j = round & 1; j + 1 < kSsItems; j += 2) {
+            if (static_cast<uint32_t>(j + 1) < mine && before<K, KIND>(k[j + 1], k[j], o)) {
+                const K tk = k[j];
+                k[j] = k[j + 1];
+                k[j + 1] = tk;
+                if constexpr (PAIRS) {
+                    const V tv = v[j];
+                    v[j] = v[j + 1];
+                    v[j + 1] = tv;
+                }
+            }
+        }
+    }
+    __syncthreads();  // the previous chunk's readers of s_keys are done
+#pragma unroll
+    for (int j = 0; j < kSsItems; ++j) {
+        s_keys[0][pad<PAIRS>(base + j)] = k[j];
+        if constexpr (PAIRS) s_vals[0][pad<PAIRS>(base + j)] = v[j];
+    }
+    __syncthreads();
+    int cur = 0;
+    for (uint32_t w = kSsItems; w < len; w *= 2) {
+        // Output positions [base, base + 8) of the merged pair of runs that holds them.
+        if (base < len) {
+            const uint32_t l0 = base / (2 * w) * (2 * w);
+            const uint32_t lw = len - l0 < w ? len - l0 : w;
+            const uint32_t r0 = l0 + lw;
+            const uint32_t rw = r0 < len ? (len - r0 < w ? len - r0 : w) : 0u;
+            const uint32_t diag = base - l0;
+            const K* sk = s_keys[cur];
+            auto left = [&](uint32_t i) { return sk[pad<PAIRS>(l0 + i)]; };
+            auto right = [&](uint32_t i) { return sk[pad<PAIRS>(r0 + i)]; };
+            uint32_t li = merge_path<K, KIND>(diag, lw, rw, left, right, o);
+            uint32_t ri = diag - li;
+            const uint32_t count = len - base < kSsItems ? len - base : kSsItems;
+            for (uint32_t j = 0; j < count; ++j) {
+                const K rk = sk[pad<PAIRS>(r0 + ri)], lk = sk[pad<PAIRS>(l0 + li)];
+                const bool take_left = li < lw && (ri >= rw || !before<K, KIND>(rk, lk, o));
+                const uint32_t src = pad<PAIRS>(take_left ? l0 + li : r0 + ri);
+                s_keys[cur ^ 1][pad<PAIRS>(base + j)] = sk[src];
+                if constexpr (PAIRS) s_vals[cur ^ 1][pad<PAIRS>(base + j)] = s_vals[cur][src];
+                if (take_left) ++li;
+                else ++ri;
+            }
+        }
+        cur ^= 1;
+        __syncthreads();
+    }
+    for (uint32_t q = tid; q < len; q += kSsBlock) {
+        kdst[c + q] = s_keys[cur][pad<PAIRS>(q)];
+        if constexpr (PAIRS) vdst[c + q] = s_vals[cur][pad<PAIRS>(q)];
+    }
+}
+
+// Block phase, segments of at most 2,048 items: one workgroup per segment.  Longer segments report
+// their length (so that the global passes above the longest one end at once; n < 2^32, so it fits) and
+// are left to the chunk kernel.
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, const V* values_in,
+                                                                 V* values_out, const uint32_t* __restrict__ begins,
                                                                  const uint32_t* __restrict__ ends, uint64_t n,
                                                                  SortOrder o, uint32_t* longest) {
     __shared__ K s_keys[2][kSsPadded<PAIRS>];
@@ -118,86 +201,15 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
     const uint64_t b = begins[seg];
     const uint64_t e = ends[seg];
     if (b >= e || e > n) return;
-    const uint32_t tid = threadIdx.x;
-    // Segments longer than one chunk report their length, so that the global passes above the longest
-    // one end at once (n < 2^32, so the length fits).
-    if (longest && tid == 0 && e - b > kSsChunk) atomicMax(longest, static_cast<uint32_t>(e - b));
-    // A segment that takes an odd number of global passes starts them from the scratch buffer, so that
-    // its last pass writes the output (a chunk is read whole before it is written, so the scratch may
-    // be the input itself).
-    const bool to_scratch = global_passes(e - b) & 1u;
-    K* kdst = to_scratch ? keys_scratch : keys_out;
-    V* vdst = to_scratch ? values_scratch : values_out;
-    for (uint64_t c = b; c < e; c += kSsChunk) {
-        const uint32_t len = static_cast<uint32_t>(e - c < kSsChunk ? e - c : kSsChunk);
-        // Thread-local stable sort of items [8 tid, 8 tid + 8) of the chunk (padding never moves
-        // before real items: it is only compared with other padding).
-        K k[kSsItems];
-        V v[kSsItems];
-        const uint32_t base = tid * kSsItems;
-#pragma unroll
-        for (int j = 0; j < kSsItems; ++j) {
-            const bool ok = base + j < len;
-            k[j] = ok ? keys_in[c + base + j] : K(0);
-            if constexpr (PAIRS) v[j] = ok ? values_in[c + base + j] : V(0);
-        }
-        const uint32_t mine = base < len ? (len - base < kSsItems ? len - base : kSsItems) : 0u;
-#pragma unroll
-        for (int round = 0; round < kSsItems; ++round) {
-#pragma unroll
-            for (int j = round & 1; j + 1 < kSsItems; j += 2) {
-                if (static_cast<uint32_t>(j + 1) < mine && before<K, KIND>(k[j + 1], k[j], o)) {
-                    const K tk = k[j];
-                    k[j] = k[j + 1];
-                    k[j + 1] = tk;
-                    if constexpr (PAIRS) {
-                        const V tv = v[j];
-                        v[j] = v[j + 1];
-                        v[j + 1] = tv;
-                    }
-                }
-            }
-        }
-        __syncthreads();  // the previous chunk's readers of s_keys are done
-#pragma unroll
-        for (int j = 0; j < kSsItems; ++j) {
-            s_keys[0][pad<PAIRS>(base + j)] = k[j];
-            if constexpr (PAIRS) s_vals[0][pad<PAIRS>(base + j)] = v[j];
-        }
-        __syncthreads();
-        int cur = 0;
-        for (uint32_t w = kSsItems; w < len; w *= 2) {
-            // Output positions [base, base + 8) of the merged pair of runs that holds them.
-            if (base < len) {
-                const uint32_t l0 = base / (2 * w) * (2 * w);
-                const uint32_t lw = len - l0 < w ? len - l0 : w;
-                const uint32_t r0 = l0 + lw;
-                const uint32_t rw = r0 < len ? (len - r0 < w ? len - r0 : w) : 0u;
-                const uint32_t diag = base - l0;
-                const K* sk = s_keys[cur];
-                auto left = [&](uint32_t i) { return sk[pad<PAIRS>(l0 + i)]; };
-                auto right = [&](uint32_t i) { return sk[pad<PAIRS>(r0 + i)]; };
-                uint32_t li = merge_path<K, KIND>(diag, lw, rw, left, right, o);
-                uint32_t ri = diag - li;
-                const uint32_t count = len - base < kSsItems ? len - base : kSsItems;
-                for (uint32_t j = 0; j < count; ++j) {
-                    const K rk = sk[pad<PAIRS>(r0 + ri)], lk = sk[pad<PAIRS>(l0 + li)];
-                    const bool take_left = li < lw && (ri >= rw || !before<K, KIND>(rk, lk, o));
-                    const uint32_t src = pad<PAIRS>(take_left ? l0 + li : r0 + ri);
-                    s_keys[cur ^ 1][pad<PAIRS>(base + j)] = sk[src];
-                    if constexpr (PAIRS) s_vals[cur ^ 1][pad<PAIRS>(base + j)] = s_vals[cur][src];
-                    if (take_left) ++li;
-                    else ++ri;
-                }
-            }
-            cur ^= 1;
-            __syncthreads();
-        }
-        for (uint32_t q = tid; q < len; q += kSsBlock) {
-            kdst[c + q] = s_keys[cur][pad<PAIRS>(q)];
-            if constexpr (PAIRS) vdst[c + q] = s_vals[cur][pad<PAIRS>(q)];
-        }
+    if (e - b > kSsChunk) {
+        // Same-address atomics serialise (~11 ns each), so only a length above the value seen is posted.
+        const uint32_t len = static_cast<uint32_t>(e - b);
+        if (longest && threadIdx.x == 0 && __hip_atomic_load(longest, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < len)
+            atomicMax(longest, len);
+        return;
     }
+    sort_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b, static_cast<uint32_t>(e - b), o,
+                                  s_keys, s_vals);
 }
 
 // Segment of item i (begins ascending): the last segment whose begin <= i, or -1.
@@ -231,6 +243,53 @@ __device__ __forceinline__ uint64_t wave_search(uint64_t lo, uint64_t hi, Pred p
         }
     }
     return lo;
+}
+
+// Block phase, segments longer than 2,048 items: grid-stride over 2,048-item tiles of the item range; a
+// tile sorts the segment-aligned chunks [b + 2,048 k, ...) that start inside it.  A long segment is
+// longer than a tile, so it meets a tile only as the segment holding the tile's first or last item, and
+// its chunk starts are a tile apart: a tile sorts at most two chunks.  A segment that takes an odd number
+// of global passes is sorted into the scratch buffer, so that its last pass writes the output (in place
+// when the scratch buffer is the input of a DoubleBuffer sort).
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(kSsBlock) void segsort_chunk_kernel(const K* keys_in, K* keys_out, K* keys_scratch,
+                                                                 const V* values_in, V* values_out, V* values_scratch,
+                                                                 const uint32_t* __restrict__ begins,
+                                                                 const uint32_t* __restrict__ ends,
+                                                                 uint32_t num_segments, uint64_t n, SortOrder o,
+                                                                 const uint32_t* longest) {
+    if (longest && *longest <= kSsChunk) return;  // no segment is longer than a chunk
+    __shared__ K s_keys[2][kSsPadded<PAIRS>];
+    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    __shared__ uint64_t s_seg[2];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6;
+    const uint64_t tiles = ceil_div(n, kSsChunk);
+    for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const uint64_t t0 = t * kSsChunk;
+        const uint64_t t1 = t0 + kSsChunk < n ? t0 + kSsChunk : n;
+        if (wave < 2) {
+            const uint64_t at = wave == 0 ? t0 : t1 - 1;
+            const uint64_t c = wave_search(0, num_segments, [&](uint64_t x) { return begins[x] > at; });
+            if ((tid & 63u) == 0) s_seg[wave] = c;  // segment index + 1 (0: before every segment)
+        }
+        __syncthreads();
+        const uint64_t c0 = s_seg[0], c1 = s_seg[1];
+        __syncthreads();
+        for (uint64_t c = c0; c <= c1; c = (c == c0 && c1 != c0) ? c1 : c1 + 1) {
+            if (c == 0) continue;
+            const uint64_t b = begins[c - 1], e = ends[c - 1];
+            if (b >= e || e > n || e - b <= kSsChunk || e <= t0 || b >= t1) continue;
+            const uint64_t from = b > t0 ? b : t0;
+            const uint64_t cs = b + ceil_div(from - b, kSsChunk) * kSsChunk;  // first chunk start >= from
+            if (cs >= t1 || cs >= e) continue;
+            const bool to_scratch = global_passes(e - b) & 1u;
+            sort_chunk<K, V, PAIRS, KIND>(keys_in, to_scratch ? keys_scratch : keys_out, values_in,
+                                          to_scratch ? values_scratch : values_out, cs,
+                                          static_cast<uint32_t>(e - cs < kSsChunk ? e - cs : kSsChunk), o, s_keys,
+                                          s_vals);
+        }
+    }
 }
 
 // One piece of a global pass: outputs [p0, p1) (at most 2,048) of the merge of the runs
@@ -411,16 +470,27 @@ int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_ou
     {
         LaunchScope scope("segsort_block", stream);
         segsort_block_kernel<K, V, PAIRS, KIND><<<static_cast<unsigned>(num_segments), kSsBlock, 0, stream>>>(
-            keys_in, keys_out, keys_scratch, values_in, values_out, values_scratch, begins, ends, n, o, longest);
+            keys_in, keys_out, values_in, values_out, begins, ends, n, o, longest);
         st = check_hip(hipGetLastError(), "segsort block launch");
         if (st != kOk) return st;
     }
     if (n <= kSsChunk) return kOk;
-    // Grid-stride over 2,048-item tiles on a bounded grid: a pass at or above the longest segment costs
-    // one word read per workgroup.
+    // Chunk kernel and global passes: grid-stride over 2,048-item tiles on a bounded grid, so a launch
+    // with no work (no segment longer than its width) costs one word read per workgroup.
     const uint64_t tiles = ceil_div(n, kSsChunk);
     const uint64_t cap = static_cast<uint64_t>(device_cu_count()) * 8;
     const unsigned grid = static_cast<unsigned>(tiles < cap ? tiles : cap);
+    {
+        // More workgroups than the passes use: each tile's segment searches are latency to hide.
+        const uint64_t chunk_cap = cap * 4;
+        const unsigned chunk_grid = static_cast<unsigned>(tiles < chunk_cap ? tiles : chunk_cap);
+        LaunchScope scope("segsort_chunk", stream);
+        segsort_chunk_kernel<K, V, PAIRS, KIND><<<chunk_grid, kSsBlock, 0, stream>>>(
+            keys_in, keys_out, keys_scratch, values_in, values_out, values_scratch, begins, ends,
+            static_cast<uint32_t>(num_segments), n, o, longest);
+        st = check_hip(hipGetLastError(), "segsort chunk launch");
+        if (st != kOk) return st;
+    }
     uint32_t pass = 0;
     for (uint64_t w = kSsChunk; w < n; w *= 2, ++pass) {
         LaunchScope scope("segsort_merge", stream);
