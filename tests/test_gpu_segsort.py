@@ -194,3 +194,29 @@ def test_errors(hip, dev):
     with pytest.raises(hip.LcppHipError) as err:
         hip.segmented_sort("u32", a, a.clone(), n, 1, b, e, temp=torch.empty(4, dtype=torch.int32, device=dev))
     assert err.value.status == hip.ERR_TEMP_TOO_SMALL
+
+
+def test_concurrent_streams_keep_their_own_longest_segment(hip, orc, dev):
+    """Two streams sort at the same time, one with a 300,000-item segment (nine global passes) and one whose
+    longest segment is 3,000 items: each stream's passes stop at its own longest segment, and both results
+    are exact."""
+    rng = np.random.default_rng(77)
+    n = 400_000
+    keys = keys_for(rng, n, "u32")
+    cases = [(np.array([0, 300_000], np.uint32), np.array([300_000, n], np.uint32)),
+             (np.arange(0, n, 3000, dtype=np.uint32), np.minimum(np.arange(0, n, 3000) + 3000, n).astype(np.uint32))]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    d_keys = to_dev(keys)
+    outs = [fill_dev(n, 4, 0x3C), fill_dev(n, 4, 0x3C)]
+    temps = [torch.empty(hip.bytes_to_uint_count(hip.segmented_sort_keys_temp_bytes(n, 4)), dtype=torch.int32,
+                         device=dev) for _ in range(2)]
+    offs = [(to_dev(b), to_dev(e)) for b, e in cases]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                hip.segmented_sort("u32", d_keys, outs[i], n, len(cases[i][0]), offs[i][0], offs[i][1], temp=temps[i],
+                                   stream=streams[i])
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            check(orc, keys, cases[i][0], cases[i][1], to_host(outs[i], np.uint32, n))
