@@ -280,7 +280,7 @@ def extra_segsort(hip, dev, steps, warmup, extra):
     import torch
     # DeviceSegmentedRadixSort::SortPairs over 2^26 uint32 keys + uint32 values in 2^14 segments of 4096
     # (the chunk kernel sorts their 2048-item chunks, then one global merge pass), and SortKeys over 2^26
-    # uint32 keys in 2^16 segments of 1024 (the per-segment block kernel only).  Algorithmic bytes: every key (and value) read once and
+    # uint32 keys in 2^16 segments of 1024 (the block kernel, one workgroup per segment).  Algorithmic bytes: every key (and value) read once and
     # written once.
     m = 1 << 26
     keys = torch.empty(m, dtype=torch.int32, device=dev)

@@ -11,10 +11,11 @@
 // leaves a DoubleBuffer untouched.
 //
 // MI355X design:
-//   * Block phase: 2,048-item chunks are sorted by one 256-thread workgroup each (8 items per thread):
-//     one workgroup per segment for segments of at most 2,048 items, and for longer segments a
-//     grid-stride kernel over 2,048-item tiles of the item range that sorts the segment-aligned chunks
-//     starting in each tile (so a few long segments still fill the GPU).  Per chunk: a stable
+//   * Block phase: chunks of at most 2,048 items, each sorted by one 256-thread workgroup (8 items per
+//     thread).  Small segments (<= 512 items) are sorted together per 2,048-item tile of the item
+//     range (a joint sort with position labels when a tile holds more than two), medium ones (<= 2,048)
+//     by one workgroup each, and long ones chunk by chunk by a grid-stride kernel over tiles, so
+//     neither many tiny segments nor a few long ones leave the GPU idle.  Per chunk: a stable
 //     odd-even transposition sort of each thread's 8 items in registers,
 //     then 8 merge-path passes in LDS (widths 8 .. 1,024), each thread producing 8 outputs after one
 //     binary search; chunks are written to the output.
@@ -23,8 +24,8 @@
 //     wave-level searches, inputs staged in LDS); a segment takes part while the width is below its
 //     length.  The block phase writes a segment with an odd number of global passes
 //     to the scratch buffer, so that every segment's last pass lands in the output.  The block phase
-//     also records the longest segment in a per-stream device word (a slot of a static device array);
-//     passes at or above that length exit after reading it.
+//     also records the longest segment (and whether a small one exists) in per-stream device words (a
+//     slot of a static device array); launches with nothing to do exit after reading them.
 //   * Orders: radix order compares (twiddled bits >> begin_bit) & mask (descending: the complement);
 //     value order (floats of DeviceSegmentedSort) compares the values, so -0.0 equals +0.0.
 // Algorithmic traffic: 2 * (sizeof(K) + sizeof(V)) per item in segments up to 2,048 items, plus the
@@ -42,6 +43,11 @@ namespace {
 constexpr int kSsBlock = 256;
 constexpr int kSsItems = 8;
 constexpr uint32_t kSsChunk = kSsBlock * kSsItems;  // 2048
+// Segments of at most this many items are sorted jointly per 2,048-item tile (tile kernel); longer ones
+// up to a chunk by one workgroup each (block kernel), longer still chunk by chunk (chunk kernel).  The
+// crossover was measured: 2^24 keys in 256-item segments 0.31 ms jointly vs 0.42 ms per segment, in
+// 1,024-item segments 0.27 vs 0.22 ms.
+constexpr uint32_t kSsSmall = 512;
 // Pair sorts' LDS arrays hold one pad word per 8 items: a thread's 8 consecutive outputs then start 9
 // words after its neighbour's, so the 64 lanes of a store hit distinct banks (measured: SortPairs block
 // phase 1.13 -> 1.03 ms; keys-only sorts ran slower padded, 0.75 -> 0.87 ms, and stay unpadded).
@@ -90,17 +96,23 @@ __device__ __forceinline__ bool before(K a, K b, const SortOrder& o) {
 
 // Number of items taken from `left` among the first `diag` outputs of the stable merge of left[0, lw)
 // and right[0, rw) (ties take left first).
-template <typename K, int KIND, typename GetLeft, typename GetRight>
-__device__ __forceinline__ uint32_t merge_path(uint32_t diag, uint32_t lw, uint32_t rw, GetLeft left, GetRight right,
-                                               const SortOrder& o) {
+template <typename RightFirst>
+__device__ __forceinline__ uint32_t merge_split(uint32_t diag, uint32_t lw, uint32_t rw, RightFirst right_first) {
     uint32_t lo = diag > rw ? diag - rw : 0u;
     uint32_t hi = diag < lw ? diag : lw;
     while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
-        if (before<K, KIND>(right(diag - 1 - mid), left(mid), o)) hi = mid;
+        if (right_first(mid)) hi = mid;
         else lo = mid + 1;
     }
     return lo;
+}
+
+// merge_split with right_first(mid) = "right[diag - 1 - mid] goes before left[mid]".
+template <typename K, int KIND, typename GetLeft, typename GetRight>
+__device__ __forceinline__ uint32_t merge_path(uint32_t diag, uint32_t lw, uint32_t rw, GetLeft left, GetRight right,
+                                               const SortOrder& o) {
+    return merge_split(diag, lw, rw, [&](uint32_t mid) { return before<K, KIND>(right(diag - 1 - mid), left(mid), o); });
 }
 
 // Number of global passes a segment of `len` items takes (widths 2048, 4096, ... below len).
@@ -113,11 +125,18 @@ __device__ __forceinline__ uint32_t global_passes(uint64_t len) {
 // Sorts the chunk [c, c + len) (len <= 2,048) of keys_in / values_in into kdst / vdst with the whole
 // workgroup (it may be in place: every item is read before any is written).  Collective: every thread of
 // the workgroup calls it with the same arguments.
-template <typename K, typename V, bool PAIRS, int KIND>
+//
+// LABELS: the chunk holds several groups (contiguous position ranges; s_label[p], bits 0-14, numbers the
+// group of position p in ascending order) that are sorted independently, and only positions with bit 15
+// set are written.  Because groups are contiguous and their labels ascend, every sorted run keeps each
+// group on the group's own positions, so a label is read by position and never moves: a right-run item
+// goes before a left-run item only when both positions have the same label and its key is before.
+template <typename K, typename V, bool PAIRS, int KIND, bool LABELS>
 __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* values_in, V* vdst, uint64_t c,
                                            uint32_t len, const SortOrder& o, K (*s_keys)[kSsPadded<PAIRS>],
-                                           V (*s_vals)[PAIRS ? kSsPadded<PAIRS> : 1]) {
+                                           V (*s_vals)[PAIRS ? kSsPadded<PAIRS> : 1], const uint16_t* s_label) {
     const uint32_t tid = threadIdx.x;
+    auto same_group = [&](uint32_t pa, uint32_t pb) { return !LABELS || s_label[pa] == s_label[pb]; };
     // Thread-local stable sort of items [8 tid, 8 tid + 8) of the chunk (padding never moves
     // before real items: it is only compared with other padding).
     K k[kSsItems];
@@ -134,7 +153,8 @@ __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* v
     for (int round = 0; round < kSsItems; ++round) {
 #pragma unroll
         for (int j = round & 1; j + 1 < kSsItems; j += 2) {
-            if (static_cast<uint32_t>(j + 1) < mine && before<K, KIND>(k[j + 1], k[j], o)) {
+            if (static_cast<uint32_t>(j + 1) < mine && before<K, KIND>(k[j + 1], k[j], o) &&
+                same_group(base + j, base + j + 1)) {
                 const K tk = k[j];
                 k[j] = k[j + 1];
                 k[j + 1] = tk;
@@ -163,14 +183,16 @@ __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* v
             const uint32_t rw = r0 < len ? (len - r0 < w ? len - r0 : w) : 0u;
             const uint32_t diag = base - l0;
             const K* sk = s_keys[cur];
-            auto left = [&](uint32_t i) { return sk[pad<PAIRS>(l0 + i)]; };
-            auto right = [&](uint32_t i) { return sk[pad<PAIRS>(r0 + i)]; };
-            uint32_t li = merge_path<K, KIND>(diag, lw, rw, left, right, o);
+            uint32_t li = merge_split(diag, lw, rw, [&](uint32_t mid) {
+                const uint32_t pr = r0 + diag - 1 - mid, pl = l0 + mid;
+                return before<K, KIND>(sk[pad<PAIRS>(pr)], sk[pad<PAIRS>(pl)], o) && same_group(pr, pl);
+            });
             uint32_t ri = diag - li;
             const uint32_t count = len - base < kSsItems ? len - base : kSsItems;
             for (uint32_t j = 0; j < count; ++j) {
                 const K rk = sk[pad<PAIRS>(r0 + ri)], lk = sk[pad<PAIRS>(l0 + li)];
-                const bool take_left = li < lw && (ri >= rw || !before<K, KIND>(rk, lk, o));
+                const bool take_left =
+                    li < lw && (ri >= rw || !(before<K, KIND>(rk, lk, o) && same_group(r0 + ri, l0 + li)));
                 const uint32_t src = pad<PAIRS>(take_left ? l0 + li : r0 + ri);
                 s_keys[cur ^ 1][pad<PAIRS>(base + j)] = sk[src];
                 if constexpr (PAIRS) s_vals[cur ^ 1][pad<PAIRS>(base + j)] = s_vals[cur][src];
@@ -182,34 +204,10 @@ __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* v
         __syncthreads();
     }
     for (uint32_t q = tid; q < len; q += kSsBlock) {
+        if (LABELS && !(s_label[q] >> 15)) continue;
         kdst[c + q] = s_keys[cur][pad<PAIRS>(q)];
         if constexpr (PAIRS) vdst[c + q] = s_vals[cur][pad<PAIRS>(q)];
     }
-}
-
-// Block phase, segments of at most 2,048 items: one workgroup per segment.  Longer segments report
-// their length (so that the global passes above the longest one end at once; n < 2^32, so it fits) and
-// are left to the chunk kernel.
-template <typename K, typename V, bool PAIRS, int KIND>
-__global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, const V* values_in,
-                                                                 V* values_out, const uint32_t* __restrict__ begins,
-                                                                 const uint32_t* __restrict__ ends, uint64_t n,
-                                                                 SortOrder o, uint32_t* longest) {
-    __shared__ K s_keys[2][kSsPadded<PAIRS>];
-    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
-    const uint32_t seg = blockIdx.x;
-    const uint64_t b = begins[seg];
-    const uint64_t e = ends[seg];
-    if (b >= e || e > n) return;
-    if (e - b > kSsChunk) {
-        // Same-address atomics serialise (~11 ns each), so only a length above the value seen is posted.
-        const uint32_t len = static_cast<uint32_t>(e - b);
-        if (longest && threadIdx.x == 0 && __hip_atomic_load(longest, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < len)
-            atomicMax(longest, len);
-        return;
-    }
-    sort_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b, static_cast<uint32_t>(e - b), o,
-                                  s_keys, s_vals);
 }
 
 // Segment of item i (begins ascending): the last segment whose begin <= i, or -1.
@@ -245,7 +243,58 @@ __device__ __forceinline__ uint64_t wave_search(uint64_t lo, uint64_t hi, Pred p
     return lo;
 }
 
-// Block phase, segments longer than 2,048 items: grid-stride over 2,048-item tiles of the item range; a
+// Medium segments (kSsSmall < items <= 2,048): one workgroup sorts each.  Workgroup g takes segment
+// indices [g * per_group, (g + 1) * per_group), one per thread at a time, so that many small segments
+// cost a read of their offsets rather than a workgroup each; per_group is 1 whenever segments average
+// more than kSsSmall items.  The kernel also sets words[1] when a small segment exists and posts the
+// longest segment above 2,048 items to words[0] (a relaxed load first: same-address atomics serialise at
+// ~11 ns each).
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, const V* values_in,
+                                                                 V* values_out, const uint32_t* __restrict__ begins,
+                                                                 const uint32_t* __restrict__ ends,
+                                                                 uint32_t num_segments, uint32_t per_group,
+                                                                 uint64_t n, SortOrder o, uint32_t* words) {
+    __shared__ K s_keys[2][kSsPadded<PAIRS>];
+    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    __shared__ uint32_t s_medium[kSsBlock];
+    __shared__ uint32_t s_count, s_small, s_long;
+    const uint32_t tid = threadIdx.x;
+    const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * per_group;
+    const uint64_t g1 = g0 + per_group < num_segments ? g0 + per_group : num_segments;
+    if (tid == 0) s_small = 0, s_long = 0;
+    for (uint64_t x0 = g0; x0 < g1; x0 += kSsBlock) {
+        if (tid == 0) s_count = 0;
+        __syncthreads();
+        const uint64_t x = x0 + tid;
+        if (x < g1) {
+            const uint64_t b = begins[x], e = ends[x];
+            if (b < e && e <= n) {
+                const uint64_t len = e - b;
+                if (len <= kSsSmall) s_small = 1;  // benign race: every writer stores 1
+                else if (len <= kSsChunk) s_medium[atomicAdd(&s_count, 1u)] = static_cast<uint32_t>(x);
+                else atomicMax(&s_long, static_cast<uint32_t>(len));
+            }
+        }
+        __syncthreads();
+        const uint32_t count = s_count;
+        for (uint32_t k = 0; k < count; ++k) {
+            const uint32_t x2 = s_medium[k];
+            const uint64_t b = begins[x2], e = ends[x2];
+            sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, b,
+                                                 static_cast<uint32_t>(e - b), o, s_keys, s_vals, nullptr);
+        }
+        __syncthreads();  // s_medium and s_count are rewritten next
+    }
+    if (words && tid == 0) {
+        if (s_small && __hip_atomic_load(&words[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+            __hip_atomic_store(&words[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (s_long && __hip_atomic_load(&words[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < s_long)
+            atomicMax(&words[0], s_long);
+    }
+}
+
+// Long segments (more than 2,048 items): grid-stride over 2,048-item tiles of the item range; a
 // tile sorts the segment-aligned chunks [b + 2,048 k, ...) that start inside it.  A long segment is
 // longer than a tile, so it meets a tile only as the segment holding the tile's first or last item, and
 // its chunk starts are a tile apart: a tile sorts at most two chunks.  A segment that takes an odd number
@@ -284,11 +333,119 @@ __global__ __launch_bounds__(kSsBlock) void segsort_chunk_kernel(const K* keys_i
             const uint64_t cs = b + ceil_div(from - b, kSsChunk) * kSsChunk;  // first chunk start >= from
             if (cs >= t1 || cs >= e) continue;
             const bool to_scratch = global_passes(e - b) & 1u;
-            sort_chunk<K, V, PAIRS, KIND>(keys_in, to_scratch ? keys_scratch : keys_out, values_in,
+            sort_chunk<K, V, PAIRS, KIND, false>(keys_in, to_scratch ? keys_scratch : keys_out, values_in,
                                           to_scratch ? values_scratch : values_out, cs,
                                           static_cast<uint32_t>(e - cs < kSsChunk ? e - cs : kSsChunk), o, s_keys,
-                                          s_vals);
+                                          s_vals, nullptr);
         }
+    }
+}
+
+// Small segments (at most kSsSmall items): grid-stride over 2,048-item tiles [t0, t1) of the item range,
+// one workgroup per tile.  The segments wholly inside the tile are sorted together: one or two on their
+// own, more in one joint sort of the tile (sort_chunk with labels: a position's label counts the begins
+// and ends of those segments at or before it, so each segment and each gap between them is one group;
+// only segment positions are written).  A small segment that starts in the tile and ends after it is
+// sorted on its own.  The block kernel sets words[1] when any small segment exists; otherwise this
+// kernel exits at once.
+template <typename K, typename V, bool PAIRS, int KIND>
+__global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in, K* keys_out, K* keys_scratch,
+                                                                const V* values_in, V* values_out, V* values_scratch,
+                                                                const uint32_t* __restrict__ begins,
+                                                                const uint32_t* __restrict__ ends,
+                                                                uint32_t num_segments, uint64_t n, SortOrder o,
+                                                                const uint32_t* words) {
+    if (words && words[1] == 0) return;  // no small segment
+    __shared__ K s_keys[2][kSsPadded<PAIRS>];
+    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    __shared__ uint16_t s_label[kSsChunk];
+    __shared__ uint64_t s_seg[2];
+    __shared__ uint32_t s_inside;       // segments of at most 2,048 items wholly inside the tile
+    __shared__ uint32_t s_pick[2][2];   // the first two of them (begin, end relative to t0)
+    // Thread totals of the label scan share s_label's space (they are read before labels are written).
+    uint32_t* s_total = reinterpret_cast<uint32_t*>(s_label);
+    // Boundary counts per position, packed (begins in the low half, ends in the high half), live in the
+    // second key buffer before the joint sort uses it (at least 2,048 words for every key type).
+    uint32_t* s_count = reinterpret_cast<uint32_t*>(&s_keys[1][0]);
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6;
+    const uint64_t tiles = ceil_div(n, kSsChunk);
+    for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const uint64_t t0 = t * kSsChunk;
+        const uint64_t t1 = t0 + kSsChunk < n ? t0 + kSsChunk : n;
+        const uint32_t tlen = static_cast<uint32_t>(t1 - t0);
+        if (wave < 2) {
+            const uint64_t at = wave == 0 ? t0 : t1 - 1;
+            const uint64_t c = wave_search(0, num_segments, [&](uint64_t x) { return begins[x] > at; });
+            if ((tid & 63u) == 0) s_seg[wave] = c;  // segment index + 1 (0: before every segment)
+        }
+        if (tid == 0) s_inside = 0;
+        __syncthreads();
+        const uint64_t c0 = s_seg[0], c1 = s_seg[1];
+        // Segments c0 - 1 .. c1 - 1 meet the tile; count the small ones wholly inside it.  One or two are
+        // sorted on their own; more take one joint sort with labels.
+        const uint64_t first = c0 > 0 ? c0 - 1 : 0;
+        for (uint64_t x = first + tid; x < c1; x += kSsBlock) {
+            const uint64_t b = begins[x], e = ends[x];
+            if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall) continue;
+            const uint32_t slot = atomicAdd(&s_inside, 1u);
+            if (slot < 2) {
+                s_pick[slot][0] = static_cast<uint32_t>(b - t0);
+                s_pick[slot][1] = static_cast<uint32_t>(e - t0);
+            }
+        }
+        __syncthreads();
+        const uint32_t inside = s_inside;
+        if (inside > 0 && inside <= 2) {
+            for (uint32_t k = 0; k < inside; ++k) {
+                const uint32_t pb = s_pick[k][0], pe = s_pick[k][1];
+                sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, t0 + pb, pe - pb, o,
+                                                     s_keys, s_vals, nullptr);
+            }
+        } else if (inside > 2) {
+            for (uint32_t q = tid; q < kSsChunk; q += kSsBlock) s_count[q] = 0;
+            __syncthreads();
+            for (uint64_t x = first + tid; x < c1; x += kSsBlock) {
+                const uint64_t b = begins[x], e = ends[x];
+                if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall) continue;
+                atomicAdd(&s_count[b - t0], 1u);
+                if (e < t1) atomicAdd(&s_count[e - t0], 1u << 16);
+            }
+            __syncthreads();
+            // Inclusive prefix of the packed counts: thread totals, a block scan over them, then labels.
+            const uint32_t base = tid * kSsItems;
+            uint32_t run = 0;
+#pragma unroll
+            for (int j = 0; j < kSsItems; ++j) run += s_count[base + j];
+            s_total[tid] = run;
+            __syncthreads();
+            for (uint32_t d = 1; d < kSsBlock; d <<= 1) {
+                const uint32_t add = tid >= d ? s_total[tid - d] : 0u;
+                __syncthreads();
+                s_total[tid] += add;
+                __syncthreads();
+            }
+            uint32_t acc = tid > 0 ? s_total[tid - 1] : 0u;
+            __syncthreads();  // every total is read before labels overwrite them
+#pragma unroll
+            for (int j = 0; j < kSsItems; ++j) {
+                acc += s_count[base + j];
+                const uint32_t opened = acc & 0xFFFFu, closed = acc >> 16;
+                s_label[base + j] = static_cast<uint16_t>((opened + closed) | (opened > closed ? 0x8000u : 0u));
+            }
+            __syncthreads();  // labels complete; s_count (in s_keys[1]) is free again
+            sort_chunk<K, V, PAIRS, KIND, true>(keys_in, keys_out, values_in, values_out, t0, tlen, o, s_keys,
+                                                s_vals, s_label);
+        }
+        __syncthreads();
+        // A small segment that starts in the tile and ends after it holds the tile's last item.
+        if (c1 > 0) {
+            const uint64_t b = begins[c1 - 1], e = ends[c1 - 1];
+            if (b < e && e <= n && e - b <= kSsSmall && b >= t0 && e > t1)
+                sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, b,
+                                                     static_cast<uint32_t>(e - b), o, s_keys, s_vals, nullptr);
+        }
+        __syncthreads();  // s_seg, s_count and s_label are rewritten by the next tile
     }
 }
 
@@ -412,13 +569,13 @@ uint32_t reference_pass_count(uint64_t n) {
     return p;
 }
 
-// One device word per (device, stream) receives the longest segment of the call in flight on that
-// stream (calls on one stream run in order, so they never share it while running).  The words are slots
+// Two device words per (device, stream) receive the longest segment and the small-segment flag of the
+// call in flight on that stream (calls on one stream run in order, so they never share them while running).  The words are slots
 // of a static device array (each GPU holds its own copy, found by hipGetSymbolAddress), handed out to
 // streams on their first call; no entry point allocates.  Past kLongestSlots distinct streams a call gets
 // nullptr and its global passes run without the early exit (same results).
 constexpr uint32_t kLongestSlots = 4096;
-__device__ uint32_t g_longest_slots[kLongestSlots];
+__device__ uint32_t g_longest_slots[2 * kLongestSlots];
 
 uint32_t* longest_word(hipStream_t stream) {
     static std::mutex mu;
@@ -440,7 +597,7 @@ uint32_t* longest_word(hipStream_t stream) {
         slot.first = static_cast<uint32_t*>(base);
     }
     if (slot.second >= kLongestSlots) return nullptr;
-    uint32_t* word = slot.first + slot.second++;
+    uint32_t* word = slot.first + 2 * slot.second++;
     words.emplace(key, word);
     return word;
 }
@@ -462,35 +619,49 @@ int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_ou
     }
     (void)width;
     int st;
-    uint32_t* longest = n > kSsChunk ? longest_word(stream) : nullptr;
-    if (longest) {
-        st = launch_fill_u32(longest, 1, 0u, stream);
+    // words[0]: the longest segment above 2,048 items; words[1]: set when a small segment exists.
+    uint32_t* words = longest_word(stream);
+    if (words) {
+        st = launch_fill_u32(words, 2, 0u, stream);
         if (st != kOk) return st;
     }
+    const uint64_t tiles = ceil_div(n, kSsChunk);
+    const uint64_t cap = static_cast<uint64_t>(device_cu_count()) * 8;
     {
+        // At most n / kSsSmall segments can be medium: never more workgroups than that.
+        const uint64_t target = n / kSsSmall > 0 ? n / kSsSmall : 1;
+        const uint64_t per_group = ceil_div(num_segments, target);
+        const unsigned groups = static_cast<unsigned>(ceil_div(num_segments, per_group));
         LaunchScope scope("segsort_block", stream);
-        segsort_block_kernel<K, V, PAIRS, KIND><<<static_cast<unsigned>(num_segments), kSsBlock, 0, stream>>>(
-            keys_in, keys_out, values_in, values_out, begins, ends, n, o, longest);
+        segsort_block_kernel<K, V, PAIRS, KIND><<<groups, kSsBlock, 0, stream>>>(
+            keys_in, keys_out, values_in, values_out, begins, ends, static_cast<uint32_t>(num_segments),
+            static_cast<uint32_t>(per_group), n, o, words);
         st = check_hip(hipGetLastError(), "segsort block launch");
         if (st != kOk) return st;
     }
-    if (n <= kSsChunk) return kOk;
-    // Chunk kernel and global passes: grid-stride over 2,048-item tiles on a bounded grid, so a launch
-    // with no work (no segment longer than its width) costs one word read per workgroup.
-    const uint64_t tiles = ceil_div(n, kSsChunk);
-    const uint64_t cap = static_cast<uint64_t>(device_cu_count()) * 8;
-    const unsigned grid = static_cast<unsigned>(tiles < cap ? tiles : cap);
     {
-        // More workgroups than the passes use: each tile's segment searches are latency to hide.
-        const uint64_t chunk_cap = cap * 4;
-        const unsigned chunk_grid = static_cast<unsigned>(tiles < chunk_cap ? tiles : chunk_cap);
-        LaunchScope scope("segsort_chunk", stream);
-        segsort_chunk_kernel<K, V, PAIRS, KIND><<<chunk_grid, kSsBlock, 0, stream>>>(
+        // Tile and chunk kernels: grid-stride over 2,048-item tiles with enough workgroups to hide each
+        // tile's segment searches; with no small (long) segment they exit after one word read.
+        const uint64_t tile_cap = cap * 4;
+        const unsigned tile_grid = static_cast<unsigned>(tiles < tile_cap ? tiles : tile_cap);
+        LaunchScope scope("segsort_tile", stream);
+        segsort_tile_kernel<K, V, PAIRS, KIND><<<tile_grid, kSsBlock, 0, stream>>>(
             keys_in, keys_out, keys_scratch, values_in, values_out, values_scratch, begins, ends,
-            static_cast<uint32_t>(num_segments), n, o, longest);
+            static_cast<uint32_t>(num_segments), n, o, words);
+        st = check_hip(hipGetLastError(), "segsort tile launch");
+        if (st != kOk) return st;
+        if (n <= kSsChunk) return kOk;
+        LaunchScope scope2("segsort_chunk", stream);
+        segsort_chunk_kernel<K, V, PAIRS, KIND><<<tile_grid, kSsBlock, 0, stream>>>(
+            keys_in, keys_out, keys_scratch, values_in, values_out, values_scratch, begins, ends,
+            static_cast<uint32_t>(num_segments), n, o, words);
         st = check_hip(hipGetLastError(), "segsort chunk launch");
         if (st != kOk) return st;
     }
+    // Global passes: grid-stride over 2,048-item tiles on a bounded grid; a pass with no work (no segment
+    // longer than its width) costs one word read per workgroup.
+    const uint32_t* longest = words;
+    const unsigned grid = static_cast<unsigned>(tiles < cap ? tiles : cap);
     uint32_t pass = 0;
     for (uint64_t w = kSsChunk; w < n; w *= 2, ++pass) {
         LaunchScope scope("segsort_merge", stream);
