@@ -220,3 +220,32 @@ def test_concurrent_streams_keep_their_own_longest_segment(hip, orc, dev):
         torch.cuda.synchronize()
         for i in (0, 1):
             check(orc, keys, cases[i][0], cases[i][1], to_host(outs[i], np.uint32, n))
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_mixed_lengths_with_gaps(hip, orc, dev, seed):
+    """Small (joint per-tile sorts with labels, including ones that cross a tile edge), medium (one
+    workgroup each) and long (chunked, global passes) segments in one call, with gaps of unsorted items
+    between segments that must stay untouched; pairs, ascending and descending."""
+    rng = np.random.default_rng(500 + seed)
+    n = 300_000
+    keys = keys_for(rng, n, "i32")
+    vals = np.arange(n, dtype=np.uint32)
+    b, e, pos = [], [], 0
+    while pos < n:
+        kind = rng.random()
+        length = int(rng.integers(1, 40) if kind < 0.6 else rng.integers(513, 2049) if kind < 0.85
+                     else rng.integers(2049, 20_000))
+        gap = int(rng.integers(0, 5)) if rng.random() < 0.5 else 0
+        start = pos + gap
+        end = min(start + length, n)
+        if start >= n:
+            break
+        b.append(start)
+        e.append(end)
+        pos = end
+    b = np.array(b, np.uint32)
+    e = np.array(e, np.uint32)
+    for desc in (False, True):
+        gk, gv = g_sort(hip, keys, b, e, values=vals, descending=desc)
+        check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
