@@ -183,3 +183,21 @@ def test_large_segmented(hip, orc, dev):
     got = g_scan(hip, x, b, e, inclusive=True)
     want, _ = orc.segmented_scan(x, b, e, inclusive=True)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ts", ["i32", "f32", "u64"])
+def test_segment_reduce_many_segments_grouped(hip, orc, dev, ts):
+    """More than 65,536 segments, so workgroups take several segments each: tiny segments reduced by one
+    wave, some longer than 1,024 items by the whole workgroup, empty and reversed ones, all ops."""
+    rng = np.random.default_rng(90 + len(ts))
+    m = 150_000
+    lengths = np.where(rng.random(m) < 0.002, rng.integers(1025, 6000, m), rng.integers(0, 12, m))
+    b = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.uint32)
+    e = (b.astype(np.int64) + lengths).astype(np.uint32)
+    n = int(e[-1])
+    x = values_for(rng, n, ts)
+    e[5::1000] = b[5::1000] // 2  # begin > end: empty
+    ops = ["sum", "min", "max"] + (["argmin", "argmax"] if ts in ("i32", "f32") else [])
+    for op in ops:
+        got, idx = g_reduce(hip, op, x, b, e)
+        check_reduce(orc, op, x, b, e, got, idx, ts)
