@@ -16,7 +16,8 @@
 // registers, then a wave shuffle reduction and a 4-wave combine in LDS.  With more segments the reduce
 // grid stays at 65,536 workgroups and each takes every 65,536th segment, four at a time: a wave reduces
 // a segment of at most 1,024 items alone, the workgroup reduces longer ones together (workgroup dispatch
-// bounds one-workgroup-per-segment grids: 2^24 items in 4-item segments 2.51 -> 0.61 ms).  Scans walk the segment in chunks of 2048
+// bounds one-workgroup-per-segment grids: 2^24 items in 4-item segments 2.51 -> 0.61 ms); scans are
+// grouped the same way, a wave scanning a short segment 64 items per step.  Workgroup scans walk the segment in chunks of 2048
 // items: each thread folds 8 consecutive items (16-byte accesses when the segment start is aligned),
 // a DPP wave scan and the LDS wave totals give every thread its chunk prefix, and a running carry
 // crosses chunks.  Segments with begin >= end are empty.  Integer sums wrap; float sums are ordered
@@ -102,6 +103,19 @@ __device__ __forceinline__ T shfl_xor_any(T v, int mask) {
         const uint64_t u = __builtin_bit_cast(uint64_t, v);
         const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u)), mask));
         const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u >> 32)), mask));
+        return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+}
+
+// Lane `src`'s value of v, for 32- and 64-bit types.
+template <typename T>
+__device__ __forceinline__ T read_lane_any(T v, int src) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __shfl(__builtin_bit_cast(int, v), src));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(u)), src));
+        const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(u >> 32)), src));
         return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
     }
 }
@@ -254,19 +268,12 @@ __device__ __forceinline__ T wave_scan_sum(T x) {
     return x;
 }
 
+// Scan of the non-empty segment [b, e) into out + ob by the whole workgroup (collective).
 template <typename T>
-__global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __restrict__ in, T* __restrict__ out,
-                                                                  const uint32_t* __restrict__ begins,
-                                                                  const uint32_t* __restrict__ ends,
-                                                                  const uint32_t* __restrict__ out_begins,
-                                                                  int inclusive, int use_init, T init) {
+__device__ __forceinline__ void block_scan_segment(const T* __restrict__ in, T* __restrict__ out, uint64_t b,
+                                                   uint64_t e, uint64_t ob, int inclusive, int use_init, T init,
+                                                   T* s_wave) {
     constexpr uint64_t kChunk = static_cast<uint64_t>(kSgBlock) * kScanItems;
-    __shared__ T s_wave[kSgWaves];
-    const uint32_t seg = blockIdx.x;
-    const uint64_t b = begins[seg];
-    const uint64_t e = ends[seg];
-    if (b >= e) return;
-    const uint64_t ob = out_begins[seg];
     const uint32_t wave = threadIdx.x / kWave;
     // Every thread's run of items starts at a multiple of kScanItems from the segment's begin, so
     // 16-byte vector accesses apply when the segment starts on a 16-byte boundary.
@@ -323,6 +330,68 @@ __global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __res
     }
 }
 
+// Scan of the non-empty segment [b, e) into out + ob by one wave: 64 items per step, a DPP wave scan and
+// a running carry.
+template <typename T>
+__device__ __forceinline__ void wave_scan_segment(const T* __restrict__ in, T* __restrict__ out, uint64_t b,
+                                                  uint64_t e, uint64_t ob, int inclusive, int use_init, T init) {
+    const uint32_t lane = lane_id();
+    T carry = use_init ? init : T(0);
+    for (uint64_t c = b; c < e; c += kWave) {
+        const uint64_t i = c + lane;
+        const T v = i < e ? in[i] : T(0);
+        const T inc = wave_scan_sum(v);
+        const T run = add_wrap(carry, dpp_move<dpp::kWaveShr1>(T(0), inc));
+        if (i < e) out[ob + (i - b)] = inclusive ? add_wrap(run, v) : run;
+        carry = add_wrap(carry, read_lane_any(inc, kWave - 1));
+    }
+}
+
+// Up to 65,536 segments: one workgroup per segment.  Above that the grid stays at 65,536 workgroups and
+// each takes every 65,536th segment, four at a time: a wave scans a segment of at most 1,024 items alone,
+// the workgroup scans longer ones together (one workgroup per segment is bound by dispatch).
+template <typename T>
+__global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                                  const uint32_t* __restrict__ begins,
+                                                                  const uint32_t* __restrict__ ends,
+                                                                  const uint32_t* __restrict__ out_begins,
+                                                                  int inclusive, int use_init, T init,
+                                                                  uint64_t num_segments) {
+    __shared__ T s_wave[kSgWaves];
+    __shared__ uint64_t s_big[kSgWaves];
+    __shared__ uint32_t s_nbig;
+    const uint64_t groups = gridDim.x;
+    if (num_segments <= groups) {
+        const uint32_t seg = blockIdx.x;
+        const uint64_t b = begins[seg], e = ends[seg];
+        if (b < e) block_scan_segment(in, out, b, e, static_cast<uint64_t>(out_begins[seg]), inclusive, use_init, init,
+                                      s_wave);
+        return;
+    }
+    const uint32_t wave = threadIdx.x / kWave;
+    for (uint64_t j = 0;; j += kSgWaves) {
+        if (blockIdx.x + j * groups >= num_segments) break;
+        if (threadIdx.x == 0) s_nbig = 0;
+        __syncthreads();
+        const uint64_t seg = blockIdx.x + (j + wave) * groups;
+        if (seg < num_segments) {
+            const uint64_t b = begins[seg], e = ends[seg];
+            if (b < e) {
+                if (e - b <= kSgWaveMax) wave_scan_segment(in, out, b, e, out_begins[seg], inclusive, use_init, init);
+                else if (lane_id() == 0) s_big[atomicAdd(&s_nbig, 1u)] = seg;
+            }
+        }
+        __syncthreads();
+        const uint32_t nbig = s_nbig;
+        for (uint32_t k = 0; k < nbig; ++k) {
+            const uint64_t big = s_big[k];
+            block_scan_segment(in, out, begins[big], ends[big], static_cast<uint64_t>(out_begins[big]), inclusive,
+                               use_init, init, s_wave);
+            __syncthreads();
+        }
+    }
+}
+
 unsigned checked_grid(uint64_t segments) { return static_cast<unsigned>(segments); }
 
 template <typename T, int OP>
@@ -357,8 +426,9 @@ int segmented_scan(const T* in, T* out, const uint32_t* begins, const uint32_t* 
     if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
     if (!in || !out || !begins || !ends) return set_error(kInvalidArgument, "%s: null input or output", what);
     LaunchScope scope("segmented_scan", stream);
-    segmented_scan_kernel<T><<<checked_grid(num_segments), kSgBlock, 0, stream>>>(
-        in, out, begins, ends, out_begins ? out_begins : begins, inclusive, use_init, init);
+    const uint64_t groups = num_segments < kSgMaxGroups ? num_segments : kSgMaxGroups;
+    segmented_scan_kernel<T><<<checked_grid(groups), kSgBlock, 0, stream>>>(
+        in, out, begins, ends, out_begins ? out_begins : begins, inclusive, use_init, init, num_segments);
     return check_hip(hipGetLastError(), "segmented_scan launch");
 }
 

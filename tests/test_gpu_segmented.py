@@ -201,3 +201,24 @@ def test_segment_reduce_many_segments_grouped(hip, orc, dev, ts):
     for op in ops:
         got, idx = g_reduce(hip, op, x, b, e)
         check_reduce(orc, op, x, b, e, got, idx, ts)
+
+
+@pytest.mark.parametrize("ts", ["i32", "u64", "f64"])
+def test_segmented_scan_many_segments_grouped(hip, orc, dev, ts):
+    """More than 65,536 segments: short segments scanned by one wave, some longer than 1,024 items by the
+    whole workgroup; exclusive, inclusive and with an initial value, packed output offsets."""
+    rng = np.random.default_rng(120 + len(ts))
+    m = 140_000
+    lengths = np.where(rng.random(m) < 0.002, rng.integers(1025, 5000, m), rng.integers(0, 150, m))
+    b = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.uint32)
+    e = (b.astype(np.int64) + lengths).astype(np.uint32)
+    n = int(e[-1])
+    x = values_for(rng, n, ts)
+    ob = b.copy()
+    for kw in ({}, {"inclusive": True}, {"inclusive": True, "init": 3}):
+        got = g_scan(hip, x, b, e, ob=ob, out_size=n, **kw)
+        want, ab = orc.segmented_scan(x, b, e, out_begins=ob, out_size=n, **kw)
+        if ts in REL:
+            assert np.all(np.abs(got.astype(np.float64) - want.astype(np.float64)) <= REL[ts] * ab + 1e-30), kw
+        else:
+            np.testing.assert_array_equal(got, want)
