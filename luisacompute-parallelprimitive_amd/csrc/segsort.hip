@@ -412,20 +412,23 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
                 if (e < t1) atomicAdd(&s_count[e - t0], 1u << 16);
             }
             __syncthreads();
-            // Inclusive prefix of the packed counts: thread totals, a block scan over them, then labels.
+            // Inclusive prefix of the packed counts: thread totals, a DPP wave scan, the four wave totals
+            // through LDS, then labels.
             const uint32_t base = tid * kSsItems;
             uint32_t run = 0;
 #pragma unroll
             for (int j = 0; j < kSsItems; ++j) run += s_count[base + j];
-            s_total[tid] = run;
+            uint32_t inc = run;
+            inc += dpp_move<dpp::kRowShr1>(0u, inc);
+            inc += dpp_move<dpp::kRowShr2>(0u, inc);
+            inc += dpp_move<dpp::kRowShr4>(0u, inc);
+            inc += dpp_move<dpp::kRowShr8>(0u, inc);
+            inc += dpp_move<dpp::kRowBcast15, 0xa>(0u, inc);
+            inc += dpp_move<dpp::kRowBcast31, 0xc>(0u, inc);
+            if ((tid & 63u) == 63u) s_total[wave] = inc;
             __syncthreads();
-            for (uint32_t d = 1; d < kSsBlock; d <<= 1) {
-                const uint32_t add = tid >= d ? s_total[tid - d] : 0u;
-                __syncthreads();
-                s_total[tid] += add;
-                __syncthreads();
-            }
-            uint32_t acc = tid > 0 ? s_total[tid - 1] : 0u;
+            uint32_t acc = inc - run;  // this thread's exclusive prefix within its wave
+            for (uint32_t w = 0; w < wave; ++w) acc += s_total[w];
             __syncthreads();  // every total is read before labels overwrite them
 #pragma unroll
             for (int j = 0; j < kSsItems; ++j) {
