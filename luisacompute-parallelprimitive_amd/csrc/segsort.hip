@@ -573,14 +573,22 @@ uint32_t reference_pass_count(uint64_t n) {
 }
 
 // Two device words per (device, stream) receive the longest segment and the small-segment flag of the
-// call in flight on that stream (calls on one stream run in order, so they never share them while running).  The words are slots
-// of a static device array (each GPU holds its own copy, found by hipGetSymbolAddress), handed out to
-// streams on their first call; no entry point allocates.  Past kLongestSlots distinct streams a call gets
-// nullptr and its global passes run without the early exit (same results).
+// call in flight on that stream (eager calls on one stream run in order, so they never share them while
+// running).  The words are slots of a static device array (each GPU holds its own copy, found by
+// hipGetSymbolAddress), handed out to streams on their first call; no entry point allocates.  A call
+// recorded into a graph gets no words: the graph may later replay on any stream, beside eager calls
+// or other replays, so its launches must not share a slot.  Such calls, and calls past kLongestSlots
+// distinct streams, get nullptr, and their kernels run without the early exits (same results).
 constexpr uint32_t kLongestSlots = 4096;
 __device__ uint32_t g_longest_slots[2 * kLongestSlots];
 
 uint32_t* longest_word(hipStream_t stream) {
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (capture != hipStreamCaptureStatusNone) return nullptr;
     static std::mutex mu;
     static std::map<std::pair<int, hipStream_t>, uint32_t*> words;
     static std::map<int, std::pair<uint32_t*, uint32_t>> slots;  // device -> (array address, next slot)
