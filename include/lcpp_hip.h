@@ -52,6 +52,13 @@ int lcpp_hip_profile_reset(void);
 int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches);
 int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes);
 
+#ifdef LCPP_HIP_PHASE_TRACE
+/* Diagnostic build (liblcpp_hip_trace.so) only: the onesweep and scan kernels write one record of
+ * 16 64-bit words per tile to `buffer` (device memory holding `records` records; null stops it).  No
+ * counterpart in the reference; its analogue is the per-phase timing of docs/epoch3_radix_sort.md:38-57. */
+int lcpp_hip_trace_set_buffer(void* buffer, uint64_t records);
+#endif
+
 /* Polls of a look-back predecessor that has not published yet before the waiting workgroup computes
  * that predecessor's contribution from the input itself (scan and onesweep sort).  Any value is
  * correct; 0 takes the fallback at once (used by tests), the default is 64.  Process-wide.
@@ -89,13 +96,22 @@ size_t lcpp_hip_scan_temp_bytes(uint64_t n, size_t elem_bytes); /* default polic
 int lcpp_hip_scan_exclusive_sum_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, void* stream);
 int lcpp_hip_scan_exclusive_sum_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
 int lcpp_hip_scan_exclusive_sum_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, void* stream);
+int lcpp_hip_scan_exclusive_sum_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_exclusive_sum_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_exclusive_sum_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, void* stream);
 int lcpp_hip_scan_inclusive_sum_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, void* stream);
 int lcpp_hip_scan_inclusive_sum_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
 int lcpp_hip_scan_inclusive_sum_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, void* stream);
+int lcpp_hip_scan_inclusive_sum_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, void* stream);
 /* Sum scan with an initial value: exclusive: out[i] = init + sum(in[0..i)); inclusive: init + sum(in[0..i]). */
 int lcpp_hip_scan_sum_init_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, int inclusive, int32_t init, void* stream);
 int lcpp_hip_scan_sum_init_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, int inclusive, uint32_t init, void* stream);
 int lcpp_hip_scan_sum_init_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, int inclusive, float init, void* stream);
+int lcpp_hip_scan_sum_init_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int64_t init, void* stream);
+int lcpp_hip_scan_sum_init_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, uint64_t init, void* stream);
+int lcpp_hip_scan_sum_init_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, double init, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * DeviceRadixSort (onesweep, 8-bit digits, stable LSD)
@@ -449,7 +465,7 @@ int lcpp_hip_generate(int kind, void* out, uint64_t n, uint64_t seed, uint64_t s
  * actually carve, the onesweep portion count for a given temp size, and the in-wave ranking variant
  * of the onesweep kernel (0 ballot match, 1 LDS lane-mask table, the default; same ranks).
  * ------------------------------------------------------------------------------------------- */
-size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n);
+size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n, size_t elem_bytes);
 size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
                                             uint32_t end_bit, int double_buffer);
 uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,

@@ -4,7 +4,11 @@ Every ``csrc/*.hip`` file is compiled by ``hipcc --offload-arch=gfx950`` into it
 parallel), host-only ``csrc/*.cpp`` files by ``g++``, and the objects are linked into one shared
 library next to this file.  The C-ABI is declared in ``include/lcpp_hip.h``.
 
-Usage: ``python luisacompute-parallelprimitive_amd/build.py [--jobs N]``
+``--phase-trace`` builds the diagnostic variant ``liblcpp_hip_trace.so`` instead: the same sources with
+``LCPP_HIP_PHASE_TRACE`` defined, whose onesweep and scan kernels write per-tile phase stamps
+(``phase_trace.py`` reads them).  The product library never contains that code.
+
+Usage: ``python luisacompute-parallelprimitive_amd/build.py [--jobs N] [--phase-trace]``
 """
 from __future__ import annotations
 
@@ -21,6 +25,8 @@ REPO = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "liblcpp_hip.so"
+TRACE_BUILD = PKG / "_build_trace"
+TRACE_LIB = PKG / "liblcpp_hip_trace.so"
 ARCH = "gfx950"
 
 HIP_FLAGS = [
@@ -39,43 +45,46 @@ def _hipcc() -> str:
     return path
 
 
-def _compile(src: pathlib.Path) -> pathlib.Path:
-    obj = BUILD / (src.name + ".o")
+def _compile(src: pathlib.Path, out_dir: pathlib.Path, defines: list[str]) -> pathlib.Path:
+    obj = out_dir / (src.name + ".o")
     if src.suffix == ".hip":
-        cmd = [_hipcc(), "-x", "hip", *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [_hipcc(), "-x", "hip", *HIP_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
     else:
-        cmd = ["g++", *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = ["g++", *HOST_FLAGS, *defines, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = False, phase_trace: bool = False) -> pathlib.Path:
+    out_dir, lib = (TRACE_BUILD, TRACE_LIB) if phase_trace else (BUILD, LIB)
+    defines = ["-DLCPP_HIP_PHASE_TRACE"] if phase_trace else []
+    out_dir.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, out_dir, defines), sources))
+    tmp = lib.with_suffix(".so.tmp")
     # Only the C-ABI (lcpp_hip_*) is exported: kernel stubs and C++ internals stay local, so two builds
     # loaded into one process never resolve each other's internals.
-    exports = BUILD / "exports.map"
+    exports = out_dir / "exports.map"
     exports.write_text("{\n  global: lcpp_hip_*;\n  local: *;\n};\n")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={exports}", "-o", str(tmp),
            *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--phase-trace", action="store_true", help="build the diagnostic liblcpp_hip_trace.so")
     args = ap.parse_args()
-    build(args.jobs, verbose=True)
+    build(args.jobs, verbose=True, phase_trace=args.phase_trace)
     sys.exit(0)

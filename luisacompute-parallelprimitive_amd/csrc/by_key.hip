@@ -521,7 +521,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     by_key_kernel<K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
-        values_out != nullptr && values_out == values_in, g_lookback_spin_limit);
+        values_out != nullptr && values_out == values_in, lookback_spin_limit());
     return check_hip(hipGetLastError(), MODE == kModeScan ? "scan_by_key launch" : "reduce_by_key launch");
 }
 

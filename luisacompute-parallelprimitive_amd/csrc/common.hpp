@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstddef>
 #include <type_traits>
@@ -135,6 +136,56 @@ __device__ __forceinline__ T atomic_add_agent(T* p, T v) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Per-tile phase stamps, compiled in only when LCPP_HIP_PHASE_TRACE is defined (the diagnostic
+// library liblcpp_hip_trace.so; the product library carries none of this).  A kernel takes
+// `s_memtime` (shader clock cycles) at its phase boundaries and thread 0 writes one record of
+// kTraceWords 64-bit words per tile: [0] s_memrealtime at start (100 MHz), [1..N] s_memtime
+// stamps, [13] kernel-specific counters, [14] HW_ID, [15] s_memrealtime at the end.
+// ------------------------------------------------------------------------------------------------
+#ifdef LCPP_HIP_PHASE_TRACE
+constexpr bool kPhaseTrace = true;
+#else
+constexpr bool kPhaseTrace = false;
+#endif
+constexpr int kTraceWords = 16;
+constexpr int kTraceStamps = 12;  // s_memtime slots 1..12
+
+struct PhaseClock {
+    uint64_t wall0 = 0;
+    uint64_t t[kTraceStamps] = {};
+    __device__ __forceinline__ void start() {
+        if constexpr (kPhaseTrace) {
+            wall0 = __builtin_amdgcn_s_memrealtime();
+            t[0] = __builtin_amdgcn_s_memtime();
+        }
+    }
+    // Stamp I (1 <= I < kTraceStamps).  `drain` first waits for the wave's outstanding memory
+    // operations, so the stamp marks their completion rather than their issue.
+    template <int I>
+    __device__ __forceinline__ void mark(bool drain = false) {
+        static_assert(I > 0 && I < kTraceStamps, "stamp index");
+        if constexpr (kPhaseTrace) {
+            if (drain) __builtin_amdgcn_s_waitcnt(0);
+            t[I] = __builtin_amdgcn_s_memtime();
+        }
+    }
+    // Called by one thread: writes the record of `slot` if the buffer has room for it.
+    __device__ __forceinline__ void write(uint64_t* buffer, uint64_t records, uint64_t slot, uint64_t counters) {
+        if constexpr (kPhaseTrace) {
+            if (buffer == nullptr || slot >= records) return;
+            uint64_t* r = buffer + slot * kTraceWords;
+            r[0] = wall0;
+#pragma unroll
+            for (int i = 0; i < kTraceStamps; ++i) r[1 + i] = t[i];
+            r[13] = counters;
+            // HW_ID (wave, SIMD, CU, shader array and engine of this wave): s_getreg_b32 of hwreg 4, bits 0..31.
+            r[14] = static_cast<uint32_t>(__builtin_amdgcn_s_getreg((31 << 11) | 4));
+            r[15] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
 // Small fill kernel (used instead of hipMemsetAsync so that callers may capture our launches
 // into HIP graphs).
 // ------------------------------------------------------------------------------------------------
@@ -171,11 +222,20 @@ struct LaunchScope {
 
 int launch_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, hipStream_t stream);
 
+#ifdef LCPP_HIP_PHASE_TRACE
+// Points the phase-trace records of one translation unit's kernels at `buffer` (diagnostic build).
+int radix_trace_set_buffer(void* buffer, uint64_t records);
+int scan_trace_set_buffer(void* buffer, uint64_t records);
+#endif
+
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
 // Polls of an INVALID look-back predecessor before the waiting workgroup computes that
-// predecessor's contribution itself (0: at once).  Shared by the scan and the onesweep sort.
-extern uint32_t g_lookback_spin_limit;
+// predecessor's contribution itself (0: at once).  Shared by every look-back kernel.  A test hook: any
+// value gives the same results.  Entry points read it once per call, so a concurrent change on another
+// thread takes effect at the next call.
+extern std::atomic<uint32_t> g_lookback_spin_limit;
+inline uint32_t lookback_spin_limit() { return g_lookback_spin_limit.load(std::memory_order_relaxed); }
 
 }  // namespace lcpp_hip

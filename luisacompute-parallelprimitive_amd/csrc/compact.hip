@@ -747,7 +747,7 @@ int run_compact(const char* what, void* temp, size_t temp_bytes, const U* in, co
     a.key_mask = key_mask;
     a.pred = pred;
     a.pred2 = pred2;
-    a.spin_limit = g_lookback_spin_limit;
+    a.spin_limit = lookback_spin_limit();
     a.partition = partition;
 
     int st = launch_fill_u32(reinterpret_cast<uint32_t*>(temp), plan.state_bytes / 4, 0u, stream);

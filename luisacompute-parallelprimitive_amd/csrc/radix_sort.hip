@@ -54,6 +54,12 @@ constexpr uint32_t kMaxPasses = 8;
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
 
+#ifdef LCPP_HIP_PHASE_TRACE
+// Phase-trace buffer of the diagnostic build: one record per (pass, tile), slot (shift / 8) * tiles + tile.
+__device__ uint64_t* g_trace_buffer = nullptr;
+__device__ uint64_t g_trace_records = 0;
+#endif
+
 enum KeyKind { kUnsigned = 0, kSigned = 1, kFloat = 2 };
 
 template <typename K> struct KeyTraits;
@@ -245,23 +251,129 @@ __device__ __forceinline__ uint32_t tile_of_block(uint32_t b, uint32_t tiles) {
     return ((j / kXcdGroup) * kXcds + x) * kXcdGroup + j % kXcdGroup;
 }
 
-// Look-back fallback: digit counts of the full tile `tile` of `keys`, accumulated in LDS `counts`
-// (256 words).  Called by every thread of the workgroup.
-template <typename K, bool DESC, int BLOCK, int ITEMS>
-__device__ void tile_digit_counts(const K* __restrict__ keys, uint32_t tile, uint32_t shift, uint32_t mask,
-                                  uint32_t* counts) {
+struct MinOpU32 {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return a < b ? a : b; }
+    template <typename T>
+    __device__ __forceinline__ static constexpr T identity() { return ~T(0); }
+};
+
+// Look-back of one wave.  Lane l owns digit d = 64 w + l (w = the wave, one of the four waves that hold
+// the 256 digits) and returns the number of keys with digit d in the tiles before `tile` of this
+// portion: the counts the predecessors published for d, newest first, down to and including the
+// nearest INCLUSIVE entry (tile 0 publishes INCLUSIVE at once, so every walk ends).  Each step loads
+// the entries of WIN consecutive predecessors (one cross-XCD round trip); a window of PARTIAL entries
+// only is summed with min / max / add alone (the status bits 01 of WIN words add up to a multiple of
+// 2^32, as WIN is a multiple of 4).  Waves walk independently, with no barrier.
+//
+// An entry still unpublished before the lane's nearest INCLUSIVE one is polled; after `spin_limit`
+// polls the wave counts the digits of the newest such tile itself (its 64 digits only, in the wave's
+// 64 words of `s_fb`) and publishes them as PARTIAL by compare-and-swap, so progress never depends on
+// dispatch order.  A predecessor tile is always full (only the last tile is partial).
+template <typename K, bool DESC, int BLOCK, int ITEMS, int WIN>
+__device__ __forceinline__ uint32_t lookback_digit(uint32_t* __restrict__ lookback, uint32_t tile, uint32_t d,
+                                                   const K* __restrict__ keys_in, uint32_t shift, uint32_t mask,
+                                                   uint32_t spin_limit, uint32_t* s_fb, uint32_t& steps,
+                                                   uint32_t& spins_total, uint32_t& fallbacks) {
+    static_assert(WIN % 4 == 0, "WIN * 2^30 must vanish modulo 2^32");
     using U = typename KeyTraits<K>::U;
     constexpr int KIND = KeyTraits<K>::kind;
     constexpr uint32_t TILE = static_cast<uint32_t>(BLOCK) * ITEMS;
-    for (uint32_t i = threadIdx.x; i < kDigits; i += BLOCK) counts[i] = 0;
-    __syncthreads();
-    const U* ukeys = reinterpret_cast<const U*>(keys) + static_cast<uint64_t>(tile) * TILE;
-    for (uint32_t i = threadIdx.x; i < TILE; i += BLOCK) {
-        const U ordered = twiddle_in<U, KIND, DESC>(ukeys[i]);
-        atomicAdd(&counts[digit_of<U, KIND>(ordered, shift, mask)], 1u);
+    const uint32_t lane = lane_id();
+    uint32_t excl = 0;
+    bool done = false;
+    // Newest predecessor of the window; wave-uniform, so each entry's address is a scalar row base
+    // plus the lane's digit offset.  It never goes below 0: the window holding tile 0 ends every walk.
+    uint32_t top = tile - 1;
+    while (true) {
+        top = __builtin_amdgcn_readfirstlane(top);
+        // The row addresses are recomputed at each load site rather than kept in registers across the
+        // polling loop (an empty asm statement hides `top` from loop-invariant code motion).
+        asm volatile("" : "+s"(top));
+        uint32_t v[WIN];
+#pragma unroll
+        for (int w = 0; w < WIN; ++w) {
+            v[w] = kFlagInclusive;  // entries before tile 0 stop the walk
+            if (top >= static_cast<uint32_t>(w) && !done)
+                v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
+        }
+        uint32_t spins = 0;
+        uint32_t sum = 0;
+        bool stop = false;
+        while (true) {
+            uint32_t lo = v[0], hi = v[0], all = 0;
+#pragma unroll
+            for (int w = 0; w < WIN; ++w) {
+                lo = min(lo, v[w]);
+                hi = max(hi, v[w]);
+                all += v[w];
+            }
+            bool wait = false;
+            uint32_t first_wait = ~0u;
+            if (lo >= kFlagPartial && hi < kFlagInclusive) {
+                sum = all;
+                stop = false;
+            } else {
+                sum = 0;
+                stop = false;
+#pragma unroll
+                for (int w = 0; w < WIN; ++w) {
+                    if (!stop && !wait) {
+                        if ((v[w] & ~kCountMask) == 0) {
+                            wait = true;
+                            first_wait = static_cast<uint32_t>(w);
+                        } else {
+                            sum += v[w] & kCountMask;
+                            stop = (v[w] & kFlagInclusive) != 0;
+                        }
+                    }
+                }
+            }
+            wait = wait && !done;
+            if (wave_ballot(wait) == 0) break;
+            if (spins >= spin_limit) {
+                // Count the newest tile some lane waits for and publish this wave's 64 digits of it
+                // (a compare-and-swap from 0 that loses to the owner's own publication changes
+                // nothing); the reload below then reads it.
+                if constexpr (kPhaseTrace) ++fallbacks;
+                const uint32_t wf = wave_reduce(wait ? first_wait : ~0u, MinOpU32{});
+                const uint64_t jf = top - wf;
+                const uint32_t d0 = d - lane;
+                __hip_atomic_store(&s_fb[lane], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                const U* ukeys = reinterpret_cast<const U*>(keys_in) + jf * TILE;
+                for (uint32_t i = lane; i < TILE; i += kWave) {
+                    const uint32_t dk = digit_of<U, KIND>(twiddle_in<U, KIND, DESC>(ukeys[i]), shift, mask) - d0;
+                    if (dk < kWave) __hip_atomic_fetch_add(&s_fb[dk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                const uint32_t cnt = __hip_atomic_load(&s_fb[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+                uint32_t expected = 0;
+                __hip_atomic_compare_exchange_strong(lookback + jf * kDigits + d, &expected, kFlagPartial | cnt,
+                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __builtin_amdgcn_s_sleep(1);
+                ++spins;
+                if constexpr (kPhaseTrace) ++spins_total;
+            }
+            asm volatile("" : "+s"(top));
+#pragma unroll
+            for (int w = 0; w < WIN; ++w) {
+                if (top >= static_cast<uint32_t>(w) && wait && (v[w] & ~kCountMask) == 0)
+                    v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
+            }
+        }
+        if (!done) {
+            excl += sum;
+            done = stop;
+        }
+        if constexpr (kPhaseTrace) ++steps;
+        if (wave_ballot(!done) == 0) break;
+        top -= WIN;  // some lane has not reached an INCLUSIVE entry, so the window held no tile 0
     }
-    __syncthreads();
+    return excl;
 }
+
 template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW, int RANK>
 // Register budget for two workgroups per CU: BLOCK / 128 waves per SIMD (128 VGPRs at 512 threads,
 // 64 at 1024).
@@ -287,17 +399,13 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // digit-count row (256 x 4 B; running counts during the rank, then the wave's offsets inside the
     // tile).  Once every thread has read its offsets back (a barrier), the buffer holds the keys
     // reordered by digit, and after the key scatter the values.
-    constexpr int LB_GROUPS = BLOCK / static_cast<int>(kDigits);
     static_assert(W * kDigits * (sizeof(uint64_t) + sizeof(uint32_t)) <= TILE * ELEM,
                   "rank tables and count rows must fit the tile buffer");
     __shared__ __attribute__((aligned(16))) unsigned char s_tile[TILE * ELEM];
-    __shared__ uint32_t s_lb[LB_GROUPS][kDigits];  // look-back: group sums (rows 0..G-2), done flag (row G-1)
-    // Digit counts of a predecessor tile during the look-back fallback, then (after the look-back's
-    // last barrier) each digit's global-minus-local output offset.
+    // Each digit's global-minus-local output offset.  Before a look-back wave writes its 64 entries,
+    // they are its scratch for the look-back fallback.
     __shared__ uint32_t s_global_minus_local[kDigits];
     __shared__ uint32_t s_scan[kDigits / kWave];
-    __shared__ uint32_t s_fallback_tile;
-    uint32_t* const s_fallback = s_global_minus_local;
     uint64_t (*s_match)[kDigits] = reinterpret_cast<uint64_t (*)[kDigits]>(s_tile);
     uint32_t (*s_counts)[kDigits] =
         reinterpret_cast<uint32_t (*)[kDigits]>(s_tile + W * kDigits * sizeof(uint64_t));
@@ -306,6 +414,9 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t mask = (1u << num_bits) - 1u;
+    PhaseClock clk;
+    clk.start();
+    uint32_t trace_steps = 0, trace_spins = 0, trace_fallbacks = 0;
 
     // Wave-private tables: no barrier needed before the wave uses them.
 #pragma unroll
@@ -340,6 +451,8 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
             vals[k] = i < valid ? __builtin_nontemporal_load(&uvals[i]) : VW(0);
         }
     }
+
+    clk.mark<1>(true);  // keys loaded
 
     // Rank inside the wave: rank = keys of the same digit in earlier rounds (the wave's LDS counter)
     // + lanes of the same digit below this lane in this round.  The highest such lane advances the
@@ -380,6 +493,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         }
     }
     __syncthreads();
+    clk.mark<2>();  // every wave ranked
 
     // Per digit: wave offsets, tile count, PARTIAL publish, tile-local start.
     uint32_t count = 0, local_start = 0;
@@ -408,6 +522,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         for (int w = 0; w < W; ++w) s_counts[w][d] += local_start;
     }
     __syncthreads();
+    clk.mark<3>();  // PARTIAL published, tile offsets scanned
 
     // Reorder keys by digit in LDS now: local positions do not depend on the look-back, and the key
     // registers are free while the look-back runs.  The offsets are read first: their rows share
@@ -418,124 +533,17 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     U* s_keys = reinterpret_cast<U*>(s_tile);
 #pragma unroll
     for (int k = 0; k < ITEMS; ++k) s_keys[rank[k]] = keys[k];
+    clk.mark<4>();  // keys reordered in LDS (this wave)
 
-    // Look-back.  Each step inspects LB_GROUPS * WINDOW predecessor tiles: thread
-    // d + 256 g (group g) loads, for digit d, the WINDOW entries just older than those of
-    // group g - 1, all loads of a step issued together (one memory latency per step).  Each group sums
-    // back to the nearest INCLUSIVE entry of its window; group 0 chains the group sums, newest window
-    // first, until some window holds an INCLUSIVE entry (or tile 0).  Fewer, wider steps matter
-    // because the walk usually crosses tens of PARTIAL tiles and every step costs one cross-XCD round
-    // trip.  Steps are workgroup-synchronous.  A group waits only for the unpublished entries of its own
-    // window up to its own nearest INCLUSIVE entry (possibly more than the walk needs, never less;
-    // older tiles publish without waiting on this one).  An entry that stays unpublished for
-    // `spin_limit` polls is counted here from its tile's keys (a predecessor tile is always full: only
-    // the last tile is partial) and published as PARTIAL by compare-and-swap.
-    // The group sums and the done flag travel through s_lb.
+    // Look-back: the four waves that hold one digit per lane walk independently (lookback_digit); the
+    // other waves go straight to the barrier below.
     uint32_t excl = 0;
-    if (tile > 0) {
-        const uint32_t grp = tid / kDigits;
-        const uint32_t ld = tid % kDigits;  // look-back digit of this thread
-        bool done = false;                  // same value in every group (group 0 decides)
-        int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
-        uint32_t* const column = lookback + ld;
-        while (true) {
-            const int64_t gtop = top - static_cast<int64_t>(grp) * WINDOW;  // this group's newest
-            uint32_t v[WINDOW];
-#pragma unroll
-            for (int w = 0; w < WINDOW; ++w) {
-                const int64_t j = gtop - w;
-                v[w] = (!done && j >= 0) ? atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]) : 0u;
-            }
-            uint32_t spins = 0;
-            while (true) {
-                // First entry of the window, up to its nearest INCLUSIVE one (and not past tile 0), that is
-                // still unpublished.
-                int first_invalid = -1;
-                bool scanning = !done;
-#pragma unroll
-                for (int w = 0; w < WINDOW; ++w) {
-                    const bool live = scanning && gtop - w >= 0;
-                    if (live && (v[w] & ~kCountMask) == 0) first_invalid = w;
-                    scanning = live && (v[w] & ~kCountMask) != 0 && (v[w] & kFlagInclusive) == 0;
-                }
-                if (!__syncthreads_or(first_invalid >= 0)) break;
-                if (spins >= spin_limit) {
-                    // Fallback: count the newest tile that some thread is still waiting for.
-                    if (tid == 0) s_fallback_tile = 0;
-                    __syncthreads();
-                    if (first_invalid >= 0) atomicMax(&s_fallback_tile, static_cast<uint32_t>(gtop - first_invalid) + 1u);
-                    __syncthreads();
-                    const uint32_t jf = s_fallback_tile - 1u;
-                    tile_digit_counts<K, DESC, BLOCK, ITEMS>(keys_in, jf, shift, mask, s_fallback);
-                    const int wf = static_cast<int>(gtop - static_cast<int64_t>(jf));
-                    if (!done) {
-#pragma unroll
-                        for (int w = 0; w < WINDOW; ++w) {
-                            if (w == wf && (v[w] & ~kCountMask) == 0) {
-                                uint32_t expected = 0;
-                                const uint32_t desired = kFlagPartial | s_fallback[ld];
-                                v[w] = __hip_atomic_compare_exchange_strong(
-                                           &column[static_cast<uint64_t>(jf) * kDigits], &expected, desired,
-                                           __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                           ? desired
-                                           : expected;
-                            }
-                        }
-                    }
-                    continue;
-                }
-                __builtin_amdgcn_s_sleep(1);
-                ++spins;
-                if (!done) {
-#pragma unroll
-                    for (int w = 0; w < WINDOW; ++w) {
-                        const int64_t j = gtop - w;
-                        if (j >= 0 && (v[w] & ~kCountMask) == 0)
-                            v[w] = atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]);
-                    }
-                }
-            }
-            // Sum of the window down to (and including) its nearest INCLUSIVE entry or tile 0.
-            uint32_t window_sum = 0;
-            bool window_stops = false;
-            if (!done) {
-#pragma unroll
-                for (int w = 0; w < WINDOW; ++w) {
-                    if (!window_stops && gtop - w >= 0) {
-                        window_sum += v[w] & kCountMask;
-                        // Tile 0's counts start at the portion base, so the walk always ends there.
-                        if ((v[w] & kFlagInclusive) || gtop - w == 0) window_stops = true;
-                    }
-                }
-            }
-            if constexpr (LB_GROUPS > 1) {
-                if (grp > 0) s_lb[grp - 1][ld] = window_sum | (window_stops ? 0x80000000u : 0u);
-                __syncthreads();
-                if (grp == 0 && !done) {
-#pragma unroll
-                    for (int g = 1; g < LB_GROUPS; ++g) {
-                        if (window_stops) break;
-                        const uint32_t x = s_lb[g - 1][ld];
-                        window_sum += x & 0x7FFFFFFFu;
-                        window_stops = (x >> 31) != 0;
-                    }
-                }
-            }
-            // (Upgrading the crossed PARTIAL entries to INCLUSIVE was measured slower: the extra
-            // agent-scope stores cost more than the shorter walks they buy.)
-            if (grp == 0 && !done) {
-                excl += window_sum;
-                done = window_stops;
-                if constexpr (LB_GROUPS > 1) s_lb[LB_GROUPS - 1][ld] = done ? 1u : 0u;
-            }
-            const bool more = __syncthreads_or(grp == 0 && !done);
-            if constexpr (LB_GROUPS > 1) {
-                if (grp > 0) done = s_lb[LB_GROUPS - 1][ld] != 0;
-            }
-            if (!more) break;
-            top -= static_cast<int64_t>(LB_GROUPS) * WINDOW;
-        }
-        if (tid < kDigits) atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
+    if (tile > 0 && tid < kDigits) {
+        excl = lookback_digit<K, DESC, BLOCK, ITEMS, WINDOW>(lookback, tile, d, keys_in, shift, mask, spin_limit,
+                                                             &s_global_minus_local[wave * kWave], trace_steps,
+                                                             trace_spins, trace_fallbacks);
+        clk.mark<5>();  // look-back walked (wave 0)
+        atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
     }
     if (tid < kDigits) {
         const uint32_t base = digit_offsets[d];
@@ -544,6 +552,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         s_global_minus_local[d] = base + excl - local_start;
     }
     __syncthreads();
+    clk.mark<6>();  // global offsets known
 
     U* ukeys_out = reinterpret_cast<U*>(keys_out);
     uint32_t gpos[VB ? ITEMS : 1];
@@ -572,6 +581,13 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
             if (i < valid && gpos[j] < out_items) uvals_out[gpos[j]] = s_vals[i];
         }
     }
+#ifdef LCPP_HIP_PHASE_TRACE
+    clk.mark<7>();  // scatter stores issued (this wave)
+    if (tid == 0)
+        clk.write(g_trace_buffer, g_trace_records, static_cast<uint64_t>(shift / 8) * gridDim.x + tile,
+                  trace_steps | (static_cast<uint64_t>(trace_spins) << 16) |
+                      (static_cast<uint64_t>(trace_fallbacks) << 32));
+#endif
 }
 
 // --------------------------------------------------------------------------------------------
@@ -594,9 +610,9 @@ struct Geometry {
 // fit 64 VGPRs.  The window is the widest that compiles without register spills (4 tiles with
 // values at 1024 threads, 8 otherwise; a spilling window runs several times slower).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 16, 8};
-    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 4 : 8};
-    return Geometry{512, 16, 8};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 16, 32};
+    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 16 : 32};
+    return Geometry{512, 16, 32};
 }
 
 template <typename K, int VB>
@@ -604,16 +620,19 @@ constexpr Geometry geometry() {
     return geometry_for(sizeof(K), VB);
 }
 
-uint32_t g_portion_limit = 0;  // 0: default
-int g_rank_mode = kRankLdsMatch;
+// Test hooks (any setting gives the same results): the largest portion a launch ranks (0: the
+// default) and the in-wave ranking variant.  Each sort reads them once, so a concurrent change on
+// another thread applies from the next call.
+std::atomic<uint32_t> g_portion_limit{0};
+std::atomic<int> g_rank_mode{kRankLdsMatch};
 
 // Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
 // portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
 // never larger than the reference's and the layout always fits a reference-sized temp buffer.
-uint32_t portion_size(uint32_t tile, bool compact) {
+uint32_t portion_size(uint32_t tile, bool compact, uint32_t limit) {
     const uint32_t def = compact ? ((1u << 28) - 1u) / tile * tile : ((1u << 30) - 1u) / tile * tile;
-    if (g_portion_limit == 0) return def;
-    uint32_t p = g_portion_limit / tile * tile;
+    if (limit == 0) return def;
+    uint32_t p = limit / tile * tile;
     if (p < tile) p = tile;
     return std::min(p, def);
 }
@@ -622,13 +641,15 @@ struct Layout {
     uint32_t passes, portions, portion, tiles_max;
     size_t bins_off, lookback_off, keys_tmp_off, values_tmp_off, total;
     size_t clear_bytes;  // bins, zeroed per call
+    int rank_mode = kRankLdsMatch;  // test hooks as read at the start of the call
+    uint32_t spin_limit = 64;
 };
 
 Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit, uint32_t end_bit,
-                   uint32_t tile, bool need_tmp, bool compact) {
+                   uint32_t tile, bool need_tmp, bool compact, uint32_t portion_limit) {
     Layout L{};
     L.passes = (end_bit - begin_bit + 7) / 8;
-    L.portion = portion_size(tile, compact);
+    L.portion = portion_size(tile, compact, portion_limit);
     L.portions = static_cast<uint32_t>(ceil_div(n, L.portion));
     L.tiles_max = static_cast<uint32_t>(ceil_div(std::min(n, L.portion), tile));
     size_t off = 0;
@@ -732,12 +753,12 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
-            if (g_rank_mode == kRankBallot)
+            if (L.rank_mode == kRankBallot)
                 onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankBallot><<<tiles, G.block, 0, stream>>>(
-                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
+                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit);
             else
                 onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankLdsMatch><<<tiles, G.block, 0, stream>>>(
-                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, g_lookback_spin_limit);
+                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit);
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
@@ -772,8 +793,11 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
                                         stream), "value copy");
     }
     constexpr Geometry G = geometry<K, VB>();
-    Layout L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, false);
-    if (temp_bytes < L.total) L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, true);
+    const uint32_t portion_limit = g_portion_limit.load(std::memory_order_relaxed);
+    Layout L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, false, portion_limit);
+    if (temp_bytes < L.total) L = make_layout(n, sizeof(K), VB, begin_bit, end_bit, G.tile(), !db, true, portion_limit);
+    L.rank_mode = g_rank_mode.load(std::memory_order_relaxed);
+    L.spin_limit = lookback_spin_limit();
     if (!temp || temp_bytes < L.total)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, L.total);
     if (reinterpret_cast<uintptr_t>(temp) % 4 != 0) return set_error(kInvalidArgument, "%s: temp not 4-byte aligned", what);
@@ -800,10 +824,21 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
 using namespace lcpp_hip;
 using namespace lcpp_hip::radix;
 
+#ifdef LCPP_HIP_PHASE_TRACE
+namespace lcpp_hip {
+int radix_trace_set_buffer(void* buffer, uint64_t records) {
+    uint64_t* p = static_cast<uint64_t*>(buffer);
+    int st = check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_buffer), &p, sizeof(p)), "trace buffer");
+    if (st != kOk) return st;
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_records), &records, sizeof(records)), "trace records");
+}
+}  // namespace lcpp_hip
+#endif
+
 extern "C" {
 
 int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion) {
-    g_portion_limit = max_items_per_portion;
+    g_portion_limit.store(max_items_per_portion, std::memory_order_relaxed);
     return kOk;
 }
 
@@ -811,7 +846,7 @@ int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion) {
 // (default).  Both give the same stable ranks; the switch exists for tests and measurements.
 int lcpp_hip_internal_radix_rank_mode(int mode) {
     if (mode != kRankBallot && mode != kRankLdsMatch) return set_error(kInvalidArgument, "rank mode must be 0 or 1");
-    g_rank_mode = mode;
+    g_rank_mode.store(mode, std::memory_order_relaxed);
     return kOk;
 }
 
@@ -827,7 +862,7 @@ size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t
                                             uint32_t end_bit, int double_buffer) {
     if (n == 0 || begin_bit >= end_bit) return 0;
     return make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, geometry_for(key_bytes, value_bytes).tile(), !double_buffer,
-                       true)
+                       true, g_portion_limit.load(std::memory_order_relaxed))
         .total;
 }
 
@@ -836,8 +871,10 @@ uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t v
                                           uint32_t end_bit, int double_buffer, size_t temp_bytes) {
     if (n == 0 || begin_bit >= end_bit) return 0;
     const uint32_t tile = geometry_for(key_bytes, value_bytes).tile();
-    Layout L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, false);
-    if (temp_bytes < L.total) L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, true);
+    const uint32_t portion_limit = g_portion_limit.load(std::memory_order_relaxed);
+    Layout L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, false, portion_limit);
+    if (temp_bytes < L.total)
+        L = make_layout(n, key_bytes, value_bytes, begin_bit, end_bit, tile, !double_buffer, true, portion_limit);
     return temp_bytes < L.total ? 0 : L.portions;
 }
 

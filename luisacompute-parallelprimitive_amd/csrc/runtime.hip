@@ -95,7 +95,7 @@ LaunchScope::~LaunchScope() {
     }
 }
 
-uint32_t g_lookback_spin_limit = 64;
+std::atomic<uint32_t> g_lookback_spin_limit{64};
 
 int device_cu_count() {
     static int cached[64] = {0};
@@ -120,11 +120,21 @@ const char* lcpp_hip_last_error(void) { return g_last_error; }
 const char* lcpp_hip_version(void) { return "lcpp-hip 0.1.0 (gfx950)"; }
 
 int lcpp_hip_set_lookback_spin_limit(uint32_t polls) {
-    g_lookback_spin_limit = polls;
+    g_lookback_spin_limit.store(polls, std::memory_order_relaxed);
     return kOk;
 }
 
-uint32_t lcpp_hip_get_lookback_spin_limit(void) { return g_lookback_spin_limit; }
+uint32_t lcpp_hip_get_lookback_spin_limit(void) { return lookback_spin_limit(); }
+
+#ifdef LCPP_HIP_PHASE_TRACE
+// Diagnostic build only: per-tile phase records of the onesweep and scan kernels go to `buffer`
+// (device memory, `records` records of kTraceWords 64-bit words; null to stop).
+int lcpp_hip_trace_set_buffer(void* buffer, uint64_t records) {
+    int st = radix_trace_set_buffer(buffer, records);
+    if (st != kOk) return st;
+    return scan_trace_set_buffer(buffer, records);
+}
+#endif
 
 int lcpp_hip_profile_enable(int enable) {
     ProfileState& p = profile();

@@ -7,9 +7,9 @@
 //
 // MI355X design
 //   * Tile = 256 threads x 24 rows x one 128-bit vector per thread per row (96 x 4-byte items per
-//     thread, 24,576 items, held in registers).  Row r of a tile is the contiguous range
-//     [r*1024, (r+1)*1024) and thread t holds items 4t..4t+3 of every row, so each row is one fully
-//     coalesced 4 KiB load and store.
+//     thread, 24,576 items; 48 x 8-byte items, 12,288), held in registers.  Row r of a tile is a
+//     contiguous 4 KiB range and thread t holds the t-th 16 bytes of every row, so each row is one
+//     fully coalesced 4 KiB load and store.
 //   * Tile = workgroup index.  There is no tile ticket: a same-address agent-scope atomic costs
 //     ~11 ns on MI355X and serialises, which would cap a 2^28 scan at ~0.75 ms.  Workgroups are
 //     dispatched in index order in practice, so predecessors are normally running; forward progress
@@ -24,8 +24,12 @@
 //   * Look-back: wave 0 publishes PARTIAL, then inspects 64 predecessors per step (one per lane)
 //     with agent-scope loads, sums back to the nearest INCLUSIVE predecessor with a DPP reduction,
 //     and publishes INCLUSIVE.  Status and value share one 64-bit word: flag in the low half,
-//     value bits in the high half, so one relaxed atomic load observes both consistently.
-// Algorithmic traffic: 2 * n * sizeof(T) bytes (read input, write output) + 8 bytes per tile.
+//     value bits in the high half, so one relaxed atomic load observes both consistently.  An
+//     8-byte value takes two such words (low and high 32 bits); a reader accepts a state only when
+//     both words carry the same published flag, and every publication writes word 1 before word 0
+//     (word 0 with release ordering where a helper and the owner could both write word 1), so the
+//     flag pair identifies one publication.
+// Algorithmic traffic: 2 * n * sizeof(T) bytes (read input, write output) + 8 * sizeof(T) / 4 bytes per tile.
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
 
@@ -38,25 +42,81 @@ namespace {
 constexpr int kScanBlock = 256;
 constexpr int kScanRows = 24;
 constexpr int kScanWaves = kScanBlock / kWave;
-constexpr uint32_t kScanTile = kScanBlock * kScanRows * 4;  // 24,576 items of 4 bytes
+template <typename T>
+constexpr int kVec = 16 / static_cast<int>(sizeof(T));  // items per thread per row
+template <typename T>
+constexpr uint32_t kScanTile = kScanBlock * kScanRows * kVec<T>;  // 24,576 4-byte or 12,288 8-byte items
+template <typename T>
+constexpr int kStateWords = static_cast<int>(sizeof(T)) / 4;  // 64-bit status words per tile
+// Three workgroups per CU (at most 168 VGPRs): one workgroup's look-back wait is covered by the others'
+// loads and stores.  (Measured at 2^28 u32: 0.388 ms, against 0.395 ms at two per CU with row bases
+// kept in registers, and 0.405 ms with 16-row tiles at four per CU.)
+constexpr int kScanBlocksPerCu = 3;
 
 constexpr uint32_t kFlagInvalid = 0;
 constexpr uint32_t kFlagPartial = 1;
 constexpr uint32_t kFlagInclusive = 2;
 constexpr uint32_t kFlagClaimed = 3;  // a look-back is computing this tile's aggregate
 
-// Temp layout: one 8-byte status word per tile.
-size_t scan_needed_bytes(uint64_t n) { return ceil_div(n, kScanTile) * 8; }
+#ifdef LCPP_HIP_PHASE_TRACE
+// Phase-trace buffer of the diagnostic build: one record per tile.
+__device__ uint64_t* g_trace_buffer = nullptr;
+__device__ uint64_t g_trace_records = 0;
+#endif
 
-
-template <typename T>
-__device__ __forceinline__ uint64_t pack_status(uint32_t flag, T value) {
-    return (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, value)) << 32) | flag;
+// Temp layout: sizeof(T) / 4 status words of 8 bytes per tile.
+size_t scan_needed_bytes(uint64_t n, size_t elem_bytes) {
+    const uint64_t tile = static_cast<uint64_t>(kScanBlock) * kScanRows * (16 / elem_bytes);
+    return ceil_div(n, tile) * 8 * (elem_bytes / 4);
 }
 
-// PARTIAL or INCLUSIVE: the word carries a usable value.
-__device__ __forceinline__ bool status_published(uint64_t st) {
-    return static_cast<uint32_t>(st) - kFlagPartial < 2u;
+// Status word w of a tile: flag in the low half, bits 32w..32w+31 of the value in the high half.
+template <typename T>
+__device__ __forceinline__ uint64_t pack_word(uint32_t flag, T value, int w) {
+    uint64_t bits;
+    if constexpr (sizeof(T) == 4) bits = __builtin_bit_cast(uint32_t, value);
+    else bits = __builtin_bit_cast(uint64_t, value) >> (32 * w);
+    return (static_cast<uint64_t>(static_cast<uint32_t>(bits)) << 32) | flag;
+}
+
+template <typename T>
+struct TileState {
+    uint32_t flag;  // kFlagInvalid also stands for "words of two different publications"
+    T value;
+};
+
+// PARTIAL or INCLUSIVE: the state carries a usable value.
+__device__ __forceinline__ bool flag_published(uint32_t flag) { return flag - kFlagPartial < 2u; }
+
+template <typename T>
+__device__ __forceinline__ TileState<T> load_state(uint64_t* states, uint64_t tile) {
+    if constexpr (sizeof(T) == 4) {
+        const uint64_t w = atomic_load_agent(&states[tile]);
+        return {static_cast<uint32_t>(w), __builtin_bit_cast(T, static_cast<uint32_t>(w >> 32))};
+    } else {
+        const uint64_t w0 = atomic_load_agent(&states[2 * tile]);
+        const uint64_t w1 = atomic_load_agent(&states[2 * tile + 1]);
+        const uint32_t f0 = static_cast<uint32_t>(w0), f1 = static_cast<uint32_t>(w1);
+        // CLAIMED lives in word 0 only; any other mismatch is a publication in progress.
+        const uint32_t flag = f0 == f1 ? f0 : (f0 == kFlagClaimed ? kFlagClaimed : kFlagInvalid);
+        return {flag, __builtin_bit_cast(T, (w0 >> 32) | (w1 & 0xFFFFFFFF00000000ull))};
+    }
+}
+
+// Publishes (flag, value) for `tile`: word 1 first, then word 0 (release when `release`, so that a
+// reader of word 0 with acquire ordering also observes word 1).
+template <typename T>
+__device__ __forceinline__ void store_state(uint64_t* states, uint64_t tile, uint32_t flag, T value, bool release) {
+    if constexpr (sizeof(T) == 4) {
+        (void)release;
+        atomic_store_agent(&states[tile], pack_word(flag, value, 0));
+    } else {
+        atomic_store_agent(&states[2 * tile + 1], pack_word(flag, value, 1));
+        if (release)
+            __hip_atomic_store(&states[2 * tile], pack_word(flag, value, 0), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            atomic_store_agent(&states[2 * tile], pack_word(flag, value, 0));
+    }
 }
 
 // Item `idx` of the input, or 0 past the end.
@@ -70,27 +130,25 @@ __device__ __forceinline__ T load_item(const T* in, uint64_t n, uint64_t idx) {
 // rows summed in row order.
 template <typename T>
 __device__ T tile_aggregate(const T* in, uint64_t n, uint32_t tile, int vector_io) {
-    using Vec = T __attribute__((ext_vector_type(4)));
+    constexpr int V = kVec<T>;
+    using Vec = T __attribute__((ext_vector_type(V)));
     const uint32_t lane = lane_id();
-    const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile;
+    const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile<T>;
     T running = T(0);
     for (int r = 0; r < kScanRows; ++r) {
         T row_total = T(0);
         for (int w = 0; w < kScanWaves; ++w) {
-            const uint64_t first = tile_base + (static_cast<uint64_t>(r) * kScanBlock + w * kWave + lane) * 4;
+            const uint64_t first = tile_base + (static_cast<uint64_t>(r) * kScanBlock + w * kWave + lane) * V;
             Vec v;
-            if (vector_io && tile_base + kScanTile <= n) {
+            if (vector_io && tile_base + kScanTile<T> <= n) {
                 v = *reinterpret_cast<const Vec*>(in + first);
             } else {
-                v[0] = load_item(in, n, first);
-                v[1] = load_item(in, n, first + 1);
-                v[2] = load_item(in, n, first + 2);
-                v[3] = load_item(in, n, first + 3);
+#pragma unroll
+                for (int j = 0; j < V; ++j) v[j] = load_item(in, n, first + j);
             }
-            v[1] += v[0];
-            v[2] += v[1];
-            v[3] += v[2];
-            row_total += wave_read_lane(wave_inclusive_scan(v[3], SumOp{}), kWave - 1);
+#pragma unroll
+            for (int j = 1; j < V; ++j) v[j] += v[j - 1];
+            row_total += wave_read_lane(wave_inclusive_scan(v[V - 1], SumOp{}), kWave - 1);
         }
         running += row_total;
     }
@@ -100,46 +158,51 @@ __device__ T tile_aggregate(const T* in, uint64_t n, uint32_t tile, int vector_i
 // Exclusive prefix of tile `tile` (> 0) over all earlier tiles; called by all 64 lanes of one wave.
 template <typename T>
 __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_t n, int vector_io,
-                           uint32_t spin_limit) {
+                           uint32_t spin_limit, uint64_t& trace_counters) {
     const uint32_t lane = lane_id();
     T prefix = T(0);
     int64_t end = tile;  // exclusive end of the window of predecessors
     while (true) {
         const int64_t idx = end - kWave + static_cast<int64_t>(lane);
-        uint64_t st = idx >= 0 ? atomic_load_agent(&states[idx]) : pack_status(kFlagInclusive, T(0));
+        TileState<T> st = idx >= 0 ? load_state<T>(states, static_cast<uint64_t>(idx)) : TileState<T>{kFlagInclusive, T(0)};
         uint32_t spins = 0;
-        while (wave_ballot(!status_published(st)) != 0) {
+        while (wave_ballot(!flag_published(st.flag)) != 0) {
             if (spins >= spin_limit) {
                 // Fallback: claim every still-INVALID predecessor and compute its aggregate here.
                 // Predecessors CLAIMED by another look-back are simply polled until published.
-                uint64_t invalid = wave_ballot(static_cast<uint32_t>(st) == kFlagInvalid);
+                uint64_t invalid = wave_ballot(st.flag == kFlagInvalid);
                 while (invalid != 0) {
                     const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(invalid));
                     invalid &= invalid - 1;
                     const uint32_t j = static_cast<uint32_t>(end - kWave + src);
                     bool won = false;
                     if (lane == src) {
-                        uint64_t expected = 0;  // INVALID with value 0, as the clear leaves it
-                        won = __hip_atomic_compare_exchange_strong(&states[j], &expected, uint64_t(kFlagClaimed),
-                                                                   __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                                   __HIP_MEMORY_SCOPE_AGENT);
-                        st = won ? uint64_t(kFlagClaimed) : expected;
+                        // Word 0 INVALID with value 0, as the clear leaves it.  (A tile whose words are
+                        // mid-publication fails the exchange and is polled again.)
+                        uint64_t expected = 0;
+                        won = __hip_atomic_compare_exchange_strong(&states[static_cast<uint64_t>(j) * kStateWords<T>],
+                                                                   &expected, uint64_t(kFlagClaimed), __ATOMIC_RELAXED,
+                                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (won) st.flag = kFlagClaimed;
                     }
                     if (wave_ballot(won) != 0) {
+                        if constexpr (kPhaseTrace) trace_counters += 1ull << 32;
                         const T agg = tile_aggregate(in, n, j, vector_io);
                         if (lane == src) {
-                            st = pack_status(kFlagPartial, agg);
-                            atomic_store_agent(&states[j], st);
+                            st = TileState<T>{kFlagPartial, agg};
+                            store_state(states, j, kFlagPartial, agg, true);
                         }
                     }
                 }
             }
             __builtin_amdgcn_s_sleep(1);
             ++spins;
-            if (!status_published(st)) st = atomic_load_agent(&states[idx]);
+            if constexpr (kPhaseTrace) trace_counters += 1ull << 16;
+            if (!flag_published(st.flag)) st = load_state<T>(states, static_cast<uint64_t>(idx));
         }
-        const T value = __builtin_bit_cast(T, static_cast<uint32_t>(st >> 32));
-        const uint64_t inclusive = wave_ballot(static_cast<uint32_t>(st) == kFlagInclusive);
+        if constexpr (kPhaseTrace) trace_counters += 1;
+        const T value = st.value;
+        const uint64_t inclusive = wave_ballot(st.flag == kFlagInclusive);
         if (inclusive != 0) {
             const uint32_t last = 63 - __builtin_clzll(inclusive);
             prefix += wave_reduce(lane >= last ? value : T(0), SumOp{});
@@ -151,10 +214,12 @@ __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_
 }
 
 template <typename T, bool INCLUSIVE>
-__global__ __launch_bounds__(kScanBlock, 2) void scan_sum_kernel(const T* in, T* out,
-                                                              uint64_t n, uint64_t* __restrict__ states, T init,
-                                                              int vector_io, uint32_t spin_limit) {
-    using Vec = T __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(const T* in, T* out, uint64_t n,
+                                                                             uint64_t* __restrict__ states, T init,
+                                                                             int vector_io, uint32_t spin_limit) {
+    constexpr int V = kVec<T>;
+    constexpr uint32_t TILE = kScanTile<T>;
+    using Vec = T __attribute__((ext_vector_type(V)));
     __shared__ T s_wave_totals[kScanRows][kScanWaves];
     __shared__ T s_tile_prefix;
 
@@ -162,8 +227,11 @@ __global__ __launch_bounds__(kScanBlock, 2) void scan_sum_kernel(const T* in, T*
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t tile = blockIdx.x;
-    const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile;
-    const bool full = vector_io && tile_base + kScanTile <= n;
+    const uint64_t tile_base = static_cast<uint64_t>(tile) * TILE;
+    const bool full = vector_io && tile_base + TILE <= n;
+    PhaseClock clk;
+    clk.start();
+    uint64_t trace_counters = 0;  // look-back steps | spins << 16 | fallback tiles << 32
 
     Vec v[kScanRows];
     if (full) {
@@ -174,92 +242,94 @@ __global__ __launch_bounds__(kScanBlock, 2) void scan_sum_kernel(const T* in, T*
 #pragma unroll
         for (int r = 0; r < kScanRows; ++r) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint64_t idx = tile_base + (static_cast<uint64_t>(r) * kScanBlock + tid) * 4 + j;
+            for (int j = 0; j < V; ++j) {
+                const uint64_t idx = tile_base + (static_cast<uint64_t>(r) * kScanBlock + tid) * V + j;
                 v[r][j] = idx < n ? in[idx] : T(0);
             }
         }
     }
 
-    // Thread-local inclusive scans and per-row wave scans.
+    // Thread-local inclusive scans and per-row wave scans; the wave totals go to LDS.  Only
+    // v[r][0..V-2] and the wave scan stay live: the thread's row total is the wave scan minus its
+    // shifted copy, and row offsets are re-read from LDS when the outputs are formed, so the kernel
+    // fits 128 VGPRs (four workgroups per CU).
     T wave_incl[kScanRows];
 #pragma unroll
     for (int r = 0; r < kScanRows; ++r) {
-        v[r][1] += v[r][0];
-        v[r][2] += v[r][1];
-        v[r][3] += v[r][2];
-        wave_incl[r] = wave_inclusive_scan(v[r][3], SumOp{});
-    }
-    if (lane == kWave - 1) {
 #pragma unroll
-        for (int r = 0; r < kScanRows; ++r) s_wave_totals[r][wave] = wave_incl[r];
+        for (int j = 1; j < V; ++j) v[r][j] += v[r][j - 1];
+        wave_incl[r] = wave_inclusive_scan(v[r][V - 1], SumOp{});
+        if (lane == kWave - 1) s_wave_totals[r][wave] = wave_incl[r];
     }
     __syncthreads();
 
-    // Exclusive in-tile offset of (row r, this wave) and the tile aggregate.
-    T row_base[kScanRows];
-    T running = T(0);
+    // Tile aggregate: rows in order, each row's wave totals in wave order (the order tile_aggregate
+    // repeats for a helper).
+    T aggregate = T(0);
 #pragma unroll
     for (int r = 0; r < kScanRows; ++r) {
-        T before = T(0);
         T row_total = T(0);
+#pragma unroll
+        for (int w = 0; w < kScanWaves; ++w) row_total += s_wave_totals[r][w];
+        aggregate += row_total;
+    }
+    clk.mark<1>(true);  // tile loaded and scanned in registers
+
+    // Publish (tile 0: INCLUSIVE at once; others PARTIAL, then INCLUSIVE after the look-back).  The
+    // publication ends with a compare-and-swap of word 0 from INVALID: if a look-back has CLAIMED
+    // this tile, the owner waits for the claimer's PARTIAL (the claimer has finished reading this
+    // tile's input) before the barrier that precedes every output store.
+    if (wave == 0) {
+        bool claimed_by_other = false;
+        if (lane == 0) {
+            const uint32_t flag = tile == 0 ? kFlagInclusive : kFlagPartial;
+            if constexpr (kStateWords<T> == 2) atomic_store_agent(&states[2 * tile + 1], pack_word(flag, aggregate, 1));
+            uint64_t expected = 0;
+            claimed_by_other = !__hip_atomic_compare_exchange_strong(
+                &states[static_cast<uint64_t>(tile) * kStateWords<T>], &expected, pack_word(flag, aggregate, 0),
+                __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const T excl =
+            tile == 0 ? T(0) : scan_lookback<T>(states, tile, in, n, vector_io, spin_limit, trace_counters);
+        clk.mark<2>();  // look-back walked
+        if (lane == 0) {
+            if (claimed_by_other) {
+                // The claimer's word 0 is stored with release ordering after its word 1.
+                while (static_cast<uint32_t>(__hip_atomic_load(&states[static_cast<uint64_t>(tile) * kStateWords<T>],
+                                                               __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)) !=
+                       kFlagPartial)
+                    __builtin_amdgcn_s_sleep(1);
+            }
+            if (tile != 0 || claimed_by_other) store_state(states, tile, kFlagInclusive, T(excl + aggregate), false);
+            s_tile_prefix = excl;
+        }
+    }
+    __syncthreads();
+
+    T running = init + s_tile_prefix;  // tile prefix + rows before r
+#pragma unroll
+    for (int r = 0; r < kScanRows; ++r) {
+        T before = T(0), row_total = T(0);
 #pragma unroll
         for (int w = 0; w < kScanWaves; ++w) {
             const T x = s_wave_totals[r][w];
             if (w < static_cast<int>(wave)) before += x;
             row_total += x;
         }
-        row_base[r] = running + before;
-        running += row_total;
-    }
-    const T aggregate = running;
-
-    // Publish (tile 0: INCLUSIVE at once; others PARTIAL, then INCLUSIVE after the look-back).  The
-    // publication is a compare-and-swap from INVALID: if a look-back has CLAIMED this tile, the owner
-    // waits for the claimer's PARTIAL (the claimer has finished reading this tile's input) before the
-    // barrier that precedes every output store.
-    if (wave == 0) {
-        bool claimed_by_other = false;
-        if (lane == 0) {
-            uint64_t expected = 0;
-            claimed_by_other = !__hip_atomic_compare_exchange_strong(
-                &states[tile], &expected, pack_status(tile == 0 ? kFlagInclusive : kFlagPartial, aggregate),
-                __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        const T excl = tile == 0 ? T(0) : scan_lookback<T>(states, tile, in, n, vector_io, spin_limit);
-        if (lane == 0) {
-            if (claimed_by_other) {
-                while (static_cast<uint32_t>(atomic_load_agent(&states[tile])) != kFlagPartial)
-                    __builtin_amdgcn_s_sleep(1);
-            }
-            if (tile != 0 || claimed_by_other)
-                atomic_store_agent(&states[tile], pack_status(kFlagInclusive, excl + aggregate));
-            s_tile_prefix = excl;
-        }
-    }
-    __syncthreads();
-    const T tile_prefix = s_tile_prefix;
-
-    const T base_all = init + tile_prefix;
-#pragma unroll
-    for (int r = 0; r < kScanRows; ++r) {
         const T thread_excl = wave_shift_exclusive<T, SumOp>(wave_incl[r]);
-        const T p = base_all + row_base[r] + thread_excl;
+        const T p = running + before + thread_excl;
         Vec o;
         if constexpr (INCLUSIVE) {
-            // The last item's inclusive value comes from the wave scan, so v[r][3] need not stay live
-            // (keeps the kernel within 256 VGPRs, two workgroups per CU).
-            o[0] = p + v[r][0];
-            o[1] = p + v[r][1];
-            o[2] = p + v[r][2];
-            o[3] = base_all + row_base[r] + wave_incl[r];
+#pragma unroll
+            for (int j = 0; j < V - 1; ++j) o[j] = p + v[r][j];
+            o[V - 1] = running + before + wave_incl[r];
         } else {
             o[0] = p;
-            o[1] = p + v[r][0];
-            o[2] = p + v[r][1];
-            o[3] = p + v[r][2];
+#pragma unroll
+            for (int j = 1; j < V; ++j) o[j] = p + v[r][j - 1];
         }
         v[r] = o;
+        running += row_total;
     }
     if (full) {
         Vec* dst = reinterpret_cast<Vec*>(out + tile_base);
@@ -269,18 +339,22 @@ __global__ __launch_bounds__(kScanBlock, 2) void scan_sum_kernel(const T* in, T*
 #pragma unroll
         for (int r = 0; r < kScanRows; ++r) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint64_t idx = tile_base + (static_cast<uint64_t>(r) * kScanBlock + tid) * 4 + j;
+            for (int j = 0; j < V; ++j) {
+                const uint64_t idx = tile_base + (static_cast<uint64_t>(r) * kScanBlock + tid) * V + j;
                 if (idx < n) out[idx] = v[r][j];
             }
         }
     }
+#ifdef LCPP_HIP_PHASE_TRACE
+    clk.mark<3>();  // outputs issued (this wave)
+    if (tid == 0) clk.write(g_trace_buffer, g_trace_records, tile, trace_counters);
+#endif
 }
 
 template <typename T>
 int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, T init,
              void* stream_ptr) {
-    static_assert(sizeof(T) == 4, "packed tile status holds 4-byte values");
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- and 8-byte items");
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceScan: too many items (%llu > UINT_MAX)",
                                             static_cast<unsigned long long>(n));
@@ -288,36 +362,49 @@ int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, boo
     if (!in || !out) return set_error(kInvalidArgument, "DeviceScan: null input or output");
     if (reinterpret_cast<uintptr_t>(in) % sizeof(T) != 0 || reinterpret_cast<uintptr_t>(out) % sizeof(T) != 0)
         return set_error(kInvalidArgument, "DeviceScan: input/output not aligned to the element size");
-    const size_t needed = scan_needed_bytes(n);
+    const size_t needed = scan_needed_bytes(n, sizeof(T));
     if (!temp || temp_bytes < needed)
         return set_error(kTempTooSmall, "DeviceScan: temp storage too small (%zu < %zu bytes)", temp_bytes, needed);
     if (reinterpret_cast<uintptr_t>(temp) % 8 != 0)
         return set_error(kInvalidArgument, "DeviceScan: temp storage must be 8-byte aligned");
 
-    const uint64_t tiles = ceil_div(n, kScanTile);
+    const uint64_t tiles = ceil_div(n, kScanTile<T>);
     uint64_t* states = static_cast<uint64_t*>(temp);
     int st = launch_fill_u32(static_cast<uint32_t*>(temp), needed / 4, 0u, stream);
     if (st != kOk) return st;
 
     const int vector_io = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+    const uint32_t spin_limit = lookback_spin_limit();
     LaunchScope scope("scan_sum", stream);
     if (inclusive)
         scan_sum_kernel<T, true><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
-                                                                                         vector_io, g_lookback_spin_limit);
+                                                                                         vector_io, spin_limit);
     else
         scan_sum_kernel<T, false><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
-                                                                                          vector_io, g_lookback_spin_limit);
+                                                                                          vector_io, spin_limit);
     return check_hip(hipGetLastError(), "scan_sum launch");
 }
 
 }  // namespace
+
+#ifdef LCPP_HIP_PHASE_TRACE
+int scan_trace_set_buffer(void* buffer, uint64_t records) {
+    uint64_t* p = static_cast<uint64_t*>(buffer);
+    int st = check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_buffer), &p, sizeof(p)), "trace buffer");
+    if (st != kOk) return st;
+    return check_hip(hipMemcpyToSymbol(HIP_SYMBOL(g_trace_records), &records, sizeof(records)), "trace records");
+}
+#endif
 }  // namespace lcpp_hip
 
 using namespace lcpp_hip;
 
 extern "C" {
 
-size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n) { return n == 0 ? 0 : scan_needed_bytes(n); }
+size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n, size_t elem_bytes) {
+    if (elem_bytes != 4 && elem_bytes != 8) return 0;
+    return n == 0 ? 0 : scan_needed_bytes(n, elem_bytes);
+}
 
 // Signed sums run in the unsigned type of the same width (identical two's-complement bits).
 #define LCPP_HIP_DEFINE_SCAN(S, T, A)                                                                           \
@@ -339,6 +426,9 @@ size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n) { return n == 0 ? 0 : sca
 LCPP_HIP_DEFINE_SCAN(i32, int32_t, uint32_t)
 LCPP_HIP_DEFINE_SCAN(u32, uint32_t, uint32_t)
 LCPP_HIP_DEFINE_SCAN(f32, float, float)
+LCPP_HIP_DEFINE_SCAN(i64, int64_t, uint64_t)
+LCPP_HIP_DEFINE_SCAN(u64, uint64_t, uint64_t)
+LCPP_HIP_DEFINE_SCAN(f64, double, double)
 #undef LCPP_HIP_DEFINE_SCAN
 
 }  // extern "C"

@@ -164,8 +164,9 @@ class DeviceScan : public LuisaModule {
     template <NumericT T>
     void record(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
                 size_t num_items, bool inclusive, T init) {
-        static_assert(std::is_same_v<T, int32_t> || std::is_same_v<T, uint32_t> || std::is_same_v<T, float>,
-                      "DeviceScan sums support int, uint and float");
+        static_assert((std::is_integral_v<T> && (sizeof(T) == 4 || sizeof(T) == 8) && !std::is_same_v<T, bool>) ||
+                          std::is_same_v<T, float> || std::is_same_v<T, double>,
+                      "DeviceScan sums support 4- and 8-byte integers, float and double");
         LCPP_ASSERT(m_created, "DeviceScan::create must be called before dispatch.");
         LCPP_ASSERT(num_items <= std::numeric_limits<uint>::max(), "Too many items for DeviceScan.");
         if (num_items == 0u) return;
@@ -181,9 +182,20 @@ class DeviceScan : public LuisaModule {
         cmdlist << [=](hipStream_t s) {
             void* st = detail::stream_ptr(s);
             int rc;
-            if constexpr (std::is_same_v<T, int32_t>) rc = lcpp_hip_scan_sum_init_i32(temp, temp_bytes, in, out, num_items, inc, init, st);
-            else if constexpr (std::is_same_v<T, uint32_t>) rc = lcpp_hip_scan_sum_init_u32(temp, temp_bytes, in, out, num_items, inc, init, st);
-            else rc = lcpp_hip_scan_sum_init_f32(temp, temp_bytes, in, out, num_items, inc, init, st);
+            // Integer sums wrap, so signed and unsigned items of one width share the unsigned entry point.
+            if constexpr (std::is_same_v<T, float>) {
+                rc = lcpp_hip_scan_sum_init_f32(temp, temp_bytes, in, out, num_items, inc, init, st);
+            } else if constexpr (std::is_same_v<T, double>) {
+                rc = lcpp_hip_scan_sum_init_f64(temp, temp_bytes, in, out, num_items, inc, init, st);
+            } else if constexpr (sizeof(T) == 4) {
+                rc = lcpp_hip_scan_sum_init_u32(temp, temp_bytes, reinterpret_cast<const uint32_t*>(in),
+                                                reinterpret_cast<uint32_t*>(out), num_items, inc,
+                                                static_cast<uint32_t>(init), st);
+            } else {
+                rc = lcpp_hip_scan_sum_init_u64(temp, temp_bytes, reinterpret_cast<const uint64_t*>(in),
+                                                reinterpret_cast<uint64_t*>(out), num_items, inc,
+                                                static_cast<uint64_t>(init), st);
+            }
             luisa::detail::abi_check(rc, inc ? "DeviceScan::InclusiveSum" : "DeviceScan::ExclusiveSum");
         };
     }

@@ -28,7 +28,8 @@ ERR_UNSUPPORTED = -4
 GEN_U64, GEN_U32_HI, GEN_I32_PM1000, GEN_U32_LT16, GEN_U64_AND3, GEN_U32_IOTA, GEN_F32_PM1 = range(7)
 
 SCALAR_SUFFIXES = ("i32", "u32", "f32", "i64", "u64", "f64")
-SCAN_SUFFIXES = ("i32", "u32", "f32")
+SCAN_SUFFIXES = SCALAR_SUFFIXES
+ARG_SUFFIXES = ("i32", "u32", "f32")  # segment ArgMin / ArgMax item types
 SORT_KEY_SUFFIXES = ("u32", "i32", "f32", "u64", "i64", "f64")
 SPMV_SUFFIXES = [(v, i) for v in ("f32", "f64", "i32", "u32") for i in ("i32", "u32")]
 BY_KEY_KEY_SUFFIXES = ("i32", "u32", "i64", "u64")
@@ -88,7 +89,7 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_set_lookback_spin_limit", i32, u32)
     sig("lcpp_hip_get_lookback_spin_limit", u32)
     sig("lcpp_hip_radix_tile_items", u32, sz, sz)
-    sig("lcpp_hip_internal_scan_needed_bytes", sz, u64)
+    sig("lcpp_hip_internal_scan_needed_bytes", sz, u64, sz)
     sig("lcpp_hip_internal_radix_needed_bytes", sz, u32, sz, sz, u32, u32, i32)
     sig("lcpp_hip_internal_radix_portions", u32, u32, sz, sz, u32, u32, i32, sz)
     sig("lcpp_hip_internal_radix_rank_mode", i32, i32)
@@ -125,7 +126,7 @@ def _declare(lib: C.CDLL) -> None:
             sig(f"lcpp_hip_segment_reduce_{op}_{t}", i32, vp, sz, vp, vp, u64, vp, vp, vp)
             sig(f"lcpp_hip_segment_reduce_fixed_{op}_{t}", i32, vp, sz, vp, vp, u64, u32, vp)
         sig(f"lcpp_hip_segmented_scan_sum_{t}", i32, vp, sz, vp, vp, vp, vp, vp, u64, i32, i32, _CTYPE[t], vp)
-    for t in SCAN_SUFFIXES:
+    for t in ARG_SUFFIXES:
         for op in ("argmin", "argmax"):
             sig(f"lcpp_hip_segment_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, vp, vp, vp)
             sig(f"lcpp_hip_segment_fixed_{op}_{t}", i32, vp, sz, vp, vp, vp, u64, u32, vp)

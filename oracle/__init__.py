@@ -41,6 +41,10 @@ def lib() -> C.CDLL:
         h.oracle_scan_sum_u32.argtypes = [vp, vp, u64, i32, u32]
         h.oracle_scan_sum_f32.restype = None
         h.oracle_scan_sum_f32.argtypes = [vp, vp, vp, u64, i32, C.c_float]
+        h.oracle_scan_sum_u64.restype = None
+        h.oracle_scan_sum_u64.argtypes = [vp, vp, u64, i32, u64]
+        h.oracle_scan_sum_f64.restype = None
+        h.oracle_scan_sum_f64.argtypes = [vp, vp, vp, u64, i32, C.c_double]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -140,6 +144,24 @@ def scan_sum_f32(a: np.ndarray, inclusive: bool = False, init: float = 0.0) -> t
     out = np.empty(a.size, dtype=np.float64)
     aout = np.empty(a.size, dtype=np.float64)
     lib().oracle_scan_sum_f32(_p(a), _p(out), _p(aout), a.size, int(inclusive), init)
+    return out, aout
+
+
+def scan_sum_u64(a: np.ndarray, inclusive: bool = False, init: int = 0) -> np.ndarray:
+    """64-bit wrap-around sum scan (int64 inputs are scanned through their bits)."""
+    src = np.ascontiguousarray(a).view(np.uint64)
+    out = np.empty_like(src)
+    lib().oracle_scan_sum_u64(_p(src), _p(out), src.size, int(inclusive), init & 0xFFFFFFFFFFFFFFFF)
+    return out.view(a.dtype)
+
+
+def scan_sum_f64(a: np.ndarray, inclusive: bool = False, init: float = 0.0) -> tuple[np.ndarray, np.ndarray]:
+    """Double scan accumulated in long double: (values, running sums of |x|), both as float64 arrays
+    of the long-double results."""
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    out = np.empty(a.size, dtype=np.longdouble)
+    aout = np.empty(a.size, dtype=np.longdouble)
+    lib().oracle_scan_sum_f64(_p(a), _p(out), _p(aout), a.size, int(inclusive), init)
     return out, aout
 
 

@@ -103,6 +103,26 @@ void oracle_scan_sum_u32(const uint32_t* in, uint32_t* out, uint64_t n, int incl
         else { out[i] = run; run += x; }
     }
 }
+/* The same over 64-bit words (int64 and uint64 share the bits; sums wrap modulo 2^64). */
+void oracle_scan_sum_u64(const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, uint64_t init) {
+    uint64_t run = init;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t x = in[i];
+        if (inclusive) { run += x; out[i] = run; }
+        else { out[i] = run; run += x; }
+    }
+}
+/* Double-precision scan accumulated in long double (reference value for a tolerance check), plus
+ * running |x| sums. */
+void oracle_scan_sum_f64(const double* in, long double* out, long double* abs_out, uint64_t n, int inclusive,
+                         double init) {
+    long double run = init, arun = fabsl((long double)init);
+    for (uint64_t i = 0; i < n; ++i) {
+        const long double x = in[i];
+        if (inclusive) { run += x; arun += fabsl(x); out[i] = run; abs_out[i] = arun; }
+        else { out[i] = run; abs_out[i] = arun; run += x; arun += fabsl(x); }
+    }
+}
 /* Floating-point scan in double (reference value for a tolerance check), plus running |x| sums. */
 void oracle_scan_sum_f32(const float* in, double* out, double* abs_out, uint64_t n, int inclusive, float init) {
     double run = init, arun = fabs((double)init);

@@ -178,6 +178,43 @@ void scan_sums_of_ones() {
     }
 }
 
+// tests/device_scan_test.cpp:267-286: InclusiveSum<double> over 17 ones with reference-sized temp storage.
+void scan_double_inclusive_sum() {
+    auto& e = *g_env;
+    constexpr size_t n = 17u;
+    std::vector<double> input(n, 1.0), result(n, -1.0);
+    auto in = e.device.create_buffer<double>(n);
+    auto out = e.device.create_buffer<double>(n);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<double>(n)));
+    CommandList cmd;
+    e.scan.InclusiveSum(cmd, temp.view(), in.view(), out.view(), n);
+    e.stream << in.copy_from(luisa::span{input}) << cmd.commit() << out.copy_to(luisa::span{result}) << synchronize();
+    bool ok = true;
+    for (size_t i = 0; i < n; ++i) ok = ok && result[i] == static_cast<double>(i + 1u);
+    EXPECT(ok);
+}
+
+// 64-bit integers wrap modulo 2^64 like std::exclusive_scan over int64_t bits.
+void scan_int64_exclusive_vs_std() {
+    auto& e = *g_env;
+    const uint n = 100003u;
+    std::vector<int64_t> a(n), got(n), want(n);
+    uint64_t x = 0x9E3779B97F4A7C15ull;
+    for (uint i = 0; i < n; ++i) {
+        x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+        a[i] = static_cast<int64_t>(x);
+    }
+    uint64_t run = 0;
+    for (uint i = 0; i < n; ++i) { want[i] = static_cast<int64_t>(run); run += static_cast<uint64_t>(a[i]); }
+    auto in = e.device.create_buffer<int64_t>(n);
+    auto out = e.device.create_buffer<int64_t>(n);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<int64_t>(n)));
+    CommandList cmd;
+    e.scan.ExclusiveSum(cmd, temp.view(), in.view(), out.view(), n);
+    e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(luisa::span{got}) << synchronize();
+    EXPECT(got == want);
+}
+
 void scan_inclusive_init_in_place() {
     auto& e = *g_env;
     std::array<int, 4> input{1, 2, 3, 4};
@@ -1205,6 +1242,8 @@ const std::vector<Case>& cases() {
         {"reduce_bench_pattern_int_and_float", reduce_bench_pattern_int_and_float},
         {"scan_sums_of_ones", scan_sums_of_ones},
         {"scan_inclusive_init_in_place", scan_inclusive_init_in_place},
+        {"scan_double_inclusive_sum", scan_double_inclusive_sum},
+        {"scan_int64_exclusive_vs_std", scan_int64_exclusive_vs_std},
         {"scan_bench_pattern_vs_std", scan_bench_pattern_vs_std},
         {"radix_stable_partial_bit_ranges", radix_stable_partial_bit_ranges},
         {"radix_zero_width_copies", radix_zero_width_copies},

@@ -3,7 +3,10 @@
 Cases follow the reference tests: sums of 2^i ones (tests/device_scan_test.cpp:80-127), (i%7)-3 data
 (:189-265), InclusiveScanInit {1,2,3,4}+10 (:288-321), the regression sizes around tile edges
 (tests/scan_optimization_regression_test.cpp:49-61,116-208), the decoupled look-back over many tiles
-(tests/decoupled_look_back.cpp:56-186), and the benchmark input (2^28 uint32 in [0, 16)).
+(tests/decoupled_look_back.cpp:56-186), and the benchmark input (2^28 uint32 in [0, 16)).  8-byte items
+(int64 / uint64 / double; device_scan.h accepts any NumericT) follow the reference's InclusiveSum<double>
+case (tests/device_scan_test.cpp:267-286) and are bit-exact for integers (64-bit wrap-around), within a
+stated bound for doubles.
 """
 import numpy as np
 import pytest
@@ -112,8 +115,10 @@ def forced_fallback(hip):
     lib = hip.lib()
     old = lib.lcpp_hip_get_lookback_spin_limit()
     lib.lcpp_hip_set_lookback_spin_limit(0)
-    yield
-    lib.lcpp_hip_set_lookback_spin_limit(old)
+    try:
+        yield
+    finally:
+        lib.lcpp_hip_set_lookback_spin_limit(old)
 
 
 @pytest.mark.parametrize("n", [4097, 65536 * 3 + 5, (1 << 22) + 77])
@@ -164,3 +169,82 @@ def test_in_place_forced_fallback(hip, orc, dev, forced_fallback, n):
     a = orc.generate(1, n, n + 2)
     for inclusive in (False, True):
         assert np.array_equal(gpu_scan_in_place(hip, "u32", a, inclusive), orc.scan_sum_u32(a, inclusive))
+
+
+# ---- 8-byte items --------------------------------------------------------------------------------
+TILE64 = 12288  # 8-byte items per scan tile
+SIZES64 = [1, 17, 255, 256, 257, TILE64 - 1, TILE64, TILE64 + 1, 3 * TILE64 + 5, 1000003]
+
+
+def test_inclusive_sum_double_known_answer(hip, dev):
+    """tests/device_scan_test.cpp:267-286: InclusiveSum<double> of 17 ones is 1..17 exactly."""
+    got = gpu_scan(hip, "f64", np.ones(17))
+    assert got.tolist() == list(range(17))
+    got = gpu_scan(hip, "f64", np.ones(17), inclusive=True)
+    assert got.tolist() == [float(i + 1) for i in range(17)]
+
+
+@pytest.mark.parametrize("n", SIZES64)
+def test_u64_ones(hip, orc, dev, n):
+    ones = np.ones(n, np.uint64)
+    assert np.array_equal(gpu_scan(hip, "u64", ones), np.arange(n, dtype=np.uint64))
+    assert np.array_equal(gpu_scan(hip, "u64", ones, inclusive=True), np.arange(1, n + 1, dtype=np.uint64))
+
+
+@pytest.mark.parametrize("n", SIZES64)
+def test_i64_wraparound(hip, orc, dev, n):
+    a = orc.generate(0, n, n + 5).view(np.int64)  # full 64-bit words: the running sum wraps
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan(hip, "i64", a, inclusive), orc.scan_sum_u64(a, inclusive))
+    assert np.array_equal(gpu_scan(hip, "i64", a, True, init=-3), orc.scan_sum_u64(a, True, -3))
+    u = a.view(np.uint64)
+    assert np.array_equal(gpu_scan(hip, "u64", u, False, init=12345), orc.scan_sum_u64(u, False, 12345))
+
+
+def test_64bit_unaligned_views(hip, orc, dev):
+    a = orc.generate(0, 100003, 11)
+    for offset_in, offset_out in ((1, 0), (0, 1), (1, 1)):
+        got = gpu_scan(hip, "u64", a, offset_in=offset_in, offset_out=offset_out)
+        assert np.array_equal(got, orc.scan_sum_u64(a[offset_in:]))
+
+
+def test_f64_within_tolerance(hip, orc, dev):
+    # |gpu - exact| <= (i+2) * eps64 * running sum|x| per element (any summation order satisfies it).
+    n = 1000003
+    rng = np.random.default_rng(17)
+    a = rng.uniform(-1.0, 1.0, n)
+    for inclusive in (False, True):
+        got = gpu_scan(hip, "f64", a, inclusive).astype(np.longdouble)
+        exact, absum = orc.scan_sum_f64(a, inclusive)
+        bound = (np.arange(n) + 2) * np.finfo(np.float64).eps * absum
+        assert np.all(np.abs(got - exact) <= bound)
+
+
+def test_u64_2p27_full(hip, orc, dev):
+    """2^27 uint64 words (10,923 tiles of look-back), full output compared bit-exact."""
+    n = 1 << 27
+    log("scan u64 2^27")
+    d = torch.empty(n, dtype=torch.int64, device=dev)
+    hip.generate(hip.GEN_U64, d, n, 114521)
+    out = torch.empty_like(d)
+    hip.scan_sum("u64", d, out, n)
+    assert np.array_equal(to_host(out, np.uint64), orc.scan_sum_u64(to_host(d, np.uint64)))
+
+
+@pytest.mark.parametrize("n", [TILE64 * 3 + 7, (1 << 22) + 77])
+def test_64bit_forced_fallback(hip, orc, dev, forced_fallback, n):
+    """Claimed predecessors publish both words of their state; readers accept only matching pairs."""
+    log(f"scan u64 forced fallback n={n}")
+    a = orc.generate(0, n, n + 9)
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan(hip, "u64", a, inclusive), orc.scan_sum_u64(a, inclusive))
+    b = np.ones(n, np.float64)
+    assert gpu_scan(hip, "f64", b, inclusive=True).tolist() == [float(i + 1) for i in range(n)]
+
+
+@pytest.mark.parametrize("n", [TILE64 * 5 + 3, (1 << 22) + 77])
+def test_64bit_in_place_forced_fallback(hip, orc, dev, forced_fallback, n):
+    log(f"scan u64 in-place forced fallback n={n}")
+    a = orc.generate(0, n, n + 13)
+    for inclusive in (False, True):
+        assert np.array_equal(gpu_scan_in_place(hip, "u64", a, inclusive), orc.scan_sum_u64(a, inclusive))

@@ -261,6 +261,35 @@ def test_spmv_invalid_rows_and_columns(orc):
     assert zero.tolist() == [0, 0, 0, 0]
 
 
+def test_scan_u64_ones_and_wrap(orc):
+    # Exclusive sums of ones are iota; full-range 64-bit words wrap like numpy's uint64 cumsum.
+    ones = np.ones(1000, np.uint64)
+    assert np.array_equal(orc.scan_sum_u64(ones), np.arange(1000, dtype=np.uint64))
+    rng = np.random.default_rng(9)
+    a = rng.integers(0, 2**64 - 1, 5000, dtype=np.uint64, endpoint=True)
+    with np.errstate(over="ignore"):
+        ref = np.cumsum(a, dtype=np.uint64)
+    assert np.array_equal(orc.scan_sum_u64(a, inclusive=True), ref)
+    assert np.array_equal(orc.scan_sum_u64(a)[1:], ref[:-1])
+    assert orc.scan_sum_u64(a)[0] == 0
+    # init: every output shifts by init (mod 2^64); int64 through the same bits.
+    assert np.array_equal(orc.scan_sum_u64(a, inclusive=True, init=7), ref + np.uint64(7))
+    s = a.view(np.int64)
+    assert np.array_equal(orc.scan_sum_u64(s, inclusive=True).view(np.uint64), ref)
+
+
+def test_scan_f64_known_answer_and_exactness(orc):
+    # tests/device_scan_test.cpp:267-286: InclusiveSum<double> of 17 ones is 1..17.
+    out, _ = orc.scan_sum_f64(np.ones(17), inclusive=True)
+    assert [float(x) for x in out] == [float(i + 1) for i in range(17)]
+    # Integer-valued doubles below 2^53 sum exactly in any order: the long-double scan equals int64 cumsum.
+    rng = np.random.default_rng(3)
+    a = rng.integers(-1000, 1000, 100000)
+    out, absum = orc.scan_sum_f64(a.astype(np.float64))
+    assert np.array_equal(out.astype(np.int64)[1:], np.cumsum(a)[:-1])
+    assert np.array_equal(absum.astype(np.int64)[1:], np.cumsum(np.abs(a))[:-1])
+
+
 # ---- scan-by-key / reduce-by-key ---------------------------------------------------------------
 
 def numpy_by_key(keys, values, key_mask=-1):

@@ -49,7 +49,8 @@ SIZES = [1, 2, 63, 64, 255, 256, 257, 1000, 2047, 2048, 2049, 3839, 3840, 3841, 
 
 @pytest.mark.parametrize("n", SIZES)
 def test_scan_needs_fit_reference_temp(hip, n):
-    assert hip.lib().lcpp_hip_internal_scan_needed_bytes(n) <= hip.scan_temp_bytes(n, 4)
+    for eb in (4, 8):
+        assert hip.lib().lcpp_hip_internal_scan_needed_bytes(n, eb) <= hip.scan_temp_bytes(n, eb)
 
 
 @pytest.mark.parametrize("n", SIZES)
