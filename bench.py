@@ -1,12 +1,15 @@
 """Benchmark of the LCPP device hot path on one MI355X.
 
 Headline (`value`): onesweep SortKeys of 2^28 uniform uint32 keys (4 x 8-bit passes), Gkeys/s, inputs
-resident in HBM, one step = one SortKeys call.  The JSON line also carries the roofline of the
-dominant kernel (the onesweep pass), the CPU baseline (the oracle's LSD sort on a bounded sample,
-one host thread), and the other benchmark configurations (reduce, scan, SortPairs, CsrMV) plus
-ExclusiveSumByKey / ReduceByKey and the stream-compaction family (select, partition, unique, run-length
-encode), the segmented reduce / scan and the segmented sorts as achieved GB/s against the 8 TB/s HBM
-peak.
+resident in HBM, one step = one SortKeys call.  Every timed configuration records one HIP event per
+step on the launch stream and reports the mean (`ms`) with the median, minimum and maximum step.  The
+JSON line also carries the roofline of the dominant kernel (the onesweep pass) with the achievable copy
+rate measured in the same run (a 1 GiB device-to-device copy by the library's copy kernel), the CPU
+baseline of every benchmark configuration (the oracle's host restatement, one thread and all host
+threads, median of five runs on a stated sample), and the other benchmark configurations (reduce,
+scan, SortPairs, CsrMV) plus ExclusiveSumByKey / ReduceByKey and the stream-compaction family (select,
+partition, unique, run-length encode), the segmented reduce / scan and the segmented sorts as achieved
+GB/s against the 8 TB/s HBM peak.
 
 `roofline.traffic` is the HBM bytes per onesweep launch read from the committed rocprofv3
 FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `--copy-calibration`
@@ -42,19 +45,47 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def time_steps(fn, steps: int, warmup: int):
-    """Runs `warmup` untimed steps, then times exactly `steps` steps on the current stream."""
+class Timing:
+    """Per-step times of one timed loop, in ms."""
+
+    def __init__(self, per_step: list[float]):
+        self.per_step = per_step
+        self.mean = sum(per_step) / len(per_step)
+
+    def fields(self, key: str = "ms") -> dict:
+        import statistics
+        return {key: round(self.mean, 5), f"{key}_median": round(statistics.median(self.per_step), 5),
+                f"{key}_min": round(min(self.per_step), 5), f"{key}_max": round(max(self.per_step), 5)}
+
+
+def time_steps(fn, steps: int, warmup: int) -> Timing:
+    """Runs `warmup` untimed steps, then times exactly `steps` steps on the current stream with one event
+    per step boundary."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    events[0].record()
+    for i in range(steps):
         fn()
-    end.record()
+        events[i + 1].record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return Timing([events[i].elapsed_time(events[i + 1]) for i in range(steps)])
+
+
+def achievable_copy_gbps(hip, dev, reps: int = 10) -> dict:
+    """1 GiB device-to-device copy by the library's copy kernel (8-byte lanes, one 64 KiB tile per
+    workgroup): the copy rate this GPU reaches in this run, median of `reps`."""
+    import torch
+    src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    t = time_steps(lambda: hip.device_copy(dst, src, 1 << 30), reps, 5)
+    import statistics
+    ms = statistics.median(t.per_step)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes": 2 << 30, "ms_median": round(ms, 5), "GBps": round((2 << 30) / ms / 1e6, 1)}
 
 
 def kernel_avg_ms(hip, fn, kernel: str, reps: int):
@@ -106,6 +137,21 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+_CSR = {}
+
+
+def zipf_matrix():
+    """The config-5 CSR matrix (built once per run; the host generation takes tens of seconds)."""
+    if "m" not in _CSR:
+        import workloads
+        _CSR["m"] = workloads.zipf_csr(1 << 20, 1 << 20, SEED)
+    return _CSR["m"]
+
+
+def rate(nbytes: float, ms: float) -> float:
+    return round(nbytes / ms / 1e6, 1)
+
+
 def extra_reduce(hip, dev, steps, warmup, extra):
     import torch
     flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
@@ -118,9 +164,8 @@ def extra_reduce(hip, dev, steps, warmup, extra):
     hot = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
     cold_k, _ = kernel_avg_ms(hip, lambda: (flush_mall(flush), hip.reduce_sum("i32", a, s, m, temp=rt)),
                               "reduce_sum_partials", 5)
-    extra["reduce_sum_i32_2p24"] = {"ms_hot": round(hot, 5), "GBps_hot": round(4 * m / hot / 1e6, 1),
-                                    "kernel_ms_cold": round(cold_k, 5),
-                                    "GBps_cold": round(4 * m / cold_k / 1e6, 1)}
+    extra["reduce_sum_i32_2p24"] = {**hot.fields("ms_hot"), "GBps_hot": rate(4 * m, hot.mean),
+                                    "kernel_ms_cold": round(cold_k, 5), "GBps_cold": rate(4 * m, cold_k)}
     del flush
     # Reduce 2^28 int32 (north-star size).
     m = 1 << 28
@@ -128,11 +173,11 @@ def extra_reduce(hip, dev, steps, warmup, extra):
     hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
     rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
     t = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
-    extra["reduce_sum_i32_2p28"] = {"ms": round(t, 5), "GBps": round(4 * m / t / 1e6, 1),
-                                    "frac": round(4 * m / t / 1e6 / HBM_PEAK_GBS, 4)}
+    extra["reduce_sum_i32_2p28"] = {**t.fields(), "GBps": rate(4 * m, t.mean),
+                                    "frac": round(4 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
-def extra_scan(hip, dev, steps, warmup, extra):
+def extra_scan(hip, dev, steps, warmup, extra, copy=None):
     import torch
     # ExclusiveSum 2^28 uint32 in [0, 16) (config 2).
     m = 1 << 28
@@ -142,9 +187,21 @@ def extra_scan(hip, dev, steps, warmup, extra):
     st = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
     t = time_steps(lambda: hip.scan_sum("u32", b, c, m, temp=st), steps, warmup)
     sk, _ = kernel_avg_ms(hip, lambda: hip.scan_sum("u32", b, c, m, temp=st), "scan_sum", 5)
-    extra["exclusive_sum_u32_2p28"] = {"ms": round(t, 5), "GBps": round(8 * m / t / 1e6, 1),
-                                       "frac": round(8 * m / t / 1e6 / HBM_PEAK_GBS, 4),
-                                       "kernel_ms": round(sk, 5)}
+    e = {**t.fields(), "GBps": rate(8 * m, t.mean), "frac": round(8 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4),
+         "kernel_ms": round(sk, 5)}
+    if copy:
+        e["frac_of_achievable_copy"] = round(copy["ms_median"] / t.mean, 4)
+    extra["exclusive_sum_u32_2p28"] = e
+    # ExclusiveSum 2^27 uint64 (the same 1 GiB in, 1 GiB out, 8-byte items).
+    del b, c
+    m = 1 << 27
+    b = torch.empty(m, dtype=torch.int64, device=dev)
+    hip.generate(hip.GEN_U64, b, m, SEED)
+    c = torch.empty_like(b)
+    st = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(m, 8)), dtype=torch.int32, device=dev)
+    t = time_steps(lambda: hip.scan_sum("u64", b, c, m, temp=st), steps, warmup)
+    extra["exclusive_sum_u64_2p27"] = {**t.fields(), "GBps": rate(16 * m, t.mean),
+                                       "frac": round(16 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def extra_sort_pairs(hip, dev, steps, warmup, extra):
@@ -160,26 +217,25 @@ def extra_sort_pairs(hip, dev, steps, warmup, extra):
         pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32, device=dev)
         t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), 1)
         extra[f"sort_pairs_u64_u32_2p27_{kind}"] = {
-            "ms": round(t, 4), "Gpairs_per_s": round(m / t / 1e6, 3),
-            "GBps_8pass_model": round(2 * 8 * m * 12 / t / 1e6, 1),
-            "frac": round(2 * 8 * m * 12 / t / 1e6 / HBM_PEAK_GBS, 4)}
+            **t.fields(), "Gpairs_per_s": round(m / t.mean / 1e6, 3),
+            "GBps_8pass_model": rate(2 * 8 * m * 12, t.mean),
+            "frac": round(2 * 8 * m * 12 / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
         del k, v, ko, vo, pt
 
 
 def extra_spmv(hip, dev, steps, warmup, extra):
     import torch
-    import workloads
     # CsrMV fp32 (config 5): 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
     rows = cols = 1 << 20
-    va, ro, ci, xv, nnz = workloads.zipf_csr(rows, cols, SEED)
+    va, ro, ci, xv, nnz = zipf_matrix()
     d = [torch.from_numpy(t).to(dev) for t in (va, ro, ci, xv)]
     y = torch.empty(rows, dtype=torch.float32, device=dev)
     spmv = lambda: hip.spmv_csr("f32", "i32", d[0], d[1], d[2], d[3], y, rows, cols, nnz)
     t = time_steps(spmv, steps, warmup)
     sk, _ = kernel_avg_ms(hip, spmv, "spmv_csr", 5)
     spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * cols
-    extra["spmv_csr_f32_zipf1.5_2p20"] = {"nnz": nnz, "ms": round(t, 5), "kernel_ms": round(sk, 5),
-                                          "GBps": round(spmv_bytes / sk / 1e6, 1),
+    extra["spmv_csr_f32_zipf1.5_2p20"] = {"nnz": nnz, **t.fields(), "kernel_ms": round(sk, 5),
+                                          "GBps": rate(spmv_bytes, sk),
                                           "frac": round(spmv_bytes / sk / 1e6 / HBM_PEAK_GBS, 4)}
 
 
@@ -198,8 +254,8 @@ def extra_by_key(hip, dev, steps, warmup, extra):
     st = torch.empty(hip.bytes_to_uint_count(hip.scan_by_key_temp_bytes(m, 4, 4)), dtype=torch.int32, device=dev)
     t = time_steps(lambda: hip.scan_by_key("i32", "u32", keys, vals, out, m, inclusive=False, temp=st), steps, warmup)
     sk, _ = kernel_avg_ms(hip, lambda: hip.scan_by_key("i32", "u32", keys, vals, out, m, temp=st), "scan_by_key", 5)
-    extra["exclusive_sum_by_key_i32_u32_2p28"] = {"ms": round(t, 5), "GBps": round(12 * m / t / 1e6, 1),
-                                                  "frac": round(12 * m / t / 1e6 / HBM_PEAK_GBS, 4),
+    extra["exclusive_sum_by_key_i32_u32_2p28"] = {**t.fields(), "GBps": rate(12 * m, t.mean),
+                                                  "frac": round(12 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4),
                                                   "kernel_ms": round(sk, 5)}
     runs_out = torch.zeros(1, dtype=torch.int32, device=dev)
     rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_by_key_temp_bytes(m, 4, 4)), dtype=torch.int32, device=dev)
@@ -207,8 +263,8 @@ def extra_by_key(hip, dev, steps, warmup, extra):
     t = time_steps(lambda: hip.reduce_by_key("i32", "u32", keys, vals, uniq, agg, runs_out, m, temp=rt), steps, warmup)
     runs = int(runs_out.item())
     moved = 8 * m + 8 * runs
-    extra["reduce_by_key_i32_u32_2p28"] = {"ms": round(t, 5), "runs": runs, "GBps": round(moved / t / 1e6, 1),
-                                           "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+    extra["reduce_by_key_i32_u32_2p28"] = {**t.fields(), "runs": runs, "GBps": rate(moved, t.mean),
+                                           "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def extra_compact(hip, dev, steps, warmup, extra):
@@ -230,8 +286,8 @@ def extra_compact(hip, dev, steps, warmup, extra):
         kept = int(num[0].item())
         moved = 4 * m + 4 * (kept if written is None else written)
         kms, _ = kernel_avg_ms(hip, call, "compact", 5)
-        extra[name] = {"ms": round(t, 5), "kernel_ms": round(kms, 5), "selected": kept,
-                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+        extra[name] = {**t.fields(), "kernel_ms": round(kms, 5), "selected": kept,
+                       "GBps": rate(moved, t.mean), "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
     r = x
     hip.generate(hip.GEN_U32_HI, r, m, SEED + 7)
     runs_in = torch.cumsum(((r & 63) == 0).to(torch.int32), 0, dtype=torch.int32)
@@ -245,8 +301,8 @@ def extra_compact(hip, dev, steps, warmup, extra):
         runs = int(num[0].item())
         moved = 4 * m + per_run * runs
         kms, _ = kernel_avg_ms(hip, call, "compact", 5)
-        extra[name] = {"ms": round(t, 5), "kernel_ms": round(kms, 5), "runs": runs,
-                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+        extra[name] = {**t.fields(), "kernel_ms": round(kms, 5), "runs": runs,
+                       "GBps": rate(moved, t.mean), "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def extra_segmented(hip, dev, steps, warmup, extra):
@@ -263,25 +319,25 @@ def extra_segmented(hip, dev, steps, warmup, extra):
     t = time_steps(call, steps, warmup)
     kms, _ = kernel_avg_ms(hip, call, "segment_reduce", 5)
     moved = 4 * m + 12 * segs
-    extra["segment_reduce_sum_i32_2p28_4096"] = {"ms": round(t, 5), "kernel_ms": round(kms, 5),
-                                                 "GBps": round(moved / t / 1e6, 1),
-                                                 "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+    extra["segment_reduce_sum_i32_2p28_4096"] = {**t.fields(), "kernel_ms": round(kms, 5),
+                                                 "GBps": rate(moved, t.mean),
+                                                 "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
     y = torch.empty_like(x)
     call = lambda: hip.segmented_scan("i32", x, y, begins, ends, segs, inclusive=True)
     t = time_steps(call, steps, warmup)
     kms, _ = kernel_avg_ms(hip, call, "segmented_scan", 5)
     moved = 8 * m + 8 * segs
-    extra["segmented_inclusive_sum_i32_2p28_4096"] = {"ms": round(t, 5), "kernel_ms": round(kms, 5),
-                                                      "GBps": round(moved / t / 1e6, 1),
-                                                      "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+    extra["segmented_inclusive_sum_i32_2p28_4096"] = {**t.fields(), "kernel_ms": round(kms, 5),
+                                                      "GBps": rate(moved, t.mean),
+                                                      "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def extra_segsort(hip, dev, steps, warmup, extra):
     import torch
     # DeviceSegmentedRadixSort::SortPairs over 2^26 uint32 keys + uint32 values in 2^14 segments of 4096
     # (the chunk kernel sorts their 2048-item chunks, then one global merge pass), and SortKeys over 2^26
-    # uint32 keys in 2^16 segments of 1024 (the block kernel, one workgroup per segment).  Algorithmic bytes: every key (and value) read once and
-    # written once.
+    # uint32 keys in 2^16 segments of 1024 (the block kernel, one workgroup per segment).  Algorithmic
+    # bytes: every key (and value) read once and written once.
     m = 1 << 26
     keys = torch.empty(m, dtype=torch.int32, device=dev)
     hip.generate(hip.GEN_U32_HI, keys, m, SEED + 13)
@@ -305,11 +361,11 @@ def extra_segsort(hip, dev, steps, warmup, extra):
         chunk_ms, _ = kernel_avg_ms(hip, call, "segsort_chunk", 3)
         merge_ms, merges = kernel_avg_ms(hip, call, "segsort_merge", 3)
         moved = (16 if pairs else 8) * m
-        extra[name] = {"ms": round(t, 5), "Gkeys_per_s": round(m / t / 1e6, 2),
+        extra[name] = {**t.fields(), "Gkeys_per_s": round(m / t.mean / 1e6, 2),
                        "block_kernel_ms": round(block_ms, 5), "chunk_kernel_ms": round(chunk_ms, 5),
                        "merge_kernel_ms": round(merge_ms, 5),
                        "merge_launches_per_call": merges // 3,
-                       "GBps": round(moved / t / 1e6, 1), "frac": round(moved / t / 1e6 / HBM_PEAK_GBS, 4)}
+                       "GBps": rate(moved, t.mean), "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
@@ -317,13 +373,110 @@ EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pa
           "segmented": extra_segmented, "segsort": extra_segsort}
 
 
-def run_extras(hip, dev, steps, warmup, names):
+def run_extras(hip, dev, steps, warmup, names, copy=None):
     import torch
     extra = {}
     for name in names:
-        EXTRAS[name](hip, dev, steps, warmup, extra)
+        if name == "scan":
+            extra_scan(hip, dev, steps, warmup, extra, copy)
+        else:
+            EXTRAS[name](hip, dev, steps, warmup, extra)
         torch.cuda.empty_cache()
     return extra
+
+
+# ---- CPU baseline ----------------------------------------------------------------------------------
+def cpu_baseline(keys_dev, reps: int = 5) -> dict:
+    """The oracle's host restatement of every benchmark configuration (oracle/cpu_baseline.cpp), on one
+    thread and on every host thread, median of `reps` runs after one untimed run, on the samples named
+    in each entry.  Inputs are the same seeded streams as the GPU runs (the SortKeys sample is the first
+    2^24 of the GPU's keys)."""
+    import statistics
+    import numpy as np
+    sys.path.insert(0, str(REPO))
+    import oracle
+    threads_all = os.cpu_count() or 1
+
+    def timed(fn, prep=None):
+        out = {}
+        for label, th in (("1_thread", 1), (f"{threads_all}_threads", threads_all)):
+            ts = []
+            for r in range(reps + 1):
+                args = prep() if prep else ()
+                t0 = time.perf_counter()
+                fn(th, *args)
+                dt = time.perf_counter() - t0
+                if r:
+                    ts.append(dt)
+            out[label] = statistics.median(ts)
+        return out
+
+    res = {}
+    # Reduce: config 1 in full (2^24 int32 in [-1000, 1000]).
+    n = 1 << 24
+    a = oracle.generate(2, n, SEED)
+    t = timed(lambda th: oracle.par_reduce_sum_i32(a, th))
+    res["reduce_sum_i32_2p24"] = {"sample": "all 2^24 items", "unit": "GB/s",
+                                  **{k: round(4 * n / v / 1e9, 2) for k, v in t.items()}}
+    # Scan: 2^26 of config 2's 2^28 u32 in [0, 16).
+    n = 1 << 26
+    b = oracle.generate(3, n, SEED)
+    out = np.empty_like(b)
+    t = timed(lambda th: oracle.par_scan_sum_u32(b, th, out))
+    res["exclusive_sum_u32_2p28"] = {"sample": "first 2^26 of the 2^28 items", "unit": "GB/s",
+                                     **{k: round(8 * n / v / 1e9, 2) for k, v in t.items()}}
+    del b, out
+    # SortKeys: 2^24 of config 3's keys (stable 8-bit LSD, as on the GPU), plus std::sort on one thread.
+    n = 1 << 24
+    sample = keys_dev[:n].cpu().numpy().view(np.uint32).copy()
+    work, tmp = np.empty_like(sample), np.empty_like(sample)
+
+    def fresh():
+        np.copyto(work, sample)
+        return ()
+    t = timed(lambda th: oracle.par_radix_sort_u32(work, th, tmp), fresh)
+    std_ts = []
+    for r in range(reps + 1):
+        fresh()
+        t0 = time.perf_counter()
+        oracle.std_sort_u32(work)
+        if r:
+            std_ts.append(time.perf_counter() - t0)
+    res["sort_keys_u32_2p28"] = {"sample": "first 2^24 of the 2^28 keys", "unit": "Gkeys/s",
+                                 **{k: round(n / v / 1e9, 4) for k, v in t.items()},
+                                 "std_sort_1_thread": round(n / statistics.median(std_ts) / 1e9, 4)}
+    del sample, work, tmp
+    # SortPairs: 2^22 uniform u64 keys with u32 index values (config 4a stream).
+    n = 1 << 22
+    k0 = oracle.generate(0, n, SEED)
+    v0 = np.arange(n, dtype=np.uint32)
+    kw, vw, tk, tv = np.empty_like(k0), np.empty_like(v0), np.empty_like(k0), np.empty_like(v0)
+
+    def fresh_pairs():
+        np.copyto(kw, k0)
+        np.copyto(vw, v0)
+        return ()
+    t = timed(lambda th: oracle.par_radix_sort_u64_u32(kw, vw, th, (tk, tv)), fresh_pairs)
+    res["sort_pairs_u64_u32_2p27_uniform"] = {"sample": "2^22 pairs of the same key stream", "unit": "Gpairs/s",
+                                              **{k: round(n / v / 1e9, 4) for k, v in t.items()}}
+    del k0, v0, kw, vw, tk, tv
+    # CsrMV: the whole config-5 matrix.
+    rows = cols = 1 << 20
+    va, ro, ci, xv, nnz = zipf_matrix()
+    y = np.empty(rows, np.float32)
+    t = timed(lambda th: oracle.par_spmv_csr_f32(va, ro, ci, xv, rows, th, y))
+    spmv_bytes = 8 * nnz + 4 * (rows + 1) + 4 * rows + 4 * cols
+    res["spmv_csr_f32_zipf1.5_2p20"] = {"sample": f"the whole matrix ({nnz} nonzeros)", "unit": "GB/s",
+                                        **{k: round(spmv_bytes / v / 1e9, 2) for k, v in t.items()}}
+    res["threads_all"] = threads_all
+    return res
+
+
+def device_info(torch, dev) -> dict:
+    props = torch.cuda.get_device_properties(dev)
+    return {"device": props.name, "gcnArchName": getattr(props, "gcnArchName", ""),
+            "compute_units": props.multi_processor_count,
+            "hbm_GiB": round(props.total_memory / 2**30, 1)}
 
 
 def main() -> int:
@@ -349,7 +502,6 @@ def main() -> int:
     import lcpp_hip as hip
 
     dev = torch.device("cuda:0")
-    props = torch.cuda.get_device_properties(dev)
     steps, warmup = args.steps, args.warmup
     if args.only:
         print(json.dumps({"only": args.only, "extra": run_extras(hip, dev, steps, warmup, [args.only])}))
@@ -365,12 +517,16 @@ def main() -> int:
     def sort_step():
         hip.sort_keys("u32", keys, out, n, temp=temp)
 
-    ms = time_steps(sort_step, steps, warmup)
+    t = time_steps(sort_step, steps, warmup)
+    ms = t.mean
     gkeys = n / (ms * 1e-3) / 1e9
     onesweep_ms, launches = kernel_avg_ms(hip, sort_step, "radix_onesweep", max(3, steps // 4))
     hist_ms, _ = kernel_avg_ms(hip, sort_step, "radix_histogram", 3)
     pass_bytes = 2 * n * 4  # read + write of the keys in one 8-bit pass
     achieved = pass_bytes / (onesweep_ms * 1e-3) / 1e9
+    del temp, out
+    torch.cuda.empty_cache()
+    copy = achievable_copy_gbps(hip, dev)  # after the sort, with the GPU at its working clocks
     line = {
         "metric": "onesweep SortKeys 2^28 u32 Gkeys/s; reduce/scan achieved HBM GB/s vs peak",
         "value": round(gkeys, 3),
@@ -385,7 +541,8 @@ def main() -> int:
         "dtype": "u32",
         "data": "synthetic (splitmix64, seed 114521), generated on the device",
         "config": {"workload": "DeviceRadixSort::SortKeys, 2^28 uniform uint32 keys, 4 x 8-bit onesweep passes",
-                   "items": n, "device": props.name or getattr(props, "gcnArchName", "")},
+                   "items": n, **device_info(torch, dev)},
+        "timing": t.fields("ms_per_step"),
         "roofline": {
             "kernel": "radix_onesweep",
             "bound": "hbm",
@@ -398,38 +555,33 @@ def main() -> int:
             "algorithmic_bytes_per_launch": pass_bytes,
             "whole_sort_frac_4pass_model": round((32 * n) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "histogram_avg_ms": round(hist_ms, 5),
+            "achievable_copy_GBps": copy["GBps"],
+            "frac_of_achievable_copy": round(achieved / copy["GBps"], 4),
         },
     }
-    del temp
 
-    # ---- CPU baseline: the oracle's LSD radix sort, one thread, on a bounded sample -----------------
+    # ---- CPU baseline: every configuration on the host, one thread and all threads -----------------
     if not args.no_cpu:
-        import numpy as np
-        sys.path.insert(0, str(REPO))
-        import oracle
-        m = 1 << 24
-        sample = keys[:m].cpu().numpy().view(np.uint32).copy()
-        oracle.radix_sort(sample)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            oracle.radix_sort(sample)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el > 12.0 or reps >= 40:
-                break
+        per_config = cpu_baseline(keys)
+        sk = per_config["sort_keys_u32_2p28"]
+        threads_all = per_config.pop("threads_all")
         line["cpu_baseline"] = {
-            "value": round(m * reps / el / 1e9, 4),
+            "value": sk[f"{threads_all}_threads"],
             "unit": "Gkeys/s",
-            "cores": 1,
+            "cores": threads_all,
             "kind": "port",
-            "sample": f"first 2^24 of the same keys, stable 8-bit LSD sort (oracle/oracle.c), {reps} reps",
+            "sample": "first 2^24 of the same keys, stable 8-bit LSD sort (oracle/cpu_baseline.cpp) on every "
+                      "host thread, median of 5",
             "cpu": cpu_model(),
-            "host_threads_available": os.cpu_count(),
+            "per_config": per_config,
         }
 
     # ---- other configurations -----------------------------------------------------------------------
     if not args.no_extra:
-        line["extra"] = run_extras(hip, dev, steps, warmup, list(EXTRAS))
+        del keys
+        torch.cuda.empty_cache()
+        line["extra"] = run_extras(hip, dev, steps, warmup, list(EXTRAS), copy)
+        line["extra"]["achievable_copy_1GiB"] = copy
 
     print(json.dumps(line))
     return 0

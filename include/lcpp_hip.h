@@ -52,6 +52,11 @@ int lcpp_hip_profile_reset(void);
 int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches);
 int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes);
 
+/* Device-to-device copy of `bytes` bytes on `stream` by a library kernel (8-byte lanes when both
+ * pointers and the size are 8-byte aligned).  No reference counterpart: the sorts' zero-width
+ * case (begin_bit == end_bit) copies with it, and bench.py times it as the achievable copy rate. */
+int lcpp_hip_device_copy(void* dst, const void* src, uint64_t bytes, void* stream);
+
 #ifdef LCPP_HIP_PHASE_TRACE
 /* Diagnostic build (liblcpp_hip_trace.so) only: the onesweep and scan kernels write one record of
  * 16 64-bit words per tile to `buffer` (device memory holding `records` records; null stops it).  No
@@ -463,7 +468,8 @@ int lcpp_hip_generate(int kind, void* out, uint64_t n, uint64_t seed, uint64_t s
 /* ---------------------------------------------------------------------------------------------
  * Introspection and test hooks (no reference counterpart): the bytes of temp storage the kernels
  * actually carve, the onesweep portion count for a given temp size, and the in-wave ranking variant
- * of the onesweep kernel (0 ballot match, 1 LDS lane-mask table, the default; same ranks).
+ * of the onesweep kernel (0 ballot match in every wave, 1 LDS lane-mask tables in every wave, 2 a
+ * split of the waves between them, the default; all give the same ranks).
  * ------------------------------------------------------------------------------------------- */
 size_t lcpp_hip_internal_scan_needed_bytes(uint64_t n, size_t elem_bytes);
 size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,

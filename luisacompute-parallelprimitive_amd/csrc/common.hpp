@@ -222,6 +222,9 @@ struct LaunchScope {
 
 int launch_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, hipStream_t stream);
 
+// Device-to-device copy of `bytes` (a kernel, so graph capture records no memcpy node).  Ranges must not overlap.
+int launch_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream);
+
 #ifdef LCPP_HIP_PHASE_TRACE
 // Points the phase-trace records of one translation unit's kernels at `buffer` (diagnostic build).
 int radix_trace_set_buffer(void* buffer, uint64_t records);

@@ -51,8 +51,18 @@ constexpr uint32_t kFlagPartial = 1u << 30;
 constexpr uint32_t kFlagInclusive = 2u << 30;
 constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
+// In-wave ranking: the last `ballot_sixteenths` / 16 of a workgroup's waves match digits with ballots
+// (VALU), the others with LDS lane-mask tables (LDS pipe); the test hook selects all-ballot (mode 0),
+// all-table (mode 1) or the default split (mode 2).
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
+constexpr int kRankMixed = 2;
+// A quarter of the waves on ballots: SortKeys 2^28 u32 2.430 ms, against 2.455 ms with tables only,
+// 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots only (MI355X).
+constexpr uint32_t kMixedBallotSixteenths = 4;
+constexpr uint32_t ballot_sixteenths_for(int mode) {
+    return mode == kRankBallot ? 16u : mode == kRankLdsMatch ? 0u : kMixedBallotSixteenths;
+}
 
 #ifdef LCPP_HIP_PHASE_TRACE
 // Phase-trace buffer of the diagnostic build: one record per (pass, tile), slot (shift / 8) * tiles + tile.
@@ -103,6 +113,17 @@ __device__ __forceinline__ uint32_t digit_of(U ordered, uint32_t shift, uint32_t
         if (ordered == U(~kHigh)) ordered = kHigh;
     }
     return static_cast<uint32_t>(ordered >> shift) & mask;
+}
+
+// The same digit from the bit count of the pass: one bit-field extract for 4-byte keys.
+template <typename U, int KIND>
+__device__ __forceinline__ uint32_t digit_bits(U ordered, uint32_t shift, uint32_t num_bits) {
+    if constexpr (KIND == kFloat) {
+        constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+        if (ordered == U(~kHigh)) ordered = kHigh;
+    }
+    if constexpr (sizeof(U) == 4) return __builtin_amdgcn_ubfe(ordered, shift, num_bits);
+    else return static_cast<uint32_t>(ordered >> shift) & ((1u << num_bits) - 1u);
 }
 
 // Lanes of the wave whose 8-bit digit equals this lane's.  Per digit bit: t = 0 or ~0 (the bit,
@@ -374,7 +395,7 @@ __device__ __forceinline__ uint32_t lookback_digit(uint32_t* __restrict__ lookba
     return excl;
 }
 
-template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW, int RANK>
+template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW>
 // Register budget for two workgroups per CU: BLOCK / 128 waves per SIMD (128 VGPRs at 512 threads,
 // 64 at 1024).
 __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* __restrict__ keys_in,
@@ -385,7 +406,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
                                                          uint32_t* __restrict__ next_offsets,
                                                          uint32_t* __restrict__ lookback, uint32_t shift,
                                                          uint32_t num_bits, uint32_t out_items,
-                                                         uint32_t spin_limit) {
+                                                         uint32_t spin_limit, uint32_t ballot_sixteenths) {
     using U = typename KeyTraits<K>::U;
     using VW = typename ValueWord<VB>::type;
     constexpr int KIND = KeyTraits<K>::kind;
@@ -422,7 +443,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
 #pragma unroll
     for (uint32_t i = lane; i < kDigits; i += kWave) {
         s_counts[wave][i] = 0;
-        if constexpr (RANK == kRankLdsMatch) s_match[wave][i] = 0;
+        s_match[wave][i] = 0;
     }
     const uint32_t tile = tile_of_block(blockIdx.x, gridDim.x);
     const uint32_t tile_base = tile * TILE;
@@ -456,17 +477,22 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
 
     // Rank inside the wave: rank = keys of the same digit in earlier rounds (the wave's LDS counter)
     // + lanes of the same digit below this lane in this round.  The highest such lane advances the
-    // counter.  The peer mask comes from 8 ballots (RANK == kRankBallot) or from an LDS table of
-    // 64-bit lane masks, one per digit (RANK == kRankLdsMatch): every lane ORs its bit into its digit's
+    // counter.  The peer mask comes from 8 ballots (ballot waves) or from an LDS table of 64-bit lane
+    // masks, one per digit (table waves): every lane ORs its bit into its digit's
     // entry, reads the entry back (all ORs of the instruction have landed: a wave's LDS operations
     // complete in issue order), and the highest peer clears it.  OR is order-independent, so the mask
     // does not depend on how the hardware serialises conflicting lanes.
     uint32_t rank[ITEMS];
-    if constexpr (RANK == kRankLdsMatch) {
+    // Mixed ranking splits the work between the LDS pipe (tables) and the VALU (ballots); the choice is
+    // per wave, so the branch is uniform.
+    // The ballot waves are the last ones: waves 0..3 publish and walk the look-back after the rank, so
+    // they take the faster table ranking.
+    const bool table_rank = (W - 1 - __builtin_amdgcn_readfirstlane(wave)) * 16 >= ballot_sixteenths * W;
+    if (table_rank) {
         const uint64_t lane_bit = 1ull << lane;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
-            const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+            const uint32_t d = digit_bits<U, KIND>(keys[k], shift, num_bits);
             uint64_t* slot = &s_match[wave][d];
             __hip_atomic_fetch_or(slot, lane_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             __builtin_amdgcn_wave_barrier();
@@ -484,7 +510,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     } else {
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
-            const uint32_t d = digit_of<U, KIND>(keys[k], shift, mask);
+            const uint32_t d = digit_bits<U, KIND>(keys[k], shift, num_bits);
             const uint64_t peers = match_digit(d);
             const uint32_t below = popc_lanes_below(peers);
             const uint32_t base = s_counts[wave][d];
@@ -528,7 +554,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // registers are free while the look-back runs.  The offsets are read first: their rows share
     // the buffer the keys go to.
 #pragma unroll
-    for (int k = 0; k < ITEMS; ++k) rank[k] += s_counts[wave][digit_of<U, KIND>(keys[k], shift, mask)];
+    for (int k = 0; k < ITEMS; ++k) rank[k] += s_counts[wave][digit_bits<U, KIND>(keys[k], shift, num_bits)];
     __syncthreads();
     U* s_keys = reinterpret_cast<U*>(s_tile);
 #pragma unroll
@@ -554,17 +580,30 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     __syncthreads();
     clk.mark<6>();  // global offsets known
 
+    // Scatter from LDS in digit order.  Full tiles (all but the last) take a branch-free path, so the
+    // reads of all ITEMS keys and offsets are in flight together; the clamp to the output keeps every
+    // store in bounds whatever the offsets (a correct sort never needs it).
     U* ukeys_out = reinterpret_cast<U*>(keys_out);
     uint32_t gpos[VB ? ITEMS : 1];
+    if (valid == TILE) {
 #pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-        const uint32_t i = tid + j * BLOCK;
-        if (i < valid) {
+        for (int j = 0; j < ITEMS; ++j) {
+            const uint32_t i = tid + j * BLOCK;
             const U key = s_keys[i];
-            const uint32_t d = digit_of<U, KIND>(key, shift, mask);
-            const uint32_t g = s_global_minus_local[d] + i;
-            if (g < out_items) ukeys_out[g] = twiddle_out<U, KIND, DESC>(key);  // always true for a correct sort
+            const uint32_t g = min(s_global_minus_local[digit_bits<U, KIND>(key, shift, num_bits)] + i, out_items - 1u);
+            ukeys_out[g] = twiddle_out<U, KIND, DESC>(key);
             if constexpr (VB != 0) gpos[j] = g;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+            const uint32_t i = tid + j * BLOCK;
+            if (i < valid) {
+                const U key = s_keys[i];
+                const uint32_t g = s_global_minus_local[digit_bits<U, KIND>(key, shift, num_bits)] + i;
+                if (g < out_items) ukeys_out[g] = twiddle_out<U, KIND, DESC>(key);  // always true for a correct sort
+                if constexpr (VB != 0) gpos[j] = g;
+            }
         }
     }
 
@@ -575,10 +614,15 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         for (int k = 0; k < ITEMS; ++k) s_vals[rank[k]] = vals[k];
         __syncthreads();
         VW* uvals_out = reinterpret_cast<VW*>(values_out);
+        if (valid == TILE) {
 #pragma unroll
-        for (int j = 0; j < ITEMS; ++j) {
-            const uint32_t i = tid + j * BLOCK;
-            if (i < valid && gpos[j] < out_items) uvals_out[gpos[j]] = s_vals[i];
+            for (int j = 0; j < ITEMS; ++j) uvals_out[gpos[j]] = s_vals[tid + j * BLOCK];
+        } else {
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                const uint32_t i = tid + j * BLOCK;
+                if (i < valid && gpos[j] < out_items) uvals_out[gpos[j]] = s_vals[i];
+            }
         }
     }
 #ifdef LCPP_HIP_PHASE_TRACE
@@ -624,7 +668,7 @@ constexpr Geometry geometry() {
 // default) and the in-wave ranking variant.  Each sort reads them once, so a concurrent change on
 // another thread applies from the next call.
 std::atomic<uint32_t> g_portion_limit{0};
-std::atomic<int> g_rank_mode{kRankLdsMatch};
+std::atomic<int> g_rank_mode{kRankMixed};
 
 // Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
 // portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
@@ -641,7 +685,7 @@ struct Layout {
     uint32_t passes, portions, portion, tiles_max;
     size_t bins_off, lookback_off, keys_tmp_off, values_tmp_off, total;
     size_t clear_bytes;  // bins, zeroed per call
-    int rank_mode = kRankLdsMatch;  // test hooks as read at the start of the call
+    int rank_mode = kRankMixed;  // test hooks as read at the start of the call
     uint32_t spin_limit = 64;
 };
 
@@ -753,12 +797,9 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
-            if (L.rank_mode == kRankBallot)
-                onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankBallot><<<tiles, G.block, 0, stream>>>(
-                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit);
-            else
-                onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, kRankLdsMatch><<<tiles, G.block, 0, stream>>>(
-                    src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit);
+            onesweep_kernel<K, DESC, VB, G.block, G.items, G.window><<<tiles, G.block, 0, stream>>>(
+                src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit,
+                ballot_sixteenths_for(L.rank_mode));
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
@@ -786,11 +827,9 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
     }
     if (begin_bit == end_bit) {
         if (db) return kOk;
-        int st = check_hip(hipMemcpyAsync(keys_out, keys_in, static_cast<size_t>(n) * sizeof(K), hipMemcpyDeviceToDevice,
-                                          stream), "key copy");
+        int st = launch_copy(keys_out, keys_in, static_cast<uint64_t>(n) * sizeof(K), stream);
         if (st != kOk || !VB) return st;
-        return check_hip(hipMemcpyAsync(values_out, values_in, static_cast<size_t>(n) * VB, hipMemcpyDeviceToDevice,
-                                        stream), "value copy");
+        return launch_copy(values_out, values_in, static_cast<uint64_t>(n) * VB, stream);
     }
     constexpr Geometry G = geometry<K, VB>();
     const uint32_t portion_limit = g_portion_limit.load(std::memory_order_relaxed);
@@ -842,10 +881,12 @@ int lcpp_hip_radix_set_portion_limit(uint32_t max_items_per_portion) {
     return kOk;
 }
 
-// Selects the in-wave ranking of the onesweep kernel: 0 ballot match, 1 LDS lane-mask table
-// (default).  Both give the same stable ranks; the switch exists for tests and measurements.
+// Selects the in-wave ranking of the onesweep kernel: 0 ballot match in every wave, 1 LDS lane-mask
+// tables in every wave, 2 both (default).  All give the same stable ranks; the switch exists for tests
+// and measurements.
 int lcpp_hip_internal_radix_rank_mode(int mode) {
-    if (mode != kRankBallot && mode != kRankLdsMatch) return set_error(kInvalidArgument, "rank mode must be 0 or 1");
+    if (mode != kRankBallot && mode != kRankLdsMatch && mode != kRankMixed)
+        return set_error(kInvalidArgument, "rank mode must be 0, 1 or 2");
     g_rank_mode.store(mode, std::memory_order_relaxed);
     return kOk;
 }

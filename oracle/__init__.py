@@ -41,6 +41,19 @@ def lib() -> C.CDLL:
         h.oracle_scan_sum_u32.argtypes = [vp, vp, u64, i32, u32]
         h.oracle_scan_sum_f32.restype = None
         h.oracle_scan_sum_f32.argtypes = [vp, vp, vp, u64, i32, C.c_float]
+        i64, i32p = C.c_int64, C.c_int
+        h.oracle_par_reduce_sum_i32.restype = i64
+        h.oracle_par_reduce_sum_i32.argtypes = [vp, u64, i32p]
+        h.oracle_par_scan_sum_u32.restype = None
+        h.oracle_par_scan_sum_u32.argtypes = [vp, vp, u64, i32p]
+        h.oracle_par_radix_sort_u32.restype = None
+        h.oracle_par_radix_sort_u32.argtypes = [vp, vp, u64, i32p]
+        h.oracle_std_sort_u32.restype = None
+        h.oracle_std_sort_u32.argtypes = [vp, u64]
+        h.oracle_par_radix_sort_u64_u32.restype = None
+        h.oracle_par_radix_sort_u64_u32.argtypes = [vp, vp, vp, vp, u64, i32p]
+        h.oracle_par_spmv_csr_f32.restype = None
+        h.oracle_par_spmv_csr_f32.argtypes = [vp, vp, vp, vp, vp, u64, i32p]
         h.oracle_scan_sum_u64.restype = None
         h.oracle_scan_sum_u64.argtypes = [vp, vp, u64, i32, u64]
         h.oracle_scan_sum_f64.restype = None
@@ -163,6 +176,44 @@ def scan_sum_f64(a: np.ndarray, inclusive: bool = False, init: float = 0.0) -> t
     aout = np.empty(a.size, dtype=np.longdouble)
     lib().oracle_scan_sum_f64(_p(a), _p(out), _p(aout), a.size, int(inclusive), init)
     return out, aout
+
+
+# ---- host baselines (oracle/cpu_baseline.cpp): `threads` std::threads over contiguous chunks ----------
+def par_reduce_sum_i32(a: np.ndarray, threads: int) -> int:
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return int(lib().oracle_par_reduce_sum_i32(_p(a), a.size, threads))
+
+
+def par_scan_sum_u32(a: np.ndarray, threads: int, out: np.ndarray | None = None) -> np.ndarray:
+    src = np.ascontiguousarray(a).view(np.uint32)
+    out = np.empty_like(src) if out is None else out
+    lib().oracle_par_scan_sum_u32(_p(src), _p(out), src.size, threads)
+    return out
+
+
+def par_radix_sort_u32(keys: np.ndarray, threads: int, tmp: np.ndarray | None = None) -> np.ndarray:
+    """Sorts `keys` (uint32) in place, stable LSD with 8-bit digits."""
+    tmp = np.empty_like(keys) if tmp is None else tmp
+    lib().oracle_par_radix_sort_u32(_p(keys), _p(tmp), keys.size, threads)
+    return keys
+
+
+def std_sort_u32(keys: np.ndarray) -> np.ndarray:
+    lib().oracle_std_sort_u32(_p(keys), keys.size)
+    return keys
+
+
+def par_radix_sort_u64_u32(keys: np.ndarray, vals: np.ndarray, threads: int, tmp=None):
+    """Sorts (keys uint64, vals uint32) in place by key, stable."""
+    tk, tv = (np.empty_like(keys), np.empty_like(vals)) if tmp is None else tmp
+    lib().oracle_par_radix_sort_u64_u32(_p(keys), _p(vals), _p(tk), _p(tv), keys.size, threads)
+    return keys, vals
+
+
+def par_spmv_csr_f32(values, row_offsets, cols, x, rows: int, threads: int, y: np.ndarray | None = None) -> np.ndarray:
+    y = np.empty(rows, np.float32) if y is None else y
+    lib().oracle_par_spmv_csr_f32(_p(values), _p(row_offsets), _p(cols), _p(x), _p(y), rows, threads)
+    return y
 
 
 KEY_KINDS = {np.dtype(np.uint32): (4, 0), np.dtype(np.int32): (4, 1), np.dtype(np.float32): (4, 2),

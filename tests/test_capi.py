@@ -9,9 +9,10 @@ REPO = pathlib.Path(__file__).resolve().parents[1]
 HEADER = REPO / "include" / "lcpp_hip.h"
 
 
-def declared_symbols():
+def declared_symbols(*defines):
     """Function names declared in the header, with the declaration macros expanded by the C preprocessor."""
-    out = subprocess.run(["gcc", "-E", "-P", "-x", "c", str(HEADER)], capture_output=True, text=True, check=True)
+    out = subprocess.run(["gcc", "-E", "-P", *defines, "-x", "c", str(HEADER)], capture_output=True, text=True,
+                         check=True)
     return sorted(set(re.findall(r"\b(lcpp_hip_\w+)\s*\(", out.stdout)))
 
 
@@ -28,6 +29,20 @@ def test_library_exports_every_declared_symbol(hip):
     lib = ctypes.CDLL(str(hip.LIB_PATH))
     missing = [s for s in declared_symbols() if not hasattr(lib, s)]
     assert not missing, missing
+
+
+def test_phase_trace_library_exports_its_hook(hip):
+    """The diagnostic build (build.py --phase-trace) exports everything, plus the trace hook; the product
+    library has no trace hook."""
+    import pytest
+    trace = pathlib.Path(hip.LIB_PATH).with_name("liblcpp_hip_trace.so")
+    if not trace.exists():
+        pytest.skip("liblcpp_hip_trace.so is built by __graft_entry__.build() (build.py --phase-trace)")
+    lib = ctypes.CDLL(str(trace))
+    missing = [s for s in declared_symbols("-DLCPP_HIP_PHASE_TRACE") if not hasattr(lib, s)]
+    assert not missing, missing
+    assert hasattr(lib, "lcpp_hip_trace_set_buffer")
+    assert not hasattr(ctypes.CDLL(str(hip.LIB_PATH)), "lcpp_hip_trace_set_buffer")
 
 
 def test_error_reporting_without_gpu(hip):

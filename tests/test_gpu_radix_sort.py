@@ -299,11 +299,12 @@ def test_forced_lookback_fallback(hip, orc, dev, kdtype, vbytes, descending, n):
         lib.lcpp_hip_set_lookback_spin_limit(old)
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("case", ["u32_random", "u64_and3_pairs", "u32_low_entropy_desc", "f32_pairs"])
 def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
-    """Both in-wave rankers (ballot match, LDS lane-mask table) give the stable ranks; low-entropy keys
-    put many lanes of a wave on the same digit entry."""
+    """Every in-wave ranker (ballot match in all waves, LDS lane-mask tables in all waves, and the default
+    split between them) gives the stable ranks; low-entropy keys put many lanes of a wave on the same
+    digit entry."""
     lib = hip.lib()
     n = 500009
     raw = orc.generate(0, n, 4040)
@@ -328,7 +329,7 @@ def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
             check_bits(ko, eko)
             assert np.array_equal(vo, evo)
     finally:
-        lib.lcpp_hip_internal_radix_rank_mode(1)
+        lib.lcpp_hip_internal_radix_rank_mode(2)
 
 
 def test_constant_keys_large(hip, dev):

@@ -744,3 +744,55 @@ def test_segmented_sort_value_order_floats(orc):
     k = np.array([0.0, -0.0, 0.0, -0.0], np.float32)
     ko, _ = orc.segmented_sort(k, [0], [4])
     assert np.signbit(ko).tolist() == [True, True, False, False]
+
+
+# ---- host baselines (oracle/cpu_baseline.cpp) ------------------------------------------------------
+# Each multi-threaded baseline must give the serial oracle's result for every thread count, including
+# thread counts that do not divide n and more threads than items.
+@pytest.mark.parametrize("threads", [1, 2, 3, 8, 17])
+def test_par_reduce_and_scan_match_serial(orc, threads):
+    rng = np.random.default_rng(threads)
+    for n in (0, 1, 5, 1000003):
+        a = rng.integers(-1000, 1001, n).astype(np.int32)
+        assert orc.par_reduce_sum_i32(a, threads) == int(a.astype(np.int64).sum())
+        u = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        assert np.array_equal(orc.par_scan_sum_u32(u, threads), orc.scan_sum_u32(u))
+
+
+@pytest.mark.parametrize("threads", [1, 2, 5, 16])
+def test_par_sorts_match_serial(orc, threads):
+    rng = np.random.default_rng(100 + threads)
+    for n in (1, 7, 300001):
+        k = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        got = orc.par_radix_sort_u32(k.copy(), threads)
+        assert np.array_equal(got, orc.radix_sort(k))
+        assert np.array_equal(orc.std_sort_u32(k.copy()), got)
+        # Pairs with index values and low-entropy keys: stability is visible in the values.
+        k64 = (rng.integers(0, 2**63, n, dtype=np.int64).astype(np.uint64) & np.uint64(0x0101010101010101))
+        v = np.arange(n, dtype=np.uint32)
+        gk, gv = orc.par_radix_sort_u64_u32(k64.copy(), v.copy(), threads)
+        ek, ev = orc.radix_sort(k64, v)
+        assert np.array_equal(gk, ek) and np.array_equal(gv, ev)
+
+
+@pytest.mark.parametrize("threads", [1, 4, 9])
+def test_par_spmv_matches_row_loop(orc, threads):
+    rng = np.random.default_rng(7)
+    rows = cols = 4000
+    lengths = rng.integers(0, 40, rows)
+    lengths[::97] = 0  # empty rows
+    ro = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+    nnz = int(ro[-1])
+    ci = rng.integers(0, cols, nnz).astype(np.int32)
+    av = rng.uniform(-1, 1, nnz).astype(np.float32)
+    xv = rng.uniform(-1, 1, cols).astype(np.float32)
+    y = orc.par_spmv_csr_f32(av, ro, ci, xv, rows, threads)
+    ref = np.zeros(rows, np.float32)
+    for r in range(rows):  # the same float row loop, in order
+        s = np.float32(0)
+        for j in range(ro[r], ro[r + 1]):
+            s = np.float32(s + np.float32(av[j] * xv[ci[j]]))
+        ref[r] = s
+    assert np.array_equal(y, ref)
+    exact, absum = orc.spmv_csr_fp(av, ro, ci, xv, rows, cols, nnz)
+    assert np.all(np.abs(y.astype(np.float64) - exact) <= 1e-5 * np.maximum(np.abs(exact), absum))
