@@ -479,6 +479,9 @@ uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t v
 int lcpp_hip_internal_radix_rank_mode(int mode);
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);
 size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int words, int staged);
+/* 1 when a segmented sort called now on `stream` would use a per-stream device word (eager calls), 0 when
+ * it would not (calls recorded into a graph; a graph may replay on any stream). */
+int lcpp_hip_internal_segsort_uses_stream_slot(void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

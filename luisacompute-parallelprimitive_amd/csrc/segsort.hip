@@ -775,6 +775,12 @@ using namespace lcpp_hip;
 
 extern "C" {
 
+// 1 when a segmented sort called now on `stream` would use a per-stream slot word (an eager call), 0 when
+// it would not (a call recorded into a graph, or past the slot count).
+int lcpp_hip_internal_segsort_uses_stream_slot(void* stream) {
+    return longest_word(static_cast<hipStream_t>(stream)) != nullptr ? 1 : 0;
+}
+
 size_t lcpp_hip_segmented_sort_keys_temp_bytes(uint64_t n, size_t key_bytes) {
     return segsort_temp_bytes(n, key_bytes, 0);
 }

@@ -96,3 +96,31 @@ def test_captured_sequence_replays_match_eager(hip, dev):
         g = b["seg_sorted"].cpu().numpy().view(np.uint32)
         for lo, hi in ((3000, 303_000), (400_000, N)):
             assert np.all(g[lo + 1:hi] >= g[lo:hi - 1])
+
+
+def test_segmented_sort_takes_no_stream_slot_under_capture(hip, dev):
+    """An eager segmented sort uses a per-stream device word for its early exits; a call recorded into a
+    graph must not (the graph may replay on any stream beside eager calls and other replays), so its
+    kernels run without the early exits.  Checked through the library's own query, inside and outside
+    a capture on the same stream."""
+    import ctypes
+    lib = hip.lib()
+    handle = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()) == 1
+    x = torch.ones(5000, dtype=torch.int32, device=dev)
+    y = torch.empty_like(x)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(5000, 4)), dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    seen = []
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        seen.append(lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()))
+        hip.scan_sum("u32", x, y, 5000, temp=temp)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert seen == [0]
+    with torch.cuda.stream(side):
+        assert lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()) == 1
+    assert torch.equal(y, torch.arange(5000, dtype=torch.int32, device=dev))
