@@ -117,6 +117,13 @@ int lcpp_hip_scan_sum_init_f32(void* temp, size_t temp_bytes, const float* in, f
 int lcpp_hip_scan_sum_init_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int64_t init, void* stream);
 int lcpp_hip_scan_sum_init_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, uint64_t init, void* stream);
 int lcpp_hip_scan_sum_init_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, double init, void* stream);
+/* ExclusiveSum over uint32 with no temp argument: the same kernels, with their tile status words in a
+ * static device array of the library (349,528 bytes per GPU, held until the process ends) instead of
+ * caller-provided temp storage, and no allocation of any kind.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under graph capture, allocation-free serving loops).  At most
+ * 2^30 items (larger n returns LCPP_HIP_ERR_INVALID_ARGUMENT).  Every call on one GPU shares the array:
+ * calls that overlap in time on one GPU race (calls in order on one stream are safe). */
+int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * DeviceRadixSort (onesweep, 8-bit digits, stable LSD)

@@ -33,6 +33,8 @@
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
 
+#include <mutex>
+
 namespace lcpp_hip {
 namespace {
 
@@ -385,6 +387,44 @@ int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, boo
     return check_hip(hipGetLastError(), "scan_sum launch");
 }
 
+// ---- ExclusiveSum over uint32 with no temp argument and no allocation ------------------------------
+// The tile status words live in `scratch`, a static device array (each GPU holds its own copy until the
+// process ends).  Host code never uses the array's name as an address: the first call on a device, with
+// that device current, looks up the device's copy with hipGetSymbolAddress and keeps it.  Every call on
+// one GPU shares that copy, so calls that overlap in time on one GPU (other streams, other threads) race;
+// calls in order on one stream do not, since each clears the words it uses (fill kernel) before its scan.
+constexpr uint64_t kNoAllocMaxItems = 1ull << 30;
+constexpr uint64_t kNoAllocWords = (kNoAllocMaxItems + kScanTile<uint32_t> - 1) / kScanTile<uint32_t>;  // 43,691
+static __device__ __align__(256) uint64_t scratch[kNoAllocWords];  // 349,528 bytes per GPU
+
+uint64_t* scratch_of_current_device() {
+    static std::mutex mu;
+    static uint64_t* ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        set_error(kHipError, "ExclusiveSum (no allocation): no current device");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= 64) {
+        set_error(kUnsupported, "ExclusiveSum (no allocation): device index %d out of range", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            set_error(kHipError, "ExclusiveSum (no allocation): hipGetSymbolAddress of the static scratch failed: %s",
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        ptrs[dev] = static_cast<uint64_t*>(p);
+    }
+    return ptrs[dev];
+}
+
 }  // namespace
 
 #ifdef LCPP_HIP_PHASE_TRACE
@@ -430,5 +470,16 @@ LCPP_HIP_DEFINE_SCAN(i64, int64_t, uint64_t)
 LCPP_HIP_DEFINE_SCAN(u64, uint64_t, uint64_t)
 LCPP_HIP_DEFINE_SCAN(f64, double, double)
 #undef LCPP_HIP_DEFINE_SCAN
+
+int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, uint64_t n, void* stream) {
+    if (n > kNoAllocMaxItems)
+        return set_error(kInvalidArgument,
+                         "ExclusiveSum (no allocation): %llu items exceed the static scratch (at most %llu items)",
+                         static_cast<unsigned long long>(n), static_cast<unsigned long long>(kNoAllocMaxItems));
+    if (n == 0) return kOk;
+    uint64_t* words = scratch_of_current_device();
+    if (!words) return kHipError;
+    return scan_sum<uint32_t>(words, kNoAllocWords * sizeof(uint64_t), in, out, n, false, 0u, stream);
+}
 
 }  // extern "C"
