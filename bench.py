@@ -16,7 +16,7 @@ FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `-
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only bykey|compact|reduce|scan|segmented|segsort|sortpairs|spmv]
+                       [--only bykey|compact|reduce|scan|segmented|segsort|sortpairs|spmv|spmv-footprint]
 """
 from __future__ import annotations
 
@@ -368,9 +368,31 @@ def extra_segsort(hip, dev, steps, warmup, extra):
                        "GBps": rate(moved, t.mean), "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+def study_spmv_footprint(hip, dev, steps, warmup, extra):
+    import torch
+    import workloads
+    # CsrMV time against the footprint of x: the same Zipf(1.5) row lengths over 2^20 rows with 2^20,
+    # 2^19, 2^17 and 2^15 columns (x of 4 MB down to 128 KB), so that the x gathers go from missing
+    # the L2 to hitting it (and, at 128 KB, partly the L1) while the streamed matrix bytes stay fixed.
+    # Not part of the default run.
+    rows = 1 << 20
+    for lc in (20, 19, 17, 15):
+        cols = 1 << lc
+        va, ro, ci, xv, nnz = zipf_matrix() if lc == 20 else workloads.zipf_csr(rows, cols, SEED)
+        d = [torch.from_numpy(a).to(dev) for a in (va, ro, ci, xv)]
+        y = torch.empty(rows, dtype=torch.float32, device=dev)
+        call = lambda: hip.spmv_csr("f32", "i32", d[0], d[1], d[2], d[3], y, rows, cols, nnz)
+        t = time_steps(call, steps, warmup)
+        extra[f"spmv_csr_f32_zipf1.5_2p20_x{4 * cols // 1024}KiB"] = {"cols": cols, "nnz": nnz, **t.fields()}
+        del d, y
+        torch.cuda.empty_cache()
+
+
 EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pairs, "spmv": extra_spmv,
           "bykey": extra_by_key, "compact": extra_compact,
           "segmented": extra_segmented, "segsort": extra_segsort}
+# Studies run only when named with --only.
+STUDIES = {"spmv-footprint": study_spmv_footprint}
 
 
 def run_extras(hip, dev, steps, warmup, names, copy=None):
@@ -380,7 +402,7 @@ def run_extras(hip, dev, steps, warmup, names, copy=None):
         if name == "scan":
             extra_scan(hip, dev, steps, warmup, extra, copy)
         else:
-            EXTRAS[name](hip, dev, steps, warmup, extra)
+            {**EXTRAS, **STUDIES}[name](hip, dev, steps, warmup, extra)
         torch.cuda.empty_cache()
     return extra
 
@@ -486,7 +508,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extra", action="store_true", help="headline SortKeys only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=sorted(EXTRAS), default=None,
+    ap.add_argument("--only", choices=sorted(EXTRAS) + sorted(STUDIES), default=None,
                     help="run only this secondary configuration (for profiling); prints its extra entry")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")

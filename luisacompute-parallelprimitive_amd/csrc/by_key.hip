@@ -17,13 +17,13 @@
 // num_runs_out[0] = runs (0 for n == 0).  Integer sums wrap.
 //
 // MI355X design
-//   * Tile = 256 threads x 16 consecutive items per thread (4096 items), read and written as
+//   * Tile = 512 threads x 16 consecutive items per thread (8192 items), read and written as
 //     16-byte vectors when the arrays are 16-byte aligned.  The previous item of a thread's first
 //     item is read from global memory (it sits in the neighbour's cache line).
 //   * State of a span of items: (heads, sum since the last head).  States combine as
 //     (c1, s1) + (c2, s2) = (c1 + c2, c2 ? s2 : s1 + s2), which is associative.  Each thread folds its
 //     items serially; a DPP wave scan (the shared row_shr / row_bcast pattern) and one pass over the
-//     4 wave totals in LDS give each thread its carry-in and the tile its aggregate.
+//     8 wave totals in LDS give each thread its carry-in and the tile its aggregate.
 //   * Tile states are 64-bit words with the status in the low half and 32 payload bits in the high
 //     half.  Reduce-by-key: word 0 holds the head count, words 1.. the sum.  Scan-by-key needs only
 //     a has-head flag, kept beside the status, so its state is just the sum words (one word for
@@ -53,10 +53,12 @@
 namespace lcpp_hip {
 namespace {
 
-constexpr int kBkBlock = 256;
 constexpr int kBkItems = 16;
-constexpr int kBkWaves = kBkBlock / kWave;
-constexpr uint32_t kBkTile = static_cast<uint32_t>(kBkBlock) * kBkItems;  // 4096 items
+// 512 threads: 8192-item tiles halve the tiles (and look-backs) of 256-thread ones at the same items
+// per CU in flight (two workgroups per CU at the register use of the reduce instantiations);
+// ExclusiveSumByKey 2^28 0.906 -> 0.819 ms, ReduceByKey 0.802 -> 0.760 ms, 1024 threads no better.
+constexpr int kBkBlock = 512;
+constexpr uint32_t kBkTile = static_cast<uint32_t>(kBkBlock) * kBkItems;  // 8192 items
 
 constexpr uint32_t kStInvalid = 0;
 constexpr uint32_t kStPartial = 1;
@@ -248,7 +250,7 @@ __device__ __forceinline__ Seg<V> seg_dpp_step(Seg<V> x) {
 
 // Exclusive prefix of each thread's state within the tile, and the tile aggregate.  Called by every
 // thread; leaves `s_wave` free for reuse (barriers on both sides of its use).
-template <typename V>
+template <int BLOCK, typename V>
 __device__ __forceinline__ void block_seg_scan(Seg<V> x, Seg<V>* s_wave, Seg<V>& exclusive, Seg<V>& aggregate) {
     Seg<V> inc = x;
     inc = seg_dpp_step<dpp::kRowShr1>(inc);
@@ -267,7 +269,7 @@ __device__ __forceinline__ void block_seg_scan(Seg<V> x, Seg<V>* s_wave, Seg<V>&
     Seg<V> prefix{0u, V(0)};
     Seg<V> total{0u, V(0)};
 #pragma unroll
-    for (int w = 0; w < kBkWaves; ++w) {
+    for (int w = 0; w < BLOCK / kWave; ++w) {
         if (static_cast<uint32_t>(w) == wave) prefix = total;
         total = seg_combine(total, s_wave[w]);
     }
@@ -276,14 +278,14 @@ __device__ __forceinline__ void block_seg_scan(Seg<V> x, Seg<V>* s_wave, Seg<V>&
 }
 
 // Aggregate of tile `tile`, computed by the whole workgroup exactly as the tile's owner computes it.
-template <typename K, typename V>
+template <int BLOCK, typename K, typename V>
 __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
                                  bool vec_v, Seg<V>* s_wave) {
-    const uint64_t first = static_cast<uint64_t>(tile) * kBkTile + static_cast<uint64_t>(threadIdx.x) * kBkItems;
+    const uint64_t first = static_cast<uint64_t>(tile) * (BLOCK * kBkItems) + static_cast<uint64_t>(threadIdx.x) * kBkItems;
     ThreadItems<K, V> t;
     load_thread(keys, values, n, first, mask, vec_k, vec_v, t);
     Seg<V> ex, agg;
-    block_seg_scan(fold_thread(t, first, n), s_wave, ex, agg);
+    block_seg_scan<BLOCK>(fold_thread(t, first, n), s_wave, ex, agg);
     return agg;
 }
 
@@ -307,8 +309,8 @@ __device__ __forceinline__ void scan_outputs(const ThreadItems<K, V>& t, Seg<V> 
     store_items(values_out, first, n, vec_o, out);
 }
 
-template <typename K, typename V, int MODE>
-__global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ keys, const V* values_in,
+template <int BLOCK, typename K, typename V, int MODE>
+__global__ __launch_bounds__(BLOCK) void by_key_kernel(const K* __restrict__ keys, const V* values_in,
                                                           V* values_out, K* __restrict__ unique_out,
                                                           V* __restrict__ aggregates_out,
                                                           uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
@@ -321,8 +323,8 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
     // The thread that publishes this tile's states and closes its claim word: lane 0 of the last
     // wave.  A wave's vector memory operations complete in issue order, so publishing from wave 0
     // would make its look-back loads wait for the publishing stores and the compare-and-swap.
-    constexpr uint32_t kPublisher = kBkBlock - kWave;
-    __shared__ Seg<V> s_wave[kBkWaves];
+    constexpr uint32_t kPublisher = BLOCK - kWave;
+    __shared__ Seg<V> s_wave[BLOCK / kWave];
     __shared__ uint32_t s_ctl[2][2];  // look-back decision and helped tile, two alternating rows
     __shared__ Seg<V> s_prefix;
 
@@ -330,12 +332,12 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t tile = blockIdx.x;
-    const uint64_t first = static_cast<uint64_t>(tile) * kBkTile + static_cast<uint64_t>(tid) * kBkItems;
+    const uint64_t first = static_cast<uint64_t>(tile) * (BLOCK * kBkItems) + static_cast<uint64_t>(tid) * kBkItems;
 
     ThreadItems<K, V> t;
     load_thread(keys, values_in, n, first, mask, vec_k, vec_v, t);
     Seg<V> in_tile, agg;
-    block_seg_scan(fold_thread(t, first, n), s_wave, in_tile, agg);
+    block_seg_scan<BLOCK>(fold_thread(t, first, n), s_wave, in_tile, agg);
 
     // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
     // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
@@ -441,7 +443,7 @@ __global__ __launch_bounds__(kBkBlock) void by_key_kernel(const K* __restrict__ 
             const bool claimed = s_ctl[row][0] != 0;
             row ^= 1u;
             if (claimed) {
-                const Seg<V> h = tile_aggregate<K, V>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_wave);
+                const Seg<V> h = tile_aggregate<BLOCK, K, V>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_wave);
                 if (tid == 0) {
                     publish_state<V, COUNTED>(slot, kStPartial, h);
                     __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -518,7 +520,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     if (st != kOk) return st;
     const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kBkTile));
     LaunchScope scope(MODE == kModeScan ? "scan_by_key" : "reduce_by_key", stream);
-    by_key_kernel<K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
+    by_key_kernel<kBkBlock, K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
         values_out != nullptr && values_out == values_in, lookback_spin_limit());
@@ -532,7 +534,7 @@ using namespace lcpp_hip;
 
 extern "C" {
 
-// Temp storage the reduce-by-key kernel carves (the larger of the two layouts: per 4096-item tile a
+// Temp storage the reduce-by-key kernel carves (the larger of the two layouts: per 8192-item tile a
 // count word, sizeof(V)/4 sum words and a claim word); never more than the reference's
 // GetScanByKeyTempStorageBytes / GetReduceByKeyTempStorageBytes.
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) { return state_bytes(n, value_bytes, true); }

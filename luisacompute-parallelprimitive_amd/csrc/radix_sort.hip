@@ -651,11 +651,12 @@ struct Geometry {
 // wave's rank is a chain of dependent LDS round trips, and shorter chains on more waves hide them
 // better (SortKeys 2^28 u32 3.04 -> 2.81 ms, SortPairs 2^27 u64 + u32 6.08 -> 5.97 ms on MI355X).
 // 4-byte keys with values keep 512 threads: their keys, values, ranks and output positions do not
-// fit 64 VGPRs.  The window is the widest that compiles without register spills (4 tiles with
-// values at 1024 threads, 8 otherwise; a spilling window runs several times slower).
+// fit 64 VGPRs.  Look-back window (predecessor tiles per step and lane): 32, except 12 for 8-byte keys
+// with values, whose registers are tighter (SortPairs 2^27 u64 + u32: 6.22 ms with 16, 6.16 with 8
+// or 12, slower with 24; a window that spills runs several times slower).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
     if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 16, 32};
-    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 16 : 32};
+    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 12 : 32};
     return Geometry{512, 16, 32};
 }
 

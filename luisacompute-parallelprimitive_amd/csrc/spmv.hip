@@ -11,7 +11,10 @@
 //     value/column loads, then a DPP wave reduction; the row's lane writes y.  Rows longer than
 //     kVecRow read both streams in groups of kGroup consecutive elements per lane (16-byte-aligned
 //     vector loads) when the arrays are 16-byte aligned, cutting the vector memory instructions per
-//     nonzero (the texture addresser, not HBM, limits this kernel).
+//     nonzero, two groups per lane in flight.  The gathers of x bound the kernel: one L1 -> L2
+//     request per nonzero (random columns never share an L1 line), so the texture addresser and the
+//     L2 request rate, not HBM bytes, set its time; with x wholly L2-resident it would still need
+//     one request per nonzero.
 //   Power-law row lengths therefore cost each wave about (longest short row) + sum(long/64) steps,
 //   instead of one 64-lane pass per row.
 // Floating-point order: short rows are summed left to right; other rows as 64 per-lane partial sums
@@ -99,10 +102,38 @@ __global__ __launch_bounds__(kSpmvBlock) void spmv_csr_kernel(const V* __restric
         A part = A(0);
         if (vec_ok && re - rb > kVecRow) {
             // Lane l takes the kGroup-element groups starting at (rb & ~3) + kGroup l, then every
-            // kGroup * kWave elements: 16-byte column and value loads instead of one load per element.
-            // Group elements outside [rb, re) belong to neighbouring rows and are masked; a group
-            // reaching past the arrays' end is loaded element-wise.
-            for (uint32_t g = (rb & ~3u) + kGroup * lane; g < re; g += kGroup * kWave) {
+            // kGroup * kWave elements: 16-byte column and value loads instead of one load per element,
+            // two groups in flight per iteration while both lie before nnz (the partial sum still adds
+            // the groups in order).  Group elements outside [rb, re) belong to neighbouring rows and
+            // are masked; a group reaching past the arrays' end is loaded element-wise.
+            constexpr uint32_t kStride = kGroup * kWave;
+            uint32_t g = (rb & ~3u) + kGroup * lane;
+            // Two groups per lane in flight while both lie wholly before nnz.
+            for (; g + kStride < re && g + kStride + (kGroup - 1) < nnz; g += 2 * kStride) {
+                uint32_t c[2][kGroup];
+                A v[2][kGroup];
+                load_group(column_indices + g, c[0]);
+                load_group(column_indices + g + kStride, c[1]);
+                load_group(values + g, v[0]);
+                load_group(values + g + kStride, v[1]);
+                bool use[2][kGroup];
+                A xv[2][kGroup];
+#pragma unroll
+                for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+                for (uint32_t k = 0; k < kGroup; ++k) {
+                    const uint32_t e = g + h * kStride + k;
+                    use[h][k] = e >= rb && e < re && c[h][k] < cols;
+                    xv[h][k] = use[h][k] ? static_cast<A>(x[c[h][k]]) : A(0);
+                }
+#pragma unroll
+                for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+                for (uint32_t k = 0; k < kGroup; ++k) {
+                    if (use[h][k]) part += v[h][k] * xv[h][k];
+                }
+            }
+            for (; g < re; g += kStride) {
                 uint32_t c[kGroup];
                 A v[kGroup];
                 if (g + (kGroup - 1) < nnz) {
@@ -164,9 +195,9 @@ int spmv_csr(void* /*temp*/, size_t /*temp_bytes*/, const V* values, const I* ro
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (rows > 0xFFFFFFFFull / 32) return set_error(kInvalidArgument, "DeviceSpmv: too many rows");
     if (cols > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceSpmv: too many columns");
-    // 32-bit element indices advance by up to max(kLongUnroll, kGroup) * kWave past a row's end
-    // without wrapping.
-    if (nnz > 0xFFFFFFFFull - (kLongUnroll > kGroup ? kLongUnroll : kGroup) * kWave)
+    // 32-bit element indices run up to 2 * max(kLongUnroll, kGroup) * kWave past a row's end (the
+    // grouped loop tests the group after next) without wrapping.
+    if (nnz > 0xFFFFFFFFull - 4 * (kLongUnroll > kGroup ? kLongUnroll : kGroup) * kWave)
         return set_error(kInvalidArgument, "DeviceSpmv: too many nonzero values");
     if (rows == 0) return kOk;
     if (!y) return set_error(kInvalidArgument, "DeviceSpmv: null output vector");

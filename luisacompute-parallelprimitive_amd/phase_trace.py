@@ -16,7 +16,9 @@ every phase boundary and write one 16-word record per tile (layout in ``csrc/com
 The trace build perturbs what it measures a little (a wait for outstanding memory operations before two
 stamps); the product library has no trace code.
 
-Usage: python luisacompute-parallelprimitive_amd/phase_trace.py [--log2n 28]
+``--pairs`` traces SortPairs of 2^27 uniform u64 keys with u32 values (8 passes) instead.
+
+Usage: python luisacompute-parallelprimitive_amd/phase_trace.py [--log2n 28] [--pairs]
 """
 from __future__ import annotations
 
@@ -98,6 +100,7 @@ def summarize_scan(rec: np.ndarray) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--log2n", type=int, default=28)
+    ap.add_argument("--pairs", action="store_true", help="SortPairs 2^27 u64 + u32 (8 passes) only")
     args = ap.parse_args()
     import torch
     import lcpp_hip as hip
@@ -111,6 +114,30 @@ def main() -> int:
     lib.lcpp_hip_trace_set_buffer.argtypes = [C.c_void_p, C.c_uint64]
 
     dev = torch.device("cuda:0")
+    if args.pairs:
+        m = 1 << 27
+        k = torch.empty(m, dtype=torch.int64, device=dev)
+        hip.generate(hip.GEN_U64, k, m, 114521)
+        v = torch.empty(m, dtype=torch.int32, device=dev)
+        hip.generate(hip.GEN_U32_IOTA, v, m, 0)
+        ko, vo = torch.empty_like(k), torch.empty_like(v)
+        pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32, device=dev)
+        tile = hip.lib().lcpp_hip_radix_tile_items(8, 4)
+        tiles = (m + tile - 1) // tile
+        pbuf = torch.zeros(8 * tiles * WORDS, dtype=torch.int64, device=dev)
+        assert lib.lcpp_hip_trace_set_buffer(None, 0) == 0
+        for _ in range(2):
+            hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt)
+        torch.cuda.synchronize()
+        assert lib.lcpp_hip_trace_set_buffer(C.c_void_p(pbuf.data_ptr()), 8 * tiles) == 0
+        hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt)
+        torch.cuda.synchronize()
+        assert lib.lcpp_hip_trace_set_buffer(None, 0) == 0
+        rec = pbuf.cpu().numpy().view(np.uint64).reshape(-1, WORDS)
+        for p in range(8):
+            print(json.dumps({"workload": "SortPairs 2^27 u64+u32", **summarize_sort(rec[p * tiles:(p + 1) * tiles], p)}),
+                  flush=True)
+        return 0
     n = 1 << args.log2n
     keys = torch.empty(n, dtype=torch.int32, device=dev)
     hip.generate(hip.GEN_U32_HI, keys, n, 114521)

@@ -3,7 +3,7 @@
 Known answers of the reference's tests (device_scan_test.cpp:325-447, device_reduce_test.cpp:420-512)
 exactly; integer values bit-exact against the oracle for every key/value type and scan mode; float
 values within |got - exact| <= rel * (sum of |terms|) with rel 1e-5 (f32) / 1e-12 (f64), where the
-oracle sums in long double.  Also: tile-boundary sizes, runs spanning many 4096-item tiles, in-place
+oracle sums in long double.  Also: tile-boundary sizes, runs spanning many 8192-item tiles, in-place
 scans, the forced look-back fallback (spin limit 0) and misaligned (element-offset) views."""
 import numpy as np
 import pytest
@@ -14,7 +14,7 @@ from gpu_util import fill_dev, log, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 NP = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64, "f64": np.float64}
-TILE = 4096
+TILE = 8192
 
 
 def run_keys(rng, n, mean_len, key_dtype, distinct=1 << 30):
