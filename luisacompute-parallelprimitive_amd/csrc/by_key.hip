@@ -17,13 +17,17 @@
 // num_runs_out[0] = runs (0 for n == 0).  Integer sums wrap.
 //
 // MI355X design
-//   * Tile = 512 threads x 16 consecutive items per thread (8192 items), read and written as
-//     16-byte vectors when the arrays are 16-byte aligned.  The previous item of a thread's first
-//     item is read from global memory (it sits in the neighbour's cache line).
+//   * Tile = 256 threads x R rows x 4 consecutive items per thread and row (R = 16 for 4-byte keys and
+//     values in the scan, 10 in the reduce: 16,384 / 10,240 items; fewer for 8-byte types), every
+//     row a contiguous 1,024 items read (and, for the scan, written) with 16-byte vectors, all rows'
+//     loads in flight together; three workgroups per CU.  The key before a thread-row is the previous
+//     lane's last key (DPP wave shift) or, for lane 0, the last key of the previous wave or row (a
+//     small LDS table).
 //   * State of a span of items: (heads, sum since the last head).  States combine as
-//     (c1, s1) + (c2, s2) = (c1 + c2, c2 ? s2 : s1 + s2), which is associative.  Each thread folds its
-//     items serially; a DPP wave scan (the shared row_shr / row_bcast pattern) and one pass over the
-//     8 wave totals in LDS give each thread its carry-in and the tile its aggregate.
+//     (c1, s1) + (c2, s2) = (c1 + c2, c2 ? s2 : s1 + s2), which is associative.  Each thread folds a
+//     row's 4 items serially, a DPP wave scan (the shared row_shr / row_bcast pattern) per row gives
+//     the lanes' carries, and one more wave scan over the (row, wave) totals gives every (row, wave)
+//     its carry inside the tile and the tile its aggregate.
 //   * Tile states are 64-bit words with the status in the low half and 32 payload bits in the high
 //     half.  Reduce-by-key: word 0 holds the head count, words 1.. the sum.  Scan-by-key needs only
 //     a has-head flag, kept beside the status, so its state is just the sum words (one word for
@@ -35,12 +39,12 @@
 //   * Look-back: wave 0 reads 64 predecessors per step (one per lane).  Ballots find the newest
 //     INCLUSIVE state (or tile 0) and, for the scan, the newest state with a head: the scan stops
 //     there because older sums cannot reach this tile; ReduceByKey continues to an INCLUSIVE state
-//     since run indices need the full head count.  Counts and sums reduce with DPP.
+//     since run indices need the full head count.  Counts and sums reduce with DPP.  Meanwhile the
+//     other waves store the scan outputs that need no prefix (a head lies before them in the tile).
 //   * Forward progress never depends on dispatch order.  Each tile has a claim word (in an array
 //     after the state slots).  A predecessor still unpublished after `spin_limit` polls is claimed
-//     by compare-and-swap
-//     (OPEN -> HELPER), its state computed by the whole waiting workgroup with the owner's own code
-//     (the same float summation order) and published PARTIAL, then the claim is marked DONE with
+//     by compare-and-swap (OPEN -> HELPER), its state computed by the whole waiting workgroup row by
+//     row with the owner's own arithmetic (the same float summation order) and published PARTIAL, then the claim is marked DONE with
 //     release ordering.  The owner closes its claim word (OPEN -> OWNED) right after publishing and
 //     looks at the result only after its look-back; if a helper got there first it waits for DONE
 //     before publishing INCLUSIVE or storing outputs, so no PARTIAL store can land after its
@@ -48,17 +52,34 @@
 // Algorithmic traffic: scan n*(sizeof(K) + 2*sizeof(V)); reduce n*(sizeof(K) + sizeof(V)) plus
 // runs*(sizeof(K) + sizeof(V)) written.
 #include "common.hpp"
+
+#include <algorithm>
 #include "../../include/lcpp_hip.h"
 
 namespace lcpp_hip {
 namespace {
 
-constexpr int kBkItems = 16;
-// 512 threads: 8192-item tiles halve the tiles (and look-backs) of 256-thread ones at the same items
-// per CU in flight (two workgroups per CU at the register use of the reduce instantiations);
-// ExclusiveSumByKey 2^28 0.906 -> 0.819 ms, ReduceByKey 0.802 -> 0.760 ms, 1024 threads no better.
-constexpr int kBkBlock = 512;
-constexpr uint32_t kBkTile = static_cast<uint32_t>(kBkBlock) * kBkItems;  // 8192 items
+constexpr int kBkBlock = 256;
+constexpr int kBkWaves = kBkBlock / kWave;
+constexpr int kBkVec = 4;  // consecutive items per thread and row (one 16-byte vector of 4-byte items)
+// Three workgroups per CU (at most 168 VGPRs), like the scan: one workgroup's look-back wait is
+// covered by the others' loads and stores.
+constexpr int kBkBlocksPerCu = 3;
+// Rows per tile: a thread's keys and values of every row are in flight together (4 * R * (sizeof(K) +
+// sizeof(V)) / 4 VGPRs, 128 for 4-byte keys and values at 16 rows); the scan then keeps only the
+// values, the reduce also the keys it writes out (80 VGPRs of both: 10 rows).  Re-reading the run keys
+// from memory instead, to afford 16 reduce rows, measured slower (ReduceByKey 2^28 0.60 -> 0.89 ms).
+#ifndef LCPP_BK_SCAN_VGPRS
+#define LCPP_BK_SCAN_VGPRS 128
+#endif
+#ifndef LCPP_BK_REDUCE_VGPRS
+#define LCPP_BK_REDUCE_VGPRS 80
+#endif
+template <typename K, typename V, int MODE>
+constexpr int kBkRows = (MODE == 0 ? LCPP_BK_SCAN_VGPRS - (sizeof(V) == 8 ? 16 : 0) : LCPP_BK_REDUCE_VGPRS) /
+                        static_cast<int>(sizeof(K) + sizeof(V));
+template <typename K, typename V, int MODE>
+constexpr uint32_t kBkTileItems = static_cast<uint32_t>(kBkBlock * kBkVec * kBkRows<K, V, MODE>);
 
 constexpr uint32_t kStInvalid = 0;
 constexpr uint32_t kStPartial = 1;
@@ -103,8 +124,8 @@ template <typename V, bool COUNTED>
 constexpr int kStateWords = (COUNTED ? 1 : 0) + kValueWords<V>;
 
 // Temp layout: tiles x state words, then one claim word per tile.
-size_t state_bytes(uint64_t n, size_t value_bytes, bool counted) {
-    return ceil_div(n, kBkTile) * ((counted ? 2 : 1) + value_bytes / 4) * sizeof(uint64_t);
+size_t state_bytes(uint64_t n, uint32_t tile_items, size_t value_bytes, bool counted) {
+    return ceil_div(n, tile_items) * ((counted ? 2 : 1) + value_bytes / 4) * sizeof(uint64_t);
 }
 
 constexpr uint32_t kStatusMask = 3;
@@ -164,80 +185,6 @@ __device__ __forceinline__ uint32_t read_state(const uint64_t* slot, Seg<V>& s) 
     return ok ? st : kStInvalid;
 }
 
-template <typename T>
-struct alignas(16) Run16 {
-    T v[kBkItems];
-};
-
-// The 16 items [first, first + 16) of `p` (0 past n): one 64/128-byte vector load when aligned.
-template <typename T>
-__device__ __forceinline__ void load_items(const T* p, uint64_t first, uint64_t n, bool vec, T (&out)[kBkItems]) {
-    if (vec && first + kBkItems <= n) {
-        const Run16<T> r = *reinterpret_cast<const Run16<T>*>(p + first);
-#pragma unroll
-        for (int k = 0; k < kBkItems; ++k) out[k] = r.v[k];
-    } else {
-#pragma unroll
-        for (int k = 0; k < kBkItems; ++k) out[k] = first + k < n ? p[first + k] : T(0);
-    }
-}
-
-template <typename T>
-__device__ __forceinline__ void store_items(T* p, uint64_t first, uint64_t n, bool vec, const T (&in)[kBkItems]) {
-    if (vec && first + kBkItems <= n) {
-        Run16<T> r;
-#pragma unroll
-        for (int k = 0; k < kBkItems; ++k) r.v[k] = in[k];
-        *reinterpret_cast<Run16<T>*>(p + first) = r;
-    } else {
-#pragma unroll
-        for (int k = 0; k < kBkItems; ++k) {
-            if (first + k < n) p[first + k] = in[k];
-        }
-    }
-}
-
-template <typename K, typename V>
-struct ThreadItems {
-    K key[kBkItems];
-    V val[kBkItems];
-    uint32_t heads;  // bit k: item k starts a run
-};
-
-template <typename K, typename V>
-__device__ __forceinline__ void load_thread(const K* keys, const V* values, uint64_t n, uint64_t first, K mask,
-                                            bool vec_k, bool vec_v, ThreadItems<K, V>& t) {
-    load_items(keys, first, n, vec_k, t.key);
-    load_items(values, first, n, vec_v, t.val);
-    K prev = (first > 0 && first - 1 < n) ? keys[first - 1] : K(0);
-    uint32_t heads = 0;
-#pragma unroll
-    for (int k = 0; k < kBkItems; ++k) {
-        const uint64_t i = first + k;
-        const bool head = i < n && (i == 0 || ((t.key[k] ^ prev) & mask) != 0);
-        heads |= (head ? 1u : 0u) << k;
-        prev = t.key[k];
-    }
-    t.heads = heads;
-}
-
-template <typename K, typename V>
-__device__ __forceinline__ Seg<V> fold_thread(const ThreadItems<K, V>& t, uint64_t first, uint64_t n) {
-    Seg<V> s{0u, V(0)};
-#pragma unroll
-    for (int k = 0; k < kBkItems; ++k) {
-        if (first + k < n) {
-            if ((t.heads >> k) & 1u) {
-                s.count += 1;
-                s.sum = t.val[k];
-            } else {
-                s.sum = static_cast<V>(s.sum + t.val[k]);
-            }
-        }
-    }
-    return s;
-}
-
 // One step of the wave scan: combine with the state DPP brings from an older lane (identity where
 // the pattern has no source).
 template <int CTRL, int ROW_MASK = 0xf, typename V>
@@ -248,96 +195,253 @@ __device__ __forceinline__ Seg<V> seg_dpp_step(Seg<V> x) {
     return seg_combine(o, x);
 }
 
-// Exclusive prefix of each thread's state within the tile, and the tile aggregate.  Called by every
-// thread; leaves `s_wave` free for reuse (barriers on both sides of its use).
-template <int BLOCK, typename V>
-__device__ __forceinline__ void block_seg_scan(Seg<V> x, Seg<V>* s_wave, Seg<V>& exclusive, Seg<V>& aggregate) {
-    Seg<V> inc = x;
-    inc = seg_dpp_step<dpp::kRowShr1>(inc);
-    inc = seg_dpp_step<dpp::kRowShr2>(inc);
-    inc = seg_dpp_step<dpp::kRowShr4>(inc);
-    inc = seg_dpp_step<dpp::kRowShr8>(inc);
-    inc = seg_dpp_step<dpp::kRowBcast15, 0xa>(inc);
-    inc = seg_dpp_step<dpp::kRowBcast31, 0xc>(inc);
-    Seg<V> ex;
-    ex.count = dpp_move_u32<dpp::kWaveShr1>(0u, inc.count);
-    ex.sum = dpp_move<dpp::kWaveShr1>(V(0), inc.sum);
-    const uint32_t wave = threadIdx.x / kWave;
-    __syncthreads();  // earlier readers of s_wave are done
-    if (lane_id() == kWave - 1) s_wave[wave] = inc;
-    __syncthreads();
-    Seg<V> prefix{0u, V(0)};
-    Seg<V> total{0u, V(0)};
-#pragma unroll
-    for (int w = 0; w < BLOCK / kWave; ++w) {
-        if (static_cast<uint32_t>(w) == wave) prefix = total;
-        total = seg_combine(total, s_wave[w]);
-    }
-    exclusive = seg_combine(prefix, ex);
-    aggregate = total;
+// Inclusive scan of a segmented state over the 64 lanes of a wave (row_shr / row_bcast pattern).
+template <typename V>
+__device__ __forceinline__ Seg<V> wave_seg_scan(Seg<V> x) {
+    x = seg_dpp_step<dpp::kRowShr1>(x);
+    x = seg_dpp_step<dpp::kRowShr2>(x);
+    x = seg_dpp_step<dpp::kRowShr4>(x);
+    x = seg_dpp_step<dpp::kRowShr8>(x);
+    x = seg_dpp_step<dpp::kRowBcast15, 0xa>(x);
+    x = seg_dpp_step<dpp::kRowBcast31, 0xc>(x);
+    return x;
 }
 
-// Aggregate of tile `tile`, computed by the whole workgroup exactly as the tile's owner computes it.
-template <int BLOCK, typename K, typename V>
-__device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
-                                 bool vec_v, Seg<V>* s_wave) {
-    const uint64_t first = static_cast<uint64_t>(tile) * (BLOCK * kBkItems) + static_cast<uint64_t>(threadIdx.x) * kBkItems;
-    ThreadItems<K, V> t;
-    load_thread(keys, values, n, first, mask, vec_k, vec_v, t);
-    Seg<V> ex, agg;
-    block_seg_scan<BLOCK>(fold_thread(t, first, n), s_wave, ex, agg);
+// The previous lane's inclusive state (identity in lane 0).
+template <typename V>
+__device__ __forceinline__ Seg<V> wave_seg_exclusive(Seg<V> inclusive) {
+    Seg<V> e;
+    e.count = dpp_move_u32<dpp::kWaveShr1>(0u, inclusive.count);
+    e.sum = dpp_move<dpp::kWaveShr1>(V(0), inclusive.sum);
+    return e;
+}
+
+template <typename T>
+struct alignas(16) Quad {
+    T v[kBkVec];
+};
+
+// Items [first, first + 4) of `p`, in range, 16-byte aligned: one (or, for 8-byte items, two) vector loads.
+template <typename T>
+__device__ __forceinline__ void load_quad_vec(const T* p, uint64_t first, T (&out)[kBkVec]) {
+    typedef T Vec __attribute__((ext_vector_type(kBkVec), aligned(16)));
+    const Vec q = __builtin_nontemporal_load(reinterpret_cast<const Vec*>(p + first));
+#pragma unroll
+    for (int k = 0; k < kBkVec; ++k) out[k] = q[k];
+}
+
+// Items [first, first + 4) of `p`, 0 past n, any alignment.
+template <typename T>
+__device__ __forceinline__ void load_quad_any(const T* p, uint64_t first, uint64_t n, T (&out)[kBkVec]) {
+#pragma unroll
+    for (int k = 0; k < kBkVec; ++k) out[k] = first + k < n ? p[first + k] : T(0);
+}
+
+template <typename T>
+__device__ __forceinline__ void load_quad(const T* p, uint64_t first, uint64_t n, bool vec, T (&out)[kBkVec]) {
+    if (vec && first + kBkVec <= n) load_quad_vec(p, first, out);
+    else load_quad_any(p, first, n, out);
+}
+
+// Stores the items of `valid` (bit k: item first + k exists) of a thread-row: one vector store when all
+// four exist and the array is 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void store_quad(T* p, uint64_t first, uint32_t valid, bool vec, const T (&in)[kBkVec]) {
+    if (vec && valid == 0xFu) {
+        Quad<T> q;
+#pragma unroll
+        for (int k = 0; k < kBkVec; ++k) q.v[k] = in[k];
+        *reinterpret_cast<Quad<T>*>(p + first) = q;
+    } else {
+#pragma unroll
+        for (int k = 0; k < kBkVec; ++k) {
+            if ((valid >> k) & 1u) p[first + k] = in[k];
+        }
+    }
+}
+
+// Bit k set when item first + k < n.
+__device__ __forceinline__ uint32_t quad_valid(uint64_t first, uint64_t n) {
+    return first >= n ? 0u : (n - first >= kBkVec ? 0xFu : (1u << static_cast<uint32_t>(n - first)) - 1u);
+}
+
+// Head bits (bit k: item first + k starts a run) of a thread-row, given the key before it; `at_start`:
+// the row's first item is item 0.
+template <typename K>
+__device__ __forceinline__ uint32_t quad_heads(const K (&key)[kBkVec], K prev, uint32_t valid, bool at_start, K mask) {
+    uint32_t heads = 0;
+#pragma unroll
+    for (int k = 0; k < kBkVec; ++k) {
+        const bool head = (k == 0 && at_start) || ((key[k] ^ prev) & mask) != 0;
+        heads |= (head ? 1u : 0u) << k;
+        prev = key[k];
+    }
+    return heads & valid;
+}
+
+// State of a thread-row: its items folded in order.
+template <typename V>
+__device__ __forceinline__ Seg<V> fold_quad(const V (&val)[kBkVec], uint32_t heads, uint32_t valid) {
+    Seg<V> s{0u, V(0)};
+#pragma unroll
+    for (int k = 0; k < kBkVec; ++k) {
+        const bool head = (heads >> k) & 1u;
+        const V x = ((valid >> k) & 1u) ? val[k] : V(0);
+        s.count += head ? 1u : 0u;
+        s.sum = head ? x : static_cast<V>(s.sum + x);
+    }
+    return s;
+}
+
+// Item index of thread `tid`'s first item in row r of a tile.
+template <int R>
+__device__ __forceinline__ uint64_t row_first(uint32_t tile, int r, uint32_t tid) {
+    return static_cast<uint64_t>(tile) * (kBkBlock * kBkVec * R) + static_cast<uint64_t>(r) * (kBkBlock * kBkVec) +
+           static_cast<uint64_t>(tid) * kBkVec;
+}
+
+// Carries and aggregate from the (row, wave) totals, by wave 0: lane l takes total l (row l / 4, wave
+// l % 4; R * 4 <= 64), one wave scan gives every (row, wave) its in-tile carry (the totals before it, in
+// row-major order), written back over the table, and lane 63 the tile aggregate, which wave 0 returns.
+template <typename V, int R>
+__device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
+    static_assert(R * kBkWaves <= kWave, "one wave scans the (row, wave) totals");
+    const uint32_t lane = lane_id();
+    Seg<V>* flat = &s_wave[0][0];
+    const Seg<V> t = lane < static_cast<uint32_t>(R * kBkWaves) ? flat[lane] : Seg<V>{0u, V(0)};
+    const Seg<V> incl = wave_seg_scan(t);
+    if (lane < static_cast<uint32_t>(R * kBkWaves)) flat[lane] = wave_seg_exclusive(incl);
+    Seg<V> agg;
+    agg.count = wave_read_lane(incl.count, kWave - 1);
+    agg.sum = wave_read_lane(incl.sum, kWave - 1);
     return agg;
 }
 
-// Scan outputs of a thread's items from the state carried into its first item.
-template <typename K, typename V>
-__device__ __forceinline__ void scan_outputs(const ThreadItems<K, V>& t, Seg<V> run, int inclusive, int use_init, V init,
-                                             V* values_out, uint64_t first, uint64_t n, bool vec_o) {
-    V out[kBkItems];
+// Aggregate of tile `tile`, computed by the whole workgroup with the owner's own arithmetic (same
+// heads, folds, wave scans and combination order, so float sums match bit for bit).  Row by row, with
+// the key before each thread-row read from memory, to keep the helper's registers small.
+template <typename K, typename V, int R>
+__device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
+                                 bool vec_v, Seg<V> (*s_help)[kBkWaves]) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid / kWave;
+#pragma unroll 1
+    for (int r = 0; r < R; ++r) {
+        const uint64_t first = row_first<R>(tile, r, tid);
+        K key[kBkVec];
+        V val[kBkVec];
+        load_quad(keys, first, n, vec_k, key);
+        load_quad(values, first, n, vec_v, val);
+        const K prev = (first > 0 && first - 1 < n) ? keys[first - 1] : K(0);
+        const uint32_t valid = quad_valid(first, n);
+        const Seg<V> incl = wave_seg_scan(fold_quad(val, quad_heads(key, prev, valid, first == 0, mask), valid));
+        if (lane_id() == kWave - 1) s_help[r][wave] = incl;
+    }
+    __syncthreads();
+    // Only thread 0 publishes the helped state, so wave 0's result is all that is needed.
+    Seg<V> agg{0u, V(0)};
+    if (wave == 0) agg = scan_totals<V, R>(s_help);
+    __syncthreads();  // s_help is free again
+    return agg;
+}
+
+// Outputs of one thread-row of a scan from the state carried into its first item.
+template <typename V>
+__device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32_t heads, Seg<V> run, int inclusive,
+                                                  int use_init, V init, V* values_out, uint64_t first, uint32_t valid,
+                                                  bool vec_o) {
+    V out[kBkVec];
 #pragma unroll
-    for (int k = 0; k < kBkItems; ++k) {
-        const bool head = (t.heads >> k) & 1u;
+    for (int k = 0; k < kBkVec; ++k) {
+        const bool head = (heads >> k) & 1u;
         if (!inclusive) out[k] = head ? init : static_cast<V>(init + run.sum);
         if (head) {
             run.count += 1;
-            run.sum = t.val[k];
+            run.sum = val[k];
         } else {
-            run.sum = static_cast<V>(run.sum + t.val[k]);
+            run.sum = static_cast<V>(run.sum + val[k]);
         }
         if (inclusive) out[k] = use_init ? static_cast<V>(init + run.sum) : run.sum;
     }
-    store_items(values_out, first, n, vec_o, out);
+    store_quad(values_out, first, valid, vec_o, out);
 }
 
-template <int BLOCK, typename K, typename V, int MODE>
-__global__ __launch_bounds__(BLOCK) void by_key_kernel(const K* __restrict__ keys, const V* values_in,
-                                                          V* values_out, K* __restrict__ unique_out,
-                                                          V* __restrict__ aggregates_out,
-                                                          uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
-                                                          uint64_t* __restrict__ states, int inclusive, int use_init,
-                                                          V init, bool vec_k, bool vec_v, bool vec_o,
-                                                          bool in_place, uint32_t spin_limit) {
+template <typename K, typename V, int MODE, int R>
+__global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
+    const K* __restrict__ keys, const V* values_in, V* values_out, K* __restrict__ unique_out,
+    V* __restrict__ aggregates_out, uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
+    uint64_t* __restrict__ states, int inclusive, int use_init, V init, bool vec_k, bool vec_v, bool vec_o,
+    bool in_place, uint32_t spin_limit) {
     constexpr bool COUNTED = MODE == kModeReduce;
     constexpr int W = kStateWords<V, COUNTED>;
     uint64_t* const claims = states + static_cast<uint64_t>(gridDim.x) * W;
     // The thread that publishes this tile's states and closes its claim word: lane 0 of the last
     // wave.  A wave's vector memory operations complete in issue order, so publishing from wave 0
     // would make its look-back loads wait for the publishing stores and the compare-and-swap.
-    constexpr uint32_t kPublisher = BLOCK - kWave;
-    __shared__ Seg<V> s_wave[BLOCK / kWave];
-    __shared__ uint32_t s_ctl[2][2];  // look-back decision and helped tile, two alternating rows
+    constexpr uint32_t kPublisher = kBkBlock - kWave;
+    __shared__ Seg<V> s_wave[R][kBkWaves];  // (row, wave) totals of this tile, then their in-tile carries
+    __shared__ Seg<V> s_help[R][kBkWaves];  // the same for a tile this workgroup computes as a helper
+    __shared__ K s_edge[R][kBkWaves];       // last key of each (row, wave)
+    __shared__ uint32_t s_ctl[2][2];        // look-back decision and helped tile, two alternating rows
     __shared__ Seg<V> s_prefix;
+    __shared__ Seg<V> s_agg;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
     const uint32_t wave = tid / kWave;
     const uint32_t tile = blockIdx.x;
-    const uint64_t first = static_cast<uint64_t>(tile) * (BLOCK * kBkItems) + static_cast<uint64_t>(tid) * kBkItems;
+    const uint64_t tile_base = static_cast<uint64_t>(tile) * (kBkBlock * kBkVec * R);
 
-    ThreadItems<K, V> t;
-    load_thread(keys, values_in, n, first, mask, vec_k, vec_v, t);
-    Seg<V> in_tile, agg;
-    block_seg_scan<BLOCK>(fold_thread(t, first, n), s_wave, in_tile, agg);
+    // Load every row (row r: 4 KiB of keys and of values per 1,024 items, thread t the t-th quad).  A
+    // full, aligned tile takes only unconditional vector loads, so all of them are in flight together.
+    constexpr uint32_t TILE = kBkBlock * kBkVec * R;
+    const bool full = vec_k && vec_v && tile_base + TILE <= n;
+    K key[R][kBkVec];
+    V val[R][kBkVec];
+    if (full) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            load_quad_vec(keys, row_first<R>(tile, r, tid), key[r]);
+            load_quad_vec(values_in, row_first<R>(tile, r, tid), val[r]);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            load_quad_any(keys, row_first<R>(tile, r, tid), n, key[r]);
+            load_quad_any(values_in, row_first<R>(tile, r, tid), n, val[r]);
+        }
+    }
+    const K before_tile = (tid == 0 && tile_base > 0) ? keys[tile_base - 1] : K(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (lane == kWave - 1) s_edge[r][wave] = key[r][kBkVec - 1];
+    }
+    __syncthreads();
+
+    // Heads (the key before a thread-row: the previous lane's last key, across waves and rows through
+    // the edge table), folds and per-row wave scans.
+    uint32_t heads[(R + 7) / 8];  // four bits per row
+#pragma unroll
+    for (int i = 0; i < (R + 7) / 8; ++i) heads[i] = 0;
+    Seg<V> incl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        K prev = dpp_move<dpp::kWaveShr1>(K(0), key[r][kBkVec - 1]);
+        if (lane == 0) prev = wave > 0 ? s_edge[r][wave - 1] : (r > 0 ? s_edge[r - 1][kBkWaves - 1] : before_tile);
+        const uint32_t valid = full ? 0xFu : quad_valid(row_first<R>(tile, r, tid), n);
+        const uint32_t h = quad_heads(key[r], prev, valid, tile == 0 && r == 0 && tid == 0, mask);
+        heads[r / 8] |= h << (4 * (r % 8));
+        incl[r] = wave_seg_scan(fold_quad(val[r], h, valid));
+        if (lane == kWave - 1) s_wave[r][wave] = incl[r];
+    }
+    __syncthreads();
+    // Wave 0 turns the totals into in-tile carries and the aggregate (to LDS for the publisher).
+    if (wave == 0) {
+        const Seg<V> a = scan_totals<V, R>(s_wave);
+        if (lane == 0) s_agg = a;
+    }
+    __syncthreads();
+    const Seg<V> agg = s_agg;
 
     // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
     // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
@@ -352,15 +456,26 @@ __global__ __launch_bounds__(BLOCK) void by_key_kernel(const K* __restrict__ key
                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // Scan outputs that do not depend on the tile's prefix (a run starts in this tile before or at the
-    // thread's first item) are stored now, after the publish and by waves other than wave 0, so they
-    // overlap the look-back without delaying the publish or wave 0's look-back loads (a wave's
-    // vector memory operations complete in issue order).  Not for in-place scans: their input may
-    // still be read by a helper until the claim is settled.
-    bool early = false;
+    // In-tile carry into each thread-row: rows before it, waves before it in its row, lanes before it.
+    // Scan outputs whose carry already holds a head (or whose first item is one) do not depend on the
+    // tile's prefix; waves other than wave 0 store them now, while wave 0 walks the look-back (a
+    // wave's vector memory operations complete in issue order).  Not for in-place scans: their input
+    // may still be read by a helper until the claim is settled.
+    uint32_t stored = 0;  // rows already stored
     if constexpr (MODE == kModeScan) {
-        early = !in_place && wave != 0 && (in_tile.count != 0 || (t.heads & 1u) != 0);
-        if (early) scan_outputs(t, in_tile, inclusive, use_init, init, values_out, first, n, vec_o);
+        if (!in_place && wave != 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const Seg<V> carry = seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r]));
+                const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
+                if (carry.count != 0 || (h & 1u) != 0) {
+                    const uint64_t first = row_first<R>(tile, r, tid);
+                    scan_quad_outputs(val[r], h, carry, inclusive, use_init, init, values_out, first,
+                                      full ? 0xFu : quad_valid(first, n), vec_o);
+                    stored |= 1u << r;
+                }
+            }
+        }
     }
 
     Seg<V> prefix{0u, V(0)};
@@ -443,7 +558,7 @@ __global__ __launch_bounds__(BLOCK) void by_key_kernel(const K* __restrict__ key
             const bool claimed = s_ctl[row][0] != 0;
             row ^= 1u;
             if (claimed) {
-                const Seg<V> h = tile_aggregate<BLOCK, K, V>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_wave);
+                const Seg<V> h = tile_aggregate<K, V, R>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_help);
                 if (tid == 0) {
                     publish_state<V, COUNTED>(slot, kStPartial, h);
                     __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -463,32 +578,39 @@ __global__ __launch_bounds__(BLOCK) void by_key_kernel(const K* __restrict__ key
                 __builtin_amdgcn_s_sleep(1);
         }
         if (tile > 0 || !owned) {
-            const Seg<V> incl = seg_combine(prefix, agg);
-            publish_state<V, COUNTED>(my_slot, kStInclusive, incl);
+            const Seg<V> incl_state = seg_combine(prefix, agg);
+            publish_state<V, COUNTED>(my_slot, kStInclusive, incl_state);
         }
     }
     __syncthreads();  // outputs only after the claim is settled
 
-    Seg<V> run = seg_combine(prefix, in_tile);
-    if constexpr (MODE == kModeScan) {
-        if (!early) scan_outputs(t, run, inclusive, use_init, init, values_out, first, n, vec_o);
-    } else {
 #pragma unroll
-        for (int k = 0; k < kBkItems; ++k) {
-            if (first + k < n) {
-                if ((t.heads >> k) & 1u) {
-                    if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
-                    unique_out[run.count] = t.key[k];
-                    run.count += 1;
-                    run.sum = t.val[k];
-                } else {
-                    run.sum = static_cast<V>(run.sum + t.val[k]);
+    for (int r = 0; r < R; ++r) {
+        Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r])));
+        const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
+        const uint64_t first = row_first<R>(tile, r, tid);
+        const uint32_t valid = full ? 0xFu : quad_valid(first, n);
+        if constexpr (MODE == kModeScan) {
+            if (((stored >> r) & 1u) == 0)
+                scan_quad_outputs(val[r], h, run, inclusive, use_init, init, values_out, first, valid, vec_o);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kBkVec; ++k) {
+                if ((valid >> k) & 1u) {
+                    if ((h >> k) & 1u) {
+                        if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
+                        unique_out[run.count] = key[r][k];
+                        run.count += 1;
+                        run.sum = val[r][k];
+                    } else {
+                        run.sum = static_cast<V>(run.sum + val[r][k]);
+                    }
                 }
             }
-        }
-        if (first < n && n - first <= kBkItems) {  // this thread holds the last item
-            aggregates_out[run.count - 1] = run.sum;
-            num_runs_out[0] = run.count;
+            if (valid != 0 && n - first <= kBkVec) {  // this thread-row holds the last item
+                aggregates_out[run.count - 1] = run.sum;
+                num_runs_out[0] = run.count;
+            }
         }
     }
 }
@@ -511,16 +633,17 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
         if (!values_out) return set_error(kInvalidArgument, "%s: null output", what);
     }
     if (!keys || !values_in) return set_error(kInvalidArgument, "%s: null input", what);
-    const size_t need = state_bytes(n, sizeof(V), MODE == kModeReduce);
+    constexpr uint32_t kTile = kBkTileItems<K, V, MODE>;
+    const size_t need = state_bytes(n, kTile, sizeof(V), MODE == kModeReduce);
     if (!temp || temp_bytes < need)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, need);
     if (reinterpret_cast<uintptr_t>(temp) % 8 != 0) return set_error(kInvalidArgument, "%s: temp not 8-byte aligned", what);
     uint64_t* states = static_cast<uint64_t*>(temp);
     int st = launch_fill_u32(reinterpret_cast<uint32_t*>(states), need / 4, 0u, stream);
     if (st != kOk) return st;
-    const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kBkTile));
+    const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kTile));
     LaunchScope scope(MODE == kModeScan ? "scan_by_key" : "reduce_by_key", stream);
-    by_key_kernel<kBkBlock, K, V, MODE><<<tiles, kBkBlock, 0, stream>>>(
+    by_key_kernel<K, V, MODE, kBkRows<K, V, MODE>><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
         values_out != nullptr && values_out == values_in, lookback_spin_limit());
@@ -534,10 +657,18 @@ using namespace lcpp_hip;
 
 extern "C" {
 
-// Temp storage the reduce-by-key kernel carves (the larger of the two layouts: per 8192-item tile a
-// count word, sizeof(V)/4 sum words and a claim word); never more than the reference's
-// GetScanByKeyTempStorageBytes / GetReduceByKeyTempStorageBytes.
-size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) { return state_bytes(n, value_bytes, true); }
+// Temp storage the by-key kernels carve for values of `value_bytes`, whatever the key width and mode:
+// the reduce layout (per tile a count word, sizeof(V)/4 sum words and a claim word) at the smallest
+// tile of those instantiations; never more than the reference's GetScanByKeyTempStorageBytes /
+// GetReduceByKeyTempStorageBytes.
+size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes) {
+    const uint32_t tile = value_bytes == 8
+                              ? std::min({kBkTileItems<uint32_t, uint64_t, kModeScan>, kBkTileItems<uint64_t, uint64_t, kModeScan>,
+                                          kBkTileItems<uint32_t, uint64_t, kModeReduce>, kBkTileItems<uint64_t, uint64_t, kModeReduce>})
+                              : std::min({kBkTileItems<uint32_t, uint32_t, kModeScan>, kBkTileItems<uint64_t, uint32_t, kModeScan>,
+                                          kBkTileItems<uint32_t, uint32_t, kModeReduce>, kBkTileItems<uint64_t, uint32_t, kModeReduce>});
+    return state_bytes(n, tile, value_bytes, true);
+}
 
 #define LCPP_HIP_DEFINE_BY_KEY(KS, KT, KU, VS, VT, VU)                                                                 \
     int lcpp_hip_scan_by_key_sum_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in,      \

@@ -3,7 +3,7 @@
 Known answers of the reference's tests (device_scan_test.cpp:325-447, device_reduce_test.cpp:420-512)
 exactly; integer values bit-exact against the oracle for every key/value type and scan mode; float
 values within |got - exact| <= rel * (sum of |terms|) with rel 1e-5 (f32) / 1e-12 (f64), where the
-oracle sums in long double.  Also: tile-boundary sizes, runs spanning many 8192-item tiles, in-place
+oracle sums in long double.  Also: tile-boundary sizes (the scan's 16,384-item and the reduce's 10,240-item tiles of 4-byte keys and values), runs spanning many tiles, in-place
 scans, the forced look-back fallback (spin limit 0) and misaligned (element-offset) views."""
 import numpy as np
 import pytest
@@ -14,7 +14,8 @@ from gpu_util import fill_dev, log, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 NP = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64, "f64": np.float64}
-TILE = 8192
+TILE = 16384         # scan tile, 4-byte keys and values
+REDUCE_TILE = 10240  # reduce tile, 4-byte keys and values
 
 
 def run_keys(rng, n, mean_len, key_dtype, distinct=1 << 30):
@@ -162,7 +163,9 @@ def test_reduce_by_key_types(hip, orc, dev, ks, vs):
     check_reduce(orc, keys, vals, uniq, agg, runs, vs, -1)
 
 
-@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 255, 256, 257, TILE - 1, TILE, TILE + 1, 2 * TILE + 1, 64 * TILE + 3])
+@pytest.mark.parametrize("n", [1, 2, 15, 16, 17, 255, 256, 257, 1023, 1024, 1025, REDUCE_TILE - 1, REDUCE_TILE,
+                               REDUCE_TILE + 1, 2 * REDUCE_TILE + 1, TILE - 1, TILE, TILE + 1, 2 * TILE + 1,
+                               64 * TILE + 3])
 def test_tile_boundary_sizes(hip, orc, dev, n):
     rng = np.random.default_rng(n)
     keys = run_keys(rng, n, 3.0, np.int32)
