@@ -95,46 +95,52 @@ struct Reducer {
     }
 };
 
-template <typename T>
-__device__ __forceinline__ T shfl_xor_any(T v, int mask) {
-    if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, __shfl_xor(__builtin_bit_cast(int, v), mask));
-    } else {
-        const uint64_t u = __builtin_bit_cast(uint64_t, v);
-        const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u)), mask));
-        const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(u >> 32)), mask));
-        return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
-    }
-}
-
-// Lane `src`'s value of v, for 32- and 64-bit types.
+// Lane `src`'s value of v (src the same in every lane), for 32- and 64-bit types, as a scalar read.
 template <typename T>
 __device__ __forceinline__ T read_lane_any(T v, int src) {
     if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, __shfl(__builtin_bit_cast(int, v), src));
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), src));
     } else {
         const uint64_t u = __builtin_bit_cast(uint64_t, v);
-        const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(u)), src));
-        const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(u >> 32)), src));
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), src);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), src);
         return __builtin_bit_cast(T, (static_cast<uint64_t>(hi) << 32) | lo);
     }
 }
 
+// One DPP step of the wave reduction: combine with the accumulator of the lane the pattern names
+// (the identity where it names none).
+template <int CTRL, int ROW_MASK, typename T, int OP>
+__device__ __forceinline__ typename Reducer<T, OP>::Acc dpp_combine(typename Reducer<T, OP>::Acc x) {
+    using R = Reducer<T, OP>;
+    const typename R::Acc id = R::identity();
+    typename R::Acc o;
+    if constexpr (OP == kOpArgMin || OP == kOpArgMax) {
+        o.value = dpp_move<CTRL, ROW_MASK>(id.value, x.value);
+        o.index = dpp_move_u32<CTRL, ROW_MASK>(id.index, x.index);
+    } else {
+        o = dpp_move<CTRL, ROW_MASK>(id, x);
+    }
+    return R::combine(x, o);
+}
+
+// Reduction over the 64 lanes, the result in every lane: the row_shr / row_bcast scan pattern on the
+// DPP datapath (no LDS traffic) leaves the total in lane 63, which is then read into a scalar.
 template <typename T, int OP>
 __device__ __forceinline__ typename Reducer<T, OP>::Acc wave_combine(typename Reducer<T, OP>::Acc x) {
-    using R = Reducer<T, OP>;
-#pragma unroll
-    for (int off = kWave / 2; off >= 1; off >>= 1) {
-        if constexpr (OP == kOpArgMin || OP == kOpArgMax) {
-            Arg<T> o;
-            o.value = shfl_xor_any(x.value, off);
-            o.index = static_cast<uint32_t>(__shfl_xor(static_cast<int>(x.index), off));
-            x = R::combine(x, o);
-        } else {
-            x = R::combine(x, shfl_xor_any(x, off));
-        }
+    x = dpp_combine<dpp::kRowShr1, 0xf, T, OP>(x);
+    x = dpp_combine<dpp::kRowShr2, 0xf, T, OP>(x);
+    x = dpp_combine<dpp::kRowShr4, 0xf, T, OP>(x);
+    x = dpp_combine<dpp::kRowShr8, 0xf, T, OP>(x);
+    x = dpp_combine<dpp::kRowBcast15, 0xa, T, OP>(x);
+    x = dpp_combine<dpp::kRowBcast31, 0xc, T, OP>(x);
+    if constexpr (OP == kOpArgMin || OP == kOpArgMax) {
+        x.value = read_lane_any(x.value, kWave - 1);
+        x.index = __builtin_amdgcn_readlane(x.index, kWave - 1);
+        return x;
+    } else {
+        return read_lane_any(x, kWave - 1);
     }
-    return x;
 }
 
 // Writes segment seg's result (relative index for the Arg forms; empty segments take the identity and

@@ -248,7 +248,9 @@ def test_run_length_encode_known_answers(hip, dev):
         assert int(to_host(num, np.uint32, 1)[0]) == 0
 
 
-@pytest.mark.parametrize("count", [1, 2, 3, 31, 32, 33, 3839, 3840, 3841, 5761, 8191, 8192, 8193, 230413])
+# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles) and their multiples.
+@pytest.mark.parametrize("count", [1, 2, 3, 31, 32, 33, 3839, 3840, 3841, 4095, 4096, 4097, 5761, 8191, 8192, 8193,
+                                   16383, 16384, 16385, 32769, 230413])
 def test_run_length_encode_long_runs_across_tiles(hip, orc, dev, count):
     """device_run_length_encode_test.cpp:74-136: x[i] = i / run_length for run lengths 1, 2, 17, 18001, n."""
     for run_length in (1, 2, 17, 18001, count):
