@@ -251,6 +251,203 @@ __global__ __launch_bounds__(kDigits) void bins_scan_kernel(uint32_t* __restrict
 }
 
 // --------------------------------------------------------------------------------------------
+// First-pass tile offsets without a look-back.
+//
+// The histogram reads every key anyway, so it can also count the first pass's digits per onesweep
+// tile.  An exclusive scan of those counts over the tiles (per digit, plus the digit's base) gives
+// every tile of the first pass its output offsets before that pass starts, so the pass skips its
+// publish and look-back.  Used for single-portion sorts of 4-byte keys without values whose keys are
+// 16-byte aligned, when the caller's temp storage has room for the per-workgroup totals.
+// --------------------------------------------------------------------------------------------
+
+// histogram_kernel plus the first pass's digit counts per TILE keys: tile_counts[t][d] for every tile
+// of the slice, and the slice's totals in chunk_sums[blockIdx.x][d].  The slice starts on a tile
+// boundary and holds whole tiles (the last slice may end in a partial one).  The first pass's
+// counters are two buffers of bank-private copies: one counts a tile while the other, the previous
+// tile's, is summed and cleared by 128 threads, so a tile costs one barrier.
+template <typename K, bool DESC, bool FULL, uint32_t TILE>
+// Two workgroups per CU for 4-byte keys (80 KB of LDS each, at most 64 VGPRs), one for 8-byte keys.
+__global__ __launch_bounds__(kHistBlock, (sizeof(K) == 4 ? 8 : 4)) void histogram_tiles_kernel(const K* __restrict__ keys, uint32_t n,
+                                                                      uint32_t per_block, uint32_t* __restrict__ bins,
+                                                                      uint32_t begin_bit, uint32_t end_bit,
+                                                                      uint32_t passes,
+                                                                      uint32_t* __restrict__ tile_counts,
+                                                                      uint32_t* __restrict__ chunk_sums) {
+    using U = typename KeyTraits<K>::U;
+    constexpr int KIND = KeyTraits<K>::kind;
+    constexpr int PASSES_MAX = sizeof(U);
+    constexpr int PER_VEC = 16 / sizeof(U);
+    constexpr uint32_t PASS_WORDS = kDigits / 2 * kHistCopies;
+    constexpr int VECS = static_cast<int>(TILE / (PER_VEC * kHistBlock));  // 16-byte loads per thread and tile
+    static_assert(TILE % (PER_VEC * kHistBlock) == 0, "a tile is whole 16-byte steps of the workgroup");
+    // Slots 0 and 1: the first pass's tile buffers; slot p + 1: pass p >= 1.
+    __shared__ uint32_t s_hist[(PASSES_MAX + 1) * PASS_WORDS];
+    if constexpr (FULL) passes = PASSES_MAX;
+    for (uint32_t i = threadIdx.x; i < (passes + 1) * PASS_WORDS; i += kHistBlock) s_hist[i] = 0;
+    __syncthreads();
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t copy = tid % kHistCopies;
+    const uint64_t first = static_cast<uint64_t>(blockIdx.x) * per_block;
+    const uint64_t last = min(static_cast<uint64_t>(n), first + per_block);
+    auto count = [&](U key, uint32_t buf) {
+        U ordered = twiddle_in<U, KIND, DESC>(key);
+        if constexpr (KIND == kFloat) {
+            constexpr U kHigh = U(1) << (sizeof(U) * 8 - 1);
+            if (ordered == U(~kHigh)) ordered = kHigh;
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < PASSES_MAX; ++p) {
+            uint32_t pair, odd;
+            if constexpr (FULL) {
+                pair = static_cast<uint32_t>(ordered >> (8 * p + 1)) & 0x7Fu;
+                odd = static_cast<uint32_t>(ordered >> (8 * p)) & 1u;
+            } else {
+                if (p >= passes) break;
+                const uint32_t shift = begin_bit + 8 * p;
+                const uint32_t nb = min(8u, end_bit - shift);
+                const uint32_t d = static_cast<uint32_t>(ordered >> shift) & ((1u << nb) - 1u);
+                pair = d >> 1;
+                odd = d & 1u;
+            }
+            // Pass 0 counts into this tile's buffer; pass p >= 1 at a fixed offset from the same base.
+            uint32_t* const base = p == 0 ? s_hist + buf * PASS_WORDS + copy : s_hist + (p + 1) * PASS_WORDS + copy;
+            atomicAdd(base + pair * kHistCopies, 1u + odd * 0xFFFFu);
+        }
+    };
+    const U* ukeys = reinterpret_cast<const U*>(keys);
+    using Vec = U __attribute__((ext_vector_type(PER_VEC)));
+    uint32_t chunk_lo = 0, chunk_hi = 0;  // threads < 128: the slice's first-pass counts of digits 2 tid, 2 tid + 1
+    const uint32_t tiles = static_cast<uint32_t>(ceil_div(last - first, TILE));
+    const uint32_t full_tiles = static_cast<uint32_t>((last - first) / TILE);
+    // Sums and clears buffer `buf` (tile t0) once every thread has counted it: thread w < 128 takes the
+    // word of digits 2w and 2w + 1, starting at a different copy per lane so the reads spread over the
+    // banks.  (The copy index rotates in the loop; precomputed, its 32 values would stay in registers.)
+    auto flush = [&](uint32_t buf, uint64_t t0) {
+        if (tid < kDigits / 2) {
+            uint32_t* row = &s_hist[buf * PASS_WORDS + tid * kHistCopies];
+            uint32_t lo = 0, hi = 0;
+            uint32_t c = tid % kHistCopies;
+#pragma unroll 4
+            for (uint32_t k = 0; k < kHistCopies; ++k) {
+                asm volatile("" : "+v"(c));
+                const uint32_t x = row[c];
+                lo += x & 0xFFFFu;
+                hi += x >> 16;
+                row[c] = 0;
+                c = (c + 1) % kHistCopies;
+            }
+            uint32_t* out = tile_counts + (t0 / TILE) * kDigits + 2 * tid;
+            out[0] = lo;
+            out[1] = hi;
+            chunk_lo += lo;
+            chunk_hi += hi;
+        }
+    };
+    // Full tiles, software-pipelined: the next tile's loads are issued before this tile is counted, so
+    // they are in flight across the barrier and the flush.
+    Vec k[VECS], next[VECS];
+    if (full_tiles > 0) {
+        const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + first);
+#pragma unroll
+        for (int u = 0; u < VECS; ++u) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
+    }
+    for (uint32_t j = 0; j < full_tiles; ++j) {
+        const uint32_t buf = j & 1u;
+        const uint64_t t0 = first + static_cast<uint64_t>(j) * TILE;
+#pragma unroll
+        for (int u = 0; u < VECS; ++u) k[u] = next[u];
+        if (j + 1 < full_tiles) {
+            const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + t0 + TILE);
+#pragma unroll
+            for (int u = 0; u < VECS; ++u) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
+        }
+#pragma unroll
+        for (int u = 0; u < VECS; ++u)
+#pragma unroll
+            for (int e = 0; e < PER_VEC; ++e) count(k[u][e], buf);
+        // Tile j is counted; the flush of buffer buf ^ 1 (tile j - 1) is finished.
+        __syncthreads();
+        flush(buf, t0);
+    }
+    if (full_tiles < tiles) {  // the slice's last, partial tile
+        const uint32_t buf = full_tiles & 1u;
+        const uint64_t t0 = first + static_cast<uint64_t>(full_tiles) * TILE;
+        for (uint64_t i = t0 + tid; i < last; i += kHistBlock) count(ukeys[i], buf);
+        __syncthreads();
+        flush(buf, t0);
+    }
+    if (tid < kDigits / 2) {
+        chunk_sums[static_cast<uint64_t>(blockIdx.x) * kDigits + 2 * tid] = chunk_lo;
+        chunk_sums[static_cast<uint64_t>(blockIdx.x) * kDigits + 2 * tid + 1] = chunk_hi;
+        if (chunk_lo) atomic_add_agent(&bins[2 * tid], chunk_lo);
+        if (chunk_hi) atomic_add_agent(&bins[2 * tid + 1], chunk_hi);
+    }
+    // The other passes as in histogram_kernel.  (Their counting ended before the loop's last barrier.)
+    for (uint32_t i = tid; i < (passes - 1) * kDigits; i += kHistBlock) {
+        const uint32_t p = 1 + i / kDigits, d = i % kDigits;
+        const uint32_t* row = &s_hist[(p + 1) * PASS_WORDS + (d >> 1) * kHistCopies];
+        uint32_t total = 0;
+        for (uint32_t c = 0; c < kHistCopies; ++c) total += (row[(c + i) % kHistCopies] >> ((d & 1u) * 16u)) & 0xFFFFu;
+        if (total) atomic_add_agent(&bins[p * kDigits + d], total);
+    }
+}
+
+// chunk_sums[c][d] -> the first output position of digit d's keys in chunk c's slice: the digit's base
+// (bins[d], already scanned over the digits) plus the counts of the slices before c.  One workgroup per
+// digit; thread t takes the consecutive chunks [t k, t k + k).
+__global__ __launch_bounds__(kDigits) void chunk_scan_kernel(uint32_t* __restrict__ chunk_sums,
+                                                             const uint32_t* __restrict__ bins, uint32_t chunks) {
+    __shared__ uint32_t s_wave_totals[kDigits / kWave];
+    const uint32_t d = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per = (chunks + kDigits - 1) / kDigits;
+    constexpr uint32_t kMaxPer = 8;  // chunks <= 2,048
+    uint32_t v[kMaxPer];
+    uint32_t sum = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxPer; ++k) {
+        const uint32_t c = tid * per + k;
+        v[k] = (k < per && c < chunks) ? chunk_sums[static_cast<uint64_t>(c) * kDigits + d] : 0u;
+        sum += v[k];
+    }
+    const uint32_t incl = wave_inclusive_scan(sum, SumOp{});
+    const uint32_t wave = tid / kWave;
+    if (lane_id() == kWave - 1) s_wave_totals[wave] = incl;
+    __syncthreads();
+    uint32_t run = bins[d] + incl - sum;
+    for (uint32_t w = 0; w < wave; ++w) run += s_wave_totals[w];
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxPer; ++k) {
+        const uint32_t c = tid * per + k;
+        if (k < per && c < chunks) chunk_sums[static_cast<uint64_t>(c) * kDigits + d] = run;
+        run += v[k];
+    }
+}
+
+// tile_counts[t][d] -> tile t's first output position for digit d: its chunk's position plus the
+// counts of the chunk's tiles before t.  One workgroup per chunk, one thread per digit.
+__global__ __launch_bounds__(kDigits) void tile_offsets_kernel(uint32_t* __restrict__ tile_counts,
+                                                               const uint32_t* __restrict__ chunk_sums,
+                                                               uint32_t tiles_per_chunk, uint32_t tiles) {
+    const uint32_t d = threadIdx.x;
+    const uint32_t t0 = blockIdx.x * tiles_per_chunk;
+    const uint32_t t1 = min(tiles, t0 + tiles_per_chunk);
+    uint32_t run = chunk_sums[static_cast<uint64_t>(blockIdx.x) * kDigits + d];
+    constexpr uint32_t kBatch = 16;
+    for (uint32_t t = t0; t < t1; t += kBatch) {
+        uint32_t c[kBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) c[k] = t + k < t1 ? tile_counts[static_cast<uint64_t>(t + k) * kDigits + d] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+            if (t + k < t1) tile_counts[static_cast<uint64_t>(t + k) * kDigits + d] = run;
+            run += c[k];
+        }
+    }
+}
+
+// --------------------------------------------------------------------------------------------
 // Onesweep pass.
 // --------------------------------------------------------------------------------------------
 
@@ -404,7 +601,8 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
                                                          void* __restrict__ values_out, uint32_t n,
                                                          const uint32_t* __restrict__ digit_offsets,
                                                          uint32_t* __restrict__ next_offsets,
-                                                         uint32_t* __restrict__ lookback, uint32_t shift,
+                                                         uint32_t* __restrict__ lookback,
+                                                         const uint32_t* __restrict__ tile_offsets, uint32_t shift,
                                                          uint32_t num_bits, uint32_t out_items,
                                                          uint32_t spin_limit, uint32_t ballot_sixteenths) {
     using U = typename KeyTraits<K>::U;
@@ -448,6 +646,10 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     const uint32_t tile = tile_of_block(blockIdx.x, gridDim.x);
     const uint32_t tile_base = tile * TILE;
     const uint32_t valid = min(TILE, n - tile_base);
+    // With precomputed first-pass offsets (tile_offsets[tile][d]: the tile's first output position of
+    // digit d), the tile neither publishes nor looks back; the offset is read now, behind the rank.
+    const bool precomputed = tile_offsets != nullptr;
+    const uint32_t tile_offset = (precomputed && tid < kDigits) ? tile_offsets[tile * kDigits + tid] : 0u;
 
     // Load (wave-striped) and twiddle; missing items become all-ones keys, which rank last.
     const U* ukeys = reinterpret_cast<const U*>(keys_in) + tile_base;
@@ -534,7 +736,8 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         }
         count = run;
         const uint32_t real = (d == mask) ? count - (TILE - valid) : count;  // missing items excluded
-        atomic_store_agent(&lookback[tile * kDigits + d], (tile == 0 ? kFlagInclusive : kFlagPartial) | real);
+        if (!precomputed)
+            atomic_store_agent(&lookback[tile * kDigits + d], (tile == 0 ? kFlagInclusive : kFlagPartial) | real);
         const uint32_t incl = wave_inclusive_scan(count, SumOp{});
         if (lane == kWave - 1) s_scan[wave] = incl;
         local_start = incl - count;
@@ -564,7 +767,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // Look-back: the four waves that hold one digit per lane walk independently (lookback_digit); the
     // other waves go straight to the barrier below.
     uint32_t excl = 0;
-    if (tile > 0 && tid < kDigits) {
+    if (!precomputed && tile > 0 && tid < kDigits) {
         excl = lookback_digit<K, DESC, BLOCK, ITEMS, WINDOW>(lookback, tile, d, keys_in, shift, mask, spin_limit,
                                                              &s_global_minus_local[wave * kWave], trace_steps,
                                                              trace_spins, trace_fallbacks);
@@ -575,7 +778,7 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
         const uint32_t base = digit_offsets[d];
         // Carry to the next portion of this pass: first position of digit d after this portion.
         if (next_offsets != nullptr && tile == gridDim.x - 1) next_offsets[d] = base + excl + real;
-        s_global_minus_local[d] = base + excl - local_start;
+        s_global_minus_local[d] = (precomputed ? tile_offset : base + excl) - local_start;
     }
     __syncthreads();
     clk.mark<6>();  // global offsets known
@@ -641,7 +844,7 @@ struct Geometry {
     int block;
     int items;
     int window;  // predecessor tiles per 256-thread group and look-back step
-    uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
+    constexpr uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
 // The reordering buffer takes at most 64 KB of LDS, so two workgroups share a CU.  16K-key tiles
@@ -670,6 +873,7 @@ constexpr Geometry geometry() {
 // another thread applies from the next call.
 std::atomic<uint32_t> g_portion_limit{0};
 std::atomic<int> g_rank_mode{kRankMixed};
+std::atomic<bool> g_precount{true};  // precomputed first-pass offsets when the call allows them
 
 // Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
 // portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
@@ -685,6 +889,9 @@ uint32_t portion_size(uint32_t tile, bool compact, uint32_t limit) {
 struct Layout {
     uint32_t passes, portions, portion, tiles_max;
     size_t bins_off, lookback_off, keys_tmp_off, values_tmp_off, total;
+    // First-pass tile offsets precomputed by the histogram (0: the first pass looks back like the
+    // others): the per-workgroup totals start here, past `total`, when the caller's temp has room.
+    size_t chunk_off = 0;
     size_t clear_bytes;  // bins, zeroed per call
     int rank_mode = kRankMixed;  // test hooks as read at the start of the call
     uint32_t spin_limit = 64;
@@ -719,6 +926,21 @@ Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t be
     return L;
 }
 
+// Histogram workgroups over `len` keys: two per CU for 4-byte keys (64 KB of counters each), one for
+// 8-byte keys; contiguous slices of at most kHistMaxItems keys, whole 16-byte steps of the workgroup.
+struct HistPlan {
+    uint64_t per;
+    unsigned grid;
+};
+template <typename K>
+HistPlan hist_plan(uint32_t len) {
+    constexpr uint32_t hist_step = static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
+    const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
+    uint64_t per = ceil_div(ceil_div(len, hist_target), hist_step) * hist_step;
+    per = std::min<uint64_t>(per, kHistMaxItems);
+    return HistPlan{per, static_cast<unsigned>(ceil_div(len, per))};
+}
+
 template <typename K, bool DESC, int VB>
 int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, const void* values_in, void* values_out,
                 K* keys_tmp, void* values_tmp, K* const* db_keys, void* const* db_values, int sel, uint32_t n,
@@ -731,19 +953,30 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
     if (st != kOk) return st;
 
     const K* hist_src = db_keys ? db_keys[sel] : keys_in;
-    // Two workgroups per CU for 4-byte keys (64 KB of counters each), one for 8-byte keys; contiguous
-    // slices of at most kHistMaxItems keys, rounded to whole 16-byte steps of the workgroup.
-    constexpr uint32_t hist_step = static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
-    const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
     const bool full = begin_bit == 0 && end_bit == sizeof(K) * 8;
+    // Precomputed first-pass offsets (a single portion): the histogram also writes the first pass's
+    // per-tile digit counts into the look-back region and per-workgroup totals into the chunk region.
+    const bool precount = L.chunk_off != 0;
+    uint32_t* chunk_sums = precount ? reinterpret_cast<uint32_t*>(temp + L.chunk_off) : nullptr;
+    HistPlan hp0{};
     for (uint32_t q = 0; q < L.portions; ++q) {
         const uint32_t len = std::min(L.portion, n - q * L.portion);
-        uint64_t per = ceil_div(ceil_div(len, hist_target), hist_step) * hist_step;
-        per = std::min<uint64_t>(per, kHistMaxItems);
-        const unsigned grid = static_cast<unsigned>(ceil_div(len, per));
+        const HistPlan hp = hist_plan<K>(len);
+        const uint64_t per = hp.per;
+        const unsigned grid = hp.grid;
+        if (q == 0) hp0 = hp;
         LaunchScope scope("radix_histogram", stream);
         // Every portion adds into the totals of portion 0's slots.
-        if (full)
+        if (precount) {
+            static_assert(static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K)) % G.tile() == 0,
+                          "histogram slices hold whole onesweep tiles");
+            if (full)
+                histogram_tiles_kernel<K, DESC, true, G.tile()><<<grid, kHistBlock, 0, stream>>>(
+                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, lookback, chunk_sums);
+            else
+                histogram_tiles_kernel<K, DESC, false, G.tile()><<<grid, kHistBlock, 0, stream>>>(
+                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, lookback, chunk_sums);
+        } else if (full)
             histogram_kernel<K, DESC, true><<<grid, kHistBlock, 0, stream>>>(
                 hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit,
                 end_bit, L.passes);
@@ -758,6 +991,17 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         LaunchScope scope("radix_bins_scan", stream);
         bins_scan_kernel<<<1, kDigits, 0, stream>>>(bins, L.passes);
         st = check_hip(hipGetLastError(), "radix_bins_scan launch");
+        if (st != kOk) return st;
+    }
+    if (precount) {
+        LaunchScope scope("radix_tile_offsets", stream);
+        chunk_scan_kernel<<<kDigits, kDigits, 0, stream>>>(chunk_sums, bins, hp0.grid);
+        st = check_hip(hipGetLastError(), "radix_chunk_scan launch");
+        if (st != kOk) return st;
+        tile_offsets_kernel<<<hp0.grid, kDigits, 0, stream>>>(lookback, chunk_sums,
+                                                               static_cast<uint32_t>(hp0.per / G.tile()),
+                                                               static_cast<uint32_t>(ceil_div(n, G.tile())));
+        st = check_hip(hipGetLastError(), "radix_tile_offsets launch");
         if (st != kOk) return st;
     }
 
@@ -791,16 +1035,19 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         for (uint32_t q = 0; q < L.portions; ++q) {
             const uint32_t len = std::min(L.portion, n - q * L.portion);
             const uint32_t tiles = static_cast<uint32_t>(ceil_div(len, G.tile()));
-            st = launch_fill_u32(lookback, static_cast<uint64_t>(tiles) * kDigits, 0u, stream);
-            if (st != kOk) return st;
+            const bool pre = precount && p == 0;  // the look-back region holds the first pass's offsets
+            if (!pre) {
+                st = launch_fill_u32(lookback, static_cast<uint64_t>(tiles) * kDigits, 0u, stream);
+                if (st != kOk) return st;
+            }
             const size_t qoff = static_cast<size_t>(q) * L.portion;
             LaunchScope scope("radix_onesweep", stream);
             const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
             onesweep_kernel<K, DESC, VB, G.block, G.items, G.window><<<tiles, G.block, 0, stream>>>(
-                src + qoff, dst, vs, vdst, len, offsets, next, lookback, shift, nb, n, L.spin_limit,
-                ballot_sixteenths_for(L.rank_mode));
+                src + qoff, dst, vs, vdst, len, offsets, next, lookback, pre ? lookback : nullptr, shift, nb, n,
+                L.spin_limit, ballot_sixteenths_for(L.rank_mode));
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
@@ -840,6 +1087,19 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
     L.spin_limit = lookback_spin_limit();
     if (!temp || temp_bytes < L.total)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, L.total);
+    {
+        // First-pass offsets from the histogram: 4-byte keys without values (SortKeys 2^28 u32, kernel
+        // trace: first pass 586 -> 504 us for 14 us more histogram and 12 us of offset kernels; for 8-byte
+        // keys with values both the histogram and the first pass got slower: 737 -> 801 us), one portion,
+        // 16-byte aligned keys (the histogram's slices then hold whole tiles) and room for the
+        // per-workgroup totals.
+        const void* first_src = db ? (*selector ? db1 : db0) : keys_in;
+        const size_t off = align_up(L.total, kViewAlign);
+        if (sizeof(K) == 4 && VB == 0 && L.portions == 1 && reinterpret_cast<uintptr_t>(first_src) % 16 == 0 &&
+            g_precount.load(std::memory_order_relaxed) &&
+            temp_bytes >= off + static_cast<size_t>(hist_plan<K>(n).grid) * kDigits * 4)
+            L.chunk_off = off;
+    }
     if (reinterpret_cast<uintptr_t>(temp) % 4 != 0) return set_error(kInvalidArgument, "%s: temp not 4-byte aligned", what);
     char* t = static_cast<char*>(temp);
     K* keys_tmp = L.keys_tmp_off ? reinterpret_cast<K*>(t + L.keys_tmp_off) : nullptr;
@@ -890,6 +1150,10 @@ int lcpp_hip_internal_radix_rank_mode(int mode) {
         return set_error(kInvalidArgument, "rank mode must be 0, 1 or 2");
     g_rank_mode.store(mode, std::memory_order_relaxed);
     return kOk;
+}
+
+int lcpp_hip_internal_radix_precount(int enable) {
+    return g_precount.exchange(enable != 0, std::memory_order_relaxed) ? 1 : 0;
 }
 
 uint32_t lcpp_hip_radix_tile_items(size_t key_bytes, size_t value_bytes) {

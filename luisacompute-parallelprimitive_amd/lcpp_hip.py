@@ -96,6 +96,7 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_internal_radix_needed_bytes", sz, u32, sz, sz, u32, u32, i32)
     sig("lcpp_hip_internal_radix_portions", u32, u32, sz, sz, u32, u32, i32, sz)
     sig("lcpp_hip_internal_radix_rank_mode", i32, i32)
+    sig("lcpp_hip_internal_radix_precount", i32, i32)
     sig("lcpp_hip_generate", i32, i32, vp, u64, u64, u64, vp)
     for s in SCALAR_SUFFIXES:
         sig(f"lcpp_hip_reduce_sum_{s}", i32, vp, sz, vp, vp, u64, vp)

@@ -54,6 +54,9 @@ def summarize_sort(rec: np.ndarray, p: int) -> dict:
     # Stamps: t0 start, t1 loaded, t2 ranked, t3 published, t4 reordered, t5 looked back (tiles > 0),
     # t6 offsets known, t7 stored.
     t = rec[:, 1:9].astype(np.int64)
+    # A pass with offsets precomputed by the histogram (the first pass, by default) does not look back:
+    # its look-back stamp stays 0, and the phase counts as empty.
+    t[:, 5] = np.where(t[:, 5] == 0, t[:, 4], t[:, 5])
     mhz = _clock_mhz(rec, 7)
     body = rec[1:]  # tile 0 has no look-back
     tb = t[1:]

@@ -332,6 +332,44 @@ def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
         lib.lcpp_hip_internal_radix_rank_mode(2)
 
 
+@pytest.mark.parametrize("precount", [0, 1])
+@pytest.mark.parametrize("case", ["u32_random", "u64_pairs_desc", "f32_bits_3_29", "i32_partial_tile", "u32_db"])
+def test_first_pass_offsets_from_histogram(hip, orc, dev, precount, case):
+    """The first pass takes its tile offsets from the histogram's per-tile counts (precount 1, the default
+    for a single portion with aligned keys) or walks the look-back like the other passes (0): the same
+    stable order either way, for full and partial bit ranges, a partial last tile, pairs, descending
+    order and the DoubleBuffer form."""
+    lib = hip.lib()
+    raw = orc.generate(0, 1 << 20, 5150)
+    try:
+        old = lib.lcpp_hip_internal_radix_precount(precount)
+        if case == "u32_random":
+            keys = (raw >> np.uint64(32)).astype(np.uint32)
+            check_bits(gpu_sort(hip, keys), orc.radix_sort(keys))
+        elif case == "u64_pairs_desc":
+            keys = raw[:300007] & np.uint64(0x0F0F0F0F0F0F0F0F)
+            vals = np.arange(keys.size, dtype=np.uint32)
+            ko, vo = gpu_sort(hip, keys, vals, descending=True)
+            eko, evo = orc.radix_sort(keys, vals, descending=True)
+            check_bits(ko, eko)
+            assert np.array_equal(vo, evo)
+        elif case == "f32_bits_3_29":
+            keys = orc.generate(6, 250001, 5151)
+            check_bits(gpu_sort(hip, keys, begin_bit=3, end_bit=29), orc.radix_sort(keys, begin_bit=3, end_bit=29))
+        elif case == "i32_partial_tile":
+            keys = (raw[:16384 * 7 + 1234] >> np.uint64(40)).astype(np.int32) - (1 << 23)
+            check_bits(gpu_sort(hip, keys), orc.radix_sort(keys))
+        else:
+            n = 1 << 19
+            keys = (raw[:n] >> np.uint64(16)).astype(np.uint32)
+            d0, d1 = to_dev(keys), fill_dev(n, 4, -1)
+            sel = hip.sort_keys_db("u32", d0, d1, 0, n)
+            got = to_host(d1 if sel == 1 else d0, np.uint32, n)
+            check_bits(got, orc.radix_sort(keys))
+    finally:
+        lib.lcpp_hip_internal_radix_precount(old)
+
+
 def test_constant_keys_large(hip, dev):
     """2^25 identical keys: every histogram count lands in one digit of every pass (the packed 16-bit
     per-bank counters of one workgroup must not overflow), and the sort is the identity."""
