@@ -117,6 +117,24 @@ int lcpp_hip_scan_sum_init_f32(void* temp, size_t temp_bytes, const float* in, f
 int lcpp_hip_scan_sum_init_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int64_t init, void* stream);
 int lcpp_hip_scan_sum_init_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, uint64_t init, void* stream);
 int lcpp_hip_scan_sum_init_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, double init, void* stream);
+/* Min / max scans: DeviceScan<>::ExclusiveScan / InclusiveScan / InclusiveScanInit with MinOp or MaxOp
+ * (device_scan.h:321-368, operators common/thread_operators.h:58-74).  exclusive: out[i] = op(init,
+ * in[0], ..., in[i-1]) (out[0] = init); inclusive: op(init, in[0], ..., in[i]), init omitted when
+ * use_init is 0 (the operator's identity: the type's max / lowest; a quiet NaN for floats, so an
+ * exclusive scan's out[0] is NaN).  Signed types compare as signed; floats like fmin / fmax (a NaN
+ * operand yields the other one; of -0.0 and +0.0 the earlier is kept). */
+int lcpp_hip_scan_min_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, int inclusive, int use_init, int32_t init, void* stream);
+int lcpp_hip_scan_min_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, int inclusive, int use_init, uint32_t init, void* stream);
+int lcpp_hip_scan_min_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, int inclusive, int use_init, float init, void* stream);
+int lcpp_hip_scan_min_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int use_init, int64_t init, void* stream);
+int lcpp_hip_scan_min_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, int use_init, uint64_t init, void* stream);
+int lcpp_hip_scan_min_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, int use_init, double init, void* stream);
+int lcpp_hip_scan_max_i32(void* temp, size_t temp_bytes, const int32_t* in, int32_t* out, uint64_t n, int inclusive, int use_init, int32_t init, void* stream);
+int lcpp_hip_scan_max_u32(void* temp, size_t temp_bytes, const uint32_t* in, uint32_t* out, uint64_t n, int inclusive, int use_init, uint32_t init, void* stream);
+int lcpp_hip_scan_max_f32(void* temp, size_t temp_bytes, const float* in, float* out, uint64_t n, int inclusive, int use_init, float init, void* stream);
+int lcpp_hip_scan_max_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int use_init, int64_t init, void* stream);
+int lcpp_hip_scan_max_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, int use_init, uint64_t init, void* stream);
+int lcpp_hip_scan_max_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, int use_init, double init, void* stream);
 /* ExclusiveSum over uint32 with no temp argument: the same kernels, with their tile status words in a
  * static device array of the library (349,528 bytes per GPU, held until the process ends) instead of
  * caller-provided temp storage, and no allocation of any kind.  No counterpart in the reference: it is

@@ -73,15 +73,17 @@ __device__ __forceinline__ T dpp_move(T old, T src) {
 // Inclusive scan over the 64 lanes of a wave (all lanes must be active).
 // Rows of 16 lanes are scanned with row_shr 1/2/4/8, then row totals are carried with
 // row_bcast:15 (row r-1's last lane into rows 1 and 3) and row_bcast:31 (lane 31 into rows 2, 3).
+// The value from lower lanes is always the left operand, so an operator that is associative but not
+// commutative (a min that keeps the earlier of two equal values) sees its operands in lane order.
 template <typename T, typename Op>
 __device__ __forceinline__ T wave_inclusive_scan(T x, Op op) {
     const T id = Op::template identity<T>();
-    x = op(x, dpp_move<dpp::kRowShr1>(id, x));
-    x = op(x, dpp_move<dpp::kRowShr2>(id, x));
-    x = op(x, dpp_move<dpp::kRowShr4>(id, x));
-    x = op(x, dpp_move<dpp::kRowShr8>(id, x));
-    x = op(x, dpp_move<dpp::kRowBcast15, 0xa>(id, x));
-    x = op(x, dpp_move<dpp::kRowBcast31, 0xc>(id, x));
+    x = op(dpp_move<dpp::kRowShr1>(id, x), x);
+    x = op(dpp_move<dpp::kRowShr2>(id, x), x);
+    x = op(dpp_move<dpp::kRowShr4>(id, x), x);
+    x = op(dpp_move<dpp::kRowShr8>(id, x), x);
+    x = op(dpp_move<dpp::kRowBcast15, 0xa>(id, x), x);
+    x = op(dpp_move<dpp::kRowBcast31, 0xc>(id, x), x);
     return x;
 }
 

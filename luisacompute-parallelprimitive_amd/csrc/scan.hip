@@ -33,7 +33,9 @@
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
 
+#include <limits>
 #include <mutex>
+#include <type_traits>
 
 namespace lcpp_hip {
 namespace {
@@ -59,6 +61,37 @@ constexpr uint32_t kFlagInvalid = 0;
 constexpr uint32_t kFlagPartial = 1;
 constexpr uint32_t kFlagInclusive = 2;
 constexpr uint32_t kFlagClaimed = 3;  // a look-back is computing this tile's aggregate
+
+// Scan operators: the reference's SumOp, MinOp and MaxOp (common/thread_operators.h:49-74).  Integer sums
+// run in the unsigned type (wrap-around); min / max compare in the item's own type, for floats like
+// fmin / fmax (a NaN operand yields the other one; -0.0 and +0.0 compare equal, so the older is kept).
+// Identities: the type's max / lowest for integers; a quiet NaN for floats, the one value that every
+// float operand, NaN included, absorbs (op(x, NaN) = op(NaN, x) = x), so padding and empty prefixes
+// leave an inclusive scan equal to the plain left-to-right fold of its items.
+struct ScanMinOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const {
+        if constexpr (std::is_floating_point_v<T>) return (b < a || a != a) ? b : a;  // a NaN operand yields the other
+        else return b < a ? b : a;
+    }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() {
+        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
+        else return std::numeric_limits<T>::max();
+    }
+};
+struct ScanMaxOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const {
+        if constexpr (std::is_floating_point_v<T>) return (b > a || a != a) ? b : a;
+        else return b > a ? b : a;
+    }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() {
+        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
+        else return std::numeric_limits<T>::lowest();
+    }
+};
 
 #ifdef LCPP_HIP_PHASE_TRACE
 // Phase-trace buffer of the diagnostic build: one record per tile.
@@ -121,24 +154,25 @@ __device__ __forceinline__ void store_state(uint64_t* states, uint64_t tile, uin
     }
 }
 
-// Item `idx` of the input, or 0 past the end.
-template <typename T>
+// Item `idx` of the input, or the operator's identity past the end.
+template <typename T, typename Op>
 __device__ __forceinline__ T load_item(const T* in, uint64_t n, uint64_t idx) {
-    return idx < n ? in[idx] : T(0);
+    return idx < n ? in[idx] : Op::template identity<T>();
 }
 
 // Aggregate of (full) tile `tile`, computed by one wave in exactly the order its owner uses: per
 // thread ((x0+x1)+x2)+x3, a DPP wave scan per (row, wave), wave totals summed per row in wave order,
 // rows summed in row order.
-template <typename T>
+template <typename T, typename Op>
 __device__ T tile_aggregate(const T* in, uint64_t n, uint32_t tile, int vector_io) {
     constexpr int V = kVec<T>;
     using Vec = T __attribute__((ext_vector_type(V)));
     const uint32_t lane = lane_id();
     const uint64_t tile_base = static_cast<uint64_t>(tile) * kScanTile<T>;
-    T running = T(0);
+    const Op op{};
+    T running = Op::template identity<T>();
     for (int r = 0; r < kScanRows; ++r) {
-        T row_total = T(0);
+        T row_total = Op::template identity<T>();
         for (int w = 0; w < kScanWaves; ++w) {
             const uint64_t first = tile_base + (static_cast<uint64_t>(r) * kScanBlock + w * kWave + lane) * V;
             Vec v;
@@ -146,27 +180,28 @@ __device__ T tile_aggregate(const T* in, uint64_t n, uint32_t tile, int vector_i
                 v = *reinterpret_cast<const Vec*>(in + first);
             } else {
 #pragma unroll
-                for (int j = 0; j < V; ++j) v[j] = load_item(in, n, first + j);
+                for (int j = 0; j < V; ++j) v[j] = load_item<T, Op>(in, n, first + j);
             }
 #pragma unroll
-            for (int j = 1; j < V; ++j) v[j] += v[j - 1];
-            row_total += wave_read_lane(wave_inclusive_scan(v[V - 1], SumOp{}), kWave - 1);
+            for (int j = 1; j < V; ++j) v[j] = op(v[j - 1], v[j]);
+            row_total = op(row_total, wave_read_lane(wave_inclusive_scan(v[V - 1], op), kWave - 1));
         }
-        running += row_total;
+        running = op(running, row_total);
     }
     return running;
 }
 
 // Exclusive prefix of tile `tile` (> 0) over all earlier tiles; called by all 64 lanes of one wave.
-template <typename T>
+template <typename T, typename Op>
 __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_t n, int vector_io,
                            uint32_t spin_limit, uint64_t& trace_counters) {
     const uint32_t lane = lane_id();
-    T prefix = T(0);
+    const Op op{};
+    T prefix = Op::template identity<T>();
     int64_t end = tile;  // exclusive end of the window of predecessors
     while (true) {
         const int64_t idx = end - kWave + static_cast<int64_t>(lane);
-        TileState<T> st = idx >= 0 ? load_state<T>(states, static_cast<uint64_t>(idx)) : TileState<T>{kFlagInclusive, T(0)};
+        TileState<T> st = idx >= 0 ? load_state<T>(states, static_cast<uint64_t>(idx)) : TileState<T>{kFlagInclusive, Op::template identity<T>()};
         uint32_t spins = 0;
         while (wave_ballot(!flag_published(st.flag)) != 0) {
             if (spins >= spin_limit) {
@@ -189,7 +224,7 @@ __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_
                     }
                     if (wave_ballot(won) != 0) {
                         if constexpr (kPhaseTrace) trace_counters += 1ull << 32;
-                        const T agg = tile_aggregate(in, n, j, vector_io);
+                        const T agg = tile_aggregate<T, Op>(in, n, j, vector_io);
                         if (lane == src) {
                             st = TileState<T>{kFlagPartial, agg};
                             store_state(states, j, kFlagPartial, agg, true);
@@ -207,16 +242,16 @@ __device__ T scan_lookback(uint64_t* states, uint32_t tile, const T* in, uint64_
         const uint64_t inclusive = wave_ballot(st.flag == kFlagInclusive);
         if (inclusive != 0) {
             const uint32_t last = 63 - __builtin_clzll(inclusive);
-            prefix += wave_reduce(lane >= last ? value : T(0), SumOp{});
-            return prefix;
+            return op(wave_reduce(lane >= last ? value : Op::template identity<T>(), op), prefix);
         }
-        prefix += wave_reduce(value, SumOp{});
+        // The window precedes everything folded so far: it is the left operand.
+        prefix = op(wave_reduce(value, op), prefix);
         end -= kWave;
     }
 }
 
-template <typename T, bool INCLUSIVE>
-__global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(const T* in, T* out, uint64_t n,
+template <typename T, bool INCLUSIVE, typename Op>
+__global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_kernel(const T* in, T* out, uint64_t n,
                                                                              uint64_t* __restrict__ states, T init,
                                                                              int vector_io, uint32_t spin_limit) {
     constexpr int V = kVec<T>;
@@ -224,6 +259,7 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
     using Vec = T __attribute__((ext_vector_type(V)));
     __shared__ T s_wave_totals[kScanRows][kScanWaves];
     __shared__ T s_tile_prefix;
+    const Op op{};
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
@@ -246,7 +282,7 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
 #pragma unroll
             for (int j = 0; j < V; ++j) {
                 const uint64_t idx = tile_base + (static_cast<uint64_t>(r) * kScanBlock + tid) * V + j;
-                v[r][j] = idx < n ? in[idx] : T(0);
+                v[r][j] = idx < n ? in[idx] : Op::template identity<T>();
             }
         }
     }
@@ -259,21 +295,21 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
 #pragma unroll
     for (int r = 0; r < kScanRows; ++r) {
 #pragma unroll
-        for (int j = 1; j < V; ++j) v[r][j] += v[r][j - 1];
-        wave_incl[r] = wave_inclusive_scan(v[r][V - 1], SumOp{});
+        for (int j = 1; j < V; ++j) v[r][j] = op(v[r][j - 1], v[r][j]);
+        wave_incl[r] = wave_inclusive_scan(v[r][V - 1], op);
         if (lane == kWave - 1) s_wave_totals[r][wave] = wave_incl[r];
     }
     __syncthreads();
 
     // Tile aggregate: rows in order, each row's wave totals in wave order (the order tile_aggregate
     // repeats for a helper).
-    T aggregate = T(0);
+    T aggregate = Op::template identity<T>();
 #pragma unroll
     for (int r = 0; r < kScanRows; ++r) {
-        T row_total = T(0);
+        T row_total = Op::template identity<T>();
 #pragma unroll
-        for (int w = 0; w < kScanWaves; ++w) row_total += s_wave_totals[r][w];
-        aggregate += row_total;
+        for (int w = 0; w < kScanWaves; ++w) row_total = op(row_total, s_wave_totals[r][w]);
+        aggregate = op(aggregate, row_total);
     }
     clk.mark<1>(true);  // tile loaded and scanned in registers
 
@@ -292,7 +328,8 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
                 __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         const T excl =
-            tile == 0 ? T(0) : scan_lookback<T>(states, tile, in, n, vector_io, spin_limit, trace_counters);
+            tile == 0 ? Op::template identity<T>()
+                      : scan_lookback<T, Op>(states, tile, in, n, vector_io, spin_limit, trace_counters);
         clk.mark<2>();  // look-back walked
         if (lane == 0) {
             if (claimed_by_other) {
@@ -302,36 +339,36 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
                        kFlagPartial)
                     __builtin_amdgcn_s_sleep(1);
             }
-            if (tile != 0 || claimed_by_other) store_state(states, tile, kFlagInclusive, T(excl + aggregate), false);
+            if (tile != 0 || claimed_by_other) store_state(states, tile, kFlagInclusive, op(excl, aggregate), false);
             s_tile_prefix = excl;
         }
     }
     __syncthreads();
 
-    T running = init + s_tile_prefix;  // tile prefix + rows before r
+    T running = op(init, s_tile_prefix);  // tile prefix + rows before r
 #pragma unroll
     for (int r = 0; r < kScanRows; ++r) {
-        T before = T(0), row_total = T(0);
+        T before = Op::template identity<T>(), row_total = Op::template identity<T>();
 #pragma unroll
         for (int w = 0; w < kScanWaves; ++w) {
             const T x = s_wave_totals[r][w];
-            if (w < static_cast<int>(wave)) before += x;
-            row_total += x;
+            if (w < static_cast<int>(wave)) before = op(before, x);
+            row_total = op(row_total, x);
         }
-        const T thread_excl = wave_shift_exclusive<T, SumOp>(wave_incl[r]);
-        const T p = running + before + thread_excl;
+        const T thread_excl = wave_shift_exclusive<T, Op>(wave_incl[r]);
+        const T p = op(op(running, before), thread_excl);
         Vec o;
         if constexpr (INCLUSIVE) {
 #pragma unroll
-            for (int j = 0; j < V - 1; ++j) o[j] = p + v[r][j];
-            o[V - 1] = running + before + wave_incl[r];
+            for (int j = 0; j < V - 1; ++j) o[j] = op(p, v[r][j]);
+            o[V - 1] = op(op(running, before), wave_incl[r]);
         } else {
             o[0] = p;
 #pragma unroll
-            for (int j = 1; j < V; ++j) o[j] = p + v[r][j - 1];
+            for (int j = 1; j < V; ++j) o[j] = op(p, v[r][j - 1]);
         }
         v[r] = o;
-        running += row_total;
+        running = op(running, row_total);
     }
     if (full) {
         Vec* dst = reinterpret_cast<Vec*>(out + tile_base);
@@ -353,22 +390,22 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_sum_kernel(
 #endif
 }
 
-template <typename T>
-int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, T init,
-             void* stream_ptr) {
+template <typename T, typename Op>
+int scan_op(const char* what, void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, T init,
+            void* stream_ptr) {
     static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- and 8-byte items");
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "DeviceScan: too many items (%llu > UINT_MAX)",
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items (%llu > UINT_MAX)", what,
                                             static_cast<unsigned long long>(n));
     if (n == 0) return kOk;
-    if (!in || !out) return set_error(kInvalidArgument, "DeviceScan: null input or output");
+    if (!in || !out) return set_error(kInvalidArgument, "%s: null input or output", what);
     if (reinterpret_cast<uintptr_t>(in) % sizeof(T) != 0 || reinterpret_cast<uintptr_t>(out) % sizeof(T) != 0)
-        return set_error(kInvalidArgument, "DeviceScan: input/output not aligned to the element size");
+        return set_error(kInvalidArgument, "%s: input/output not aligned to the element size", what);
     const size_t needed = scan_needed_bytes(n, sizeof(T));
     if (!temp || temp_bytes < needed)
-        return set_error(kTempTooSmall, "DeviceScan: temp storage too small (%zu < %zu bytes)", temp_bytes, needed);
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, needed);
     if (reinterpret_cast<uintptr_t>(temp) % 8 != 0)
-        return set_error(kInvalidArgument, "DeviceScan: temp storage must be 8-byte aligned");
+        return set_error(kInvalidArgument, "%s: temp storage must be 8-byte aligned", what);
 
     const uint64_t tiles = ceil_div(n, kScanTile<T>);
     uint64_t* states = static_cast<uint64_t*>(temp);
@@ -377,14 +414,19 @@ int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, boo
 
     const int vector_io = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
     const uint32_t spin_limit = lookback_spin_limit();
-    LaunchScope scope("scan_sum", stream);
+    LaunchScope scope(std::is_same_v<Op, SumOp> ? "scan_sum" : "scan_minmax", stream);
     if (inclusive)
-        scan_sum_kernel<T, true><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
-                                                                                         vector_io, spin_limit);
+        scan_kernel<T, true, Op><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
+                                                                                        vector_io, spin_limit);
     else
-        scan_sum_kernel<T, false><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
-                                                                                          vector_io, spin_limit);
-    return check_hip(hipGetLastError(), "scan_sum launch");
+        scan_kernel<T, false, Op><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
+                                                                                         vector_io, spin_limit);
+    return check_hip(hipGetLastError(), "scan launch");
+}
+
+template <typename T>
+int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, T init, void* stream) {
+    return scan_op<T, SumOp>("DeviceScan", temp, temp_bytes, in, out, n, inclusive, init, stream);
 }
 
 // ---- ExclusiveSum over uint32 with no temp argument and no allocation ------------------------------
@@ -470,6 +512,26 @@ LCPP_HIP_DEFINE_SCAN(i64, int64_t, uint64_t)
 LCPP_HIP_DEFINE_SCAN(u64, uint64_t, uint64_t)
 LCPP_HIP_DEFINE_SCAN(f64, double, double)
 #undef LCPP_HIP_DEFINE_SCAN
+
+// Min / max scans compare in the item's own type (signed integers as signed).
+#define LCPP_HIP_DEFINE_SCAN_MINMAX(S, T)                                                                        \
+    int lcpp_hip_scan_min_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,    \
+                              int use_init, T init, void* stream) {                                             \
+        return scan_op<T, ScanMinOp>("DeviceScan (MinOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
+                                     use_init ? init : ScanMinOp::identity<T>(), stream);                         \
+    }                                                                                                           \
+    int lcpp_hip_scan_max_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,    \
+                              int use_init, T init, void* stream) {                                             \
+        return scan_op<T, ScanMaxOp>("DeviceScan (MaxOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
+                                     use_init ? init : ScanMaxOp::identity<T>(), stream);                         \
+    }
+LCPP_HIP_DEFINE_SCAN_MINMAX(i32, int32_t)
+LCPP_HIP_DEFINE_SCAN_MINMAX(u32, uint32_t)
+LCPP_HIP_DEFINE_SCAN_MINMAX(f32, float)
+LCPP_HIP_DEFINE_SCAN_MINMAX(i64, int64_t)
+LCPP_HIP_DEFINE_SCAN_MINMAX(u64, uint64_t)
+LCPP_HIP_DEFINE_SCAN_MINMAX(f64, double)
+#undef LCPP_HIP_DEFINE_SCAN_MINMAX
 
 int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, uint64_t n, void* stream) {
     if (n > kNoAllocMaxItems)

@@ -1,7 +1,8 @@
 // DeviceScan sums over the MI355X C-ABI (lcpp_hip_scan_*), with the reference's module shape
 // (src/lcpp/device/device_scan.h:40-49 template, :269-284 create, :295-308 temp query) and entry
 // points ExclusiveSum (:370-385), InclusiveSum (:409-422), ExclusiveScan / InclusiveScan /
-// InclusiveScanInit with a sum operator (:321-368), checked like validate_scan_views (:213-226).
+// InclusiveScanInit with a sum, min or max operator (:321-368; operators common/thread_operators.h:49-74),
+// checked like validate_scan_views (:213-226).
 // The single-pass kernel is a decoupled look-back over the caller's temp storage.  The by-key
 // entry points (:424-597, temp query :310-315) run the segmented scan of lcpp_hip_scan_by_key_sum_*,
 // checked like validate_scan_by_key_views (:228-246).
@@ -76,6 +77,30 @@ class DeviceScan : public LuisaModule {
     void InclusiveScanInit(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in,
                            BufferView<T> d_out, size_t num_items, SumOp, T initial_value) {
         record(cmdlist, temp_storage, d_in, d_out, num_items, true, initial_value);
+    }
+
+    // ---- min / max operators (lcpp_hip_scan_min_* / lcpp_hip_scan_max_*) ---------------------------
+    // ExclusiveScan (:321-335) seeds the scan with initial_value; InclusiveScan without one (:337-350)
+    // folds the items alone; InclusiveScanInit (:352-368) folds initial_value in front of them.
+    template <NumericT T, typename Op>
+        requires(std::is_same_v<Op, MinOp> || std::is_same_v<Op, MaxOp>)
+    void ExclusiveScan(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                       size_t num_items, Op, T initial_value) {
+        record_minmax<Op>(cmdlist, temp_storage, d_in, d_out, num_items, false, true, initial_value);
+    }
+
+    template <NumericT T, typename Op>
+        requires(std::is_same_v<Op, MinOp> || std::is_same_v<Op, MaxOp>)
+    void InclusiveScan(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                       size_t num_items, Op) {
+        record_minmax<Op>(cmdlist, temp_storage, d_in, d_out, num_items, true, false, T(0));
+    }
+
+    template <NumericT T, typename Op>
+        requires(std::is_same_v<Op, MinOp> || std::is_same_v<Op, MaxOp>)
+    void InclusiveScanInit(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in,
+                           BufferView<T> d_out, size_t num_items, Op, T initial_value) {
+        record_minmax<Op>(cmdlist, temp_storage, d_in, d_out, num_items, true, true, initial_value);
     }
 
     // ---- by key ---------------------------------------------------------------------------------
@@ -197,6 +222,45 @@ class DeviceScan : public LuisaModule {
                                                 static_cast<uint64_t>(init), st);
             }
             luisa::detail::abi_check(rc, inc ? "DeviceScan::InclusiveSum" : "DeviceScan::ExclusiveSum");
+        };
+    }
+
+    template <typename Op, NumericT T>
+    void record_minmax(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                       size_t num_items, bool inclusive, bool use_init, T init) {
+        static_assert((std::is_integral_v<T> && (sizeof(T) == 4 || sizeof(T) == 8) && !std::is_same_v<T, bool>) ||
+                          std::is_same_v<T, float> || std::is_same_v<T, double>,
+                      "DeviceScan min / max support 4- and 8-byte integers, float and double");
+        LCPP_ASSERT(m_created, "DeviceScan::create must be called before dispatch.");
+        LCPP_ASSERT(num_items <= std::numeric_limits<uint>::max(), "Too many items for DeviceScan.");
+        if (num_items == 0u) return;
+        LCPP_ASSERT(d_in.size() >= num_items, "DeviceScan input view is too small.");
+        LCPP_ASSERT(d_out.size() >= num_items, "DeviceScan output view is too small.");
+        LCPP_ASSERT(temp_storage.size() >= bytes_to_uint_count(GetTempStorageBytes<T>(num_items)),
+                    "DeviceScan temporary storage is too small.");
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const T* in = d_in.data();
+        T* out = d_out.data();
+        const int inc = inclusive ? 1 : 0, ui = use_init ? 1 : 0;
+        constexpr bool is_min = std::is_same_v<Op, MinOp>;
+        cmdlist << [=](hipStream_t s) {
+            void* st = detail::stream_ptr(s);
+            int rc;
+            // Signed and unsigned items compare differently, so each has its own entry point.
+#define LCPP_SCAN_MINMAX_CALL(SFX, U)                                                                           \
+    rc = is_min ? lcpp_hip_scan_min_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                          num_items, inc, ui, static_cast<U>(init), st)                          \
+                : lcpp_hip_scan_max_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                          num_items, inc, ui, static_cast<U>(init), st)
+            if constexpr (std::is_same_v<T, float>) LCPP_SCAN_MINMAX_CALL(f32, float);
+            else if constexpr (std::is_same_v<T, double>) LCPP_SCAN_MINMAX_CALL(f64, double);
+            else if constexpr (sizeof(T) == 4 && std::is_signed_v<T>) LCPP_SCAN_MINMAX_CALL(i32, int32_t);
+            else if constexpr (sizeof(T) == 4) LCPP_SCAN_MINMAX_CALL(u32, uint32_t);
+            else if constexpr (std::is_signed_v<T>) LCPP_SCAN_MINMAX_CALL(i64, int64_t);
+            else LCPP_SCAN_MINMAX_CALL(u64, uint64_t);
+#undef LCPP_SCAN_MINMAX_CALL
+            luisa::detail::abi_check(rc, is_min ? "DeviceScan::Scan(MinOp)" : "DeviceScan::Scan(MaxOp)");
         };
     }
 };

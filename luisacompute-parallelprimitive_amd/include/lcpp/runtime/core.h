@@ -245,10 +245,19 @@ struct DoubleBuffer {
 // common/utils.h:247-250.
 inline size_t bytes_to_uint_count(size_t byte_size) { return (byte_size + sizeof(uint) - 1) / sizeof(uint); }
 
-// common/thread_operators.h: the sum operator accepted by the scan entry points.
+// common/thread_operators.h:49-74: the sum, max and min operators accepted by the scan entry points.
+// On the device, float min / max ignore a NaN operand (fmin / fmax).
 struct SumOp {
     template <typename T>
     T operator()(const T& a, const T& b) const { return a + b; }
+};
+struct MaxOp {
+    template <typename T>
+    T operator()(const T& a, const T& b) const { return b > a ? b : a; }
+};
+struct MinOp {
+    template <typename T>
+    T operator()(const T& a, const T& b) const { return b < a ? b : a; }
 };
 
 template <typename T>

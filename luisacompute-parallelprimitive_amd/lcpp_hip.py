@@ -104,6 +104,8 @@ def _declare(lib: C.CDLL) -> None:
         sig(f"lcpp_hip_scan_exclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
         sig(f"lcpp_hip_scan_inclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
         sig(f"lcpp_hip_scan_sum_init_{s}", i32, vp, sz, vp, vp, u64, i32, _CTYPE[s], vp)
+        for op in ("min", "max"):
+            sig(f"lcpp_hip_scan_{op}_{s}", i32, vp, sz, vp, vp, u64, i32, i32, _CTYPE[s], vp)
     for k in SORT_KEY_SUFFIXES:
         sig(f"lcpp_hip_radix_sort_keys_{k}", i32, vp, sz, vp, vp, u32, u32, u32, i32, vp)
         sig(f"lcpp_hip_radix_sort_keys_db_{k}", i32, vp, sz, vp, vp, C.POINTER(C.c_int), u32, u32, u32, i32, vp)
@@ -253,6 +255,19 @@ def scan_sum(suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=Non
     else:
         call(f"lcpp_hip_scan_sum_init_{suffix}", ptr(temp), tb, ptr(d_in), ptr(d_out), n, int(inclusive),
              _CTYPE[suffix](init), stream_handle(stream))
+
+
+def scan_minmax(op: str, suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=None, temp=None,
+                stream=None) -> None:
+    """DeviceScan::ExclusiveScan / InclusiveScan with MinOp (op "min") or MaxOp ("max"); without `init` the
+    operator's identity stands in for it."""
+    if op not in ("min", "max"):
+        raise ValueError(f"scan operator {op!r}: min or max")
+    if temp is None:
+        temp = _temp(scan_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    tb = temp.numel() * temp.element_size()
+    call(f"lcpp_hip_scan_{op}_{suffix}", ptr(temp), tb, ptr(d_in), ptr(d_out), n, int(inclusive),
+         int(init is not None), _CTYPE[suffix](0 if init is None else init), stream_handle(stream))
 
 
 def device_copy(dst, src, nbytes: int, stream=None) -> None:

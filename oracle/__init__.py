@@ -58,6 +58,12 @@ def lib() -> C.CDLL:
         h.oracle_scan_sum_u64.argtypes = [vp, vp, u64, i32, u64]
         h.oracle_scan_sum_f64.restype = None
         h.oracle_scan_sum_f64.argtypes = [vp, vp, vp, u64, i32, C.c_double]
+        for name, ct in (("i32", C.c_int32), ("u32", C.c_uint32), ("f32", C.c_float), ("i64", C.c_int64),
+                         ("u64", C.c_uint64), ("f64", C.c_double)):
+            for op in ("min", "max"):
+                f = getattr(h, f"oracle_scan_{op}_{name}")
+                f.restype = None
+                f.argtypes = [vp, vp, u64, i32, ct]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -176,6 +182,27 @@ def scan_sum_f64(a: np.ndarray, inclusive: bool = False, init: float = 0.0) -> t
     aout = np.empty(a.size, dtype=np.longdouble)
     lib().oracle_scan_sum_f64(_p(a), _p(out), _p(aout), a.size, int(inclusive), init)
     return out, aout
+
+
+_MINMAX_SUFFIX = {np.dtype(np.int32): "i32", np.dtype(np.uint32): "u32", np.dtype(np.float32): "f32",
+                  np.dtype(np.int64): "i64", np.dtype(np.uint64): "u64", np.dtype(np.float64): "f64"}
+
+
+def scan_minmax(op: str, a: np.ndarray, inclusive: bool = False, init=None) -> np.ndarray:
+    """Min (op "min") or max ("max") scan in the array's own type; without `init` the operator's identity
+    (the type's max / lowest; a quiet NaN for floats, which the NaN-ignoring min / max absorbs) stands in
+    for it."""
+    a = np.ascontiguousarray(a)
+    sfx = _MINMAX_SUFFIX[a.dtype]
+    if init is None:
+        if a.dtype.kind == "f":
+            init = np.nan
+        else:
+            info = np.iinfo(a.dtype)
+            init = info.max if op == "min" else info.min
+    out = np.empty_like(a)
+    getattr(lib(), f"oracle_scan_{op}_{sfx}")(_p(a), _p(out), a.size, int(inclusive), a.dtype.type(init).item())
+    return out
 
 
 # ---- host baselines (oracle/cpu_baseline.cpp): `threads` std::threads over contiguous chunks ----------

@@ -123,6 +123,38 @@ void oracle_scan_sum_f64(const double* in, long double* out, long double* abs_ou
         else { out[i] = run; abs_out[i] = arun; run += x; arun += fabsl(x); }
     }
 }
+/* Min / max scans (DeviceScan<>::ExclusiveScan / InclusiveScan with MinOp / MaxOp, device_scan.h:321-368,
+ * common/thread_operators.h:58-74): run = init; exclusive: out[i] = run, run = op(run, in[i]);
+ * inclusive: run = op(run, in[i]), out[i] = run.  op(run, x) keeps run unless x is strictly smaller
+ * (larger) or run is a NaN; so a NaN operand yields the other one, as fmin / fmax do, and of -0.0 and
+ * +0.0 the older is kept. */
+#define ORACLE_SCAN_MINMAX(NAME, T)                                                                      \
+    void oracle_scan_min_##NAME(const T* in, T* out, uint64_t n, int inclusive, T init) {              \
+        T run = init;                                                                                  \
+        for (uint64_t i = 0; i < n; ++i) {                                                             \
+            const T x = in[i];                                                                         \
+            if (!inclusive) out[i] = run;                                                              \
+            if (x < run || run != run) run = x;                                                        \
+            if (inclusive) out[i] = run;                                                               \
+        }                                                                                              \
+    }                                                                                                  \
+    void oracle_scan_max_##NAME(const T* in, T* out, uint64_t n, int inclusive, T init) {              \
+        T run = init;                                                                                  \
+        for (uint64_t i = 0; i < n; ++i) {                                                             \
+            const T x = in[i];                                                                         \
+            if (!inclusive) out[i] = run;                                                              \
+            if (x > run || run != run) run = x;                                                        \
+            if (inclusive) out[i] = run;                                                               \
+        }                                                                                              \
+    }
+ORACLE_SCAN_MINMAX(i32, int32_t)
+ORACLE_SCAN_MINMAX(u32, uint32_t)
+ORACLE_SCAN_MINMAX(f32, float)
+ORACLE_SCAN_MINMAX(i64, int64_t)
+ORACLE_SCAN_MINMAX(u64, uint64_t)
+ORACLE_SCAN_MINMAX(f64, double)
+#undef ORACLE_SCAN_MINMAX
+
 /* Floating-point scan in double (reference value for a tolerance check), plus running |x| sums. */
 void oracle_scan_sum_f32(const float* in, double* out, double* abs_out, uint64_t n, int inclusive, float init) {
     double run = init, arun = fabs((double)init);

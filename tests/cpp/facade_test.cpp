@@ -230,6 +230,50 @@ void scan_inclusive_init_in_place() {
     EXPECT(result == expected);
 }
 
+// tests/pr6_review_regression_test.cpp:146-151,247-265: ExclusiveScan with a max operator and init 0
+// over i % 7 + 1 gives min(i, 7); InclusiveScan / InclusiveScanInit with MinOp against std::inclusive_scan
+// over signed 64-bit items (signed comparison: negative items are the smaller).
+void scan_min_max_operators() {
+    auto& e = *g_env;
+    {
+        constexpr uint n = 4097u;
+        std::vector<int> a(n), got(n);
+        for (uint i = 0; i < n; ++i) a[i] = static_cast<int>(i % 7u) + 1;
+        auto in = e.device.create_buffer<int>(n);
+        auto out = e.device.create_buffer<int>(n);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<int>(n)));
+        CommandList cmd;
+        e.scan.ExclusiveScan(cmd, temp.view(), in.view(), out.view(), n, MaxOp{}, 0);
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(luisa::span{got}) << synchronize();
+        bool ok = true;
+        for (uint i = 0; i < n; ++i) ok = ok && got[i] == static_cast<int>(std::min(i, 7u));
+        EXPECT(ok);
+    }
+    {
+        const uint n = 3u * 12288u + 11u;
+        std::vector<int64_t> a(n), got(n), got_init(n), want(n), want_init(n);
+        uint64_t x = 0x2545F4914F6CDD1Dull;
+        for (uint i = 0; i < n; ++i) {
+            x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+            a[i] = static_cast<int64_t>(x);
+        }
+        const auto lesser = [](int64_t p, int64_t q) { return std::min(p, q); };
+        std::inclusive_scan(a.begin(), a.end(), want.begin(), lesser);
+        std::inclusive_scan(a.begin(), a.end(), want_init.begin(), lesser, int64_t(-5));
+        auto in = e.device.create_buffer<int64_t>(n);
+        auto out = e.device.create_buffer<int64_t>(n);
+        auto out_init = e.device.create_buffer<int64_t>(n);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetTempStorageBytes<int64_t>(n)));
+        CommandList cmd;
+        e.scan.InclusiveScan(cmd, temp.view(), in.view(), out.view(), n, MinOp{});
+        e.scan.InclusiveScanInit(cmd, temp.view(), in.view(), out_init.view(), n, MinOp{}, int64_t(-5));
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(luisa::span{got})
+                 << out_init.copy_to(luisa::span{got_init}) << synchronize();
+        EXPECT(got == want);
+        EXPECT(got_init == want_init);
+    }
+}
+
 void scan_bench_pattern_vs_std() {
     auto& e = *g_env;
     const uint n = (1u << 22) + 5u;
@@ -1244,6 +1288,7 @@ const std::vector<Case>& cases() {
         {"scan_inclusive_init_in_place", scan_inclusive_init_in_place},
         {"scan_double_inclusive_sum", scan_double_inclusive_sum},
         {"scan_int64_exclusive_vs_std", scan_int64_exclusive_vs_std},
+        {"scan_min_max_operators", scan_min_max_operators},
         {"scan_bench_pattern_vs_std", scan_bench_pattern_vs_std},
         {"radix_stable_partial_bit_ranges", radix_stable_partial_bit_ranges},
         {"radix_zero_width_copies", radix_zero_width_copies},

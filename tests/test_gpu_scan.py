@@ -248,3 +248,136 @@ def test_64bit_in_place_forced_fallback(hip, orc, dev, forced_fallback, n):
     a = orc.generate(0, n, n + 13)
     for inclusive in (False, True):
         assert np.array_equal(gpu_scan_in_place(hip, "u64", a, inclusive), orc.scan_sum_u64(a, inclusive))
+
+
+# ---- min / max operators -------------------------------------------------------------------------
+# DeviceScan<>::ExclusiveScan / InclusiveScan / InclusiveScanInit with MinOp / MaxOp (device_scan.h:321-368,
+# common/thread_operators.h:58-74), bit-exact against the oracle's left-to-right fold for every type.
+MINMAX_SUFFIX = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64,
+                 "f64": np.float64}
+TILE32 = 24576  # 4-byte items per scan tile
+
+
+def gpu_scan_minmax(hip, op, suffix, a, inclusive=False, init=None):
+    n = a.size
+    d_in = to_dev(a)
+    d_out = fill_dev(n, a.dtype.itemsize, 0x7E7E7E7E)
+    hip.scan_minmax(op, suffix, d_in, d_out, n, inclusive=inclusive, init=init)
+    return to_host(d_out, a.dtype)
+
+
+def minmax_input(suffix, n, seed, nan_fraction=0.02):
+    """Full-range integers, or floats with canonical NaNs and no zeros (the sign of a zero tie is tested
+    apart)."""
+    dtype = np.dtype(MINMAX_SUFFIX[suffix])
+    rng = np.random.default_rng(seed)
+    if dtype.kind == "f":
+        a = (rng.standard_normal(n) * 1000).astype(dtype)
+        a[a == 0] = 1
+        a[rng.random(n) < nan_fraction] = np.nan
+        return a
+    info = np.iinfo(dtype)
+    return rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+
+
+def same_bits(x, y):
+    return x.dtype == y.dtype and np.array_equal(x.view(f"u{x.dtype.itemsize}"), y.view(f"u{y.dtype.itemsize}"))
+
+
+def test_scan_max_exclusive_known_answer(hip, dev):
+    """tests/pr6_review_regression_test.cpp:146-151,247-265: exclusive max with init 0 over i % 7 + 1."""
+    n = 4097
+    a = (np.arange(n) % 7 + 1).astype(np.int32)
+    assert np.array_equal(gpu_scan_minmax(hip, "max", "i32", a, init=0), np.minimum(np.arange(n), 7))
+
+
+@pytest.mark.parametrize("suffix", list(MINMAX_SUFFIX))
+@pytest.mark.parametrize("op", ["min", "max"])
+@pytest.mark.parametrize("n", [1, 31, 257, TILE64 - 1, TILE64 + 1, TILE32 + 1, 3 * TILE32 + 7, (1 << 22) + 77])
+def test_scan_minmax_vs_oracle(hip, orc, dev, suffix, op, n):
+    log(f"scan {op} {suffix} n={n}")
+    a = minmax_input(suffix, n, n * 7 + len(suffix))
+    inits = [None, np.nan, 0.5] if a.dtype.kind == "f" else [None, 0, 12345]
+    for inclusive in (False, True):
+        for init in inits:
+            got = gpu_scan_minmax(hip, op, suffix, a, inclusive, init)
+            assert same_bits(got, orc.scan_minmax(op, a, inclusive, init)), (inclusive, init)
+
+
+@pytest.mark.parametrize("suffix", ["i32", "u64", "f32", "f64"])
+def test_scan_minmax_monotone(hip, orc, dev, suffix):
+    """Descending input: every item is a new minimum, so every tile's prefix comes from the look-back."""
+    n = (1 << 22) + 77
+    a = np.arange(n, 0, -1).astype(MINMAX_SUFFIX[suffix])
+    for op in ("min", "max"):
+        for inclusive in (False, True):
+            got = gpu_scan_minmax(hip, op, suffix, a, inclusive)
+            assert same_bits(got, orc.scan_minmax(op, a, inclusive))
+
+
+@pytest.mark.parametrize("suffix", ["f32", "f64"])
+def test_scan_minmax_signed_zero_order(hip, orc, dev, suffix):
+    """Zeros of both signs compare equal and the earlier is kept: +0.0 first and -0.0 everywhere after
+    must give +0.0 at every position across lanes, waves, rows, tiles and look-back windows (an operand
+    swapped anywhere lets a -0.0 through), and the mirror case -0.0 first."""
+    n = (1 << 22) + 77
+    dtype = MINMAX_SUFFIX[suffix]
+    a = np.full(n, -0.0, dtype)
+    a[0] = 0.0
+    rng = np.random.default_rng(5)
+    b = np.where(rng.random(n) < 0.5, dtype(0.0), dtype(-0.0)).astype(dtype)
+    b[0] = -0.0
+    for op in ("min", "max"):
+        for x in (a, b):
+            got = gpu_scan_minmax(hip, op, suffix, x, inclusive=True)
+            assert same_bits(got, orc.scan_minmax(op, x, inclusive=True))
+            assert np.all(np.signbit(got) == np.signbit(x[0]))
+
+
+@pytest.mark.parametrize("suffix", ["u32", "f32", "i64", "f64"])
+def test_scan_minmax_forced_fallback(hip, orc, dev, forced_fallback, suffix):
+    """Predecessors computed by the waiting workgroup fold in the owner's order, signed zeros included."""
+    n = (1 << 22) + 77
+    log(f"scan minmax forced fallback {suffix}")
+    a = minmax_input(suffix, n, 23)
+    for op in ("min", "max"):
+        for inclusive in (False, True):
+            got = gpu_scan_minmax(hip, op, suffix, a, inclusive)
+            assert same_bits(got, orc.scan_minmax(op, a, inclusive))
+    if suffix.startswith("f"):
+        z = np.full(n, -0.0, MINMAX_SUFFIX[suffix])
+        z[0] = 0.0
+        assert not np.any(np.signbit(gpu_scan_minmax(hip, "min", suffix, z, inclusive=True)))
+
+
+def test_scan_minmax_all_nan_prefix(hip, orc, dev):
+    """Floats like fmin / fmax: NaN items are skipped, an all-NaN prefix stays NaN."""
+    for suffix in ("f32", "f64"):
+        a = np.full(TILE32 * 2 + 5, np.nan, MINMAX_SUFFIX[suffix])
+        a[TILE32 + 3] = 2.0
+        a[TILE32 + 9] = -1.0
+        for op in ("min", "max"):
+            got = gpu_scan_minmax(hip, op, suffix, a, inclusive=True)
+            assert same_bits(got, orc.scan_minmax(op, a, inclusive=True))
+            assert np.all(np.isnan(got[:TILE32 + 3])) and got[TILE32 + 3] == 2.0
+
+
+def test_scan_minmax_empty_and_errors(hip, dev):
+    d = torch.empty(0, dtype=torch.int32, device=dev)
+    hip.scan_minmax("min", "i32", d, d, 0)
+    with pytest.raises(ValueError):
+        hip.scan_minmax("sum", "i32", d, d, 0)
+    a = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    with pytest.raises(hip.LcppHipError) as e:
+        hip.scan_minmax("max", "i32", a, a, 1 << 20, temp=torch.empty(2, dtype=torch.int32, device=dev))
+    assert e.value.status == hip.ERR_TEMP_TOO_SMALL
+
+
+def test_scan_minmax_in_place_forced_fallback(hip, orc, dev, forced_fallback):
+    """In place: a claimed tile's owner stores only after its claimer has read the tile."""
+    n = (1 << 22) + 77
+    for suffix in ("i32", "f64"):
+        a = minmax_input(suffix, n, 31)
+        d = to_dev(a)
+        hip.scan_minmax("min", suffix, d, d, n, inclusive=True)
+        assert same_bits(to_host(d, a.dtype), orc.scan_minmax("min", a, inclusive=True))

@@ -290,6 +290,61 @@ def test_scan_f64_known_answer_and_exactness(orc):
     assert np.array_equal(absum.astype(np.int64)[1:], np.cumsum(np.abs(a))[:-1])
 
 
+# ---- min / max scans ----------------------------------------------------------------------------
+def test_scan_max_exclusive_known_answer(orc):
+    """tests/pr6_review_regression_test.cpp:146-151,247-265: ExclusiveScan with max and init 0 over
+    host[i] = i % 7 + 1 (4,097 items) gives the running maximum before i: min(i, 7)."""
+    n = 4097
+    a = (np.arange(n) % 7 + 1).astype(np.int32)
+    assert np.array_equal(orc.scan_minmax("max", a, init=0), np.minimum(np.arange(n), 7).astype(np.int32))
+
+
+def _accumulate(ufunc, a, inclusive, init):
+    """Running min / max by numpy's ufunc.accumulate, with `init` put in front of the items."""
+    if init is None:
+        if inclusive:
+            return ufunc.accumulate(a)
+        init = np.nan if a.dtype.kind == "f" else (np.iinfo(a.dtype).max if ufunc in (np.minimum, np.fmin)
+                                                     else np.iinfo(a.dtype).min)
+    run = ufunc.accumulate(np.concatenate([np.array([init], a.dtype), a]))
+    return run[1:] if inclusive else run[:-1]
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32, np.int64, np.uint64, np.float32, np.float64])
+@pytest.mark.parametrize("op", ["min", "max"])
+def test_scan_minmax_vs_numpy_accumulate(orc, dtype, op):
+    """Integers against np.minimum / np.maximum.accumulate; floats (with NaNs, no signed zeros) against
+    np.fmin / np.fmax.accumulate, which ignore a NaN operand as the operators do."""
+    rng = np.random.default_rng(17)
+    n = 20000
+    if np.dtype(dtype).kind == "f":
+        a = rng.standard_normal(n).astype(dtype) * 1000
+        a[a == 0] = 1
+        a[rng.random(n) < 0.05] = np.nan
+        a[:3] = np.nan  # an all-NaN prefix stays NaN
+        ufunc = np.fmin if op == "min" else np.fmax
+        inits = [None, 1.5, np.nan]
+    else:
+        info = np.iinfo(dtype)
+        a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        ufunc = np.minimum if op == "min" else np.maximum
+        inits = [None, 0, info.max, info.min]
+    for inclusive in (False, True):
+        for init in inits:
+            got = orc.scan_minmax(op, a, inclusive=inclusive, init=init)
+            ref = _accumulate(ufunc, a, inclusive, init)
+            assert np.array_equal(got, ref, equal_nan=np.dtype(dtype).kind == "f"), (inclusive, init)
+
+
+def test_scan_minmax_signed_zero_keeps_earlier(orc):
+    """-0.0 and +0.0 compare equal, so the running value keeps the earlier of the two (sign bit checked)."""
+    a = np.array([0.0, -0.0, -0.0, 0.0], np.float32)
+    for op in ("min", "max"):
+        assert np.signbit(orc.scan_minmax(op, a, inclusive=True)).tolist() == [False] * 4
+        assert np.signbit(orc.scan_minmax(op, -a, inclusive=True)).tolist() == [True] * 4
+    assert np.signbit(orc.scan_minmax("min", a, init=-0.0)).tolist() == [True] * 4
+
+
 # ---- scan-by-key / reduce-by-key ---------------------------------------------------------------
 
 def numpy_by_key(keys, values, key_mask=-1):
