@@ -66,18 +66,22 @@ constexpr int kBkVec = 4;  // consecutive items per thread and row (one 16-byte 
 // covered by the others' loads and stores.
 constexpr int kBkBlocksPerCu = 3;
 // Rows per tile: a thread's keys and values of every row are in flight together (4 * R * (sizeof(K) +
-// sizeof(V)) / 4 VGPRs, 128 for 4-byte keys and values at 16 rows); the scan then keeps only the
-// values, the reduce also the keys it writes out (80 VGPRs of both: 10 rows).  Re-reading the run keys
-// from memory instead, to afford 16 reduce rows, measured slower (ReduceByKey 2^28 0.60 -> 0.89 ms).
+// sizeof(V)) / 4 VGPRs, 128 for 4-byte keys and values at 16 rows).  The scan keeps its values through
+// the look-back; the reduce stages its run heads in LDS before it, so nothing of the rows stays live and
+// 120 VGPRs of keys and values fit (15 rows of 4-byte keys and values; ReduceByKey 2^28 0.61 -> 0.49 ms
+// against 10 rows kept in registers through the look-back).
 #ifndef LCPP_BK_SCAN_VGPRS
 #define LCPP_BK_SCAN_VGPRS 128
 #endif
 #ifndef LCPP_BK_REDUCE_VGPRS
-#define LCPP_BK_REDUCE_VGPRS 80
+#define LCPP_BK_REDUCE_VGPRS 120
 #endif
 template <typename K, typename V, int MODE>
 constexpr int kBkRows = (MODE == 0 ? LCPP_BK_SCAN_VGPRS - (sizeof(V) == 8 ? 16 : 0) : LCPP_BK_REDUCE_VGPRS) /
                         static_cast<int>(sizeof(K) + sizeof(V));
+// Runs a reduce tile stages in LDS (32 KiB of keys and sums).
+template <typename K, typename V>
+constexpr uint32_t kBkStageItems = 32768u / static_cast<uint32_t>(sizeof(K) + sizeof(V));
 template <typename K, typename V, int MODE>
 constexpr uint32_t kBkTileItems = static_cast<uint32_t>(kBkBlock * kBkVec * kBkRows<K, V, MODE>);
 
@@ -366,6 +370,51 @@ __device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32
     store_quad(values_out, first, valid, vec_o, out);
 }
 
+// Reduce outputs of a tile with more runs than the LDS stage holds, after its look-back: each row is
+// read again and folded exactly as before (heads from the edge table, the same wave scans), and every
+// run head writes its key and the sum of the run before it.
+template <typename K, typename V, int R>
+__device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out, V* aggregates_out,
+                                   uint32_t* num_runs_out, uint64_t n, K mask, uint32_t tile, Seg<V> prefix,
+                                   Seg<V> (*s_wave)[kBkWaves], K (*s_edge)[kBkWaves], bool vec_k, bool vec_v) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint64_t tile_base = static_cast<uint64_t>(tile) * (kBkBlock * kBkVec * R);
+    const K before_tile = (tid == 0 && tile_base > 0) ? keys[tile_base - 1] : K(0);
+#pragma unroll 1
+    for (int r = 0; r < R; ++r) {
+        const uint64_t first = row_first<R>(tile, r, tid);
+        K key[kBkVec];
+        V val[kBkVec];
+        load_quad(keys, first, n, vec_k, key);
+        load_quad(values, first, n, vec_v, val);
+        K prev = dpp_move<dpp::kWaveShr1>(K(0), key[kBkVec - 1]);
+        if (lane == 0) prev = wave > 0 ? s_edge[r][wave - 1] : (r > 0 ? s_edge[r - 1][kBkWaves - 1] : before_tile);
+        const uint32_t valid = quad_valid(first, n);
+        const uint32_t h = quad_heads(key, prev, valid, tile == 0 && r == 0 && tid == 0, mask);
+        const Seg<V> incl = wave_seg_scan(fold_quad(val, h, valid));
+        Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl)));
+#pragma unroll
+        for (int k = 0; k < kBkVec; ++k) {
+            if ((valid >> k) & 1u) {
+                if ((h >> k) & 1u) {
+                    if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
+                    unique_out[run.count] = key[k];
+                    run.count += 1;
+                    run.sum = val[k];
+                } else {
+                    run.sum = static_cast<V>(run.sum + val[k]);
+                }
+            }
+        }
+        if (valid != 0 && n - first <= kBkVec) {  // this thread-row holds the last item
+            aggregates_out[run.count - 1] = run.sum;
+            num_runs_out[0] = run.count;
+        }
+    }
+}
+
 template <typename K, typename V, int MODE, int R>
 __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     const K* __restrict__ keys, const V* values_in, V* values_out, K* __restrict__ unique_out,
@@ -385,6 +434,11 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     __shared__ uint32_t s_ctl[2][2];        // look-back decision and helped tile, two alternating rows
     __shared__ Seg<V> s_prefix;
     __shared__ Seg<V> s_agg;
+    // Reduce: the tile's run heads in order (key, and the sum of the items before the head back to the
+    // previous head in the tile, or to the tile's start for the first), staged before the look-back.
+    constexpr uint32_t kStage = MODE == kModeReduce ? kBkStageItems<K, V> : 1u;
+    __shared__ K s_run_key[kStage];
+    __shared__ V s_run_sum[kStage];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = lane_id();
@@ -442,6 +496,34 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     }
     __syncthreads();
     const Seg<V> agg = s_agg;
+
+    // Reduce: a tile of at most kStage runs stages its outputs in LDS now, so its keys and values are
+    // dead during the look-back and the outputs leave as contiguous stores; a tile of more runs reads
+    // its rows again after the look-back (reduce_rows_direct).
+    const bool staged = MODE == kModeReduce && agg.count <= kStage;
+    if constexpr (MODE == kModeReduce) {
+        if (staged) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                Seg<V> run = seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r]));
+                const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
+                const uint32_t valid = full ? 0xFu : quad_valid(row_first<R>(tile, r, tid), n);
+#pragma unroll
+                for (int k = 0; k < kBkVec; ++k) {
+                    if ((valid >> k) & 1u) {
+                        if ((h >> k) & 1u) {
+                            s_run_key[run.count] = key[r][k];
+                            s_run_sum[run.count] = run.sum;
+                            run.count += 1;
+                            run.sum = val[r][k];
+                        } else {
+                            run.sum = static_cast<V>(run.sum + val[r][k]);
+                        }
+                    }
+                }
+            }
+        }
+    }
 
     // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
     // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
@@ -584,34 +666,33 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     }
     __syncthreads();  // outputs only after the claim is settled
 
+    if constexpr (MODE == kModeScan) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r])));
-        const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
-        const uint64_t first = row_first<R>(tile, r, tid);
-        const uint32_t valid = full ? 0xFu : quad_valid(first, n);
-        if constexpr (MODE == kModeScan) {
+        for (int r = 0; r < R; ++r) {
+            const Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r])));
+            const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
+            const uint64_t first = row_first<R>(tile, r, tid);
             if (((stored >> r) & 1u) == 0)
-                scan_quad_outputs(val[r], h, run, inclusive, use_init, init, values_out, first, valid, vec_o);
-        } else {
-#pragma unroll
-            for (int k = 0; k < kBkVec; ++k) {
-                if ((valid >> k) & 1u) {
-                    if ((h >> k) & 1u) {
-                        if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
-                        unique_out[run.count] = key[r][k];
-                        run.count += 1;
-                        run.sum = val[r][k];
-                    } else {
-                        run.sum = static_cast<V>(run.sum + val[r][k]);
-                    }
-                }
-            }
-            if (valid != 0 && n - first <= kBkVec) {  // this thread-row holds the last item
-                aggregates_out[run.count - 1] = run.sum;
-                num_runs_out[0] = run.count;
-            }
+                scan_quad_outputs(val[r], h, run, inclusive, use_init, init, values_out, first,
+                                  full ? 0xFu : quad_valid(first, n), vec_o);
         }
+    } else if (staged) {
+        // Run i of the tile is run prefix.count + i overall; the run before the tile's first head
+        // began in an earlier tile (none before item 0) and takes the prefix's sum.
+        const uint32_t base = prefix.count;
+        for (uint32_t i = tid; i < agg.count; i += kBkBlock) {
+            unique_out[base + i] = s_run_key[i];
+            if (i > 0) aggregates_out[base + i - 1] = s_run_sum[i];
+            else if (base > 0) aggregates_out[base - 1] = static_cast<V>(prefix.sum + s_run_sum[0]);
+        }
+        if (tid == 0 && tile_base + TILE >= n) {  // the tile holding the last item closes the last run
+            const Seg<V> total = seg_combine(prefix, agg);
+            aggregates_out[total.count - 1] = total.sum;
+            num_runs_out[0] = total.count;
+        }
+    } else {
+        reduce_rows_direct<K, V, R>(keys, values_in, unique_out, aggregates_out, num_runs_out, n, mask, tile, prefix,
+                                    s_wave, s_edge, vec_k, vec_v);
     }
 }
 

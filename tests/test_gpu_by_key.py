@@ -3,8 +3,10 @@
 Known answers of the reference's tests (device_scan_test.cpp:325-447, device_reduce_test.cpp:420-512)
 exactly; integer values bit-exact against the oracle for every key/value type and scan mode; float
 values within |got - exact| <= rel * (sum of |terms|) with rel 1e-5 (f32) / 1e-12 (f64), where the
-oracle sums in long double.  Also: tile-boundary sizes (the scan's 16,384-item and the reduce's 10,240-item tiles of 4-byte keys and values), runs spanning many tiles, in-place
-scans, the forced look-back fallback (spin limit 0) and misaligned (element-offset) views."""
+oracle sums in long double.  Also: tile-boundary sizes (the scan's 16,384-item and the reduce's 15,360-item
+tiles of 4-byte keys and values), runs spanning many tiles, reduce tiles with fewer and with more runs than
+the kernel stages in LDS (4,096 for 4-byte keys and values, 2,048 for 8-byte ones), in-place scans, the forced
+look-back fallback (spin limit 0) and misaligned (element-offset) views."""
 import numpy as np
 import pytest
 import torch
@@ -15,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 NP = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64, "f64": np.float64}
 TILE = 16384         # scan tile, 4-byte keys and values
-REDUCE_TILE = 10240  # reduce tile, 4-byte keys and values
+REDUCE_TILE = 15360  # reduce tile, 4-byte keys and values
 
 
 def run_keys(rng, n, mean_len, key_dtype, distinct=1 << 30):
@@ -245,6 +247,40 @@ def test_misaligned_views(hip, orc, dev, which):
            else torch.empty(n, dtype=torch.int32, device=dev))
     hip.scan_by_key("i32", "u32", d_k, d_v, d_o, n, inclusive=True)
     check_scan(orc, keys, vals, to_host(d_o, np.uint32, n), "u32", True, None, -1)
+
+
+@pytest.mark.parametrize("ks,vs", [("u32", "u32"), ("i32", "f32"), ("u64", "i64"), ("i64", "f64"), ("u32", "u64")])
+def test_reduce_staged_and_direct_tiles(hip, orc, dev, ks, vs):
+    """Run lengths 1..6 in 4,096-item stretches: some reduce tiles hold more runs than the LDS stage (they
+    write their outputs row by row after the look-back), others fewer (staged outputs), side by side."""
+    rng = np.random.default_rng(77)
+    n = 40 * TILE + 321
+    length = 1 + (np.arange(n) // 4096) % 6
+    starts = np.zeros(n, bool)
+    pos = 0
+    while pos < n:
+        starts[pos] = True
+        pos += int(length[pos])
+    keys = np.cumsum(starts).astype(NP[ks]) * NP[ks](3)
+    vals = values_for(rng, n, vs)
+    log(f"reduce staged/direct {ks} {vs}")
+    uniq, agg, runs = gpu_reduce_by_key(hip, ks, vs, keys, vals)
+    check_reduce(orc, keys, vals, uniq, agg, runs, vs, -1)
+
+
+def test_reduce_misaligned_keys_and_values(hip, orc, dev):
+    rng = np.random.default_rng(56)
+    n = 9 * TILE + 3
+    keys = run_keys(rng, n, 11.0, np.int32)
+    vals = values_for(rng, n, "u32")
+    d_k = to_dev(np.concatenate([[7], keys]).astype(np.int32))[1:]
+    d_v = to_dev(np.concatenate([[7], vals]).astype(np.uint32))[1:]
+    uniq = fill_dev(n, 4, 0x5A5A5A5A)
+    agg = fill_dev(n, 4, 0x5A5A5A5A)
+    runs = fill_dev(1, 4, 17)
+    hip.reduce_by_key("i32", "u32", d_k, d_v, uniq, agg, runs, n)
+    r = int(to_host(runs, np.uint32, 1)[0])
+    check_reduce(orc, keys, vals, to_host(uniq, np.int32, r), to_host(agg, np.uint32, r), r, "u32", -1)
 
 
 def test_large_random_runs(hip, orc, dev):
