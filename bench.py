@@ -300,7 +300,7 @@ def extra_compact(hip, dev, steps, warmup, extra):
         t = time_steps(call, steps, warmup)
         runs = int(num[0].item())
         moved = 4 * m + per_run * runs
-        kms, _ = kernel_avg_ms(hip, call, "compact", 5)
+        kms, _ = kernel_avg_ms(hip, call, "runs_by_key", 5)
         extra[name] = {**t.fields(), "kernel_ms": round(kms, 5), "runs": runs,
                        "GBps": rate(moved, t.mean), "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 

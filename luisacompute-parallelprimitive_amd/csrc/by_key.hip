@@ -76,9 +76,16 @@ constexpr int kBkBlocksPerCu = 3;
 #ifndef LCPP_BK_REDUCE_VGPRS
 #define LCPP_BK_REDUCE_VGPRS 120
 #endif
+// Run lengths and unique items load keys only: 16 rows of 4-byte keys (the most one wave scan of the
+// (row, wave) totals takes), 12 of 8-byte keys.
+#ifndef LCPP_BK_COUNT_VGPRS
+#define LCPP_BK_COUNT_VGPRS 96
+#endif
 template <typename K, typename V, int MODE>
-constexpr int kBkRows = (MODE == 0 ? LCPP_BK_SCAN_VGPRS - (sizeof(V) == 8 ? 16 : 0) : LCPP_BK_REDUCE_VGPRS) /
-                        static_cast<int>(sizeof(K) + sizeof(V));
+constexpr int kBkRows =
+    MODE == 2 ? (LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) < 16 ? LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) : 16)
+              : (MODE == 0 ? LCPP_BK_SCAN_VGPRS - (sizeof(V) == 8 ? 16 : 0) : LCPP_BK_REDUCE_VGPRS) /
+                    static_cast<int>(sizeof(K) + sizeof(V));
 // Runs a reduce tile stages in LDS (32 KiB of keys and sums).
 template <typename K, typename V>
 constexpr uint32_t kBkStageItems = 32768u / static_cast<uint32_t>(sizeof(K) + sizeof(V));
@@ -98,6 +105,9 @@ constexpr uint64_t kClaimDone = 3;    // the helper's PARTIAL stores have all be
 
 constexpr int kModeScan = 0;
 constexpr int kModeReduce = 1;
+// Reduce of implicit ones (V = uint32_t, no value input): run lengths, the unique items and their run
+// count (DeviceRunLengthEncode::Encode; DeviceSelect::Unique when no lengths are asked for).
+constexpr int kModeCount = 2;
 
 // Look-back decisions broadcast from wave 0.
 constexpr uint32_t kActDone = 0;
@@ -269,6 +279,29 @@ __device__ __forceinline__ uint32_t quad_valid(uint64_t first, uint64_t n) {
     return first >= n ? 0u : (n - first >= kBkVec ? 0xFu : (1u << static_cast<uint32_t>(n - first)) - 1u);
 }
 
+// Adjacent keys differ: integers on the masked bits, floats by value (-0.0 == +0.0, a NaN differs from
+// everything), as the reference's lhs == rhs does.
+template <typename K>
+__device__ __forceinline__ bool keys_differ(K a, K b, K mask) {
+    if constexpr (std::is_floating_point_v<K>) {
+        (void)mask;
+        return !(a == b);
+    } else {
+        return ((a ^ b) & mask) != 0;
+    }
+}
+
+// Values of a thread-row: loaded, or implicit ones (kModeCount).
+template <int MODE, typename V>
+__device__ __forceinline__ void load_values(const V* p, uint64_t first, uint64_t n, bool vec, V (&out)[kBkVec]) {
+    if constexpr (MODE == kModeCount) {
+#pragma unroll
+        for (int k = 0; k < kBkVec; ++k) out[k] = V(1);
+    } else {
+        load_quad(p, first, n, vec, out);
+    }
+}
+
 // Head bits (bit k: item first + k starts a run) of a thread-row, given the key before it; `at_start`:
 // the row's first item is item 0.
 template <typename K>
@@ -276,7 +309,7 @@ __device__ __forceinline__ uint32_t quad_heads(const K (&key)[kBkVec], K prev, u
     uint32_t heads = 0;
 #pragma unroll
     for (int k = 0; k < kBkVec; ++k) {
-        const bool head = (k == 0 && at_start) || ((key[k] ^ prev) & mask) != 0;
+        const bool head = (k == 0 && at_start) || keys_differ(key[k], prev, mask);
         heads |= (head ? 1u : 0u) << k;
         prev = key[k];
     }
@@ -324,7 +357,7 @@ __device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
 // Aggregate of tile `tile`, computed by the whole workgroup with the owner's own arithmetic (same
 // heads, folds, wave scans and combination order, so float sums match bit for bit).  Row by row, with
 // the key before each thread-row read from memory, to keep the helper's registers small.
-template <typename K, typename V, int R>
+template <typename K, typename V, int MODE, int R>
 __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
                                  bool vec_v, Seg<V> (*s_help)[kBkWaves]) {
     const uint32_t tid = threadIdx.x;
@@ -335,7 +368,7 @@ __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uin
         K key[kBkVec];
         V val[kBkVec];
         load_quad(keys, first, n, vec_k, key);
-        load_quad(values, first, n, vec_v, val);
+        load_values<MODE>(values, first, n, vec_v, val);
         const K prev = (first > 0 && first - 1 < n) ? keys[first - 1] : K(0);
         const uint32_t valid = quad_valid(first, n);
         const Seg<V> incl = wave_seg_scan(fold_quad(val, quad_heads(key, prev, valid, first == 0, mask), valid));
@@ -373,7 +406,7 @@ __device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32
 // Reduce outputs of a tile with more runs than the LDS stage holds, after its look-back: each row is
 // read again and folded exactly as before (heads from the edge table, the same wave scans), and every
 // run head writes its key and the sum of the run before it.
-template <typename K, typename V, int R>
+template <typename K, typename V, int MODE, int R>
 __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out, V* aggregates_out,
                                    uint32_t* num_runs_out, uint64_t n, K mask, uint32_t tile, Seg<V> prefix,
                                    Seg<V> (*s_wave)[kBkWaves], K (*s_edge)[kBkWaves], bool vec_k, bool vec_v) {
@@ -388,7 +421,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
         K key[kBkVec];
         V val[kBkVec];
         load_quad(keys, first, n, vec_k, key);
-        load_quad(values, first, n, vec_v, val);
+        load_values<MODE>(values, first, n, vec_v, val);
         K prev = dpp_move<dpp::kWaveShr1>(K(0), key[kBkVec - 1]);
         if (lane == 0) prev = wave > 0 ? s_edge[r][wave - 1] : (r > 0 ? s_edge[r - 1][kBkWaves - 1] : before_tile);
         const uint32_t valid = quad_valid(first, n);
@@ -399,7 +432,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
         for (int k = 0; k < kBkVec; ++k) {
             if ((valid >> k) & 1u) {
                 if ((h >> k) & 1u) {
-                    if (run.count > 0) aggregates_out[run.count - 1] = run.sum;
+                    if (run.count > 0 && aggregates_out) aggregates_out[run.count - 1] = run.sum;
                     unique_out[run.count] = key[k];
                     run.count += 1;
                     run.sum = val[k];
@@ -409,7 +442,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
             }
         }
         if (valid != 0 && n - first <= kBkVec) {  // this thread-row holds the last item
-            aggregates_out[run.count - 1] = run.sum;
+            if (aggregates_out) aggregates_out[run.count - 1] = run.sum;
             num_runs_out[0] = run.count;
         }
     }
@@ -421,7 +454,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     V* __restrict__ aggregates_out, uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
     uint64_t* __restrict__ states, int inclusive, int use_init, V init, bool vec_k, bool vec_v, bool vec_o,
     bool in_place, uint32_t spin_limit) {
-    constexpr bool COUNTED = MODE == kModeReduce;
+    constexpr bool COUNTED = MODE != kModeScan;
     constexpr int W = kStateWords<V, COUNTED>;
     uint64_t* const claims = states + static_cast<uint64_t>(gridDim.x) * W;
     // The thread that publishes this tile's states and closes its claim word: lane 0 of the last
@@ -436,7 +469,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     __shared__ Seg<V> s_agg;
     // Reduce: the tile's run heads in order (key, and the sum of the items before the head back to the
     // previous head in the tile, or to the tile's start for the first), staged before the look-back.
-    constexpr uint32_t kStage = MODE == kModeReduce ? kBkStageItems<K, V> : 1u;
+    constexpr uint32_t kStage = MODE != kModeScan ? kBkStageItems<K, V> : 1u;
     __shared__ K s_run_key[kStage];
     __shared__ V s_run_sum[kStage];
 
@@ -456,13 +489,14 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             load_quad_vec(keys, row_first<R>(tile, r, tid), key[r]);
-            load_quad_vec(values_in, row_first<R>(tile, r, tid), val[r]);
+            if constexpr (MODE == kModeCount) load_values<MODE>(values_in, 0, 0, true, val[r]);
+            else load_quad_vec(values_in, row_first<R>(tile, r, tid), val[r]);
         }
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             load_quad_any(keys, row_first<R>(tile, r, tid), n, key[r]);
-            load_quad_any(values_in, row_first<R>(tile, r, tid), n, val[r]);
+            load_values<MODE>(values_in, row_first<R>(tile, r, tid), n, false, val[r]);
         }
     }
     const K before_tile = (tid == 0 && tile_base > 0) ? keys[tile_base - 1] : K(0);
@@ -500,8 +534,8 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     // Reduce: a tile of at most kStage runs stages its outputs in LDS now, so its keys and values are
     // dead during the look-back and the outputs leave as contiguous stores; a tile of more runs reads
     // its rows again after the look-back (reduce_rows_direct).
-    const bool staged = MODE == kModeReduce && agg.count <= kStage;
-    if constexpr (MODE == kModeReduce) {
+    const bool staged = MODE != kModeScan && agg.count <= kStage;
+    if constexpr (MODE != kModeScan) {
         if (staged) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -640,7 +674,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
             const bool claimed = s_ctl[row][0] != 0;
             row ^= 1u;
             if (claimed) {
-                const Seg<V> h = tile_aggregate<K, V, R>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_help);
+                const Seg<V> h = tile_aggregate<K, V, MODE, R>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_help);
                 if (tid == 0) {
                     publish_state<V, COUNTED>(slot, kStPartial, h);
                     __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -682,40 +716,61 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         const uint32_t base = prefix.count;
         for (uint32_t i = tid; i < agg.count; i += kBkBlock) {
             unique_out[base + i] = s_run_key[i];
-            if (i > 0) aggregates_out[base + i - 1] = s_run_sum[i];
-            else if (base > 0) aggregates_out[base - 1] = static_cast<V>(prefix.sum + s_run_sum[0]);
+            if (aggregates_out) {
+                if (i > 0) aggregates_out[base + i - 1] = s_run_sum[i];
+                else if (base > 0) aggregates_out[base - 1] = static_cast<V>(prefix.sum + s_run_sum[0]);
+            }
         }
         if (tid == 0 && tile_base + TILE >= n) {  // the tile holding the last item closes the last run
             const Seg<V> total = seg_combine(prefix, agg);
-            aggregates_out[total.count - 1] = total.sum;
+            if (aggregates_out) aggregates_out[total.count - 1] = total.sum;
             num_runs_out[0] = total.count;
         }
     } else {
-        reduce_rows_direct<K, V, R>(keys, values_in, unique_out, aggregates_out, num_runs_out, n, mask, tile, prefix,
+        reduce_rows_direct<K, V, MODE, R>(keys, values_in, unique_out, aggregates_out, num_runs_out, n, mask, tile, prefix,
                                     s_wave, s_edge, vec_k, vec_v);
     }
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+bool ranges_overlap(const void* a, uint64_t a_bytes, const void* b, uint64_t b_bytes) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return a_bytes != 0 && b_bytes != 0 && x < y + b_bytes && y < x + a_bytes;
+}
+
 template <typename K, typename V, int MODE>
 int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* values_out, K* unique_out,
            V* aggregates_out, uint32_t* num_runs_out, uint64_t n, uint64_t key_mask, int inclusive, int use_init,
            V init, void* stream_ptr) {
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const char* what = MODE == kModeScan ? "DeviceScan::ScanByKey" : "DeviceReduce::ReduceByKey";
+    const char* what = MODE == kModeScan     ? "DeviceScan::ScanByKey"
+                       : MODE == kModeReduce ? "DeviceReduce::ReduceByKey"
+                                             : "DeviceRunLengthEncode::Encode";
     if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items", what);
-    if constexpr (MODE == kModeReduce) {
+    if constexpr (MODE != kModeScan) {
         if (!num_runs_out) return set_error(kInvalidArgument, "%s: null run-count output", what);
         if (n == 0) return launch_fill_u32(num_runs_out, 1, 0u, stream);
-        if (!unique_out || !aggregates_out) return set_error(kInvalidArgument, "%s: null output", what);
+        if (!unique_out || (MODE == kModeReduce && !aggregates_out)) return set_error(kInvalidArgument, "%s: null output", what);
     } else {
         if (n == 0) return kOk;
         if (!values_out) return set_error(kInvalidArgument, "%s: null output", what);
     }
-    if (!keys || !values_in) return set_error(kInvalidArgument, "%s: null input", what);
+    if (!keys || (MODE != kModeCount && !values_in)) return set_error(kInvalidArgument, "%s: null input", what);
+    if constexpr (MODE != kModeScan) {
+        // A tile with more runs than its LDS stage reads its input again after its look-back, when later
+        // tiles may already be writing runs: outputs overlapping the inputs would race with that read.
+        const uint64_t out_bytes[2] = {n * sizeof(K), aggregates_out ? n * sizeof(V) : 0};
+        const uint64_t in_bytes[2] = {n * sizeof(K), MODE == kModeReduce ? n * sizeof(V) : 0};
+        const void* outs[2] = {unique_out, aggregates_out};
+        const void* ins[2] = {keys, values_in};
+        for (int o = 0; o < 2; ++o)
+            for (int i = 0; i < 2; ++i)
+                if (ranges_overlap(outs[o], out_bytes[o], ins[i], in_bytes[i]))
+                    return set_error(kInvalidArgument, "%s: outputs must not overlap the inputs", what);
+    }
     constexpr uint32_t kTile = kBkTileItems<K, V, MODE>;
-    const size_t need = state_bytes(n, kTile, sizeof(V), MODE == kModeReduce);
+    const size_t need = state_bytes(n, kTile, sizeof(V), MODE != kModeScan);
     if (!temp || temp_bytes < need)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, need);
     if (reinterpret_cast<uintptr_t>(temp) % 8 != 0) return set_error(kInvalidArgument, "%s: temp not 8-byte aligned", what);
@@ -723,7 +778,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     int st = launch_fill_u32(reinterpret_cast<uint32_t*>(states), need / 4, 0u, stream);
     if (st != kOk) return st;
     const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kTile));
-    LaunchScope scope(MODE == kModeScan ? "scan_by_key" : "reduce_by_key", stream);
+    LaunchScope scope(MODE == kModeScan ? "scan_by_key" : MODE == kModeReduce ? "reduce_by_key" : "runs_by_key", stream);
     by_key_kernel<K, V, MODE, kBkRows<K, V, MODE>><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
@@ -732,6 +787,32 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
 }
 
 }  // namespace
+
+// Run-length encode (counts_out non-null) or unique (counts_out null) over the by-key reduce kernels
+// with implicit ones: keys compare on the masked bits (integers) or by value (floats).  Returns
+// kRunsDeclined without doing anything when the outputs overlap the input (in-place forms) or the
+// temp storage is smaller than the tile states, so the caller can take its general path.
+template <typename K>
+int runs_by_key(void* temp, size_t temp_bytes, const K* in, K* unique_out, uint32_t* counts_out, uint32_t* num_out,
+                uint64_t n, uint64_t key_mask, hipStream_t stream) {
+    if (n > 0 && n <= 0xFFFFFFFFull) {
+        const size_t need = state_bytes(n, kBkTileItems<K, uint32_t, kModeCount>, sizeof(uint32_t), true);
+        if (!temp || temp_bytes < need || ranges_overlap(unique_out, n * sizeof(K), in, n * sizeof(K)) ||
+            ranges_overlap(counts_out, counts_out ? n * 4 : 0, in, n * sizeof(K)))
+            return kRunsDeclined;
+    }
+    return by_key<K, uint32_t, kModeCount>(temp, temp_bytes, in, nullptr, nullptr, unique_out, counts_out, num_out, n,
+                                           key_mask, 0, 0, 0u, stream);
+}
+template int runs_by_key<uint32_t>(void*, size_t, const uint32_t*, uint32_t*, uint32_t*, uint32_t*, uint64_t, uint64_t,
+                                   hipStream_t);
+template int runs_by_key<uint64_t>(void*, size_t, const uint64_t*, uint64_t*, uint32_t*, uint32_t*, uint64_t, uint64_t,
+                                   hipStream_t);
+template int runs_by_key<float>(void*, size_t, const float*, float*, uint32_t*, uint32_t*, uint64_t, uint64_t,
+                                hipStream_t);
+template int runs_by_key<double>(void*, size_t, const double*, double*, uint32_t*, uint32_t*, uint64_t, uint64_t,
+                                 hipStream_t);
+
 }  // namespace lcpp_hip
 
 using namespace lcpp_hip;

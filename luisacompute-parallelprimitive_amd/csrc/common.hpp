@@ -19,6 +19,14 @@ namespace lcpp_hip {
 
 constexpr int kWave = 64;
 
+// Returned by an alternative implementation that leaves a call to the general one (not an error).
+constexpr int kRunsDeclined = 1;
+// by_key.hip: DeviceRunLengthEncode::Encode (counts_out non-null) or DeviceSelect::Unique (null) over the
+// by-key reduce kernels; K is uint32_t, uint64_t, float or double.
+template <typename K>
+int runs_by_key(void* temp, size_t temp_bytes, const K* in, K* unique_out, uint32_t* counts_out, uint32_t* num_out,
+                uint64_t n, uint64_t key_mask, hipStream_t stream);
+
 // ------------------------------------------------------------------------------------------------
 // Arithmetic operators (the subset of common/thread_operators.h used on the hot path).
 // ------------------------------------------------------------------------------------------------

@@ -884,6 +884,9 @@ size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int
     int lcpp_hip_select_unique_##TS(void* temp, size_t temp_bytes, const TT* in, TT* out,                           \
                                     uint32_t* num_selected_out, uint64_t n, uint64_t key_mask, void* stream) {      \
         using K = KeyOf<TT>;                                                                                         \
+        const int fast = runs_by_key<K>(temp, temp_bytes, reinterpret_cast<const K*>(in), reinterpret_cast<K*>(out), \
+                                        nullptr, num_selected_out, n, key_mask, static_cast<hipStream_t>(stream));  \
+        if (fast != kRunsDeclined) return fast;                                                                      \
         Outputs o;                                                                                                   \
         o.out = out;                                                                                                 \
         o.num_out = num_selected_out;                                                                                \
@@ -895,6 +898,10 @@ size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int
     int lcpp_hip_run_length_encode_##TS(void* temp, size_t temp_bytes, const TT* in, TT* unique_out,                \
                                         uint32_t* counts_out, uint32_t* num_runs_out, uint64_t n, void* stream) {   \
         using K = KeyOf<TT>;                                                                                         \
+        const int fast = runs_by_key<K>(temp, temp_bytes, reinterpret_cast<const K*>(in),                           \
+                                        reinterpret_cast<K*>(unique_out), counts_out, num_runs_out, n, ~0ull,       \
+                                        static_cast<hipStream_t>(stream));                                           \
+        if (fast != kRunsDeclined) return fast;                                                                      \
         Outputs o;                                                                                                   \
         o.out = unique_out;                                                                                          \
         o.aux0 = counts_out;                                                                                         \

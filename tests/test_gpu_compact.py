@@ -248,9 +248,10 @@ def test_run_length_encode_known_answers(hip, dev):
         assert int(to_host(num, np.uint32, 1)[0]) == 0
 
 
-# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles) and their multiples.
+# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles), 12,288 and 16,384 (the
+# run kernels' tiles of eight- and four-byte items) and their multiples.
 @pytest.mark.parametrize("count", [1, 2, 3, 31, 32, 33, 3839, 3840, 3841, 4095, 4096, 4097, 5761, 8191, 8192, 8193,
-                                   16383, 16384, 16385, 32769, 230413])
+                                   12287, 12288, 12289, 16383, 16384, 16385, 24577, 32769, 49153, 230413])
 def test_run_length_encode_long_runs_across_tiles(hip, orc, dev, count):
     """device_run_length_encode_test.cpp:74-136: x[i] = i / run_length for run lengths 1, 2, 17, 18001, n."""
     for run_length in (1, 2, 17, 18001, count):
@@ -349,6 +350,41 @@ def test_run_length_and_unique_types(hip, orc, dev, ts):
     for mean in (1.2, 9.0, 700.0):
         x = runs_of(rng, 5 * T4 + 77, mean, NP[ts])
         check_all_runs(hip, orc, x)
+
+
+@pytest.mark.parametrize("ts", ["u32", "f32", "i64", "f64"])
+def test_runs_staged_and_direct_tiles(hip, orc, dev, ts):
+    """Run lengths 1..6 in 4,096-item stretches: tiles with more runs than the run kernel stages in LDS
+    (4,096 for four-byte items, 2,730 for eight-byte ones) write them row by row, the others from LDS."""
+    n = 30 * 16384 + 5
+    length = 1 + (np.arange(n) // 4096) % 6
+    starts = np.zeros(n, bool)
+    pos = 0
+    while pos < n:
+        starts[pos] = True
+        pos += int(length[pos])
+    x = (np.cumsum(starts) % 1000).astype(NP[ts])
+    log(f"runs staged/direct {ts}")
+    check_all_runs(hip, orc, x)
+
+
+def test_unique_and_encode_overlapping_outputs(hip, orc, dev):
+    """Unique in place (a select's in-place form) and an encode whose unique output is its input take the
+    general compaction path; results match the oracle."""
+    rng = np.random.default_rng(8)
+    x = runs_of(rng, 40 * T4 + 3, 5.0, np.int32, distinct=7)
+    g, k = g_unique(hip, x, in_place=True)
+    want, wk = orc.select(x, orc.run_heads(x))
+    assert k == wk and np.array_equal(g, want[:k])
+    d = to_dev(x)
+    co = fill_dev(x.size, 4, 0x5A)
+    num = fill_dev(1, 4, 99)
+    hip.run_length_encode("i32", d, d, co, num, x.size)
+    r = int(to_host(num, np.uint32, 1)[0])
+    wu, wc = orc.run_length_encode(x)
+    assert r == wu.size
+    np.testing.assert_array_equal(to_host(d, np.int32, r), wu)
+    np.testing.assert_array_equal(to_host(co, np.uint32, r), wc)
 
 
 def test_float_run_equality_is_by_value(hip, orc, dev):
