@@ -76,14 +76,14 @@ constexpr int kBkBlocksPerCu = 3;
 #ifndef LCPP_BK_REDUCE_VGPRS
 #define LCPP_BK_REDUCE_VGPRS 120
 #endif
-// Run lengths and unique items load keys only: 16 rows of 4-byte keys (the most one wave scan of the
-// (row, wave) totals takes), 12 of 8-byte keys.
+// Run lengths and unique items load keys only and keep no per-row scans: 28 rows of 4-byte keys, 14 of
+// 8-byte keys (Encode 2^28 u32 in runs of 64: 0.316 ms at 16 rows, 0.314 at 24, 0.303 at 28).
 #ifndef LCPP_BK_COUNT_VGPRS
-#define LCPP_BK_COUNT_VGPRS 96
+#define LCPP_BK_COUNT_VGPRS 112
 #endif
 template <typename K, typename V, int MODE>
 constexpr int kBkRows =
-    MODE == 2 ? (LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) < 16 ? LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) : 16)
+    MODE == 2 ? (LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) < 32 ? LCPP_BK_COUNT_VGPRS / static_cast<int>(sizeof(K)) : 32)
               : (MODE == 0 ? LCPP_BK_SCAN_VGPRS - (sizeof(V) == 8 ? 16 : 0) : LCPP_BK_REDUCE_VGPRS) /
                     static_cast<int>(sizeof(K) + sizeof(V));
 // Runs a reduce tile stages in LDS (32 KiB of keys and sums).
@@ -338,16 +338,37 @@ __device__ __forceinline__ uint64_t row_first(uint32_t tile, int r, uint32_t tid
 }
 
 // Carries and aggregate from the (row, wave) totals, by wave 0: lane l takes total l (row l / 4, wave
-// l % 4; R * 4 <= 64), one wave scan gives every (row, wave) its in-tile carry (the totals before it, in
-// row-major order), written back over the table, and lane 63 the tile aggregate, which wave 0 returns.
+// l % 4) when R * 4 <= 64, else P = ceil(R * 4 / 64) consecutive totals folded in order; one wave scan gives
+// every (row, wave) its in-tile carry (the totals before it, in row-major order), written back over
+// the table, and lane 63 the tile aggregate, which wave 0 returns.
 template <typename V, int R>
 __device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
-    static_assert(R * kBkWaves <= kWave, "one wave scans the (row, wave) totals");
+    constexpr int E = R * kBkWaves;
+    constexpr int P = (E + kWave - 1) / kWave;
     const uint32_t lane = lane_id();
     Seg<V>* flat = &s_wave[0][0];
-    const Seg<V> t = lane < static_cast<uint32_t>(R * kBkWaves) ? flat[lane] : Seg<V>{0u, V(0)};
-    const Seg<V> incl = wave_seg_scan(t);
-    if (lane < static_cast<uint32_t>(R * kBkWaves)) flat[lane] = wave_seg_exclusive(incl);
+    Seg<V> incl;
+    if constexpr (P == 1) {
+        const Seg<V> t = lane < static_cast<uint32_t>(E) ? flat[lane] : Seg<V>{0u, V(0)};
+        incl = wave_seg_scan(t);
+        if (lane < static_cast<uint32_t>(E)) flat[lane] = wave_seg_exclusive(incl);
+    } else {
+        const uint32_t first = lane * P;
+        Seg<V> t = first < static_cast<uint32_t>(E) ? flat[first] : Seg<V>{0u, V(0)};
+#pragma unroll
+        for (int p = 1; p < P; ++p)
+            if (first + p < static_cast<uint32_t>(E)) t = seg_combine(t, flat[first + p]);
+        incl = wave_seg_scan(t);
+        Seg<V> run = wave_seg_exclusive(incl);
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (first + p < static_cast<uint32_t>(E)) {
+                const Seg<V> x = flat[first + p];
+                flat[first + p] = run;
+                run = seg_combine(run, x);
+            }
+        }
+    }
     Seg<V> agg;
     agg.count = wave_read_lane(incl.count, kWave - 1);
     agg.sum = wave_read_lane(incl.sum, kWave - 1);
@@ -511,7 +532,10 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     uint32_t heads[(R + 7) / 8];  // four bits per row
 #pragma unroll
     for (int i = 0; i < (R + 7) / 8; ++i) heads[i] = 0;
-    Seg<V> incl[R];
+    // Run lengths (kModeCount) need no per-row scan: a wave-row's state is its head count and the
+    // items after its last head, both read off four ballots of the head bits.
+    constexpr bool kBallotRuns = MODE == kModeCount;
+    Seg<V> incl[kBallotRuns ? 1 : R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         K prev = dpp_move<dpp::kWaveShr1>(K(0), key[r][kBkVec - 1]);
@@ -519,8 +543,25 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         const uint32_t valid = full ? 0xFu : quad_valid(row_first<R>(tile, r, tid), n);
         const uint32_t h = quad_heads(key[r], prev, valid, tile == 0 && r == 0 && tid == 0, mask);
         heads[r / 8] |= h << (4 * (r % 8));
-        incl[r] = wave_seg_scan(fold_quad(val[r], h, valid));
-        if (lane == kWave - 1) s_wave[r][wave] = incl[r];
+        if constexpr (kBallotRuns) {
+            // Heads of the wave-row, and the item index of its last head (the state's sum counts the
+            // items from that head on; all items when there is none).
+            uint32_t count = 0, last = 0;
+#pragma unroll
+            for (int k = 0; k < kBkVec; ++k) {
+                const uint64_t b = wave_ballot((h >> k) & 1u);
+                count += static_cast<uint32_t>(__builtin_popcountll(b));
+                if (b != 0) last = max(last, 4u * (63u - static_cast<uint32_t>(__builtin_clzll(b))) + k);
+            }
+            if (lane == 0) {
+                const uint64_t row_base = row_first<R>(tile, r, wave * kWave);
+                const uint32_t items = row_base >= n ? 0u : static_cast<uint32_t>(min<uint64_t>(n - row_base, kWave * kBkVec));
+                s_wave[r][wave] = Seg<V>{count, static_cast<V>(count != 0 ? items - last : items)};
+            }
+        } else {
+            incl[r] = wave_seg_scan(fold_quad(val[r], h, valid));
+            if (lane == kWave - 1) s_wave[r][wave] = incl[r];
+        }
     }
     __syncthreads();
     // Wave 0 turns the totals into in-tile carries and the aggregate (to LDS for the publisher).
@@ -535,7 +576,28 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     // dead during the look-back and the outputs leave as contiguous stores; a tile of more runs reads
     // its rows again after the look-back (reduce_rows_direct).
     const bool staged = MODE != kModeScan && agg.count <= kStage;
-    if constexpr (MODE != kModeScan) {
+    if constexpr (kBallotRuns) {
+        // Run heads in order: the wave-row's carry, the heads of lower lanes (ballot ranks) and of the
+        // quad's lower items.  Staged: key and tile-local position (lengths are position differences).
+        if (staged) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
+                uint32_t idx = s_wave[r][wave].count;
+#pragma unroll
+                for (int k = 0; k < kBkVec; ++k) idx += popc_lanes_below(wave_ballot((h >> k) & 1u));
+                const uint32_t pos = static_cast<uint32_t>(r) * (kBkBlock * kBkVec) + tid * kBkVec;
+#pragma unroll
+                for (int k = 0; k < kBkVec; ++k) {
+                    if ((h >> k) & 1u) {
+                        s_run_key[idx] = key[r][k];
+                        s_run_sum[idx] = static_cast<V>(pos + k);
+                        ++idx;
+                    }
+                }
+            }
+        }
+    } else if constexpr (MODE != kModeScan) {
         if (staged) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -717,8 +779,10 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         for (uint32_t i = tid; i < agg.count; i += kBkBlock) {
             unique_out[base + i] = s_run_key[i];
             if (aggregates_out) {
-                if (i > 0) aggregates_out[base + i - 1] = s_run_sum[i];
-                else if (base > 0) aggregates_out[base - 1] = static_cast<V>(prefix.sum + s_run_sum[0]);
+                // Run lengths: staged positions (differences of consecutive heads) for kModeCount.
+                const V before = i > 0 ? (kBallotRuns ? static_cast<V>(s_run_sum[i] - s_run_sum[i - 1]) : s_run_sum[i])
+                                       : static_cast<V>(prefix.sum + s_run_sum[0]);
+                if (i > 0 || base > 0) aggregates_out[base + i - 1] = before;
             }
         }
         if (tid == 0 && tile_base + TILE >= n) {  // the tile holding the last item closes the last run

@@ -248,10 +248,11 @@ def test_run_length_encode_known_answers(hip, dev):
         assert int(to_host(num, np.uint32, 1)[0]) == 0
 
 
-# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles), 12,288 and 16,384 (the
+# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles), 14,336 and 28,672 (the
 # run kernels' tiles of eight- and four-byte items) and their multiples.
 @pytest.mark.parametrize("count", [1, 2, 3, 31, 32, 33, 3839, 3840, 3841, 4095, 4096, 4097, 5761, 8191, 8192, 8193,
-                                   12287, 12288, 12289, 16383, 16384, 16385, 24577, 32769, 49153, 230413])
+                                   14335, 14336, 14337, 16383, 16384, 16385, 28671, 28672, 28673, 32769, 57345,
+                                   230413])
 def test_run_length_encode_long_runs_across_tiles(hip, orc, dev, count):
     """device_run_length_encode_test.cpp:74-136: x[i] = i / run_length for run lengths 1, 2, 17, 18001, n."""
     for run_length in (1, 2, 17, 18001, count):
@@ -356,7 +357,7 @@ def test_run_length_and_unique_types(hip, orc, dev, ts):
 def test_runs_staged_and_direct_tiles(hip, orc, dev, ts):
     """Run lengths 1..6 in 4,096-item stretches: tiles with more runs than the run kernel stages in LDS
     (4,096 for four-byte items, 2,730 for eight-byte ones) write them row by row, the others from LDS."""
-    n = 30 * 16384 + 5
+    n = 20 * 28672 + 5
     length = 1 + (np.arange(n) // 4096) % 6
     starts = np.zeros(n, bool)
     pos = 0
