@@ -572,6 +572,19 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     __syncthreads();
     const Seg<V> agg = s_agg;
 
+    // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
+    // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
+    // first stores the same PARTIAL values.  Before the reduce's staging, so successors see it sooner.
+    uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
+    bool owned = true;
+    if (tid == kPublisher) {
+        const uint32_t st = tile == 0 ? kStInclusive : kStPartial;
+        publish_state<V, COUNTED>(my_slot, st, agg);
+        uint64_t expected = kClaimOpen;
+        owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // Reduce: a tile of at most kStage runs stages its outputs in LDS now, so its keys and values are
     // dead during the look-back and the outputs leave as contiguous stores; a tile of more runs reads
     // its rows again after the look-back (reduce_rows_direct).
@@ -619,19 +632,6 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                 }
             }
         }
-    }
-
-    // Publish PARTIAL (INCLUSIVE for tile 0) with plain stores, then close the claim word; the
-    // compare-and-swap's result is only needed after the look-back.  A helper that claimed the tile
-    // first stores the same PARTIAL values.
-    uint64_t* const my_slot = states + static_cast<uint64_t>(tile) * W;
-    bool owned = true;
-    if (tid == kPublisher) {
-        const uint32_t st = tile == 0 ? kStInclusive : kStPartial;
-        publish_state<V, COUNTED>(my_slot, st, agg);
-        uint64_t expected = kClaimOpen;
-        owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // In-tile carry into each thread-row: rows before it, waves before it in its row, lanes before it.
