@@ -175,6 +175,15 @@ def extra_reduce(hip, dev, steps, warmup, extra):
     t = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
     extra["reduce_sum_i32_2p28"] = {**t.fields(), "GBps": rate(4 * m, t.mean),
                                     "frac": round(4 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
+    # DeviceReduce::Min and ArgMin over the same 2^28 int32 items (the same bytes read).
+    t = time_steps(lambda: hip.reduce_minmax("min", "i32", a, s, m, temp=rt), steps, warmup)
+    extra["reduce_min_i32_2p28"] = {**t.fields(), "GBps": rate(4 * m, t.mean),
+                                    "frac": round(4 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
+    at = torch.empty(hip.bytes_to_uint_count(hip.reduce_arg_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
+    ix = torch.empty(1, dtype=torch.int32, device=dev)
+    t = time_steps(lambda: hip.reduce_arg("min", "i32", a, s, ix, m, temp=at), steps, warmup)
+    extra["reduce_argmin_i32_2p28"] = {**t.fields(), "GBps": rate(4 * m, t.mean),
+                                       "frac": round(4 * m / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def extra_scan(hip, dev, steps, warmup, extra, copy=None):

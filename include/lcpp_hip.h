@@ -86,6 +86,31 @@ int lcpp_hip_reduce_sum_f32(void* temp, size_t temp_bytes, const float* in, floa
 int lcpp_hip_reduce_sum_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, void* stream);
 int lcpp_hip_reduce_sum_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, void* stream);
 int lcpp_hip_reduce_sum_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, void* stream);
+/* DeviceReduce<>::Min / Max (device_reduce.h:291-309): the fold of the items with the reference's MinOp /
+ * MaxOp (common/thread_operators.h:58-74) and its initial value, the type's max / lowest (so an empty
+ * input writes that value).  Signed types compare as signed; floats like fmin / fmax (a NaN item is
+ * skipped; of -0.0 and +0.0 either may result).  Temp: lcpp_hip_reduce_temp_bytes(n, sizeof(T)). */
+#define LCPP_HIP_DECLARE_REDUCE_EXT(S, T)                                                                        \
+    int lcpp_hip_reduce_min_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, void* stream);  \
+    int lcpp_hip_reduce_max_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, void* stream);  \
+    int lcpp_hip_reduce_argmin_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint32_t* out_index,      \
+                                   uint64_t n, void* stream);                                                  \
+    int lcpp_hip_reduce_argmax_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint32_t* out_index,      \
+                                   uint64_t n, void* stream);
+/* DeviceReduce<>::ArgMin / ArgMax (device_reduce.h:311-436, ArgMinOp / ArgMaxOp of
+ * common/thread_operators.h:10-47): *out = the smallest (largest) item, *out_index = its index, the lowest
+ * index among equal items (-0.0 == +0.0); NaN items never win (an all-NaN input gives the initial pair:
+ * the type's max / lowest and index 0xFFFFFFFF); n == 0 writes the type's max / lowest and index 1.
+ * Temp: lcpp_hip_reduce_arg_temp_bytes(n, sizeof(T)), the reference's GetArgTempStorageBytes (the
+ * kernels use 8-12 bytes per workgroup of it). */
+LCPP_HIP_DECLARE_REDUCE_EXT(i32, int32_t)
+LCPP_HIP_DECLARE_REDUCE_EXT(u32, uint32_t)
+LCPP_HIP_DECLARE_REDUCE_EXT(f32, float)
+LCPP_HIP_DECLARE_REDUCE_EXT(i64, int64_t)
+LCPP_HIP_DECLARE_REDUCE_EXT(u64, uint64_t)
+LCPP_HIP_DECLARE_REDUCE_EXT(f64, double)
+#undef LCPP_HIP_DECLARE_REDUCE_EXT
+size_t lcpp_hip_reduce_arg_temp_bytes(uint64_t n, size_t elem_bytes);
 
 /* ---------------------------------------------------------------------------------------------
  * DeviceScan::ExclusiveSum / InclusiveSum (decoupled look-back, single pass)

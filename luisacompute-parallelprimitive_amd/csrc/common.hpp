@@ -13,6 +13,7 @@
 #include <atomic>
 #include <cstdint>
 #include <cstddef>
+#include <limits>
 #include <type_traits>
 
 namespace lcpp_hip {
@@ -35,6 +36,37 @@ struct SumOp {
     __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
     template <typename T>
     __device__ __forceinline__ static constexpr T identity() { return T(0); }
+};
+
+// Min / max operators: the reference's MinOp and MaxOp (common/thread_operators.h:58-74).  They compare
+// in the item's own type, floats like fmin / fmax (a NaN operand yields the other one; -0.0 and +0.0
+// compare equal, so the older is kept).  Identities: the type's max / lowest for integers; a quiet NaN
+// for floats, the one value that every float operand, NaN included, absorbs (op(x, NaN) = op(NaN, x) =
+// x), so padding and empty prefixes leave a scan or a reduction equal to the left-to-right fold of its
+// items.
+struct MinValueOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const {
+        if constexpr (std::is_floating_point_v<T>) return (b < a || a != a) ? b : a;  // a NaN operand yields the other
+        else return b < a ? b : a;
+    }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() {
+        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
+        else return std::numeric_limits<T>::max();
+    }
+};
+struct MaxValueOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const {
+        if constexpr (std::is_floating_point_v<T>) return (b > a || a != a) ? b : a;
+        else return b > a ? b : a;
+    }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() {
+        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
+        else return std::numeric_limits<T>::lowest();
+    }
 };
 
 // ------------------------------------------------------------------------------------------------

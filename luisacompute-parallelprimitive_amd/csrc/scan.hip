@@ -62,36 +62,8 @@ constexpr uint32_t kFlagPartial = 1;
 constexpr uint32_t kFlagInclusive = 2;
 constexpr uint32_t kFlagClaimed = 3;  // a look-back is computing this tile's aggregate
 
-// Scan operators: the reference's SumOp, MinOp and MaxOp (common/thread_operators.h:49-74).  Integer sums
-// run in the unsigned type (wrap-around); min / max compare in the item's own type, for floats like
-// fmin / fmax (a NaN operand yields the other one; -0.0 and +0.0 compare equal, so the older is kept).
-// Identities: the type's max / lowest for integers; a quiet NaN for floats, the one value that every
-// float operand, NaN included, absorbs (op(x, NaN) = op(NaN, x) = x), so padding and empty prefixes
-// leave an inclusive scan equal to the plain left-to-right fold of its items.
-struct ScanMinOp {
-    template <typename T>
-    __device__ __forceinline__ T operator()(T a, T b) const {
-        if constexpr (std::is_floating_point_v<T>) return (b < a || a != a) ? b : a;  // a NaN operand yields the other
-        else return b < a ? b : a;
-    }
-    template <typename T>
-    __host__ __device__ __forceinline__ static constexpr T identity() {
-        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
-        else return std::numeric_limits<T>::max();
-    }
-};
-struct ScanMaxOp {
-    template <typename T>
-    __device__ __forceinline__ T operator()(T a, T b) const {
-        if constexpr (std::is_floating_point_v<T>) return (b > a || a != a) ? b : a;
-        else return b > a ? b : a;
-    }
-    template <typename T>
-    __host__ __device__ __forceinline__ static constexpr T identity() {
-        if constexpr (std::is_floating_point_v<T>) return std::numeric_limits<T>::quiet_NaN();
-        else return std::numeric_limits<T>::lowest();
-    }
-};
+// Scan operators: SumOp, MinValueOp and MaxValueOp (common.hpp), the reference's SumOp, MinOp and MaxOp
+// (common/thread_operators.h:49-74).
 
 #ifdef LCPP_HIP_PHASE_TRACE
 // Phase-trace buffer of the diagnostic build: one record per tile.
@@ -517,13 +489,13 @@ LCPP_HIP_DEFINE_SCAN(f64, double, double)
 #define LCPP_HIP_DEFINE_SCAN_MINMAX(S, T)                                                                        \
     int lcpp_hip_scan_min_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,    \
                               int use_init, T init, void* stream) {                                             \
-        return scan_op<T, ScanMinOp>("DeviceScan (MinOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
-                                     use_init ? init : ScanMinOp::identity<T>(), stream);                         \
+        return scan_op<T, MinValueOp>("DeviceScan (MinOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
+                                     use_init ? init : MinValueOp::identity<T>(), stream);                         \
     }                                                                                                           \
     int lcpp_hip_scan_max_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,    \
                               int use_init, T init, void* stream) {                                             \
-        return scan_op<T, ScanMaxOp>("DeviceScan (MaxOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
-                                     use_init ? init : ScanMaxOp::identity<T>(), stream);                         \
+        return scan_op<T, MaxValueOp>("DeviceScan (MaxOp)", temp, temp_bytes, in, out, n, inclusive != 0,         \
+                                     use_init ? init : MaxValueOp::identity<T>(), stream);                         \
     }
 LCPP_HIP_DEFINE_SCAN_MINMAX(i32, int32_t)
 LCPP_HIP_DEFINE_SCAN_MINMAX(u32, uint32_t)

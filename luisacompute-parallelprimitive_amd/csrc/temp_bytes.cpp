@@ -83,6 +83,19 @@ size_t lcpp_hip_reduce_temp_bytes(uint64_t n, size_t elem_bytes) {
     return lcpp_hip_reduce_temp_bytes_policy(n, elem_bytes, 256, 8);
 }
 
+// DeviceReduce<>::GetArgTempStorageBytes (device_reduce.h:198-210): the reduce temp of (index, value)
+// pairs (a 4-byte index beside the value, padded to the value's alignment), then n pairs and one pair,
+// each 256-byte aligned.
+size_t lcpp_hip_reduce_arg_temp_bytes(uint64_t n, size_t elem_bytes) {
+    if (elem_bytes != 4 && elem_bytes != 8) return 0;
+    const size_t pair = elem_bytes == 4 ? 8 : 16;
+    size_t bytes = lcpp_hip_reduce_temp_bytes(n, pair);
+    bytes = align_up(bytes);
+    bytes += n * pair;
+    bytes = align_up(bytes);
+    return bytes + pair;
+}
+
 // DeviceScan::GetTempStorageBytes (device/device_scan.h:295-308) with scan_temp_storage_bytes
 // (:111-126) and num_tiles_for (:102-109).  `default_policy` selects the extra reservation for the
 // runtime-chosen 320x25 packed layout that the default template arguments add for 4-byte values.

@@ -1,6 +1,6 @@
-// DeviceReduce::Sum over the MI355X C-ABI (lcpp_hip_reduce_sum_*), with the reference's module
-// shape (src/lcpp/device/device_reduce.h:102-113 template, :154-173 create, :184-189 temp query,
-// :280-288 Sum) and its record-time checks (:238-264).  Sum records one command; the kernels run on
+// DeviceReduce::Sum / Min / Max / ArgMin / ArgMax over the MI355X C-ABI (lcpp_hip_reduce_{sum,min,max,
+// argmin,argmax}_*), with the reference's module shape (src/lcpp/device/device_reduce.h:102-113 template,
+// :154-173 create, :184-210 temp queries, :280-436 Sum to ArgMax) and its record-time checks (:238-264).  Sum records one command; the kernels run on
 // the stream the command list is committed to.  ReduceByKey with a sum operator (:437-487, temp
 // query :207-223) runs lcpp_hip_reduce_by_key_sum_*, which writes 0 runs for empty input (:449-458).
 #pragma once
@@ -73,6 +73,37 @@ class DeviceReduce : public LuisaModule {
         };
     }
 
+    // Temp bytes of ArgMin / ArgMax: the reference's layout of (index, value) pairs (:198-210).
+    template <typename T>
+    static size_t GetArgTempStorageBytes(size_t num_item) {
+        return lcpp_hip_reduce_arg_temp_bytes(num_item, sizeof(T));
+    }
+
+    // The smallest / largest item, folded from the type's max / lowest (an empty input writes it).
+    template <NumericT T>
+    void Min(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             size_t num_item) {
+        record_ext<false>(cmdlist, temp_storage, d_in, d_out, num_item);
+    }
+    template <NumericT T>
+    void Max(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+             size_t num_item) {
+        record_ext<true>(cmdlist, temp_storage, d_in, d_out, num_item);
+    }
+
+    // The smallest / largest item and its index (the lowest among equal items); an empty input writes
+    // the type's max / lowest and index 1.
+    template <NumericT T>
+    void ArgMin(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, size_t num_item) {
+        record_arg<false>(cmdlist, temp_storage, d_in, d_out, d_index_out, num_item);
+    }
+    template <NumericT T>
+    void ArgMax(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                BufferView<uint> d_index_out, size_t num_item) {
+        record_arg<true>(cmdlist, temp_storage, d_in, d_out, d_index_out, num_item);
+    }
+
     template <NumericT T>
     void Sum(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
              size_t num_item) {
@@ -104,6 +135,87 @@ class DeviceReduce : public LuisaModule {
             else if constexpr (std::is_same_v<T, double>) rc = lcpp_hip_reduce_sum_f64(temp, temp_bytes, in, out, num_item, st);
             else static_assert(sizeof(T) == 0, "DeviceReduce::Sum: unsupported element type");
             luisa::detail::abi_check(rc, "DeviceReduce::Sum");
+        };
+    }
+
+  private:
+    // The C-ABI suffix type of T: signed and unsigned integers compare differently, so each keeps its own.
+    template <typename T>
+    using ExtAbi = std::conditional_t<std::is_floating_point_v<T>, T,
+                                      std::conditional_t<std::is_signed_v<T>,
+                                                         std::conditional_t<sizeof(T) == 4, int32_t, int64_t>,
+                                                         std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>>>;
+
+    template <bool MAX, NumericT T>
+    void record_ext(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                    size_t num_item) {
+        static_assert(sizeof(T) == 4 || sizeof(T) == 8, "DeviceReduce::Min / Max support 4- and 8-byte numbers");
+        LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
+        LCPP_ASSERT(num_item <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
+        LCPP_ASSERT(d_out.size() >= 1u, "DeviceReduce output view is empty.");
+        if (num_item > 0) {
+            LCPP_ASSERT(d_in.size() >= num_item, "DeviceReduce input view is too small.");
+            LCPP_ASSERT(temp_storage.size() >= bytes_to_uint_count(GetTempStorageBytes<T>(num_item)),
+                        "DeviceReduce temporary storage is too small.");
+        }
+        using A = ExtAbi<T>;
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const A* in = reinterpret_cast<const A*>(d_in.data());
+        A* out = reinterpret_cast<A*>(d_out.data());
+        cmdlist << [=](hipStream_t s) {
+            void* st = detail::stream_ptr(s);
+            int rc;
+#define LCPP_REDUCE_EXT_CALL(SFX, U)                                                                          \
+    rc = MAX ? lcpp_hip_reduce_max_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                         num_item, st)                                                          \
+             : lcpp_hip_reduce_min_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                         num_item, st)
+            if constexpr (std::is_same_v<A, int32_t>) LCPP_REDUCE_EXT_CALL(i32, int32_t);
+            else if constexpr (std::is_same_v<A, uint32_t>) LCPP_REDUCE_EXT_CALL(u32, uint32_t);
+            else if constexpr (std::is_same_v<A, float>) LCPP_REDUCE_EXT_CALL(f32, float);
+            else if constexpr (std::is_same_v<A, int64_t>) LCPP_REDUCE_EXT_CALL(i64, int64_t);
+            else if constexpr (std::is_same_v<A, uint64_t>) LCPP_REDUCE_EXT_CALL(u64, uint64_t);
+            else LCPP_REDUCE_EXT_CALL(f64, double);
+#undef LCPP_REDUCE_EXT_CALL
+            luisa::detail::abi_check(rc, MAX ? "DeviceReduce::Max" : "DeviceReduce::Min");
+        };
+    }
+
+    template <bool MAX, NumericT T>
+    void record_arg(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                    BufferView<uint> d_index_out, size_t num_item) {
+        static_assert(sizeof(T) == 4 || sizeof(T) == 8, "DeviceReduce::ArgMin / ArgMax support 4- and 8-byte numbers");
+        LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
+        LCPP_ASSERT(num_item <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
+        LCPP_ASSERT(d_out.size() >= 1u && d_index_out.size() >= 1u, "DeviceReduce output view is empty.");
+        if (num_item > 0) {
+            LCPP_ASSERT(d_in.size() >= num_item, "DeviceReduce input view is too small.");
+            LCPP_ASSERT(temp_storage.size() >= bytes_to_uint_count(GetArgTempStorageBytes<T>(num_item)),
+                        "DeviceReduce temporary storage is too small.");
+        }
+        using A = ExtAbi<T>;
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const A* in = reinterpret_cast<const A*>(d_in.data());
+        A* out = reinterpret_cast<A*>(d_out.data());
+        uint32_t* index = d_index_out.data();
+        cmdlist << [=](hipStream_t s) {
+            void* st = detail::stream_ptr(s);
+            int rc;
+#define LCPP_REDUCE_ARG_CALL(SFX, U)                                                                             \
+    rc = MAX ? lcpp_hip_reduce_argmax_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                            index, num_item, st)                                                   \
+             : lcpp_hip_reduce_argmin_##SFX(temp, temp_bytes, reinterpret_cast<const U*>(in), reinterpret_cast<U*>(out), \
+                                            index, num_item, st)
+            if constexpr (std::is_same_v<A, int32_t>) LCPP_REDUCE_ARG_CALL(i32, int32_t);
+            else if constexpr (std::is_same_v<A, uint32_t>) LCPP_REDUCE_ARG_CALL(u32, uint32_t);
+            else if constexpr (std::is_same_v<A, float>) LCPP_REDUCE_ARG_CALL(f32, float);
+            else if constexpr (std::is_same_v<A, int64_t>) LCPP_REDUCE_ARG_CALL(i64, int64_t);
+            else if constexpr (std::is_same_v<A, uint64_t>) LCPP_REDUCE_ARG_CALL(u64, uint64_t);
+            else LCPP_REDUCE_ARG_CALL(f64, double);
+#undef LCPP_REDUCE_ARG_CALL
+            luisa::detail::abi_check(rc, MAX ? "DeviceReduce::ArgMax" : "DeviceReduce::ArgMin");
         };
     }
 };

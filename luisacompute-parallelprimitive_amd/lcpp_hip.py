@@ -100,6 +100,10 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_generate", i32, i32, vp, u64, u64, u64, vp)
     for s in SCALAR_SUFFIXES:
         sig(f"lcpp_hip_reduce_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
+        for op in ("min", "max"):
+            sig(f"lcpp_hip_reduce_{op}_{s}", i32, vp, sz, vp, vp, u64, vp)
+            sig(f"lcpp_hip_reduce_arg{op}_{s}", i32, vp, sz, vp, vp, vp, u64, vp)
+    sig("lcpp_hip_reduce_arg_temp_bytes", sz, u64, sz)
     for s in SCAN_SUFFIXES:
         sig(f"lcpp_hip_scan_exclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
         sig(f"lcpp_hip_scan_inclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
@@ -242,6 +246,31 @@ def reduce_sum(suffix: str, d_in, d_out, n: int, temp=None, stream=None) -> None
         temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
     call(f"lcpp_hip_reduce_sum_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out), n,
          stream_handle(stream))
+
+
+def reduce_arg_temp_bytes(n: int, elem_bytes: int) -> int:
+    return lib().lcpp_hip_reduce_arg_temp_bytes(n, elem_bytes)
+
+
+def reduce_minmax(op: str, suffix: str, d_in, d_out, n: int, temp=None, stream=None) -> None:
+    """DeviceReduce::Min (op "min") or Max ("max") over d_in[0:n) into d_out[0]."""
+    if op not in ("min", "max"):
+        raise ValueError(f"reduce operator {op!r}: min or max")
+    if temp is None:
+        temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    call(f"lcpp_hip_reduce_{op}_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out), n,
+         stream_handle(stream))
+
+
+def reduce_arg(op: str, suffix: str, d_in, d_value, d_index, n: int, temp=None, stream=None) -> None:
+    """DeviceReduce::ArgMin (op "min") or ArgMax ("max"): the extreme item into d_value[0], its index
+    (uint32) into d_index[0]."""
+    if op not in ("min", "max"):
+        raise ValueError(f"reduce operator {op!r}: min or max")
+    if temp is None:
+        temp = _temp(reduce_arg_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    call(f"lcpp_hip_reduce_arg{op}_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in),
+         ptr(d_value), ptr(d_index), n, stream_handle(stream))
 
 
 def scan_sum(suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=None, temp=None, stream=None) -> None:

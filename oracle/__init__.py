@@ -64,6 +64,12 @@ def lib() -> C.CDLL:
                 f = getattr(h, f"oracle_scan_{op}_{name}")
                 f.restype = None
                 f.argtypes = [vp, vp, u64, i32, ct]
+                f = getattr(h, f"oracle_reduce_{op}_{name}")
+                f.restype = ct
+                f.argtypes = [vp, u64]
+            f = getattr(h, f"oracle_reduce_arg_{name}")
+            f.restype = None
+            f.argtypes = [vp, u64, i32, C.POINTER(ct), C.POINTER(u32)]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -184,8 +190,27 @@ def scan_sum_f64(a: np.ndarray, inclusive: bool = False, init: float = 0.0) -> t
     return out, aout
 
 
+_MINMAX_CTYPE = {np.dtype(np.int32): C.c_int32, np.dtype(np.uint32): C.c_uint32, np.dtype(np.float32): C.c_float,
+                 np.dtype(np.int64): C.c_int64, np.dtype(np.uint64): C.c_uint64, np.dtype(np.float64): C.c_double}
 _MINMAX_SUFFIX = {np.dtype(np.int32): "i32", np.dtype(np.uint32): "u32", np.dtype(np.float32): "f32",
                   np.dtype(np.int64): "i64", np.dtype(np.uint64): "u64", np.dtype(np.float64): "f64"}
+
+
+def reduce_minmax(op: str, a: np.ndarray):
+    """DeviceReduce::Min / Max: the fold from the type's max / lowest, NaN items skipped."""
+    a = np.ascontiguousarray(a)
+    return a.dtype.type(getattr(lib(), f"oracle_reduce_{op}_{_MINMAX_SUFFIX[a.dtype]}")(_p(a), a.size))
+
+
+def reduce_arg(op: str, a: np.ndarray):
+    """DeviceReduce::ArgMin / ArgMax: (value, index); first index among equal values, NaN never wins,
+    (initial value, 1) for an empty input."""
+    a = np.ascontiguousarray(a)
+    ct = _MINMAX_CTYPE[a.dtype]
+    v, i = ct(), C.c_uint32()
+    getattr(lib(), f"oracle_reduce_arg_{_MINMAX_SUFFIX[a.dtype]}")(_p(a), a.size, int(op == "max"), C.byref(v),
+                                                                  C.byref(i))
+    return a.dtype.type(v.value), int(i.value)
 
 
 def scan_minmax(op: str, a: np.ndarray, inclusive: bool = False, init=None) -> np.ndarray:

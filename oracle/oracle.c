@@ -14,6 +14,7 @@
  * Conventions: sizes are uint64_t; integer sums wrap modulo 2^bits (two's complement), as the
  * reference's int32/uint32 arithmetic does on the device.
  */
+#include <float.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -123,6 +124,44 @@ void oracle_scan_sum_f64(const double* in, long double* out, long double* abs_ou
         else { out[i] = run; abs_out[i] = arun; run += x; arun += fabsl(x); }
     }
 }
+/* DeviceReduce<>::Min / Max (device_reduce.h:291-309): run = the type's max (min) / lowest (max), then
+ * run = op(run, in[i]) left to right with the min / max scans' operator (a NaN item is skipped).
+ * ArgMin / ArgMax (device_reduce.h:311-436 with ArgMinOp / ArgMaxOp, common/thread_operators.h:10-47):
+ * best = (that value, index 0xFFFFFFFF); item i replaces it when it is strictly smaller (larger), or
+ * equal at a lower index; NaN items never replace it.  n == 0: the initial value and index 1. */
+#define ORACLE_REDUCE_EXT(NAME, T, TMAX, TLOW)                                                          \
+    T oracle_reduce_min_##NAME(const T* in, uint64_t n) {                                               \
+        T run = TMAX;                                                                                   \
+        for (uint64_t i = 0; i < n; ++i) if (in[i] < run || run != run) run = in[i];                    \
+        return run;                                                                                     \
+    }                                                                                                   \
+    T oracle_reduce_max_##NAME(const T* in, uint64_t n) {                                               \
+        T run = TLOW;                                                                                   \
+        for (uint64_t i = 0; i < n; ++i) if (in[i] > run || run != run) run = in[i];                    \
+        return run;                                                                                     \
+    }                                                                                                   \
+    void oracle_reduce_arg_##NAME(const T* in, uint64_t n, int is_max, T* value, uint32_t* index) {     \
+        T best = is_max ? TLOW : TMAX;                                                                  \
+        uint32_t at = 0xFFFFFFFFu;                                                                      \
+        for (uint64_t i = 0; i < n; ++i) {                                                              \
+            const T x = in[i];                                                                          \
+            if (x != x) continue;                                                                       \
+            if ((is_max ? x > best : x < best) || (x == best && (uint32_t)i < at)) {                    \
+                best = x;                                                                               \
+                at = (uint32_t)i;                                                                       \
+            }                                                                                           \
+        }                                                                                               \
+        *value = best;                                                                                  \
+        *index = n == 0 ? 1u : at;                                                                      \
+    }
+ORACLE_REDUCE_EXT(i32, int32_t, INT32_MAX, INT32_MIN)
+ORACLE_REDUCE_EXT(u32, uint32_t, UINT32_MAX, 0u)
+ORACLE_REDUCE_EXT(f32, float, FLT_MAX, -FLT_MAX)
+ORACLE_REDUCE_EXT(i64, int64_t, INT64_MAX, INT64_MIN)
+ORACLE_REDUCE_EXT(u64, uint64_t, UINT64_MAX, 0ull)
+ORACLE_REDUCE_EXT(f64, double, DBL_MAX, -DBL_MAX)
+#undef ORACLE_REDUCE_EXT
+
 /* Min / max scans (DeviceScan<>::ExclusiveScan / InclusiveScan with MinOp / MaxOp, device_scan.h:321-368,
  * common/thread_operators.h:58-74): run = init; exclusive: out[i] = run, run = op(run, in[i]);
  * inclusive: run = op(run, in[i]), out[i] = run.  op(run, x) keeps run unless x is strictly smaller

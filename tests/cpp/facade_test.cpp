@@ -125,6 +125,88 @@ void reduce_empty_writes_init() {
     EXPECT(result == 0);
 }
 
+// tests/device_reduce_test.cpp:175-345: Min / Max against std::min_element / max_element, Max of floats
+// from the lowest identity, ArgMax's first equal extremum, ArgMax of negative floats, and the empty-input
+// sentinels (value max / lowest, index 1).
+void reduce_min_max_and_arg() {
+    auto& e = *g_env;
+    {
+        const uint n = 100003u;
+        std::vector<int> a(n);
+        uint32_t x = 12345u;
+        for (uint i = 0; i < n; ++i) {
+            x = x * 1664525u + 1013904223u;
+            a[i] = static_cast<int>(x);
+        }
+        auto in = e.device.create_buffer<int>(n);
+        auto lo = e.device.create_buffer<int>(1);
+        auto hi = e.device.create_buffer<int>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<int>(n)));
+        CommandList cmd;
+        e.reduce.Min(cmd, temp.view(), in.view(), lo.view(), n);
+        e.reduce.Max(cmd, temp.view(), in.view(), hi.view(), n);
+        int rlo = 0, rhi = 0;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << lo.copy_to(&rlo) << hi.copy_to(&rhi)
+                 << synchronize();
+        EXPECT(rlo == *std::min_element(a.begin(), a.end()));
+        EXPECT(rhi == *std::max_element(a.begin(), a.end()));
+    }
+    {
+        std::vector<float> a{-8.0f, -2.5f, -9.0f, -4.0f};
+        auto in = e.device.create_buffer<float>(a.size());
+        auto out = e.device.create_buffer<float>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<float>(a.size())));
+        CommandList cmd;
+        e.reduce.Max(cmd, temp.view(), in.view(), out.view(), a.size());
+        float r = 0.0f;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(&r) << synchronize();
+        EXPECT(r == -2.5f);
+    }
+    {
+        std::vector<int> a{1, 9, 4, 9, 3};
+        auto in = e.device.create_buffer<int>(a.size());
+        auto value = e.device.create_buffer<int>(1);
+        auto index = e.device.create_buffer<uint>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetArgTempStorageBytes<int>(a.size())));
+        CommandList cmd;
+        e.reduce.ArgMax(cmd, temp.view(), in.view(), value.view(), index.view(), a.size());
+        int v = 0;
+        uint i = 0;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << value.copy_to(&v) << index.copy_to(&i)
+                 << synchronize();
+        EXPECT(v == 9 && i == 1u);
+    }
+    {
+        std::vector<float> a{-7.0f, -3.0f, -5.0f};
+        auto in = e.device.create_buffer<float>(a.size());
+        auto value = e.device.create_buffer<float>(1);
+        auto index = e.device.create_buffer<uint>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetArgTempStorageBytes<float>(a.size())));
+        CommandList cmd;
+        e.reduce.ArgMax(cmd, temp.view(), in.view(), value.view(), index.view(), a.size());
+        float v = 0.0f;
+        uint i = 0;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << value.copy_to(&v) << index.copy_to(&i)
+                 << synchronize();
+        EXPECT(v == -3.0f && i == 1u);
+    }
+    {
+        auto min_value = e.device.create_buffer<int>(1);
+        auto min_index = e.device.create_buffer<uint>(1);
+        auto max_value = e.device.create_buffer<int>(1);
+        auto max_index = e.device.create_buffer<uint>(1);
+        CommandList cmd;
+        e.reduce.ArgMin(cmd, BufferView<uint>{}, BufferView<int>{}, min_value.view(), min_index.view(), 0u);
+        e.reduce.ArgMax(cmd, BufferView<uint>{}, BufferView<int>{}, max_value.view(), max_index.view(), 0u);
+        int vmin = 0, vmax = 0;
+        uint imin = 0, imax = 0;
+        e.stream << cmd.commit() << min_value.copy_to(&vmin) << min_index.copy_to(&imin) << max_value.copy_to(&vmax)
+                 << max_index.copy_to(&imax) << synchronize();
+        EXPECT(vmin == std::numeric_limits<int>::max() && imin == 1u);
+        EXPECT(vmax == std::numeric_limits<int>::lowest() && imax == 1u);
+    }
+}
+
 void reduce_bench_pattern_int_and_float() {
     auto& e = *g_env;
     const uint n = (1u << 22) + 13u;
@@ -1284,6 +1366,7 @@ const std::vector<Case>& cases() {
         {"reduce_sum_of_ones", reduce_sum_of_ones},
         {"reduce_empty_writes_init", reduce_empty_writes_init},
         {"reduce_bench_pattern_int_and_float", reduce_bench_pattern_int_and_float},
+        {"reduce_min_max_and_arg", reduce_min_max_and_arg},
         {"scan_sums_of_ones", scan_sums_of_ones},
         {"scan_inclusive_init_in_place", scan_inclusive_init_in_place},
         {"scan_double_inclusive_sum", scan_double_inclusive_sum},

@@ -109,3 +109,132 @@ def test_north_star_size_2p28(hip, orc, dev):
     out = fill_dev(1, 4, 0)
     hip.reduce_sum("i32", d, out, n)
     assert to_host(out, np.int32, 1)[0] == orc.reduce_sum_i32(to_host(d, np.int32))[0]
+
+
+# ---- Min / Max / ArgMin / ArgMax -------------------------------------------------------------------
+# device_reduce.h:291-436 (MinOp / MaxOp / ArgMinOp / ArgMaxOp): bit-exact against the oracle's left-to-right
+# fold for every type; the reference's cases of tests/device_reduce_test.cpp:175-345.
+EXT_TYPES = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64,
+             "f64": np.float64}
+
+
+def ext_input(suffix, n, seed, nan_fraction=0.0):
+    dtype = np.dtype(EXT_TYPES[suffix])
+    rng = np.random.default_rng(seed)
+    if dtype.kind == "f":
+        a = (rng.standard_normal(n) * 1e3).astype(dtype)
+        if nan_fraction:
+            a[rng.random(n) < nan_fraction] = np.nan
+        return a
+    info = np.iinfo(dtype)
+    return rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+
+
+def gpu_ext(hip, op, suffix, a, offset=0):
+    d = to_dev(a)[offset:]
+    out = fill_dev(1, a.dtype.itemsize, 0x5A5A5A5A)
+    hip.reduce_minmax(op, suffix, d, out, a.size - offset)
+    return to_host(out, a.dtype, 1)[0]
+
+
+def gpu_arg(hip, op, suffix, a, offset=0):
+    d = to_dev(a)[offset:]
+    out = fill_dev(1, a.dtype.itemsize, 0x5A5A5A5A)
+    idx = fill_dev(1, 4, 0x5A5A5A5A)
+    hip.reduce_arg(op, suffix, d, out, idx, a.size - offset)
+    return to_host(out, a.dtype, 1)[0], int(to_host(idx, np.uint32, 1)[0])
+
+
+def same(x, y):
+    return np.asarray(x).tobytes() == np.asarray(y).tobytes()
+
+
+def test_reference_cases_min_max_arg(hip, dev):
+    """device_reduce_test.cpp:218-345: float Max from the lowest identity, ArgMax's first equal extremum,
+    ArgMax of negative floats, empty-input sentinels."""
+    assert gpu_ext(hip, "max", "f32", np.array([-8.0, -2.5, -9.0, -4.0], np.float32)) == np.float32(-2.5)
+    assert gpu_arg(hip, "max", "i32", np.array([1, 9, 4, 9, 3], np.int32)) == (9, 1)
+    assert gpu_arg(hip, "max", "f32", np.array([-7.0, -3.0, -5.0], np.float32)) == (np.float32(-3.0), 1)
+    for op, want in (("min", np.iinfo(np.int32).max), ("max", np.iinfo(np.int32).min)):
+        d = torch.empty(0, dtype=torch.int32, device=dev)
+        out, idx = fill_dev(1, 4, 7), fill_dev(1, 4, 7)
+        hip.reduce_arg(op, "i32", d, out, idx, 0)
+        assert int(to_host(out, np.int32, 1)[0]) == want and int(to_host(idx, np.uint32, 1)[0]) == 1
+        hip.reduce_minmax(op, "i32", d, out, 0)
+        assert int(to_host(out, np.int32, 1)[0]) == want
+
+
+@pytest.mark.parametrize("suffix", list(EXT_TYPES))
+@pytest.mark.parametrize("n", [1, 3, 31, 1025, 4097, 65537, 1000003, (1 << 22) + 5])
+def test_min_max_arg_vs_oracle(hip, orc, dev, suffix, n):
+    log(f"reduce min/max/arg {suffix} n={n}")
+    a = ext_input(suffix, n, n + len(suffix))
+    for op in ("min", "max"):
+        assert same(gpu_ext(hip, op, suffix, a), orc.reduce_minmax(op, a)), op
+        v, i = gpu_arg(hip, op, suffix, a)
+        ov, oi = orc.reduce_arg(op, a)
+        assert same(v, ov) and i == oi, (op, v, i, ov, oi)
+        want_i = int(np.argmin(a) if op == "min" else np.argmax(a))
+        assert i == want_i
+
+
+@pytest.mark.parametrize("suffix", ["i32", "f64"])
+def test_min_max_arg_unaligned_and_ties(hip, orc, dev, suffix):
+    """Subviews off the 16-byte grid; many equal extrema: the lowest index wins wherever the copies sit."""
+    n = (1 << 20) + 77
+    dtype = EXT_TYPES[suffix]
+    rng = np.random.default_rng(4)
+    a = rng.integers(-50, 50, n).astype(dtype)
+    a[rng.integers(0, n, 40)] = dtype(-1000)
+    a[rng.integers(0, n, 40)] = dtype(1000)
+    for offset in (1, 2, 3):
+        b = a[offset:]
+        for op in ("min", "max"):
+            assert same(gpu_ext(hip, op, suffix, a, offset), orc.reduce_minmax(op, b))
+            v, i = gpu_arg(hip, op, suffix, a, offset)
+            assert (v, i) == orc.reduce_arg(op, b)
+
+
+def test_float_nan_and_signed_zero(hip, orc, dev):
+    """NaN items never win; -0.0 == +0.0, so ArgMin / ArgMax take the first zero (its sign bit included);
+    an all-NaN input gives the initial pair (the type's max / lowest, index 0xFFFFFFFF); Min / Max of
+    +-infinity stop at the initial value (the type's max / lowest), as the reference's fold does."""
+    for dtype, sfx in ((np.float32, "f32"), (np.float64, "f64")):
+        n = (1 << 21) + 9
+        a = ext_input(sfx, n, 3, nan_fraction=0.1)
+        for op in ("min", "max"):
+            assert same(gpu_ext(hip, op, sfx, a), orc.reduce_minmax(op, a))
+            assert gpu_arg(hip, op, sfx, a) == orc.reduce_arg(op, a)
+        z = np.full(70000, np.nan, dtype)
+        z[5000], z[9000], z[65000] = 0.0, -0.0, 0.0
+        for op in ("min", "max"):
+            v, i = gpu_arg(hip, op, sfx, z)
+            assert i == 5000 and not np.signbit(v)
+        z[5000] = -0.0
+        v, i = gpu_arg(hip, "min", sfx, z)
+        assert i == 5000 and np.signbit(v)
+        allnan = np.full(3000, np.nan, dtype)
+        assert gpu_arg(hip, "min", sfx, allnan) == (np.finfo(dtype).max, 0xFFFFFFFF)
+        assert gpu_arg(hip, "max", sfx, allnan) == (np.finfo(dtype).min, 0xFFFFFFFF)
+        inf = np.array([np.inf, 1.0, np.inf], dtype)
+        assert gpu_ext(hip, "max", sfx, inf) == np.inf and gpu_ext(hip, "min", sfx, -inf) == -np.inf
+        assert gpu_ext(hip, "min", sfx, np.array([np.inf], dtype)) == np.finfo(dtype).max
+
+
+def test_min_max_arg_2p28(hip, orc, dev):
+    """The 2^28 benchmark size: int32 from the on-device generator, the extremes planted late."""
+    n = 1 << 28
+    log("reduce min/max/arg 2^28")
+    d = torch.empty(n, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_I32_PM1000, d, n, 114521)
+    d[n - 3] = -5000
+    d[n - 7] = 5000
+    d[n - 2] = -5000
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    idx = torch.zeros(1, dtype=torch.int32, device=dev)
+    hip.reduce_arg("min", "i32", d, out, idx, n)
+    assert int(out.item()) == -5000 and int(idx.item()) == n - 3
+    hip.reduce_arg("max", "i32", d, out, idx, n)
+    assert int(out.item()) == 5000 and int(idx.item()) == n - 7
+    hip.reduce_minmax("min", "i32", d, out, n)
+    assert int(out.item()) == -5000

@@ -345,6 +345,50 @@ def test_scan_minmax_signed_zero_keeps_earlier(orc):
     assert np.signbit(orc.scan_minmax("min", a, init=-0.0)).tolist() == [True] * 4
 
 
+# ---- min / max / arg reductions ------------------------------------------------------------------
+def test_reduce_min_max_arg_known_answers(orc):
+    """tests/device_reduce_test.cpp:218-345: float Max from the lowest identity, ArgMax's first equal
+    extremum, ArgMax of negative floats, empty-input sentinels (value max / lowest, index 1)."""
+    assert orc.reduce_minmax("max", np.array([-8.0, -2.5, -9.0, -4.0], np.float32)) == np.float32(-2.5)
+    assert orc.reduce_arg("max", np.array([1, 9, 4, 9, 3], np.int32)) == (9, 1)
+    assert orc.reduce_arg("max", np.array([-7.0, -3.0, -5.0], np.float32)) == (np.float32(-3.0), 1)
+    e = np.array([], np.int32)
+    assert orc.reduce_arg("min", e) == (np.iinfo(np.int32).max, 1)
+    assert orc.reduce_arg("max", e) == (np.iinfo(np.int32).min, 1)
+    assert orc.reduce_minmax("min", e) == np.iinfo(np.int32).max
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32, np.int64, np.uint64, np.float32, np.float64])
+def test_reduce_min_max_arg_vs_numpy(orc, dtype):
+    """Integers against np.min / max / argmin / argmax (first occurrence); floats with NaNs against np.nanmin /
+    nanmax / nanargmin / nanargmax, which skip NaNs as the operators do."""
+    rng = np.random.default_rng(5)
+    for n in (1, 2, 100, 20001):
+        if np.dtype(dtype).kind == "f":
+            a = rng.integers(-40, 40, n).astype(dtype)   # many ties
+            a[rng.random(n) < 0.1] = np.nan
+            a[0] = 7 if np.isnan(a).all() else a[0]
+            fmin, fmax, amin, amax = np.nanmin, np.nanmax, np.nanargmin, np.nanargmax
+        else:
+            info = np.iinfo(dtype)
+            a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+            a[rng.integers(0, n, 3)] = a.max()
+            fmin, fmax, amin, amax = np.min, np.max, np.argmin, np.argmax
+        assert orc.reduce_minmax("min", a) == fmin(a) and orc.reduce_minmax("max", a) == fmax(a)
+        assert orc.reduce_arg("min", a) == (fmin(a), int(amin(a)))
+        assert orc.reduce_arg("max", a) == (fmax(a), int(amax(a)))
+
+
+def test_reduce_arg_float_edges(orc):
+    """The fold starts at the type's max / lowest: +inf items leave Min at FLT_MAX; all-NaN gives the initial
+    pair with index 0xFFFFFFFF; -0.0 and +0.0 tie, the first wins."""
+    f = np.float32
+    assert orc.reduce_minmax("min", np.array([np.inf], f)) == np.finfo(f).max
+    assert orc.reduce_arg("min", np.full(5, np.nan, f)) == (np.finfo(f).max, 0xFFFFFFFF)
+    v, i = orc.reduce_arg("min", np.array([1.0, -0.0, 0.0], f))
+    assert i == 1 and np.signbit(v)
+
+
 # ---- scan-by-key / reduce-by-key ---------------------------------------------------------------
 
 def numpy_by_key(keys, values, key_mask=-1):
