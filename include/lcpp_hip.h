@@ -296,6 +296,32 @@ LCPP_HIP_DECLARE_BY_KEY_VALUES(i64, int64_t)
 LCPP_HIP_DECLARE_BY_KEY_VALUES(u64, uint64_t)
 #undef LCPP_HIP_DECLARE_BY_KEY_VALUES
 #undef LCPP_HIP_DECLARE_BY_KEY
+/* The same entry points with MinOp / MaxOp in place of the sum (device_scan.h:424-597 and
+ * device_reduce.h:437-487 take any ScanOp / ReduceOp; common/thread_operators.h:58-74): values compare
+ * in their own type (signed as signed; floats like fmin / fmax, a NaN item skipped), an exclusive scan
+ * without an initial value gives run heads the operator's identity (the type's max / lowest, a quiet
+ * NaN for floats), and with one out[i] = op(init, the run's items before i).  Same temp queries. */
+#define LCPP_HIP_DECLARE_BY_KEY_OP(NAME, KS, KT, VS, VT)                                                              \
+    int lcpp_hip_scan_by_key_##NAME##_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in, \
+                                                 VT* values_out, uint64_t n, int inclusive, int use_init, VT init,    \
+                                                 uint64_t key_mask, void* stream);                                   \
+    int lcpp_hip_reduce_by_key_##NAME##_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in,                \
+                                                   const VT* values_in, KT* unique_out, VT* aggregates_out,          \
+                                                   uint32_t* num_runs_out, uint64_t n, uint64_t key_mask,            \
+                                                   void* stream);
+#define LCPP_HIP_DECLARE_BY_KEY_OP_VALUES(KS, KT)                                                                      \
+    LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, i32, int32_t) LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, u32, uint32_t)       \
+    LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, f32, float) LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, i64, int64_t)         \
+    LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, u64, uint64_t) LCPP_HIP_DECLARE_BY_KEY_OP(min, KS, KT, f64, double)       \
+    LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, i32, int32_t) LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, u32, uint32_t)       \
+    LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, f32, float) LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, i64, int64_t)         \
+    LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, u64, uint64_t) LCPP_HIP_DECLARE_BY_KEY_OP(max, KS, KT, f64, double)
+LCPP_HIP_DECLARE_BY_KEY_OP_VALUES(i32, int32_t)
+LCPP_HIP_DECLARE_BY_KEY_OP_VALUES(u32, uint32_t)
+LCPP_HIP_DECLARE_BY_KEY_OP_VALUES(i64, int64_t)
+LCPP_HIP_DECLARE_BY_KEY_OP_VALUES(u64, uint64_t)
+#undef LCPP_HIP_DECLARE_BY_KEY_OP_VALUES
+#undef LCPP_HIP_DECLARE_BY_KEY_OP
 
 /* ---------------------------------------------------------------------------------------------
  * Stream compaction: DeviceSelect, DevicePartition, DeviceRunLengthEncode.

@@ -118,14 +118,35 @@ constexpr uint32_t kActHelp = 3;
 template <typename V>
 struct Seg {
     uint32_t count;  // run heads in the span
-    V sum;           // sum of the items after the span's last head (all items if it has none)
+    V sum;           // the items from the span's last head on (all items if it has none) folded by Op
 };
 
-template <typename V>
+// The value operator Op is SumOp (the reference's SumOp), MinValueOp or MaxValueOp (MinOp / MaxOp):
+// Op{}(a, b) and Op::identity<V>().
+template <typename Op, typename V>
+__device__ __forceinline__ V op_apply(V a, V b) {
+    return static_cast<V>(Op{}(a, b));
+}
+template <typename Op, typename V>
+__device__ __forceinline__ V op_identity() {
+    return Op::template identity<V>();
+}
+
+// Op with its operands swapped: a wave reduction over lanes ordered newest first (the look-back's
+// predecessor windows) then still folds older before newer, which decides ties of a min / max.
+template <typename Op>
+struct SwappedOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return static_cast<T>(Op{}(b, a)); }
+    template <typename T>
+    __device__ __forceinline__ static constexpr T identity() { return Op::template identity<T>(); }
+};
+
+template <typename Op, typename V>
 __device__ __forceinline__ Seg<V> seg_combine(Seg<V> older, Seg<V> newer) {
     Seg<V> r;
     r.count = older.count + newer.count;
-    r.sum = newer.count != 0 ? newer.sum : static_cast<V>(older.sum + newer.sum);
+    r.sum = newer.count != 0 ? newer.sum : op_apply<Op>(older.sum, newer.sum);
     return r;
 }
 
@@ -201,32 +222,32 @@ __device__ __forceinline__ uint32_t read_state(const uint64_t* slot, Seg<V>& s) 
 
 // One step of the wave scan: combine with the state DPP brings from an older lane (identity where
 // the pattern has no source).
-template <int CTRL, int ROW_MASK = 0xf, typename V>
+template <typename Op, int CTRL, int ROW_MASK, typename V>
 __device__ __forceinline__ Seg<V> seg_dpp_step(Seg<V> x) {
     Seg<V> o;
     o.count = dpp_move_u32<CTRL, ROW_MASK>(0u, x.count);
-    o.sum = dpp_move<CTRL, ROW_MASK>(V(0), x.sum);
-    return seg_combine(o, x);
+    o.sum = dpp_move<CTRL, ROW_MASK>(op_identity<Op, V>(), x.sum);
+    return seg_combine<Op>(o, x);
 }
 
 // Inclusive scan of a segmented state over the 64 lanes of a wave (row_shr / row_bcast pattern).
-template <typename V>
+template <typename Op, typename V>
 __device__ __forceinline__ Seg<V> wave_seg_scan(Seg<V> x) {
-    x = seg_dpp_step<dpp::kRowShr1>(x);
-    x = seg_dpp_step<dpp::kRowShr2>(x);
-    x = seg_dpp_step<dpp::kRowShr4>(x);
-    x = seg_dpp_step<dpp::kRowShr8>(x);
-    x = seg_dpp_step<dpp::kRowBcast15, 0xa>(x);
-    x = seg_dpp_step<dpp::kRowBcast31, 0xc>(x);
+    x = seg_dpp_step<Op, dpp::kRowShr1, 0xf>(x);
+    x = seg_dpp_step<Op, dpp::kRowShr2, 0xf>(x);
+    x = seg_dpp_step<Op, dpp::kRowShr4, 0xf>(x);
+    x = seg_dpp_step<Op, dpp::kRowShr8, 0xf>(x);
+    x = seg_dpp_step<Op, dpp::kRowBcast15, 0xa>(x);
+    x = seg_dpp_step<Op, dpp::kRowBcast31, 0xc>(x);
     return x;
 }
 
 // The previous lane's inclusive state (identity in lane 0).
-template <typename V>
+template <typename Op, typename V>
 __device__ __forceinline__ Seg<V> wave_seg_exclusive(Seg<V> inclusive) {
     Seg<V> e;
     e.count = dpp_move_u32<dpp::kWaveShr1>(0u, inclusive.count);
-    e.sum = dpp_move<dpp::kWaveShr1>(V(0), inclusive.sum);
+    e.sum = dpp_move<dpp::kWaveShr1>(op_identity<Op, V>(), inclusive.sum);
     return e;
 }
 
@@ -317,15 +338,15 @@ __device__ __forceinline__ uint32_t quad_heads(const K (&key)[kBkVec], K prev, u
 }
 
 // State of a thread-row: its items folded in order.
-template <typename V>
+template <typename Op, typename V>
 __device__ __forceinline__ Seg<V> fold_quad(const V (&val)[kBkVec], uint32_t heads, uint32_t valid) {
-    Seg<V> s{0u, V(0)};
+    Seg<V> s{0u, op_identity<Op, V>()};
 #pragma unroll
     for (int k = 0; k < kBkVec; ++k) {
         const bool head = (heads >> k) & 1u;
-        const V x = ((valid >> k) & 1u) ? val[k] : V(0);
+        const V x = ((valid >> k) & 1u) ? val[k] : op_identity<Op, V>();
         s.count += head ? 1u : 0u;
-        s.sum = head ? x : static_cast<V>(s.sum + x);
+        s.sum = head ? x : op_apply<Op>(s.sum, x);
     }
     return s;
 }
@@ -341,7 +362,7 @@ __device__ __forceinline__ uint64_t row_first(uint32_t tile, int r, uint32_t tid
 // l % 4) when R * 4 <= 64, else P = ceil(R * 4 / 64) consecutive totals folded in order; one wave scan gives
 // every (row, wave) its in-tile carry (the totals before it, in row-major order), written back over
 // the table, and lane 63 the tile aggregate, which wave 0 returns.
-template <typename V, int R>
+template <typename Op, typename V, int R>
 __device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
     constexpr int E = R * kBkWaves;
     constexpr int P = (E + kWave - 1) / kWave;
@@ -349,23 +370,23 @@ __device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
     Seg<V>* flat = &s_wave[0][0];
     Seg<V> incl;
     if constexpr (P == 1) {
-        const Seg<V> t = lane < static_cast<uint32_t>(E) ? flat[lane] : Seg<V>{0u, V(0)};
-        incl = wave_seg_scan(t);
-        if (lane < static_cast<uint32_t>(E)) flat[lane] = wave_seg_exclusive(incl);
+        const Seg<V> t = lane < static_cast<uint32_t>(E) ? flat[lane] : Seg<V>{0u, op_identity<Op, V>()};
+        incl = wave_seg_scan<Op>(t);
+        if (lane < static_cast<uint32_t>(E)) flat[lane] = wave_seg_exclusive<Op>(incl);
     } else {
         const uint32_t first = lane * P;
-        Seg<V> t = first < static_cast<uint32_t>(E) ? flat[first] : Seg<V>{0u, V(0)};
+        Seg<V> t = first < static_cast<uint32_t>(E) ? flat[first] : Seg<V>{0u, op_identity<Op, V>()};
 #pragma unroll
         for (int p = 1; p < P; ++p)
-            if (first + p < static_cast<uint32_t>(E)) t = seg_combine(t, flat[first + p]);
-        incl = wave_seg_scan(t);
-        Seg<V> run = wave_seg_exclusive(incl);
+            if (first + p < static_cast<uint32_t>(E)) t = seg_combine<Op>(t, flat[first + p]);
+        incl = wave_seg_scan<Op>(t);
+        Seg<V> run = wave_seg_exclusive<Op>(incl);
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             if (first + p < static_cast<uint32_t>(E)) {
                 const Seg<V> x = flat[first + p];
                 flat[first + p] = run;
-                run = seg_combine(run, x);
+                run = seg_combine<Op>(run, x);
             }
         }
     }
@@ -378,7 +399,7 @@ __device__ __forceinline__ Seg<V> scan_totals(Seg<V> (*s_wave)[kBkWaves]) {
 // Aggregate of tile `tile`, computed by the whole workgroup with the owner's own arithmetic (same
 // heads, folds, wave scans and combination order, so float sums match bit for bit).  Row by row, with
 // the key before each thread-row read from memory, to keep the helper's registers small.
-template <typename K, typename V, int MODE, int R>
+template <typename Op, typename K, typename V, int MODE, int R>
 __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uint32_t tile, K mask, bool vec_k,
                                  bool vec_v, Seg<V> (*s_help)[kBkWaves]) {
     const uint32_t tid = threadIdx.x;
@@ -392,19 +413,19 @@ __device__ Seg<V> tile_aggregate(const K* keys, const V* values, uint64_t n, uin
         load_values<MODE>(values, first, n, vec_v, val);
         const K prev = (first > 0 && first - 1 < n) ? keys[first - 1] : K(0);
         const uint32_t valid = quad_valid(first, n);
-        const Seg<V> incl = wave_seg_scan(fold_quad(val, quad_heads(key, prev, valid, first == 0, mask), valid));
+        const Seg<V> incl = wave_seg_scan<Op>(fold_quad<Op>(val, quad_heads(key, prev, valid, first == 0, mask), valid));
         if (lane_id() == kWave - 1) s_help[r][wave] = incl;
     }
     __syncthreads();
     // Only thread 0 publishes the helped state, so wave 0's result is all that is needed.
-    Seg<V> agg{0u, V(0)};
-    if (wave == 0) agg = scan_totals<V, R>(s_help);
+    Seg<V> agg{0u, op_identity<Op, V>()};
+    if (wave == 0) agg = scan_totals<Op, V, R>(s_help);
     __syncthreads();  // s_help is free again
     return agg;
 }
 
 // Outputs of one thread-row of a scan from the state carried into its first item.
-template <typename V>
+template <typename Op, typename V>
 __device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32_t heads, Seg<V> run, int inclusive,
                                                   int use_init, V init, V* values_out, uint64_t first, uint32_t valid,
                                                   bool vec_o) {
@@ -412,14 +433,14 @@ __device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32
 #pragma unroll
     for (int k = 0; k < kBkVec; ++k) {
         const bool head = (heads >> k) & 1u;
-        if (!inclusive) out[k] = head ? init : static_cast<V>(init + run.sum);
+        if (!inclusive) out[k] = head ? init : op_apply<Op>(init, run.sum);
         if (head) {
             run.count += 1;
             run.sum = val[k];
         } else {
-            run.sum = static_cast<V>(run.sum + val[k]);
+            run.sum = op_apply<Op>(run.sum, val[k]);
         }
-        if (inclusive) out[k] = use_init ? static_cast<V>(init + run.sum) : run.sum;
+        if (inclusive) out[k] = use_init ? op_apply<Op>(init, run.sum) : run.sum;
     }
     store_quad(values_out, first, valid, vec_o, out);
 }
@@ -427,7 +448,7 @@ __device__ __forceinline__ void scan_quad_outputs(const V (&val)[kBkVec], uint32
 // Reduce outputs of a tile with more runs than the LDS stage holds, after its look-back: each row is
 // read again and folded exactly as before (heads from the edge table, the same wave scans), and every
 // run head writes its key and the sum of the run before it.
-template <typename K, typename V, int MODE, int R>
+template <typename Op, typename K, typename V, int MODE, int R>
 __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out, V* aggregates_out,
                                    uint32_t* num_runs_out, uint64_t n, K mask, uint32_t tile, Seg<V> prefix,
                                    Seg<V> (*s_wave)[kBkWaves], K (*s_edge)[kBkWaves], bool vec_k, bool vec_v) {
@@ -447,8 +468,8 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
         if (lane == 0) prev = wave > 0 ? s_edge[r][wave - 1] : (r > 0 ? s_edge[r - 1][kBkWaves - 1] : before_tile);
         const uint32_t valid = quad_valid(first, n);
         const uint32_t h = quad_heads(key, prev, valid, tile == 0 && r == 0 && tid == 0, mask);
-        const Seg<V> incl = wave_seg_scan(fold_quad(val, h, valid));
-        Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl)));
+        const Seg<V> incl = wave_seg_scan<Op>(fold_quad<Op>(val, h, valid));
+        Seg<V> run = seg_combine<Op>(prefix, seg_combine<Op>(s_wave[r][wave], wave_seg_exclusive<Op>(incl)));
 #pragma unroll
         for (int k = 0; k < kBkVec; ++k) {
             if ((valid >> k) & 1u) {
@@ -458,7 +479,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
                     run.count += 1;
                     run.sum = val[k];
                 } else {
-                    run.sum = static_cast<V>(run.sum + val[k]);
+                    run.sum = op_apply<Op>(run.sum, val[k]);
                 }
             }
         }
@@ -469,7 +490,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
     }
 }
 
-template <typename K, typename V, int MODE, int R>
+template <typename K, typename V, int MODE, int R, typename Op>
 __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     const K* __restrict__ keys, const V* values_in, V* values_out, K* __restrict__ unique_out,
     V* __restrict__ aggregates_out, uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
@@ -559,14 +580,14 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                 s_wave[r][wave] = Seg<V>{count, static_cast<V>(count != 0 ? items - last : items)};
             }
         } else {
-            incl[r] = wave_seg_scan(fold_quad(val[r], h, valid));
+            incl[r] = wave_seg_scan<Op>(fold_quad<Op>(val[r], h, valid));
             if (lane == kWave - 1) s_wave[r][wave] = incl[r];
         }
     }
     __syncthreads();
     // Wave 0 turns the totals into in-tile carries and the aggregate (to LDS for the publisher).
     if (wave == 0) {
-        const Seg<V> a = scan_totals<V, R>(s_wave);
+        const Seg<V> a = scan_totals<Op, V, R>(s_wave);
         if (lane == 0) s_agg = a;
     }
     __syncthreads();
@@ -614,7 +635,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         if (staged) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                Seg<V> run = seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r]));
+                Seg<V> run = seg_combine<Op>(s_wave[r][wave], wave_seg_exclusive<Op>(incl[r]));
                 const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
                 const uint32_t valid = full ? 0xFu : quad_valid(row_first<R>(tile, r, tid), n);
 #pragma unroll
@@ -626,7 +647,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                             run.count += 1;
                             run.sum = val[r][k];
                         } else {
-                            run.sum = static_cast<V>(run.sum + val[r][k]);
+                            run.sum = op_apply<Op>(run.sum, val[r][k]);
                         }
                     }
                 }
@@ -644,11 +665,11 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         if (!in_place && wave != 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const Seg<V> carry = seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r]));
+                const Seg<V> carry = seg_combine<Op>(s_wave[r][wave], wave_seg_exclusive<Op>(incl[r]));
                 const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
                 if (carry.count != 0 || (h & 1u) != 0) {
                     const uint64_t first = row_first<R>(tile, r, tid);
-                    scan_quad_outputs(val[r], h, carry, inclusive, use_init, init, values_out, first,
+                    scan_quad_outputs<Op>(val[r], h, carry, inclusive, use_init, init, values_out, first,
                                       full ? 0xFu : quad_valid(first, n), vec_o);
                     stored |= 1u << r;
                 }
@@ -656,16 +677,16 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
         }
     }
 
-    Seg<V> prefix{0u, V(0)};
+    Seg<V> prefix{0u, op_identity<Op, V>()};
     if (tile > 0) {
         int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
-        Seg<V> acc{0u, V(0)};                           // states consumed so far (wave 0)
+        Seg<V> acc{0u, op_identity<Op, V>()};           // states consumed so far (wave 0)
         uint32_t spins = 0;
         uint32_t row = 0;
         while (true) {
             if (wave == 0) {
                 const int64_t j = top - static_cast<int64_t>(lane);
-                Seg<V> s{0u, V(0)};
+                Seg<V> s{0u, op_identity<Op, V>()};
                 const uint32_t st = j >= 0 ? read_state<V, COUNTED>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
                 const bool exists = j >= 0;
                 const bool published = st != kStInvalid;
@@ -694,8 +715,8 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                     const uint32_t sum_cut = heads_in ? min(cut, static_cast<uint32_t>(__builtin_ctzll(heads_in))) : cut;
                     Seg<V> window;
                     window.count = wave_reduce(take ? s.count : 0u, SumOp{});
-                    window.sum = wave_reduce((exists && lane <= sum_cut) ? s.sum : V(0), SumOp{});
-                    acc = seg_combine(window, acc);
+                    window.sum = wave_reduce((exists && lane <= sum_cut) ? s.sum : op_identity<Op, V>(), SwappedOp<Op>{});
+                    acc = seg_combine<Op>(window, acc);
                     const bool complete = stop_mask != 0 && cut == static_cast<uint32_t>(__builtin_ctzll(stop_mask));
                     const bool found_head = MODE == kModeScan && heads_in != 0;
                     action = (complete || found_head || top < kWave) ? kActDone : kActAdvance;
@@ -736,7 +757,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
             const bool claimed = s_ctl[row][0] != 0;
             row ^= 1u;
             if (claimed) {
-                const Seg<V> h = tile_aggregate<K, V, MODE, R>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_help);
+                const Seg<V> h = tile_aggregate<Op, K, V, MODE, R>(keys, values_in, n, help_tile, mask, vec_k, vec_v, s_help);
                 if (tid == 0) {
                     publish_state<V, COUNTED>(slot, kStPartial, h);
                     __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -756,7 +777,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                 __builtin_amdgcn_s_sleep(1);
         }
         if (tile > 0 || !owned) {
-            const Seg<V> incl_state = seg_combine(prefix, agg);
+            const Seg<V> incl_state = seg_combine<Op>(prefix, agg);
             publish_state<V, COUNTED>(my_slot, kStInclusive, incl_state);
         }
     }
@@ -765,11 +786,11 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
     if constexpr (MODE == kModeScan) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const Seg<V> run = seg_combine(prefix, seg_combine(s_wave[r][wave], wave_seg_exclusive(incl[r])));
+            const Seg<V> run = seg_combine<Op>(prefix, seg_combine<Op>(s_wave[r][wave], wave_seg_exclusive<Op>(incl[r])));
             const uint32_t h = (heads[r / 8] >> (4 * (r % 8))) & 0xFu;
             const uint64_t first = row_first<R>(tile, r, tid);
             if (((stored >> r) & 1u) == 0)
-                scan_quad_outputs(val[r], h, run, inclusive, use_init, init, values_out, first,
+                scan_quad_outputs<Op>(val[r], h, run, inclusive, use_init, init, values_out, first,
                                   full ? 0xFu : quad_valid(first, n), vec_o);
         }
     } else if (staged) {
@@ -781,17 +802,17 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
             if (aggregates_out) {
                 // Run lengths: staged positions (differences of consecutive heads) for kModeCount.
                 const V before = i > 0 ? (kBallotRuns ? static_cast<V>(s_run_sum[i] - s_run_sum[i - 1]) : s_run_sum[i])
-                                       : static_cast<V>(prefix.sum + s_run_sum[0]);
+                                       : op_apply<Op>(prefix.sum, s_run_sum[0]);
                 if (i > 0 || base > 0) aggregates_out[base + i - 1] = before;
             }
         }
         if (tid == 0 && tile_base + TILE >= n) {  // the tile holding the last item closes the last run
-            const Seg<V> total = seg_combine(prefix, agg);
+            const Seg<V> total = seg_combine<Op>(prefix, agg);
             if (aggregates_out) aggregates_out[total.count - 1] = total.sum;
             num_runs_out[0] = total.count;
         }
     } else {
-        reduce_rows_direct<K, V, MODE, R>(keys, values_in, unique_out, aggregates_out, num_runs_out, n, mask, tile, prefix,
+        reduce_rows_direct<Op, K, V, MODE, R>(keys, values_in, unique_out, aggregates_out, num_runs_out, n, mask, tile, prefix,
                                     s_wave, s_edge, vec_k, vec_v);
     }
 }
@@ -803,7 +824,7 @@ bool ranges_overlap(const void* a, uint64_t a_bytes, const void* b, uint64_t b_b
     return a_bytes != 0 && b_bytes != 0 && x < y + b_bytes && y < x + a_bytes;
 }
 
-template <typename K, typename V, int MODE>
+template <typename K, typename V, int MODE, typename Op = SumOp>
 int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* values_out, K* unique_out,
            V* aggregates_out, uint32_t* num_runs_out, uint64_t n, uint64_t key_mask, int inclusive, int use_init,
            V init, void* stream_ptr) {
@@ -843,7 +864,7 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     if (st != kOk) return st;
     const uint32_t tiles = static_cast<uint32_t>(ceil_div(n, kTile));
     LaunchScope scope(MODE == kModeScan ? "scan_by_key" : MODE == kModeReduce ? "reduce_by_key" : "runs_by_key", stream);
-    by_key_kernel<K, V, MODE, kBkRows<K, V, MODE>><<<tiles, kBkBlock, 0, stream>>>(
+    by_key_kernel<K, V, MODE, kBkRows<K, V, MODE>, Op><<<tiles, kBkBlock, 0, stream>>>(
         keys, values_in, values_out, unique_out, aggregates_out, num_runs_out, n, static_cast<K>(key_mask), states,
         inclusive, use_init, init, aligned16(keys), aligned16(values_in), values_out != nullptr && aligned16(values_out),
         values_out != nullptr && values_out == values_in, lookback_spin_limit());
@@ -928,5 +949,44 @@ LCPP_HIP_DEFINE_BY_KEY_VALUES(i64, int64_t, uint64_t)
 LCPP_HIP_DEFINE_BY_KEY_VALUES(u64, uint64_t, uint64_t)
 #undef LCPP_HIP_DEFINE_BY_KEY_VALUES
 #undef LCPP_HIP_DEFINE_BY_KEY
+
+// Min / max by key: values compare in their own type (signed as signed; floats like fmin / fmax); without
+// an initial value an exclusive scan's run heads get the operator's identity (the type's max / lowest,
+// a quiet NaN for floats).
+#define LCPP_HIP_DEFINE_BY_KEY_OP(NAME, OPT, KS, KT, KU, VS, VT)                                                       \
+    int lcpp_hip_scan_by_key_##NAME##_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys, const VT* values_in, \
+                                                 VT* values_out, uint64_t n, int inclusive, int use_init, VT init,    \
+                                                 uint64_t key_mask, void* stream) {                                  \
+        return by_key<KU, VT, kModeScan, OPT>(temp, temp_bytes, reinterpret_cast<const KU*>(keys), values_in,         \
+                                              values_out, nullptr, nullptr, nullptr, n, key_mask, inclusive, use_init, \
+                                              use_init ? init : OPT::identity<VT>(), stream);                        \
+    }                                                                                                                 \
+    int lcpp_hip_reduce_by_key_##NAME##_##KS##_##VS(void* temp, size_t temp_bytes, const KT* keys_in,                \
+                                                   const VT* values_in, KT* unique_out, VT* aggregates_out,          \
+                                                   uint32_t* num_runs_out, uint64_t n, uint64_t key_mask,            \
+                                                   void* stream) {                                                   \
+        return by_key<KU, VT, kModeReduce, OPT>(temp, temp_bytes, reinterpret_cast<const KU*>(keys_in), values_in,    \
+                                                nullptr, reinterpret_cast<KU*>(unique_out), aggregates_out,           \
+                                                num_runs_out, n, key_mask, 0, 0, OPT::identity<VT>(), stream);       \
+    }
+#define LCPP_HIP_DEFINE_BY_KEY_OP_VALUES(KS, KT, KU)                          \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, i32, int32_t)      \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, u32, uint32_t)     \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, f32, float)        \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, i64, int64_t)      \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, u64, uint64_t)     \
+    LCPP_HIP_DEFINE_BY_KEY_OP(min, MinValueOp, KS, KT, KU, f64, double)       \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, i32, int32_t)      \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, u32, uint32_t)     \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, f32, float)        \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, i64, int64_t)      \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, u64, uint64_t)     \
+    LCPP_HIP_DEFINE_BY_KEY_OP(max, MaxValueOp, KS, KT, KU, f64, double)
+LCPP_HIP_DEFINE_BY_KEY_OP_VALUES(i32, int32_t, uint32_t)
+LCPP_HIP_DEFINE_BY_KEY_OP_VALUES(u32, uint32_t, uint32_t)
+LCPP_HIP_DEFINE_BY_KEY_OP_VALUES(i64, int64_t, uint64_t)
+LCPP_HIP_DEFINE_BY_KEY_OP_VALUES(u64, uint64_t, uint64_t)
+#undef LCPP_HIP_DEFINE_BY_KEY_OP_VALUES
+#undef LCPP_HIP_DEFINE_BY_KEY_OP
 
 }  // extern "C"

@@ -2,7 +2,8 @@
 // argmin,argmax}_*), with the reference's module shape (src/lcpp/device/device_reduce.h:102-113 template,
 // :154-173 create, :184-210 temp queries, :280-436 Sum to ArgMax) and its record-time checks (:238-264).  Sum records one command; the kernels run on
 // the stream the command list is committed to.  ReduceByKey with a sum operator (:437-487, temp
-// query :207-223) runs lcpp_hip_reduce_by_key_sum_*, which writes 0 runs for empty input (:449-458).
+// query :207-223) with SumOp, MinOp or MaxOp runs lcpp_hip_reduce_by_key_{sum,min,max}_*, which writes 0
+// runs for empty input (:449-458).
 #pragma once
 
 #include <limits>
@@ -37,15 +38,17 @@ class DeviceReduce : public LuisaModule {
                                                         static_cast<uint32_t>(BLOCK_SIZE));
     }
 
-    // Runs of equal keys (under `equality_op`) reduce to (first key, sum); g_num_runs_out[0] = runs.
+    // Runs of equal keys (under `equality_op`) reduce to (first key, aggregate); g_num_runs_out[0] = runs.
     // d_unique_out and g_aggregates_out must hold one element per run.
-    template <NumericT KeyType, NumericT ValueType>
+    // The reduce operator: SumOp, MinOp or MaxOp.
+    template <NumericT KeyType, NumericT ValueType, typename Op>
+        requires(detail::by_key_op_ok<Op>)
     void ReduceByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
                      BufferView<ValueType> d_values_in, BufferView<KeyType> d_unique_out,
-                     BufferView<ValueType> g_aggregates_out, BufferView<uint> g_num_runs_out, SumOp,
+                     BufferView<ValueType> g_aggregates_out, BufferView<uint> g_num_runs_out, Op op,
                      size_t num_elements, KeyMaskEquality equality_op = {}) {
         static_assert(detail::by_key_key_ok<KeyType>, "ReduceByKey takes 4- or 8-byte integer keys");
-        static_assert(detail::by_key_value_ok<ValueType>, "ReduceByKey sums 4- or 8-byte integers, float or double");
+        static_assert(detail::by_key_value_ok<ValueType>, "ReduceByKey takes 4- or 8-byte integers, float or double");
         LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
         LCPP_ASSERT(num_elements <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
         LCPP_ASSERT(g_num_runs_out.size() >= 1u, "DeviceReduce run-count output view is empty.");
@@ -67,8 +70,8 @@ class DeviceReduce : public LuisaModule {
         uint32_t* runs = g_num_runs_out.data();
         const uint64_t mask = equality_op.mask;
         cmdlist << [=](hipStream_t s) {
-            const int rc = detail::reduce_by_key_sum(temp, temp_bytes, keys, values, unique, aggregates, runs,
-                                                     num_elements, mask, detail::stream_ptr(s));
+            const int rc = detail::reduce_by_key(op, temp, temp_bytes, keys, values, unique, aggregates, runs,
+                                                 num_elements, mask, detail::stream_ptr(s));
             luisa::detail::abi_check(rc, "DeviceReduce::ReduceByKey");
         };
     }

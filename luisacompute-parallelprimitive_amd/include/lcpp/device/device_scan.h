@@ -4,7 +4,7 @@
 // InclusiveScanInit with a sum, min or max operator (:321-368; operators common/thread_operators.h:49-74),
 // checked like validate_scan_views (:213-226).
 // The single-pass kernel is a decoupled look-back over the caller's temp storage.  The by-key
-// entry points (:424-597, temp query :310-315) run the segmented scan of lcpp_hip_scan_by_key_sum_*,
+// entry points (:424-597, temp query :310-315; SumOp, MinOp or MaxOp) run lcpp_hip_scan_by_key_{sum,min,max}_*,
 // checked like validate_scan_by_key_views (:228-246).
 #pragma once
 
@@ -111,28 +111,32 @@ class DeviceScan : public LuisaModule {
                                                       static_cast<uint32_t>(ITEMS_PER_THREAD));
     }
 
-    template <NumericT KeyType, NumericT ValueType>
+    // The scan operator: SumOp, MinOp or MaxOp.
+    template <NumericT KeyType, NumericT ValueType, typename Op>
+        requires(detail::by_key_op_ok<Op>)
     void ExclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
-                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, Op op,
                             size_t num_items, ValueType initial_value, KeyMaskEquality equality_op = {}) {
-        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
+        record_by_key(op, cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
                       initial_value, equality_op, "DeviceScan::ExclusiveScanByKey");
     }
 
-    template <NumericT KeyType, NumericT ValueType>
+    template <NumericT KeyType, NumericT ValueType, typename Op>
+        requires(detail::by_key_op_ok<Op>)
     void InclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
-                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, Op op,
                             size_t num_items, KeyMaskEquality equality_op = {}) {
-        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
+        record_by_key(op, cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
                       ValueType(0), equality_op, "DeviceScan::InclusiveScanByKey");
     }
 
     // Inclusive scan with `initial_value` prepended to every segment (device_scan.h:488-519).
-    template <NumericT KeyType, NumericT ValueType>
+    template <NumericT KeyType, NumericT ValueType, typename Op>
+        requires(detail::by_key_op_ok<Op>)
     void InclusiveScanByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
-                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, SumOp,
+                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, Op op,
                             size_t num_items, ValueType initial_value, KeyMaskEquality equality_op = {}) {
-        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, true,
+        record_by_key(op, cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, true,
                       initial_value, equality_op, "DeviceScan::InclusiveScanByKey");
     }
 
@@ -140,7 +144,7 @@ class DeviceScan : public LuisaModule {
     void ExclusiveSumByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
                            KeyMaskEquality equality_op = {}) {
-        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
+        record_by_key(SumOp{}, cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, false, true,
                       ValueType(0), equality_op, "DeviceScan::ExclusiveSumByKey");
     }
 
@@ -148,17 +152,17 @@ class DeviceScan : public LuisaModule {
     void InclusiveSumByKey(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
                            BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
                            KeyMaskEquality equality_op = {}) {
-        record_by_key(cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
+        record_by_key(SumOp{}, cmdlist, temp_storage, d_keys_in, d_values_in, d_values_out, num_items, true, false,
                       ValueType(0), equality_op, "DeviceScan::InclusiveSumByKey");
     }
 
   private:
-    template <NumericT KeyType, NumericT ValueType>
-    void record_by_key(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
+    template <typename Op, NumericT KeyType, NumericT ValueType>
+    void record_by_key(Op op, CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<KeyType> d_keys_in,
                        BufferView<ValueType> d_values_in, BufferView<ValueType> d_values_out, size_t num_items,
                        bool inclusive, bool use_init, ValueType init, KeyMaskEquality equality_op, const char* what) {
         static_assert(detail::by_key_key_ok<KeyType>, "scan by key takes 4- or 8-byte integer keys");
-        static_assert(detail::by_key_value_ok<ValueType>, "scan by key sums 4- or 8-byte integers, float or double");
+        static_assert(detail::by_key_value_ok<ValueType>, "scan by key takes 4- or 8-byte integers, float or double");
         LCPP_ASSERT(m_created, "DeviceScan::create must be called before dispatch.");
         LCPP_ASSERT(num_items <= std::numeric_limits<uint>::max(), "Too many items for DeviceScan.");
         if (num_items == 0u) return;
@@ -180,8 +184,8 @@ class DeviceScan : public LuisaModule {
         const int with_init = use_init ? 1 : 0;
         const uint64_t mask = equality_op.mask;
         cmdlist << [=](hipStream_t s) {
-            const int rc = detail::scan_by_key_sum(temp, temp_bytes, keys, in, out, num_items, inc, with_init,
-                                                   init_abi, mask, detail::stream_ptr(s));
+            const int rc = detail::scan_by_key(op, temp, temp_bytes, keys, in, out, num_items, inc, with_init,
+                                               init_abi, mask, detail::stream_ptr(s));
             luisa::detail::abi_check(rc, what);
         };
     }

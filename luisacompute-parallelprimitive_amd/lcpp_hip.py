@@ -126,8 +126,9 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_internal_by_key_needed_bytes", sz, u64, sz)
     for k in BY_KEY_KEY_SUFFIXES:
         for v in BY_KEY_VALUE_SUFFIXES:
-            sig(f"lcpp_hip_scan_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, u64, i32, i32, _CTYPE[v], u64, vp)
-            sig(f"lcpp_hip_reduce_by_key_sum_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
+            for op in ("sum", "min", "max"):
+                sig(f"lcpp_hip_scan_by_key_{op}_{k}_{v}", i32, vp, sz, vp, vp, vp, u64, i32, i32, _CTYPE[v], u64, vp)
+                sig(f"lcpp_hip_reduce_by_key_{op}_{k}_{v}", i32, vp, sz, vp, vp, vp, vp, vp, u64, u64, vp)
     sig("lcpp_hip_segment_reduce_temp_bytes", sz, u64)
     sig("lcpp_hip_segment_reduce_arg_temp_bytes", sz, u64, u64)
     sig("lcpp_hip_segmented_scan_temp_bytes", sz, u64, u64)
@@ -383,25 +384,30 @@ def profile_query(kernel: str) -> tuple[float, int]:
 
 
 def scan_by_key(key_suffix: str, value_suffix: str, keys, values_in, values_out, n: int, inclusive: bool = False,
-                init=None, key_mask: int = -1, temp=None, stream=None) -> None:
-    """DeviceScan::ExclusiveSumByKey / InclusiveSumByKey (sum operator); `init` as in
-    ExclusiveScanByKey / InclusiveScanByKey with an initial value; keys equal when
+                init=None, key_mask: int = -1, temp=None, stream=None, op: str = "sum") -> None:
+    """DeviceScan::ExclusiveSumByKey / InclusiveSumByKey (op "sum"), or ExclusiveScanByKey / InclusiveScanByKey
+    with MinOp ("min") or MaxOp ("max"); `init` as in the overloads with an initial value; keys equal when
     ((a ^ b) & key_mask) == 0."""
+    if op not in ("sum", "min", "max"):
+        raise ValueError(f"by-key operator {op!r}: sum, min or max")
     if temp is None:
         temp = _temp(scan_by_key_temp_bytes(n, ELEM_BYTES[key_suffix], ELEM_BYTES[value_suffix]), values_in.device)
     use_init = init is not None
-    call(f"lcpp_hip_scan_by_key_sum_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
+    call(f"lcpp_hip_scan_by_key_{op}_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
          ptr(keys), ptr(values_in), ptr(values_out), n, int(inclusive), int(use_init),
          _CTYPE[value_suffix](init if use_init else 0), key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))
 
 
 def reduce_by_key(key_suffix: str, value_suffix: str, keys, values, unique_out, aggregates_out, num_runs_out,
-                  n: int, key_mask: int = -1, temp=None, stream=None) -> None:
-    """DeviceReduce::ReduceByKey (sum operator): first key and sum of each run, and the run count."""
+                  n: int, key_mask: int = -1, temp=None, stream=None, op: str = "sum") -> None:
+    """DeviceReduce::ReduceByKey with SumOp (op "sum"), MinOp ("min") or MaxOp ("max"): first key and
+    aggregate of each run, and the run count."""
+    if op not in ("sum", "min", "max"):
+        raise ValueError(f"by-key operator {op!r}: sum, min or max")
     if temp is None:
         temp = _temp(reduce_by_key_temp_bytes(n, ELEM_BYTES[key_suffix], ELEM_BYTES[value_suffix]),
                      num_runs_out.device)
-    call(f"lcpp_hip_reduce_by_key_sum_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
+    call(f"lcpp_hip_reduce_by_key_{op}_{key_suffix}_{value_suffix}", ptr(temp), temp.numel() * temp.element_size(),
          ptr(keys), ptr(values), ptr(unique_out), ptr(aggregates_out), ptr(num_runs_out), n,
          key_mask & 0xFFFFFFFFFFFFFFFF, stream_handle(stream))
 

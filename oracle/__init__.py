@@ -70,6 +70,12 @@ def lib() -> C.CDLL:
             f = getattr(h, f"oracle_reduce_arg_{name}")
             f.restype = None
             f.argtypes = [vp, u64, i32, C.POINTER(ct), C.POINTER(u32)]
+            f = getattr(h, f"oracle_scan_by_key_minmax_{name}")
+            f.restype = None
+            f.argtypes = [vp, i32, vp, vp, u64, i32, i32, ct, u64, i32]
+            f = getattr(h, f"oracle_reduce_by_key_minmax_{name}")
+            f.restype = u64
+            f.argtypes = [vp, i32, vp, vp, vp, u64, u64, i32]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -362,6 +368,30 @@ def reduce_by_key_fp(keys: np.ndarray, values: np.ndarray, key_mask: int = -1):
     runs = lib().oracle_reduce_by_key_fp(_p(keys), keys.itemsize, _p(values), values.itemsize, _p(uniq), _p(agg),
                                          _p(ab), values.size, _mask(key_mask))
     return uniq[:runs], agg[:runs], ab[:runs]
+
+
+def scan_by_key_minmax(op: str, keys: np.ndarray, values: np.ndarray, inclusive: bool = False, init=None,
+                       key_mask: int = -1) -> np.ndarray:
+    """Min (op "min") / max ("max") scan by key in the values' own type; without `init` the operator's
+    identity (the type's max / lowest, NaN for floats) starts every run."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    out = np.empty_like(values)
+    sfx = _MINMAX_SUFFIX[values.dtype]
+    getattr(lib(), f"oracle_scan_by_key_minmax_{sfx}")(_p(keys), keys.itemsize, _p(values), _p(out), values.size,
+                                                       int(inclusive), int(init is not None),
+                                                       values.dtype.type(0 if init is None else init).item(),
+                                                       _mask(key_mask), int(op == "max"))
+    return out
+
+
+def reduce_by_key_minmax(op: str, keys: np.ndarray, values: np.ndarray, key_mask: int = -1):
+    """(first key of each run, min / max of each run)."""
+    keys, values = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    uniq = np.empty(max(keys.size, 1), keys.dtype)
+    agg = np.empty(max(values.size, 1), values.dtype)
+    runs = getattr(lib(), f"oracle_reduce_by_key_minmax_{_MINMAX_SUFFIX[values.dtype]}")(
+        _p(keys), keys.itemsize, _p(values), _p(uniq), _p(agg), values.size, _mask(key_mask), int(op == "max"))
+    return uniq[:runs], agg[:runs]
 
 
 # ---- stream compaction (oracle.c: select, partition, run-length encode) -------------------------

@@ -124,6 +124,51 @@ void oracle_scan_sum_f64(const double* in, long double* out, long double* abs_ou
         else { out[i] = run; abs_out[i] = arun; run += x; arun += fabsl(x); }
     }
 }
+/* Min / max scan and reduce by key (device_scan.h:424-597, device_reduce.h:437-487 with MinOp / MaxOp):
+ * item i starts a run when i == 0 or ((key[i] ^ key[i-1]) & mask) != 0 (4- or 8-byte keys).  At each
+ * run start run = start (init when use_init, else the identity: the type's max / lowest, NaN for
+ * floats); exclusive: out[i] = run, run = op(run, x); inclusive: run = op(run, x), out[i] = run, with
+ * op(run, x) = x when x is strictly smaller (larger) or run is a NaN.  Reduce: per run, the fold of its
+ * items from the identity; returns the run count. */
+static uint64_t by_key_load(const void* keys, int kb, uint64_t i) {
+    return kb == 4 ? ((const uint32_t*)keys)[i] : ((const uint64_t*)keys)[i];
+}
+#define ORACLE_BY_KEY_MINMAX(NAME, T, IDMIN, IDMAX)                                                          \
+    static T by_key_op_##NAME(T run, T x, int is_max) {                                                      \
+        return ((is_max ? x > run : x < run) || run != run) ? x : run;                                       \
+    }                                                                                                        \
+    void oracle_scan_by_key_minmax_##NAME(const void* keys, int kb, const T* in, T* out, uint64_t n,         \
+                                          int inclusive, int use_init, T init, uint64_t mask, int is_max) {  \
+        const T start = use_init ? init : (is_max ? IDMAX : IDMIN);                                          \
+        T run = start;                                                                                       \
+        for (uint64_t i = 0; i < n; ++i) {                                                                   \
+            if (i == 0 || ((by_key_load(keys, kb, i) ^ by_key_load(keys, kb, i - 1)) & mask) != 0) run = start; \
+            if (!inclusive) out[i] = run;                                                                    \
+            run = by_key_op_##NAME(run, in[i], is_max);                                                      \
+            if (inclusive) out[i] = run;                                                                     \
+        }                                                                                                    \
+    }                                                                                                        \
+    uint64_t oracle_reduce_by_key_minmax_##NAME(const void* keys, int kb, const T* in, void* unique, T* agg,  \
+                                                uint64_t n, uint64_t mask, int is_max) {                     \
+        uint64_t runs = 0;                                                                                   \
+        for (uint64_t i = 0; i < n; ++i) {                                                                   \
+            if (i == 0 || ((by_key_load(keys, kb, i) ^ by_key_load(keys, kb, i - 1)) & mask) != 0) {         \
+                if (kb == 4) ((uint32_t*)unique)[runs] = ((const uint32_t*)keys)[i];                         \
+                else ((uint64_t*)unique)[runs] = ((const uint64_t*)keys)[i];                                 \
+                agg[runs++] = (is_max ? IDMAX : IDMIN);                                                      \
+            }                                                                                                \
+            agg[runs - 1] = by_key_op_##NAME(agg[runs - 1], in[i], is_max);                                  \
+        }                                                                                                    \
+        return runs;                                                                                         \
+    }
+ORACLE_BY_KEY_MINMAX(i32, int32_t, INT32_MAX, INT32_MIN)
+ORACLE_BY_KEY_MINMAX(u32, uint32_t, UINT32_MAX, 0u)
+ORACLE_BY_KEY_MINMAX(f32, float, NAN, NAN)
+ORACLE_BY_KEY_MINMAX(i64, int64_t, INT64_MAX, INT64_MIN)
+ORACLE_BY_KEY_MINMAX(u64, uint64_t, UINT64_MAX, 0ull)
+ORACLE_BY_KEY_MINMAX(f64, double, NAN, NAN)
+#undef ORACLE_BY_KEY_MINMAX
+
 /* DeviceReduce<>::Min / Max (device_reduce.h:291-309): run = the type's max (min) / lowest (max), then
  * run = op(run, in[i]) left to right with the min / max scans' operator (a NaN item is skipped).
  * ArgMin / ArgMax (device_reduce.h:311-436 with ArgMinOp / ArgMaxOp, common/thread_operators.h:10-47):

@@ -764,6 +764,35 @@ void reduce_by_key_segments_of_100() {
 }
 
 // tests/device_reduce_test.cpp:483-513: empty input writes zero runs.
+// Scan and reduce by key with MinOp / MaxOp: keys {1,1,1,2,2,3}, values {5,3,7,1,9,4}.
+void by_key_min_max() {
+    auto& e = *g_env;
+    std::vector<int> keys{1, 1, 1, 2, 2, 3}, vals{5, 3, 7, 1, 9, 4}, scan_max(6), scan_min_init(6), uniq(6), mins(6);
+    uint runs = 0;
+    const size_t n = keys.size();
+    auto k = e.device.create_buffer<int>(n);
+    auto v = e.device.create_buffer<int>(n);
+    auto o1 = e.device.create_buffer<int>(n);
+    auto o2 = e.device.create_buffer<int>(n);
+    auto u = e.device.create_buffer<int>(n);
+    auto a = e.device.create_buffer<int>(n);
+    auto r = e.device.create_buffer<uint>(1);
+    auto st = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceScan<>::GetScanByKeyTempStorageBytes<int, int>(n)));
+    auto rt = e.device.create_buffer<uint>(
+        bytes_to_uint_count(DeviceReduce<>::GetReduceByKeyTempStorageBytes<int, int>(n)));
+    CommandList cmd;
+    e.scan.InclusiveScanByKey(cmd, st.view(), k.view(), v.view(), o1.view(), MaxOp{}, n);
+    e.scan.ExclusiveScanByKey(cmd, st.view(), k.view(), v.view(), o2.view(), MinOp{}, n, 4);
+    e.reduce.ReduceByKey(cmd, rt.view(), k.view(), v.view(), u.view(), a.view(), r.view(), MinOp{}, n);
+    e.stream << k.copy_from(luisa::span{keys}) << v.copy_from(luisa::span{vals}) << cmd.commit()
+             << o1.copy_to(luisa::span{scan_max}) << o2.copy_to(luisa::span{scan_min_init}) << u.copy_to(luisa::span{uniq})
+             << a.copy_to(luisa::span{mins}) << r.copy_to(&runs) << synchronize();
+    EXPECT((scan_max == std::vector<int>{5, 5, 7, 1, 9, 4}));
+    EXPECT((scan_min_init == std::vector<int>{4, 4, 3, 4, 1, 4}));
+    EXPECT(runs == 3u);
+    EXPECT(uniq[0] == 1 && uniq[1] == 2 && uniq[2] == 3 && mins[0] == 3 && mins[1] == 1 && mins[2] == 4);
+}
+
 void reduce_by_key_empty_input() {
     auto& e = *g_env;
     auto kb = e.device.create_buffer<int>(1), vb = e.device.create_buffer<int>(1);
@@ -1386,6 +1415,7 @@ const std::vector<Case>& cases() {
         {"scan_by_key_initial_values_float_in_place", scan_by_key_initial_values_float_in_place},
         {"reduce_by_key_segments_of_100", reduce_by_key_segments_of_100},
         {"reduce_by_key_empty_input", reduce_by_key_empty_input},
+        {"by_key_min_max", by_key_min_max},
         {"select_flagged_and_if_are_stable", select_flagged_and_if_are_stable},
         {"select_unique_by_key_and_flagged_if", select_unique_by_key_and_flagged_if},
         {"select_in_place_forms", select_in_place_forms},

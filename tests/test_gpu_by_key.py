@@ -39,21 +39,21 @@ def values_for(rng, n, vs):
     return rng.integers(info.min, info.max, n, dtype=dt, endpoint=True)
 
 
-def gpu_scan_by_key(hip, ks, vs, keys, vals, inclusive, init=None, key_mask=-1, in_place=False):
+def gpu_scan_by_key(hip, ks, vs, keys, vals, inclusive, init=None, key_mask=-1, in_place=False, op="sum"):
     n = keys.size
     d_k, d_v = to_dev(keys), to_dev(vals)
     d_o = d_v if in_place else torch.empty_like(d_v)
-    hip.scan_by_key(ks, vs, d_k, d_v, d_o, n, inclusive=inclusive, init=init, key_mask=key_mask)
+    hip.scan_by_key(ks, vs, d_k, d_v, d_o, n, inclusive=inclusive, init=init, key_mask=key_mask, op=op)
     return to_host(d_o, NP[vs], n)
 
 
-def gpu_reduce_by_key(hip, ks, vs, keys, vals, key_mask=-1):
+def gpu_reduce_by_key(hip, ks, vs, keys, vals, key_mask=-1, op="sum"):
     n = keys.size
     d_k, d_v = to_dev(keys), to_dev(vals)
     uniq = fill_dev(max(n, 1), keys.itemsize, 0x5A5A5A5A)
     agg = fill_dev(max(n, 1), vals.itemsize, 0x5A5A5A5A)
     runs = fill_dev(1, 4, 17)
-    hip.reduce_by_key(ks, vs, d_k, d_v, uniq, agg, runs, n, key_mask=key_mask)
+    hip.reduce_by_key(ks, vs, d_k, d_v, uniq, agg, runs, n, key_mask=key_mask, op=op)
     r = int(to_host(runs, np.uint32, 1)[0])
     return to_host(uniq, keys.dtype, r), to_host(agg, NP[vs], r), r
 
@@ -302,3 +302,81 @@ def test_temp_too_small_is_an_error(hip, dev):
     with pytest.raises(hip.LcppHipError) as e:
         hip.scan_by_key("i32", "i32", one, one, one.clone(), n, temp=temp)
     assert e.value.status == hip.ERR_TEMP_TOO_SMALL
+
+
+# ---- min / max operators -----------------------------------------------------------------------------
+# ScanByKey / ReduceByKey with MinOp / MaxOp (device_scan.h:424-597, device_reduce.h:437-487): bit-exact
+# against the oracle's left-to-right fold for every value type (floats included: the result is one of the
+# items or the initial value, and ties of -0.0 / +0.0 keep the older, as the oracle does).
+def minmax_values(rng, n, vs):
+    dt = np.dtype(NP[vs])
+    if dt.kind == "f":
+        v = np.round(rng.standard_normal(n) * 100).astype(dt)   # many ties, zeros of both signs
+        v[rng.random(n) < 0.3] *= -0.0
+        v[rng.random(n) < 0.02] = np.nan
+        return v
+    info = np.iinfo(dt)
+    return rng.integers(info.min, info.max, n, dtype=dt, endpoint=True)
+
+
+def same_bits(x, y):
+    return x.dtype == y.dtype and x.tobytes() == y.tobytes()
+
+
+@pytest.mark.parametrize("ks", ["i32", "u64"])
+@pytest.mark.parametrize("vs", ["i32", "u32", "f32", "i64", "u64", "f64"])
+@pytest.mark.parametrize("op", ["min", "max"])
+def test_minmax_by_key_vs_oracle(hip, orc, dev, ks, vs, op):
+    rng = np.random.default_rng(hash((ks, vs, op)) % 1000)
+    n = 5 * TILE + 1234
+    keys = run_keys(rng, n, 40.0, NP[ks])
+    vals = minmax_values(rng, n, vs)
+    log(f"by_key {op} {ks} {vs}")
+    for inclusive in (False, True):
+        for init in (None, NP[vs](3)):
+            got = gpu_scan_by_key(hip, ks, vs, keys, vals, inclusive, init, op=op)
+            want = orc.scan_by_key_minmax(op, keys, vals, inclusive, init)
+            assert same_bits(got, want), (inclusive, init)
+    uniq, agg, runs = gpu_reduce_by_key(hip, ks, vs, keys, vals, op=op)
+    ou, oa = orc.reduce_by_key_minmax(op, keys, vals)
+    assert runs == ou.size and np.array_equal(uniq, ou) and same_bits(agg, oa)
+
+
+@pytest.mark.parametrize("op", ["min", "max"])
+def test_minmax_by_key_long_runs_and_fallback(hip, orc, dev, op):
+    """Runs spanning many tiles (the look-back folds whole windows of predecessors), with every look-back
+    taking the fallback (spin limit 0) on the second pass."""
+    rng = np.random.default_rng(31)
+    n = 120 * TILE + 7
+    keys = run_keys(rng, n, 50000.0, np.int32)
+    vals = minmax_values(rng, n, "f32")
+    lib = hip.lib()
+    old = lib.lcpp_hip_get_lookback_spin_limit()
+    try:
+        for spin in (old, 0):
+            lib.lcpp_hip_set_lookback_spin_limit(spin)
+            log(f"by_key {op} long runs spin={spin}")
+            got = gpu_scan_by_key(hip, "i32", "f32", keys, vals, True, op=op)
+            assert same_bits(got, orc.scan_by_key_minmax(op, keys, vals, True))
+            uniq, agg, runs = gpu_reduce_by_key(hip, "i32", "f32", keys, vals, op=op)
+            ou, oa = orc.reduce_by_key_minmax(op, keys, vals)
+            assert runs == ou.size and same_bits(agg, oa)
+    finally:
+        lib.lcpp_hip_set_lookback_spin_limit(old)
+
+
+def test_minmax_by_key_staged_and_direct_tiles(hip, orc, dev):
+    """Reduce tiles with more runs than the LDS stage (runs of length 1-2) beside staged ones."""
+    n = 20 * REDUCE_TILE + 9
+    length = 1 + (np.arange(n) // 4096) % 6
+    starts = np.zeros(n, bool)
+    pos = 0
+    while pos < n:
+        starts[pos] = True
+        pos += int(length[pos])
+    keys = np.cumsum(starts).astype(np.uint32)
+    vals = minmax_values(np.random.default_rng(2), n, "i64")
+    for op in ("min", "max"):
+        uniq, agg, runs = gpu_reduce_by_key(hip, "u32", "i64", keys, vals, op=op)
+        ou, oa = orc.reduce_by_key_minmax(op, keys, vals)
+        assert runs == ou.size and np.array_equal(agg, oa)

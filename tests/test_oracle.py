@@ -345,6 +345,38 @@ def test_scan_minmax_signed_zero_keeps_earlier(orc):
     assert np.signbit(orc.scan_minmax("min", a, init=-0.0)).tolist() == [True] * 4
 
 
+@pytest.mark.parametrize("vdt", [np.int32, np.uint64, np.float32, np.float64])
+def test_minmax_by_key_vs_numpy(orc, vdt):
+    """Per run (split at the heads): np.minimum / maximum.accumulate (integers), np.fmin / fmax.accumulate
+    (floats with NaNs) for the scans, with the initial value put in front; reduceat for the reduce."""
+    rng = np.random.default_rng(8)
+    n = 3000
+    keys = np.repeat(np.arange(400), rng.integers(1, 14, 400))[:n].astype(np.int32)
+    n = keys.size
+    if np.dtype(vdt).kind == "f":
+        vals = rng.integers(-50, 50, n).astype(vdt)
+        vals[rng.random(n) < 0.05] = np.nan
+        fmin, fmax, ident = np.fmin, np.fmax, (np.nan, np.nan)
+    else:
+        info = np.iinfo(vdt)
+        vals = rng.integers(info.min, info.max, n, dtype=vdt, endpoint=True)
+        fmin, fmax, ident = np.minimum, np.maximum, (info.max, info.min)
+    heads = np.flatnonzero(np.r_[True, keys[1:] != keys[:-1]])
+    for op, uf, idv in (("min", fmin, ident[0]), ("max", fmax, ident[1])):
+        for inclusive in (False, True):
+            for init in (None, vdt(5)):
+                want = np.empty_like(vals)
+                start = idv if init is None else init
+                for a, b in zip(heads, np.r_[heads[1:], n]):
+                    run = uf.accumulate(np.r_[np.array([start], vals.dtype), vals[a:b]])
+                    want[a:b] = run[1:] if inclusive else run[:-1]
+                got = orc.scan_by_key_minmax(op, keys, vals, inclusive, init)
+                assert np.array_equal(got, want, equal_nan=np.dtype(vdt).kind == "f"), (op, inclusive, init)
+        u, agg = orc.reduce_by_key_minmax(op, keys, vals)
+        assert np.array_equal(u, keys[heads])
+        assert np.array_equal(agg, uf.reduceat(vals, heads), equal_nan=np.dtype(vdt).kind == "f")
+
+
 # ---- min / max / arg reductions ------------------------------------------------------------------
 def test_reduce_min_max_arg_known_answers(orc):
     """tests/device_reduce_test.cpp:218-345: float Max from the lowest identity, ArgMax's first equal
