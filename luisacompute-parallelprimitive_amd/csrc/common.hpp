@@ -161,6 +161,25 @@ __device__ __forceinline__ uint32_t popc_lanes_below(uint64_t mask) {
 
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
 
+// Lanes of the wave whose 8-bit digit equals this lane's.  Per digit bit: t = 0 or ~0 (the bit,
+// sign-extended by one bit-field extract), one ballot of t != 0, and differ |= ballot ^ t on each 32-bit
+// half as one three-input bit operation (truth table 0xF6: S0 | (S1 ^ S2)); peers = ~differ.  Four VALU
+// operations per bit.  The empty asm keeps t opaque, so that the ballot compares t itself instead of a
+// shifted copy of the digit (which costs a shift more per bit).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d) {
+    uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        uint32_t t = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int32_t>(d), b, 1));
+        asm volatile("" : "+v"(t));
+        const uint64_t m = wave_ballot(t != 0);
+        lo = __builtin_amdgcn_bitop3_b32(lo, static_cast<uint32_t>(m), t, 0xF6);
+        hi = __builtin_amdgcn_bitop3_b32(hi, static_cast<uint32_t>(m >> 32), t, 0xF6);
+    }
+    return (static_cast<uint64_t>(~hi) << 32) | ~lo;
+}
+
+
 // ------------------------------------------------------------------------------------------------
 // Agent-scope (whole-GPU, all XCDs) relaxed atomics for cross-workgroup status words.
 // ------------------------------------------------------------------------------------------------

@@ -126,21 +126,6 @@ __device__ __forceinline__ uint32_t digit_bits(U ordered, uint32_t shift, uint32
     else return static_cast<uint32_t>(ordered >> shift) & ((1u << num_bits) - 1u);
 }
 
-// Lanes of the wave whose 8-bit digit equals this lane's.  Per digit bit: t = 0 or ~0 (the bit,
-// sign-extended), one ballot of t, and peers &= ~(ballot ^ t) on each 32-bit half, which gfx950
-// folds into a single three-input bit operation per half.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d) {
-    uint32_t lo = ~0u, hi = ~0u;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const uint32_t t = static_cast<uint32_t>(static_cast<int32_t>(d << (31 - b)) >> 31);
-        const uint64_t m = wave_ballot(t != 0);
-        lo &= ~(static_cast<uint32_t>(m) ^ t);
-        hi &= ~(static_cast<uint32_t>(m >> 32) ^ t);
-    }
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 // --------------------------------------------------------------------------------------------
 // Histogram: digit counts of every pass for one portion.
 //

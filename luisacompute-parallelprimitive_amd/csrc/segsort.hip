@@ -1,5 +1,5 @@
 // DeviceSegmentedRadixSort and DeviceSegmentedSort (keys and key-value pairs, ascending and
-// descending, bit ranges, DoubleBuffer) for gfx950: a stable merge sort per segment.
+// descending, bit ranges, DoubleBuffer) for gfx950: a stable sort per segment.
 //
 // Reference paths (src/lcpp/device/): DeviceSegmentedSort<> (device_segmented_sort.h:43-505): a
 // stable merge sort by a comparator (lhs < rhs, or lhs > rhs for the descending forms) in passes of
@@ -8,27 +8,31 @@
 // (dispatch_key_merge, :300-420); DoubleBuffer forms flip the selector once per pass, ceil(log2 n)
 // times.  DeviceSegmentedRadixSort<> (device_segmented_radix_sort.h:26-246) is that sort with the
 // comparator "twiddled key bits [begin_bit, end_bit) compare less (greater)"; begin_bit == end_bit
-// leaves a DoubleBuffer untouched.
+// leaves a DoubleBuffer untouched.  Any stable sort by the same order gives the same output, so the
+// sort here is free to differ from the reference's merge passes.
 //
 // MI355X design:
-//   * Block phase: chunks of at most 2,048 items, each sorted by one 256-thread workgroup (8 items per
-//     thread).  Small segments (<= 512 items) are sorted together per 2,048-item tile of the item
-//     range (a joint sort with position labels when a tile holds more than two), medium ones (<= 2,048)
-//     by one workgroup each, and long ones chunk by chunk by a grid-stride kernel over tiles, so
-//     neither many tiny segments nor a few long ones leave the GPU idle.  Per chunk: a stable
-//     odd-even transposition sort of each thread's 8 items in registers,
-//     then 8 merge-path passes in LDS (widths 8 .. 1,024), each thread producing 8 outputs after one
-//     binary search; chunks are written to the output.
-//   * Global phase, only for segments longer than 2,048 items: merge-path passes of width 2,048, 4,096,
-//     ... between the output and a scratch buffer, over 2,048-item output tiles (merge-path splits by
-//     wave-level searches, inputs staged in LDS); a segment takes part while the width is below its
-//     length.  The block phase writes a segment with an odd number of global passes
-//     to the scratch buffer, so that every segment's last pass lands in the output.  The block phase
-//     also records the longest segment (and whether a small one exists) in per-stream device words (a
-//     slot of a static device array); launches with nothing to do exit after reading them.
+//   * Block phase: chunks sorted in LDS by one 256-thread workgroup each, C = 4,096 items in radix
+//     order and 2,048 in value order.  Small segments (<= 512 items) are sorted together per
+//     2,048-item tile of the item range (a joint merge sort with position labels when a tile holds more
+//     than two), medium ones (<= C) by one workgroup each, and long ones chunk by chunk by a grid-stride
+//     kernel over C-item tiles, so neither many tiny segments nor a few long ones leave the GPU idle.
+//   * Radix order, medium segments and chunks: a stable LSD radix sort in LDS, 8-bit digits, 4, 8 or
+//     16 items per thread by length; per pass a ballot match ranks each wave's items against per-wave
+//     digit counters, one workgroup scan orders (digit, wave), items are scattered to LDS and read back.
+//   * Value order, and small segments in either order: a stable odd-even transposition sort of each
+//     thread's 8 items in registers, then merge-path passes in LDS (widths 8 .. 1,024), each thread
+//     producing 8 outputs after one binary search.
+//   * Global phase, only for segments longer than C: merge-path passes of width C, 2 C, ... between the
+//     output and a scratch buffer, over 2,048-item output tiles (merge-path splits by wave-level
+//     searches, inputs staged in LDS); a segment takes part while the width is below its length.  The
+//     block phase writes a segment with an odd number of global passes to the scratch buffer, so that
+//     every segment's last pass lands in the output.  The block phase also records the longest segment
+//     (and whether a small one exists) in per-stream device words (a slot of a static device array);
+//     launches with nothing to do exit after reading them.
 //   * Orders: radix order compares (twiddled bits >> begin_bit) & mask (descending: the complement);
 //     value order (floats of DeviceSegmentedSort) compares the values, so -0.0 equals +0.0.
-// Algorithmic traffic: 2 * (sizeof(K) + sizeof(V)) per item in segments up to 2,048 items, plus the
+// Algorithmic traffic: 2 * (sizeof(K) + sizeof(V)) per item in segments up to C items, plus the
 // same per global pass for longer segments.
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
@@ -115,10 +119,11 @@ __device__ __forceinline__ uint32_t merge_path(uint32_t diag, uint32_t lw, uint3
     return merge_split(diag, lw, rw, [&](uint32_t mid) { return before<K, KIND>(right(diag - 1 - mid), left(mid), o); });
 }
 
-// Number of global passes a segment of `len` items takes (widths 2048, 4096, ... below len).
-__device__ __forceinline__ uint32_t global_passes(uint64_t len) {
+// Number of global passes a segment of `len` items takes after its chunks of `chunk` items are sorted
+// (widths chunk, 2 chunk, ... below len).
+__device__ __forceinline__ uint32_t global_passes(uint64_t len, uint32_t chunk) {
     uint32_t p = 0;
-    for (uint64_t w = kSsChunk; w < len; w *= 2) ++p;
+    for (uint64_t w = chunk; w < len; w *= 2) ++p;
     return p;
 }
 
@@ -210,6 +215,165 @@ __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* v
     }
 }
 
+// Radix order (o.value_order == 0): sorts the chunk [c, c + len) (len <= 256 ITEMS) like sort_chunk, by a
+// stable LSD radix sort in LDS over 8-bit digits of (twiddled bits >> begin_bit) & mask (complemented
+// for descending orders).  Wave w holds items [64 ITEMS w, 64 ITEMS (w + 1)): item 64 k + lane of its
+// range in register k.  Per pass: digits; each wave ranks its items with ballot matches and per-wave
+// digit counters; one workgroup scan turns the (digit, wave) counts into output offsets (digit-major,
+// wave order within a digit: stable); every item goes to LDS at its offset and is read back in the same
+// layout.  Items past len take digit 255 in every pass, so they stay behind the real ones; a wave with no
+// real item (its range starts at or past len) takes no part in ranking or scatter.  s_k / s_v hold
+// 256 ITEMS entries, s_cnt 4 x 256 counters, s_tot 4 words.  Collective, and may be in place like
+// sort_chunk (every item is read before the first barrier, written after the last).
+template <typename K, typename V, bool PAIRS, int KIND, int ITEMS>
+__device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, const V* values_in, V* vdst, uint64_t c,
+                                                 uint32_t len, const SortOrder& o, K* s_k, V* s_v, uint32_t* s_cnt,
+                                                 uint32_t* s_tot) {
+    static_assert(kSsBlock == 256, "thread t scans digit t");
+    static_assert(kSsBlock * ITEMS <= 0x10000, "ranks are packed in 16 bits");
+    constexpr int kWaves = kSsBlock / kWave;
+    constexpr uint32_t kPerWave = kWave * ITEMS;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint32_t first = wave * kPerWave + lane;  // item of register 0
+    // Register j is real when 64 j < left; items are addressed from per-lane bases, so that only these
+    // stay live and every register's offset is an instruction immediate.
+    const int32_t left = static_cast<int32_t>(len) - static_cast<int32_t>(first);
+    const K* kin = keys_in + c + first;
+    const V* vin = PAIRS ? values_in + c + first : nullptr;
+    K k[ITEMS];
+    V v[PAIRS ? ITEMS : 1];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        k[j] = j * kWave < left ? kin[j * kWave] : K(0);
+        if constexpr (PAIRS) v[j] = j * kWave < left ? vin[j * kWave] : V(0);
+    }
+    const uint32_t bits = o.mask == 0 ? 0u : 64u - static_cast<uint32_t>(__builtin_clzll(o.mask));
+    const uint32_t passes = (bits + 7) / 8;
+    for (uint32_t i = tid; i < kWaves * 256; i += kSsBlock) s_cnt[i] = 0;
+    __syncthreads();  // the previous chunk's readers of s_k / s_v and s_cnt are done
+    uint32_t* cnt = s_cnt + wave * 256;
+    const bool idle = wave * kPerWave >= len;  // wave-uniform
+    for (uint32_t p = 0; p < passes; ++p) {
+        const uint32_t shift = o.begin_bit + 8 * p;
+        const uint32_t nb = bits - 8 * p < 8 ? bits - 8 * p : 8u;
+        uint32_t rd[ITEMS];  // digit << 16 | rank within the wave's digit
+        if (!idle) {
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                uint32_t d = static_cast<uint32_t>((twiddle<K, KIND>(k[j]) >> shift)) & ((1u << nb) - 1u);
+                if (o.descending) d ^= (1u << nb) - 1u;
+                d = j * kWave < left ? d : 255u;
+                const uint64_t peers = match_digit(d);
+                const uint32_t below = popc_lanes_below(peers);
+                const uint32_t base = cnt[d];
+                rd[j] = (d << 16) | (base + below);
+                if ((peers >> lane) == 1ull) cnt[d] = base + below + 1;
+            }
+        }
+        __syncthreads();
+        // Thread t owns digit t: the digit's total over the waves, scanned over the digits.
+        uint32_t wc[kWaves];
+        uint32_t total = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            wc[w] = s_cnt[w * 256 + tid];
+            total += wc[w];
+        }
+        const uint32_t incl = wave_inclusive_scan(total, SumOp{});
+        if (lane == kWave - 1) s_tot[wave] = incl;
+        __syncthreads();
+        uint32_t off = incl - total;
+        for (uint32_t w = 0; w < wave; ++w) off += s_tot[w];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            s_cnt[w * 256 + tid] = off;
+            off += wc[w];
+        }
+        __syncthreads();
+        if (!idle) {
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                const uint32_t pos = cnt[rd[j] >> 16] + (rd[j] & 0xFFFFu);
+                s_k[pos] = k[j];
+                if constexpr (PAIRS) s_v[pos] = v[j];
+            }
+        }
+        __syncthreads();
+        if (!idle) {
+            const K* sk = s_k + first;
+            const V* sv = s_v + first;
+#pragma unroll
+            for (int j = 0; j < ITEMS; ++j) {
+                k[j] = sk[j * kWave];
+                if constexpr (PAIRS) v[j] = sv[j * kWave];
+            }
+        }
+        // Each wave clears its own counters (only it writes them before the next barrier).
+        for (uint32_t i = lane; i < 256; i += kWave) cnt[i] = 0;
+    }
+    K* kout = kdst + c + first;
+    V* vout = PAIRS ? vdst + c + first : nullptr;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+        if (j * kWave < left) {
+            kout[j * kWave] = k[j];
+            if constexpr (PAIRS) vout[j * kWave] = v[j];
+        }
+    }
+}
+
+// Radix order sorts chunks of up to kSsRadixChunk items in LDS; value order merges 2,048-item chunks.
+constexpr uint32_t kSsRadixChunk = 2 * kSsChunk;  // 4096
+
+// Items sorted in LDS per chunk, the width the global passes start from, and the longest medium segment.
+__device__ __forceinline__ uint32_t chunk_items(const SortOrder& o) {
+    return o.value_order ? kSsChunk : kSsRadixChunk;
+}
+
+// LDS of the block and chunk kernels, one byte array used either way: the merge sort's two padded key
+// (and value) buffers, or the radix sort's flat key (and value) arrays of kSsRadixChunk entries followed
+// by its 4 x 256 digit counters.  Integer keys are always sorted in radix order and need only the latter.
+template <typename K, typename V, bool PAIRS, int KIND>
+struct ChunkLds {
+    using KeyBuf = K[kSsPadded<PAIRS>];
+    using ValBuf = V[PAIRS ? kSsPadded<PAIRS> : 1];
+    static constexpr size_t kMergeKeys = sizeof(K) * 2 * kSsPadded<PAIRS>;
+    static constexpr size_t kMergeBytes = kMergeKeys + (PAIRS ? sizeof(V) * 2 * kSsPadded<PAIRS> : 0);
+    static constexpr size_t kRadixKeys = sizeof(K) * kSsRadixChunk;
+    static constexpr size_t kRadixVals = PAIRS ? sizeof(V) * kSsRadixChunk : 0;
+    static constexpr size_t kRadixBytes = kRadixKeys + kRadixVals + 4 * 256 * sizeof(uint32_t);
+    static constexpr size_t kBytes = (KIND == kKindFloat && kMergeBytes > kRadixBytes) ? kMergeBytes : kRadixBytes;
+    static_assert(kRadixKeys % 16 == 0 && kMergeKeys % 16 == 0, "value arrays stay aligned");
+};
+
+// Sorts one chunk of len <= chunk_items(o) items: radix order with 4, 8 or 16 items per thread
+// (whichever fits len), value order by sort_chunk.  `lds` is the kernel's ChunkLds array.
+template <typename K, typename V, bool PAIRS, int KIND>
+__device__ __forceinline__ void sort_any_chunk(const K* keys_in, K* kdst, const V* values_in, V* vdst, uint64_t c,
+                                               uint32_t len, const SortOrder& o, unsigned char* lds,
+                                               uint32_t* s_tot) {
+    using L = ChunkLds<K, V, PAIRS, KIND>;
+    if constexpr (KIND == kKindFloat) {
+        if (o.value_order) {
+            sort_chunk<K, V, PAIRS, KIND, false>(keys_in, kdst, values_in, vdst, c, len, o,
+                                                 reinterpret_cast<typename L::KeyBuf*>(lds),
+                                                 reinterpret_cast<typename L::ValBuf*>(lds + L::kMergeKeys), nullptr);
+            return;
+        }
+    }
+    K* s_k = reinterpret_cast<K*>(lds);
+    V* s_v = reinterpret_cast<V*>(lds + L::kRadixKeys);
+    uint32_t* s_cnt = reinterpret_cast<uint32_t*>(lds + L::kRadixKeys + L::kRadixVals);
+    if (len <= kSsBlock * 4)
+        radix_sort_chunk<K, V, PAIRS, KIND, 4>(keys_in, kdst, values_in, vdst, c, len, o, s_k, s_v, s_cnt, s_tot);
+    else if (len <= kSsBlock * 8)
+        radix_sort_chunk<K, V, PAIRS, KIND, 8>(keys_in, kdst, values_in, vdst, c, len, o, s_k, s_v, s_cnt, s_tot);
+    else
+        radix_sort_chunk<K, V, PAIRS, KIND, 16>(keys_in, kdst, values_in, vdst, c, len, o, s_k, s_v, s_cnt, s_tot);
+}
+
 // Segment of item i (begins ascending): the last segment whose begin <= i, or -1.
 __device__ __forceinline__ int64_t find_segment(const uint32_t* begins, uint32_t num_segments, uint64_t i) {
     uint32_t lo = 0, hi = num_segments;
@@ -243,11 +407,11 @@ __device__ __forceinline__ uint64_t wave_search(uint64_t lo, uint64_t hi, Pred p
     return lo;
 }
 
-// Medium segments (kSsSmall < items <= 2,048): one workgroup sorts each.  Workgroup g takes segment
+// Medium segments (kSsSmall < items <= chunk_items(o)): one workgroup sorts each.  Workgroup g takes segment
 // indices [g * per_group, (g + 1) * per_group), one per thread at a time, so that many small segments
 // cost a read of their offsets rather than a workgroup each; per_group is 1 whenever segments average
 // more than kSsSmall items.  The kernel also sets words[1] when a small segment exists and posts the
-// longest segment above 2,048 items to words[0] (a relaxed load first: same-address atomics serialise at
+// longest segment above a chunk to words[0] (a relaxed load first: same-address atomics serialise at
 // ~11 ns each).
 template <typename K, typename V, bool PAIRS, int KIND>
 __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_in, K* keys_out, const V* values_in,
@@ -255,11 +419,12 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
                                                                  const uint32_t* __restrict__ ends,
                                                                  uint32_t num_segments, uint32_t per_group,
                                                                  uint64_t n, SortOrder o, uint32_t* words) {
-    __shared__ K s_keys[2][kSsPadded<PAIRS>];
-    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    __shared__ __align__(16) unsigned char s_lds[ChunkLds<K, V, PAIRS, KIND>::kBytes];
     __shared__ uint32_t s_medium[kSsBlock];
+    __shared__ uint32_t s_tot[kSsBlock / kWave];
     __shared__ uint32_t s_count, s_small, s_long;
     const uint32_t tid = threadIdx.x;
+    const uint32_t chunk = chunk_items(o);
     const uint64_t g0 = static_cast<uint64_t>(blockIdx.x) * per_group;
     const uint64_t g1 = g0 + per_group < num_segments ? g0 + per_group : num_segments;
     if (tid == 0) s_small = 0, s_long = 0;
@@ -272,7 +437,7 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
             if (b < e && e <= n) {
                 const uint64_t len = e - b;
                 if (len <= kSsSmall) s_small = 1;  // benign race: every writer stores 1
-                else if (len <= kSsChunk) s_medium[atomicAdd(&s_count, 1u)] = static_cast<uint32_t>(x);
+                else if (len <= chunk) s_medium[atomicAdd(&s_count, 1u)] = static_cast<uint32_t>(x);
                 else atomicMax(&s_long, static_cast<uint32_t>(len));
             }
         }
@@ -281,8 +446,8 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
         for (uint32_t k = 0; k < count; ++k) {
             const uint32_t x2 = s_medium[k];
             const uint64_t b = begins[x2], e = ends[x2];
-            sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, b,
-                                                 static_cast<uint32_t>(e - b), o, s_keys, s_vals, nullptr);
+            sort_any_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b,
+                                              static_cast<uint32_t>(e - b), o, s_lds, s_tot);
         }
         __syncthreads();  // s_medium and s_count are rewritten next
     }
@@ -294,11 +459,11 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
     }
 }
 
-// Long segments (more than 2,048 items): grid-stride over 2,048-item tiles of the item range; a
-// tile sorts the segment-aligned chunks [b + 2,048 k, ...) that start inside it.  A long segment is
-// longer than a tile, so it meets a tile only as the segment holding the tile's first or last item, and
-// its chunk starts are a tile apart: a tile sorts at most two chunks.  A segment that takes an odd number
-// of global passes is sorted into the scratch buffer, so that its last pass writes the output (in place
+// Long segments (more than C = chunk_items(o) items): grid-stride over C-item tiles of the item range; a
+// tile sorts the segment-aligned chunks [b + C k, ...) that start inside it.  A long segment is longer
+// than a tile, so it meets a tile only as the segment holding the tile's first or last item, and its
+// chunk starts are a tile apart: a tile sorts at most two chunks.  A segment that takes an odd number of
+// global passes is sorted into the scratch buffer, so that its last pass writes the output (in place
 // when the scratch buffer is the input of a DoubleBuffer sort).
 template <typename K, typename V, bool PAIRS, int KIND>
 __global__ __launch_bounds__(kSsBlock) void segsort_chunk_kernel(const K* keys_in, K* keys_out, K* keys_scratch,
@@ -307,16 +472,17 @@ __global__ __launch_bounds__(kSsBlock) void segsort_chunk_kernel(const K* keys_i
                                                                  const uint32_t* __restrict__ ends,
                                                                  uint32_t num_segments, uint64_t n, SortOrder o,
                                                                  const uint32_t* longest) {
-    if (longest && *longest <= kSsChunk) return;  // no segment is longer than a chunk
-    __shared__ K s_keys[2][kSsPadded<PAIRS>];
-    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    const uint32_t chunk = chunk_items(o);
+    if (longest && *longest <= chunk) return;  // no segment is longer than a chunk
+    __shared__ __align__(16) unsigned char s_lds[ChunkLds<K, V, PAIRS, KIND>::kBytes];
     __shared__ uint64_t s_seg[2];
+    __shared__ uint32_t s_tot[kSsBlock / kWave];
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
-    const uint64_t tiles = ceil_div(n, kSsChunk);
+    const uint64_t tiles = ceil_div(n, chunk);
     for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
-        const uint64_t t0 = t * kSsChunk;
-        const uint64_t t1 = t0 + kSsChunk < n ? t0 + kSsChunk : n;
+        const uint64_t t0 = t * chunk;
+        const uint64_t t1 = t0 + chunk < n ? t0 + chunk : n;
         if (wave < 2) {
             const uint64_t at = wave == 0 ? t0 : t1 - 1;
             const uint64_t c = wave_search(0, num_segments, [&](uint64_t x) { return begins[x] > at; });
@@ -328,15 +494,15 @@ __global__ __launch_bounds__(kSsBlock) void segsort_chunk_kernel(const K* keys_i
         for (uint64_t c = c0; c <= c1; c = (c == c0 && c1 != c0) ? c1 : c1 + 1) {
             if (c == 0) continue;
             const uint64_t b = begins[c - 1], e = ends[c - 1];
-            if (b >= e || e > n || e - b <= kSsChunk || e <= t0 || b >= t1) continue;
+            if (b >= e || e > n || e - b <= chunk || e <= t0 || b >= t1) continue;
             const uint64_t from = b > t0 ? b : t0;
-            const uint64_t cs = b + ceil_div(from - b, kSsChunk) * kSsChunk;  // first chunk start >= from
+            const uint64_t cs = b + ceil_div(from - b, chunk) * chunk;  // first chunk start >= from
             if (cs >= t1 || cs >= e) continue;
-            const bool to_scratch = global_passes(e - b) & 1u;
-            sort_chunk<K, V, PAIRS, KIND, false>(keys_in, to_scratch ? keys_scratch : keys_out, values_in,
-                                          to_scratch ? values_scratch : values_out, cs,
-                                          static_cast<uint32_t>(e - cs < kSsChunk ? e - cs : kSsChunk), o, s_keys,
-                                          s_vals, nullptr);
+            const bool to_scratch = global_passes(e - b, chunk) & 1u;
+            sort_any_chunk<K, V, PAIRS, KIND>(keys_in, to_scratch ? keys_scratch : keys_out, values_in,
+                                              to_scratch ? values_scratch : values_out, cs,
+                                              static_cast<uint32_t>(e - cs < chunk ? e - cs : chunk), o, s_lds,
+                                              s_tot);
         }
     }
 }
@@ -459,7 +625,7 @@ struct MergePiece {
     uint32_t to_out;
 };
 
-// Global pass `pass` (width w = 2,048 << pass) over 2,048-item output tiles, grid-stride.  A segment of
+// Global pass `pass` (width w = chunk_items(o) << pass) over 2,048-item output tiles, grid-stride.  A segment of
 // P > pass global passes writes the output when P - 1 - pass is even and the scratch buffer otherwise,
 // reading the other one.  A segment longer than w is longer than a tile, so a tile meets at most two
 // such segments: the one holding its first item and the one holding its last; any other segment in the
@@ -473,7 +639,8 @@ __global__ __launch_bounds__(256) void segsort_merge_kernel(K* __restrict__ out_
                                                             const uint32_t* __restrict__ ends, uint32_t num_segments,
                                                             uint64_t n, uint32_t pass, SortOrder o,
                                                             const uint32_t* longest) {
-    const uint64_t w = static_cast<uint64_t>(kSsChunk) << pass;
+    const uint32_t chunk = chunk_items(o);
+    const uint64_t w = static_cast<uint64_t>(chunk) << pass;
     if (longest && w >= *longest) return;  // no segment is longer than this width
     __shared__ K s_keys[2][kSsPadded<PAIRS>];
     __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
@@ -497,7 +664,7 @@ __global__ __launch_bounds__(256) void segsort_merge_kernel(K* __restrict__ out_
             if (c == 0) continue;
             const uint64_t b = begins[c - 1], e = ends[c - 1];
             if (b >= e || e > n || e - b <= w || e <= t0 || b >= t1) continue;
-            const bool to_out = ((global_passes(e - b) - 1u - pass) & 1u) == 0;
+            const bool to_out = ((global_passes(e - b, chunk) - 1u - pass) & 1u) == 0;
             K* src_k = to_out ? scr_k : out_k;
             K* dst_k = to_out ? out_k : scr_k;
             V* src_v = to_out ? scr_v : out_v;
@@ -630,7 +797,7 @@ int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_ou
     }
     (void)width;
     int st;
-    // words[0]: the longest segment above 2,048 items; words[1]: set when a small segment exists.
+    // words[0]: the longest segment above a chunk; words[1]: set when a small segment exists.
     uint32_t* words = longest_word(stream);
     if (words) {
         st = launch_fill_u32(words, 2, 0u, stream);
@@ -661,7 +828,8 @@ int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_ou
             static_cast<uint32_t>(num_segments), n, o, words);
         st = check_hip(hipGetLastError(), "segsort tile launch");
         if (st != kOk) return st;
-        if (n <= kSsChunk) return kOk;
+        const uint32_t chunk = o.value_order ? kSsChunk : kSsRadixChunk;
+        if (n <= chunk) return kOk;
         LaunchScope scope2("segsort_chunk", stream);
         segsort_chunk_kernel<K, V, PAIRS, KIND><<<tile_grid, kSsBlock, 0, stream>>>(
             keys_in, keys_out, keys_scratch, values_in, values_out, values_scratch, begins, ends,
@@ -674,7 +842,7 @@ int segsort(K* keys_in, K* keys_out, K* keys_scratch, V* values_in, V* values_ou
     const uint32_t* longest = words;
     const unsigned grid = static_cast<unsigned>(tiles < cap ? tiles : cap);
     uint32_t pass = 0;
-    for (uint64_t w = kSsChunk; w < n; w *= 2, ++pass) {
+    for (uint64_t w = o.value_order ? kSsChunk : kSsRadixChunk; w < n; w *= 2, ++pass) {
         LaunchScope scope("segsort_merge", stream);
         segsort_merge_kernel<K, V, PAIRS, KIND><<<grid, 256, 0, stream>>>(
             keys_out, keys_scratch, values_out, values_scratch, begins, ends, static_cast<uint32_t>(num_segments), n,

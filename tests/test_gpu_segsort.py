@@ -100,9 +100,11 @@ def test_partial_bit_ranges(hip, orc, dev, lo, hi):
     check(orc, keys, b, e, gk, gv, values=vals, begin_bit=lo, end_bit=hi)
 
 
-@pytest.mark.parametrize("length", [2047, 2048, 2049, 4096, 5000, 65_537, 1 << 20])
+@pytest.mark.parametrize("length", [1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 5000, 8193, 65_537, 1 << 20])
 def test_long_segments_global_passes(hip, orc, dev, length):
-    """Segments longer than one 2,048-item chunk take the global merge passes (odd and even counts)."""
+    """Segment lengths at the in-LDS sort's size classes (radix order: 4, 8 or 16 items per thread up to
+    4,096 items; value order: 2,048-item chunks) and longer ones that take the global merge passes (odd
+    and even counts)."""
     rng = np.random.default_rng(length)
     n = length * 2 + 123
     keys = keys_for(rng, n, "i32")
@@ -112,6 +114,10 @@ def test_long_segments_global_passes(hip, orc, dev, length):
     for desc in (False, True):
         gk, gv = g_sort(hip, keys, b, e, values=vals, descending=desc)
         check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
+    fk = keys_for(rng, n, "f32")
+    for value_order in (False, True):
+        gk, gv = g_sort(hip, fk, b, e, values=vals, value_order=value_order)
+        check(orc, fk, b, e, gk, gv, values=vals, value_order=value_order)
 
 
 @pytest.mark.parametrize("ks", ["u64", "i64", "f64"])
@@ -122,8 +128,8 @@ def test_eight_byte_keys_and_values(hip, orc, dev, ks):
     n = 60_000
     keys = keys_for(rng, n, ks)
     vals = rng.integers(0, 1 << 63, n, dtype=np.uint64)
-    b = np.array([0, 5, 2000, 2049, 9000, 31_000], np.uint32)
-    e = np.array([5, 2000, 2049, 9000, 31_000, n - 7], np.uint32)
+    b = np.array([0, 5, 2000, 2049, 6145, 9000, 31_000], np.uint32)
+    e = np.array([5, 2000, 2049, 6145, 9000, 31_000, n - 7], np.uint32)
     for desc in (False, True):
         gk, gv = g_sort(hip, keys, b, e, values=vals, descending=desc)
         check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
