@@ -225,10 +225,17 @@ __device__ __forceinline__ void sort_chunk(const K* keys_in, K* kdst, const V* v
 // real item (its range starts at or past len) takes no part in ranking or scatter.  s_k / s_v hold
 // 256 ITEMS entries, s_cnt 4 x 256 counters, s_tot 4 words.  Collective, and may be in place like
 // sort_chunk (every item is read before the first barrier, written after the last).
-template <typename K, typename V, bool PAIRS, int KIND, int ITEMS>
+//
+// LABELS (the groups of sort_chunk: contiguous position ranges numbered in ascending order by bits 0-14
+// of s_label, written where bit 15 is set): every item carries its position's label, and after the key
+// passes `label_passes` more passes sort by the label's bytes.  Labels are the most significant part of
+// the order and ascend with position, so every group returns to its own positions, sorted by key.  The
+// carried labels move through s_l (256 ITEMS entries).
+template <typename K, typename V, bool PAIRS, int KIND, int ITEMS, bool LABELS = false>
 __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, const V* values_in, V* vdst, uint64_t c,
                                                  uint32_t len, const SortOrder& o, K* s_k, V* s_v, uint32_t* s_cnt,
-                                                 uint32_t* s_tot) {
+                                                 uint32_t* s_tot, const uint16_t* s_label = nullptr,
+                                                 uint16_t* s_l = nullptr, uint32_t label_passes = 0) {
     static_assert(kSsBlock == 256, "thread t scans digit t");
     static_assert(kSsBlock * ITEMS <= 0x10000, "ranks are packed in 16 bits");
     constexpr int kWaves = kSsBlock / kWave;
@@ -244,13 +251,16 @@ __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, cons
     const V* vin = PAIRS ? values_in + c + first : nullptr;
     K k[ITEMS];
     V v[PAIRS ? ITEMS : 1];
+    uint32_t lab[LABELS ? ITEMS : 1];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
         k[j] = j * kWave < left ? kin[j * kWave] : K(0);
         if constexpr (PAIRS) v[j] = j * kWave < left ? vin[j * kWave] : V(0);
+        if constexpr (LABELS) lab[j] = j * kWave < left ? s_label[first + j * kWave] : 0u;
     }
     const uint32_t bits = o.mask == 0 ? 0u : 64u - static_cast<uint32_t>(__builtin_clzll(o.mask));
-    const uint32_t passes = (bits + 7) / 8;
+    const uint32_t key_passes = (bits + 7) / 8;
+    const uint32_t passes = key_passes + (LABELS ? label_passes : 0u);
     for (uint32_t i = tid; i < kWaves * 256; i += kSsBlock) s_cnt[i] = 0;
     __syncthreads();  // the previous chunk's readers of s_k / s_v and s_cnt are done
     uint32_t* cnt = s_cnt + wave * 256;
@@ -262,8 +272,13 @@ __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, cons
         if (!idle) {
 #pragma unroll
             for (int j = 0; j < ITEMS; ++j) {
-                uint32_t d = static_cast<uint32_t>((twiddle<K, KIND>(k[j]) >> shift)) & ((1u << nb) - 1u);
-                if (o.descending) d ^= (1u << nb) - 1u;
+                uint32_t d;
+                if (!LABELS || p < key_passes) {
+                    d = static_cast<uint32_t>((twiddle<K, KIND>(k[j]) >> shift)) & ((1u << nb) - 1u);
+                    if (o.descending) d ^= (1u << nb) - 1u;
+                } else {
+                    d = ((lab[j] & 0x7FFFu) >> (8 * (p - key_passes))) & 0xFFu;
+                }
                 d = j * kWave < left ? d : 255u;
                 const uint64_t peers = match_digit(d);
                 const uint32_t below = popc_lanes_below(peers);
@@ -298,6 +313,7 @@ __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, cons
                 const uint32_t pos = cnt[rd[j] >> 16] + (rd[j] & 0xFFFFu);
                 s_k[pos] = k[j];
                 if constexpr (PAIRS) s_v[pos] = v[j];
+                if constexpr (LABELS) s_l[pos] = static_cast<uint16_t>(lab[j]);
             }
         }
         __syncthreads();
@@ -308,6 +324,7 @@ __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, cons
             for (int j = 0; j < ITEMS; ++j) {
                 k[j] = sk[j * kWave];
                 if constexpr (PAIRS) v[j] = sv[j * kWave];
+                if constexpr (LABELS) lab[j] = s_l[first + j * kWave];
             }
         }
         // Each wave clears its own counters (only it writes them before the next barrier).
@@ -317,7 +334,7 @@ __device__ __forceinline__ void radix_sort_chunk(const K* keys_in, K* kdst, cons
     V* vout = PAIRS ? vdst + c + first : nullptr;
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
-        if (j * kWave < left) {
+        if (j * kWave < left && (!LABELS || (lab[j] >> 15))) {
             kout[j * kWave] = k[j];
             if constexpr (PAIRS) vout[j * kWave] = v[j];
         }
@@ -522,17 +539,19 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
                                                                 uint32_t num_segments, uint64_t n, SortOrder o,
                                                                 const uint32_t* words) {
     if (words && words[1] == 0) return;  // no small segment
-    __shared__ K s_keys[2][kSsPadded<PAIRS>];
-    __shared__ V s_vals[PAIRS ? 2 : 1][PAIRS ? kSsPadded<PAIRS> : 1];
+    using L = ChunkLds<K, V, PAIRS, KIND>;
+    __shared__ __align__(16) unsigned char s_lds[L::kBytes];
     __shared__ uint16_t s_label[kSsChunk];
     __shared__ uint64_t s_seg[2];
+    __shared__ uint32_t s_tot[kSsBlock / kWave];
     __shared__ uint32_t s_inside;       // segments of at most 2,048 items wholly inside the tile
     __shared__ uint32_t s_pick[2][2];   // the first two of them (begin, end relative to t0)
     // Thread totals of the label scan share s_label's space (they are read before labels are written).
     uint32_t* s_total = reinterpret_cast<uint32_t*>(s_label);
     // Boundary counts per position, packed (begins in the low half, ends in the high half), live in the
-    // second key buffer before the joint sort uses it (at least 2,048 words for every key type).
-    uint32_t* s_count = reinterpret_cast<uint32_t*>(&s_keys[1][0]);
+    // sort's LDS before the joint sort uses it (2,048 words: the array holds at least 2 x 2,048 keys).
+    static_assert(L::kBytes >= kSsChunk * sizeof(uint32_t), "boundary counts fit the sort's LDS");
+    uint32_t* s_count = reinterpret_cast<uint32_t*>(s_lds);
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint64_t tiles = ceil_div(n, kSsChunk);
@@ -565,8 +584,8 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
         if (inside > 0 && inside <= 2) {
             for (uint32_t k = 0; k < inside; ++k) {
                 const uint32_t pb = s_pick[k][0], pe = s_pick[k][1];
-                sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, t0 + pb, pe - pb, o,
-                                                     s_keys, s_vals, nullptr);
+                sort_any_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, t0 + pb, pe - pb, o,
+                                                  s_lds, s_tot);
             }
         } else if (inside > 2) {
             for (uint32_t q = tid; q < kSsChunk; q += kSsBlock) s_count[q] = 0;
@@ -602,17 +621,35 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
                 const uint32_t opened = acc & 0xFFFFu, closed = acc >> 16;
                 s_label[base + j] = static_cast<uint16_t>((opened + closed) | (opened > closed ? 0x8000u : 0u));
             }
-            __syncthreads();  // labels complete; s_count (in s_keys[1]) is free again
-            sort_chunk<K, V, PAIRS, KIND, true>(keys_in, keys_out, values_in, values_out, t0, tlen, o, s_keys,
-                                                s_vals, s_label);
+            __syncthreads();  // labels complete; s_count (in the sort's LDS) is free again
+            bool merged = false;
+            if constexpr (KIND == kKindFloat) {
+                if (o.value_order) {
+                    sort_chunk<K, V, PAIRS, KIND, true>(keys_in, keys_out, values_in, values_out, t0, tlen, o,
+                                                        reinterpret_cast<typename L::KeyBuf*>(s_lds),
+                                                        reinterpret_cast<typename L::ValBuf*>(s_lds + L::kMergeKeys),
+                                                        s_label);
+                    merged = true;
+                }
+            }
+            if (!merged) {
+                // Labels ascend with position: the last one is the largest.
+                const uint32_t label_passes = (s_label[tlen - 1] & 0x7FFFu) < 256u ? 1u : 2u;
+                static_assert(L::kRadixKeys >= kSsChunk * (sizeof(K) + sizeof(uint16_t)), "labels fit");
+                radix_sort_chunk<K, V, PAIRS, KIND, kSsItems, true>(
+                    keys_in, keys_out, values_in, values_out, t0, tlen, o, reinterpret_cast<K*>(s_lds),
+                    reinterpret_cast<V*>(s_lds + L::kRadixKeys),
+                    reinterpret_cast<uint32_t*>(s_lds + L::kRadixKeys + L::kRadixVals), s_tot, s_label,
+                    reinterpret_cast<uint16_t*>(s_lds + kSsChunk * sizeof(K)), label_passes);
+            }
         }
         __syncthreads();
         // A small segment that starts in the tile and ends after it holds the tile's last item.
         if (c1 > 0) {
             const uint64_t b = begins[c1 - 1], e = ends[c1 - 1];
             if (b < e && e <= n && e - b <= kSsSmall && b >= t0 && e > t1)
-                sort_chunk<K, V, PAIRS, KIND, false>(keys_in, keys_out, values_in, values_out, b,
-                                                     static_cast<uint32_t>(e - b), o, s_keys, s_vals, nullptr);
+                sort_any_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b,
+                                                  static_cast<uint32_t>(e - b), o, s_lds, s_tot);
         }
         __syncthreads();  // s_seg, s_count and s_label are rewritten by the next tile
     }

@@ -189,6 +189,31 @@ def test_many_tiny_segments_and_large_input(hip, orc, dev):
     check(orc, keys2, b2, e2, gk, descending=True)
 
 
+@pytest.mark.parametrize("ks", ["u32", "f32", "i64"])
+def test_tiles_of_hundreds_of_segments(hip, orc, dev, ks):
+    """Segments of 1 to 8 items with gaps: a 2,048-item tile holds hundreds of them, so its position
+    labels exceed one byte (the radix order's joint sort then takes two label passes); pairs, ascending
+    and descending, a partial bit range, and value order for floats."""
+    rng = np.random.default_rng(31 + len(ks))
+    n = 1 << 18
+    keys = keys_for(rng, n, ks)
+    vals = np.arange(n, dtype=np.uint32)
+    lengths = rng.integers(1, 9, n // 4)
+    gaps = rng.integers(0, 2, n // 4)
+    b = np.cumsum(lengths + gaps) - lengths
+    keep = b + lengths <= n
+    b = b[keep].astype(np.uint32)
+    e = (b + lengths[keep]).astype(np.uint32)
+    for desc in (False, True):
+        gk, gv = g_sort(hip, keys, b, e, values=vals, descending=desc)
+        check(orc, keys, b, e, gk, gv, values=vals, descending=desc)
+    gk, gv = g_sort(hip, keys, b, e, values=vals, begin_bit=3, end_bit=13)
+    check(orc, keys, b, e, gk, gv, values=vals, begin_bit=3, end_bit=13)
+    if ks == "f32":
+        gk, gv = g_sort(hip, keys, b, e, values=vals, value_order=True)
+        check(orc, keys, b, e, gk, gv, values=vals, value_order=True)
+
+
 def test_errors(hip, dev):
     n = 10_000
     a = torch.zeros(n, dtype=torch.int32, device=dev)
