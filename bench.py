@@ -16,7 +16,7 @@ FETCH_SIZE/WRITE_SIZE summary (profiles/radix_onesweep_sortkeys_2p28_u32.md); `-
 runs the plain copy whose counter readings scale those counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu] [--copy-calibration MIB]
-                       [--only bykey|compact|reduce|scan|segmented|segsort|sortpairs|spmv|spmv-footprint]
+                       [--only bykey|compact|reduce|scan|segmented|segsort|segsort-sweep|sortpairs|spmv|spmv-footprint]
 """
 from __future__ import annotations
 
@@ -401,7 +401,38 @@ EXTRAS = {"reduce": extra_reduce, "scan": extra_scan, "sortpairs": extra_sort_pa
           "bykey": extra_by_key, "compact": extra_compact,
           "segmented": extra_segmented, "segsort": extra_segsort}
 # Studies run only when named with --only.
-STUDIES = {"spmv-footprint": study_spmv_footprint}
+def study_segsort_sweep(hip, dev, steps, warmup, extra):
+    import torch
+    # DeviceSegmentedRadixSort::SortKeys over 2^24 uint32 keys in equal segments of 4 .. 65,536 items (the
+    # tile kernel's joint sorts, the block kernel's one sort per segment, the chunk kernel plus global
+    # merge passes), and SortPairs with uint32 values at three of the lengths.  Not part of the default run.
+    m = 1 << 24
+    keys = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_HI, keys, m, SEED + 13)
+    vals = torch.empty(m, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_U32_IOTA, vals, m, 0)
+    ko, vo = torch.empty_like(keys), torch.empty_like(vals)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.segmented_sort_pairs_temp_bytes(m, 4, 4)), dtype=torch.int32,
+                       device=dev)
+    for seg_len, pairs in ((4, False), (16, False), (64, False), (256, False), (1024, False), (2048, False),
+                           (4096, False), (65536, False), (64, True), (1024, True), (4096, True)):
+        segs = m // seg_len
+        begins = torch.arange(segs, dtype=torch.int64, device=dev).mul_(seg_len).to(torch.int32)
+        ends = begins + seg_len
+        if pairs:
+            call = lambda: hip.segmented_sort("u32", keys, ko, m, segs, begins, ends, values_in=vals, values_out=vo,
+                                              temp=temp)
+        else:
+            call = lambda: hip.segmented_sort("u32", keys, ko, m, segs, begins, ends, temp=temp)
+        t = time_steps(call, steps, warmup)
+        moved = (16 if pairs else 8) * m
+        extra[f"segmented_radix_sort_{'pairs' if pairs else 'keys'}_u32_2p24_{seg_len}"] = {
+            **t.fields(), "Gkeys_per_s": round(m / t.mean / 1e6, 2), "GBps": rate(moved, t.mean),
+            "frac": round(moved / t.mean / 1e6 / HBM_PEAK_GBS, 4)}
+        del begins, ends
+
+
+STUDIES = {"spmv-footprint": study_spmv_footprint, "segsort-sweep": study_segsort_sweep}
 
 
 def run_extras(hip, dev, steps, warmup, names, copy=None):
