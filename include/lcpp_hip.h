@@ -559,9 +559,10 @@ int lcpp_hip_internal_radix_rank_mode(int mode);
 int lcpp_hip_internal_radix_precount(int enable);
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);
 size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int words, int staged);
-/* 1 when a segmented sort called now on `stream` would use a per-stream device word (eager calls), 0 when
- * it would not (calls recorded into a graph; a graph may replay on any stream). */
-int lcpp_hip_internal_segsort_uses_stream_slot(void* stream);
+/* The device words a segmented sort called now on `stream` would use, without taking them: 1 the stream's
+ * slot (eager calls), 2 a slot of the call's own (calls recorded into a graph, which may replay on any
+ * stream), 0 none (slots used up: the kernels then run without their early exits). */
+int lcpp_hip_internal_segsort_slot_kind(void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

@@ -776,45 +776,81 @@ uint32_t reference_pass_count(uint64_t n) {
     return p;
 }
 
-// Two device words per (device, stream) receive the longest segment and the small-segment flag of the
-// call in flight on that stream (eager calls on one stream run in order, so they never share them while
-// running).  The words are slots of a static device array (each GPU holds its own copy, found by
-// hipGetSymbolAddress), handed out to streams on their first call; no entry point allocates.  A call
-// recorded into a graph gets no words: the graph may later replay on any stream, beside eager calls
-// or other replays, so its launches must not share a slot.  Such calls, and calls past kLongestSlots
-// distinct streams, get nullptr, and their kernels run without the early exits (same results).
-constexpr uint32_t kLongestSlots = 4096;
+// Two device words per call receive the longest segment and the small-segment flag: slots of a static
+// device array (each GPU holds its own copy, found by hipGetSymbolAddress); no entry point allocates.
+// An eager call uses its stream's slot, handed out on the stream's first call: eager calls on one stream
+// run in order, so they never share it while running.  A call recorded into a graph gets a slot of its
+// own, never handed out again, so the graph's replays share their words with no eager call and no other
+// graph (only with concurrent replays of the same graph, which share every buffer of the call anyway).
+// Past kLongestSlots slots, and for a call recorded before any eager call on its device (the array's
+// address is not looked up during a capture), a call gets nullptr and its kernels run without the early
+// exits (same results).
+constexpr uint32_t kLongestSlots = 16384;
 __device__ uint32_t g_longest_slots[2 * kLongestSlots];
 
-uint32_t* longest_word(hipStream_t stream) {
+enum : int { kSlotNone = 0, kSlotStream = 1, kSlotOwn = 2 };
+
+struct SlotPool {
+    std::mutex mu;
+    std::map<std::pair<int, hipStream_t>, uint32_t*> stream_words;
+    std::map<int, std::pair<uint32_t*, uint32_t>> devices;  // device -> (array address, next slot)
+};
+SlotPool& slot_pool() {
+    static SlotPool pool;
+    return pool;
+}
+
+// 0: eager, 1: recording into a graph, -1: the query failed.
+int capture_state(hipStream_t stream) {
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
         (void)hipGetLastError();
-        return nullptr;
+        return -1;
     }
-    if (capture != hipStreamCaptureStatusNone) return nullptr;
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, uint32_t*> words;
-    static std::map<int, std::pair<uint32_t*, uint32_t>> slots;  // device -> (array address, next slot)
+    return capture != hipStreamCaptureStatusNone ? 1 : 0;
+}
+
+// The slot a call on `stream` would use now (kSlot*); with `take`, the slot itself (nullptr for
+// kSlotNone), handed out if it is new.
+int longest_slot(hipStream_t stream, bool take, uint32_t** word) {
+    if (word) *word = nullptr;
+    const int capturing = capture_state(stream);
+    if (capturing < 0) return kSlotNone;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
+    if (hipGetDevice(&dev) != hipSuccess) return kSlotNone;
+    SlotPool& pool = slot_pool();
+    std::lock_guard<std::mutex> lock(pool.mu);
     const auto key = std::make_pair(dev, stream);
-    const auto it = words.find(key);
-    if (it != words.end()) return it->second;
-    auto& slot = slots[dev];
-    if (!slot.first) {
+    if (!capturing) {
+        const auto it = pool.stream_words.find(key);
+        if (it != pool.stream_words.end()) {
+            if (word) *word = it->second;
+            return kSlotStream;
+        }
+    }
+    auto& d = pool.devices[dev];
+    if (d.second >= kLongestSlots) return kSlotNone;
+    // The array's address is looked up by an eager call only: no runtime query runs inside a capture.
+    if (capturing && !d.first) return kSlotNone;
+    if (!take) return capturing ? kSlotOwn : kSlotStream;
+    if (!d.first) {
         void* base = nullptr;
         if (hipGetSymbolAddress(&base, HIP_SYMBOL(g_longest_slots)) != hipSuccess || !base) {
             (void)hipGetLastError();
-            return nullptr;
+            return kSlotNone;
         }
-        slot.first = static_cast<uint32_t*>(base);
+        d.first = static_cast<uint32_t*>(base);
     }
-    if (slot.second >= kLongestSlots) return nullptr;
-    uint32_t* word = slot.first + 2 * slot.second++;
-    words.emplace(key, word);
-    return word;
+    uint32_t* w = d.first + 2 * d.second++;
+    if (!capturing) pool.stream_words.emplace(key, w);
+    if (word) *word = w;
+    return capturing ? kSlotOwn : kSlotStream;
+}
+
+uint32_t* longest_word(hipStream_t stream) {
+    uint32_t* w = nullptr;
+    longest_slot(stream, true, &w);
+    return w;
 }
 
 template <typename K, typename V, bool PAIRS, int KIND>
@@ -980,10 +1016,10 @@ using namespace lcpp_hip;
 
 extern "C" {
 
-// 1 when a segmented sort called now on `stream` would use a per-stream slot word (an eager call), 0 when
-// it would not (a call recorded into a graph, or past the slot count).
-int lcpp_hip_internal_segsort_uses_stream_slot(void* stream) {
-    return longest_word(static_cast<hipStream_t>(stream)) != nullptr ? 1 : 0;
+// The words a segmented sort called now on `stream` would use, without taking them: 1 the stream's slot
+// (an eager call), 2 a slot of its own (a call recorded into a graph), 0 none (past the slot count).
+int lcpp_hip_internal_segsort_slot_kind(void* stream) {
+    return longest_slot(static_cast<hipStream_t>(stream), false, nullptr);
 }
 
 size_t lcpp_hip_segmented_sort_keys_temp_bytes(uint64_t n, size_t key_bytes) {

@@ -79,7 +79,7 @@ def _declare(lib: C.CDLL) -> None:
     sig("lcpp_hip_profile_names", i32, C.c_char_p, sz)
     sig("lcpp_hip_device_copy", i32, vp, vp, u64, vp)
     sig("lcpp_hip_scan_exclusive_sum_u32_noalloc", i32, vp, vp, u64, vp)
-    sig("lcpp_hip_internal_segsort_uses_stream_slot", i32, vp)
+    sig("lcpp_hip_internal_segsort_slot_kind", i32, vp)
     sig("lcpp_hip_reduce_temp_bytes_policy", sz, u64, sz, u32, u32)
     sig("lcpp_hip_reduce_temp_bytes", sz, u64, sz)
     sig("lcpp_hip_scan_temp_bytes_policy", sz, u64, sz, u32, u32, i32, i32)

@@ -98,29 +98,82 @@ def test_captured_sequence_replays_match_eager(hip, dev):
             assert np.all(g[lo + 1:hi] >= g[lo:hi - 1])
 
 
-def test_segmented_sort_takes_no_stream_slot_under_capture(hip, dev):
-    """An eager segmented sort uses a per-stream device word for its early exits; a call recorded into a
-    graph must not (the graph may replay on any stream beside eager calls and other replays), so its
-    kernels run without the early exits.  Checked through the library's own query, inside and outside
-    a capture on the same stream."""
+def test_segmented_sort_slot_kinds_under_capture(hip, dev):
+    """An eager segmented sort uses its stream's device words for the early exits; a call recorded into a
+    graph gets words of its own (the graph may replay on any stream beside eager calls and other
+    replays).  Checked through the library's own query, which takes no slot, inside and outside a capture
+    on the same stream."""
     import ctypes
     lib = hip.lib()
     handle = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     side = torch.cuda.Stream()
+    n = 5000
+    keys = torch.arange(n, 0, -1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(keys)
+    b = torch.tensor([0, 2000], dtype=torch.int32, device=dev)
+    e = torch.tensor([2000, n], dtype=torch.int32, device=dev)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.segmented_sort_keys_temp_bytes(n, 4)), dtype=torch.int32,
+                       device=dev)
     with torch.cuda.stream(side):
-        assert lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()) == 1
-    x = torch.ones(5000, dtype=torch.int32, device=dev)
-    y = torch.empty_like(x)
-    temp = torch.empty(hip.bytes_to_uint_count(hip.scan_temp_bytes(5000, 4)), dtype=torch.int32, device=dev)
+        hip.segmented_sort("u32", keys, out, n, 2, b, e, temp=temp)  # eager: the stream's slot
+        assert lib.lcpp_hip_internal_segsort_slot_kind(handle()) == 1
     torch.cuda.synchronize()
     seen = []
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        seen.append(lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()))
-        hip.scan_sum("u32", x, y, 5000, temp=temp)
+        seen.append(lib.lcpp_hip_internal_segsort_slot_kind(handle()))
+        hip.segmented_sort("u32", keys, out, n, 2, b, e, temp=temp)
+    out.zero_()
     graph.replay()
     torch.cuda.synchronize()
-    assert seen == [0]
+    assert seen == [2]
     with torch.cuda.stream(side):
-        assert lib.lcpp_hip_internal_segsort_uses_stream_slot(handle()) == 1
-    assert torch.equal(y, torch.arange(5000, dtype=torch.int32, device=dev))
+        assert lib.lcpp_hip_internal_segsort_slot_kind(handle()) == 1
+    want = torch.cat([torch.arange(n - 1999, n + 1, dtype=torch.int32, device=dev),
+                      torch.arange(1, n - 1999, dtype=torch.int32, device=dev)])
+    assert torch.equal(out, want)
+
+
+def test_segmented_sort_graphs_replayed_beside_each_other(hip, orc, dev):
+    """Two segmented sorts recorded on one stream into two graphs (one with small and medium segments, one
+    with segments that take global passes) replay at the same time on two other streams while an eager
+    segmented sort runs on the capture stream: each call has its own device words, so every result is
+    exact on every repetition."""
+    rng = np.random.default_rng(91)
+    n = 300_000
+    keys = rng.integers(0, 1 << 32, n, dtype=np.uint64).astype(np.uint32)
+    cases = [(np.arange(0, n, 700, dtype=np.uint32), np.minimum(np.arange(0, n, 700) + 700, n).astype(np.uint32)),
+             (np.array([0, 100_000], np.uint32), np.array([100_000, n], np.uint32)),
+             (np.arange(0, n, 37, dtype=np.uint32), np.minimum(np.arange(0, n, 37) + 37, n).astype(np.uint32))]
+    d_keys = torch.from_numpy(keys.view(np.int32)).to(dev)
+    outs = [torch.empty_like(d_keys) for _ in cases]
+    temps = [torch.empty(hip.bytes_to_uint_count(hip.segmented_sort_keys_temp_bytes(n, 4)), dtype=torch.int32,
+                         device=dev) for _ in cases]
+    offs = [(torch.from_numpy(b.view(np.int32)).to(dev), torch.from_numpy(e.view(np.int32)).to(dev))
+            for b, e in cases]
+    call = lambda i: hip.segmented_sort("u32", d_keys, outs[i], n, len(cases[i][0]), offs[i][0], offs[i][1],
+                                        temp=temps[i])
+    capture = torch.cuda.Stream()
+    with torch.cuda.stream(capture):
+        call(2)  # an eager call first: the capture stream's slot
+    torch.cuda.synchronize()
+    graphs = [torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()]
+    for i in (0, 1):
+        with torch.cuda.graph(graphs[i], stream=capture):
+            call(i)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    want = [orc.segmented_sort(keys, b, e, keys_out=np.zeros(n, np.uint32))[0] for b, e in cases]
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                graphs[i].replay()
+        with torch.cuda.stream(capture):
+            call(2)
+        torch.cuda.synchronize()
+        for i in range(3):
+            got = outs[i].cpu().numpy().view(np.uint32)
+            np.testing.assert_array_equal(got, want[i], err_msg=f"rep {rep} call {i}")
