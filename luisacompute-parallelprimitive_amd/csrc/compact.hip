@@ -186,7 +186,8 @@ struct LaneItems {
     LaneMask<ITEMS> heads;  // run heads (run-length modes)
 };
 
-template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS>
+// LOADED: t.x already holds the items (vector_load_items); only the masks are computed.
+template <typename U, typename P, typename V, int MODE, bool FLAGS, int ITEMS, bool LOADED = false>
 __device__ __forceinline__ void load_lane(const CompactArgs<U, P, V>& a, uint64_t seg, LaneItems<U, V, ITEMS>& t) {
     using M = LaneMask<ITEMS>;
     const uint32_t lane = lane_id();
@@ -196,7 +197,7 @@ __device__ __forceinline__ void load_lane(const CompactArgs<U, P, V>& a, uint64_
         const uint64_t i = seg + static_cast<uint64_t>(kWave) * j + lane;
         const bool ok = i < a.n;
         valid |= static_cast<M>(ok ? 1 : 0) << j;
-        t.x[j] = ok ? a.in[i] : U(0);
+        if constexpr (!LOADED) t.x[j] = ok ? a.in[i] : U(0);
         if constexpr (MODE == kUniqueByKey) t.v[j] = ok ? a.values_in[i] : V(0);
     }
     t.valid = valid;
@@ -258,6 +259,33 @@ __device__ __forceinline__ void load_lane(const CompactArgs<U, P, V>& a, uint64_
             }
         }
     }
+}
+
+// The wave's 64 x ITEMS items (all inside the input, which is 16-byte aligned) read as 16-byte vectors,
+// lane l taking vector r of every 64: items seg + 64 VEC r + VEC l + c.  They reach the lane-strided
+// layout (item seg + 64 j + l in register j) through the wave's own region of LDS `wst`: vectors are
+// written at their item offsets and read back strided.  Measured on select-if / partition-if over
+// 2^28 u32: 0.463 -> 0.439 ms and 0.581 -> 0.549 ms against one 4-byte load per item and register.
+template <typename U, int ITEMS>
+__device__ __forceinline__ void vector_load_items(const U* in, uint64_t seg, U* wst, U (&x)[ITEMS]) {
+    constexpr int VEC = 16 / sizeof(U);
+    struct alignas(16) Vec {
+        U c[VEC];
+    };
+    static_assert(sizeof(Vec) == 16 && ITEMS % VEC == 0, "whole 16-byte vectors per lane");
+    const uint32_t lane = lane_id();
+    const Vec* src = reinterpret_cast<const Vec*>(in + seg);
+    Vec q[ITEMS / VEC];
+#pragma unroll
+    for (int r = 0; r < ITEMS / VEC; ++r) q[r] = src[kWave * r + lane];
+#pragma unroll
+    for (int r = 0; r < ITEMS / VEC; ++r) {
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) wst[kWave * VEC * r + VEC * lane + c] = q[r].c[c];
+    }
+    // Same wave, same element type: the reads follow the writes in LDS order.
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) x[j] = wst[kWave * j + lane];
 }
 
 struct MaxU32Op {
@@ -381,7 +409,18 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
     const uint64_t seg = static_cast<uint64_t>(tile) * kTile + static_cast<uint64_t>(wave) * kWave * ITEMS;
 
     LaneItems<U, V, ITEMS> t;
-    load_lane<U, P, V, MODE, FLAGS, ITEMS>(a, seg, t);
+    bool vector_loaded = false;
+    if constexpr ((MODE == kSelect || MODE == kThreeWay) && sizeof(U) >= 4) {
+        // s_stage is free until the staging below (after block_words' barriers); each wave uses its own
+        // 64 x ITEMS items of it.
+        if (seg + static_cast<uint64_t>(kWave) * ITEMS <= a.n && (reinterpret_cast<uintptr_t>(a.in) & 15u) == 0) {
+            U* wst = reinterpret_cast<U*>(s_stage) + static_cast<uint64_t>(wave) * kWave * ITEMS;
+            vector_load_items<U, ITEMS>(a.in, seg, wst, t.x);
+            load_lane<U, P, V, MODE, FLAGS, ITEMS, true>(a, seg, t);
+            vector_loaded = true;
+        }
+    }
+    if (!vector_loaded) load_lane<U, P, V, MODE, FLAGS, ITEMS>(a, seg, t);
     uint32_t words[W], wp[W], agg[W];
     wave_words<MODE>(t, seg, words);
     block_words<MODE>(words, s_wave, wp, agg);

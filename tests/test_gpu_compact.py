@@ -46,9 +46,15 @@ def clauses_for(ts):
 
 
 # ---- GPU calls (outputs pre-filled with a poison pattern) -------------------------------------------
-def g_select_if(hip, x, clauses, partition=False, in_place=False):
+def dev_at(x, offset_items):
+    """x on the device, starting `offset_items` items into its allocation (a view off the 16-byte
+    alignment of a fresh tensor when offset_items * itemsize is not a multiple of 16)."""
+    return to_dev(np.concatenate([np.zeros(offset_items, x.dtype), x]))[offset_items:] if offset_items else to_dev(x)
+
+
+def g_select_if(hip, x, clauses, partition=False, in_place=False, offset_items=0):
     ts, n = SUFFIX[x.dtype], x.size
-    d_in = to_dev(x)
+    d_in = dev_at(x, offset_items)
     d_out = d_in if in_place else fill_dev(n, x.itemsize, 0x5A)
     num = fill_dev(1, 4, 99)
     pred = hip.predicate(ts, *clauses)
@@ -71,9 +77,9 @@ def g_select_flagged(hip, x, flags, partition=False, in_place=False, clauses=Non
     return to_host(d_out, x.dtype, n), int(to_host(num, np.uint32, 1)[0])
 
 
-def g_three_way(hip, x, c1, c2):
+def g_three_way(hip, x, c1, c2, offset_items=0):
     ts, n = SUFFIX[x.dtype], x.size
-    d_in = to_dev(x)
+    d_in = dev_at(x, offset_items)
     o1, o2, o3 = (fill_dev(n, x.itemsize, 0x5A) for _ in range(3))
     num = fill_dev(2, 4, 99)
     hip.partition_three_way(ts, d_in, o1, o2, o3, num, n, hip.predicate(ts, *c1), hip.predicate(ts, *c2))
@@ -460,6 +466,28 @@ def test_misaligned_views(hip, orc, dev, which):
     num = fill_dev(1, 4, 99)
     hip.partition_flagged("u32", "b8", d_in, d_f, d_out, num, n)
     check_select(orc, x, flags, to_host(d_out, np.uint32, n), int(to_host(num, np.uint32, 1)[0]), True)
+
+
+@pytest.mark.parametrize("ts", ["u32", "i64", "f32"])
+@pytest.mark.parametrize("offset_items", [0, 1])
+def test_vector_loads_and_unaligned_inputs(hip, orc, dev, ts, offset_items):
+    """Select-if, partition-if and the three-way partition read a wave's items as 16-byte vectors when the
+    input is 16-byte aligned and the wave's items all exist; an input one item off that alignment, and the
+    last, partial waves, take one load per item.  Both bit-exact."""
+    rng = np.random.default_rng(311 + offset_items + len(ts))
+    n = 5 * T4 + 37
+    x = items_for(rng, n, ts)
+    cl = clauses_for(ts)
+    sel = orc.predicate(x, cl)
+    for partition in (False, True):
+        got, k = g_select_if(hip, x, cl, partition=partition, offset_items=offset_items)
+        check_select(orc, x, sel, got, k, partition)
+    c2 = [(1, 100, 0)] if ts != "f32" else [(1, 0.0, 0)]  # x < 100 (x < 0.0) as the second category
+    o1, o2, o3, c = g_three_way(hip, x, cl, c2, offset_items=offset_items)
+    w1, w2, w3, wc = orc.partition_three_way(x, sel, orc.predicate(x, c2))
+    assert c == wc
+    assert np.array_equal(o1[:wc[0]], w1[:wc[0]]) and np.array_equal(o2[:wc[1]], w2[:wc[1]])
+    assert np.array_equal(o3[:n - sum(wc)], w3[:n - sum(wc)])
 
 
 def test_large_inputs(hip, orc, dev):
