@@ -156,12 +156,50 @@ __device__ __forceinline__ void write_result(T* out, uint32_t* index_out, uint64
     }
 }
 
-// Lane-strided fold of [b, e) with kSgUnroll loads in flight per lane; `stride` lanes take part.
-template <typename T, int OP>
+// Lane-strided fold of [b, e) with kSgUnroll loads in flight per lane; `stride` lanes take part.  From
+// the first 16-byte boundary on, the lanes read 16-byte vectors, four in flight each (the items before
+// the boundary and after the last whole vector one per lane).  The vector path changes the order of the
+// fold, so it is left out for float Min / Max, where fmin / fmax may pick either zero of -0.0 and +0.0
+// by operand order; sums of floats are held to a tolerance, and the other operators select.  VECTOR
+// false: the item loads only (short ranges: the vector path's set-up measured 6-20 % slower on 37-item
+// segments).
+template <typename T, int OP, bool VECTOR = true>
 __device__ __forceinline__ typename Reducer<T, OP>::Acc fold_range(const T* __restrict__ in, uint64_t b, uint64_t e,
                                                                    uint32_t lane, uint32_t stride) {
     using R = Reducer<T, OP>;
     typename R::Acc acc = R::identity();
+    constexpr bool kVector =
+        VECTOR && sizeof(T) >= 4 && !(std::is_floating_point_v<T> && (OP == kOpMin || OP == kOpMax));
+    if constexpr (kVector) {
+        constexpr int VEC = 16 / static_cast<int>(sizeof(T));
+        const uint64_t a0 = b + ((16u - (reinterpret_cast<uintptr_t>(in + b) & 15u)) & 15u) / sizeof(T);
+        if (a0 + static_cast<uint64_t>(VEC) * stride <= e && (reinterpret_cast<uintptr_t>(in) % sizeof(T)) == 0) {
+            using Vec = T __attribute__((ext_vector_type(VEC)));
+            if (b + lane < a0) acc = R::lift(in[b + lane], static_cast<uint32_t>(b + lane));  // a0 - b < VEC <= stride
+            const Vec* vin = reinterpret_cast<const Vec*>(in + a0);
+            const uint64_t nvec = (e - a0) / VEC;
+            uint64_t v = lane;
+            for (; v + 3ull * stride < nvec; v += 4ull * stride) {
+                Vec q[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) q[u] = vin[v + static_cast<uint64_t>(u) * stride];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint64_t i0 = a0 + (v + static_cast<uint64_t>(u) * stride) * VEC;
+#pragma unroll
+                    for (int c = 0; c < VEC; ++c) acc = R::combine(acc, R::lift(q[u][c], static_cast<uint32_t>(i0 + c)));
+                }
+            }
+            for (; v < nvec; v += stride) {
+                const Vec q = vin[v];
+#pragma unroll
+                for (int c = 0; c < VEC; ++c) acc = R::combine(acc, R::lift(q[c], static_cast<uint32_t>(a0 + v * VEC + c)));
+            }
+            const uint64_t t = a0 + nvec * VEC + lane;
+            if (t < e) acc = R::combine(acc, R::lift(in[t], static_cast<uint32_t>(t)));  // e - (a0 + nvec VEC) < VEC
+            return acc;
+        }
+    }
     uint64_t i = b + lane;
     for (; i + static_cast<uint64_t>(kSgUnroll - 1) * stride < e; i += static_cast<uint64_t>(kSgUnroll) * stride) {
         T v[kSgUnroll];
@@ -178,6 +216,8 @@ __device__ __forceinline__ typename Reducer<T, OP>::Acc fold_range(const T* __re
 // When workgroups take several segments, segments of at most this many items are reduced by one wave and
 // longer ones by the whole workgroup.
 constexpr uint64_t kSgWaveMax = 1024;
+// A wave reads segments of at least this many items as 16-byte vectors.
+constexpr uint64_t kSgWaveVector = 512;
 // Workgroups of the reduce grid: one per segment up to this many segments, then each workgroup takes
 // every G-th segment, four at a time (one per wave), so that many short segments do not each cost a
 // workgroup dispatch while the grid still fills the GPU.
@@ -236,10 +276,15 @@ __global__ __launch_bounds__(kSgBlock) void segment_reduce_kernel(const T* __res
         if (seg < num_segments) {
             uint64_t b, e;
             bounds(seg, b, e);
+            // The wave's segment bounds are uniform: scalar registers, so its branches are scalar.
+            b = read_lane_any(b, 0);
+            e = read_lane_any(e, 0);
             if (b >= e) {
                 if (lane_id() == 0) write_result<T, OP>(out, index_out, seg, b, true, R::identity());
             } else if (e - b <= kSgWaveMax) {
-                const Acc total = wave_combine<T, OP>(fold_range<T, OP>(in, b, e, lane_id(), kWave));
+                const Acc total = wave_combine<T, OP>(e - b >= kSgWaveVector
+                                                          ? fold_range<T, OP>(in, b, e, lane_id(), kWave)
+                                                          : fold_range<T, OP, false>(in, b, e, lane_id(), kWave));
                 if (lane_id() == 0) write_result<T, OP>(out, index_out, seg, b, false, total);
             } else if (lane_id() == 0) {
                 s_big[atomicAdd(&s_nbig, 1u)] = seg;
