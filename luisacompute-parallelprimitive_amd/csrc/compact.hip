@@ -20,7 +20,8 @@
 //   * One workgroup of 256 threads (4 waves) per tile.  A wave owns 64 x ITEMS consecutive items
 //     (ITEMS = 128 / item bytes: 32 four-byte or 16 eight-byte items per lane), lane l holding items
 //     seg + 64 j + l, so every load instruction of a wave reads consecutive addresses and a tile is
-//     8,192 or 4,096 items.
+//     8,192 or 4,096 items.  Select and partition read a whole wave of an aligned input as 16-byte
+//     vectors and move them to that layout through the wave's part of the staging buffer.
 //   * Selection masks are per-lane bit sets (bit j = item j of the lane).  Ranks come from wave ballots:
 //     row j's selected items take consecutive tile ranks (k + selected lanes below), so they are
 //     staged in LDS at consecutive addresses (no bank conflicts) and the workgroup copies each
