@@ -331,9 +331,10 @@ __device__ __forceinline__ void block_scan_segment(const T* __restrict__ in, T* 
     const bool vec_in = (reinterpret_cast<uintptr_t>(in + b) & 15) == 0;
     const bool vec_out = (reinterpret_cast<uintptr_t>(out + ob) & 15) == 0;
     T carry = use_init ? init : T(0);
-    for (uint64_t c = b; c < e; c += kChunk) {
+    // This thread's run of the chunk at c; the next chunk's run is loaded before the current one is
+    // scanned and stored, so its loads are in flight across the barriers.
+    auto load_run = [&](uint64_t c, T (&v)[kScanItems]) {
         const uint64_t first = c + static_cast<uint64_t>(threadIdx.x) * kScanItems;
-        T v[kScanItems];
         if (vec_in && first + kScanItems <= e) {
             const ScanRun<T> r = *reinterpret_cast<const ScanRun<T>*>(in + first);
 #pragma unroll
@@ -342,6 +343,15 @@ __device__ __forceinline__ void block_scan_segment(const T* __restrict__ in, T* 
 #pragma unroll
             for (int k = 0; k < kScanItems; ++k) v[k] = first + k < e ? in[first + k] : T(0);
         }
+    };
+    T nv[kScanItems];
+    load_run(b, nv);
+    for (uint64_t c = b; c < e; c += kChunk) {
+        const uint64_t first = c + static_cast<uint64_t>(threadIdx.x) * kScanItems;
+        T v[kScanItems];
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) v[k] = nv[k];
+        if (c + kChunk < e) load_run(c + kChunk, nv);
         T own = v[0];
 #pragma unroll
         for (int k = 1; k < kScanItems; ++k) own = add_wrap(own, v[k]);
