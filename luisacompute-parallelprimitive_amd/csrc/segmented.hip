@@ -218,21 +218,31 @@ __device__ __forceinline__ typename Reducer<T, OP>::Acc fold_range(const T* __re
 constexpr uint64_t kSgWaveMax = 1024;
 // A wave reads segments of at least this many items as 16-byte vectors.
 constexpr uint64_t kSgWaveVector = 512;
-// Workgroups of the reduce grid: one per segment up to this many segments, then each workgroup takes
-// every G-th segment, four at a time (one per wave), so that many short segments do not each cost a
-// workgroup dispatch while the grid still fills the GPU.
+// Workgroups of the reduce grid: one per segment up to this many segments; beyond, each wave takes
+// batches of `batch` consecutive segments (workgroup g's waves take batches 4 g .. 4 g + 3 of every round
+// of 4 G), so that many short segments do not each cost a workgroup dispatch while the grid still fills
+// the GPU.  The host sizes the batch to about num_segments / 65,536 (1 to 64): calls with somewhat more
+// than 65,536 segments keep about one segment per wave, calls with millions fill every lane.
 constexpr uint64_t kSgMaxGroups = 65536;
+constexpr uint64_t kSgBatchWaves = 65536;
+// A batch whose segments all hold at most this many items is reduced one segment per lane (coalesced
+// offset loads and result stores); otherwise the wave takes its segments one at a time.  Measured on 2^28
+// i32 Sum, ms per call against one wave per segment: 4-item segments 10.2 -> 0.40, 16: 2.51 -> 0.49,
+// 37: 1.17 -> 0.76, 60: 0.75 -> 0.50, 300: 0.44 -> 0.37; with lanes up to 64 items, 60-item segments
+// took 1.06 ms.
+constexpr uint64_t kSgLaneMax = 16;
 
 template <typename T, int OP>
 __global__ __launch_bounds__(kSgBlock) void segment_reduce_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                                   uint32_t* __restrict__ index_out,
                                                                   const uint32_t* __restrict__ begins,
                                                                   const uint32_t* __restrict__ ends,
-                                                                  uint64_t fixed_size, uint64_t num_segments) {
+                                                                  uint64_t fixed_size, uint64_t num_segments,
+                                                                  uint32_t batch) {
     using R = Reducer<T, OP>;
     using Acc = typename R::Acc;
     __shared__ Acc s_wave[kSgWaves];
-    __shared__ uint64_t s_big[kSgWaves];
+    __shared__ uint64_t s_big[kSgBlock];
     __shared__ uint32_t s_nbig;
     const uint32_t wave = threadIdx.x / kWave;
     const uint64_t groups = gridDim.x;
@@ -266,28 +276,48 @@ __global__ __launch_bounds__(kSgBlock) void segment_reduce_kernel(const T* __res
         block_reduce(blockIdx.x, b, e);
         return;
     }
-    for (uint64_t j = 0;; j += kSgWaves) {
-        // Segments of this round: blockIdx.x + (j + w) * groups for waves w = 0..3.
-        const uint64_t first = blockIdx.x + j * groups;
-        if (first >= num_segments) break;
+    for (uint64_t r = 0;; ++r) {
+        // Batches of this round: 4 (blockIdx.x + r groups) + w for waves w = 0..3, `batch` segments each.
+        const uint64_t batch0 = (blockIdx.x + r * groups) * kSgWaves;
+        if (batch0 * batch >= num_segments) break;
         if (threadIdx.x == 0) s_nbig = 0;
         __syncthreads();
-        const uint64_t seg = blockIdx.x + (j + wave) * groups;
-        if (seg < num_segments) {
-            uint64_t b, e;
-            bounds(seg, b, e);
-            // The wave's segment bounds are uniform: scalar registers, so its branches are scalar.
-            b = read_lane_any(b, 0);
-            e = read_lane_any(e, 0);
-            if (b >= e) {
-                if (lane_id() == 0) write_result<T, OP>(out, index_out, seg, b, true, R::identity());
-            } else if (e - b <= kSgWaveMax) {
-                const Acc total = wave_combine<T, OP>(e - b >= kSgWaveVector
-                                                          ? fold_range<T, OP>(in, b, e, lane_id(), kWave)
-                                                          : fold_range<T, OP, false>(in, b, e, lane_id(), kWave));
-                if (lane_id() == 0) write_result<T, OP>(out, index_out, seg, b, false, total);
-            } else if (lane_id() == 0) {
-                s_big[atomicAdd(&s_nbig, 1u)] = seg;
+        const uint64_t first = (batch0 + wave) * batch;
+        if (first < num_segments) {
+            const uint32_t count = num_segments - first < batch ? static_cast<uint32_t>(num_segments - first) : batch;
+            const uint64_t seg = first + lane_id();
+            uint64_t b = 0, e = 0;
+            if (lane_id() < count) bounds(seg, b, e);
+            const uint64_t len = e > b ? e - b : 0;
+            if (wave_ballot(len > kSgLaneMax) == 0) {
+                // One segment per lane, 8 loads in flight per step.
+                Acc acc = R::identity();
+                for (uint64_t i = b; i < e; i += 8) {
+                    T v[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = i + k < e ? in[i + k] : T(0);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        if (i + k < e) acc = R::combine(acc, R::lift(v[k], static_cast<uint32_t>(i + k)));
+                    }
+                }
+                if (lane_id() < count) write_result<T, OP>(out, index_out, seg, b, b >= e, acc);
+            } else {
+                for (uint32_t k = 0; k < count; ++k) {
+                    // The wave's segment bounds are uniform: scalar registers, so its branches are scalar.
+                    const uint64_t bk = read_lane_any(b, static_cast<int>(k));
+                    const uint64_t ek = read_lane_any(e, static_cast<int>(k));
+                    if (bk >= ek) {
+                        if (lane_id() == 0) write_result<T, OP>(out, index_out, first + k, bk, true, R::identity());
+                    } else if (ek - bk <= kSgWaveMax) {
+                        const Acc total = wave_combine<T, OP>(ek - bk >= kSgWaveVector
+                                                                  ? fold_range<T, OP>(in, bk, ek, lane_id(), kWave)
+                                                                  : fold_range<T, OP, false>(in, bk, ek, lane_id(), kWave));
+                        if (lane_id() == 0) write_result<T, OP>(out, index_out, first + k, bk, false, total);
+                    } else if (lane_id() == 0) {
+                        s_big[atomicAdd(&s_nbig, 1u)] = first + k;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -472,9 +502,16 @@ int segment_reduce(const T* in, T* out, uint32_t* index_out, uint64_t num_segmen
         return set_error(kInvalidArgument, "%s: segments exceed 2^32 items", what);
     if (begins == nullptr && ends != nullptr) return set_error(kInvalidArgument, "%s: bad offsets", what);
     LaunchScope scope("segment_reduce", stream);
-    const uint64_t groups = num_segments < kSgMaxGroups ? num_segments : kSgMaxGroups;
-    segment_reduce_kernel<T, OP><<<checked_grid(groups), kSgBlock, 0, stream>>>(in, out, index_out, begins, ends,
-                                                                               fixed_size, num_segments);
+    // Up to kSgMaxGroups segments one workgroup each; beyond, batches of about num_segments / kSgBatchWaves
+    // segments (1 to 64) per wave and enough workgroups for one round of them, at most kSgMaxGroups.
+    uint64_t batch = num_segments / kSgBatchWaves;
+    batch = batch < 1 ? 1 : (batch > static_cast<uint64_t>(kWave) ? kWave : batch);
+    const uint64_t wave_batches = ceil_div(num_segments, batch);
+    const uint64_t wg_batches = ceil_div(wave_batches, static_cast<uint64_t>(kSgWaves));
+    const uint64_t groups = num_segments <= kSgMaxGroups ? num_segments
+                                                         : (wg_batches < kSgMaxGroups ? wg_batches : kSgMaxGroups);
+    segment_reduce_kernel<T, OP><<<checked_grid(groups), kSgBlock, 0, stream>>>(
+        in, out, index_out, begins, ends, fixed_size, num_segments, static_cast<uint32_t>(batch));
     return check_hip(hipGetLastError(), "segment_reduce launch");
 }
 

@@ -203,6 +203,28 @@ def test_segment_reduce_many_segments_grouped(hip, orc, dev, ts):
         check_reduce(orc, op, x, b, e, got, idx, ts)
 
 
+@pytest.mark.parametrize("ts", ["i32", "f32", "u64"])
+def test_segment_reduce_millions_of_segments(hip, orc, dev, ts):
+    """About 4.2 M segments, so every wave takes batches of 64 consecutive segments: batches of segments of
+    at most 16 items reduced one segment per lane, batches holding a longer one (up to 1,024 items: by the
+    wave; over 1,024: by the workgroup) one segment at a time; empty and reversed segments; all ops."""
+    rng = np.random.default_rng(700 + len(ts))
+    m = (1 << 22) + 77
+    r = rng.random(m)
+    lengths = np.where(r < 0.0005, rng.integers(1025, 3000, m),
+                       np.where(r < 0.003, rng.integers(17, 1025, m), rng.integers(0, 17, m)))
+    b = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.uint32)
+    e = (b.astype(np.int64) + lengths).astype(np.uint32)
+    n = int(e[-1])
+    x = values_for(rng, n, ts)
+    e[7::5000] = b[7::5000] // 2  # begin > end: empty
+    ops = ["sum", "min", "argmax"] if ts in ("i32", "f32") else ["sum", "max"]
+    log(f"segment reduce {m} segments {ts}")
+    for op in ops:
+        got, idx = g_reduce(hip, op, x, b, e)
+        check_reduce(orc, op, x, b, e, got, idx, ts)
+
+
 @pytest.mark.parametrize("ts", ["i32", "u64", "f64"])
 def test_segmented_scan_many_segments_grouped(hip, orc, dev, ts):
     """More than 65,536 segments: short segments scanned by one wave, some longer than 1,024 items by the
