@@ -438,18 +438,20 @@ __device__ __forceinline__ void wave_scan_segment(const T* __restrict__ in, T* _
     }
 }
 
-// Up to 65,536 segments: one workgroup per segment.  Above that the grid stays at 65,536 workgroups and
-// each takes every 65,536th segment, four at a time: a wave scans a segment of at most 1,024 items alone,
-// the workgroup scans longer ones together (one workgroup per segment is bound by dispatch).
+// Up to 65,536 segments: one workgroup per segment.  Above that, each wave takes batches of `batch`
+// consecutive segments like the reduce: a batch whose segments all hold at most kSgLaneMax items is
+// scanned one segment per lane; any other batch one segment at a time, a wave scanning a segment of at
+// most 1,024 items alone and the workgroup longer ones together (one workgroup per segment is bound by
+// dispatch).
 template <typename T>
 __global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                                   const uint32_t* __restrict__ begins,
                                                                   const uint32_t* __restrict__ ends,
                                                                   const uint32_t* __restrict__ out_begins,
                                                                   int inclusive, int use_init, T init,
-                                                                  uint64_t num_segments) {
+                                                                  uint64_t num_segments, uint32_t batch) {
     __shared__ T s_wave[kSgWaves];
-    __shared__ uint64_t s_big[kSgWaves];
+    __shared__ uint64_t s_big[kSgBlock];
     __shared__ uint32_t s_nbig;
     const uint64_t groups = gridDim.x;
     if (num_segments <= groups) {
@@ -460,16 +462,50 @@ __global__ __launch_bounds__(kSgBlock) void segmented_scan_kernel(const T* __res
         return;
     }
     const uint32_t wave = threadIdx.x / kWave;
-    for (uint64_t j = 0;; j += kSgWaves) {
-        if (blockIdx.x + j * groups >= num_segments) break;
+    for (uint64_t r = 0;; ++r) {
+        const uint64_t batch0 = (blockIdx.x + r * groups) * kSgWaves;
+        if (batch0 * batch >= num_segments) break;
         if (threadIdx.x == 0) s_nbig = 0;
         __syncthreads();
-        const uint64_t seg = blockIdx.x + (j + wave) * groups;
-        if (seg < num_segments) {
-            const uint64_t b = begins[seg], e = ends[seg];
-            if (b < e) {
-                if (e - b <= kSgWaveMax) wave_scan_segment(in, out, b, e, out_begins[seg], inclusive, use_init, init);
-                else if (lane_id() == 0) s_big[atomicAdd(&s_nbig, 1u)] = seg;
+        const uint64_t first = (batch0 + wave) * batch;
+        if (first < num_segments) {
+            const uint32_t count = num_segments - first < batch ? static_cast<uint32_t>(num_segments - first) : batch;
+            const uint64_t seg = first + lane_id();
+            uint64_t b = 0, e = 0, ob = 0;
+            if (lane_id() < count) {
+                b = begins[seg];
+                e = ends[seg];
+                ob = out_begins[seg];
+            }
+            const uint64_t len = e > b ? e - b : 0;
+            if (wave_ballot(len > kSgLaneMax) == 0) {
+                // One segment per lane, 8 loads in flight per step.
+                T run = use_init ? init : T(0);
+                for (uint64_t i = b; i < e; i += 8) {
+                    T v[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[k] = i + k < e ? in[i + k] : T(0);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        if (i + k < e) {
+                            const T next = add_wrap(run, v[k]);
+                            out[ob + (i + k - b)] = inclusive ? next : run;
+                            run = next;
+                        }
+                    }
+                }
+            } else {
+                for (uint32_t k = 0; k < count; ++k) {
+                    const uint64_t bk = read_lane_any(b, static_cast<int>(k));
+                    const uint64_t ek = read_lane_any(e, static_cast<int>(k));
+                    if (bk < ek) {
+                        if (ek - bk <= kSgWaveMax)
+                            wave_scan_segment(in, out, bk, ek, read_lane_any(ob, static_cast<int>(k)), inclusive,
+                                              use_init, init);
+                        else if (lane_id() == 0)
+                            s_big[atomicAdd(&s_nbig, 1u)] = first + k;
+                    }
+                }
             }
         }
         __syncthreads();
@@ -524,9 +560,15 @@ int segmented_scan(const T* in, T* out, const uint32_t* begins, const uint32_t* 
     if (num_segments > 0x7FFFFFFFull) return set_error(kInvalidArgument, "%s: too many segments", what);
     if (!in || !out || !begins || !ends) return set_error(kInvalidArgument, "%s: null input or output", what);
     LaunchScope scope("segmented_scan", stream);
-    const uint64_t groups = num_segments < kSgMaxGroups ? num_segments : kSgMaxGroups;
+    // Batches as for the reduce (segment_reduce above).
+    uint64_t batch = num_segments / kSgBatchWaves;
+    batch = batch < 1 ? 1 : (batch > static_cast<uint64_t>(kWave) ? kWave : batch);
+    const uint64_t wg_batches = ceil_div(ceil_div(num_segments, batch), static_cast<uint64_t>(kSgWaves));
+    const uint64_t groups = num_segments <= kSgMaxGroups ? num_segments
+                                                         : (wg_batches < kSgMaxGroups ? wg_batches : kSgMaxGroups);
     segmented_scan_kernel<T><<<checked_grid(groups), kSgBlock, 0, stream>>>(
-        in, out, begins, ends, out_begins ? out_begins : begins, inclusive, use_init, init, num_segments);
+        in, out, begins, ends, out_begins ? out_begins : begins, inclusive, use_init, init, num_segments,
+        static_cast<uint32_t>(batch));
     return check_hip(hipGetLastError(), "segmented_scan launch");
 }
 

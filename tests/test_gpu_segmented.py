@@ -225,6 +225,31 @@ def test_segment_reduce_millions_of_segments(hip, orc, dev, ts):
         check_reduce(orc, op, x, b, e, got, idx, ts)
 
 
+@pytest.mark.parametrize("ts", ["i32", "f64"])
+def test_segmented_scan_millions_of_segments(hip, orc, dev, ts):
+    """About 2.1 M segments in batches of 32 per wave: batches of segments of at most 16 items scanned one
+    segment per lane, other batches one segment at a time (by the wave, or the workgroup beyond 1,024
+    items); empty and reversed segments; exclusive with an initial value, and inclusive."""
+    rng = np.random.default_rng(800 + len(ts))
+    m = (1 << 21) + 33
+    r = rng.random(m)
+    lengths = np.where(r < 0.0005, rng.integers(1025, 2500, m),
+                       np.where(r < 0.003, rng.integers(17, 1025, m), rng.integers(0, 17, m)))
+    b = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.uint32)
+    e = (b.astype(np.int64) + lengths).astype(np.uint32)
+    n = int(e[-1])
+    x = values_for(rng, n, ts)
+    e[9::4000] = b[9::4000] // 2  # begin > end: empty
+    log(f"segmented scan {m} segments {ts}")
+    for kw in ({"init": 5}, {"inclusive": True}):
+        got = g_scan(hip, x, b, e, ob=b.copy(), out_size=n, **kw)
+        want, ab = orc.segmented_scan(x, b, e, out_begins=b.copy(), out_size=n, **kw)
+        if ts in REL:
+            assert np.all(np.abs(got.astype(np.float64) - want.astype(np.float64)) <= REL[ts] * ab + 1e-30), kw
+        else:
+            np.testing.assert_array_equal(got, want)
+
+
 @pytest.mark.parametrize("ts", ["i32", "u64", "f64"])
 def test_segmented_scan_many_segments_grouped(hip, orc, dev, ts):
     """More than 65,536 segments: short segments scanned by one wave, some longer than 1,024 items by the
