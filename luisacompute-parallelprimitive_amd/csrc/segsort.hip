@@ -13,9 +13,9 @@
 //
 // MI355X design:
 //   * Block phase: chunks sorted in LDS by one 256-thread workgroup each, C = 4,096 items in radix
-//     order and 2,048 in value order.  Small segments (<= 512 items) are sorted together per
-//     2,048-item tile of the item range (a joint merge sort with position labels when a tile holds more
-//     than two), medium ones (<= C) by one workgroup each, and long ones chunk by chunk by a grid-stride
+//     order and 2,048 in value order.  Tiny segments (<= 16 items) are sorted by one thread each, in
+//     registers; small ones (<= 512 items) together per 2,048-item tile of the item range (a joint sort
+//     with position labels when a tile holds more than two), medium ones (<= C) by one workgroup each, and long ones chunk by chunk by a grid-stride
 //     kernel over C-item tiles, so neither many tiny segments nor a few long ones leave the GPU idle.
 //   * Radix order, medium segments and chunks: a stable LSD radix sort in LDS, 8-bit digits, 4, 8 or
 //     16 items per thread by length; per pass a ballot match ranks each wave's items against per-wave
@@ -391,6 +391,47 @@ __device__ __forceinline__ void sort_any_chunk(const K* keys_in, K* kdst, const 
         radix_sort_chunk<K, V, PAIRS, KIND, 16>(keys_in, kdst, values_in, vdst, c, len, o, s_k, s_v, s_cnt, s_tot);
 }
 
+// Segments of at most this many items are sorted by one thread each, in registers, when the block
+// kernel reads their offsets (the tile kernel leaves them alone).
+constexpr uint32_t kSsTiny = 16;
+
+// Stable odd-even transposition sort of [b, b + len) (len <= kSsTiny) by one thread, into the outputs.
+template <typename K, typename V, bool PAIRS, int KIND>
+__device__ __forceinline__ void sort_tiny(const K* keys_in, K* keys_out, const V* values_in, V* values_out, uint64_t b,
+                                          uint32_t len, const SortOrder& o) {
+    K k[kSsTiny];
+    V v[PAIRS ? kSsTiny : 1];
+#pragma unroll
+    for (int j = 0; j < static_cast<int>(kSsTiny); ++j) {
+        const bool ok = static_cast<uint32_t>(j) < len;
+        k[j] = ok ? keys_in[b + j] : K(0);
+        if constexpr (PAIRS) v[j] = ok ? values_in[b + j] : V(0);
+    }
+#pragma unroll
+    for (int round = 0; round < static_cast<int>(kSsTiny); ++round) {
+#pragma unroll
+        for (int j = round & 1; j + 1 < static_cast<int>(kSsTiny); j += 2) {
+            if (static_cast<uint32_t>(j + 1) < len && before<K, KIND>(k[j + 1], k[j], o)) {
+                const K tk = k[j];
+                k[j] = k[j + 1];
+                k[j + 1] = tk;
+                if constexpr (PAIRS) {
+                    const V tv = v[j];
+                    v[j] = v[j + 1];
+                    v[j + 1] = tv;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < static_cast<int>(kSsTiny); ++j) {
+        if (static_cast<uint32_t>(j) < len) {
+            keys_out[b + j] = k[j];
+            if constexpr (PAIRS) values_out[b + j] = v[j];
+        }
+    }
+}
+
 // Segment of item i (begins ascending): the last segment whose begin <= i, or -1.
 __device__ __forceinline__ int64_t find_segment(const uint32_t* begins, uint32_t num_segments, uint64_t i) {
     uint32_t lo = 0, hi = num_segments;
@@ -427,7 +468,9 @@ __device__ __forceinline__ uint64_t wave_search(uint64_t lo, uint64_t hi, Pred p
 // Medium segments (kSsSmall < items <= chunk_items(o)): one workgroup sorts each.  Workgroup g takes segment
 // indices [g * per_group, (g + 1) * per_group), one per thread at a time, so that many small segments
 // cost a read of their offsets rather than a workgroup each; per_group is 1 whenever segments average
-// more than kSsSmall items.  The kernel also sets words[1] when a small segment exists and posts the
+// more than kSsSmall items.  The thread that reads a tiny segment's offsets (at most kSsTiny items) sorts
+// it at once (sort_tiny).  The kernel also sets words[1] when a small segment (more than kSsTiny, at most
+// kSsSmall items) exists and posts the
 // longest segment above a chunk to words[0] (a relaxed load first: same-address atomics serialise at
 // ~11 ns each).
 template <typename K, typename V, bool PAIRS, int KIND>
@@ -453,7 +496,10 @@ __global__ __launch_bounds__(kSsBlock) void segsort_block_kernel(const K* keys_i
             const uint64_t b = begins[x], e = ends[x];
             if (b < e && e <= n) {
                 const uint64_t len = e - b;
-                if (len <= kSsSmall) s_small = 1;  // benign race: every writer stores 1
+                if (len <= kSsTiny)
+                    sort_tiny<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b,
+                                                 static_cast<uint32_t>(len), o);
+                else if (len <= kSsSmall) s_small = 1;  // benign race: every writer stores 1
                 else if (len <= chunk) s_medium[atomicAdd(&s_count, 1u)] = static_cast<uint32_t>(x);
                 else atomicMax(&s_long, static_cast<uint32_t>(len));
             }
@@ -572,7 +618,7 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
         const uint64_t first = c0 > 0 ? c0 - 1 : 0;
         for (uint64_t x = first + tid; x < c1; x += kSsBlock) {
             const uint64_t b = begins[x], e = ends[x];
-            if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall) continue;
+            if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall || e - b <= kSsTiny) continue;
             const uint32_t slot = atomicAdd(&s_inside, 1u);
             if (slot < 2) {
                 s_pick[slot][0] = static_cast<uint32_t>(b - t0);
@@ -592,7 +638,7 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
             __syncthreads();
             for (uint64_t x = first + tid; x < c1; x += kSsBlock) {
                 const uint64_t b = begins[x], e = ends[x];
-                if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall) continue;
+                if (b >= e || e > n || b < t0 || e > t1 || e - b > kSsSmall || e - b <= kSsTiny) continue;
                 atomicAdd(&s_count[b - t0], 1u);
                 if (e < t1) atomicAdd(&s_count[e - t0], 1u << 16);
             }
@@ -647,7 +693,7 @@ __global__ __launch_bounds__(kSsBlock) void segsort_tile_kernel(const K* keys_in
         // A small segment that starts in the tile and ends after it holds the tile's last item.
         if (c1 > 0) {
             const uint64_t b = begins[c1 - 1], e = ends[c1 - 1];
-            if (b < e && e <= n && e - b <= kSsSmall && b >= t0 && e > t1)
+            if (b < e && e <= n && e - b <= kSsSmall && e - b > kSsTiny && b >= t0 && e > t1)
                 sort_any_chunk<K, V, PAIRS, KIND>(keys_in, keys_out, values_in, values_out, b,
                                                   static_cast<uint32_t>(e - b), o, s_lds, s_tot);
         }
