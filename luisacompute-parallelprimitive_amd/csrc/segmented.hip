@@ -12,13 +12,16 @@
 // output[out_begin[s] + k]; exclusive scans start from the initial value (0 for the Sum forms).
 //
 // MI355X design: one 256-thread workgroup per segment, up to 65,536 segments.  Reductions stream the
-// segment with eight loads in flight per thread (consecutive lanes read consecutive items), fold in
-// registers, then a wave shuffle reduction and a 4-wave combine in LDS.  With more segments the reduce
-// grid stays at 65,536 workgroups and each takes every 65,536th segment, four at a time: a wave reduces
-// a segment of at most 1,024 items alone, the workgroup reduces longer ones together (workgroup dispatch
-// bounds one-workgroup-per-segment grids: 2^24 items in 4-item segments 2.51 -> 0.61 ms); scans are
-// grouped the same way, a wave scanning a short segment 64 items per step.  Workgroup scans walk the segment in chunks of 2048
-// items: each thread folds 8 consecutive items (16-byte accesses when the segment start is aligned),
+// segment with eight loads in flight per thread (consecutive lanes read consecutive items; four 16-byte
+// vectors per lane for ranges of at least 512 items), fold in registers, then a DPP wave reduction and a
+// 4-wave combine in LDS.  With more segments each wave
+// takes batches of consecutive segments (about num_segments / 65,536 of them, 1 to 64): a batch whose
+// segments all hold at most 16 items is reduced or scanned one segment per lane, with coalesced offset
+// loads; any other batch one segment at a time, a wave taking a segment of at most 1,024 items alone and
+// the workgroup longer ones together (workgroup dispatch bounds one-workgroup-per-segment grids).
+// Workgroup scans walk the segment in chunks of 2048 items (the next chunk's loads issued before the
+// current one is scanned): each thread folds 8 consecutive items (16-byte accesses when the segment
+// start is aligned),
 // a DPP wave scan and the LDS wave totals give every thread its chunk prefix, and a running carry
 // crosses chunks.  Segments with begin >= end are empty.  Integer sums wrap; float sums are ordered
 // (per-thread folds, then a fixed tree).
