@@ -101,7 +101,8 @@ def test_benchmark_input_2p24(hip, orc, dev):
     assert to_host(out, np.int32, 1)[0] == wrapped
 
 
-def test_north_star_size_2p28(hip, orc, dev):
+def test_sum_2p28_i32(hip, orc, dev):
+    """Sum of 2^28 int32 values in [-1000, 1000], bit-exact against the oracle."""
     n = 1 << 28
     log("reduce 2^28")
     d = torch.empty(n, dtype=torch.int32, device=dev)
