@@ -554,7 +554,7 @@ def main() -> int:
                     help="only run a plain MIB-MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only",
+        print(json.dumps({"error": "this library runs on one GPU; sharding across GPUs is design-only",
                           "n_gpus": args.gpus}))
         return 2
     if args.copy_calibration:

@@ -2,7 +2,8 @@
  * CPU oracle for the LCPP device hot path — TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library, and only
- * as the checker (or the timed CPU baseline).  The product (liblcpp_hip.so) never calls it.
+ * as the reference results the GPU results are compared with (or the timed CPU baseline).  The product
+ * (liblcpp_hip.so) never calls it.
  *
  * The reference (LuisaCompute-ParallelPrimitive) cannot be built here: every header includes
  * LuisaCompute (src/lcpp/runtime/core.h:10-13), which is fetched from the network at configure time

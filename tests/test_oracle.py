@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the GPU tests compare their results with it.
 
 Each oracle function is checked against (a) the known-answer cases of the reference's own tests
 (paths relative to the LCPP root), (b) closed forms, and (c) an independent algorithm (numpy / Python
