@@ -297,6 +297,13 @@ def radix_sort(keys: np.ndarray, values: np.ndarray | None = None, begin_bit: in
     return (ko, vo) if values is not None else ko
 
 
+def twiddle_in(key: int, dtype, descending: bool = False) -> int:
+    """The ordered unsigned image of a key's bits (oracle.c: signed XOR high bit, floats by sign,
+    descending inverts)."""
+    kb, kind = KEY_KINDS[np.dtype(dtype)]
+    return int(lib().oracle_twiddle_in(key, kb, kind, int(descending)))
+
+
 def radix_digit(key: int, dtype, descending: bool, shift: int, bits: int) -> int:
     kb, kind = KEY_KINDS[np.dtype(dtype)]
     return int(lib().oracle_radix_digit(key, kb, kind, int(descending), shift, bits))

@@ -5,7 +5,11 @@ Each oracle function is checked against (a) the known-answer cases of the refere
 comparison sorts), chosen so that a dropped term, a wrong sign or index, or a wrong twiddle fails.
 """
 import math
+import os
+import shutil
 import struct
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -67,6 +71,28 @@ def test_reduce_closed_form_random(orc):
     assert math.isclose(absum, math.fsum(np.abs(f.astype(np.float64))), rel_tol=1e-12)
 
 
+def test_reduce_sum_f64_closed_forms(orc):
+    """The double branch (oracle_reduce_sum_f64).  Integers below 2^63 add exactly in long double, so the
+    result is the int64 sum rounded once to double (a double accumulator would round along the way);
+    the reference's exact binary fractions (i % 7 + 1) * 0.25 (tests/scan_optimization_regression_test.cpp:49-61)
+    give 0.25 * the integer sum; random doubles agree with math.fsum (correctly rounded) to the long
+    double's error bound."""
+    rng = np.random.default_rng(21)
+    a = rng.integers(-2**40, 2**40, 100000)
+    s, absum = orc.reduce_sum_fp(a.astype(np.float64))
+    assert s == float(int(a.sum()))
+    assert absum == float(int(np.abs(a).sum()))
+    big = np.array([2.0**53, 1.0, 1.0, -2.0**53], np.float64)  # a double accumulator loses both ones
+    assert orc.reduce_sum_fp(big)[0] == 2.0
+    q = np.arange(262147) % 7 + 1
+    assert orc.reduce_sum_fp(q * 0.25)[0] == 0.25 * int(q.sum())
+    r = rng.standard_normal(20000) * 1e3
+    s, absum = orc.reduce_sum_fp(r)
+    assert abs(s - math.fsum(r)) <= 1e-15 * absum
+    assert math.isclose(absum, math.fsum(np.abs(r)), rel_tol=1e-15)
+    assert orc.reduce_sum_fp(np.zeros(0, np.float64)) == (0.0, 0.0)
+
+
 # ---- scan ----------------------------------------------------------------------------------------
 @pytest.mark.parametrize("i", [0, 1, 5, 12, 17])
 def test_scan_ones_known_answer(orc, i):
@@ -75,6 +101,30 @@ def test_scan_ones_known_answer(orc, i):
     ones = np.ones(n, np.uint32)
     assert np.array_equal(orc.scan_sum_u32(ones), np.arange(n, dtype=np.uint32))
     assert np.array_equal(orc.scan_sum_u32(ones, inclusive=True), np.arange(1, n + 1, dtype=np.uint32))
+
+
+def test_scan_sum_f32_exact_fractions(orc):
+    """oracle_scan_sum_f32 (double accumulation of float items).  Ones give iota; the reference's exact
+    binary fractions (i % 7 + 1) * 0.25 over 262,147 items (tests/scan_optimization_regression_test.cpp:49-61,
+    116-193) sum exactly, so each output is 0.25 * the int64 prefix sum plus init; inclusive outputs are the
+    exclusive ones shifted by one item; the running magnitudes start at |init| and add |x|."""
+    n = 262147
+    ones = np.ones(n, np.float32)
+    assert np.array_equal(orc.scan_sum_f32(ones)[0], np.arange(n, dtype=np.float64))
+    assert np.array_equal(orc.scan_sum_f32(ones, inclusive=True)[0], np.arange(1, n + 1, dtype=np.float64))
+    q = np.arange(n) % 7 + 1
+    sign = np.where(np.arange(n) % 3 == 1, -1, 1)
+    a = (sign * q * 0.25).astype(np.float32)
+    c = np.cumsum(sign * q)
+    cabs = np.cumsum(q)
+    for init in (0.0, 3.0, -2.0):
+        ex, exa = orc.scan_sum_f32(a, init=init)
+        assert np.array_equal(ex, np.r_[0, c[:-1]] * 0.25 + init)
+        assert np.array_equal(exa, np.r_[0, cabs[:-1]] * 0.25 + abs(init))
+        inc, inca = orc.scan_sum_f32(a, inclusive=True, init=init)
+        assert np.array_equal(inc, c * 0.25 + init)
+        assert np.array_equal(inca, cabs * 0.25 + abs(init))
+    assert orc.scan_sum_f32(np.zeros(0, np.float32))[0].size == 0
 
 
 def test_scan_inclusive_init_known_answer(orc):
@@ -261,6 +311,58 @@ def test_spmv_invalid_rows_and_columns(orc):
     assert zero.tolist() == [0, 0, 0, 0]
 
 
+def test_spmv_f64_vs_fsum_row_loop(orc):
+    """The double branch of oracle_spmv_csr_fp.  The reference's 4x5 case (tests/device_spmv_test.cpp:110-155)
+    with values float32 cannot hold (a float read would be off by ~1e-8), then a random matrix with empty
+    rows and out-of-range columns against a math.fsum row loop over the double products."""
+    ro = np.array([0, 3, 3, 6, 8], np.uint32)
+    ci = np.array([0, 2, 4, 1, 2, 3, 0, 4], np.uint32)
+    va = np.array([1.1, -2.0, 0.3, 3.0, 1.7, -0.5, 2.0, 4.0], np.float64)
+    x = np.array([2.0, -1.0, 0.1, 3.0, -2.0], np.float64)
+    y, ay = orc.spmv_csr_fp(va, ro, ci, x, 4, 5, 8)
+    want = [math.fsum([1.1 * 2.0, -2.0 * 0.1, 0.3 * -2.0]), 0.0, math.fsum([-3.0, 1.7 * 0.1, -1.5]), 4.0 - 8.0]
+    assert np.all(np.abs(y - want) <= 1e-15 * ay)
+    assert ay[1] == 0.0 and ay[3] == 12.0
+    rng = np.random.default_rng(13)
+    rows, cols = 3000, 2500
+    lengths = rng.integers(0, 60, rows)
+    lengths[::41] = 0
+    ro = np.concatenate([[0], np.cumsum(lengths)]).astype(np.uint32)
+    nnz = int(ro[-1])
+    ci = rng.integers(0, cols + 20, nnz).astype(np.uint32)  # some columns out of range: skipped
+    va = rng.standard_normal(nnz)
+    x = rng.standard_normal(cols)
+    y, ay = orc.spmv_csr_fp(va, ro, ci, x, rows, cols, nnz)
+    for r in range(rows):
+        terms = [va[j] * x[ci[j]] for j in range(ro[r], ro[r + 1]) if ci[j] < cols]
+        assert abs(y[r] - math.fsum(terms)) <= 1e-15 * ay[r] + 1e-300, r
+        assert math.isclose(ay[r], math.fsum(np.abs(terms)), rel_tol=1e-15, abs_tol=1e-300), r
+
+
+def test_twiddle_in_known_values_and_order(orc):
+    """oracle_twiddle_in (common/util_type.h:97-175): unsigned keys keep their bits, signed keys flip the
+    high bit, floats flip the high bit when positive and every bit when negative, descending inverts the
+    image.  The unsigned order of the images is the keys' numeric order."""
+    assert orc.twiddle_in(0x12345678, np.uint32) == 0x12345678
+    assert orc.twiddle_in(0x12345678, np.uint32, True) == 0xEDCBA987
+    assert orc.twiddle_in(0x80000000, np.int32) == 0 and orc.twiddle_in(0xFFFFFFFF, np.int32) == 0x7FFFFFFF
+    assert orc.twiddle_in(0x3F800000, np.float32) == 0xBF800000  # +1.0
+    assert orc.twiddle_in(0xBF800000, np.float32) == 0x407FFFFF  # -1.0
+    assert orc.twiddle_in(1 << 63, np.int64) == 0
+    assert orc.twiddle_in(1 << 63, np.float64) == (1 << 63) - 1  # -0.0 sits just below +0.0's 1 << 63
+    assert orc.twiddle_in(0, np.float64, True) == (1 << 63) - 1
+    rng = np.random.default_rng(17)
+    f = (rng.standard_normal(3000) * 10.0 ** rng.integers(-30, 30, 3000)).astype(np.float32)
+    f[:4] = [np.inf, -np.inf, 0.0, 3.0e38]
+    img = np.array([orc.twiddle_in(int(b), np.float32) for b in f.view(np.uint32)], np.uint64)
+    assert np.all(np.diff(f[np.argsort(img, kind="stable")]) >= 0)
+    s = rng.integers(-2**63, 2**63 - 1, 3000, dtype=np.int64)
+    img = np.array([orc.twiddle_in(int(b), np.int64) for b in s.view(np.uint64)], np.uint64)
+    assert np.array_equal(np.argsort(img, kind="stable"), np.argsort(s, kind="stable"))
+    imgd = np.array([orc.twiddle_in(int(b), np.int64, True) for b in s.view(np.uint64)], np.uint64)
+    assert np.array_equal(imgd, ~img)
+
+
 def test_scan_u64_ones_and_wrap(orc):
     # Exclusive sums of ones are iota; full-range 64-bit words wrap like numpy's uint64 cumsum.
     ones = np.ones(1000, np.uint64)
@@ -345,13 +447,18 @@ def test_scan_minmax_signed_zero_keeps_earlier(orc):
     assert np.signbit(orc.scan_minmax("min", a, init=-0.0)).tolist() == [True] * 4
 
 
-@pytest.mark.parametrize("vdt", [np.int32, np.uint64, np.float32, np.float64])
-def test_minmax_by_key_vs_numpy(orc, vdt):
+@pytest.mark.parametrize("kdt", [np.int32, np.uint64])
+@pytest.mark.parametrize("vdt", [np.int32, np.uint32, np.int64, np.uint64, np.float32, np.float64])
+def test_minmax_by_key_vs_numpy(orc, kdt, vdt):
     """Per run (split at the heads): np.minimum / maximum.accumulate (integers), np.fmin / fmax.accumulate
-    (floats with NaNs) for the scans, with the initial value put in front; reduceat for the reduce."""
+    (floats with NaNs) for the scans, with the initial value put in front; reduceat for the reduce.  Every
+    value type is covered, since each has its own identity (the type's max / lowest, NaN for floats) that
+    opens a run without init.  The 8-byte keys differ only above bit 32, so reading them as 4-byte words
+    would merge every run."""
     rng = np.random.default_rng(8)
     n = 3000
-    keys = np.repeat(np.arange(400), rng.integers(1, 14, 400))[:n].astype(np.int32)
+    ids = np.repeat(np.arange(400), rng.integers(1, 14, 400))[:n]
+    keys = ids.astype(np.int32) if kdt is np.int32 else (ids.astype(np.uint64) << np.uint64(33)) | np.uint64(5)
     n = keys.size
     if np.dtype(vdt).kind == "f":
         vals = rng.integers(-50, 50, n).astype(vdt)
@@ -927,3 +1034,44 @@ def test_par_spmv_matches_row_loop(orc, threads):
     assert np.array_equal(y, ref)
     exact, absum = orc.spmv_csr_fp(av, ro, ci, xv, rows, cols, nnz)
     assert np.all(np.abs(y.astype(np.float64) - exact) <= 1e-5 * np.maximum(np.abs(exact), absum))
+
+
+# ---- every exported oracle function is exercised by the tests above --------------------------------
+_CALLED: set[str] = set()
+
+
+class _CallRecorder:
+    """Stands in for the oracle's ctypes handle and records the name of every function looked up."""
+
+    def __init__(self, handle):
+        self._handle = handle
+
+    def __getattr__(self, name):
+        _CALLED.add(name)
+        return getattr(self._handle, name)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _record_oracle_calls(orc):
+    real = orc.lib()
+    orc._lib = _CallRecorder(real)
+    yield
+    orc._lib = real
+
+
+def test_zz_every_exported_oracle_function_is_exercised(orc, request):
+    """Each `oracle_*` symbol the library exports must have been called by a test of this module, each of
+    which compares it with an independent result.  Runs only when the whole module ran in this process."""
+    this = sys.modules[__name__]
+    names = {n for n in dir(this) if n.startswith("test_") and n != request.function.__name__}
+    ran = {item.originalname for item in request.session.items if getattr(item, "module", None) is this}
+    if not names <= ran or os.environ.get("PYTEST_XDIST_WORKER"):
+        pytest.skip("needs every test of this module in one process")
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm (binutils) not found")
+    out = subprocess.run([nm, "-D", "--defined-only", str(orc.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {f[-1] for f in (line.split() for line in out.splitlines()) if f and f[-1].startswith("oracle_")}
+    assert len(exported) > 50
+    assert exported - _CALLED == set()
