@@ -164,8 +164,12 @@ int lcpp_hip_scan_max_f64(void* temp, size_t temp_bytes, const double* in, doubl
  * static device array of the library (349,528 bytes per GPU, held until the process ends) instead of
  * caller-provided temp storage, and no allocation of any kind.  No counterpart in the reference: it is
  * for callers that cannot allocate (code under graph capture, allocation-free serving loops).  At most
- * 2^30 items (larger n returns LCPP_HIP_ERR_INVALID_ARGUMENT).  Every call on one GPU shares the array:
- * calls that overlap in time on one GPU race (calls in order on one stream are safe). */
+ * 2^30 items (larger n returns LCPP_HIP_ERR_INVALID_ARGUMENT).  The array used is that of the stream's
+ * device.  The first call on a device looks up the device's array and must run outside graph capture
+ * (a first call with n > 0 under capture returns LCPP_HIP_ERR_UNSUPPORTED and records nothing); a call
+ * with n == 0 does only that lookup, so callers that capture make one such call per device first.
+ * Every call on one GPU shares the array: calls that overlap in time on one GPU race (calls in order on
+ * one stream are safe, and so are replays of a graph holding such calls, in order on one stream). */
 int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, uint64_t n, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
@@ -262,7 +266,9 @@ LCPP_HIP_DECLARE_SPMV(u32, uint32_t, u32, uint32_t)
  * the run's items up to i; with init: init + that sum (the reference's "prepend an initial value to
  * every segment" overloads, device_scan.h:488-519).  values_out may equal values_in.
  * Reduce: unique_out[r] = first key of run r, aggregates_out[r] = sum of run r, *num_runs_out = runs;
- * n == 0 writes 0 runs (device_reduce.h:449-458).  Integer sums wrap; n <= 2^32 - 1.
+ * n == 0 writes 0 runs (device_reduce.h:449-458).  Integer sums wrap; n <= 2^32 - 1.  The outputs
+ * need room for the run count only and must not overlap the inputs: an output whose first item lies
+ * inside keys_in or values_in is rejected (-1); buffers that overlap further in are undefined.
  * Key suffixes: i32, u32, i64, u64; value suffixes i32, u32, f32, i64, u64, f64.
  * ------------------------------------------------------------------------------------------- */
 size_t lcpp_hip_scan_by_key_temp_bytes(uint64_t n, size_t key_bytes, size_t value_bytes);

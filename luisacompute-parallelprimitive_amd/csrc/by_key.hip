@@ -844,8 +844,11 @@ int by_key(void* temp, size_t temp_bytes, const K* keys, const V* values_in, V* 
     if (!keys || (MODE != kModeCount && !values_in)) return set_error(kInvalidArgument, "%s: null input", what);
     if constexpr (MODE != kModeScan) {
         // A tile with more runs than its LDS stage reads its input again after its look-back, when later
-        // tiles may already be writing runs: outputs overlapping the inputs would race with that read.
-        const uint64_t out_bytes[2] = {n * sizeof(K), aggregates_out ? n * sizeof(V) : 0};
+        // tiles may already be writing runs, so outputs must not overlap the inputs.  An output holds as
+        // many items as there are runs, which only the kernel learns; the host rejects what must overlap
+        // whatever that count is: an output whose first item (always written, n > 0) lies inside an input.
+        // An output that starts below an input and is as long as the run count never reaches it.
+        const uint64_t out_bytes[2] = {sizeof(K), aggregates_out ? sizeof(V) : 0};
         const uint64_t in_bytes[2] = {n * sizeof(K), MODE == kModeReduce ? n * sizeof(V) : 0};
         const void* outs[2] = {unique_out, aggregates_out};
         const void* ins[2] = {keys, values_in};

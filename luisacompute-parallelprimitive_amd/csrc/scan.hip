@@ -403,40 +403,58 @@ int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, boo
 
 // ---- ExclusiveSum over uint32 with no temp argument and no allocation ------------------------------
 // The tile status words live in `scratch`, a static device array (each GPU holds its own copy until the
-// process ends).  Host code never uses the array's name as an address: the first call on a device, with
-// that device current, looks up the device's copy with hipGetSymbolAddress and keeps it.  Every call on
-// one GPU shares that copy, so calls that overlap in time on one GPU (other streams, other threads) race;
-// calls in order on one stream do not, since each clears the words it uses (fill kernel) before its scan.
+// process ends).  Host code never uses the array's name as an address: the first call on a device looks
+// up that device's copy with hipGetSymbolAddress (with the device of the call's stream current) and keeps
+// it.  The lookup runs outside graph capture only, so a first call under capture is an error; any earlier
+// call on the device, with n == 0 included, does the lookup.  Every call on one GPU shares that copy, so
+// calls that overlap in time on one GPU (other streams, other threads) race; calls in order on one stream
+// do not, since each clears the words it uses (fill kernel) before its scan.
 constexpr uint64_t kNoAllocMaxItems = 1ull << 30;
 constexpr uint64_t kNoAllocWords = (kNoAllocMaxItems + kScanTile<uint32_t> - 1) / kScanTile<uint32_t>;  // 43,691
 static __device__ __align__(256) uint64_t scratch[kNoAllocWords];  // 349,528 bytes per GPU
 
-uint64_t* scratch_of_current_device() {
+// Sets *words to the device's copy of `scratch` for a call on `stream`.  Status kUnsupported when the
+// copy is not looked up yet and the stream is recording a graph; other failures kHipError / kUnsupported.
+int scratch_of_stream(hipStream_t stream, uint64_t** words) {
     static std::mutex mu;
     static uint64_t* ptrs[64] = {};
+    *words = nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) {
         (void)hipGetLastError();
-        set_error(kHipError, "ExclusiveSum (no allocation): no current device");
-        return nullptr;
+        return set_error(kHipError, "ExclusiveSum (no allocation): the stream's device is unknown");
     }
-    if (dev < 0 || dev >= 64) {
-        set_error(kUnsupported, "ExclusiveSum (no allocation): device index %d out of range", dev);
-        return nullptr;
-    }
+    if (dev < 0 || dev >= 64)
+        return set_error(kUnsupported, "ExclusiveSum (no allocation): device index %d out of range", dev);
     std::lock_guard<std::mutex> lock(mu);
-    if (!ptrs[dev]) {
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || p == nullptr) {
-            (void)hipGetLastError();
-            set_error(kHipError, "ExclusiveSum (no allocation): hipGetSymbolAddress of the static scratch failed: %s",
-                      hipGetErrorString(e));
-            return nullptr;
-        }
-        ptrs[dev] = static_cast<uint64_t*>(p);
+    if ((*words = ptrs[dev]) != nullptr) return kOk;
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capture) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(kHipError, "ExclusiveSum (no allocation): the stream's capture state is unknown");
     }
-    return ptrs[dev];
+    if (capture != hipStreamCaptureStatusNone)
+        return set_error(kUnsupported,
+                         "ExclusiveSum (no allocation): the first call on device %d is under graph capture; the "
+                         "static scratch is looked up outside capture only, so make one call on the device (n may "
+                         "be 0) first",
+                         dev);
+    int current = 0;
+    if (hipGetDevice(&current) != hipSuccess || (current != dev && hipSetDevice(dev) != hipSuccess)) {
+        (void)hipGetLastError();
+        return set_error(kHipError, "ExclusiveSum (no allocation): cannot make device %d current", dev);
+    }
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current != dev) (void)hipSetDevice(current);
+    if (e != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();
+        return set_error(kHipError,
+                         "ExclusiveSum (no allocation): hipGetSymbolAddress of the static scratch failed: %s",
+                         hipGetErrorString(e));
+    }
+    *words = ptrs[dev] = static_cast<uint64_t*>(p);
+    return kOk;
 }
 
 }  // namespace
@@ -510,9 +528,10 @@ int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, u
         return set_error(kInvalidArgument,
                          "ExclusiveSum (no allocation): %llu items exceed the static scratch (at most %llu items)",
                          static_cast<unsigned long long>(n), static_cast<unsigned long long>(kNoAllocMaxItems));
-    if (n == 0) return kOk;
-    uint64_t* words = scratch_of_current_device();
-    if (!words) return kHipError;
+    uint64_t* words = nullptr;
+    const int st = scratch_of_stream(static_cast<hipStream_t>(stream), &words);
+    if (n == 0) return st == kUnsupported ? kOk : st;  // nothing to scan; a lookup failure still reports
+    if (st != kOk) return st;
     return scan_sum<uint32_t>(words, kNoAllocWords * sizeof(uint64_t), in, out, n, false, 0u, stream);
 }
 

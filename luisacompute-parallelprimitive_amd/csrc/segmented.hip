@@ -178,7 +178,9 @@ __device__ __forceinline__ typename Reducer<T, OP>::Acc fold_range(const T* __re
         const uint64_t a0 = b + ((16u - (reinterpret_cast<uintptr_t>(in + b) & 15u)) & 15u) / sizeof(T);
         if (a0 + static_cast<uint64_t>(VEC) * stride <= e && (reinterpret_cast<uintptr_t>(in) % sizeof(T)) == 0) {
             using Vec = T __attribute__((ext_vector_type(VEC)));
-            if (b + lane < a0) acc = R::lift(in[b + lane], static_cast<uint32_t>(b + lane));  // a0 - b < VEC <= stride
+            // a0 - b < VEC <= stride.  Combined with the identity, not assigned: an Arg accumulator holding a
+            // NaN would never be replaced, while the identity drops NaN items.
+            if (b + lane < a0) acc = R::combine(acc, R::lift(in[b + lane], static_cast<uint32_t>(b + lane)));
             const Vec* vin = reinterpret_cast<const Vec*>(in + a0);
             const uint64_t nvec = (e - a0) / VEC;
             uint64_t v = lane;

@@ -828,9 +828,11 @@ uint32_t reference_pass_count(uint64_t n) {
 // run in order, so they never share it while running.  A call recorded into a graph gets a slot of its
 // own, never handed out again, so the graph's replays share their words with no eager call and no other
 // graph (only with concurrent replays of the same graph, which share every buffer of the call anyway).
-// Past kLongestSlots slots, and for a call recorded before any eager call on its device (the array's
-// address is not looked up during a capture), a call gets nullptr and its kernels run without the early
-// exits (same results).
+// Past kLongestSlots slots, for a call recorded before any eager call on its device (the array's address
+// is not looked up during a capture), for a stream of a device other than the current one (the lookup
+// needs the stream's device current), and for hipStreamPerThread (one handle naming another stream in
+// each host thread, so calls through it are not ordered with each other), a call gets nullptr and its
+// kernels run without the early exits (same results).
 constexpr uint32_t kLongestSlots = 16384;
 __device__ uint32_t g_longest_slots[2 * kLongestSlots];
 
@@ -860,10 +862,15 @@ int capture_state(hipStream_t stream) {
 // kSlotNone), handed out if it is new.
 int longest_slot(hipStream_t stream, bool take, uint32_t** word) {
     if (word) *word = nullptr;
+    if (stream == hipStreamPerThread) return kSlotNone;
     const int capturing = capture_state(stream);
     if (capturing < 0) return kSlotNone;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return kSlotNone;
+    int dev = 0, current = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || hipGetDevice(&current) != hipSuccess) {
+        (void)hipGetLastError();
+        return kSlotNone;
+    }
+    if (dev != current) return kSlotNone;
     SlotPool& pool = slot_pool();
     std::lock_guard<std::mutex> lock(pool.mu);
     const auto key = std::make_pair(dev, stream);

@@ -304,6 +304,46 @@ def test_temp_too_small_is_an_error(hip, dev):
     assert e.value.status == hip.ERR_TEMP_TOO_SMALL
 
 
+@pytest.mark.parametrize("op", ["sum", "max"])
+def test_reduce_by_key_runs_sized_outputs_below_inputs(hip, orc, dev, op):
+    """Outputs sized to the run count sit directly below the inputs in one allocation, as a caching
+    allocator may place them: accepted and exact, on tiles with more runs than the LDS stage (runs of 1-3
+    items, so every tile reads its input again after its look-back).  An output whose first item lies
+    inside an input overlaps it whatever the run count; such calls are rejected and write nothing."""
+    rng = np.random.default_rng(41)
+    n = 12 * REDUCE_TILE + 5
+    starts = np.zeros(n, bool)
+    pos = np.cumsum(rng.integers(1, 4, n))
+    starts[pos[pos < n]] = True
+    starts[0] = True
+    keys = np.cumsum(starts).astype(np.uint32)
+    vals = rng.integers(-(1 << 31), 1 << 31, n).astype(np.int32)
+    ou, oa = orc.reduce_by_key_int(keys, vals) if op == "sum" else orc.reduce_by_key_minmax(op, keys, vals)
+    runs = ou.size
+    kbuf = torch.empty(runs + n, dtype=torch.int32, device=dev)
+    vbuf = torch.empty(runs + n, dtype=torch.int32, device=dev)
+    kbuf[runs:] = to_dev(keys)
+    vbuf[runs:] = to_dev(vals)
+    d_runs = fill_dev(1, 4, 17)
+    log(f"reduce_by_key {op}: runs-sized outputs below the inputs, {runs} runs")
+    hip.reduce_by_key("u32", "i32", kbuf[runs:], vbuf[runs:], kbuf[:runs], vbuf[:runs], d_runs, n, op=op)
+    assert int(to_host(d_runs, np.uint32, 1)[0]) == runs
+    assert np.array_equal(to_host(kbuf[:runs], np.uint32), ou)
+    assert np.array_equal(to_host(vbuf[:runs], np.int32), oa)
+    assert np.array_equal(to_host(kbuf[runs:], np.uint32), keys)
+    assert np.array_equal(to_host(vbuf[runs:], np.int32), vals)
+    spare_k, spare_v = fill_dev(n, 4, 7), fill_dev(n, 4, 7)
+    d_keys, d_vals = kbuf[runs:], vbuf[runs:]
+    for uniq, agg in ((d_keys, spare_v), (spare_k, d_vals), (d_keys[n - 1:], spare_v), (spare_k, d_keys[5:]),
+                      (d_vals[1000:], spare_v)):
+        with pytest.raises(hip.LcppHipError) as e:
+            hip.reduce_by_key("u32", "i32", d_keys, d_vals, uniq, agg, d_runs, n, op=op)
+        assert e.value.status == hip.ERR_INVALID_ARGUMENT
+    assert np.array_equal(to_host(kbuf[runs:], np.uint32), keys)
+    assert np.array_equal(to_host(vbuf[runs:], np.int32), vals)
+    assert np.array_equal(to_host(spare_k, np.int32), np.full(n, 7, np.int32))
+
+
 # ---- min / max operators -----------------------------------------------------------------------------
 # ScanByKey / ReduceByKey with MinOp / MaxOp (device_scan.h:424-597, device_reduce.h:437-487): bit-exact
 # against the oracle's left-to-right fold for every value type (floats included: the result is one of the

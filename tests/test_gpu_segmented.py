@@ -90,6 +90,33 @@ def test_segment_reduce_known_answers(hip, dev):
     assert v.tolist() == [1, 2] and i.tolist() == [1, 2]
 
 
+@pytest.mark.parametrize("op", ["argmin", "argmax"])
+def test_arg_nan_among_unaligned_head_items(hip, orc, dev, op):
+    """Float ArgMin / ArgMax over segments of 512 to 70,000 items that start 1-3 items before a 16-byte
+    boundary (the items the lanes read one by one before the 16-byte vectors), with NaNs among those head
+    items: NaN items never win, so the true extremum and its index come out, as the oracle's fold that skips
+    NaN items gives."""
+    rng = np.random.default_rng(61)
+    n = 1 << 19
+    x = rng.standard_normal(n).astype(np.float32)
+    begins, ends = [], []
+    pos = 5
+    for length in (512, 513, 700, 1024, 1500, 4096, 5000, 70000):
+        for r in (1, 2, 3):  # b % 4 == r: 4 - r items before the boundary (the input is 16-byte aligned)
+            b = pos - pos % 4 + r + 4
+            x[b] = np.nan
+            if r == 1:
+                x[b + 1] = np.nan  # two of the three head items
+            begins.append(b)
+            ends.append(b + length)
+            pos = b + length + 7
+    assert pos < n
+    log(f"segment {op}: NaN head items in {len(begins)} unaligned segments")
+    got, idx = g_reduce(hip, op, x, begins, ends)
+    check_reduce(orc, op, x, begins, ends, got, idx, "f32")
+    assert not np.isnan(got).any()
+
+
 def test_segmented_scan_known_answers(hip, orc, dev):
     """device_segmented_scan_test.cpp:104-257: same and packed output offsets, exclusive, inclusive,
     inclusive with initial value 10, and the exact in-place inclusive sum (items outside every segment
