@@ -112,6 +112,39 @@ LCPP_HIP_DECLARE_REDUCE_EXT(f64, double)
 #undef LCPP_HIP_DECLARE_REDUCE_EXT
 size_t lcpp_hip_reduce_arg_temp_bytes(uint64_t n, size_t elem_bytes);
 
+/* DeviceReduce<>::Reduce(cmdlist, temp, in, out, n, reduce_op, initial_value) (device_reduce.h:229-252)
+ * and TransformReduce(cmdlist, temp, in, out, n, reduce_op, transform_op, init) (:491-515):
+ * *out = op(init, fold over i of op(transform(in[i]))); n == 0 writes init.  The transform is applied
+ * to input items only, once each (tests/device_reduce_test.cpp:148-173), and init enters last, on the
+ * left, as in the reference's single-tile kernel (device/details/reduce.h:227-237).  The reference
+ * takes device callables; this vocabulary covers its tests:
+ *   op:        LCPP_HIP_REDUCE_SUM (wrapping for integers), LCPP_HIP_REDUCE_MIN, LCPP_HIP_REDUCE_MAX
+ *              (MinOp / MaxOp: signed types compare as signed, floats like fmin / fmax);
+ *   transform: LCPP_HIP_TRANSFORM_IDENTITY, LCPP_HIP_TRANSFORM_AFFINE (scale * x + shift: x + c, 2x,
+ *              2x + 1 ...), LCPP_HIP_TRANSFORM_SQUARE (x * x), LCPP_HIP_TRANSFORM_ABS (|x|).
+ * Integer transforms wrap modulo 2^bits; float transforms round after every operation (no fused
+ * multiply-add).  scale / shift are read by the affine transform only.  An unknown op or transform
+ * returns LCPP_HIP_ERR_INVALID_ARGUMENT.  Temp: lcpp_hip_reduce_temp_bytes(n, sizeof(T)). */
+#define LCPP_HIP_REDUCE_SUM 0
+#define LCPP_HIP_REDUCE_MIN 1
+#define LCPP_HIP_REDUCE_MAX 2
+#define LCPP_HIP_TRANSFORM_IDENTITY 0
+#define LCPP_HIP_TRANSFORM_AFFINE 1
+#define LCPP_HIP_TRANSFORM_SQUARE 2
+#define LCPP_HIP_TRANSFORM_ABS 3
+#define LCPP_HIP_DECLARE_REDUCE_OP(S, T)                                                                         \
+    int lcpp_hip_reduce_op_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int op, T init, \
+                               void* stream);                                                                   \
+    int lcpp_hip_transform_reduce_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int op,   \
+                                      int transform, T scale, T shift, T init, void* stream);
+LCPP_HIP_DECLARE_REDUCE_OP(i32, int32_t)
+LCPP_HIP_DECLARE_REDUCE_OP(u32, uint32_t)
+LCPP_HIP_DECLARE_REDUCE_OP(f32, float)
+LCPP_HIP_DECLARE_REDUCE_OP(i64, int64_t)
+LCPP_HIP_DECLARE_REDUCE_OP(u64, uint64_t)
+LCPP_HIP_DECLARE_REDUCE_OP(f64, double)
+#undef LCPP_HIP_DECLARE_REDUCE_OP
+
 /* ---------------------------------------------------------------------------------------------
  * DeviceScan::ExclusiveSum / InclusiveSum (decoupled look-back, single pass)
  * replaces DeviceScan<>::ExclusiveSum (src/lcpp/device/device_scan.h:370-385),

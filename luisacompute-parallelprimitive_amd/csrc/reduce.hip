@@ -14,6 +14,10 @@
 // (device_reduce.h:311-436) fold (value, index) pairs: the smaller (larger) value wins, equal values the
 // lower index, NaNs never win; the reference builds an n-sized pair array first, here each thread
 // carries the index of its best item, so the pass reads the items once.
+// Reduce(op, init) and TransformReduce(op, transform, init) (device_reduce.h:229-252,491-515) run the
+// same pass with the operator and the transform as template parameters: the transform is applied once
+// to every item (never to partials), and the final kernel folds the initial value in on the left,
+// op(init, aggregate), as the reference's single-tile kernel does (device/details/reduce.h:227-237).
 // Algorithmic traffic: n * sizeof(T) bytes read (+ grid partials).
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
@@ -117,6 +121,52 @@ template <typename T>
 __global__ void write_scalar_kernel(T* out, T value) {
     *out = value;
 }
+// ---- transforms and operators of Reduce / TransformReduce ---------------------------------------
+// The reference takes any device callable; with no JIT here, a fixed vocabulary covers its tests:
+// identity, scale * x + shift (x + c, 2x, 2x + 1 ...), x * x and |x|.  Integer arithmetic wraps (it runs
+// in the unsigned type of the same width); float arithmetic rounds after every operation, with no
+// fused multiply-add, so a host loop evaluating the same expression gets the same transformed items.
+enum : int { kXformIdentity = 0, kXformAffine = 1, kXformSquare = 2, kXformAbs = 3 };
+
+template <typename T, int XF>
+__device__ __forceinline__ T apply_transform(T x, T scale, T shift) {
+#pragma clang fp contract(off)
+    if constexpr (XF == kXformIdentity) {
+        return x;
+    } else if constexpr (std::is_floating_point_v<T>) {
+        if constexpr (XF == kXformAffine) {
+            const T p = x * scale;
+            return p + shift;
+        } else if constexpr (XF == kXformSquare) {
+            return x * x;
+        } else {
+            return std::fabs(x);
+        }
+    } else {
+        using UT = std::make_unsigned_t<T>;
+        const UT u = static_cast<UT>(x);
+        if constexpr (XF == kXformAffine) return static_cast<T>(static_cast<UT>(u * static_cast<UT>(scale) + static_cast<UT>(shift)));
+        else if constexpr (XF == kXformSquare) return static_cast<T>(static_cast<UT>(u * u));
+        else if constexpr (std::is_signed_v<T>) return x < 0 ? static_cast<T>(static_cast<UT>(UT(0) - u)) : x;
+        else return x;
+    }
+}
+
+// The sum operator in the item's own type, wrapping for signed integers too.
+struct WrapSumOp {
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const {
+        if constexpr (std::is_integral_v<T>) {
+            using UT = std::make_unsigned_t<T>;
+            return static_cast<T>(static_cast<UT>(static_cast<UT>(a) + static_cast<UT>(b)));
+        } else {
+            return a + b;
+        }
+    }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() { return T(0); }
+};
+
 // ---- min / max ---------------------------------------------------------------------------------
 template <typename T, typename Op>
 __device__ __forceinline__ T block_fold(T x, T* s_waves, Op op) {
@@ -131,11 +181,13 @@ __device__ __forceinline__ T block_fold(T x, T* s_waves, Op op) {
     return total;
 }
 
-// reduce_sum_partials_kernel with a min / max operator; partials[blockIdx.x] = the workgroup's fold.
-template <typename T, typename Op>
+// reduce_sum_partials_kernel with another operator (min / max, or the sum in the item's own type) and a
+// transform of every item; partials[blockIdx.x] = the workgroup's fold.
+template <typename T, typename Op, int XF = kXformIdentity>
 __global__ __launch_bounds__(kReduceBlock) void reduce_ext_partials_kernel(const T* __restrict__ in, uint64_t n,
                                                                            uint32_t head, uint64_t nvec,
-                                                                           T* __restrict__ partials) {
+                                                                           T* __restrict__ partials, T scale,
+                                                                           T shift) {
     constexpr int V = 16 / sizeof(T);
     using Vec = Vec16<T>;
     const Op op{};
@@ -155,7 +207,7 @@ __global__ __launch_bounds__(kReduceBlock) void reduce_ext_partials_kernel(const
 #pragma unroll
         for (int u = 0; u < kReduceUnroll; ++u) {
 #pragma unroll
-            for (int j = 0; j < V; ++j) acc[u] = op(acc[u], v[u][j]);
+            for (int j = 0; j < V; ++j) acc[u] = op(acc[u], apply_transform<T, XF>(v[u][j], scale, shift));
         }
     }
     if (base < nvec) {
@@ -165,14 +217,14 @@ __global__ __launch_bounds__(kReduceBlock) void reduce_ext_partials_kernel(const
             if (idx < nvec) {
                 const Vec v = vin[idx];
 #pragma unroll
-                for (int j = 0; j < V; ++j) acc[u] = op(acc[u], v[j]);
+                for (int j = 0; j < V; ++j) acc[u] = op(acc[u], apply_transform<T, XF>(v[j], scale, shift));
             }
         }
     }
     if (blockIdx.x == 0) {
-        if (tid < head) acc[0] = op(acc[0], in[tid]);
+        if (tid < head) acc[0] = op(acc[0], apply_transform<T, XF>(in[tid], scale, shift));
         const uint64_t t = head + nvec * V + tid;
-        if (t < n) acc[1] = op(acc[1], in[t]);
+        if (t < n) acc[1] = op(acc[1], apply_transform<T, XF>(in[t], scale, shift));
     }
     T x = acc[0];
 #pragma unroll
@@ -181,7 +233,8 @@ __global__ __launch_bounds__(kReduceBlock) void reduce_ext_partials_kernel(const
     if (tid == 0) partials[blockIdx.x] = x;
 }
 
-// Folds `count` partials, then the reference's initial value (the type's max for min, lowest for max).
+// Folds `count` partials, then folds the result into the initial value: op(init, aggregate) (the type's
+// max for Min, lowest for Max, the caller's value for Reduce / TransformReduce).
 template <typename T, typename Op>
 __global__ __launch_bounds__(kFinalBlock) void reduce_ext_final_kernel(const T* __restrict__ partials, uint32_t count,
                                                                        T init, T* __restrict__ out) {
@@ -413,13 +466,11 @@ ReducePlan reduce_plan(const T* in, uint64_t n, uint64_t partial_slots) {
     return ReducePlan{head, nvec, grid};
 }
 
-// DeviceReduce::Min (MAX false) / Max (true): the fold of the items and the type's max / lowest.
-template <typename T, bool MAX>
-int reduce_ext(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, void* stream_ptr) {
-    using Op = std::conditional_t<MAX, MaxValueOp, MinValueOp>;
-    const char* what = MAX ? "DeviceReduce::Max" : "DeviceReduce::Min";
-    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const T init = MAX ? std::numeric_limits<T>::lowest() : std::numeric_limits<T>::max();
+// op(init, fold of the transformed items) over the persistent pass and a final kernel; n == 0 writes
+// init.  DeviceReduce::Min / Max are the identity transform with the type's max / lowest as init.
+template <typename T, typename Op, int XF>
+int reduce_generic(const char* what, const char* scope_name, void* temp, size_t temp_bytes, const T* in, T* out,
+                   uint64_t n, T scale, T shift, T init, hipStream_t stream) {
     if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items (%llu > UINT_MAX)", what,
                                             static_cast<unsigned long long>(n));
     if (!out) return set_error(kInvalidArgument, "%s: null output", what);
@@ -433,23 +484,76 @@ int reduce_ext(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, v
         return set_error(kInvalidArgument, "%s: input not aligned to its element size", what);
     const ReducePlan pl = reduce_plan(in, n, temp ? temp_bytes / sizeof(T) : 0);
     T* partials = static_cast<T*>(temp);
-    LaunchScope scope("reduce_extremum", stream);
+    LaunchScope scope(scope_name, stream);
     if (pl.grid == 1) {
         // One workgroup folds everything into the first temp slot (into *out when there is no temp);
-        // the final kernel then folds that value with the initial value.
+        // the final kernel then folds that value into the initial value.
         T* slot = temp && temp_bytes >= sizeof(T) ? partials : out;
-        reduce_ext_partials_kernel<T, Op><<<1, kReduceBlock, 0, stream>>>(in, n, static_cast<uint32_t>(pl.head), pl.nvec, slot);
-        int st = check_hip(hipGetLastError(), "reduce_extremum launch");
+        reduce_ext_partials_kernel<T, Op, XF><<<1, kReduceBlock, 0, stream>>>(in, n, static_cast<uint32_t>(pl.head),
+                                                                              pl.nvec, slot, scale, shift);
+        int st = check_hip(hipGetLastError(), "reduce launch");
         if (st != kOk) return st;
         reduce_ext_final_kernel<T, Op><<<1, kFinalBlock, 0, stream>>>(slot, 1u, init, out);
-        return check_hip(hipGetLastError(), "reduce_extremum final launch");
+        return check_hip(hipGetLastError(), "reduce final launch");
     }
-    reduce_ext_partials_kernel<T, Op><<<static_cast<unsigned>(pl.grid), kReduceBlock, 0, stream>>>(
-        in, n, static_cast<uint32_t>(pl.head), pl.nvec, partials);
-    int st = check_hip(hipGetLastError(), "reduce_extremum launch");
+    reduce_ext_partials_kernel<T, Op, XF><<<static_cast<unsigned>(pl.grid), kReduceBlock, 0, stream>>>(
+        in, n, static_cast<uint32_t>(pl.head), pl.nvec, partials, scale, shift);
+    int st = check_hip(hipGetLastError(), "reduce launch");
     if (st != kOk) return st;
     reduce_ext_final_kernel<T, Op><<<1, kFinalBlock, 0, stream>>>(partials, static_cast<uint32_t>(pl.grid), init, out);
-    return check_hip(hipGetLastError(), "reduce_extremum final launch");
+    return check_hip(hipGetLastError(), "reduce final launch");
+}
+
+// DeviceReduce::Min (MAX false) / Max (true): the fold of the items and the type's max / lowest.
+template <typename T, bool MAX>
+int reduce_ext(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, void* stream_ptr) {
+    using Op = std::conditional_t<MAX, MaxValueOp, MinValueOp>;
+    const T init = MAX ? std::numeric_limits<T>::lowest() : std::numeric_limits<T>::max();
+    return reduce_generic<T, Op, kXformIdentity>(MAX ? "DeviceReduce::Max" : "DeviceReduce::Min", "reduce_extremum",
+                                                 temp, temp_bytes, in, out, n, T(0), T(0), init,
+                                                 static_cast<hipStream_t>(stream_ptr));
+}
+
+// DeviceReduce::Reduce(op, init) (transform identity) and TransformReduce(op, transform, init): op 0 sum
+// (wrapping for integers), 1 min, 2 max (the NaN-ignoring MinOp / MaxOp); transform as kXform*.
+template <typename T, typename Op>
+int transform_reduce_op(const char* what, int transform, void* temp, size_t temp_bytes, const T* in, T* out,
+                        uint64_t n, T scale, T shift, T init, hipStream_t stream) {
+    switch (transform) {
+        case kXformIdentity:
+            return reduce_generic<T, Op, kXformIdentity>(what, "reduce_op", temp, temp_bytes, in, out, n, scale, shift,
+                                                         init, stream);
+        case kXformAffine:
+            return reduce_generic<T, Op, kXformAffine>(what, "reduce_op", temp, temp_bytes, in, out, n, scale, shift,
+                                                       init, stream);
+        case kXformSquare:
+            return reduce_generic<T, Op, kXformSquare>(what, "reduce_op", temp, temp_bytes, in, out, n, scale, shift,
+                                                       init, stream);
+        case kXformAbs:
+            return reduce_generic<T, Op, kXformAbs>(what, "reduce_op", temp, temp_bytes, in, out, n, scale, shift, init,
+                                                    stream);
+        default:
+            return set_error(kInvalidArgument, "%s: unknown transform %d", what, transform);
+    }
+}
+
+template <typename T>
+int transform_reduce(const char* what, void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int op,
+                     int transform, T scale, T shift, T init, void* stream_ptr) {
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    switch (op) {
+        case 0:
+            return transform_reduce_op<T, WrapSumOp>(what, transform, temp, temp_bytes, in, out, n, scale, shift, init,
+                                                     stream);
+        case 1:
+            return transform_reduce_op<T, MinValueOp>(what, transform, temp, temp_bytes, in, out, n, scale, shift, init,
+                                                      stream);
+        case 2:
+            return transform_reduce_op<T, MaxValueOp>(what, transform, temp, temp_bytes, in, out, n, scale, shift, init,
+                                                      stream);
+        default:
+            return set_error(kInvalidArgument, "%s: unknown reduce operator %d", what, op);
+    }
 }
 
 // DeviceReduce::ArgMin (MAX false) / ArgMax (true).  n == 0 writes the type's max / lowest and index 1
@@ -532,5 +636,26 @@ LCPP_HIP_DEFINE_REDUCE_EXT(i64, int64_t)
 LCPP_HIP_DEFINE_REDUCE_EXT(u64, uint64_t)
 LCPP_HIP_DEFINE_REDUCE_EXT(f64, double)
 #undef LCPP_HIP_DEFINE_REDUCE_EXT
+
+// Reduce(op, init) and TransformReduce(op, transform, init): signed integers keep their own type (min /
+// max compare as signed; sums wrap through the unsigned type).
+#define LCPP_HIP_DEFINE_REDUCE_OP(S, T)                                                                          \
+    int lcpp_hip_reduce_op_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int op, T init,  \
+                               void* stream) {                                                                   \
+        return transform_reduce<T>("DeviceReduce::Reduce", temp, temp_bytes, in, out, n, op, kXformIdentity, T(0), \
+                                   T(0), init, stream);                                                          \
+    }                                                                                                            \
+    int lcpp_hip_transform_reduce_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int op,    \
+                                      int transform, T scale, T shift, T init, void* stream) {                   \
+        return transform_reduce<T>("DeviceReduce::TransformReduce", temp, temp_bytes, in, out, n, op, transform,  \
+                                   scale, shift, init, stream);                                                  \
+    }
+LCPP_HIP_DEFINE_REDUCE_OP(i32, int32_t)
+LCPP_HIP_DEFINE_REDUCE_OP(u32, uint32_t)
+LCPP_HIP_DEFINE_REDUCE_OP(f32, float)
+LCPP_HIP_DEFINE_REDUCE_OP(i64, int64_t)
+LCPP_HIP_DEFINE_REDUCE_OP(u64, uint64_t)
+LCPP_HIP_DEFINE_REDUCE_OP(f64, double)
+#undef LCPP_HIP_DEFINE_REDUCE_OP
 
 }  // extern "C"

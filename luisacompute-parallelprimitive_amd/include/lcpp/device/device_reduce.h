@@ -1,6 +1,7 @@
-// DeviceReduce::Sum / Min / Max / ArgMin / ArgMax over the MI355X C-ABI (lcpp_hip_reduce_{sum,min,max,
-// argmin,argmax}_*), with the reference's module shape (src/lcpp/device/device_reduce.h:102-113 template,
-// :154-173 create, :184-210 temp queries, :280-436 Sum to ArgMax) and its record-time checks (:238-264).  Sum records one command; the kernels run on
+// DeviceReduce::Sum / Min / Max / ArgMin / ArgMax / Reduce / TransformReduce over the MI355X C-ABI
+// (lcpp_hip_reduce_{sum,min,max,argmin,argmax}_*, lcpp_hip_transform_reduce_*), with the reference's module
+// shape (src/lcpp/device/device_reduce.h:102-113 template, :154-173 create, :184-210 temp queries,
+// :229-252 Reduce, :280-436 Sum to ArgMax, :491-515 TransformReduce) and its record-time checks (:238-264).  Sum records one command; the kernels run on
 // the stream the command list is committed to.  ReduceByKey with a sum operator (:437-487, temp
 // query :207-223) with SumOp, MinOp or MaxOp runs lcpp_hip_reduce_by_key_{sum,min,max}_*, which writes 0
 // runs for empty input (:449-458).
@@ -107,6 +108,26 @@ class DeviceReduce : public LuisaModule {
         record_arg<true>(cmdlist, temp_storage, d_in, d_out, d_index_out, num_item);
     }
 
+    // Reduce with SumOp, MinOp or MaxOp and an initial value (device_reduce.h:229-252):
+    // d_out[0] = op(initial_value, fold of the items); an empty input writes initial_value.
+    template <NumericT T, typename ReduceOp>
+        requires(detail::by_key_op_ok<ReduceOp>)
+    void Reduce(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                size_t num_item, ReduceOp reduce_op, T initial_value) {
+        record_transform(cmdlist, temp_storage, d_in, d_out, num_item, reduce_op, IdentityOp{}, initial_value,
+                         "DeviceReduce::Reduce");
+    }
+
+    // TransformReduce (device_reduce.h:491-515): d_out[0] = op(init, fold of transform_op(item)); the
+    // transform is IdentityOp, AffineOp<T>{scale, shift}, SquareOp or AbsOp.
+    template <NumericT T, typename ReduceOp, typename TransformOp>
+        requires(detail::by_key_op_ok<ReduceOp>)
+    void TransformReduce(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                         size_t num_item, ReduceOp reduce_op, TransformOp transform_op, T init) {
+        record_transform(cmdlist, temp_storage, d_in, d_out, num_item, reduce_op, transform_op, init,
+                         "DeviceReduce::TransformReduce");
+    }
+
     template <NumericT T>
     void Sum(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
              size_t num_item) {
@@ -148,6 +169,60 @@ class DeviceReduce : public LuisaModule {
                                       std::conditional_t<std::is_signed_v<T>,
                                                          std::conditional_t<sizeof(T) == 4, int32_t, int64_t>,
                                                          std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>>>;
+
+    template <NumericT T, typename ReduceOp, typename TransformOp>
+    void record_transform(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,
+                          size_t num_item, ReduceOp, TransformOp transform_op, T init, const char* what) {
+        static_assert(sizeof(T) == 4 || sizeof(T) == 8, "DeviceReduce::Reduce supports 4- and 8-byte numbers");
+        LCPP_ASSERT(m_created, "DeviceReduce::create must be called before dispatch.");
+        LCPP_ASSERT(num_item <= std::numeric_limits<uint>::max(), "Too many items for DeviceReduce.");
+        LCPP_ASSERT(d_out.size() >= 1u, "DeviceReduce output view is empty.");
+        if (num_item > 0) {
+            LCPP_ASSERT(d_in.size() >= num_item, "DeviceReduce input view is too small.");
+            LCPP_ASSERT(temp_storage.size() >= bytes_to_uint_count(GetTempStorageBytes<T>(num_item)),
+                        "DeviceReduce temporary storage is too small.");
+        }
+        constexpr int op = std::is_same_v<ReduceOp, SumOp>   ? LCPP_HIP_REDUCE_SUM
+                           : std::is_same_v<ReduceOp, MinOp> ? LCPP_HIP_REDUCE_MIN
+                                                             : LCPP_HIP_REDUCE_MAX;
+        int transform = LCPP_HIP_TRANSFORM_IDENTITY;
+        T scale = T(0), shift = T(0);
+        if constexpr (std::is_same_v<TransformOp, AffineOp<T>>) {
+            transform = LCPP_HIP_TRANSFORM_AFFINE;
+            scale = transform_op.scale;
+            shift = transform_op.shift;
+        } else if constexpr (std::is_same_v<TransformOp, SquareOp>) {
+            transform = LCPP_HIP_TRANSFORM_SQUARE;
+        } else if constexpr (std::is_same_v<TransformOp, AbsOp>) {
+            transform = LCPP_HIP_TRANSFORM_ABS;
+        } else {
+            static_assert(std::is_same_v<TransformOp, IdentityOp>,
+                          "TransformReduce takes IdentityOp, AffineOp<T>, SquareOp or AbsOp");
+        }
+        using A = ExtAbi<T>;
+        uint* temp = temp_storage.data();
+        const size_t temp_bytes = temp_storage.size_bytes();
+        const A* in = reinterpret_cast<const A*>(d_in.data());
+        A* out = reinterpret_cast<A*>(d_out.data());
+        const A a_scale = static_cast<A>(scale), a_shift = static_cast<A>(shift), a_init = static_cast<A>(init);
+        cmdlist << [=](hipStream_t s) {
+            void* st = detail::stream_ptr(s);
+            int rc;
+            if constexpr (std::is_same_v<A, int32_t>)
+                rc = lcpp_hip_transform_reduce_i32(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            else if constexpr (std::is_same_v<A, uint32_t>)
+                rc = lcpp_hip_transform_reduce_u32(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            else if constexpr (std::is_same_v<A, float>)
+                rc = lcpp_hip_transform_reduce_f32(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            else if constexpr (std::is_same_v<A, int64_t>)
+                rc = lcpp_hip_transform_reduce_i64(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            else if constexpr (std::is_same_v<A, uint64_t>)
+                rc = lcpp_hip_transform_reduce_u64(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            else
+                rc = lcpp_hip_transform_reduce_f64(temp, temp_bytes, in, out, num_item, op, transform, a_scale, a_shift, a_init, st);
+            luisa::detail::abi_check(rc, what);
+        };
+    }
 
     template <bool MAX, NumericT T>
     void record_ext(CommandList& cmdlist, BufferView<uint> temp_storage, BufferView<T> d_in, BufferView<T> d_out,

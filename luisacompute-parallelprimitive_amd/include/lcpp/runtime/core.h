@@ -260,6 +260,27 @@ struct MinOp {
     T operator()(const T& a, const T& b) const { return b < a ? b : a; }
 };
 
+// Transforms of DeviceReduce::TransformReduce.  The reference takes any device callable
+// (common/thread_operators.h:76-84 IdentityOp); the C-ABI's fixed vocabulary covers its tests: the
+// identity, scale * x + shift, x * x and |x| (integers wrap, floats round after every operation).
+struct IdentityOp {
+    template <typename T>
+    T operator()(const T& x) const { return x; }
+};
+template <typename T>
+struct AffineOp {
+    T scale, shift;
+    T operator()(const T& x) const { return scale * x + shift; }
+};
+struct SquareOp {
+    template <typename T>
+    T operator()(const T& x) const { return x * x; }
+};
+struct AbsOp {
+    template <typename T>
+    T operator()(const T& x) const { return x < T(0) ? T(0) - x : x; }
+};
+
 template <typename T>
 concept NumericT = std::is_integral_v<T> || std::is_floating_point_v<T>;  // common/type_trait.h:14
 

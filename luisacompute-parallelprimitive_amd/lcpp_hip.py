@@ -103,6 +103,8 @@ def _declare(lib: C.CDLL) -> None:
         for op in ("min", "max"):
             sig(f"lcpp_hip_reduce_{op}_{s}", i32, vp, sz, vp, vp, u64, vp)
             sig(f"lcpp_hip_reduce_arg{op}_{s}", i32, vp, sz, vp, vp, vp, u64, vp)
+        sig(f"lcpp_hip_reduce_op_{s}", i32, vp, sz, vp, vp, u64, i32, _CTYPE[s], vp)
+        sig(f"lcpp_hip_transform_reduce_{s}", i32, vp, sz, vp, vp, u64, i32, i32, _CTYPE[s], _CTYPE[s], _CTYPE[s], vp)
     sig("lcpp_hip_reduce_arg_temp_bytes", sz, u64, sz)
     for s in SCAN_SUFFIXES:
         sig(f"lcpp_hip_scan_exclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
@@ -247,6 +249,29 @@ def reduce_sum(suffix: str, d_in, d_out, n: int, temp=None, stream=None) -> None
         temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
     call(f"lcpp_hip_reduce_sum_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out), n,
          stream_handle(stream))
+
+
+REDUCE_OPS = {"sum": 0, "min": 1, "max": 2}  # LCPP_HIP_REDUCE_*
+TRANSFORMS = {"identity": 0, "affine": 1, "square": 2, "abs": 3}  # LCPP_HIP_TRANSFORM_*
+
+
+def reduce_op(op: str, suffix: str, d_in, d_out, n: int, init=0, temp=None, stream=None) -> None:
+    """DeviceReduce::Reduce(op, init) with op "sum", "min" or "max": op(init, fold of the items) into d_out[0]."""
+    if temp is None:
+        temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    call(f"lcpp_hip_reduce_op_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out), n,
+         REDUCE_OPS[op], _CTYPE[suffix](init), stream_handle(stream))
+
+
+def transform_reduce(op: str, transform: str, suffix: str, d_in, d_out, n: int, scale=0, shift=0, init=0, temp=None,
+                     stream=None) -> None:
+    """DeviceReduce::TransformReduce(op, transform, init): transform "identity", "affine" (scale * x + shift),
+    "square" or "abs" applied to every item, then op(init, fold) into d_out[0]."""
+    if temp is None:
+        temp = _temp(reduce_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
+    ct = _CTYPE[suffix]
+    call(f"lcpp_hip_transform_reduce_{suffix}", ptr(temp), temp.numel() * temp.element_size(), ptr(d_in), ptr(d_out),
+         n, REDUCE_OPS[op], TRANSFORMS[transform], ct(scale), ct(shift), ct(init), stream_handle(stream))
 
 
 def reduce_arg_temp_bytes(n: int, elem_bytes: int) -> int:

@@ -76,6 +76,11 @@ def lib() -> C.CDLL:
             f = getattr(h, f"oracle_reduce_by_key_minmax_{name}")
             f.restype = u64
             f.argtypes = [vp, i32, vp, vp, vp, u64, u64, i32]
+        for name, ct in (("i32", C.c_int32), ("u32", C.c_uint32), ("f32", C.c_float), ("i64", C.c_int64),
+                         ("u64", C.c_uint64), ("f64", C.c_double)):
+            f = getattr(h, f"oracle_transform_reduce_{name}")
+            f.restype = ct
+            f.argtypes = [vp, u64, i32, i32, ct, ct, ct, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -234,6 +239,24 @@ def scan_minmax(op: str, a: np.ndarray, inclusive: bool = False, init=None) -> n
     out = np.empty_like(a)
     getattr(lib(), f"oracle_scan_{op}_{sfx}")(_p(a), _p(out), a.size, int(inclusive), a.dtype.type(init).item())
     return out
+
+
+REDUCE_OPS = {"sum": 0, "min": 1, "max": 2}
+TRANSFORMS = {"identity": 0, "affine": 1, "square": 2, "abs": 3}
+
+
+def transform_reduce(a: np.ndarray, op: str, transform: str = "identity", scale=0, shift=0, init=0):
+    """DeviceReduce::Reduce(op, init) / TransformReduce(op, transform, init): (result in the item type,
+    the result as a double (the long-double sum for float sums), the sum of |init| and |transformed items|
+    (float sums only, else 0))."""
+    a = np.ascontiguousarray(a)
+    ct = _MINMAX_CTYPE[a.dtype]
+    exact, absum = C.c_double(), C.c_double()
+    t = a.dtype.type
+    r = getattr(lib(), f"oracle_transform_reduce_{_MINMAX_SUFFIX[a.dtype]}")(
+        _p(a), a.size, REDUCE_OPS[op], TRANSFORMS[transform], t(scale).item(), t(shift).item(), t(init).item(),
+        C.byref(exact), C.byref(absum))
+    return t(r), float(exact.value), float(absum.value)
 
 
 # ---- host baselines (oracle/cpu_baseline.cpp): `threads` std::threads over contiguous chunks ----------

@@ -240,6 +240,70 @@ ORACLE_SCAN_MINMAX(u64, uint64_t)
 ORACLE_SCAN_MINMAX(f64, double)
 #undef ORACLE_SCAN_MINMAX
 
+/* DeviceReduce::Reduce(op, init) / TransformReduce(op, transform, init) (device_reduce.h:229-252,491-515;
+ * the initial value enters last, on the left: reduce_op(init, aggregate), device/details/reduce.h:227-237).
+ * y_i = transform(in[i]) in the item type: 0 identity, 1 scale * y + shift, 2 y * y, 3 |y| (integers
+ * wrap modulo 2^bits; floats round after every operation, no fused multiply-add).  op 0 sum, 1 min,
+ * 2 max (the min / max scans' operator: a NaN operand yields the other one, ties keep the left one).
+ * Returns op(init, fold of the y_i from the op's identity) in the item type; for float sums the value is
+ * the long-double sum rounded to T, *exact gets it in double and *abs_sum the sum of |init| and |y_i|.
+ * n == 0 gives init. */
+#define ORACLE_XFORM_INT(NAME, T, UT, SIGNED)                                                              \
+    static T xform_##NAME(T x, int transform, T scale, T shift) {                                         \
+        if (transform == 1) return (T)(UT)((UT)x * (UT)scale + (UT)shift);                                \
+        if (transform == 2) return (T)(UT)((UT)x * (UT)x);                                                \
+        if (transform == 3 && SIGNED && ((UT)x >> (8 * sizeof(T) - 1)) != 0) return (T)(UT)((UT)0 - (UT)x); \
+        return x;                                                                                         \
+    }
+#define ORACLE_XFORM_FLOAT(NAME, T, FABS)                                                                  \
+    static T xform_##NAME(T x, int transform, T scale, T shift) {                                         \
+        if (transform == 1) { const T p = x * scale; return p + shift; }                                   \
+        if (transform == 2) return x * x;                                                                 \
+        if (transform == 3) return FABS(x);                                                               \
+        return x;                                                                                         \
+    }
+ORACLE_XFORM_INT(i32, int32_t, uint32_t, 1)
+ORACLE_XFORM_INT(u32, uint32_t, uint32_t, 0)
+ORACLE_XFORM_FLOAT(f32, float, fabsf)
+ORACLE_XFORM_INT(i64, int64_t, uint64_t, 1)
+ORACLE_XFORM_INT(u64, uint64_t, uint64_t, 0)
+ORACLE_XFORM_FLOAT(f64, double, fabs)
+#undef ORACLE_XFORM_INT
+#undef ORACLE_XFORM_FLOAT
+#define ORACLE_TRANSFORM_REDUCE(NAME, T, UT, IS_FLOAT, TMAX, TLOW)                                         \
+    static T fold_##NAME(T run, T x, int op) {                                                            \
+        if (op == 1) return (x < run || run != run) ? x : run;                                            \
+        if (op == 2) return (x > run || run != run) ? x : run;                                            \
+        return IS_FLOAT ? run + x : (T)(UT)((UT)run + (UT)x);                                             \
+    }                                                                                                     \
+    T oracle_transform_reduce_##NAME(const T* in, uint64_t n, int op, int transform, T scale, T shift,     \
+                                     T init, double* exact, double* abs_sum) {                            \
+        if (op == 0 && IS_FLOAT) {                                                                        \
+            long double s = init, a = fabsl((long double)init);                                           \
+            for (uint64_t i = 0; i < n; ++i) {                                                            \
+                const T y = xform_##NAME(in[i], transform, scale, shift);                                 \
+                s += y;                                                                                   \
+                a += fabsl((long double)y);                                                               \
+            }                                                                                             \
+            if (exact) *exact = (double)s;                                                                \
+            if (abs_sum) *abs_sum = (double)a;                                                            \
+            return (T)s;                                                                                  \
+        }                                                                                                 \
+        T run = op == 1 ? (IS_FLOAT ? (T)NAN : TMAX) : op == 2 ? (IS_FLOAT ? (T)NAN : TLOW) : (T)0;        \
+        for (uint64_t i = 0; i < n; ++i) run = fold_##NAME(run, xform_##NAME(in[i], transform, scale, shift), op); \
+        const T r = fold_##NAME(init, run, op); /* init is the left operand */                            \
+        if (exact) *exact = (double)r;                                                                    \
+        if (abs_sum) *abs_sum = 0;                                                                        \
+        return r;                                                                                         \
+    }
+ORACLE_TRANSFORM_REDUCE(i32, int32_t, uint32_t, 0, INT32_MAX, INT32_MIN)
+ORACLE_TRANSFORM_REDUCE(u32, uint32_t, uint32_t, 0, UINT32_MAX, 0u)
+ORACLE_TRANSFORM_REDUCE(f32, float, uint32_t, 1, FLT_MAX, -FLT_MAX)
+ORACLE_TRANSFORM_REDUCE(i64, int64_t, uint64_t, 0, INT64_MAX, INT64_MIN)
+ORACLE_TRANSFORM_REDUCE(u64, uint64_t, uint64_t, 0, UINT64_MAX, 0ull)
+ORACLE_TRANSFORM_REDUCE(f64, double, uint64_t, 1, DBL_MAX, -DBL_MAX)
+#undef ORACLE_TRANSFORM_REDUCE
+
 /* Floating-point scan in double (reference value for a tolerance check), plus running |x| sums. */
 void oracle_scan_sum_f32(const float* in, double* out, double* abs_out, uint64_t n, int inclusive, float init) {
     double run = init, arun = fabs((double)init);

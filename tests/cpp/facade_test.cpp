@@ -21,6 +21,7 @@
 #include <functional>
 #include <limits>
 #include <numeric>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -236,6 +237,66 @@ void reduce_bench_pattern_int_and_float() {
     EXPECT(result == static_cast<int>(static_cast<uint32_t>(exact)));
     // Any summation order is within n * eps * sum|x| of the exact sum.
     EXPECT(std::fabs(double(fresult) - fexact) <= double(n) * 1.2e-7 * fabs_sum);
+}
+
+// tests/device_reduce_test.cpp:120-173: TransformReduce of the squares with max and init 0 over a shuffled
+// 0..4095, and of 2x + 1 with the sum and init 17 at eight sizes (the transform applied once per item);
+// tests/pr6_review_regression_test.cpp:144-240: Reduce with sum and max, TransformReduce with x + 1,
+// x + 7, 2x, x * x and the identity over i % 7 + 1.
+void reduce_with_operator_and_transform() {
+    auto& e = *g_env;
+    {
+        std::vector<int> a(4096);
+        std::iota(a.begin(), a.end(), 0);
+        std::mt19937 rng(114521);
+        std::shuffle(a.begin(), a.end(), rng);
+        auto in = e.device.create_buffer<int>(a.size());
+        auto out = e.device.create_buffer<int>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<int>(a.size())));
+        CommandList cmd;
+        e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(), a.size(), MaxOp{}, SquareOp{}, 0);
+        int result = 0;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(&result) << synchronize();
+        EXPECT(result == 4095 * 4095);
+    }
+    for (size_t size : {1u, 31u, 256u, 1023u, 1024u, 1025u, 1048577u, 4194304u}) {
+        std::vector<int> a(size);
+        int expected = 17;
+        for (size_t i = 0; i < size; ++i) {
+            a[i] = static_cast<int>(i % 13u) - 6;
+            expected += 2 * a[i] + 1;
+        }
+        auto in = e.device.create_buffer<int>(size);
+        auto out = e.device.create_buffer<int>(1);
+        auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<int>(size)));
+        CommandList cmd;
+        e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(), size, SumOp{}, AffineOp<int>{2, 1}, 17);
+        int result = -12345;
+        e.stream << in.copy_from(luisa::span{a}) << cmd.commit() << out.copy_to(&result) << synchronize();
+        EXPECT(result == expected);
+    }
+    const size_t n = 4097;
+    std::vector<int> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = static_cast<int>(i % 7u) + 1;
+    const int sum = std::accumulate(h.begin(), h.end(), 0);
+    int sum_square = 0;
+    for (int x : h) sum_square += x * x;
+    auto in = e.device.create_buffer<int>(n);
+    auto out = e.device.create_buffer<int>(8);
+    auto temp = e.device.create_buffer<uint>(bytes_to_uint_count(DeviceReduce<>::GetTempStorageBytes<int>(n)));
+    CommandList cmd;
+    e.reduce.Reduce(cmd, temp.view(), in.view(), out.view(0, 1), n, SumOp{}, 0);
+    e.reduce.Reduce(cmd, temp.view(), in.view(), out.view(1, 1), n, MaxOp{}, 0);
+    e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(2, 1), n, SumOp{}, AffineOp<int>{1, 1}, 0);
+    e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(3, 1), n, SumOp{}, AffineOp<int>{1, 7}, 0);
+    e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(4, 1), n, SumOp{}, AffineOp<int>{2, 0}, 0);
+    e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(5, 1), n, SumOp{}, SquareOp{}, 0);
+    e.reduce.TransformReduce(cmd, temp.view(), in.view(), out.view(6, 1), n, SumOp{}, IdentityOp{}, 0);
+    e.reduce.Reduce(cmd, BufferView<uint>{}, BufferView<int>{}, out.view(7, 1), 0u, MinOp{}, -9);  // empty: init
+    std::vector<int> r(8, 0);
+    e.stream << in.copy_from(luisa::span{h}) << cmd.commit() << out.copy_to(luisa::span{r}) << synchronize();
+    EXPECT(r[0] == sum && r[1] == 7 && r[2] == sum + static_cast<int>(n) && r[3] == sum + 7 * static_cast<int>(n));
+    EXPECT(r[4] == 2 * sum && r[5] == sum_square && r[6] == sum && r[7] == -9);
 }
 
 // ---- DeviceScan --------------------------------------------------------------------------------
@@ -1396,6 +1457,7 @@ const std::vector<Case>& cases() {
         {"reduce_empty_writes_init", reduce_empty_writes_init},
         {"reduce_bench_pattern_int_and_float", reduce_bench_pattern_int_and_float},
         {"reduce_min_max_and_arg", reduce_min_max_and_arg},
+        {"reduce_with_operator_and_transform", reduce_with_operator_and_transform},
         {"scan_sums_of_ones", scan_sums_of_ones},
         {"scan_inclusive_init_in_place", scan_inclusive_init_in_place},
         {"scan_double_inclusive_sum", scan_double_inclusive_sum},

@@ -71,6 +71,6 @@ def test_facade_tests_build_and_list_cases():
     subprocess.run(["make", "-s", "-C", str(repo / "tests" / "cpp")], check=True)
     out = subprocess.run([str(repo / "tests" / "cpp" / "bin" / "facade_test"), "--list"], check=True,
                          capture_output=True, text=True).stdout.split()
-    assert len(out) == 39 and "scan_double_inclusive_sum" in out and "radix_double_buffer_selectors" in out and "scan_inclusive_init_in_place" in out
+    assert len(out) == 40 and "reduce_with_operator_and_transform" in out and "scan_double_inclusive_sum" in out and "radix_double_buffer_selectors" in out and "scan_inclusive_init_in_place" in out
     assert "scan_by_key_custom_equality" in out and "reduce_by_key_empty_input" in out
     assert "partition_ordering_and_three_way" in out and "run_length_encode_examples" in out

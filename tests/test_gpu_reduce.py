@@ -239,3 +239,109 @@ def test_min_max_arg_2p28(hip, orc, dev):
     assert int(out.item()) == 5000 and int(idx.item()) == n - 7
     hip.reduce_minmax("min", "i32", d, out, n)
     assert int(out.item()) == -5000
+
+
+# ---- Reduce(op, init) and TransformReduce(op, transform, init) ----------------------------------------
+# device_reduce.h:229-252,491-515: op(init, fold of transform(items)), n == 0 writes init.  Integer
+# results and float min / max (selections) bit-exact against the oracle; float sums within
+# |got - exact| <= rel * (|init| + sum of |terms|), rel 1e-5 (f32) / 1e-12 (f64), the oracle summing in
+# long double.
+NP_OF = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64, "f64": np.float64}
+
+
+def run_transform_reduce(hip, suffix, a, op, transform="identity", scale=0, shift=0, init=0, offset=0):
+    d = to_dev(a) if a.size else torch.empty(1, dtype=torch.int32, device="cuda:0")
+    out = fill_dev(1, a.dtype.itemsize, 0x5A5A5A5A)
+    if transform == "identity" and scale == 0 and shift == 0:
+        hip.reduce_op(op, suffix, d[offset:], out, a.size - offset, init=init)
+    else:
+        hip.transform_reduce(op, transform, suffix, d[offset:], out, a.size - offset, scale=scale, shift=shift,
+                             init=init)
+    return to_host(out, a.dtype, 1)[0]
+
+
+def test_transform_reduce_reference_cases(hip, dev):
+    """tests/device_reduce_test.cpp:120-173 and tests/pr6_review_regression_test.cpp:144-240."""
+    a = np.random.default_rng(114521).permutation(4096).astype(np.int32)
+    assert run_transform_reduce(hip, "i32", a, "max", "square") == 4095 ** 2
+    for size in (1, 31, 256, 1023, 1024, 1025, 1048577, 4194304):
+        x = (np.arange(size) % 13 - 6).astype(np.int32)
+        log(f"transform reduce 2x+1 n={size}")
+        assert run_transform_reduce(hip, "i32", x, "sum", "affine", 2, 1, 17) == \
+            17 + int((2 * x.astype(np.int64) + 1).sum())
+    h = (np.arange(4097) % 7 + 1).astype(np.int32)
+    s, n = int(h.sum()), h.size
+    assert run_transform_reduce(hip, "i32", h, "sum") == s
+    assert run_transform_reduce(hip, "i32", h, "max") == 7
+    assert run_transform_reduce(hip, "i32", h, "sum", "affine", 1, 1) == s + n
+    assert run_transform_reduce(hip, "i32", h, "sum", "affine", 1, 7) == s + 7 * n
+    assert run_transform_reduce(hip, "i32", h, "sum", "affine", 2, 0) == 2 * s
+    assert run_transform_reduce(hip, "i32", h, "sum", "square") == int((h.astype(np.int64) ** 2).sum())
+    assert run_transform_reduce(hip, "i32", h, "sum", "identity", 5, 5) == s
+    for op in ("sum", "min", "max"):
+        assert run_transform_reduce(hip, "i32", np.zeros(0, np.int32), op, "square", init=-9) == -9
+
+
+def _check_transform_reduce(orc, suffix, got, a, op, transform, scale, shift, init):
+    want, exact, absum = orc.transform_reduce(a, op, transform, scale, shift, init)
+    if op == "sum" and suffix in ("f32", "f64"):
+        rel = 1e-5 if suffix == "f32" else 1e-12
+        assert abs(float(got) - exact) <= rel * max(absum, 1e-30), (got, exact)
+    else:
+        assert np.array([got]).view(f"u{a.itemsize}")[0] == np.array([want]).view(f"u{a.itemsize}")[0], (got, want)
+
+
+@pytest.mark.parametrize("suffix", ["i32", "u32", "f32", "i64", "u64", "f64"])
+@pytest.mark.parametrize("n", [1, 17, 4097, 1000003, (1 << 24) + 1])
+def test_transform_reduce_vs_oracle(hip, orc, dev, suffix, n):
+    dtype = NP_OF[suffix]
+    rng = np.random.default_rng(n + len(suffix))
+    if np.dtype(dtype).kind == "f":
+        a = (rng.standard_normal(n) * 100).astype(dtype)
+        a[rng.random(n) < 0.01] = np.nan if n < 5000 else a[0]
+        params = (1.5, -0.25, 3.0)
+    else:
+        info = np.iinfo(dtype)
+        a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        params = (3, 11, 7)
+    log(f"transform reduce {suffix} n={n}")
+    for transform in ("identity", "affine", "square", "abs"):
+        for op in ("sum", "min", "max"):
+            if op == "sum" and np.dtype(dtype).kind == "f" and np.isnan(a).any():
+                continue  # a NaN sum has no tolerance to check against
+            got = run_transform_reduce(hip, suffix, a, op, transform, *params)
+            _check_transform_reduce(orc, suffix, got, a, op, transform, *params)
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_transform_reduce_unaligned_and_float_edges(hip, orc, dev, offset):
+    """Views that start off a 16-byte boundary, float min / max with NaNs (skipped), all-NaN input (init),
+    the initial value as the left operand (of +0.0 and -0.0 init is kept) and a NaN initial value."""
+    rng = np.random.default_rng(offset)
+    a = rng.integers(-1000, 1000, 300_001).astype(np.int32)
+    for op, transform in (("sum", "affine"), ("max", "square"), ("min", "abs")):
+        got = run_transform_reduce(hip, "i32", a, op, transform, 3, -2, 5, offset=offset)
+        _check_transform_reduce(orc, "i32", got, a[offset:], op, transform, 3, -2, 5)
+    z = np.full(100_000, -0.0, np.float32)
+    assert not np.signbit(run_transform_reduce(hip, "f32", z, "min", init=0.0))
+    assert np.signbit(run_transform_reduce(hip, "f32", -z, "max", init=-0.0))
+    assert run_transform_reduce(hip, "f32", np.full(70_000, np.nan, np.float32), "min", init=2.5) == np.float32(2.5)
+    v = rng.standard_normal(90_001)
+    v[::7] = np.nan
+    for op in ("min", "max"):
+        got = run_transform_reduce(hip, "f64", v, op, "square", init=np.nan)
+        _check_transform_reduce(orc, "f64", got, v, op, "square", 0, 0, np.nan)
+
+
+def test_transform_reduce_rejects_unknown_op_and_transform(hip, dev):
+    lib = hip.lib()
+    a = torch.ones(1000, dtype=torch.int32, device=dev)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    temp = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(1000, 4)), dtype=torch.int32, device=dev)
+    tb = temp.numel() * 4
+    assert lib.lcpp_hip_reduce_op_i32(temp.data_ptr(), tb, a.data_ptr(), out.data_ptr(), 1000, 3, 0, None) == \
+        hip.ERR_INVALID_ARGUMENT
+    assert lib.lcpp_hip_transform_reduce_i32(temp.data_ptr(), tb, a.data_ptr(), out.data_ptr(), 1000, 0, 4, 1, 0, 0,
+                                             None) == hip.ERR_INVALID_ARGUMENT
+    torch.cuda.synchronize()
+    assert int(out.item()) == 0

@@ -93,6 +93,101 @@ def test_reduce_sum_f64_closed_forms(orc):
     assert orc.reduce_sum_fp(np.zeros(0, np.float64)) == (0.0, 0.0)
 
 
+# ---- Reduce(op, init) / TransformReduce -------------------------------------------------------------
+def test_transform_reduce_known_answers(orc):
+    """tests/device_reduce_test.cpp:120-173: max of squares over a permutation of 0..4095 with init 0 is
+    4095^2; the sum of 2x + 1 over x = i % 13 - 6 with init 17 at eight sizes.
+    tests/pr6_review_regression_test.cpp:144-240 over i % 7 + 1 (4,097 items): sum and max with init 0,
+    the transforms x + 1, x + 7, 2x, x * x and the identity under the sum."""
+    a = np.random.default_rng(114521).permutation(4096).astype(np.int32)
+    assert orc.transform_reduce(a, "max", "square", init=0)[0] == 4095 ** 2
+    for size in (1, 31, 256, 1023, 1024, 1025, 1048577, 4194304):
+        x = (np.arange(size) % 13 - 6).astype(np.int32)
+        assert orc.transform_reduce(x, "sum", "affine", 2, 1, 17)[0] == 17 + int((2 * x.astype(np.int64) + 1).sum())
+    h = (np.arange(4097) % 7 + 1).astype(np.int32)
+    s, n = int(h.sum()), h.size
+    assert orc.transform_reduce(h, "sum")[0] == s and orc.transform_reduce(h, "max")[0] == 7
+    assert orc.transform_reduce(h, "sum", "affine", 1, 1)[0] == s + n
+    assert orc.transform_reduce(h, "sum", "affine", 1, 7)[0] == s + 7 * n
+    assert orc.transform_reduce(h, "sum", "affine", 2, 0)[0] == 2 * s
+    assert orc.transform_reduce(h, "sum", "square")[0] == int((h.astype(np.int64) ** 2).sum())
+    assert orc.transform_reduce(h, "sum", "identity", 5, 5)[0] == s  # scale / shift unused
+    for op in ("sum", "min", "max"):
+        assert orc.transform_reduce(np.zeros(0, np.int32), op, "square", init=-9)[0] == -9  # empty: init
+
+
+def _numpy_transform(x, transform, scale, shift):
+    """The transform in the item type, wrapping integers through the unsigned type of the same width."""
+    if transform == "identity":
+        return x
+    if x.dtype.kind == "f":
+        with np.errstate(over="ignore", invalid="ignore"):
+            return {"affine": lambda: (x * x.dtype.type(scale)) + x.dtype.type(shift), "square": lambda: x * x,
+                    "abs": lambda: np.abs(x)}[transform]()
+    u = x.view(f"u{x.itemsize}")
+    with np.errstate(over="ignore"):
+        if transform == "affine":
+            r = u * u.dtype.type(np.array(scale).astype(x.dtype).view(u.dtype)) + \
+                u.dtype.type(np.array(shift).astype(x.dtype).view(u.dtype))
+        elif transform == "square":
+            r = u * u
+        else:
+            r = np.where(x < 0, u.dtype.type(0) - u, u) if x.dtype.kind == "i" else u
+    return r.astype(u.dtype).view(x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.uint32, np.float32, np.int64, np.uint64, np.float64])
+def test_transform_reduce_vs_numpy(orc, dtype):
+    """Every operator and transform against an independent numpy formulation: integer sums wrap (uint64
+    numpy sums), min / max are numpy's fmin / fmax (NaN skipped) or minimum / maximum reductions with the
+    initial value as the left operand, float sums within the long double's bound of math.fsum."""
+    rng = np.random.default_rng(np.dtype(dtype).itemsize * 7 + np.dtype(dtype).kind.encode()[0])
+    n = 5003
+    if np.dtype(dtype).kind == "f":
+        x = (rng.standard_normal(n) * 100).astype(dtype)
+        x[rng.random(n) < 0.01] = np.nan
+        params = [(dtype(1.5), dtype(-0.25), dtype(3.0))]
+    else:
+        info = np.iinfo(dtype)
+        x = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        params = [(3, 11, 7), (-5 if info.min < 0 else 2**31 + 3, 0, info.max)]
+    for transform in ("identity", "affine", "square", "abs"):
+        for scale, shift, init in params:
+            y = _numpy_transform(x, transform, scale, shift)
+            for op in ("sum", "min", "max"):
+                got, exact, absum = orc.transform_reduce(x, op, transform, scale, shift, init)
+                if op == "sum" and y.dtype.kind == "f":
+                    if np.isnan(y).any():
+                        assert np.isnan(exact)
+                        continue
+                    assert abs(exact - math.fsum([float(init)] + y.astype(np.float64).tolist())) <= 1e-15 * absum
+                    assert math.isclose(absum, math.fsum([abs(float(init))] + np.abs(y.astype(np.float64)).tolist()),
+                                        rel_tol=1e-15)
+                elif op == "sum":
+                    w = (int(init) + int(y.astype(object).sum())) % (1 << (8 * y.itemsize))
+                    assert int(np.array(got).astype(y.dtype).view(f"u{y.itemsize}")) == w
+                else:
+                    red = (np.fmin if op == "min" else np.fmax) if y.dtype.kind == "f" else \
+                          (np.minimum if op == "min" else np.maximum)
+                    agg = red.reduce(y)
+                    want = red(dtype(init), agg) if not np.isnan(agg) else dtype(init)
+                    assert got == want or (np.isnan(got) and np.isnan(want)), (op, transform)
+
+
+def test_transform_reduce_float_edges(orc):
+    """Min / max: NaN items are skipped, an all-NaN input gives init, the initial value is the left
+    operand (of +0.0 and -0.0, which compare equal, init is kept), and an initial NaN yields the aggregate."""
+    z = np.array([-0.0, -0.0, -0.0], np.float32)
+    assert not np.signbit(orc.transform_reduce(z, "min", init=0.0)[0])
+    assert np.signbit(orc.transform_reduce(-z, "max", init=-0.0)[0])
+    nan = np.full(4, np.nan, np.float32)
+    assert orc.transform_reduce(nan, "min", init=2.5)[0] == np.float32(2.5)
+    v = np.array([3.0, np.nan, -7.0, 1.0], np.float64)
+    assert orc.transform_reduce(v, "min", init=np.nan)[0] == -7.0
+    assert orc.transform_reduce(v, "max", "square", init=0.0)[0] == 49.0
+    assert orc.transform_reduce(v, "max", "abs", init=-1.0)[0] == 7.0
+
+
 # ---- scan ----------------------------------------------------------------------------------------
 @pytest.mark.parametrize("i", [0, 1, 5, 12, 17])
 def test_scan_ones_known_answer(orc, i):
