@@ -193,6 +193,22 @@ int lcpp_hip_scan_max_f32(void* temp, size_t temp_bytes, const float* in, float*
 int lcpp_hip_scan_max_i64(void* temp, size_t temp_bytes, const int64_t* in, int64_t* out, uint64_t n, int inclusive, int use_init, int64_t init, void* stream);
 int lcpp_hip_scan_max_u64(void* temp, size_t temp_bytes, const uint64_t* in, uint64_t* out, uint64_t n, int inclusive, int use_init, uint64_t init, void* stream);
 int lcpp_hip_scan_max_f64(void* temp, size_t temp_bytes, const double* in, double* out, uint64_t n, int inclusive, int use_init, double init, void* stream);
+/* DeviceScan<>::ExclusiveScan / InclusiveScan / InclusiveScanInit with the left projection
+ * op(lhs, rhs) = lhs (the operator of tests/device_scan_test.cpp:129-155 and
+ * tests/scan_optimization_regression_test.cpp:195-205): every output is the scan's first operand, init
+ * when use_init, else in[0]; items compare by bits only.  It does not commute, so it runs the general scan
+ * kernels with their operand order.  An exclusive scan without init returns LCPP_HIP_ERR_INVALID_ARGUMENT
+ * (the operator has no identity).  Temp: lcpp_hip_scan_temp_bytes(n, sizeof(T)). */
+#define LCPP_HIP_DECLARE_SCAN_LEFT(S, T)                                                                          \
+    int lcpp_hip_scan_left_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,     \
+                               int use_init, T init, void* stream);
+LCPP_HIP_DECLARE_SCAN_LEFT(i32, int32_t)
+LCPP_HIP_DECLARE_SCAN_LEFT(u32, uint32_t)
+LCPP_HIP_DECLARE_SCAN_LEFT(f32, float)
+LCPP_HIP_DECLARE_SCAN_LEFT(i64, int64_t)
+LCPP_HIP_DECLARE_SCAN_LEFT(u64, uint64_t)
+LCPP_HIP_DECLARE_SCAN_LEFT(f64, double)
+#undef LCPP_HIP_DECLARE_SCAN_LEFT
 /* ExclusiveSum over uint32 with no temp argument: the same kernels, with their tile status words in a
  * static device array of the library (349,528 bytes per GPU, held until the process ends) instead of
  * caller-provided temp storage, and no allocation of any kind.  No counterpart in the reference: it is

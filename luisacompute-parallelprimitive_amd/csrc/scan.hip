@@ -126,6 +126,28 @@ __device__ __forceinline__ void store_state(uint64_t* states, uint64_t tile, uin
     }
 }
 
+// Left projection, op(a, b) = a: the reference's left-operand lambda (tests/device_scan_test.cpp:129-155,
+// tests/scan_optimization_regression_test.cpp:195-205), an associative operator that does not commute,
+// so its results show the order in which every level of the scan combines operands.  It has no identity;
+// the kernels adjoin one, the all-ones bit pattern (the sentinel): op(a, b) = b when a holds the sentinel,
+// else a.  That monoid gives exactly the left projection whenever the scan's first operand (init, or
+// in[0] without init) is not the sentinel; when it is, every output is the sentinel, which the scan
+// writes directly.
+struct LeftOp {
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr bool is_sentinel(T x) {
+        using U = std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>;
+        return __builtin_bit_cast(U, x) == ~U(0);
+    }
+    template <typename T>
+    __device__ __forceinline__ T operator()(T a, T b) const { return is_sentinel(a) ? b : a; }
+    template <typename T>
+    __host__ __device__ __forceinline__ static constexpr T identity() {
+        using U = std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>;
+        return __builtin_bit_cast(T, ~U(0));
+    }
+};
+
 // Item `idx` of the input, or the operator's identity past the end.
 template <typename T, typename Op>
 __device__ __forceinline__ T load_item(const T* in, uint64_t n, uint64_t idx) {
@@ -242,6 +264,17 @@ __global__ __launch_bounds__(kScanBlock, kScanBlocksPerCu) void scan_kernel(cons
     PhaseClock clk;
     clk.start();
     uint64_t trace_counters = 0;  // look-back steps | spins << 16 | fallback tiles << 32
+
+    if constexpr (std::is_same_v<Op, LeftOp>) {
+        // Inclusive scan without an initial value (init holds the sentinel) of an input whose first item
+        // is the sentinel: every output is the sentinel.  in[0] never changes (an in-place scan writes
+        // in[0] back to out[0]), so every workgroup reads the same value and takes this path alike.
+        if (LeftOp::is_sentinel(init) && LeftOp::is_sentinel(in[0])) {
+            const uint64_t end = tile_base + TILE < n ? tile_base + TILE : n;
+            for (uint64_t i = tile_base + tid; i < end; i += kScanBlock) out[i] = init;
+            return;
+        }
+    }
 
     Vec v[kScanRows];
     if (full) {
@@ -386,7 +419,8 @@ int scan_op(const char* what, void* temp, size_t temp_bytes, const T* in, T* out
 
     const int vector_io = (reinterpret_cast<uintptr_t>(in) % 16 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
     const uint32_t spin_limit = lookback_spin_limit();
-    LaunchScope scope(std::is_same_v<Op, SumOp> ? "scan_sum" : "scan_minmax", stream);
+    LaunchScope scope(std::is_same_v<Op, SumOp> ? "scan_sum" : std::is_same_v<Op, LeftOp> ? "scan_left" : "scan_minmax",
+                      stream);
     if (inclusive)
         scan_kernel<T, true, Op><<<static_cast<unsigned>(tiles), kScanBlock, 0, stream>>>(in, out, n, states, init,
                                                                                         vector_io, spin_limit);
@@ -399,6 +433,32 @@ int scan_op(const char* what, void* temp, size_t temp_bytes, const T* in, T* out
 template <typename T>
 int scan_sum(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, T init, void* stream) {
     return scan_op<T, SumOp>("DeviceScan", temp, temp_bytes, in, out, n, inclusive, init, stream);
+}
+
+// Scan with the left projection.  Exclusive without an initial value is rejected (the operator has no
+// identity; the reference's ExclusiveScan always takes one).  An initial value equal to the sentinel makes
+// every output that value, which a fill writes; everything else runs the scan kernel.
+template <typename T>
+int scan_left(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, bool inclusive, bool use_init, T init,
+              void* stream_ptr) {
+    const char* what = "DeviceScan (left projection)";
+    if (!inclusive && !use_init)
+        return set_error(kInvalidArgument, "%s: the operator has no identity, so an exclusive scan needs an initial value",
+                         what);
+    if (!(use_init && LeftOp::is_sentinel(init)))
+        return scan_op<T, LeftOp>(what, temp, temp_bytes, in, out, n, inclusive, use_init ? init : LeftOp::identity<T>(),
+                                  stream_ptr);
+    if (n > 0xFFFFFFFFull) return set_error(kInvalidArgument, "%s: too many items (%llu > UINT_MAX)", what,
+                                            static_cast<unsigned long long>(n));
+    if (n == 0) return kOk;
+    if (!in || !out) return set_error(kInvalidArgument, "%s: null input or output", what);
+    if (reinterpret_cast<uintptr_t>(out) % sizeof(T) != 0)
+        return set_error(kInvalidArgument, "%s: output not aligned to the element size", what);
+    const size_t needed = scan_needed_bytes(n, sizeof(T));
+    if (!temp || temp_bytes < needed)
+        return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, needed);
+    return launch_fill_u32(reinterpret_cast<uint32_t*>(out), n * sizeof(T) / 4, 0xFFFFFFFFu,
+                           static_cast<hipStream_t>(stream_ptr));
 }
 
 // ---- ExclusiveSum over uint32 with no temp argument and no allocation ------------------------------
@@ -522,6 +582,21 @@ LCPP_HIP_DEFINE_SCAN_MINMAX(i64, int64_t)
 LCPP_HIP_DEFINE_SCAN_MINMAX(u64, uint64_t)
 LCPP_HIP_DEFINE_SCAN_MINMAX(f64, double)
 #undef LCPP_HIP_DEFINE_SCAN_MINMAX
+
+// Left projection: items compare by bits only (floats included).
+#define LCPP_HIP_DEFINE_SCAN_LEFT(S, T, A)                                                                      \
+    int lcpp_hip_scan_left_##S(void* temp, size_t temp_bytes, const T* in, T* out, uint64_t n, int inclusive,   \
+                               int use_init, T init, void* stream) {                                            \
+        return scan_left<A>(temp, temp_bytes, reinterpret_cast<const A*>(in), reinterpret_cast<A*>(out), n,      \
+                            inclusive != 0, use_init != 0, __builtin_bit_cast(A, init), stream);                 \
+    }
+LCPP_HIP_DEFINE_SCAN_LEFT(i32, int32_t, uint32_t)
+LCPP_HIP_DEFINE_SCAN_LEFT(u32, uint32_t, uint32_t)
+LCPP_HIP_DEFINE_SCAN_LEFT(f32, float, uint32_t)
+LCPP_HIP_DEFINE_SCAN_LEFT(i64, int64_t, uint64_t)
+LCPP_HIP_DEFINE_SCAN_LEFT(u64, uint64_t, uint64_t)
+LCPP_HIP_DEFINE_SCAN_LEFT(f64, double, uint64_t)
+#undef LCPP_HIP_DEFINE_SCAN_LEFT
 
 int lcpp_hip_scan_exclusive_sum_u32_noalloc(const uint32_t* in, uint32_t* out, uint64_t n, void* stream) {
     if (n > kNoAllocMaxItems)

@@ -110,7 +110,7 @@ def _declare(lib: C.CDLL) -> None:
         sig(f"lcpp_hip_scan_exclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
         sig(f"lcpp_hip_scan_inclusive_sum_{s}", i32, vp, sz, vp, vp, u64, vp)
         sig(f"lcpp_hip_scan_sum_init_{s}", i32, vp, sz, vp, vp, u64, i32, _CTYPE[s], vp)
-        for op in ("min", "max"):
+        for op in ("min", "max", "left"):
             sig(f"lcpp_hip_scan_{op}_{s}", i32, vp, sz, vp, vp, u64, i32, i32, _CTYPE[s], vp)
     for k in SORT_KEY_SUFFIXES:
         sig(f"lcpp_hip_radix_sort_keys_{k}", i32, vp, sz, vp, vp, u32, u32, u32, i32, vp)
@@ -314,10 +314,11 @@ def scan_sum(suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=Non
 
 def scan_minmax(op: str, suffix: str, d_in, d_out, n: int, inclusive: bool = False, init=None, temp=None,
                 stream=None) -> None:
-    """DeviceScan::ExclusiveScan / InclusiveScan with MinOp (op "min") or MaxOp ("max"); without `init` the
-    operator's identity stands in for it."""
-    if op not in ("min", "max"):
-        raise ValueError(f"scan operator {op!r}: min or max")
+    """DeviceScan::ExclusiveScan / InclusiveScan with MinOp (op "min"), MaxOp ("max") or the left projection
+    ("left", lhs of every pair); without `init` the operator's identity stands in for it (the left projection
+    has none and takes in[0])."""
+    if op not in ("min", "max", "left"):
+        raise ValueError(f"scan operator {op!r}: min, max or left")
     if temp is None:
         temp = _temp(scan_temp_bytes(n, ELEM_BYTES[suffix]), d_in.device)
     tb = temp.numel() * temp.element_size()

@@ -81,6 +81,8 @@ def lib() -> C.CDLL:
             f = getattr(h, f"oracle_transform_reduce_{name}")
             f.restype = ct
             f.argtypes = [vp, u64, i32, i32, ct, ct, ct, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        h.oracle_scan_left.restype = i32
+        h.oracle_scan_left.argtypes = [vp, vp, u64, i32, i32, i32, u64]
         h.oracle_twiddle_in.restype = u64
         h.oracle_twiddle_in.argtypes = [u64, i32, i32, i32]
         h.oracle_radix_digit.restype = u32
@@ -239,6 +241,18 @@ def scan_minmax(op: str, a: np.ndarray, inclusive: bool = False, init=None) -> n
     out = np.empty_like(a)
     getattr(lib(), f"oracle_scan_{op}_{sfx}")(_p(a), _p(out), a.size, int(inclusive), a.dtype.type(init).item())
     return out
+
+
+def scan_left(a: np.ndarray, inclusive: bool = True, init=None) -> np.ndarray:
+    """Scan with the left projection op(lhs, rhs) = lhs over the items' bits (init, when given, is taken
+    in the array's type)."""
+    a = np.ascontiguousarray(a)
+    u = a.view(f"u{a.itemsize}")
+    out = np.empty_like(u)
+    bits = 0 if init is None else int(np.array(init, dtype=a.dtype).view(u.dtype))
+    if lib().oracle_scan_left(_p(u), _p(out), a.size, a.itemsize, int(inclusive), int(init is not None), bits) != 0:
+        raise ValueError("an exclusive left-projection scan needs an initial value")
+    return out.view(a.dtype)
 
 
 REDUCE_OPS = {"sum": 0, "min": 1, "max": 2}

@@ -21,6 +21,14 @@
 #include <string.h>
 #include <math.h>
 
+static uint64_t load_bits_any(const void* p, uint64_t i, int bytes) {
+    return bytes == 4 ? ((const uint32_t*)p)[i] : ((const uint64_t*)p)[i];
+}
+static void store_bits_any(void* p, uint64_t i, int bytes, uint64_t v) {
+    if (bytes == 4) ((uint32_t*)p)[i] = (uint32_t)v;
+    else ((uint64_t*)p)[i] = v;
+}
+
 /* ------------------------------------------------------------------------------------------------
  * Seeded streams.  splitmix64 (Steele, Lea, Flood 2014; the generator of java.util.SplittableRandom):
  * r_i = mix(seed + (i + 1) * 0x9E3779B97F4A7C15).  Known answer: seed 0 gives 0xE220A8397B1DCDAF,
@@ -303,6 +311,23 @@ ORACLE_TRANSFORM_REDUCE(i64, int64_t, uint64_t, 0, INT64_MAX, INT64_MIN)
 ORACLE_TRANSFORM_REDUCE(u64, uint64_t, uint64_t, 0, UINT64_MAX, 0ull)
 ORACLE_TRANSFORM_REDUCE(f64, double, uint64_t, 1, DBL_MAX, -DBL_MAX)
 #undef ORACLE_TRANSFORM_REDUCE
+
+/* Scan with the left projection op(lhs, rhs) = lhs (tests/device_scan_test.cpp:129-155,
+ * tests/scan_optimization_regression_test.cpp:195-205), folded literally left to right over the bits of
+ * 4- or 8-byte items: with init, run = init and every output is op(run, ...) = init; without init an
+ * inclusive scan starts from in[0].  Exclusive without init has no value (the operator has no identity)
+ * and returns -1. */
+int oracle_scan_left(const void* in, void* out, uint64_t n, int item_bytes, int inclusive, int use_init, uint64_t init) {
+    if (!inclusive && !use_init) return -1;
+    uint64_t run = init;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t x = load_bits_any(in, i, item_bytes);
+        if (!inclusive) store_bits_any(out, i, item_bytes, run);
+        run = (i == 0 && !use_init) ? x : run; /* op(run, x) = run */
+        if (inclusive) store_bits_any(out, i, item_bytes, run);
+    }
+    return 0;
+}
 
 /* Floating-point scan in double (reference value for a tolerance check), plus running |x| sums. */
 void oracle_scan_sum_f32(const float* in, double* out, double* abs_out, uint64_t n, int inclusive, float init) {

@@ -381,3 +381,71 @@ def test_scan_minmax_in_place_forced_fallback(hip, orc, dev, forced_fallback):
         d = to_dev(a)
         hip.scan_minmax("min", suffix, d, d, n, inclusive=True)
         assert same_bits(to_host(d, a.dtype), orc.scan_minmax("min", a, inclusive=True))
+
+
+# ---- the left projection op(lhs, rhs) = lhs ------------------------------------------------------------
+# An associative operator that does not commute: every output is the scan's first operand, so any level
+# (lane, wave, row, tile, look-back window, fallback) that combined operands in the wrong order would show.
+# Bit-exact against the oracle's literal left-to-right fold.
+LEFT_DTYPES = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64,
+               "f64": np.float64}
+
+
+def test_scan_left_reference_cases(hip, dev):
+    """tests/device_scan_test.cpp:129-155: ExclusiveScan with lhs and init 42 over 3,841 sevens is 42
+    everywhere.  tests/scan_optimization_regression_test.cpp:195-205: InclusiveScan with lhs over
+    value(i) (i % 7 + 1, times 0.25 for floats) at 16,003 items is in[0] everywhere, for int, uint, float
+    and double."""
+    assert (gpu_scan_minmax(hip, "left", "i32", np.full(3841, 7, np.int32), inclusive=False, init=42) == 42).all()
+    q = np.arange(16003) % 7 + 1
+    for suffix in ("i32", "u32", "f32", "f64"):
+        dt = LEFT_DTYPES[suffix]
+        h = (q * 0.25).astype(dt) if np.dtype(dt).kind == "f" else q.astype(dt)
+        got = gpu_scan_minmax(hip, "left", suffix, h, inclusive=True)
+        assert same_bits(got, np.full(h.size, h[0], dt)), suffix
+
+
+@pytest.mark.parametrize("suffix", ["u32", "f32", "i64", "f64"])
+@pytest.mark.parametrize("n", [1, 31, TILE32 + 1, 3 * TILE32 + 7, (1 << 22) + 77])
+def test_scan_left_vs_oracle(hip, orc, dev, suffix, n):
+    """Random bit patterns with all-ones words among them, a first item that is all ones, and initial values
+    of every kind (an all-ones one too)."""
+    dt = np.dtype(LEFT_DTYPES[suffix])
+    u = np.dtype(f"u{dt.itemsize}")
+    rng = np.random.default_rng(n + dt.itemsize)
+    bits = rng.integers(0, np.iinfo(u).max, n, dtype=u, endpoint=True)
+    bits[rng.random(n) < 0.01] = np.iinfo(u).max
+    a = bits.view(dt)
+    log(f"scan left {suffix} n={n}")
+    ones = np.array([np.iinfo(u).max], u).view(dt)[0]  # a quiet NaN for floats: it survives ctypes
+    first_ones = bits.copy()
+    first_ones[0] = np.iinfo(u).max
+    for x in (a, first_ones.view(dt)):
+        got = gpu_scan_minmax(hip, "left", suffix, x, inclusive=True)
+        assert same_bits(got, orc.scan_left(x, inclusive=True))
+        for init in (dt.type(3), ones, np.array(-7).astype(dt)):
+            for inclusive in (False, True):
+                got = gpu_scan_minmax(hip, "left", suffix, x, inclusive=inclusive, init=init)
+                assert same_bits(got, orc.scan_left(x, inclusive=inclusive, init=init)), (inclusive, init)
+
+
+@pytest.mark.parametrize("suffix", ["u32", "f64"])
+def test_scan_left_forced_fallback_and_in_place(hip, orc, dev, forced_fallback, suffix):
+    """Predecessors computed by the waiting workgroup fold in the owner's order; an in-place scan reads in[0]
+    that the scan writes back unchanged."""
+    n = (1 << 22) + 77
+    dt = LEFT_DTYPES[suffix]
+    a = np.random.default_rng(12).integers(1, 1 << 30, n).astype(dt)
+    for init in (None, dt(9)):
+        got = gpu_scan_minmax(hip, "left", suffix, a, inclusive=True, init=init)
+        assert same_bits(got, orc.scan_left(a, inclusive=True, init=init))
+    d = to_dev(a)
+    hip.scan_minmax("left", suffix, d, d, n, inclusive=True)
+    assert same_bits(to_host(d, a.dtype), np.full(n, a[0], dt))
+
+
+def test_scan_left_exclusive_without_init_is_rejected(hip, dev):
+    a = torch.ones(1000, dtype=torch.int32, device=dev)
+    with pytest.raises(hip.LcppHipError) as e:
+        hip.scan_minmax("left", "i32", a, torch.empty_like(a), 1000, inclusive=False)
+    assert e.value.status == hip.ERR_INVALID_ARGUMENT

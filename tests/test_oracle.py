@@ -222,6 +222,32 @@ def test_scan_sum_f32_exact_fractions(orc):
     assert orc.scan_sum_f32(np.zeros(0, np.float32))[0].size == 0
 
 
+def test_scan_left_projection(orc):
+    """oracle_scan_left against the reference's cases (ExclusiveScan with lhs and init 42 over 3,841 sevens
+    gives 42 everywhere, tests/device_scan_test.cpp:129-155; InclusiveScan with lhs gives in[0] everywhere,
+    tests/scan_optimization_regression_test.cpp:195-205) and itertools.accumulate with the same lambda over
+    the items' bits (NaN payloads, -0.0 and all-ones words included)."""
+    import itertools
+    assert orc.scan_left(np.full(3841, 7, np.int32), inclusive=False, init=42).tolist() == [42] * 3841
+    h = ((np.arange(16003) % 7 + 1) * 0.25).astype(np.float32)
+    assert np.array_equal(orc.scan_left(h), np.full(16003, h[0], np.float32))
+    rng = np.random.default_rng(4)
+    for dt in (np.uint32, np.uint64):
+        bits = rng.integers(0, np.iinfo(dt).max, 500, dtype=dt, endpoint=True)
+        bits[[0, 7, 9]] = np.iinfo(dt).max  # all-ones words are ordinary items
+        left = lambda a, b: a
+        for start in (bits, bits[1:]):
+            assert orc.scan_left(start).tolist() == list(itertools.accumulate(start.tolist(), left))
+            for init in (0, 5, int(np.iinfo(dt).max)):
+                acc = list(itertools.accumulate([init] + start.tolist(), left))
+                assert orc.scan_left(start, inclusive=True, init=dt(init)).tolist() == acc[1:]
+                assert orc.scan_left(start, inclusive=False, init=dt(init)).tolist() == acc[:-1]
+    f = np.array([np.nan, -0.0, 1.0], np.float64)
+    assert np.array_equal(orc.scan_left(f).view(np.uint64), np.full(3, f.view(np.uint64)[0]))
+    with pytest.raises(ValueError):
+        orc.scan_left(np.ones(3, np.int32), inclusive=False)
+
+
 def test_scan_inclusive_init_known_answer(orc):
     # tests/device_scan_test.cpp:288-321: InclusiveScanInit {1,2,3,4} + 10 -> {11,13,16,20}.
     a = np.array([1, 2, 3, 4], np.int32)
