@@ -75,8 +75,9 @@ def time_steps(fn, steps: int, warmup: int) -> Timing:
 
 
 def achievable_copy_gbps(hip, dev, reps: int = 10) -> dict:
-    """1 GiB device-to-device copy by the library's copy kernel (8-byte lanes, one 64 KiB tile per
-    workgroup): the copy rate this GPU reaches in this run, median of `reps`."""
+    """1 GiB device-to-device copy by the library's copy kernel (grid-stride, 32 workgroups per CU, four
+    16-byte non-temporal loads and stores per thread and step, the fastest copy form measured on this GPU):
+    the copy rate this GPU reaches in this run, median of `reps`."""
     import torch
     src = torch.ones(1 << 28, dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
@@ -107,6 +108,49 @@ def kernel_avg_ms(hip, fn, kernel: str, reps: int):
 
 def flush_mall(buf):
     buf.add_(1)  # writes 1 GiB, evicting the 256 MB MALL
+
+
+def graph_call_ms(fn, calls: int, reps: int) -> Timing:
+    """Per-call device time of `fn` with the host out of the loop: `calls` calls recorded into one HIP graph
+    (torch.cuda.CUDAGraph), replayed `reps` times with an event pair around each replay; per call = replay
+    time / calls.  (The calls' kernels then run back to back, as they would in a loop the host outpaces.)"""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in events:
+        e0.record()
+        graph.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    per = [e0.elapsed_time(e1) / calls for e0, e1 in events]
+    del graph
+    return Timing(per)
+
+
+def cold_call_ms(fn, flush_buf, reps: int) -> Timing:
+    """Device time of the whole call (every kernel it launches) after the MALL is flushed: an event pair
+    around each call; the flush before it gives the host time to enqueue the call's launches."""
+    import torch
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in events:
+        flush_mall(flush_buf)
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return Timing([e0.elapsed_time(e1) for e0, e1 in events])
 
 
 TRAFFIC_PROFILE = REPO / "profiles" / "radix_onesweep_sortkeys_2p28_u32.md"
@@ -161,11 +205,20 @@ def extra_reduce(hip, dev, steps, warmup, extra):
     hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
     s = torch.empty(1, dtype=torch.int32, device=dev)
     rt = torch.empty(hip.bytes_to_uint_count(hip.reduce_temp_bytes(m, 4)), dtype=torch.int32, device=dev)
-    hot = time_steps(lambda: hip.reduce_sum("i32", a, s, m, temp=rt), steps, warmup)
-    cold_k, _ = kernel_avg_ms(hip, lambda: (flush_mall(flush), hip.reduce_sum("i32", a, s, m, temp=rt)),
-                              "reduce_sum_partials", 5)
+    call = lambda: hip.reduce_sum("i32", a, s, m, temp=rt)
+    # Per call from the host (one event per step: Python and launch gaps included), per call inside a
+    # HIP graph of 20 calls (device time only), the whole call after a MALL flush, and the floor of the
+    # call's shape: the same two launches (partials + final fold) over 8,192 items, in a graph.
+    hot = time_steps(call, steps, warmup)
+    hot_graph = graph_call_ms(call, 20, 10)
+    cold = cold_call_ms(call, flush, 10)
+    tiny = torch.empty(8192, dtype=torch.int32, device=dev)
+    hip.generate(hip.GEN_I32_PM1000, tiny, 8192, SEED)
+    floor = graph_call_ms(lambda: hip.reduce_sum("i32", tiny, s, 8192, temp=rt), 20, 10)
     extra["reduce_sum_i32_2p24"] = {**hot.fields("ms_hot"), "GBps_hot": rate(4 * m, hot.mean),
-                                    "kernel_ms_cold": round(cold_k, 5), "GBps_cold": rate(4 * m, cold_k)}
+                                    **hot_graph.fields("ms_hot_graph"), "GBps_hot_graph": rate(4 * m, hot_graph.mean),
+                                    **cold.fields("ms_cold"), "GBps_cold": rate(4 * m, cold.mean),
+                                    "ms_two_launch_floor_graph": round(floor.mean, 5)}
     del flush
     # Reduce 2^28 int32 (north-star size).
     m = 1 << 28

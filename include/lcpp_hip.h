@@ -52,8 +52,9 @@ int lcpp_hip_profile_reset(void);
 int lcpp_hip_profile_query(const char* kernel, double* total_ms, uint64_t* launches);
 int lcpp_hip_profile_names(char* buffer, size_t buffer_bytes);
 
-/* Device-to-device copy of `bytes` bytes on `stream` by a library kernel (8-byte lanes when both
- * pointers and the size are 8-byte aligned).  No reference counterpart: the sorts' zero-width
+/* Device-to-device copy of `bytes` bytes on `stream` by a library kernel (16-byte non-temporal lanes
+ * in a grid-stride loop when both pointers and the size are 16-byte aligned, 8-byte lanes when they are
+ * 8-byte aligned, bytes otherwise).  No reference counterpart: the sorts' zero-width
  * case (begin_bit == end_bit) copies with it, and bench.py times it as the achievable copy rate. */
 int lcpp_hip_device_copy(void* dst, const void* src, uint64_t bytes, void* stream);
 
