@@ -10,7 +10,7 @@
 // MI355X design
 //   * Histogram: one read of the keys counts every pass's digits in LDS copies private to each bank
 //     (see histogram_kernel); the bins are scanned once per sort.
-//   * Onesweep tiles: 1024 threads x 16 keys (4-byte keys without values), 1024 x 8 (8-byte keys)
+//   * Onesweep tiles: 1024 threads x 18 keys (4-byte keys without values), 1024 x 8 (8-byte keys)
 //     or 512 x 16 (4-byte keys with values); two workgroups per CU (see geometry_for).  Keys are
 //     loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every load
 //     instruction is one coalesced access and each wave ranks its keys in index order (stability).
@@ -263,8 +263,12 @@ __global__ __launch_bounds__(kHistBlock, (sizeof(K) == 4 ? 8 : 4)) void histogra
     constexpr int PASSES_MAX = sizeof(U);
     constexpr int PER_VEC = 16 / sizeof(U);
     constexpr uint32_t PASS_WORDS = kDigits / 2 * kHistCopies;
-    constexpr int VECS = static_cast<int>(TILE / (PER_VEC * kHistBlock));  // 16-byte loads per thread and tile
-    static_assert(TILE % (PER_VEC * kHistBlock) == 0, "a tile is whole 16-byte steps of the workgroup");
+    // A tile is TILE / PER_VEC 16-byte vectors: VECS loads per thread, the last of them by the first
+    // LAST_THREADS threads only (all of them when the tile is whole 16-byte steps of the workgroup).
+    static_assert(TILE % PER_VEC == 0, "a tile is whole 16-byte vectors");
+    constexpr uint32_t TILE_VECS = TILE / PER_VEC;
+    constexpr int VECS = static_cast<int>((TILE_VECS + kHistBlock - 1) / kHistBlock);
+    constexpr uint32_t LAST_THREADS = TILE_VECS - static_cast<uint32_t>(VECS - 1) * kHistBlock;
     // Slots 0 and 1: the first pass's tile buffers; slot p + 1: pass p >= 1.
     __shared__ uint32_t s_hist[(PASSES_MAX + 1) * PASS_WORDS];
     if constexpr (FULL) passes = PASSES_MAX;
@@ -332,10 +336,15 @@ __global__ __launch_bounds__(kHistBlock, (sizeof(K) == 4 ? 8 : 4)) void histogra
     // Full tiles, software-pipelined: the next tile's loads are issued before this tile is counted, so
     // they are in flight across the barrier and the flush.
     Vec k[VECS], next[VECS];
+    if constexpr (LAST_THREADS < kHistBlock) {
+#pragma unroll
+        for (int e = 0; e < PER_VEC; ++e) next[VECS - 1][e] = U(0);  // not loaded by the other threads
+    }
     if (full_tiles > 0) {
         const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + first);
 #pragma unroll
-        for (int u = 0; u < VECS; ++u) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
+        for (int u = 0; u < VECS; ++u)
+            if (u + 1 < VECS || tid < LAST_THREADS) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
     }
     for (uint32_t j = 0; j < full_tiles; ++j) {
         const uint32_t buf = j & 1u;
@@ -345,12 +354,15 @@ __global__ __launch_bounds__(kHistBlock, (sizeof(K) == 4 ? 8 : 4)) void histogra
         if (j + 1 < full_tiles) {
             const Vec* vkeys = reinterpret_cast<const Vec*>(ukeys + t0 + TILE);
 #pragma unroll
-            for (int u = 0; u < VECS; ++u) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
+            for (int u = 0; u < VECS; ++u)
+                if (u + 1 < VECS || tid < LAST_THREADS) next[u] = __builtin_nontemporal_load(&vkeys[u * kHistBlock + tid]);
         }
 #pragma unroll
         for (int u = 0; u < VECS; ++u)
+            if (u + 1 < VECS || tid < LAST_THREADS) {
 #pragma unroll
-            for (int e = 0; e < PER_VEC; ++e) count(k[u][e], buf);
+                for (int e = 0; e < PER_VEC; ++e) count(k[u][e], buf);
+            }
         // Tile j is counted; the flush of buffer buf ^ 1 (tile j - 1) is finished.
         __syncthreads();
         flush(buf, t0);
@@ -832,9 +844,11 @@ struct Geometry {
     constexpr uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
-// The reordering buffer takes at most 64 KB of LDS, so two workgroups share a CU.  16K-key tiles
-// for 4-byte keys without values, 8K otherwise: a tile carries enough work that the look-back (one
-// cross-XCD round trip per step) stays short relative to the rest of the tile.  1024-thread
+// The reordering buffer takes at most 72 KB of LDS, so two workgroups share a CU's 160 KB.  18K-key
+// tiles for 4-byte keys without values, 8K otherwise: a tile carries enough work that the look-back
+// (one cross-XCD round trip per step), the publish and the digit scan stay short relative to the rest
+// of the tile.  (SortKeys 2^28 u32, first pass also looking back: 2.317 ms with 16 keys per thread,
+// 2.215 with 18, 2.219 with 19, whose 64 VGPRs spill; 20 would leave one workgroup per CU.)  1024-thread
 // workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice the items per thread: every
 // wave's rank is a chain of dependent LDS round trips, and shorter chains on more waves hide them
 // better (SortKeys 2^28 u32 3.04 -> 2.81 ms, SortPairs 2^27 u64 + u32 6.08 -> 5.97 ms on MI355X).
@@ -843,7 +857,7 @@ struct Geometry {
 // with values, whose registers are tighter (SortPairs 2^27 u64 + u32: 6.22 ms with 16, 6.16 with 8
 // or 12, slower with 24; a window that spills runs several times slower).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 16, 32};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 32};
     if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 12 : 32};
     return Geometry{512, 16, 32};
 }
@@ -912,17 +926,21 @@ Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t be
 }
 
 // Histogram workgroups over `len` keys: two per CU for 4-byte keys (64 KB of counters each), one for
-// 8-byte keys; contiguous slices of at most kHistMaxItems keys, whole 16-byte steps of the workgroup.
+// 8-byte keys; contiguous slices of at most kHistMaxItems keys, each a whole number of `granule` keys:
+// 16-byte steps of the workgroup for histogram_kernel, onesweep tiles for histogram_tiles_kernel.
 struct HistPlan {
     uint64_t per;
     unsigned grid;
 };
 template <typename K>
-HistPlan hist_plan(uint32_t len) {
-    constexpr uint32_t hist_step = static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
+constexpr uint32_t hist_step() {
+    return static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
+}
+template <typename K>
+HistPlan hist_plan(uint32_t len, uint32_t granule = hist_step<K>()) {
     const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
-    uint64_t per = ceil_div(ceil_div(len, hist_target), hist_step) * hist_step;
-    per = std::min<uint64_t>(per, kHistMaxItems);
+    uint64_t per = ceil_div(ceil_div(len, hist_target), granule) * granule;
+    per = std::min<uint64_t>(per, kHistMaxItems / granule * granule);
     return HistPlan{per, static_cast<unsigned>(ceil_div(len, per))};
 }
 
@@ -946,15 +964,14 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
     HistPlan hp0{};
     for (uint32_t q = 0; q < L.portions; ++q) {
         const uint32_t len = std::min(L.portion, n - q * L.portion);
-        const HistPlan hp = hist_plan<K>(len);
+        const HistPlan hp = precount ? hist_plan<K>(len, G.tile()) : hist_plan<K>(len);
         const uint64_t per = hp.per;
         const unsigned grid = hp.grid;
         if (q == 0) hp0 = hp;
         LaunchScope scope("radix_histogram", stream);
         // Every portion adds into the totals of portion 0's slots.
         if (precount) {
-            static_assert(static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K)) % G.tile() == 0,
-                          "histogram slices hold whole onesweep tiles");
+            static_assert(G.tile() <= kHistMaxItems, "a histogram slice holds whole onesweep tiles");
             if (full)
                 histogram_tiles_kernel<K, DESC, true, G.tile()><<<grid, kHistBlock, 0, stream>>>(
                     hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, lookback, chunk_sums);
@@ -1076,13 +1093,13 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
         // First-pass offsets from the histogram: 4-byte keys without values (SortKeys 2^28 u32, kernel
         // trace: first pass 586 -> 504 us for 14 us more histogram and 12 us of offset kernels; for 8-byte
         // keys with values both the histogram and the first pass got slower: 737 -> 801 us), one portion,
-        // 16-byte aligned keys (the histogram's slices then hold whole tiles) and room for the
-        // per-workgroup totals.
+        // 16-byte aligned keys (the histogram's slices of whole tiles then load 16-byte vectors) and
+        // room for the per-workgroup totals.
         const void* first_src = db ? (*selector ? db1 : db0) : keys_in;
         const size_t off = align_up(L.total, kViewAlign);
         if (sizeof(K) == 4 && VB == 0 && L.portions == 1 && reinterpret_cast<uintptr_t>(first_src) % 16 == 0 &&
             g_precount.load(std::memory_order_relaxed) &&
-            temp_bytes >= off + static_cast<size_t>(hist_plan<K>(n).grid) * kDigits * 4)
+            temp_bytes >= off + static_cast<size_t>(hist_plan<K>(n, G.tile()).grid) * kDigits * 4)
             L.chunk_off = off;
     }
     if (reinterpret_cast<uintptr_t>(temp) % 4 != 0) return set_error(kInvalidArgument, "%s: temp not 4-byte aligned", what);
