@@ -24,10 +24,12 @@
 //     ticket (a same-address agent-scope atomic serialises at ~11 ns on MI355X).
 //   * Look-back: per-digit counts go to a row of 256 32-bit words per tile: bits 31:30 hold the
 //     status (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics
-//     because the 8 XCDs do not share an L2.  Every 256-thread group of the workgroup walks back
-//     over its own window of 4 or 8 predecessor tiles per step; an entry unpublished after a
-//     bounded spin is counted by the waiting workgroup from that tile's keys and published by
-//     compare-and-swap, so progress never depends on dispatch order.
+//     because the 8 XCDs do not share an L2.  The four waves that own one digit per lane walk back
+//     independently over windows of 32 predecessor tiles per step (lookback_digit), or, for 8-byte
+//     keys with values, every 256-thread group of the workgroup takes its own 4-tile window of each
+//     step; an entry unpublished after a bounded spin is counted by the waiting wave or workgroup
+//     from that tile's keys and published by compare-and-swap, so progress never depends on dispatch
+//     order.
 //   * Keys are reordered by digit in LDS (before the look-back) and written out from LDS in order, so
 //     consecutive lanes write consecutive addresses inside each digit's run.  Pairs move values the
 //     same way after the keys.
@@ -53,15 +55,12 @@ constexpr uint32_t kCountMask = (1u << 30) - 1;
 constexpr uint32_t kMaxPasses = 8;
 // In-wave ranking: the last `ballot_sixteenths` / 16 of a workgroup's waves match digits with ballots
 // (VALU), the others with LDS lane-mask tables (LDS pipe); the test hook selects all-ballot (mode 0),
-// all-table (mode 1) or the default split (mode 2).
+// all-table (mode 1) or the geometry's default split (mode 2, Geometry::ballot_sixteenths).
 constexpr int kRankBallot = 0;
 constexpr int kRankLdsMatch = 1;
 constexpr int kRankMixed = 2;
-// A quarter of the waves on ballots: SortKeys 2^28 u32 2.430 ms, against 2.455 ms with tables only,
-// 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots only (MI355X).
-constexpr uint32_t kMixedBallotSixteenths = 4;
-constexpr uint32_t ballot_sixteenths_for(int mode) {
-    return mode == kRankBallot ? 16u : mode == kRankLdsMatch ? 0u : kMixedBallotSixteenths;
+constexpr uint32_t ballot_sixteenths_for(int mode, uint32_t mixed) {
+    return mode == kRankBallot ? 16u : mode == kRankLdsMatch ? 0u : mixed;
 }
 
 #ifdef LCPP_HIP_PHASE_TRACE
@@ -473,115 +472,126 @@ struct MinOpU32 {
     __device__ __forceinline__ static constexpr T identity() { return ~T(0); }
 };
 
-// Look-back of one wave.  Lane l owns digit d = 64 w + l (w = the wave, one of the four waves that hold
-// the 256 digits) and returns the number of keys with digit d in the tiles before `tile` of this
-// portion: the counts the predecessors published for d, newest first, down to and including the
-// nearest INCLUSIVE entry (tile 0 publishes INCLUSIVE at once, so every walk ends).  Each step loads
-// the entries of WIN consecutive predecessors (one cross-XCD round trip); a window of PARTIAL entries
-// only is summed with min / max / add alone (the status bits 01 of WIN words add up to a multiple of
-// 2^32, as WIN is a multiple of 4).  Waves walk independently, with no barrier.
+// One look-back window of one wave.  Lane l (digit d) loads the entries of the WIN predecessor tiles
+// top, top - 1, ..., top - WIN + 1 (`top` is wave-uniform; entries before tile 0 read as an empty
+// INCLUSIVE entry, so a window that holds tile 0 always stops: tile 0 publishes INCLUSIVE at once) and
+// returns the sum of their counts, newest first, down to and including the lane's nearest INCLUSIVE entry;
+// `stop` says whether the window held one.  A window of PARTIAL entries only is summed with min / max /
+// add alone (the status bits 01 of WIN words add up to a multiple of 2^32, as WIN is a multiple of 4).
+// Lanes with `done` set load and wait for nothing.
 //
 // An entry still unpublished before the lane's nearest INCLUSIVE one is polled; after `spin_limit`
-// polls the wave counts the digits of the newest such tile itself (its 64 digits only, in the wave's
-// 64 words of `s_fb`) and publishes them as PARTIAL by compare-and-swap, so progress never depends on
-// dispatch order.  A predecessor tile is always full (only the last tile is partial).
+// polls the wave counts the digits of the newest such tile itself (its 64 digits d - l .. d - l + 63
+// only, in the wave's 64 words of `s_fb`) and publishes them as PARTIAL by compare-and-swap, so progress
+// never depends on dispatch order.  A predecessor tile is always full (only the last tile is partial).
 template <typename K, bool DESC, int BLOCK, int ITEMS, int WIN>
-__device__ __forceinline__ uint32_t lookback_digit(uint32_t* __restrict__ lookback, uint32_t tile, uint32_t d,
-                                                   const K* __restrict__ keys_in, uint32_t shift, uint32_t mask,
-                                                   uint32_t spin_limit, uint32_t* s_fb, uint32_t& steps,
-                                                   uint32_t& spins_total, uint32_t& fallbacks) {
+__device__ __forceinline__ uint32_t lookback_window(uint32_t* __restrict__ lookback, int32_t top, uint32_t d, bool done,
+                                                    bool& stop, const K* __restrict__ keys_in, uint32_t shift,
+                                                    uint32_t mask, uint32_t spin_limit, uint32_t* s_fb,
+                                                    uint32_t& spins_total, uint32_t& fallbacks) {
     static_assert(WIN % 4 == 0, "WIN * 2^30 must vanish modulo 2^32");
     using U = typename KeyTraits<K>::U;
     constexpr int KIND = KeyTraits<K>::kind;
     constexpr uint32_t TILE = static_cast<uint32_t>(BLOCK) * ITEMS;
     const uint32_t lane = lane_id();
-    uint32_t excl = 0;
-    bool done = false;
-    // Newest predecessor of the window; wave-uniform, so each entry's address is a scalar row base
-    // plus the lane's digit offset.  It never goes below 0: the window holding tile 0 ends every walk.
-    uint32_t top = tile - 1;
+    top = __builtin_amdgcn_readfirstlane(top);
+    // The row addresses are recomputed at each load site rather than kept in registers across the
+    // polling loop (an empty asm statement hides `top` from loop-invariant code motion).
+    asm volatile("" : "+s"(top));
+    uint32_t v[WIN];
+#pragma unroll
+    for (int w = 0; w < WIN; ++w) {
+        v[w] = kFlagInclusive;  // entries before tile 0 stop the walk
+        if (top >= w && !done) v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
+    }
+    uint32_t spins = 0;
+    uint32_t sum = 0;
+    stop = false;
     while (true) {
-        top = __builtin_amdgcn_readfirstlane(top);
-        // The row addresses are recomputed at each load site rather than kept in registers across the
-        // polling loop (an empty asm statement hides `top` from loop-invariant code motion).
-        asm volatile("" : "+s"(top));
-        uint32_t v[WIN];
+        uint32_t lo = v[0], hi = v[0], all = 0;
 #pragma unroll
         for (int w = 0; w < WIN; ++w) {
-            v[w] = kFlagInclusive;  // entries before tile 0 stop the walk
-            if (top >= static_cast<uint32_t>(w) && !done)
-                v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
+            lo = min(lo, v[w]);
+            hi = max(hi, v[w]);
+            all += v[w];
         }
-        uint32_t spins = 0;
-        uint32_t sum = 0;
-        bool stop = false;
-        while (true) {
-            uint32_t lo = v[0], hi = v[0], all = 0;
+        bool wait = false;
+        uint32_t first_wait = ~0u;
+        if (lo >= kFlagPartial && hi < kFlagInclusive) {
+            sum = all;
+            stop = false;
+        } else {
+            sum = 0;
+            stop = false;
 #pragma unroll
             for (int w = 0; w < WIN; ++w) {
-                lo = min(lo, v[w]);
-                hi = max(hi, v[w]);
-                all += v[w];
-            }
-            bool wait = false;
-            uint32_t first_wait = ~0u;
-            if (lo >= kFlagPartial && hi < kFlagInclusive) {
-                sum = all;
-                stop = false;
-            } else {
-                sum = 0;
-                stop = false;
-#pragma unroll
-                for (int w = 0; w < WIN; ++w) {
-                    if (!stop && !wait) {
-                        if ((v[w] & ~kCountMask) == 0) {
-                            wait = true;
-                            first_wait = static_cast<uint32_t>(w);
-                        } else {
-                            sum += v[w] & kCountMask;
-                            stop = (v[w] & kFlagInclusive) != 0;
-                        }
+                if (!stop && !wait) {
+                    if ((v[w] & ~kCountMask) == 0) {
+                        wait = true;
+                        first_wait = static_cast<uint32_t>(w);
+                    } else {
+                        sum += v[w] & kCountMask;
+                        stop = (v[w] & kFlagInclusive) != 0;
                     }
                 }
             }
-            wait = wait && !done;
-            if (wave_ballot(wait) == 0) break;
-            if (spins >= spin_limit) {
-                // Count the newest tile some lane waits for and publish this wave's 64 digits of it
-                // (a compare-and-swap from 0 that loses to the owner's own publication changes
-                // nothing); the reload below then reads it.
-                if constexpr (kPhaseTrace) ++fallbacks;
-                const uint32_t wf = wave_reduce(wait ? first_wait : ~0u, MinOpU32{});
-                const uint64_t jf = top - wf;
-                const uint32_t d0 = d - lane;
-                __hip_atomic_store(&s_fb[lane], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                const U* ukeys = reinterpret_cast<const U*>(keys_in) + jf * TILE;
-                for (uint32_t i = lane; i < TILE; i += kWave) {
-                    const uint32_t dk = digit_of<U, KIND>(twiddle_in<U, KIND, DESC>(ukeys[i]), shift, mask) - d0;
-                    if (dk < kWave) __hip_atomic_fetch_add(&s_fb[dk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-                }
-                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-                const uint32_t cnt = __hip_atomic_load(&s_fb[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-                uint32_t expected = 0;
-                __hip_atomic_compare_exchange_strong(lookback + jf * kDigits + d, &expected, kFlagPartial | cnt,
-                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                __builtin_amdgcn_s_sleep(1);
-                ++spins;
-                if constexpr (kPhaseTrace) ++spins_total;
+        }
+        wait = wait && !done;
+        if (wave_ballot(wait) == 0) break;
+        if (spins >= spin_limit) {
+            // Count the newest tile some lane waits for and publish this wave's 64 digits of it (a
+            // compare-and-swap from 0 that loses to the owner's own publication changes nothing); the
+            // reload below then reads it.
+            if constexpr (kPhaseTrace) ++fallbacks;
+            const uint32_t wf = wave_reduce(wait ? first_wait : ~0u, MinOpU32{});
+            const uint64_t jf = static_cast<uint32_t>(top) - wf;
+            const uint32_t d0 = d - lane;
+            __hip_atomic_store(&s_fb[lane], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            const U* ukeys = reinterpret_cast<const U*>(keys_in) + jf * TILE;
+            for (uint32_t i = lane; i < TILE; i += kWave) {
+                const uint32_t dk = digit_of<U, KIND>(twiddle_in<U, KIND, DESC>(ukeys[i]), shift, mask) - d0;
+                if (dk < kWave) __hip_atomic_fetch_add(&s_fb[dk], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             }
-            asm volatile("" : "+s"(top));
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            const uint32_t cnt = __hip_atomic_load(&s_fb[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+            uint32_t expected = 0;
+            __hip_atomic_compare_exchange_strong(lookback + jf * kDigits + d, &expected, kFlagPartial | cnt,
+                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            __builtin_amdgcn_s_sleep(1);
+            ++spins;
+            if constexpr (kPhaseTrace) ++spins_total;
+        }
+        asm volatile("" : "+s"(top));
 #pragma unroll
-            for (int w = 0; w < WIN; ++w) {
-                if (top >= static_cast<uint32_t>(w) && wait && (v[w] & ~kCountMask) == 0)
-                    v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
-            }
+        for (int w = 0; w < WIN; ++w) {
+            if (top >= w && wait && (v[w] & ~kCountMask) == 0)
+                v[w] = atomic_load_agent(lookback + static_cast<uint64_t>(top - w) * kDigits + d);
         }
-        if (!done) {
-            excl += sum;
-            done = stop;
-        }
+    }
+    return done ? 0u : sum;
+}
+
+// Look-back of one wave.  Lane l owns digit d = 64 w + l (w = the wave, one of the four waves that hold
+// the 256 digits) and returns the number of keys with digit d in the tiles before `tile` of this
+// portion: the counts the predecessors published for d, newest first, down to and including the
+// nearest INCLUSIVE entry.  Each step is one window of WIN consecutive predecessors (one cross-XCD
+// round trip); waves walk independently, with no barrier.
+template <typename K, bool DESC, int BLOCK, int ITEMS, int WIN>
+__device__ __forceinline__ uint32_t lookback_digit(uint32_t* __restrict__ lookback, uint32_t tile, uint32_t d,
+                                                   const K* __restrict__ keys_in, uint32_t shift, uint32_t mask,
+                                                   uint32_t spin_limit, uint32_t* s_fb, uint32_t& steps,
+                                                   uint32_t& spins_total, uint32_t& fallbacks) {
+    uint32_t excl = 0;
+    bool done = false;
+    // Newest predecessor of the window.  It never goes below 0: the window holding tile 0 ends every walk.
+    int32_t top = static_cast<int32_t>(tile) - 1;
+    while (true) {
+        bool stop;
+        excl += lookback_window<K, DESC, BLOCK, ITEMS, WIN>(lookback, top, d, done, stop, keys_in, shift, mask,
+                                                            spin_limit, s_fb, spins_total, fallbacks);
+        done = done || stop;
         if constexpr (kPhaseTrace) ++steps;
         if (wave_ballot(!done) == 0) break;
         top -= WIN;  // some lane has not reached an INCLUSIVE entry, so the window held no tile 0
@@ -589,7 +599,22 @@ __device__ __forceinline__ uint32_t lookback_digit(uint32_t* __restrict__ lookba
     return excl;
 }
 
-template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW>
+// Digit counts of one predecessor tile (always a full tile), by the whole workgroup, into counts[256].
+template <typename K, bool DESC, int BLOCK, int ITEMS>
+__device__ void count_tile_digits(const K* __restrict__ keys, uint32_t tile, uint32_t shift, uint32_t mask,
+                                  uint32_t* counts) {
+    using U = typename KeyTraits<K>::U;
+    constexpr int KIND = KeyTraits<K>::kind;
+    constexpr uint32_t TILE = static_cast<uint32_t>(BLOCK) * ITEMS;
+    for (uint32_t i = threadIdx.x; i < kDigits; i += BLOCK) counts[i] = 0;
+    __syncthreads();
+    const U* ukeys = reinterpret_cast<const U*>(keys) + static_cast<uint64_t>(tile) * TILE;
+    for (uint32_t i = threadIdx.x; i < TILE; i += BLOCK)
+        atomicAdd(&counts[digit_of<U, KIND>(twiddle_in<U, KIND, DESC>(ukeys[i]), shift, mask)], 1u);
+    __syncthreads();
+}
+
+template <typename K, bool DESC, int VB, int BLOCK, int ITEMS, int WINDOW, bool GROUPED>
 // Register budget for two workgroups per CU: BLOCK / 128 waves per SIMD (128 VGPRs at 512 threads,
 // 64 at 1024).
 __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* __restrict__ keys_in,
@@ -622,6 +647,11 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // they are its scratch for the look-back fallback.
     __shared__ uint32_t s_global_minus_local[kDigits];
     __shared__ uint32_t s_scan[kDigits / kWave];
+    // Grouped look-back only: window sums of groups 1 .. and the digits' done flags, the fallback's tile.
+    constexpr int LB_GROUPS = BLOCK / static_cast<int>(kDigits);
+    static_assert(!GROUPED || LB_GROUPS > 1, "the grouped look-back needs at least two groups");
+    __shared__ uint32_t s_lb[GROUPED ? LB_GROUPS : 1][kDigits];
+    __shared__ uint32_t s_lb_tile;
     uint64_t (*s_match)[kDigits] = reinterpret_cast<uint64_t (*)[kDigits]>(s_tile);
     uint32_t (*s_counts)[kDigits] =
         reinterpret_cast<uint32_t (*)[kDigits]>(s_tile + W * kDigits * sizeof(uint64_t));
@@ -761,10 +791,124 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     for (int k = 0; k < ITEMS; ++k) s_keys[rank[k]] = keys[k];
     clk.mark<4>();  // keys reordered in LDS (this wave)
 
-    // Look-back: the four waves that hold one digit per lane walk independently (lookback_digit); the
-    // other waves go straight to the barrier below.
+    // Look-back: either the four waves that hold one digit per lane walk independently (lookback_digit;
+    // the other waves go straight to the barrier below) or the whole workgroup walks, in LB_GROUPS groups
+    // of four waves, workgroup-synchronous (written out here: as a separate inlined function the same
+    // steps measured 2 % slower on SortPairs 2^27).
+    //
+    // Grouped look-back.  Thread t takes digit t % 256 in group g = t / 256.  Each step covers LB_GROUPS *
+    // WINDOW predecessors: group g loads the WINDOW tiles just older than group g - 1's, so every thread
+    // holds WINDOW entries and all of a step's loads are in flight together (one cross-XCD round trip per
+    // step).  The workgroup polls until no thread waits for an unpublished entry before its window's
+    // nearest INCLUSIVE one (entries past it may stay unpublished; older tiles publish without waiting on
+    // this one); each group sums its window down to that entry, and group 0 chains the sums, newest
+    // window first, up to a window that stopped.  An entry still unpublished after `spin_limit` polls is
+    // counted by the workgroup from its tile's keys (the newest such tile of any thread) and published as
+    // PARTIAL by compare-and-swap.  s_lb rows 0 .. LB_GROUPS - 2 carry the window sums of groups 1 ..
+    // (bit 31: the window stopped), row LB_GROUPS - 1 the digits' done flags.
     uint32_t excl = 0;
-    if (!precomputed && tile > 0 && tid < kDigits) {
+    if constexpr (GROUPED) {
+        if (!precomputed && tile > 0) {
+            const uint32_t grp = tid / kDigits;
+            const uint32_t ld = tid % kDigits;  // look-back digit of this thread
+            bool done = false;                  // the same in every group: group 0 decides
+            int64_t top = static_cast<int64_t>(tile) - 1;  // newest predecessor not yet consumed
+            uint32_t* const column = lookback + ld;
+            while (true) {
+                const int64_t gtop = top - static_cast<int64_t>(grp) * WINDOW;  // this group's newest
+                uint32_t v[WINDOW];
+#pragma unroll
+                for (int w = 0; w < WINDOW; ++w) {
+                    const int64_t j = gtop - w;
+                    v[w] = (!done && j >= 0) ? atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]) : 0u;
+                }
+                uint32_t spins = 0;
+                while (true) {
+                    // Newest unpublished entry of the window before its nearest INCLUSIVE one (and not
+                    // past tile 0).
+                    int waiting = -1;
+                    bool scanning = !done;
+#pragma unroll
+                    for (int w = 0; w < WINDOW; ++w) {
+                        const bool live = scanning && gtop - w >= 0;
+                        if (live && (v[w] & ~kCountMask) == 0) waiting = w;
+                        scanning = live && (v[w] & ~kCountMask) != 0 && (v[w] & kFlagInclusive) == 0;
+                    }
+                    if (!__syncthreads_or(waiting >= 0)) break;
+                    if (spins >= spin_limit) {
+                        if constexpr (kPhaseTrace) ++trace_fallbacks;
+                        if (tid == 0) s_lb_tile = 0;
+                        __syncthreads();
+                        if (waiting >= 0) atomicMax(&s_lb_tile, static_cast<uint32_t>(gtop - waiting) + 1u);
+                        __syncthreads();
+                        const uint32_t jf = s_lb_tile - 1u;
+                        count_tile_digits<K, DESC, BLOCK, ITEMS>(keys_in, jf, shift, mask, s_global_minus_local);
+                        const int wf = static_cast<int>(gtop - static_cast<int64_t>(jf));
+                        if (!done) {
+#pragma unroll
+                            for (int w = 0; w < WINDOW; ++w) {
+                                if (w == wf && (v[w] & ~kCountMask) == 0) {
+                                    // A compare-and-swap from 0 that loses to the owner's publication reads it.
+                                    uint32_t expected = 0;
+                                    const uint32_t desired = kFlagPartial | s_global_minus_local[ld];
+                                    v[w] = __hip_atomic_compare_exchange_strong(
+                                               &column[static_cast<uint64_t>(jf) * kDigits], &expected, desired,
+                                               __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                               ? desired
+                                               : expected;
+                                }
+                            }
+                        }
+                        continue;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    ++spins;
+                    if constexpr (kPhaseTrace) ++trace_spins;
+                    if (!done) {
+#pragma unroll
+                        for (int w = 0; w < WINDOW; ++w) {
+                            const int64_t j = gtop - w;
+                            if (j >= 0 && (v[w] & ~kCountMask) == 0)
+                                v[w] = atomic_load_agent(&column[static_cast<uint64_t>(j) * kDigits]);
+                        }
+                    }
+                }
+                // The window's sum down to and including its nearest INCLUSIVE entry (tile 0's is INCLUSIVE).
+                uint32_t window_sum = 0;
+                bool window_stops = false;
+                if (!done) {
+#pragma unroll
+                    for (int w = 0; w < WINDOW; ++w) {
+                        if (!window_stops && gtop - w >= 0) {
+                            window_sum += v[w] & kCountMask;
+                            if ((v[w] & kFlagInclusive) || gtop - w == 0) window_stops = true;
+                        }
+                    }
+                }
+                if (grp > 0) s_lb[grp - 1][ld] = window_sum | (window_stops ? 0x80000000u : 0u);
+                __syncthreads();
+                if (grp == 0 && !done) {
+#pragma unroll
+                    for (int g = 1; g < LB_GROUPS; ++g) {
+                        if (window_stops) break;
+                        const uint32_t x = s_lb[g - 1][ld];
+                        window_sum += x & 0x7FFFFFFFu;
+                        window_stops = (x >> 31) != 0;
+                    }
+                    excl += window_sum;
+                    done = window_stops;
+                    s_lb[LB_GROUPS - 1][ld] = done ? 1u : 0u;
+                }
+                if constexpr (kPhaseTrace) ++trace_steps;
+                const bool more = __syncthreads_or(grp == 0 && !done);
+                if (grp > 0) done = s_lb[LB_GROUPS - 1][ld] != 0;
+                if (!more) break;
+                top -= static_cast<int64_t>(LB_GROUPS) * WINDOW;
+            }
+            clk.mark<5>();  // look-back walked (wave 0)
+            if (tid < kDigits) atomic_store_agent(&lookback[tile * kDigits + d], kFlagInclusive | (excl + real));
+        }
+    } else if (!precomputed && tile > 0 && tid < kDigits) {
         excl = lookback_digit<K, DESC, BLOCK, ITEMS, WINDOW>(lookback, tile, d, keys_in, shift, mask, spin_limit,
                                                              &s_global_minus_local[wave * kWave], trace_steps,
                                                              trace_spins, trace_fallbacks);
@@ -840,7 +984,9 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
 struct Geometry {
     int block;
     int items;
-    int window;  // predecessor tiles per 256-thread group and look-back step
+    int window;    // predecessor tiles per 256-thread group and look-back step
+    bool grouped;  // look-back by the whole workgroup (lookback_groups) rather than the four digit waves
+    uint32_t ballot_sixteenths;  // waves ranked by ballots, in sixteenths of the workgroup (default mode)
     constexpr uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
@@ -853,13 +999,21 @@ struct Geometry {
 // wave's rank is a chain of dependent LDS round trips, and shorter chains on more waves hide them
 // better (SortKeys 2^28 u32 3.04 -> 2.81 ms, SortPairs 2^27 u64 + u32 6.08 -> 5.97 ms on MI355X).
 // 4-byte keys with values keep 512 threads: their keys, values, ranks and output positions do not
-// fit 64 VGPRs.  Look-back window (predecessor tiles per step and lane): 32, except 12 for 8-byte keys
-// with values, whose registers are tighter (SortPairs 2^27 u64 + u32: 6.22 ms with 16, 6.16 with 8
-// or 12, slower with 24; a window that spills runs several times slower).
+// fit 64 VGPRs.  Look-back: the four digit waves walk 32-tile windows independently, except for 8-byte
+// keys with values, whose tiles are half as long and whose registers are tighter: there the whole
+// workgroup walks, four groups of 4-tile windows per step, and every wave ranks by ballots (SortPairs
+// 2^27 u64 + u32 uniform / AND-of-3 keys: 6.19 / 5.82 ms with the digit waves' 12-tile windows and a
+// quarter of the waves on ballots, 6.01 / 5.64 ms grouped with ballots only; grouped windows of 8 or 12
+// tiles per group 6.24 / 6.47 ms).  The grouped walk measured slower for 8-byte keys without values
+// (SortKeys 2^27 u64 4.61 against 4.51 ms) and for 4-byte keys with values (SortPairs 2^27 u32 + u32
+// 2.48 against 2.41 ms).  Ballot ranking costs more VALU per key than the LDS tables but has no bank
+// conflicts, which skewed digits (few distinct values per wave) make heavy in the tables.  SortKeys of
+// 4-byte keys ranks a quarter of the waves by ballots (2^28 u32 2.430 ms, against 2.455 ms with tables
+// only, 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots only).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 32};
-    if (key_bytes == 8) return Geometry{1024, 8, value_bytes ? 12 : 32};
-    return Geometry{512, 16, 32};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 32, false, 4};
+    if (key_bytes == 8) return value_bytes ? Geometry{1024, 8, 4, true, 16} : Geometry{1024, 8, 32, false, 4};
+    return Geometry{512, 16, 32, false, 4};
 }
 
 template <typename K, int VB>
@@ -1047,9 +1201,9 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
-            onesweep_kernel<K, DESC, VB, G.block, G.items, G.window><<<tiles, G.block, 0, stream>>>(
+            onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, G.grouped><<<tiles, G.block, 0, stream>>>(
                 src + qoff, dst, vs, vdst, len, offsets, next, lookback, pre ? lookback : nullptr, shift, nb, n,
-                L.spin_limit, ballot_sixteenths_for(L.rank_mode));
+                L.spin_limit, ballot_sixteenths_for(L.rank_mode, G.ballot_sixteenths));
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
