@@ -10,10 +10,11 @@
 // MI355X design
 //   * Histogram: one read of the keys counts every pass's digits in LDS copies private to each bank
 //     (see histogram_kernel); the bins are scanned once per sort.
-//   * Onesweep tiles: 1024 threads x 18 keys (4-byte keys without values), 1024 x 8 (8-byte keys)
-//     or 512 x 16 (4-byte keys with values); two workgroups per CU (see geometry_for).  Keys are
-//     loaded wave-striped (item k of lane l of wave w is tile[w*64*ITEMS + k*64 + l]), so every load
-//     instruction is one coalesced access and each wave ranks its keys in index order (stability).
+//   * Onesweep tiles: 1024 threads x 18 keys (4-byte keys without values), 1024 x 9 (8-byte keys)
+//     or 512 x 28 / 512 x 18 (4-byte keys with 4- / 8-byte values); two workgroups per CU (see
+//     geometry_for).  Keys are loaded wave-striped (item k of lane l of wave w is
+//     tile[w*64*ITEMS + k*64 + l]), so every load instruction is one coalesced access and each wave
+//     ranks its keys in index order (stability).
 //   * Rank: per wave and round, the 64-bit mask of lanes holding the same digit comes from an LDS
 //     table of lane masks (every lane ORs its bit into its digit's entry and reads it back) or, as an
 //     alternative, from 8 ballots; the rank is the wave's running count of the digit plus the
@@ -990,30 +991,36 @@ struct Geometry {
     constexpr uint32_t tile() const { return static_cast<uint32_t>(block) * items; }
 };
 
-// The reordering buffer takes at most 72 KB of LDS, so two workgroups share a CU's 160 KB.  18K-key
-// tiles for 4-byte keys without values, 8K otherwise: a tile carries enough work that the look-back
-// (one cross-XCD round trip per step), the publish and the digit scan stay short relative to the rest
-// of the tile.  (SortKeys 2^28 u32, first pass also looking back: 2.317 ms with 16 keys per thread,
-// 2.215 with 18, 2.219 with 19, whose 64 VGPRs spill; 20 would leave one workgroup per CU.)  1024-thread
-// workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice the items per thread: every
-// wave's rank is a chain of dependent LDS round trips, and shorter chains on more waves hide them
-// better (SortKeys 2^28 u32 3.04 -> 2.81 ms, SortPairs 2^27 u64 + u32 6.08 -> 5.97 ms on MI355X).
-// 4-byte keys with values keep 512 threads: their keys, values, ranks and output positions do not
-// fit 64 VGPRs.  Look-back: the four digit waves walk 32-tile windows independently, except for 8-byte
-// keys with values, whose tiles are half as long and whose registers are tighter: there the whole
-// workgroup walks, four groups of 4-tile windows per step, and every wave ranks by ballots (SortPairs
-// 2^27 u64 + u32 uniform / AND-of-3 keys: 6.19 / 5.82 ms with the digit waves' 12-tile windows and a
-// quarter of the waves on ballots, 6.01 / 5.64 ms grouped with ballots only; grouped windows of 8 or 12
-// tiles per group 6.24 / 6.47 ms).  The grouped walk measured slower for 8-byte keys without values
-// (SortKeys 2^27 u64 4.61 against 4.51 ms) and for 4-byte keys with values (SortPairs 2^27 u32 + u32
-// 2.48 against 2.41 ms).  Ballot ranking costs more VALU per key than the LDS tables but has no bank
-// conflicts, which skewed digits (few distinct values per wave) make heavy in the tables.  SortKeys of
-// 4-byte keys ranks a quarter of the waves by ballots (2^28 u32 2.430 ms, against 2.455 ms with tables
-// only, 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots only).
+// Tiles are as large as two workgroups per CU allow (the reordering buffer holds the tile's widest
+// items: at most 77 KB of LDS each out of the CU's 160 KB, within the register budget of
+// __launch_bounds__): the look-back (one cross-XCD round trip per step), the publish and the digit scan
+// cost the same per tile whatever its length, so fewer, longer tiles spread them over more keys.
+//   * 4-byte keys without values: 1024 x 18 (SortKeys 2^28 u32 with the first pass looking back: 2.317 ms
+//     with 16 keys per thread, 2.215 with 18, 2.219 with 19, whose 64 VGPRs spill; 20 would leave one
+//     workgroup per CU).  1024-thread workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice
+//     the items per thread: every wave's rank is a chain of dependent LDS round trips, and shorter chains
+//     on more waves hide them better (SortKeys 2^28 u32 3.04 -> 2.81 ms when measured).
+//   * 8-byte keys: 1024 x 9 (SortKeys 2^27 u64 4.52 -> 4.31 ms, SortPairs 2^27 u64 + u32 5.98 -> 5.92 ms
+//     against 1024 x 8).
+//   * 4-byte keys with 4-byte values: 512 x 28, 128 VGPRs (SortPairs 2^27 u32 + u32: 2.42 ms at
+//     512 x 16, 2.21 at 512 x 24, 2.14 at 512 x 28; 768 x 16 spills); with 8-byte values 512 x 18, whose
+//     72 KB of values fit beside the other workgroup's (SortPairs 2^27 u32 + u64: 3.36 -> 3.28 ms).
+// Look-back: the four digit waves walk 32-tile windows independently, except for 8-byte keys with
+// values, whose tiles are the shortest and whose registers are tighter: there the whole workgroup walks,
+// four groups of 4-tile windows per step, and every wave ranks by ballots (SortPairs 2^27 u64 + u32
+// uniform / AND-of-3 keys, 8 pairs per thread: 6.19 / 5.82 ms with the digit waves' 12-tile windows and
+// a quarter of the waves on ballots, 6.01 / 5.64 ms grouped with ballots only; grouped windows of 8 or
+// 12 tiles per group 6.24 / 6.47 ms).  The grouped walk measured slower for 8-byte keys without values
+// (SortKeys 2^27 u64 4.61 against 4.51 ms), for 4-byte keys with values (SortPairs 2^27 u32 + u32 2.48
+// against 2.41 ms) and for SortKeys of 4-byte keys (2.38-2.51 against 2.20 ms).  Ballot ranking costs
+// more VALU per key than the LDS tables but has no bank conflicts, which skewed digits (few distinct
+// values per wave) make heavy in the tables.  SortKeys of 4-byte keys ranks a quarter of the waves by
+// ballots (2^28 u32 2.430 ms, against 2.455 ms with tables only, 2.440 ms with half, 2.481 ms with 10/16
+// and 2.563 ms with ballots only).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
     if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 32, false, 4};
-    if (key_bytes == 8) return value_bytes ? Geometry{1024, 8, 4, true, 16} : Geometry{1024, 8, 32, false, 4};
-    return Geometry{512, 16, 32, false, 4};
+    if (key_bytes == 8) return value_bytes ? Geometry{1024, 9, 4, true, 16} : Geometry{1024, 9, 32, false, 4};
+    return value_bytes > 4 ? Geometry{512, 18, 32, false, 4} : Geometry{512, 28, 32, false, 4};
 }
 
 template <typename K, int VB>

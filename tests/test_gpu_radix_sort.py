@@ -213,7 +213,11 @@ def test_multi_portion_carry(hip, orc, dev, kdtype, vbytes, descending):
     try:
         lib.lcpp_hip_radix_set_portion_limit(tile * 3)
         need = lib.lcpp_hip_internal_radix_needed_bytes(n, keys.itemsize, vbytes, 0, keys.itemsize * 8, 0)
-        assert lib.lcpp_hip_internal_radix_portions(n, keys.itemsize, vbytes, 0, keys.itemsize * 8, 0, need) == 4
+        # The limit rounds down to whole tiles of this key / value type (4 or 5 portions here).
+        kv_tile = lib.lcpp_hip_radix_tile_items(keys.itemsize, vbytes)
+        portion = max(tile * 3 // kv_tile, 1) * kv_tile
+        portions = lib.lcpp_hip_internal_radix_portions(n, keys.itemsize, vbytes, 0, keys.itemsize * 8, 0, need)
+        assert portions == -(-n // portion) and portions >= 4
         temp = torch.empty((need + 3) // 4, dtype=torch.int32, device=dev)
         sfx = SUFFIX[keys.dtype]
         kin, kout = to_dev(keys), empty_dev(n, keys.itemsize)
