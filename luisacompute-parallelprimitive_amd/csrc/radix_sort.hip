@@ -708,10 +708,11 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // Rank inside the wave: rank = keys of the same digit in earlier rounds (the wave's LDS counter)
     // + lanes of the same digit below this lane in this round.  The highest such lane advances the
     // counter.  The peer mask comes from 8 ballots (ballot waves) or from an LDS table of 64-bit lane
-    // masks, one per digit (table waves): every lane ORs its bit into its digit's
-    // entry, reads the entry back (all ORs of the instruction have landed: a wave's LDS operations
-    // complete in issue order), and the highest peer clears it.  OR is order-independent, so the mask
-    // does not depend on how the hardware serialises conflicting lanes.
+    // masks, one per digit (table waves): every lane ORs its bit into its half-wave's 32-bit word of its
+    // digit's entry (one bank per lane rather than two: SortKeys 2^28 u32 2.203 -> 2.182 ms against a
+    // 64-bit OR), reads the whole entry back (all ORs of the instruction have landed: a wave's LDS
+    // operations complete in issue order), and the highest peer clears it.  OR is order-independent, so
+    // the mask does not depend on how the hardware serialises conflicting lanes.
     uint32_t rank[ITEMS];
     // Mixed ranking splits the work between the LDS pipe (tables) and the VALU (ballots); the choice is
     // per wave, so the branch is uniform.
@@ -719,12 +720,14 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
     // they take the faster table ranking.
     const bool table_rank = (W - 1 - __builtin_amdgcn_readfirstlane(wave)) * 16 >= ballot_sixteenths * W;
     if (table_rank) {
-        const uint64_t lane_bit = 1ull << lane;
+        const uint32_t half_bit = 1u << (lane & 31u);
+        const uint32_t half = lane >> 5;
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
             const uint32_t d = digit_bits<U, KIND>(keys[k], shift, num_bits);
             uint64_t* slot = &s_match[wave][d];
-            __hip_atomic_fetch_or(slot, lane_bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(slot) + half, half_bit, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP);
             __builtin_amdgcn_wave_barrier();
             const uint64_t peers = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             const uint32_t base = s_counts[wave][d];
