@@ -26,9 +26,9 @@
 //   * Look-back: per-digit counts go to a row of 256 32-bit words per tile: bits 31:30 hold the
 //     status (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics
 //     because the 8 XCDs do not share an L2.  The four waves that own one digit per lane walk back
-//     independently over windows of 32 predecessor tiles per step (lookback_digit), or, for 8-byte
-//     keys with values, every 256-thread group of the workgroup takes its own 4-tile window of each
-//     step; an entry unpublished after a bounded spin is counted by the waiting wave or workgroup
+//     independently over windows of 8 or 16 predecessor tiles per step (lookback_digit), or, for
+//     8-byte keys with values, every 256-thread group of the workgroup takes its own 2-tile window of
+//     each step; an entry unpublished after a bounded spin is counted by the waiting wave or workgroup
 //     from that tile's keys and published by compare-and-swap, so progress never depends on dispatch
 //     order.
 //   * Keys are reordered by digit in LDS (before the look-back) and written out from LDS in order, so
@@ -1008,22 +1008,29 @@ struct Geometry {
 //   * 4-byte keys with 4-byte values: 512 x 28, 128 VGPRs (SortPairs 2^27 u32 + u32: 2.42 ms at
 //     512 x 16, 2.21 at 512 x 24, 2.14 at 512 x 28; 768 x 16 spills); with 8-byte values 512 x 18, whose
 //     72 KB of values fit beside the other workgroup's (SortPairs 2^27 u32 + u64: 3.36 -> 3.28 ms).
-// Look-back: the four digit waves walk 32-tile windows independently, except for 8-byte keys with
-// values, whose tiles are the shortest and whose registers are tighter: there the whole workgroup walks,
-// four groups of 4-tile windows per step, and every wave ranks by ballots (SortPairs 2^27 u64 + u32
-// uniform / AND-of-3 keys, 8 pairs per thread: 6.19 / 5.82 ms with the digit waves' 12-tile windows and
-// a quarter of the waves on ballots, 6.01 / 5.64 ms grouped with ballots only; grouped windows of 8 or
-// 12 tiles per group 6.24 / 6.47 ms).  The grouped walk measured slower for 8-byte keys without values
-// (SortKeys 2^27 u64 4.61 against 4.51 ms), for 4-byte keys with values (SortPairs 2^27 u32 + u32 2.48
-// against 2.41 ms) and for SortKeys of 4-byte keys (2.38-2.51 against 2.20 ms).  Ballot ranking costs
-// more VALU per key than the LDS tables but has no bank conflicts, which skewed digits (few distinct
-// values per wave) make heavy in the tables.  SortKeys of 4-byte keys ranks a quarter of the waves by
-// ballots (2^28 u32 2.430 ms, against 2.455 ms with tables only, 2.440 ms with half, 2.481 ms with 10/16
-// and 2.563 ms with ballots only).
+// Look-back: the four digit waves walk windows of WINDOW tiles independently, except for 8-byte keys
+// with values, whose tiles are the shortest and whose registers are tighter: there the whole workgroup
+// walks, four groups of WINDOW-tile windows per step, and every wave ranks by ballots.  Short windows
+// win: a step waits for every unpublished entry of its window up to the nearest INCLUSIVE one, so a
+// long window waits on predecessors that a shorter first step would not have needed, and it loads more
+// rows per step.  SortKeys 2^28 u32 (digit waves): 2.06 ms with 4-tile windows, 2.05 with 8, 2.08 with
+// 12, 2.09 with 16, 2.17-2.20 with 32 (20 and 24 spill).  SortKeys 2^27 u64: 4.17 ms with 8, 4.15 with
+// 16, 4.33 with 32.  SortPairs 2^27 u32 + u32: 2.03 ms with 8, 2.07 with 16, 2.13 with 32; u32 + u64:
+// 3.12 with 8, 3.28 with 32.  SortPairs 2^27 u64 + u32 uniform / AND-of-3 keys (grouped): 6.17 / 6.02
+// ms with 1-tile windows per group, 5.83 / 5.48 with 2, 5.93 / 5.58 with 3 or 4, 6.15 / 5.82 with 6
+// (at 8 pairs per thread: digit waves with 12-tile windows and a quarter of the waves on ballots 6.19 /
+// 5.82 ms, grouped 4-tile windows with ballots only 6.01 / 5.64).  The grouped walk measured slower for
+// 8-byte keys without values (SortKeys 2^27 u64 4.61 against 4.51 ms), for 4-byte keys with values
+// (SortPairs 2^27 u32 + u32 2.48 against 2.41 ms) and for SortKeys of 4-byte keys (2.38-2.51 against
+// 2.20 ms), each against 32-tile digit-wave windows.  Ballot ranking costs more VALU per key than the
+// LDS tables but has no bank conflicts, which skewed digits (few distinct values per wave) make heavy in
+// the tables.  SortKeys of 4-byte keys ranks a quarter of the waves by ballots (2^28 u32 2.430 ms,
+// against 2.455 ms with tables only, 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots
+// only, at 16-key tiles).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 32, false, 4};
-    if (key_bytes == 8) return value_bytes ? Geometry{1024, 9, 4, true, 16} : Geometry{1024, 9, 32, false, 4};
-    return value_bytes > 4 ? Geometry{512, 18, 32, false, 4} : Geometry{512, 28, 32, false, 4};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 8, false, 4};
+    if (key_bytes == 8) return value_bytes ? Geometry{1024, 9, 2, true, 16} : Geometry{1024, 9, 16, false, 4};
+    return value_bytes > 4 ? Geometry{512, 18, 8, false, 4} : Geometry{512, 28, 8, false, 4};
 }
 
 template <typename K, int VB>
