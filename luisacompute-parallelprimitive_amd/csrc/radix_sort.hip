@@ -1024,11 +1024,13 @@ struct Geometry {
 // (SortPairs 2^27 u32 + u32 2.48 against 2.41 ms) and for SortKeys of 4-byte keys (2.38-2.51 against
 // 2.20 ms), each against 32-tile digit-wave windows.  Ballot ranking costs more VALU per key than the
 // LDS tables but has no bank conflicts, which skewed digits (few distinct values per wave) make heavy in
-// the tables.  SortKeys of 4-byte keys ranks a quarter of the waves by ballots (2^28 u32 2.430 ms,
-// against 2.455 ms with tables only, 2.440 ms with half, 2.481 ms with 10/16 and 2.563 ms with ballots
-// only, at 16-key tiles).
+// the tables.  SortKeys of 4-byte keys ranks half of the waves by ballots (2^28 u32 with 8-tile windows:
+// 2.083 ms with 2/16, 2.063-2.072 with 4/16, 2.056 with 6/16, 2.041-2.050 with 8/16, 2.064 with 10/16;
+// at 16-key tiles and 32-tile windows a quarter was best: 2.430 ms, against 2.455 ms with tables only and
+// 2.563 ms with ballots only).  SortPairs of 8-byte keys keeps ballots only (5.82 / 5.48 ms uniform /
+// AND-of-3, against 5.85 / 5.51 with half and 5.84 / 5.62 with a quarter).
 constexpr Geometry geometry_for(size_t key_bytes, size_t value_bytes) {
-    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 8, false, 4};
+    if (key_bytes <= 4 && value_bytes == 0) return Geometry{1024, 18, 8, false, 8};
     if (key_bytes == 8) return value_bytes ? Geometry{1024, 9, 2, true, 16} : Geometry{1024, 9, 16, false, 4};
     return value_bytes > 4 ? Geometry{512, 18, 8, false, 4} : Geometry{512, 28, 8, false, 4};
 }
