@@ -36,7 +36,7 @@
 //     XCDs do not share an L2) and no fence is needed.  The owner publishes PARTIAL (tile 0:
 //     INCLUSIVE) with plain stores from lane 0 of its last wave: a wave's vector memory operations
 //     complete in issue order, so stores issued by wave 0 would delay its own look-back loads.
-//   * Look-back: wave 0 reads 64 predecessors per step (one per lane).  Ballots find the newest
+//   * Look-back: wave 0 reads 32 predecessors per step (one per lane).  Ballots find the newest
 //     INCLUSIVE state (or tile 0) and, for the scan, the newest state with a head: the scan stops
 //     there because older sums cannot reach this tile; ReduceByKey continues to an INCLUSIVE state
 //     since run indices need the full head count.  Counts and sums reduce with DPP.  Meanwhile the
@@ -62,6 +62,12 @@ namespace {
 constexpr int kBkBlock = 256;
 constexpr int kBkWaves = kBkBlock / kWave;
 constexpr int kBkVec = 4;  // consecutive items per thread and row (one 16-byte vector of 4-byte items)
+// Predecessor states wave 0 inspects per look-back step, one per lane.  Every poll of a step ends in a
+// workgroup barrier, and a step waits for its window's unpublished entries up to the nearest stop, so
+// windows shorter than the wave win (2^28 i32 keys / u32 values, runs of mean 64: ExclusiveSumByKey
+// 0.604 ms with 64, 0.57-0.60 with 32, 0.58-0.59 with 16, 0.57-0.60 with 8, 0.60-0.62 with 4; ReduceByKey
+// 0.437 / 0.405-0.424 / 0.413-0.416 / 0.431 / 0.476 ms; encode 0.252 / 0.251 / 0.254 / 0.266 / 0.299 ms).
+constexpr int kBkWindow = 32;
 // Three workgroups per CU (at most 168 VGPRs), like the scan: one workgroup's look-back wait is
 // covered by the others' loads and stores.
 constexpr int kBkBlocksPerCu = 3;
@@ -687,8 +693,8 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
             if (wave == 0) {
                 const int64_t j = top - static_cast<int64_t>(lane);
                 Seg<V> s{0u, op_identity<Op, V>()};
-                const uint32_t st = j >= 0 ? read_state<V, COUNTED>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
-                const bool exists = j >= 0;
+                const bool exists = j >= 0 && lane < static_cast<uint32_t>(kBkWindow);
+                const uint32_t st = exists ? read_state<V, COUNTED>(states + static_cast<uint64_t>(j) * W, s) : kStInvalid;
                 const bool published = st != kStInvalid;
                 // A complete prefix: an INCLUSIVE state, or tile 0 (nothing precedes it).
                 const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
@@ -719,7 +725,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
                     acc = seg_combine<Op>(window, acc);
                     const bool complete = stop_mask != 0 && cut == static_cast<uint32_t>(__builtin_ctzll(stop_mask));
                     const bool found_head = MODE == kModeScan && heads_in != 0;
-                    action = (complete || found_head || top < kWave) ? kActDone : kActAdvance;
+                    action = (complete || found_head || top < kBkWindow) ? kActDone : kActAdvance;
                 }
                 if (lane == 0) {
                     s_ctl[row][0] = action;
@@ -733,7 +739,7 @@ __global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
             row ^= 1u;
             if (action == kActDone) break;
             if (action == kActAdvance) {
-                top -= kWave;
+                top -= kBkWindow;
                 spins = 0;
                 continue;
             }

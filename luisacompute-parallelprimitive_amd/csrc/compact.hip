@@ -28,7 +28,7 @@
 //     category out with full-width coalesced stores.  Run heads compare each item with the item
 //     before it, moved across lanes with DPP wave shifts.
 //   * Wave counts (W = 1 or 2 words) are combined across the tile's 4 waves in LDS; the tile
-//     publishes its aggregate, wave 0 walks back 64 predecessor tiles per step to the newest
+//     publishes its aggregate, wave 0 walks back 32 predecessor tiles per step to the newest
 //     INCLUSIVE state, and the tile publishes INCLUSIVE.  Tile states are 64-bit words (status in the
 //     low half, count in the high half) read with agent-scope relaxed atomics; a multi-word state is
 //     accepted only when all its words show the same status.  A predecessor still unpublished after
@@ -52,6 +52,12 @@ namespace {
 
 constexpr int kCpBlock = 256;
 constexpr int kCpWaves = kCpBlock / kWave;
+// Predecessor states wave 0 inspects per look-back step, one per lane.  Every poll of a step ends in a
+// workgroup barrier, and a step waits for its window's unpublished entries up to the nearest INCLUSIVE
+// one, so windows shorter than the wave win (2^28 u32, half kept: select-if 0.435 ms with 64, 0.409-0.411
+// with 32, 0.415-0.419 with 16, 0.458-0.461 with 8, 0.546-0.548 with 4; partition-if 0.536 / 0.497-0.499 /
+// 0.494-0.495 / 0.539-0.541 / 0.627-0.629 ms).
+constexpr int kCompactWindow = 32;
 
 constexpr uint32_t kStInvalid = 0;
 constexpr uint32_t kStPartial = 1;
@@ -494,8 +500,8 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
             if (wave == 0) {
                 const int64_t j = top - static_cast<int64_t>(lane);
                 uint32_t v[W];
-                const uint32_t st = j >= 0 ? read_words<W>(states + static_cast<uint64_t>(j) * W, v) : kStInvalid;
-                const bool exists = j >= 0;
+                const bool exists = j >= 0 && lane < static_cast<uint32_t>(kCompactWindow);
+                const uint32_t st = exists ? read_words<W>(states + static_cast<uint64_t>(j) * W, v) : kStInvalid;
                 const bool published = st != kStInvalid;
                 const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
                 const uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
@@ -519,7 +525,7 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
                                                                            : wave_reduce(mine, SumOp{});
                         acc[w] = combine_word<MODE>(w, window, acc[w]);
                     }
-                    action = (stop_mask != 0 || top < kWave) ? kActDone : kActAdvance;
+                    action = (stop_mask != 0 || top < kCompactWindow) ? kActDone : kActAdvance;
                 }
                 if (lane == 0) {
                     s_ctl[row][0] = action;
@@ -536,7 +542,7 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
             row ^= 1u;
             if (action == kActDone) break;
             if (action == kActAdvance) {
-                top -= kWave;
+                top -= kCompactWindow;
                 spins = 0;
                 continue;
             }
