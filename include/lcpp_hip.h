@@ -609,8 +609,8 @@ size_t lcpp_hip_internal_radix_needed_bytes(uint32_t n, size_t key_bytes, size_t
 uint32_t lcpp_hip_internal_radix_portions(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t begin_bit,
                                           uint32_t end_bit, int double_buffer, size_t temp_bytes);
 int lcpp_hip_internal_radix_rank_mode(int mode);
-/* 1 (the default): a single-portion sort of 4-byte keys without values, 16-byte aligned, with room in its
- * temp storage takes its first pass's tile offsets from the histogram instead of a look-back; 0: every
+/* 1: a single-portion sort of 4-byte keys without values, 16-byte aligned, with room in its temp storage
+ * takes its first pass's tile offsets from the histogram instead of a look-back; 0 (the default): every
  * pass looks back.  Both give the same results.  Returns the previous setting. */
 int lcpp_hip_internal_radix_precount(int enable);
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);

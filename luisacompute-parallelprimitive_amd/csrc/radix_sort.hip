@@ -625,8 +625,9 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
                                                          const uint32_t* __restrict__ digit_offsets,
                                                          uint32_t* __restrict__ next_offsets,
                                                          uint32_t* __restrict__ lookback,
-                                                         const uint32_t* __restrict__ tile_offsets, uint32_t shift,
-                                                         uint32_t num_bits, uint32_t out_items,
+                                                         const uint32_t* __restrict__ tile_offsets,
+                                                         uint32_t* __restrict__ clear_rows, uint32_t clear_words,
+                                                         uint32_t shift, uint32_t num_bits, uint32_t out_items,
                                                          uint32_t spin_limit, uint32_t ballot_sixteenths) {
     using U = typename KeyTraits<K>::U;
     using VW = typename ValueWord<VB>::type;
@@ -701,6 +702,15 @@ __global__ __launch_bounds__(BLOCK, BLOCK / 128) void onesweep_kernel(const K* _
             const uint32_t i = wave_off + k * kWave;
             vals[k] = i < valid ? __builtin_nontemporal_load(&uvals[i]) : VW(0);
         }
+    }
+
+    // Zero the next launch's look-back rows (the other of the two regions, which the previous launch
+    // used and no launch reads until the next one): a grid-stride sweep of 16-byte stores, behind the
+    // loads.  This replaces a fill kernel before every launch.
+    if (clear_rows != nullptr) {
+        uint4* rows = reinterpret_cast<uint4*>(clear_rows);
+        const uint32_t vecs = clear_words / 4;
+        for (uint32_t i = blockIdx.x * BLOCK + tid; i < vecs; i += gridDim.x * BLOCK) rows[i] = make_uint4(0, 0, 0, 0);
     }
 
     clk.mark<1>(true);  // keys loaded
@@ -1045,7 +1055,7 @@ constexpr Geometry geometry() {
 // another thread applies from the next call.
 std::atomic<uint32_t> g_portion_limit{0};
 std::atomic<int> g_rank_mode{kRankMixed};
-std::atomic<bool> g_precount{true};  // precomputed first-pass offsets when the call allows them
+std::atomic<bool> g_precount{false};  // precomputed first-pass offsets when the call allows them
 
 // Keys ranked per launch.  The large portion keeps every look-back count below 2^30; the compact
 // portion matches the reference's PORTION_SIZE (device_radix_sort.h:1056), so its look-back region is
@@ -1065,6 +1075,9 @@ struct Layout {
     // others): the per-workgroup totals start here, past `total`, when the caller's temp has room.
     size_t chunk_off = 0;
     size_t clear_bytes;  // bins, zeroed per call
+    // Two look-back regions of tiles_max rows: launch k of a call (passes in order, portions in order
+    // within a pass) uses region k % 2 and zeroes the other one's rows for launch k + 1.
+    size_t region_words;
     int rank_mode = kRankMixed;  // test hooks as read at the start of the call
     uint32_t spin_limit = 64;
 };
@@ -1082,7 +1095,8 @@ Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t be
     L.clear_bytes = off;
     off = align_up(off, kViewAlign);
     L.lookback_off = off;
-    off += static_cast<size_t>(L.tiles_max) * kDigits * 4;
+    L.region_words = static_cast<size_t>(L.tiles_max) * kDigits;
+    off += 2 * L.region_words * 4;
     L.keys_tmp_off = L.values_tmp_off = 0;
     if (need_tmp && L.passes > 1) {
         off = align_up(off, kViewAlign);
@@ -1123,16 +1137,19 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
                 uint32_t begin_bit, uint32_t end_bit, hipStream_t stream) {
     constexpr Geometry G = geometry<K, VB>();
     uint32_t* bins = reinterpret_cast<uint32_t*>(temp + L.bins_off);
-    uint32_t* lookback = reinterpret_cast<uint32_t*>(temp + L.lookback_off);
+    uint32_t* regions = reinterpret_cast<uint32_t*>(temp + L.lookback_off);
 
-    int st = launch_fill_u32(bins, L.clear_bytes / 4, 0u, stream);
+    // Precomputed first-pass offsets (a single portion): the histogram also writes the first pass's
+    // per-tile digit counts into look-back region 0 and per-workgroup totals into the chunk region.
+    const bool precount = L.chunk_off != 0;
+    // One fill per call: the bins and, unless the histogram writes it, region 0 for the first launch
+    // (the bins come first in the layout; the alignment gap between them is zeroed with them).
+    int st = launch_fill_u32(bins, precount ? L.clear_bytes / 4 : (L.lookback_off - L.bins_off) / 4 + L.region_words,
+                             0u, stream);
     if (st != kOk) return st;
 
     const K* hist_src = db_keys ? db_keys[sel] : keys_in;
     const bool full = begin_bit == 0 && end_bit == sizeof(K) * 8;
-    // Precomputed first-pass offsets (a single portion): the histogram also writes the first pass's
-    // per-tile digit counts into the look-back region and per-workgroup totals into the chunk region.
-    const bool precount = L.chunk_off != 0;
     uint32_t* chunk_sums = precount ? reinterpret_cast<uint32_t*>(temp + L.chunk_off) : nullptr;
     HistPlan hp0{};
     for (uint32_t q = 0; q < L.portions; ++q) {
@@ -1147,10 +1164,10 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
             static_assert(G.tile() <= kHistMaxItems, "a histogram slice holds whole onesweep tiles");
             if (full)
                 histogram_tiles_kernel<K, DESC, true, G.tile()><<<grid, kHistBlock, 0, stream>>>(
-                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, lookback, chunk_sums);
+                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, regions, chunk_sums);
             else
                 histogram_tiles_kernel<K, DESC, false, G.tile()><<<grid, kHistBlock, 0, stream>>>(
-                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, lookback, chunk_sums);
+                    hist_src, len, static_cast<uint32_t>(per), bins, begin_bit, end_bit, L.passes, regions, chunk_sums);
         } else if (full)
             histogram_kernel<K, DESC, true><<<grid, kHistBlock, 0, stream>>>(
                 hist_src + static_cast<size_t>(q) * L.portion, len, static_cast<uint32_t>(per), bins, begin_bit,
@@ -1173,7 +1190,7 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         chunk_scan_kernel<<<kDigits, kDigits, 0, stream>>>(chunk_sums, bins, hp0.grid);
         st = check_hip(hipGetLastError(), "radix_chunk_scan launch");
         if (st != kOk) return st;
-        tile_offsets_kernel<<<hp0.grid, kDigits, 0, stream>>>(lookback, chunk_sums,
+        tile_offsets_kernel<<<hp0.grid, kDigits, 0, stream>>>(regions, chunk_sums,
                                                                static_cast<uint32_t>(hp0.per / G.tile()),
                                                                static_cast<uint32_t>(ceil_div(n, G.tile())));
         st = check_hip(hipGetLastError(), "radix_tile_offsets launch");
@@ -1210,19 +1227,24 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
         for (uint32_t q = 0; q < L.portions; ++q) {
             const uint32_t len = std::min(L.portion, n - q * L.portion);
             const uint32_t tiles = static_cast<uint32_t>(ceil_div(len, G.tile()));
-            const bool pre = precount && p == 0;  // the look-back region holds the first pass's offsets
-            if (!pre) {
-                st = launch_fill_u32(lookback, static_cast<uint64_t>(tiles) * kDigits, 0u, stream);
-                if (st != kOk) return st;
-            }
+            const bool pre = precount && p == 0;  // region 0 holds the first pass's offsets
+            const uint32_t k = p * L.portions + q;
+            uint32_t* lookback = regions + (k & 1u) * L.region_words;
+            // Rows the next launch walks: the next portion of this pass, else the first of the next pass.
+            uint32_t next_tiles = 0;
+            if (q + 1 < L.portions)
+                next_tiles = static_cast<uint32_t>(ceil_div(std::min(L.portion, n - (q + 1) * L.portion), G.tile()));
+            else if (p + 1 < L.passes)
+                next_tiles = static_cast<uint32_t>(ceil_div(std::min(L.portion, n), G.tile()));
+            uint32_t* clear_rows = next_tiles ? regions + ((k + 1) & 1u) * L.region_words : nullptr;
             const size_t qoff = static_cast<size_t>(q) * L.portion;
             LaunchScope scope("radix_onesweep", stream);
             const VW* vs = VB ? static_cast<const VW*>(vsrc) + qoff : nullptr;
             uint32_t* offsets = bins + (static_cast<size_t>(q) * L.passes + p) * kDigits;
             uint32_t* next = q + 1 < L.portions ? bins + (static_cast<size_t>(q + 1) * L.passes + p) * kDigits : nullptr;
             onesweep_kernel<K, DESC, VB, G.block, G.items, G.window, G.grouped><<<tiles, G.block, 0, stream>>>(
-                src + qoff, dst, vs, vdst, len, offsets, next, lookback, pre ? lookback : nullptr, shift, nb, n,
-                L.spin_limit, ballot_sixteenths_for(L.rank_mode, G.ballot_sixteenths));
+                src + qoff, dst, vs, vdst, len, offsets, next, lookback, pre ? lookback : nullptr, clear_rows,
+                next_tiles * kDigits, shift, nb, n, L.spin_limit, ballot_sixteenths_for(L.rank_mode, G.ballot_sixteenths));
             st = check_hip(hipGetLastError(), "radix_onesweep launch");
             if (st != kOk) return st;
         }
@@ -1263,11 +1285,15 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
     if (!temp || temp_bytes < L.total)
         return set_error(kTempTooSmall, "%s: temp storage too small (%zu < %zu bytes)", what, temp_bytes, L.total);
     {
-        // First-pass offsets from the histogram: 4-byte keys without values (SortKeys 2^28 u32, kernel
-        // trace: first pass 586 -> 504 us for 14 us more histogram and 12 us of offset kernels; for 8-byte
-        // keys with values both the histogram and the first pass got slower: 737 -> 801 us), one portion,
-        // 16-byte aligned keys (the histogram's slices of whole tiles then load 16-byte vectors) and
-        // room for the per-workgroup totals.
+        // First-pass offsets from the histogram (off by default; the test hook switches them on): 4-byte
+        // keys without values, one portion, 16-byte aligned keys (the histogram's slices of whole tiles
+        // then load 16-byte vectors) and room for the per-workgroup totals.  With 32-tile look-back
+        // windows they paid (SortKeys 2^28 u32, kernel trace: first pass 586 -> 504 us for 14 us more
+        // histogram and 12 us of offset kernels); with 8-tile windows every pass that looks back runs
+        // as fast as the first pass, and the tile counts cost more than they save (2.028 ms per sort
+        // without them, 2.042 ms with them: the tiles histogram 196 us against 178 us for the plain one,
+        // plus 11 us of offset kernels).  For 8-byte keys with values both the histogram and the first
+        // pass got slower (737 -> 801 us).
         const void* first_src = db ? (*selector ? db1 : db0) : keys_in;
         const size_t off = align_up(L.total, kViewAlign);
         if (sizeof(K) == 4 && VB == 0 && L.portions == 1 && reinterpret_cast<uintptr_t>(first_src) % 16 == 0 &&

@@ -339,8 +339,8 @@ def test_rank_modes_agree_with_oracle(hip, orc, dev, mode, case):
 @pytest.mark.parametrize("precount", [0, 1])
 @pytest.mark.parametrize("case", ["u32_random", "u64_pairs_desc", "f32_bits_3_29", "i32_partial_tile", "u32_db"])
 def test_first_pass_offsets_from_histogram(hip, orc, dev, precount, case):
-    """The first pass takes its tile offsets from the histogram's per-tile counts (precount 1, the default
-    for a single portion with aligned keys) or walks the look-back like the other passes (0): the same
+    """The first pass takes its tile offsets from the histogram's per-tile counts (precount 1, for a single
+    portion with aligned keys) or walks the look-back like the other passes (0, the default): the same
     stable order either way, for full and partial bit ranges, a partial last tile, pairs, descending
     order and the DoubleBuffer form."""
     lib = hip.lib()
