@@ -615,6 +615,11 @@ int lcpp_hip_internal_radix_rank_mode(int mode);
 int lcpp_hip_internal_radix_precount(int enable);
 size_t lcpp_hip_internal_by_key_needed_bytes(uint64_t n, size_t value_bytes);
 size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int words, int staged);
+/* Test hook: 1 (the default) lets selects and partitions that are not in place, whose input is 16-byte
+ * aligned (and flags of at most 4 bytes aligned to a thread's row of them), run the register-resident rows
+ * kernel; 0 sends every call to the staging kernel.  Both give the same results.  Returns the previous
+ * setting. */
+int lcpp_hip_internal_compact_rows(int enable);
 /* The device words a segmented sort called now on `stream` would use, without taking them: 1 the stream's
  * slot (eager calls), 2 a slot of the call's own (calls recorded into a graph, which may replay on any
  * stream), 0 none (slots used up: the kernels then run without their early exits). */

@@ -45,6 +45,7 @@
 #include "common.hpp"
 #include "../../include/lcpp_hip.h"
 
+#include <atomic>
 #include <cstring>
 
 namespace lcpp_hip {
@@ -145,6 +146,50 @@ __device__ __forceinline__ M clause_bits(const Clause<P>& c, const P (&x)[N]) {
     }
 #undef LCPP_CLAUSE
     return c.op == LCPP_HIP_PRED_TRUE ? static_cast<M>(~static_cast<M>(0)) : static_cast<M>(0);
+}
+
+// Bit k of words[k / 32] set when clause `c` holds for x[k]: one uniform switch for all N items (a switch
+// per small group of items would multiply the kernel's code, the clause pairs being expanded together).
+template <typename P, int N>
+__device__ __forceinline__ void clause_words(const Clause<P>& c, const P (&x)[N], uint32_t (&words)[(N + 31) / 32]) {
+#pragma unroll
+    for (int w = 0; w < (N + 31) / 32; ++w) words[w] = 0;
+#define LCPP_CLAUSE_WORDS(OP, EXPR)                                         \
+    case OP: {                                                              \
+        _Pragma("unroll") for (int k = 0; k < N; ++k) {                     \
+            const P v = x[k];                                               \
+            words[k / 32] |= static_cast<uint32_t>((EXPR) ? 1 : 0) << (k % 32); \
+        }                                                                   \
+        return;                                                             \
+    }
+    switch (c.op) {
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_LT, v < c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_LE, v <= c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_GT, v > c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_GE, v >= c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_EQ, v == c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_NE, v != c.a)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_RANGE, c.a <= v && v < c.b)
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_MASK_EQ, (__builtin_bit_cast(Bits<P>, v) & __builtin_bit_cast(Bits<P>, c.a)) ==
+                                                     __builtin_bit_cast(Bits<P>, c.b))
+        LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_MASK_NE, (__builtin_bit_cast(Bits<P>, v) & __builtin_bit_cast(Bits<P>, c.a)) !=
+                                                     __builtin_bit_cast(Bits<P>, c.b))
+        default:
+            break;
+    }
+    if constexpr (std::is_integral_v<P>) {
+        switch (c.op) {
+            LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_MOD_EQ, v % c.a == c.b)
+            LCPP_CLAUSE_WORDS(LCPP_HIP_PRED_MOD_NE, v % c.a != c.b)
+            default:
+                break;
+        }
+    }
+#undef LCPP_CLAUSE_WORDS
+    if (c.op == LCPP_HIP_PRED_TRUE) {
+#pragma unroll
+        for (int w = 0; w < (N + 31) / 32; ++w) words[w] = ~0u;
+    }
 }
 
 template <typename K>
@@ -395,6 +440,109 @@ __device__ void tile_aggregate(const CompactArgs<U, P, V>& a, uint32_t tile, uin
     block_words<MODE>(w, s_wave, wp, agg);
 }
 
+// Exclusive prefix words of tile `tile` (> 0) over its predecessors, called by the whole workgroup.  Wave 0
+// reads WINDOW predecessor states per step (one per lane), newest first, and sums them down to the
+// nearest INCLUSIVE one; its decision (done, next window, wait, help) reaches the workgroup through
+// s_ctl (two rows used alternately, so one barrier per poll suffices).  A predecessor still unpublished
+// after `spin_limit` polls is claimed (claims[t]: OPEN -> HELPER) and counted by the workgroup with
+// help(t, words), which must compute exactly what its owner publishes; the helper publishes it PARTIAL and
+// marks the claim DONE with release ordering.
+template <int MODE, int WINDOW, typename Help>
+__device__ void compact_lookback(uint64_t* states, uint64_t* claims, uint32_t tile, uint32_t spin_limit,
+                                 uint32_t (*s_ctl)[2], uint32_t* s_prefix, uint32_t (&prefix)[kWords<MODE>],
+                                 Help help) {
+    constexpr int W = kWords<MODE>;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    int64_t top = static_cast<int64_t>(tile) - 1;
+    uint32_t acc[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[w] = 0;
+    uint32_t spins = 0;
+    uint32_t row = 0;
+    while (true) {
+        if (wave == 0) {
+            const int64_t j = top - static_cast<int64_t>(lane);
+            uint32_t v[W];
+            const bool exists = j >= 0 && lane < static_cast<uint32_t>(WINDOW);
+            const uint32_t st = exists ? read_words<W>(states + static_cast<uint64_t>(j) * W, v) : kStInvalid;
+            const bool published = st != kStInvalid;
+            const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
+            const uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
+            const uint64_t upto = cut >= kWave - 1 ? ~0ull : ((2ull << cut) - 1);
+            const uint64_t missing = upto & wave_ballot(exists) & ~wave_ballot(published);
+            uint32_t action;
+            uint32_t help_tile = 0;
+            if (missing) {
+                if (spins >= spin_limit) {
+                    action = kActHelp;
+                    help_tile = static_cast<uint32_t>(top - __builtin_ctzll(missing));
+                } else {
+                    action = kActWait;
+                }
+            } else {
+                const bool take = exists && lane <= cut;
+#pragma unroll
+                for (int w = 0; w < W; ++w) {
+                    const uint32_t mine = take ? v[w] : 0u;
+                    const uint32_t window = (kWord1Max<MODE> && w == 1) ? wave_reduce(mine, MaxU32Op{})
+                                                                       : wave_reduce(mine, SumOp{});
+                    acc[w] = combine_word<MODE>(w, window, acc[w]);
+                }
+                action = (stop_mask != 0 || top < WINDOW) ? kActDone : kActAdvance;
+            }
+            if (lane == 0) {
+                s_ctl[row][0] = action;
+                s_ctl[row][1] = help_tile;
+                if (action == kActDone) {
+#pragma unroll
+                    for (int w = 0; w < W; ++w) s_prefix[w] = acc[w];
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t action = s_ctl[row][0];
+        const uint32_t help_tile = s_ctl[row][1];
+        row ^= 1u;
+        if (action == kActDone) break;
+        if (action == kActAdvance) {
+            top -= WINDOW;
+            spins = 0;
+            continue;
+        }
+        if (action == kActWait) {
+            __builtin_amdgcn_s_sleep(1);
+            ++spins;
+            continue;
+        }
+        // kActHelp: claim the unpublished predecessor, count it, publish it PARTIAL and mark the claim
+        // DONE with release ordering.
+        if (tid == 0) {
+            uint64_t expected = kClaimOpen;
+            s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&claims[help_tile], &expected, kClaimHelper,
+                                                                 __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                                 __HIP_MEMORY_SCOPE_AGENT)
+                                ? 1u
+                                : 0u;
+        }
+        __syncthreads();
+        const bool claimed = s_ctl[row][0] != 0;
+        row ^= 1u;
+        if (claimed) {
+            uint32_t h[W];
+            help(help_tile, h);
+            if (tid == 0) {
+                publish_words<W>(states + static_cast<uint64_t>(help_tile) * W, kStPartial, h);
+                __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        spins = 0;
+    }
+#pragma unroll
+    for (int w = 0; w < W; ++w) prefix[w] = s_prefix[w];
+}
+
 template <typename U, typename P, typename V, int MODE, bool FLAGS>
 __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, P, V> a) {
     constexpr int ITEMS = kCpItems<U, V>;
@@ -489,94 +637,11 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
     uint32_t prefix[W];
 #pragma unroll
     for (int w = 0; w < W; ++w) prefix[w] = 0;
-    if (tile > 0) {
-        int64_t top = static_cast<int64_t>(tile) - 1;
-        uint32_t acc[W];
-#pragma unroll
-        for (int w = 0; w < W; ++w) acc[w] = 0;
-        uint32_t spins = 0;
-        uint32_t row = 0;
-        while (true) {
-            if (wave == 0) {
-                const int64_t j = top - static_cast<int64_t>(lane);
-                uint32_t v[W];
-                const bool exists = j >= 0 && lane < static_cast<uint32_t>(kCompactWindow);
-                const uint32_t st = exists ? read_words<W>(states + static_cast<uint64_t>(j) * W, v) : kStInvalid;
-                const bool published = st != kStInvalid;
-                const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
-                const uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
-                const uint64_t upto = cut >= kWave - 1 ? ~0ull : ((2ull << cut) - 1);
-                const uint64_t missing = upto & wave_ballot(exists) & ~wave_ballot(published);
-                uint32_t action;
-                uint32_t help_tile = 0;
-                if (missing) {
-                    if (spins >= a.spin_limit) {
-                        action = kActHelp;
-                        help_tile = static_cast<uint32_t>(top - __builtin_ctzll(missing));
-                    } else {
-                        action = kActWait;
-                    }
-                } else {
-                    const bool take = exists && lane <= cut;
-#pragma unroll
-                    for (int w = 0; w < W; ++w) {
-                        const uint32_t mine = take ? v[w] : 0u;
-                        const uint32_t window = (kWord1Max<MODE> && w == 1) ? wave_reduce(mine, MaxU32Op{})
-                                                                           : wave_reduce(mine, SumOp{});
-                        acc[w] = combine_word<MODE>(w, window, acc[w]);
-                    }
-                    action = (stop_mask != 0 || top < kCompactWindow) ? kActDone : kActAdvance;
-                }
-                if (lane == 0) {
-                    s_ctl[row][0] = action;
-                    s_ctl[row][1] = help_tile;
-                    if (action == kActDone) {
-#pragma unroll
-                        for (int w = 0; w < W; ++w) s_prefix[w] = acc[w];
-                    }
-                }
-            }
-            __syncthreads();
-            const uint32_t action = s_ctl[row][0];
-            const uint32_t help_tile = s_ctl[row][1];
-            row ^= 1u;
-            if (action == kActDone) break;
-            if (action == kActAdvance) {
-                top -= kCompactWindow;
-                spins = 0;
-                continue;
-            }
-            if (action == kActWait) {
-                __builtin_amdgcn_s_sleep(1);
-                ++spins;
-                continue;
-            }
-            // kActHelp: claim the unpublished predecessor, count it, publish it PARTIAL and mark the
-            // claim DONE with release ordering.
-            if (tid == 0) {
-                uint64_t expected = kClaimOpen;
-                s_ctl[row][0] = __hip_atomic_compare_exchange_strong(&claims[help_tile], &expected, kClaimHelper,
-                                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                                     __HIP_MEMORY_SCOPE_AGENT)
-                                    ? 1u
-                                    : 0u;
-            }
-            __syncthreads();
-            const bool claimed = s_ctl[row][0] != 0;
-            row ^= 1u;
-            if (claimed) {
-                uint32_t h[W];
-                tile_aggregate<U, P, V, MODE, FLAGS, ITEMS>(a, help_tile, s_wave, h);
-                if (tid == 0) {
-                    publish_words<W>(states + static_cast<uint64_t>(help_tile) * W, kStPartial, h);
-                    __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            spins = 0;
-        }
-#pragma unroll
-        for (int w = 0; w < W; ++w) prefix[w] = s_prefix[w];
-    }
+    if (tile > 0)
+        compact_lookback<MODE, kCompactWindow>(states, claims, tile, a.spin_limit, s_ctl, s_prefix, prefix,
+                                               [&](uint32_t help_tile, uint32_t (&h)[W]) {
+                                                   tile_aggregate<U, P, V, MODE, FLAGS, ITEMS>(a, help_tile, s_wave, h);
+                                               });
 
     if (tid == kPublisher) {
         if (!owned) {
@@ -658,6 +723,334 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
     }
 }
 
+// ---- Select / partition over register-resident rows ---------------------------------------------------
+// DeviceSelect::If / Flagged / FlaggedIf and DevicePartition::If / Flagged of 4- or 8-byte items, not in
+// place, with a 16-byte aligned input (and flags of at most 4 bytes aligned to a thread's row of them).
+// Like the scan's tiles, a tile is 256 threads x ROWS rows x one 16-byte vector of items per thread and
+// row, held in registers (four workgroups per CU), rather than staged whole in LDS as by the kernel above
+// (whose 32 KB stage per tile bounds the input in flight).  Per thread and row a mask of the selected items
+// (each clause one uniform switch over all of the thread's items); per row the waves' counts go to a rows x
+// waves table in LDS.  Wave 0 publishes the tile's count and walks back alone, without a workgroup barrier
+// per poll.  Then each wave stages its part of every row in 1 KB of LDS (selected items from the front,
+// partition rejects from the back) and reads it back one slot per lane, so every store covers consecutive
+// addresses.  (Stored straight from registers, four scattered stores per row, select-if took 0.53 ms.)
+constexpr int kRowsBlock = 256;
+constexpr int kRowsWaves = kRowsBlock / kWave;
+// Predecessor states per look-back step (one per lane of wave 0): 0.393 / 0.450 ms with 8, 0.417 / 0.464 with
+// 4, 0.390 / 0.452 with 12, 0.389 / 0.453 with 16 (select-if / partition-if as above).
+constexpr int kRowsWindow = 8;
+template <typename U>
+constexpr int kRowItems = static_cast<int>(16 / sizeof(U));
+// Rows per tile: four workgroups per CU (at most 128 VGPRs) with 16 rows, 12 with flags (whose vectors take
+// registers too) or 8-byte items (whose remainder clauses do).  Select-if / partition-if of 2^28 u32, half
+// kept: 0.393 / 0.450 ms with 16 rows at four workgroups per CU, 0.445 / 0.493 with 20 rows at three,
+// 0.392 / 0.449 with 12 rows at five, 0.400 / 0.462 with 10 rows at six.
+template <typename U, bool FLAGS>
+constexpr int kSelRows = (FLAGS || sizeof(U) == 8) ? 12 : 16;
+template <typename U, bool FLAGS>
+constexpr uint32_t kRowsTile = static_cast<uint32_t>(kRowsBlock) * kSelRows<U, FLAGS> * kRowItems<U>;
+
+// One thread's items (and flags) of one row: items base + (256 r + tid) V + j, j < V, as one vector each.
+template <typename U, typename P>
+struct RowVecs {
+    static constexpr int V = kRowItems<U>;
+    using Items = U __attribute__((ext_vector_type(V)));
+    using Flags = P __attribute__((ext_vector_type(V)));
+};
+
+// Selection mask of one row (bit j: item j of the thread's vector), valid items only.
+template <typename U, typename P, bool FLAGS>
+__device__ __forceinline__ uint32_t row_selection(const Predicate<P>& pred, const typename RowVecs<U, P>::Items& it,
+                                                  const typename RowVecs<U, P>::Flags& fl, uint32_t valid) {
+    constexpr int V = kRowItems<U>;
+    P x[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        if constexpr (FLAGS) {
+            x[j] = fl[j];
+        } else {
+            x[j] = it[j];
+        }
+    }
+    return clause_bits<P, V, uint32_t>(pred.c[0], x) & clause_bits<P, V, uint32_t>(pred.c[1], x) & valid;
+}
+
+// Loads row r of the tile at `base` for this thread; items past n read as 0 and are not valid.  A vector
+// wholly before n is one vector load (of a full tile, without the test); only the vector holding item
+// n - 1 is read item by item.
+template <typename U, typename P, bool FLAGS>
+__device__ __forceinline__ void load_row(const CompactArgs<U, P, U>& a, uint64_t base, int r, bool full,
+                                         typename RowVecs<U, P>::Items& it, typename RowVecs<U, P>::Flags& fl,
+                                         uint32_t& valid) {
+    using RV = RowVecs<U, P>;
+    constexpr int V = RV::V;
+    const uint64_t vec = static_cast<uint64_t>(r) * kRowsBlock + threadIdx.x;
+    const uint64_t first = base + vec * V;
+    if (full || first + V <= a.n) {
+        it = __builtin_nontemporal_load(reinterpret_cast<const typename RV::Items*>(a.in + base) + vec);
+        if constexpr (FLAGS) fl = __builtin_nontemporal_load(reinterpret_cast<const typename RV::Flags*>(a.flags + base) + vec);
+        valid = (1u << V) - 1u;
+    } else {
+        valid = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const bool ok = first + j < a.n;
+            it[j] = ok ? a.in[first + j] : U(0);
+            if constexpr (FLAGS) fl[j] = ok ? a.flags[first + j] : P(0);
+            valid |= (ok ? 1u : 0u) << j;
+        }
+    }
+}
+
+// Selected items of tile `tile`, counted by one wave (a predecessor's count for the look-back fallback;
+// integer counts, so any order gives its owner's result).
+template <typename U, typename P, bool FLAGS>
+__device__ uint32_t rows_tile_count(const CompactArgs<U, P, U>& a, uint32_t tile) {
+    using RV = RowVecs<U, P>;
+    constexpr int V = RV::V;
+    constexpr uint32_t TILE = kRowsTile<U, FLAGS>;
+    const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+    const uint32_t lane = lane_id();
+    uint32_t c = 0;
+#pragma unroll 1
+    for (uint32_t vec = lane; vec < TILE / V; vec += kWave) {
+        const uint64_t first = base + static_cast<uint64_t>(vec) * V;
+        typename RV::Items it;
+        typename RV::Flags fl;
+        uint32_t valid = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const bool ok = first + j < a.n;
+            it[j] = ok ? a.in[first + j] : U(0);
+            if constexpr (FLAGS) fl[j] = ok ? a.flags[first + j] : P(0);
+            valid |= (ok ? 1u : 0u) << j;
+        }
+        c += static_cast<uint32_t>(__builtin_popcount(row_selection<U, P, FLAGS>(a.pred, it, fl, valid)));
+    }
+    return wave_reduce(c, SumOp{});
+}
+
+// Selected items before tile `tile` (> 0), by wave 0 alone (no workgroup barrier per poll): each step reads
+// kRowsWindow predecessor states, newest first, and sums them down to the nearest INCLUSIVE one.  A
+// predecessor still unpublished after `spin_limit` polls is claimed (claims[t]: OPEN -> HELPER), counted by
+// this wave and published PARTIAL, and its claim marked DONE with release ordering; a claim lost to the
+// owner or to another helper is simply polled again.
+template <typename U, typename P, bool FLAGS>
+__device__ uint32_t rows_lookback(const CompactArgs<U, P, U>& a, uint64_t* states, uint64_t* claims, uint32_t tile) {
+    const uint32_t lane = lane_id();
+    uint32_t acc = 0;
+    int64_t top = static_cast<int64_t>(tile) - 1;
+    uint32_t spins = 0;
+    while (true) {
+        const int64_t j = top - static_cast<int64_t>(lane);
+        const bool exists = j >= 0 && lane < static_cast<uint32_t>(kRowsWindow);
+        uint32_t v[1] = {0};
+        const uint32_t st = exists ? read_words<1>(states + j, v) : kStInvalid;
+        const bool published = st != kStInvalid;
+        const uint64_t stop_mask = wave_ballot(published && (st == kStInclusive || j == 0));
+        const uint32_t cut = stop_mask ? static_cast<uint32_t>(__builtin_ctzll(stop_mask)) : kWave - 1;
+        const uint64_t upto = cut >= kWave - 1 ? ~0ull : ((2ull << cut) - 1);
+        const uint64_t missing = upto & wave_ballot(exists) & ~wave_ballot(published);
+        if (missing) {
+            if (spins < a.spin_limit) {
+                __builtin_amdgcn_s_sleep(1);
+                ++spins;
+                continue;
+            }
+            const uint32_t help_tile = static_cast<uint32_t>(top - __builtin_ctzll(missing));
+            uint32_t won = 0;
+            if (lane == 0) {
+                uint64_t expected = kClaimOpen;
+                won = __hip_atomic_compare_exchange_strong(&claims[help_tile], &expected, kClaimHelper, __ATOMIC_RELAXED,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          ? 1u
+                          : 0u;
+            }
+            if (wave_read_lane(won, 0) != 0) {
+                const uint32_t h[1] = {rows_tile_count<U, P, FLAGS>(a, help_tile)};
+                if (lane == 0) {
+                    publish_words<1>(states + help_tile, kStPartial, h);
+                    __hip_atomic_store(&claims[help_tile], kClaimDone, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            spins = 0;
+            continue;
+        }
+        acc += wave_reduce(exists && lane <= cut ? v[0] : 0u, SumOp{});
+        if (stop_mask != 0 || top < kRowsWindow) break;
+        top -= kRowsWindow;
+        spins = 0;
+    }
+    return acc;
+}
+
+template <typename U, typename P, bool FLAGS>
+__global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const CompactArgs<U, P, U> a) {
+    using RV = RowVecs<U, P>;
+    constexpr int V = RV::V;
+    constexpr int R = kSelRows<U, FLAGS>;
+    constexpr uint32_t TILE = kRowsTile<U, FLAGS>;
+    constexpr int ROWS_PER_WORD = 32 / V;  // row masks packed into 32-bit words
+    constexpr int MW = (R + ROWS_PER_WORD - 1) / ROWS_PER_WORD;
+    constexpr uint32_t kRowSlots = static_cast<uint32_t>(kWave) * V;  // items of one wave's part of a row
+    __shared__ uint32_t s_tot[R][kRowsWaves];
+    __shared__ U s_stage[kRowsWaves][kRowSlots];
+    __shared__ uint32_t s_prefix[1];
+
+    uint64_t* const states = a.states;
+    uint64_t* const claims = states + gridDim.x;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid / kWave;
+    const uint32_t tile = blockIdx.x;
+    const uint64_t base = static_cast<uint64_t>(tile) * TILE;
+    const bool full = base + TILE <= a.n;
+
+    typename RV::Items it[R];
+    uint32_t masks[MW];
+    {
+        typename RV::Flags fl[FLAGS ? R : 1];
+        uint32_t valid[MW];
+#pragma unroll
+        for (int w = 0; w < MW; ++w) valid[w] = 0;
+        if (full) {
+            // Every row's loads in flight before any is used.
+            const typename RV::Items* src = reinterpret_cast<const typename RV::Items*>(a.in + base);
+#pragma unroll
+            for (int r = 0; r < R; ++r) it[r] = __builtin_nontemporal_load(&src[r * kRowsBlock + tid]);
+            if constexpr (FLAGS) {
+                const typename RV::Flags* fsrc = reinterpret_cast<const typename RV::Flags*>(a.flags + base);
+#pragma unroll
+                for (int r = 0; r < R; ++r) fl[r] = __builtin_nontemporal_load(&fsrc[r * kRowsBlock + tid]);
+            }
+#pragma unroll
+            for (int w = 0; w < MW; ++w) valid[w] = ~0u;
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t v;
+                load_row<U, P, FLAGS>(a, base, r, false, it[r], fl[FLAGS ? r : 0], v);
+                valid[r / ROWS_PER_WORD] |= v << (V * (r % ROWS_PER_WORD));
+            }
+        }
+        // Both clauses over all R x V items (item k = V r + j is bit k % 32 of word k / 32).
+        P x[R * V];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                if constexpr (FLAGS) {
+                    x[r * V + j] = fl[r][j];
+                } else {
+                    x[r * V + j] = it[r][j];
+                }
+            }
+        }
+        uint32_t second[MW];
+        clause_words<P, R * V>(a.pred.c[0], x, masks);
+        clause_words<P, R * V>(a.pred.c[1], x, second);
+#pragma unroll
+        for (int w = 0; w < MW; ++w) masks[w] &= second[w] & valid[w];
+    }
+    auto row_mask = [&](int r) { return (masks[r / ROWS_PER_WORD] >> (V * (r % ROWS_PER_WORD))) & ((1u << V) - 1u); };
+
+    // Row totals per wave now; each thread's offset within its row is scanned again at output time, so
+    // no per-row scan stays live across the look-back.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t total = wave_reduce(static_cast<uint32_t>(__builtin_popcount(row_mask(r))), SumOp{});
+        if (lane == 0) s_tot[r][wave] = total;
+    }
+    __syncthreads();
+    // Lane r (< R) of every wave takes row r: its total over the waves, the part in waves before this
+    // one, and (scanned over the lanes) the selected items of the tile's earlier rows.
+    uint32_t row_total = 0, row_before = 0;
+    if (lane < static_cast<uint32_t>(R)) {
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) {
+            const uint32_t x = s_tot[lane][w];
+            if (w < static_cast<int>(wave)) row_before += x;
+            row_total += x;
+        }
+    }
+    const uint32_t rows_incl = wave_inclusive_scan(row_total, SumOp{});
+    uint32_t agg[1] = {wave_read_lane(rows_incl, kWave - 1)};
+
+    // Wave 0 publishes the tile's count, walks back over its predecessors and publishes the inclusive count
+    // at once (a helper that claimed this tile first publishes its PARTIAL state; the owner then waits for
+    // the helper to finish before it publishes INCLUSIVE).
+    uint32_t prefix[1] = {0};
+    if (wave == 0) {
+        uint32_t owned = 1;
+        if (lane == 0) {
+            publish_words<1>(&states[tile], tile == 0 ? kStInclusive : kStPartial, agg);
+            uint64_t expected = kClaimOpen;
+            owned = __hip_atomic_compare_exchange_strong(&claims[tile], &expected, kClaimOwned, __ATOMIC_RELAXED,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        ? 1u
+                        : 0u;
+        }
+        if (tile > 0) prefix[0] = rows_lookback<U, P, FLAGS>(a, states, claims, tile);
+        if (lane == 0) {
+            if (!owned) {
+                while (__hip_atomic_load(&claims[tile], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != kClaimDone)
+                    __builtin_amdgcn_s_sleep(1);
+            }
+            if (tile > 0 || !owned) {
+                const uint32_t incl[1] = {prefix[0] + agg[0]};
+                publish_words<1>(&states[tile], kStInclusive, incl);
+            }
+            s_prefix[0] = prefix[0];
+        }
+    }
+    __syncthreads();
+    prefix[0] = s_prefix[0];
+    if (tile + 1 == gridDim.x && tid == 0) a.num_out[0] = prefix[0] + agg[0];
+
+    // Outputs, one row at a time per wave.  Lane r's row_base: the selected items before this wave's part
+    // of row r (the tile prefix, the earlier rows, the earlier waves of row r).  The wave stages its part of
+    // the row in its own LDS slots: selected items from slot 0 up in order, partition rejects from the last
+    // slot down, then reads the slots back one per lane, so every store of the wave covers consecutive
+    // addresses (a selected run, then a run of rejects, whose output runs backwards from the end).
+    const uint32_t row_base = prefix[0] + (rows_incl - row_total) + row_before;
+    U* const stage = s_stage[wave];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t m = row_mask(r);
+        const uint32_t c = static_cast<uint32_t>(__builtin_popcount(m));
+        const uint32_t incl = wave_inclusive_scan(c, SumOp{});
+        const uint32_t sel_base = wave_read_lane(row_base, r);
+        const uint32_t kept = wave_read_lane(incl, kWave - 1);  // selected items of the wave's row
+        const uint64_t row_first = base + (static_cast<uint64_t>(r) * kRowsBlock + wave * kWave) * V;
+        const uint32_t in_row = row_first < a.n ? static_cast<uint32_t>(min<uint64_t>(a.n - row_first, kRowSlots)) : 0u;
+        uint32_t k = incl - c;             // selected slots before the lane's items
+        uint32_t q = lane * V - (incl - c);  // rejects before them
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            if ((m >> j) & 1u) {
+                stage[k++] = it[r][j];
+            } else {
+                if (a.partition && lane * V + j < in_row) stage[kRowSlots - 1 - q] = it[r][j];
+                ++q;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // Rejects before the wave's row: its first item's index minus the selected items before it.
+        const uint64_t rej_end = a.n - 1 - (row_first - sel_base);  // output position of the row's first reject
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const uint32_t slot = static_cast<uint32_t>(j) * kWave + lane;
+            if (slot < kept) {
+                a.out[sel_base + slot] = stage[slot];
+            } else if (a.partition && slot >= kRowSlots - (in_row - kept)) {
+                // Slot kRowSlots - 1 - q holds reject q, which goes to rej_end - q.
+                a.out[rej_end - (kRowSlots - 1 - slot)] = stage[slot];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // dst[q] = src[q] for q < *count (the in-place select's copy back).
 template <typename U>
 __global__ __launch_bounds__(256) void copy_prefix_kernel(U* __restrict__ dst, const U* __restrict__ src,
@@ -676,6 +1069,10 @@ __global__ __launch_bounds__(256) void reverse_rejects_kernel(U* __restrict__ ds
     for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < u; j += stride)
         dst[u - 1 - j] = src[j];
 }
+
+// Test hook: the rows kernel for selects and partitions that allow it (default) or the staging kernel for
+// every call.  Both give the same results.
+std::atomic<bool> g_select_rows{true};
 
 bool overlaps(const void* a, size_t a_bytes, const void* b, size_t b_bytes) {
     if (!a || !b || a_bytes == 0 || b_bytes == 0) return false;
@@ -796,6 +1193,21 @@ int run_compact(const char* what, void* temp, size_t temp_bytes, const U* in, co
     a.spin_limit = lookback_spin_limit();
     a.partition = partition;
 
+    if constexpr (MODE == kSelect && std::is_same_v<U, V> && (sizeof(U) == 4 || sizeof(U) == 8) &&
+                  (!FLAGS || sizeof(P) <= 4)) {
+        // Selects and partitions that are not in place take the register-resident rows kernel when the
+        // input (and the flags) allow whole-vector row loads.  Its tiles are larger, so its states take
+        // less temp storage than the plan checked above.
+        if (!in_place && g_select_rows.load(std::memory_order_relaxed) && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+            (!FLAGS || reinterpret_cast<uintptr_t>(flags) % (kRowItems<U> * sizeof(P)) == 0)) {
+            const TempPlan rp = plan_temp(n, kRowsTile<U, FLAGS>, 1, 0);
+            int st = launch_fill_u32(reinterpret_cast<uint32_t*>(temp), rp.state_bytes / 4, 0u, stream);
+            if (st != kOk) return st;
+            LaunchScope scope("compact", stream);
+            select_rows_kernel<U, P, FLAGS><<<static_cast<unsigned>(rp.tiles), kRowsBlock, 0, stream>>>(a);
+            return check_hip(hipGetLastError(), "compact rows launch");
+        }
+    }
     int st = launch_fill_u32(reinterpret_cast<uint32_t*>(temp), plan.state_bytes / 4, 0u, stream);
     if (st != kOk) return st;
     {
@@ -838,6 +1250,10 @@ size_t lcpp_hip_internal_compact_needed_bytes(uint64_t n, size_t item_bytes, int
     if (n == 0) return 0;
     const uint64_t tile = static_cast<uint64_t>(kCpBlock) * (128 / item_bytes);
     return plan_temp(n, tile, words, staged ? item_bytes : 0).total;
+}
+
+int lcpp_hip_internal_compact_rows(int enable) {
+    return g_select_rows.exchange(enable != 0, std::memory_order_relaxed) ? 1 : 0;
 }
 
 #define LCPP_HIP_DEFINE_SELECT_FLAGS(TS, TT, FS, FT)                                                                 \

@@ -159,6 +159,7 @@ def _declare(lib: C.CDLL) -> None:
         sig(f"lcpp_hip_{name}_temp_bytes", sz, u64)
         sig(f"lcpp_hip_{name}_temp_bytes_policy", sz, u64, u32, u32)
     sig("lcpp_hip_internal_compact_needed_bytes", sz, u64, sz, i32, i32)
+    sig("lcpp_hip_internal_compact_rows", i32, i32)
     for t in SCALAR_SUFFIXES:
         sig(f"lcpp_hip_select_if_{t}", i32, vp, sz, vp, vp, vp, u64, pp, vp)
         sig(f"lcpp_hip_partition_if_{t}", i32, vp, sz, vp, vp, vp, u64, pp, vp)

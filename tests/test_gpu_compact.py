@@ -525,3 +525,102 @@ def test_errors(hip, dev):
     with pytest.raises(hip.LcppHipError) as e:
         hip.partition_if("i32", a, a, num, n, hip.predicate("i32", (hip.PRED_GT, 0)))
     assert e.value.status == hip.ERR_INVALID_ARGUMENT
+
+
+# ---- the register-resident rows kernel (selects and partitions not in place) and the staging kernel ----
+R4, R8, R4F, R8F = 16384, 6144, 12288, 6144  # rows-kernel tiles: 4- / 8-byte items, without / with flags
+
+
+@pytest.fixture(params=[True, False], ids=["rows", "staging"])
+def rows_kernel(hip, request):
+    """Runs the test with the rows kernel allowed (the default) and with every call on the staging kernel."""
+    lib = hip.lib()
+    old = lib.lcpp_hip_internal_compact_rows(1 if request.param else 0)
+    yield request.param
+    lib.lcpp_hip_internal_compact_rows(old)
+
+
+@pytest.mark.parametrize("ts", ["i32", "u32", "f32", "i64", "u64", "f64"])
+def test_select_partition_if_at_rows_tile_boundaries(hip, orc, dev, rows_kernel, ts):
+    rng = np.random.default_rng(900 + sum(map(ord, ts)))
+    tile = R8 if ts in ("i64", "u64", "f64") else R4
+    cl = clauses_for(ts)
+    for n in (1, 255, 1024, tile - 1, tile, tile + 1, 2 * tile + 7, 5 * tile - 3):
+        log(f"rows={rows_kernel} {ts} select/partition-if n={n}")
+        x = items_for(rng, n, ts)
+        sel = orc.predicate(x, cl)
+        for partition in (False, True):
+            got, k = g_select_if(hip, x, cl, partition=partition)
+            check_select(orc, x, sel, got, k, partition)
+
+
+@pytest.mark.parametrize("ts", ["i32", "u64"])
+@pytest.mark.parametrize("fs", ["b8", "i32", "u32", "u64"])
+def test_select_partition_flagged_at_rows_tile_boundaries(hip, orc, dev, rows_kernel, ts, fs):
+    """Flags of 1 and 4 bytes take the rows kernel (8-byte flags the staging kernel); every pattern of the
+    reference's flagged tests, at the rows tiles' boundaries."""
+    tile = R8F if ts == "u64" else R4F
+    rng = np.random.default_rng(77 + len(ts + fs))
+    for n in (tile - 1, tile, tile + 1, 3 * tile + 5):
+        x = items_for(rng, n, ts)
+        i = np.arange(n)
+        for pattern in range(4):
+            raw = [np.zeros(n), np.ones(n), i % 3, rng.integers(-2, 3, n)][pattern]
+            flags = (raw != 0).astype(np.uint8) if fs == "b8" else raw.astype(NP[fs])
+            sel = (flags != 0).astype(np.uint8)
+            for partition in (False, True):
+                got, k = g_select_flagged(hip, x, flags, partition=partition)
+                check_select(orc, x, sel, got, k, partition)
+        if fs in ("i32", "u32"):
+            cl = [(hip.PRED_GT, 0), (hip.PRED_MOD_NE, 2, 0)]
+            flags = rng.integers(-3, 4, n).astype(NP[fs])
+            got, k = g_select_flagged(hip, x, flags, clauses=cl)
+            check_select(orc, x, orc.predicate(flags, cl), got, k)
+
+
+def test_rows_kernel_forced_fallback(hip, orc, dev, rows_kernel):
+    """Every look-back of the rows kernel takes the fallback (spin limit 0): predecessors counted by their
+    successors, select and partition, with and without flags."""
+    rng = np.random.default_rng(4242)
+    n = 60 * R4 + 13
+    x = items_for(rng, n, "u32")
+    flags = rng.integers(0, 2, n).astype(np.uint8)
+    cl = clauses_for("u32")
+    lib = hip.lib()
+    old = lib.lcpp_hip_get_lookback_spin_limit()
+    try:
+        lib.lcpp_hip_set_lookback_spin_limit(0)
+        for partition in (False, True):
+            log(f"rows={rows_kernel} fallback partition={partition}")
+            got, k = g_select_if(hip, x, cl, partition=partition)
+            check_select(orc, x, orc.predicate(x, cl), got, k, partition)
+            got, k = g_select_flagged(hip, x, flags, partition=partition)
+            check_select(orc, x, flags, got, k, partition)
+    finally:
+        lib.lcpp_hip_set_lookback_spin_limit(old)
+
+
+def test_rows_kernel_predicates_and_flag_alignment(hip, orc, dev):
+    """Every clause kind through the rows kernel (single clauses and pairs); flags one item off their row
+    alignment (the staging kernel) against aligned flags (the rows kernel)."""
+    rng = np.random.default_rng(99)
+    n = 3 * R4 + 77
+    x = rng.integers(-5000, 5000, n).astype(np.int32)
+    P = hip
+    cases = [[(P.PRED_LT, 7)], [(P.PRED_LE, -3)], [(P.PRED_GT, 100)], [(P.PRED_GE, 0)], [(P.PRED_EQ, 5)],
+             [(P.PRED_NE, 0)], [(P.PRED_RANGE, -100, 250)], [(P.PRED_MOD_EQ, 7, 3)], [(P.PRED_MOD_NE, 4, 0)],
+             [(P.PRED_MASK_EQ, 0xF0, 0x30)], [(P.PRED_MASK_NE, 0x3, 0x1)], [(P.PRED_TRUE,)],
+             [(P.PRED_GT, -1000), (P.PRED_MOD_EQ, 3, 1)]]
+    for cl in cases:
+        sel = orc.predicate(x, cl)
+        for partition in (False, True):
+            got, k = g_select_if(hip, x, cl, partition=partition)
+            check_select(orc, x, sel, got, k, partition)
+    flags = rng.integers(0, 3, n + 1).astype(np.int32)
+    d_f = to_dev(flags)[1:]  # 4 bytes off the 16-byte row alignment
+    d_in = to_dev(x)
+    d_out = fill_dev(n, 4, 0x5A)
+    num = fill_dev(1, 4, 99)
+    hip.partition_flagged("i32", "i32", d_in, d_f, d_out, num, n)
+    check_select(orc, x, (flags[1:] != 0).astype(np.uint8), to_host(d_out, np.int32, n),
+                 int(to_host(num, np.uint32, 1)[0]), True)
