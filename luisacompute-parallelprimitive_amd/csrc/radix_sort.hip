@@ -129,15 +129,20 @@ __device__ __forceinline__ uint32_t digit_bits(U ordered, uint32_t shift, uint32
 // --------------------------------------------------------------------------------------------
 // Histogram: digit counts of every pass for one portion.
 //
-// LDS atomics are the cost here, and random digits make the lanes of one ds_add collide on banks.
-// Each of the 32 banks therefore gets its own copy of the counters: lane l counts into copy l & 31,
-// and word (pass, digit / 2, copy) sits at bank `copy`, so the 64 lanes of an instruction touch each
-// bank at most twice whatever the digits are (skewed digits included).  A word packs the 16-bit
-// counters of an even/odd digit pair; a workgroup counts at most kHistMaxItems keys, which bounds
-// every counter by kHistMaxItems / 32 (+ a few head/tail keys) < 2^16.  LDS: sizeof(key) passes x
-// 16 KB, so two 1024-thread workgroups per CU for 4-byte keys and one for 8-byte keys.
+// Random digits make the lanes of one ds_add collide on LDS banks, so the counters have 32 copies: lane l
+// counts into copy l & 31, the word of (pass, digit, copy) sitting at bank (digit & 1) * 32 + copy of the
+// 64, and the lanes of an instruction meet at most two to a bank whatever the digits are (skewed digits
+// included).  4-byte keys: one 32-bit counter per digit and copy, 4 passes x 32 KB of LDS, one
+// 1024-thread workgroup per CU.  8-byte keys: a word packs the 16-bit counters of an even/odd digit pair
+// (8 passes x 16 KB; each counter stays below kHistMaxItems / 32 + a few head/tail keys < 2^16), which
+// costs a multiply-add per key and pass more.  (SortKeys 2^28 u32: histogram 179 -> 168 us unpacked; two
+// workgroups per CU of packed counters, or unpacked ones with 16 copies, 174-180 us; 64 copies or the
+// next loads issued before the counting changed nothing.)
 // --------------------------------------------------------------------------------------------
 constexpr int kHistCopies = 32;
+// One 32-bit counter per digit and copy (else 16-bit pairs).
+template <typename U>
+constexpr bool kHistWide = sizeof(U) == 4;
 constexpr int kHistBlock = 1024;
 constexpr int kHistVecItems = 8;             // 16-byte loads per thread per step
 constexpr uint32_t kHistMaxItems = 1u << 20;  // keys per workgroup
@@ -152,7 +157,8 @@ __global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restri
     constexpr int KIND = KeyTraits<K>::kind;
     constexpr int PASSES_MAX = sizeof(U);
     constexpr int PER_VEC = 16 / sizeof(U);  // keys per 16-byte load
-    constexpr uint32_t PASS_WORDS = kDigits / 2 * kHistCopies;
+    constexpr bool WIDE = kHistWide<U>;
+    constexpr uint32_t PASS_WORDS = (WIDE ? kDigits : kDigits / 2) * kHistCopies;
     __shared__ uint32_t s_hist[PASSES_MAX * PASS_WORDS];
     if constexpr (FULL) passes = PASSES_MAX;
     for (uint32_t i = threadIdx.x; i < passes * PASS_WORDS; i += kHistBlock) s_hist[i] = 0;
@@ -182,7 +188,10 @@ __global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restri
                 pair = d >> 1;
                 odd = d & 1u;
             }
-            atomicAdd(&s_hist[p * PASS_WORDS + pair * kHistCopies + copy], 1u + odd * 0xFFFFu);
+            if constexpr (WIDE)
+                atomicAdd(&s_hist[p * PASS_WORDS + (2 * pair + odd) * kHistCopies + copy], 1u);
+            else
+                atomicAdd(&s_hist[p * PASS_WORDS + pair * kHistCopies + copy], 1u + odd * 0xFFFFu);
         }
     };
     const U* ukeys = reinterpret_cast<const U*>(keys);
@@ -210,9 +219,14 @@ __global__ __launch_bounds__(kHistBlock) void histogram_kernel(const K* __restri
     // over the banks.
     for (uint32_t i = threadIdx.x; i < passes * kDigits; i += kHistBlock) {
         const uint32_t p = i / kDigits, d = i % kDigits;
-        const uint32_t* row = &s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies];
         uint32_t total = 0;
-        for (uint32_t c = 0; c < kHistCopies; ++c) total += (row[(c + i) % kHistCopies] >> ((d & 1u) * 16u)) & 0xFFFFu;
+        if constexpr (WIDE) {
+            const uint32_t* row = &s_hist[p * PASS_WORDS + d * kHistCopies];
+            for (uint32_t c = 0; c < kHistCopies; ++c) total += row[(c + i) % kHistCopies];
+        } else {
+            const uint32_t* row = &s_hist[p * PASS_WORDS + (d >> 1) * kHistCopies];
+            for (uint32_t c = 0; c < kHistCopies; ++c) total += (row[(c + i) % kHistCopies] >> ((d & 1u) * 16u)) & 0xFFFFu;
+        }
         if (total) atomic_add_agent(&bins[p * kDigits + d], total);
     }
 }
@@ -1112,9 +1126,10 @@ Layout make_layout(uint32_t n, size_t key_bytes, size_t value_bytes, uint32_t be
     return L;
 }
 
-// Histogram workgroups over `len` keys: two per CU for 4-byte keys (64 KB of counters each), one for
-// 8-byte keys; contiguous slices of at most kHistMaxItems keys, each a whole number of `granule` keys:
-// 16-byte steps of the workgroup for histogram_kernel, onesweep tiles for histogram_tiles_kernel.
+// Histogram workgroups over `len` keys: one per CU for histogram_kernel (128 KB of counters), and for
+// histogram_tiles_kernel two per CU for 4-byte keys (80 KB each), one for 8-byte keys; contiguous slices
+// of at most kHistMaxItems keys, each a whole number of `granule` keys: 16-byte steps of the workgroup for
+// histogram_kernel, onesweep tiles for histogram_tiles_kernel.
 struct HistPlan {
     uint64_t per;
     unsigned grid;
@@ -1124,8 +1139,8 @@ constexpr uint32_t hist_step() {
     return static_cast<uint32_t>(kHistBlock) * kHistVecItems * (16 / sizeof(K));
 }
 template <typename K>
-HistPlan hist_plan(uint32_t len, uint32_t granule = hist_step<K>()) {
-    const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (sizeof(K) == 4 ? 2 : 1);
+HistPlan hist_plan(uint32_t len, uint32_t granule = hist_step<K>(), bool tiles = false) {
+    const uint64_t hist_target = static_cast<uint64_t>(device_cu_count()) * (tiles && sizeof(K) == 4 ? 2 : 1);
     uint64_t per = ceil_div(ceil_div(len, hist_target), granule) * granule;
     per = std::min<uint64_t>(per, kHistMaxItems / granule * granule);
     return HistPlan{per, static_cast<unsigned>(ceil_div(len, per))};
@@ -1154,7 +1169,7 @@ int launch_sort(char* temp, const Layout& L, const K* keys_in, K* keys_out, cons
     HistPlan hp0{};
     for (uint32_t q = 0; q < L.portions; ++q) {
         const uint32_t len = std::min(L.portion, n - q * L.portion);
-        const HistPlan hp = precount ? hist_plan<K>(len, G.tile()) : hist_plan<K>(len);
+        const HistPlan hp = precount ? hist_plan<K>(len, G.tile(), true) : hist_plan<K>(len);
         const uint64_t per = hp.per;
         const unsigned grid = hp.grid;
         if (q == 0) hp0 = hp;
@@ -1298,7 +1313,7 @@ int sort_entry(void* temp, size_t temp_bytes, const K* keys_in, K* keys_out, con
         const size_t off = align_up(L.total, kViewAlign);
         if (sizeof(K) == 4 && VB == 0 && L.portions == 1 && reinterpret_cast<uintptr_t>(first_src) % 16 == 0 &&
             g_precount.load(std::memory_order_relaxed) &&
-            temp_bytes >= off + static_cast<size_t>(hist_plan<K>(n, G.tile()).grid) * kDigits * 4)
+            temp_bytes >= off + static_cast<size_t>(hist_plan<K>(n, G.tile(), true).grid) * kDigits * 4)
             L.chunk_off = off;
     }
     if (reinterpret_cast<uintptr_t>(temp) % 4 != 0) return set_error(kInvalidArgument, "%s: temp not 4-byte aligned", what);
