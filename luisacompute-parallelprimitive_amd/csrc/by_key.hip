@@ -69,8 +69,9 @@ constexpr int kBkVec = 4;  // consecutive items per thread and row (one 16-byte 
 // 0.437 / 0.405-0.424 / 0.413-0.416 / 0.431 / 0.476 ms; encode 0.252 / 0.251 / 0.254 / 0.266 / 0.299 ms).
 constexpr int kBkWindow = 32;
 // Three workgroups per CU (at most 168 VGPRs), like the scan: one workgroup's look-back wait is
-// covered by the others' loads and stores.
-constexpr int kBkBlocksPerCu = 3;
+// covered by the others' loads and stores.  The count mode (keys only) fits four (at most 128 VGPRs).
+template <int MODE>
+constexpr int kBkBlocksPerCu = MODE == 2 ? 4 : 3;
 // Rows per tile: a thread's keys and values of every row are in flight together (4 * R * (sizeof(K) +
 // sizeof(V)) / 4 VGPRs, 128 for 4-byte keys and values at 16 rows).  The scan keeps its values through
 // the look-back; the reduce stages its run heads in LDS before it, so nothing of the rows stays live and
@@ -82,10 +83,13 @@ constexpr int kBkBlocksPerCu = 3;
 #ifndef LCPP_BK_REDUCE_VGPRS
 #define LCPP_BK_REDUCE_VGPRS 120
 #endif
-// Run lengths and unique items load keys only and keep no per-row scans: 28 rows of 4-byte keys, 14 of
-// 8-byte keys (Encode 2^28 u32 in runs of 64: 0.316 ms at 16 rows, 0.314 at 24, 0.303 at 28).
+// Run lengths and unique items load keys only and keep no per-row scans, so four workgroups per CU fit:
+// 20 rows of 4-byte keys, 10 of 8-byte keys (Encode / Unique 2^28 u32 in runs of 64: 0.247 / 0.242 ms at 20
+// rows and four workgroups per CU, 0.262 / 0.259 at 16 rows and four, 0.255 / 0.253 at 28 rows and three;
+// earlier, before the PARTIAL state was published ahead of the staging, 0.316 ms at 16 rows, 0.314 at 24,
+// 0.303 at 28, three per CU).
 #ifndef LCPP_BK_COUNT_VGPRS
-#define LCPP_BK_COUNT_VGPRS 112
+#define LCPP_BK_COUNT_VGPRS 80
 #endif
 template <typename K, typename V, int MODE>
 constexpr int kBkRows =
@@ -497,7 +501,7 @@ __device__ void reduce_rows_direct(const K* keys, const V* values, K* unique_out
 }
 
 template <typename K, typename V, int MODE, int R, typename Op>
-__global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu) void by_key_kernel(
+__global__ __launch_bounds__(kBkBlock, kBkBlocksPerCu<MODE>) void by_key_kernel(
     const K* __restrict__ keys, const V* values_in, V* values_out, K* __restrict__ unique_out,
     V* __restrict__ aggregates_out, uint32_t* __restrict__ num_runs_out, uint64_t n, K mask,
     uint64_t* __restrict__ states, int inclusive, int use_init, V init, bool vec_k, bool vec_v, bool vec_o,
