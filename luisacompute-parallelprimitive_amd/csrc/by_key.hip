@@ -17,10 +17,11 @@
 // num_runs_out[0] = runs (0 for n == 0).  Integer sums wrap.
 //
 // MI355X design
-//   * Tile = 256 threads x R rows x 4 consecutive items per thread and row (R = 16 for 4-byte keys and
-//     values in the scan, 10 in the reduce: 16,384 / 10,240 items; fewer for 8-byte types), every
-//     row a contiguous 1,024 items read (and, for the scan, written) with 16-byte vectors, all rows'
-//     loads in flight together; three workgroups per CU.  The key before a thread-row is the previous
+//   * Tile = 256 threads x R rows x 4 consecutive items per thread and row (R = 12 for 4-byte keys and
+//     values in the scan, 15 in the reduce, 20 in the count mode: 12,288 / 15,360 / 20,480 items; fewer
+//     for 8-byte types), every row a contiguous 1,024 items read (and, for the scan, written) with
+//     16-byte vectors, all rows' loads in flight together; four workgroups per CU (three for the
+//     reduce).  The key before a thread-row is the previous
 //     lane's last key (DPP wave shift) or, for lane 0, the last key of the previous wave or row (a
 //     small LDS table).
 //   * State of a span of items: (heads, sum since the last head).  States combine as
@@ -68,17 +69,19 @@ constexpr int kBkVec = 4;  // consecutive items per thread and row (one 16-byte 
 // 0.604 ms with 64, 0.57-0.60 with 32, 0.58-0.59 with 16, 0.57-0.60 with 8, 0.60-0.62 with 4; ReduceByKey
 // 0.437 / 0.405-0.424 / 0.413-0.416 / 0.431 / 0.476 ms; encode 0.252 / 0.251 / 0.254 / 0.266 / 0.299 ms).
 constexpr int kBkWindow = 32;
-// Three workgroups per CU (at most 168 VGPRs), like the scan: one workgroup's look-back wait is
-// covered by the others' loads and stores.  The count mode (keys only) fits four (at most 128 VGPRs).
+// Workgroups per CU: the others' loads and stores cover one workgroup's look-back wait.  Four (at most 128
+// VGPRs) for the scan and the count mode, three (at most 168) for the reduce, whose 15 rows outrun 11 rows
+// at four (ReduceByKey 2^28: 0.418 against 0.426 ms; ExclusiveSumByKey 0.592 ms at 16 rows and three,
+// 0.574 at 12 rows and four, 0.581 at 10 rows and four).
 template <int MODE>
-constexpr int kBkBlocksPerCu = MODE == 2 ? 4 : 3;
+constexpr int kBkBlocksPerCu = MODE == 1 ? 3 : 4;
 // Rows per tile: a thread's keys and values of every row are in flight together (4 * R * (sizeof(K) +
-// sizeof(V)) / 4 VGPRs, 128 for 4-byte keys and values at 16 rows).  The scan keeps its values through
+// sizeof(V)) / 4 VGPRs, 96 for 4-byte keys and values at 12 rows).  The scan keeps its values through
 // the look-back; the reduce stages its run heads in LDS before it, so nothing of the rows stays live and
 // 120 VGPRs of keys and values fit (15 rows of 4-byte keys and values; ReduceByKey 2^28 0.61 -> 0.49 ms
 // against 10 rows kept in registers through the look-back).
 #ifndef LCPP_BK_SCAN_VGPRS
-#define LCPP_BK_SCAN_VGPRS 128
+#define LCPP_BK_SCAN_VGPRS 96
 #endif
 #ifndef LCPP_BK_REDUCE_VGPRS
 #define LCPP_BK_REDUCE_VGPRS 120

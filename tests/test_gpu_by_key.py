@@ -16,7 +16,7 @@ from gpu_util import fill_dev, log, to_dev, to_host
 pytestmark = pytest.mark.gpu
 
 NP = {"i32": np.int32, "u32": np.uint32, "f32": np.float32, "i64": np.int64, "u64": np.uint64, "f64": np.float64}
-TILE = 16384         # scan tile, 4-byte keys and values
+TILE = 12288         # scan tile, 4-byte keys and values
 REDUCE_TILE = 15360  # reduce tile, 4-byte keys and values
 
 
