@@ -1003,28 +1003,21 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
             s_prefix[0] = prefix[0];
         }
     }
-    __syncthreads();
-    prefix[0] = s_prefix[0];
-    if (tile + 1 == gridDim.x && tid == 0) a.num_out[0] = prefix[0] + agg[0];
 
-    // Outputs, one row at a time per wave.  Lane r's row_base: the selected items before this wave's part
-    // of row r (the tile prefix, the earlier rows, the earlier waves of row r).  The wave stages its part of
-    // the row in its own LDS slots: selected items from slot 0 up in order, partition rejects from the last
-    // slot down, then reads the slots back one per lane, so every store of the wave covers consecutive
-    // addresses (a selected run, then a run of rejects, whose output runs backwards from the end).
-    const uint32_t row_base = prefix[0] + (rows_incl - row_total) + row_before;
+    // Each wave compacts its part of every row in registers through its own LDS slots: selected items from
+    // slot 0 up in order, partition rejects from the last slot down, then lane l reads back slots 64 j + l.
+    // The order inside a row does not depend on the tile's prefix, so waves 1-3 do this while wave 0 walks
+    // back (wave 0 after its walk).
     U* const stage = s_stage[wave];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t m = row_mask(r);
         const uint32_t c = static_cast<uint32_t>(__builtin_popcount(m));
-        const uint32_t incl = wave_inclusive_scan(c, SumOp{});
-        const uint32_t sel_base = wave_read_lane(row_base, r);
-        const uint32_t kept = wave_read_lane(incl, kWave - 1);  // selected items of the wave's row
+        const uint32_t before = wave_inclusive_scan(c, SumOp{}) - c;  // selected items before the lane's
         const uint64_t row_first = base + (static_cast<uint64_t>(r) * kRowsBlock + wave * kWave) * V;
         const uint32_t in_row = row_first < a.n ? static_cast<uint32_t>(min<uint64_t>(a.n - row_first, kRowSlots)) : 0u;
-        uint32_t k = incl - c;             // selected slots before the lane's items
-        uint32_t q = lane * V - (incl - c);  // rejects before them
+        uint32_t k = before;                  // slot of the lane's next selected item
+        uint32_t q = lane * V - before;       // rejects before the lane's next item
 #pragma unroll
         for (int j = 0; j < V; ++j) {
             if ((m >> j) & 1u) {
@@ -1035,19 +1028,36 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
             }
         }
         __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < V; ++j) it[r][j] = stage[static_cast<uint32_t>(j) * kWave + lane];
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    prefix[0] = s_prefix[0];
+    if (tile + 1 == gridDim.x && tid == 0) a.num_out[0] = prefix[0] + agg[0];
+
+    // Stores.  Lane r's row_base: the selected items before this wave's part of row r (the tile prefix, the
+    // earlier rows, the earlier waves of row r).  Every store of the wave covers consecutive addresses: a
+    // selected run, then a run of rejects, whose output runs backwards from the end.
+    const uint32_t row_base = prefix[0] + (rows_incl - row_total) + row_before;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t sel_base = wave_read_lane(row_base, r);
+        const uint32_t kept = s_tot[r][wave];  // selected items of the wave's part of the row
+        const uint64_t row_first = base + (static_cast<uint64_t>(r) * kRowsBlock + wave * kWave) * V;
+        const uint32_t in_row = row_first < a.n ? static_cast<uint32_t>(min<uint64_t>(a.n - row_first, kRowSlots)) : 0u;
         // Rejects before the wave's row: its first item's index minus the selected items before it.
         const uint64_t rej_end = a.n - 1 - (row_first - sel_base);  // output position of the row's first reject
 #pragma unroll
         for (int j = 0; j < V; ++j) {
             const uint32_t slot = static_cast<uint32_t>(j) * kWave + lane;
             if (slot < kept) {
-                a.out[sel_base + slot] = stage[slot];
+                a.out[sel_base + slot] = it[r][j];
             } else if (a.partition && slot >= kRowSlots - (in_row - kept)) {
                 // Slot kRowSlots - 1 - q holds reject q, which goes to rej_end - q.
-                a.out[rej_end - (kRowSlots - 1 - slot)] = stage[slot];
+                a.out[rej_end - (kRowSlots - 1 - slot)] = it[r][j];
             }
         }
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
