@@ -16,9 +16,11 @@ every phase boundary and write one 16-word record per tile (layout in ``csrc/com
 The trace build perturbs what it measures a little (a wait for outstanding memory operations before two
 stamps); the product library has no trace code.
 
-``--pairs`` traces SortPairs of 2^27 uniform u64 keys with u32 values (8 passes) instead.
+``--pairs`` traces SortPairs of 2^27 uniform u64 keys with u32 values (8 passes) instead.  ``--rank-mode M``
+traces SortKeys only, with the in-wave ranking set by the library's test hook (0 ballots, 1 LDS tables,
+2 both), after printing the untraced time per sort of the same library.
 
-Usage: python luisacompute-parallelprimitive_amd/phase_trace.py [--log2n 28] [--pairs]
+Usage: python luisacompute-parallelprimitive_amd/phase_trace.py [--log2n 28] [--pairs] [--rank-mode M]
 """
 from __future__ import annotations
 
@@ -104,6 +106,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--log2n", type=int, default=28)
     ap.add_argument("--pairs", action="store_true", help="SortPairs 2^27 u64 + u32 (8 passes) only")
+    ap.add_argument("--rank-mode", type=int, default=None, choices=(0, 1, 2),
+                    help="SortKeys in-wave ranking: 0 ballots in every wave, 1 LDS tables in every wave, 2 both "
+                         "(the default); also prints the untraced time per sort")
     args = ap.parse_args()
     import torch
     import lcpp_hip as hip
@@ -161,9 +166,27 @@ def main() -> int:
         assert lib.lcpp_hip_trace_set_buffer(None, 0) == 0
         return buf.cpu().numpy().view(np.uint64).reshape(-1, WORDS)[:records].copy()
 
-    rec = traced(lambda: hip.sort_keys("u32", keys, out, n, temp=temp), 4 * tiles)
+    sort = lambda: hip.sort_keys("u32", keys, out, n, temp=temp)
+    if args.rank_mode is not None:
+        # The trace library's own test hook; the untraced time is of the same library with tracing off.
+        assert lib.lcpp_hip_internal_radix_rank_mode(args.rank_mode) == 0
+        assert lib.lcpp_hip_trace_set_buffer(None, 0) == 0
+        for _ in range(15):
+            sort()
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        events[0].record()
+        for _ in range(10):
+            sort()
+        events[1].record()
+        torch.cuda.synchronize()
+        print(json.dumps({"rank_mode": args.rank_mode, "untraced_ms_per_sort": round(events[0].elapsed_time(events[1]) / 10, 4)}),
+              flush=True)
+    rec = traced(sort, 4 * tiles)
     for p in range(4):
         print(json.dumps(summarize_sort(rec[p * tiles:(p + 1) * tiles], p)), flush=True)
+    if args.rank_mode is not None:
+        lib.lcpp_hip_internal_radix_rank_mode(2)
+        return 0
     del temp
 
     vals = torch.empty(n, dtype=torch.int32, device=dev)
