@@ -1026,7 +1026,7 @@ struct Geometry {
 //     with 16 keys per thread, 2.215 with 18, 2.219 with 19, whose 64 VGPRs spill; 20 would leave one
 //     workgroup per CU, and one workgroup per CU measured 2.49-2.50 ms per sort with 1024 x 32 or
 //     1024 x 36 tiles against 2.01 ms at 1024 x 18: a second workgroup's scatter no longer overlaps
-//     each rank).  1024-thread workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice
+//     each rank; four 512 x 18 or 512 x 19 workgroups per CU: 2.49-2.57 ms).  1024-thread workgroups (32 waves per CU, 64 VGPRs) beat 512 threads with twice
 //     the items per thread: every wave's rank is a chain of dependent LDS round trips, and shorter chains
 //     on more waves hide them better (SortKeys 2^28 u32 3.04 -> 2.81 ms when measured).
 //   * 8-byte keys: 1024 x 9 (SortKeys 2^27 u64 4.52 -> 4.31 ms, SortPairs 2^27 u64 + u32 5.98 -> 5.92 ms
