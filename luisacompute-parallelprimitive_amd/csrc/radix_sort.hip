@@ -21,7 +21,8 @@
 //     popcount of the mask below the lane, and the highest lane of each digit group advances the
 //     count.  OR is order-independent, so ranks never depend on how conflicting lanes are serialised.
 //   * Tile order: workgroup b is tile tile_of_block(b): 16 consecutive tiles per XCD at a time, so
-//     the boundary cache lines of neighbouring tiles' digit runs merge in one L2.  There is no tile
+//     the boundary cache lines of neighbouring tiles' digit runs merge in one L2 (groups of 8, 32 and 64
+//     measured slower: longer groups make longer look-back chains between XCDs).  There is no tile
 //     ticket (a same-address agent-scope atomic serialises at ~11 ns on MI355X).
 //   * Look-back: per-digit counts go to a row of 256 32-bit words per tile: bits 31:30 hold the
 //     status (1 PARTIAL, 2 INCLUSIVE), bits 29:0 the count, read and written with agent-scope atomics
