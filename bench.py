@@ -277,7 +277,7 @@ def extra_sort_pairs(hip, dev, steps, warmup, extra):
         hip.generate(hip.GEN_U32_IOTA, v, m, 0)
         ko, vo = torch.empty_like(k), torch.empty_like(v)
         pt = torch.empty(hip.bytes_to_uint_count(hip.sort_pairs_temp_bytes(m, 8, 4)), dtype=torch.int32, device=dev)
-        t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), 1)
+        t = time_steps(lambda: hip.sort_pairs("u64", 4, k, ko, v, vo, m, temp=pt), max(3, steps // 2), warmup)
         extra[f"sort_pairs_u64_u32_2p27_{kind}"] = {
             **t.fields(), "Gpairs_per_s": round(m / t.mean / 1e6, 3),
             "GBps_8pass_model": rate(2 * 8 * m * 12, t.mean),
