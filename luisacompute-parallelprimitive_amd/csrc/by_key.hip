@@ -264,11 +264,6 @@ __device__ __forceinline__ Seg<V> wave_seg_exclusive(Seg<V> inclusive) {
     return e;
 }
 
-template <typename T>
-struct alignas(16) Quad {
-    T v[kBkVec];
-};
-
 // Items [first, first + 4) of `p`, in range, 16-byte aligned: one (or, for 8-byte items, two) vector loads.
 template <typename T>
 __device__ __forceinline__ void load_quad_vec(const T* p, uint64_t first, T (&out)[kBkVec]) {
@@ -291,15 +286,18 @@ __device__ __forceinline__ void load_quad(const T* p, uint64_t first, uint64_t n
     else load_quad_any(p, first, n, out);
 }
 
-// Stores the items of `valid` (bit k: item first + k exists) of a thread-row: one vector store when all
-// four exist and the array is 16-byte aligned.
+// Stores the items of `valid` (bit k: item first + k exists) of a thread-row: one non-temporal vector
+// store when all four exist and the array is 16-byte aligned.  The lanes of a row store consecutive 16-byte
+// vectors, so every instruction covers whole lines (ExclusiveSumByKey 2^28 i32 / u32: 0.581 -> 0.533 ms
+// per call against plain stores; non-temporal stores of single items measured slower in compaction).
 template <typename T>
 __device__ __forceinline__ void store_quad(T* p, uint64_t first, uint32_t valid, bool vec, const T (&in)[kBkVec]) {
     if (vec && valid == 0xFu) {
-        Quad<T> q;
+        typedef T Vec __attribute__((ext_vector_type(kBkVec), aligned(16)));
+        Vec q;
 #pragma unroll
-        for (int k = 0; k < kBkVec; ++k) q.v[k] = in[k];
-        *reinterpret_cast<Quad<T>*>(p + first) = q;
+        for (int k = 0; k < kBkVec; ++k) q[k] = in[k];
+        __builtin_nontemporal_store(q, reinterpret_cast<Vec*>(p + first));
     } else {
 #pragma unroll
         for (int k = 0; k < kBkVec; ++k) {
