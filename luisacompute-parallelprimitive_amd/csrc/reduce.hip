@@ -4,8 +4,9 @@
 // (src/lcpp/device/device_reduce.h:280-288,229-252,728-958) with AgentReduce tiles of 256x8 striped
 // loads (agent/agent_reduce.h:58-173) and a 32-lane warp tree (warp/details/warp_reduce_shlf.h:37-76).
 //
-// MI355X design: one persistent pass over HBM.  A grid of (CUs x 8) workgroups of 256 threads
-// streams the input with 128-bit loads, UNROLL loads in flight per thread, folds them in registers,
+// MI355X design: one persistent pass over HBM.  A grid of (CUs x 8) workgroups of 256 threads (2^28 i32
+// Sum: 0.156 ms per call with 8 or 16 per CU, 0.158 with 32, 0.159 with 64, 0.172 with one workgroup per
+// 4,096 items) streams the input with 128-bit loads, UNROLL loads in flight per thread, folds them in registers,
 // reduces each wave with DPP row shifts / row broadcasts, and writes one partial per workgroup into
 // the caller's temp storage.  A single 1024-thread workgroup folds the partials and writes *out.
 // Inputs of at most one persistent round fall back to one workgroup that writes *out directly.
