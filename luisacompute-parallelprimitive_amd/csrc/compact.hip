@@ -729,9 +729,11 @@ __global__ __launch_bounds__(kCpBlock) void compact_kernel(const CompactArgs<U, 
 // Like the scan's tiles, a tile is 256 threads x ROWS rows x one 16-byte vector of items per thread and
 // row, held in registers (four workgroups per CU), rather than staged whole in LDS as by the kernel above
 // (whose 32 KB stage per tile bounds the input in flight).  Per thread and row a mask of the selected items
-// (each clause one uniform switch over all of the thread's items); per row the waves' counts go to a rows x
-// waves table in LDS.  Wave 0 publishes the tile's count and walks back alone, without a workgroup barrier
-// per poll.  Then each wave stages its part of every row in 1 KB of LDS (selected items from the front,
+// (each clause one uniform switch over all of the thread's items).  The tile's count comes first (one wave
+// reduce per wave and one barrier: select-if / partition-if 0.387 / 0.444 -> 0.385 / 0.437 ms against
+// publishing after the per-row totals), and wave 0 publishes it and walks back alone, without a workgroup
+// barrier per poll, while the other waves put their per-row counts into a rows x waves table in LDS.  Then
+// each wave stages its part of every row in 1 KB of LDS (selected items from the front,
 // partition rejects from the back) and reads it back one slot per lane, so every store covers consecutive
 // addresses.  (Stored straight from registers, four scattered stores per row, select-if took 0.53 ms.)
 constexpr int kRowsBlock = 256;
@@ -896,6 +898,7 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
     __shared__ uint32_t s_tot[R][kRowsWaves];
     __shared__ U s_stage[kRowsWaves][kRowSlots];
     __shared__ uint32_t s_prefix[1];
+    __shared__ uint32_t s_wtot[kRowsWaves];
 
     uint64_t* const states = a.states;
     uint64_t* const claims = states + gridDim.x;
@@ -954,27 +957,19 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
     }
     auto row_mask = [&](int r) { return (masks[r / ROWS_PER_WORD] >> (V * (r % ROWS_PER_WORD))) & ((1u << V) - 1u); };
 
-    // Row totals per wave now; each thread's offset within its row is scanned again at output time, so
-    // no per-row scan stays live across the look-back.
+    // The tile's count first (one wave reduce and one barrier), so the PARTIAL state goes out as early as
+    // possible; the per-row totals follow behind the publish.
+    {
+        uint32_t c_all = 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t total = wave_reduce(static_cast<uint32_t>(__builtin_popcount(row_mask(r))), SumOp{});
-        if (lane == 0) s_tot[r][wave] = total;
+        for (int w = 0; w < MW; ++w) c_all += static_cast<uint32_t>(__builtin_popcount(masks[w]));
+        const uint32_t wt = wave_reduce(c_all, SumOp{});
+        if (lane == 0) s_wtot[wave] = wt;
     }
     __syncthreads();
-    // Lane r (< R) of every wave takes row r: its total over the waves, the part in waves before this
-    // one, and (scanned over the lanes) the selected items of the tile's earlier rows.
-    uint32_t row_total = 0, row_before = 0;
-    if (lane < static_cast<uint32_t>(R)) {
+    uint32_t agg[1] = {0};
 #pragma unroll
-        for (int w = 0; w < kRowsWaves; ++w) {
-            const uint32_t x = s_tot[lane][w];
-            if (w < static_cast<int>(wave)) row_before += x;
-            row_total += x;
-        }
-    }
-    const uint32_t rows_incl = wave_inclusive_scan(row_total, SumOp{});
-    uint32_t agg[1] = {wave_read_lane(rows_incl, kWave - 1)};
+    for (int w = 0; w < kRowsWaves; ++w) agg[0] += s_wtot[w];
 
     // Wave 0 publishes the tile's count, walks back over its predecessors and publishes the inclusive count
     // at once (a helper that claimed this tile first publishes its PARTIAL state; the owner then waits for
@@ -1008,6 +1003,13 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
     // slot 0 up in order, partition rejects from the last slot down, then lane l reads back slots 64 j + l.
     // The order inside a row does not depend on the tile's prefix, so waves 1-3 do this while wave 0 walks
     // back (wave 0 after its walk).
+    // Row totals per wave (read after the next barrier); each thread's offset within its row is scanned
+    // again at output time, so no per-row scan stays live across the look-back.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t total = wave_reduce(static_cast<uint32_t>(__builtin_popcount(row_mask(r))), SumOp{});
+        if (lane == 0) s_tot[r][wave] = total;
+    }
     U* const stage = s_stage[wave];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -1035,6 +1037,18 @@ __global__ __launch_bounds__(kRowsBlock, 4) void select_rows_kernel(const Compac
     __syncthreads();
     prefix[0] = s_prefix[0];
     if (tile + 1 == gridDim.x && tid == 0) a.num_out[0] = prefix[0] + agg[0];
+    // Lane r (< R) of every wave takes row r: its total over the waves, the part in waves before this
+    // one, and (scanned over the lanes) the selected items of the tile's earlier rows.
+    uint32_t row_total = 0, row_before = 0;
+    if (lane < static_cast<uint32_t>(R)) {
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) {
+            const uint32_t x = s_tot[lane][w];
+            if (w < static_cast<int>(wave)) row_before += x;
+            row_total += x;
+        }
+    }
+    const uint32_t rows_incl = wave_inclusive_scan(row_total, SumOp{});
 
     // Stores.  Lane r's row_base: the selected items before this wave's part of row r (the tile prefix, the
     // earlier rows, the earlier waves of row r).  Every store of the wave covers consecutive addresses: a
