@@ -72,7 +72,8 @@ constexpr int kBkWindow = 32;
 // Workgroups per CU: the others' loads and stores cover one workgroup's look-back wait.  Four (at most 128
 // VGPRs) for the scan and the count mode, three (at most 168) for the reduce, whose 15 rows outrun 11 rows
 // at four (ReduceByKey 2^28: 0.418 against 0.426 ms; ExclusiveSumByKey 0.592 ms at 16 rows and three,
-// 0.574 at 12 rows and four, 0.581 at 10 rows and four).
+// 0.574 at 12 rows and four, 0.581 at 10 rows and four; with non-temporal output stores 0.533 at 12 rows,
+// 0.531 at 10 and 0.549 at 14, which spills).
 template <int MODE>
 constexpr int kBkBlocksPerCu = MODE == 1 ? 3 : 4;
 // Rows per tile: a thread's keys and values of every row are in flight together (4 * R * (sizeof(K) +
