@@ -220,7 +220,7 @@ def extra_reduce(hip, dev, steps, warmup, extra):
                                     **cold.fields("ms_cold"), "GBps_cold": rate(4 * m, cold.mean),
                                     "ms_two_launch_floor_graph": round(floor.mean, 5)}
     del flush
-    # Reduce 2^28 int32 (north-star size).
+    # Reduce 2^28 int32 (1 GiB read).
     m = 1 << 28
     a = torch.empty(m, dtype=torch.int32, device=dev)
     hip.generate(hip.GEN_I32_PM1000, a, m, SEED)

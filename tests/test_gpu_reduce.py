@@ -3,7 +3,7 @@
 Cases follow the reference tests: sums of 2^k+1 ones (tests/device_reduce_test.cpp:95-119), shuffled
 iota (:85-91), transform sizes {1,31,256,1023,1024,1025,1048577,4194304} (:148-173), 2^24+1 zeros
 plus a tail value (tests/pr6_review_regression_test.cpp:427-457), the benchmark input (2^24 int32 in
-[-1000, 1000] from seed 114521) and the 2^28 north-star size.
+[-1000, 1000] from seed 114521) and 2^28 items (1 GiB of int32).
 """
 import numpy as np
 import pytest
