@@ -199,7 +199,7 @@ def rate(nbytes: float, ms: float) -> float:
 def extra_reduce(hip, dev, steps, warmup, extra):
     import torch
     flush = torch.empty(1 << 28, dtype=torch.int32, device=dev)
-    # Reduce 2^24 int32 (config 1): hot (MALL-resident) and cold (MALL flushed before each call).
+    # Reduce 2^24 int32 in [-1000, 1000]: hot (MALL-resident) and cold (MALL flushed before each call).
     m = 1 << 24
     a = torch.empty(m, dtype=torch.int32, device=dev)
     hip.generate(hip.GEN_I32_PM1000, a, m, SEED)
@@ -241,7 +241,7 @@ def extra_reduce(hip, dev, steps, warmup, extra):
 
 def extra_scan(hip, dev, steps, warmup, extra, copy=None):
     import torch
-    # ExclusiveSum 2^28 uint32 in [0, 16) (config 2).
+    # ExclusiveSum 2^28 uint32 in [0, 16).
     m = 1 << 28
     b = torch.empty(m, dtype=torch.int32, device=dev)
     hip.generate(hip.GEN_U32_LT16, b, m, SEED)
@@ -268,7 +268,7 @@ def extra_scan(hip, dev, steps, warmup, extra, copy=None):
 
 def extra_sort_pairs(hip, dev, steps, warmup, extra):
     import torch
-    # SortPairs 2^27 u64 keys + u32 index values (config 4), uniform and AND-of-3 keys.
+    # SortPairs 2^27 u64 keys + u32 index values, uniform and AND-of-3 keys.
     m = 1 << 27
     for kind, gen in (("uniform", hip.GEN_U64), ("and3", hip.GEN_U64_AND3)):
         k = torch.empty(m, dtype=torch.int64, device=dev)
@@ -287,7 +287,7 @@ def extra_sort_pairs(hip, dev, steps, warmup, extra):
 
 def extra_spmv(hip, dev, steps, warmup, extra):
     import torch
-    # CsrMV fp32 (config 5): 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
+    # CsrMV fp32: 2^20 x 2^20, Zipf(1.5) row lengths in [1, 4096], built on the host.
     rows = cols = 1 << 20
     va, ro, ci, xv, nnz = zipf_matrix()
     d = [torch.from_numpy(t).to(dev) for t in (va, ro, ci, xv)]
@@ -527,13 +527,13 @@ def cpu_baseline(keys_dev, reps: int = 5) -> dict:
         return out
 
     res = {}
-    # Reduce: config 1 in full (2^24 int32 in [-1000, 1000]).
+    # Reduce: all 2^24 int32 items in [-1000, 1000].
     n = 1 << 24
     a = oracle.generate(2, n, SEED)
     t = timed(lambda th: oracle.par_reduce_sum_i32(a, th))
     res["reduce_sum_i32_2p24"] = {"sample": "all 2^24 items", "unit": "GB/s",
                                   **{k: round(4 * n / v / 1e9, 2) for k, v in t.items()}}
-    # Scan: 2^26 of config 2's 2^28 u32 in [0, 16).
+    # Scan: 2^26 of the 2^28 u32 in [0, 16).
     n = 1 << 26
     b = oracle.generate(3, n, SEED)
     out = np.empty_like(b)
@@ -541,7 +541,7 @@ def cpu_baseline(keys_dev, reps: int = 5) -> dict:
     res["exclusive_sum_u32_2p28"] = {"sample": "first 2^26 of the 2^28 items", "unit": "GB/s",
                                      **{k: round(8 * n / v / 1e9, 2) for k, v in t.items()}}
     del b, out
-    # SortKeys: 2^24 of config 3's keys (stable 8-bit LSD, as on the GPU), plus std::sort on one thread.
+    # SortKeys: 2^24 of the 2^28 uniform u32 keys (stable 8-bit LSD, as on the GPU), plus std::sort on one thread.
     n = 1 << 24
     sample = keys_dev[:n].cpu().numpy().view(np.uint32).copy()
     work, tmp = np.empty_like(sample), np.empty_like(sample)
@@ -561,7 +561,7 @@ def cpu_baseline(keys_dev, reps: int = 5) -> dict:
                                  **{k: round(n / v / 1e9, 4) for k, v in t.items()},
                                  "std_sort_1_thread": round(n / statistics.median(std_ts) / 1e9, 4)}
     del sample, work, tmp
-    # SortPairs: 2^22 uniform u64 keys with u32 index values (config 4a stream).
+    # SortPairs: 2^22 uniform u64 keys with u32 index values (the uniform SortPairs key stream).
     n = 1 << 22
     k0 = oracle.generate(0, n, SEED)
     v0 = np.arange(n, dtype=np.uint32)
