@@ -145,7 +145,7 @@ constexpr int kHistCopies = 32;
 template <typename U>
 constexpr bool kHistWide = sizeof(U) == 4;
 constexpr int kHistBlock = 1024;
-constexpr int kHistVecItems = 8;             // 16-byte loads per thread per step
+constexpr int kHistVecItems = 8;  // 16-byte loads per thread per step (2^28 u32: 169 us with 4 or 8, 178 with 16)
 constexpr uint32_t kHistMaxItems = 1u << 20;  // keys per workgroup
 
 // FULL: every 8-bit digit of the key (begin_bit 0, end_bit = key bits), so digit positions are
