@@ -18,7 +18,7 @@
 //
 // MI355X design
 //   * Tile = 256 threads x R rows x 4 consecutive items per thread and row (R = 12 for 4-byte keys and
-//     values in the scan, 15 in the reduce, 20 in the count mode: 12,288 / 15,360 / 20,480 items; fewer
+//     values in the scan, 15 in the reduce, 22 in the count mode: 12,288 / 15,360 / 22,528 items; fewer
 //     for 8-byte types), every row a contiguous 1,024 items read (and, for the scan, written) with
 //     16-byte vectors, all rows' loads in flight together; four workgroups per CU (three for the
 //     reduce).  The key before a thread-row is the previous
@@ -88,12 +88,13 @@ constexpr int kBkBlocksPerCu = MODE == 1 ? 3 : 4;
 #define LCPP_BK_REDUCE_VGPRS 120
 #endif
 // Run lengths and unique items load keys only and keep no per-row scans, so four workgroups per CU fit:
-// 20 rows of 4-byte keys, 10 of 8-byte keys (Encode / Unique 2^28 u32 in runs of 64: 0.247 / 0.242 ms at 20
-// rows and four workgroups per CU, 0.262 / 0.259 at 16 rows and four, 0.255 / 0.253 at 28 rows and three;
+// 22 rows of 4-byte keys, 11 of 8-byte keys (Encode / Unique 2^28 u32 in runs of 64: 0.242 / 0.237 ms at 22
+// rows and four workgroups per CU, 0.247 / 0.242 at 20, 0.263 / 0.262 at 24, which spills, 0.262 / 0.259 at
+// 16 rows and four, 0.255 / 0.253 at 28 rows and three;
 // earlier, before the PARTIAL state was published ahead of the staging, 0.316 ms at 16 rows, 0.314 at 24,
 // 0.303 at 28, three per CU).
 #ifndef LCPP_BK_COUNT_VGPRS
-#define LCPP_BK_COUNT_VGPRS 80
+#define LCPP_BK_COUNT_VGPRS 88
 #endif
 template <typename K, typename V, int MODE>
 constexpr int kBkRows =

@@ -254,11 +254,11 @@ def test_run_length_encode_known_answers(hip, dev):
         assert int(to_host(num, np.uint32, 1)[0]) == 0
 
 
-# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles), 10,240 and 20,480 (the
+# Tile edges: 4,096 and 8,192 (the compaction kernel's eight- and four-byte tiles), 11,264 and 22,528 (the
 # run kernels' tiles of eight- and four-byte items) and their multiples, and other sizes.
 @pytest.mark.parametrize("count", [1, 2, 3, 31, 32, 33, 3839, 3840, 3841, 4095, 4096, 4097, 5761, 8191, 8192, 8193,
-                                   10239, 10240, 10241, 14336, 16383, 16384, 16385, 20479, 20480, 20481, 28672,
-                                   30721, 40961, 230413])
+                                   10240, 11263, 11264, 11265, 14336, 16383, 16384, 16385, 20480, 22527, 22528,
+                                   22529, 28672, 33793, 45057, 230413])
 def test_run_length_encode_long_runs_across_tiles(hip, orc, dev, count):
     """device_run_length_encode_test.cpp:74-136: x[i] = i / run_length for run lengths 1, 2, 17, 18001, n."""
     for run_length in (1, 2, 17, 18001, count):
