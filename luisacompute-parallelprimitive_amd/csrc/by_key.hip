@@ -80,7 +80,8 @@ constexpr int kBkBlocksPerCu = MODE == 1 ? 3 : 4;
 // sizeof(V)) / 4 VGPRs, 96 for 4-byte keys and values at 12 rows).  The scan keeps its values through
 // the look-back; the reduce stages its run heads in LDS before it, so nothing of the rows stays live and
 // 120 VGPRs of keys and values fit (15 rows of 4-byte keys and values; ReduceByKey 2^28 0.61 -> 0.49 ms
-// against 10 rows kept in registers through the look-back).
+// against 10 rows kept in registers through the look-back; later 0.414 ms at 15 rows, 0.419 at 14 and 0.512
+// at 16, which spills).
 #ifndef LCPP_BK_SCAN_VGPRS
 #define LCPP_BK_SCAN_VGPRS 96
 #endif
